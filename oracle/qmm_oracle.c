@@ -1,0 +1,1450 @@
+/*
+ * qmm_oracle.c -- CPU restatement of the reference's quantized-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels and the CPU
+ * baseline bench.py times.  The product never links or calls this file.
+ *
+ * Built with -ffp-contract=off: the reference's goldens were captured from C
+ * compiled that way (src/ggml/quants/helpers.zig:27-59), and its Zig port is
+ * strict (no contraction) -- every float expression below is evaluated in the
+ * order written, one rounding per operation, exactly as the Zig does.  The
+ * AVX2 kernels use explicit FMA intrinsics where the reference does.
+ *
+ * Parity status of each part (pinned = reproduced bit-for-bit against a
+ * golden the reference's tests hold; see tests/test_oracle_golden.py):
+ *   fp16 <-> fp32 ................. pinned through every quant/dequant golden
+ *   quantize_row_q4_K/q6_K/q8_0/q8_1/q8_K_ref, dequantize_* . pinned
+ *   quantize_q4_K / q6_K (imatrix impls) ......... pinned (chunk_imatrix goldens)
+ *   vec_dot q4_K/q6_K/q8_0 generic ............... pinned (cpu/quants/golden.zig)
+ *   vec_dot AVX2 + quantize_row_q8_0 AVX2 ........ NOT golden-pinned (the tree
+ *       holds no x86 goldens); checked against the pinned generic kernels
+ *       (integers exact, floats within a few ulp) -- "parity unpinned" for bits.
+ *   mul_mat / mul_mat_id drivers .................. pinned by construction
+ *       (each output is one vec_dot call) + thread-count invariance tests.
+ *   block_dots_q8_1 / mul_mat_q8_1_f64 ........... GPU-semantics restatement;
+ *       pinned against brute force on tiny inputs and the dequantised f64 dot.
+ */
+#include "qmm_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdatomic.h>
+#include <stdlib.h>
+#include <string.h>
+
+#if defined(__x86_64__)
+#include <immintrin.h>
+#define ORC_X86 1
+#else
+#define ORC_X86 0
+#endif
+
+#define QK_K 256
+#define QK8_0 32
+#define QK8_1 32
+#define K_SCALE_SIZE 12
+
+/* Block layouts: src/ggml/quants/blocks.zig:67-222 (ggml-common.h). */
+typedef struct { uint16_t d; int8_t qs[QK8_0]; } blk_q8_0;                  /* 34 B */
+typedef struct { uint16_t d; uint16_t s; int8_t qs[QK8_1]; } blk_q8_1;      /* 36 B */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qs[QK_K / 2]; } blk_q4_K; /* 144 B */
+typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_K;  /* 210 B */
+typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;                               /* 292 B */
+
+_Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
+_Static_assert(sizeof(blk_q8_1) == 36, "q8_1");
+_Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
+_Static_assert(sizeof(blk_q6_K) == 210, "q6_K");
+_Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
+
+size_t orc_type_size(int type) {
+    switch (type) {
+    case ORC_TYPE_F32: return 4;
+    case ORC_TYPE_Q8_0: return sizeof(blk_q8_0);
+    case ORC_TYPE_Q8_1: return sizeof(blk_q8_1);
+    case ORC_TYPE_Q4_K: return sizeof(blk_q4_K);
+    case ORC_TYPE_Q6_K: return sizeof(blk_q6_K);
+    case ORC_TYPE_Q8_K: return sizeof(blk_q8_K);
+    default: return 0;
+    }
+}
+
+int64_t orc_blck_size(int type) {
+    switch (type) {
+    case ORC_TYPE_F32: return 1;
+    case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_1: return 32;
+    case ORC_TYPE_Q4_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
+    default: return 0;
+    }
+}
+
+size_t orc_row_size(int type, int64_t ne) {
+    return orc_type_size(type) * (size_t)(ne / orc_blck_size(type));
+}
+
+/* ------------------------------------------------------------------------ */
+/* fp16 conversions: src/ggml/impl.zig:770-830 (ggml-impl.h:403, 426).  The
+ * bit-manipulation method is the public FP16 library's (M. Dukhan), which the
+ * reference uses; restated here from that published algorithm. */
+
+static inline float f_from_bits(uint32_t w) { float f; memcpy(&f, &w, 4); return f; }
+static inline uint32_t f_to_bits(float f) { uint32_t w; memcpy(&w, &f, 4); return w; }
+
+float orc_fp16_to_fp32(uint16_t h) {
+    const uint32_t w = (uint32_t)h << 16;
+    const uint32_t sign = w & 0x80000000u;
+    const uint32_t two_w = w + w;
+    const uint32_t exp_offset = 0xE0u << 23;
+    const float exp_scale = f_from_bits(0x7800000u);
+    const float normalized_value = f_from_bits((two_w >> 4) + exp_offset) * exp_scale;
+    const uint32_t magic_mask = 126u << 23;
+    const float magic_bias = 0.5f;
+    const float denormalized_value = f_from_bits((two_w >> 17) | magic_mask) - magic_bias;
+    const uint32_t denormalized_cutoff = 1u << 27;
+    const uint32_t result = sign | (two_w < denormalized_cutoff ? f_to_bits(denormalized_value)
+                                                                : f_to_bits(normalized_value));
+    return f_from_bits(result);
+}
+
+uint16_t orc_fp32_to_fp16(float f) {
+    const float scale_to_inf = f_from_bits(0x77800000u);
+    const float scale_to_zero = f_from_bits(0x08800000u);
+    float base = (fabsf(f) * scale_to_inf) * scale_to_zero;
+    const uint32_t w = f_to_bits(f);
+    const uint32_t shl1_w = w + w;
+    const uint32_t sign = w & 0x80000000u;
+    uint32_t bias = shl1_w & 0xFF000000u;
+    if (bias < 0x71000000u) bias = 0x71000000u;
+    base = f_from_bits((bias >> 1) + 0x07800000u) + base;
+    const uint32_t bits = f_to_bits(base);
+    const uint32_t exp_bits = (bits >> 13) & 0x00007C00u;
+    const uint32_t mantissa_bits = bits & 0x00000FFFu;
+    const uint32_t nonsign = exp_bits + mantissa_bits;
+    return (uint16_t)((sign >> 16) | (shl1_w > 0xFF000000u ? 0x7E00u : nonsign));
+}
+
+#define FP16(x) orc_fp32_to_fp16(x)
+#define F32(h) orc_fp16_to_fp32(h)
+
+uint64_t orc_fnv1a(const void *p, size_t n) {
+    const uint8_t *b = (const uint8_t *)p;
+    uint64_t h = 0xcbf29ce484222325ull;
+    for (size_t i = 0; i < n; ++i) { h ^= b[i]; h *= 0x100000001b3ull; }
+    return h;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Scale fitting: src/ggml/quants/helpers.zig */
+
+/* nearestInt, helpers.zig:99-104: round half to even via the 1.5*2^23 trick. */
+int orc_nearest_int(float fval) {
+    const float val = fval + 12582912.0f;
+    int32_t i; memcpy(&i, &val, 4);
+    return (i & 0x007fffff) - 0x00400000;
+}
+#define nearest_int orc_nearest_int
+
+static const float GROUP_MAX_EPS = 1e-15f; /* helpers.zig:79 */
+
+/* C float -> integer cast with the reference's clamp (impl.zig:744-752). */
+static inline int8_t trunc_i8(float f) {
+    const float t = truncf(f);
+    if (isnan(t)) return 0;
+    if (t <= -128.0f) return -128;
+    if (t >= 127.0f) return 127;
+    return (int8_t)t;
+}
+
+/* makeQxQuants, helpers.zig:125-203 (rmse_type 1 or imatrix weights). */
+static float make_qx_quants(int n, int nmax, const float *x, int8_t *L, int rmse_type,
+                            const float *qw) {
+    float max = 0, amax = 0;
+    for (int i = 0; i < n; ++i) {
+        const float ax = fabsf(x[i]);
+        if (ax > amax) { amax = ax; max = x[i]; }
+    }
+    if (amax < GROUP_MAX_EPS) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.0f;
+    }
+    float iscale = -(float)nmax / max;
+    if (rmse_type == 0) {
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            L[i] = (int8_t)(nmax + l);
+        }
+        return 1 / iscale;
+    }
+    int return_early = 0;
+    if (rmse_type < 0) { rmse_type = -rmse_type; return_early = 1; }
+#define QX_W(i) (qw ? qw[i] : (rmse_type == 1 ? x[i] * x[i] : rmse_type == 2 ? 1.0f : rmse_type == 3 ? fabsf(x[i]) : sqrtf(fabsf(x[i]))))
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+        L[i] = (int8_t)(l + nmax);
+        const float w = QX_W(i);
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    float scale = suml2 != 0 ? sumlx / suml2 : 0.0f;
+    if (return_early) return suml2 > 0 ? 0.5f * (scale + 1 / iscale) : 1 / iscale;
+    float best = scale * sumlx;
+    for (int is = -9; is <= 9; ++is) {
+        if (is == 0) continue;
+        iscale = -((float)nmax + 0.1f * (float)is) / max;
+        sumlx = suml2 = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * x[i]);
+            l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+            const float w = QX_W(i);
+            sumlx += w * x[i] * (float)l;
+            suml2 += w * (float)l * (float)l;
+        }
+        if (suml2 > 0 && sumlx * sumlx > best * suml2) {
+            for (int i = 0; i < n; ++i) {
+                int l = nearest_int(iscale * x[i]);
+                l = l < -nmax ? -nmax : (l > nmax - 1 ? nmax - 1 : l);
+                L[i] = (int8_t)(nmax + l);
+            }
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+        }
+    }
+#undef QX_W
+    return scale;
+}
+
+/* makeQkx2Quants, helpers.zig:307-405. */
+static float make_qkx2_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L,
+                              float *the_min, uint8_t *Laux, float rmin, float rdelta, int nstep,
+                              int use_mad) {
+    float min = x[0], max = x[0];
+    float sum_w = weights[0];
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = weights[i];
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max == min) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        *the_min = -min;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_error = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)(l < 0 ? 0 : (l > nmax ? nmax : l));
+        float diff = scale * (float)L[i] + min - x[i];
+        diff = use_mad ? fabsf(diff) : diff * diff;
+        best_error += weights[i] * diff;
+    }
+    if (nstep < 1) { *the_min = -min; return scale; }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * (float)is + (float)nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            const float v = iscale * (x[i] - min);
+            const float nmax_f = (float)nmax;
+            const int l = v > 0 ? nearest_int(v < nmax_f ? v : nmax_f) : 0;
+            Laux[i] = (uint8_t)l;
+            const float w = weights[i];
+            const float lf = (float)l;
+            sum_l += w * lf;
+            sum_l2 += w * lf * lf;
+            sum_xl += w * lf * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) { this_min = 0; this_scale = sum_xl / sum_l2; }
+            float cur_error = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * (float)Laux[i] + this_min - x[i];
+                diff = use_mad ? fabsf(diff) : diff * diff;
+                cur_error += weights[i] * diff;
+            }
+            if (cur_error < best_error) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_error = cur_error;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+    *the_min = -min;
+    return scale;
+}
+
+/* makeQkx3Quants, helpers.zig:420-510 (weights always given on this path). */
+static float make_qkx3_quants(int n, int nmax, const float *x, const float *weights, uint8_t *L,
+                              float *the_min, uint8_t *Laux, float rmin, float rdelta, int nstep,
+                              int use_mad) {
+#define X3_W(i) (weights ? weights[i] : x[i] * x[i])
+    float min = x[0], max = x[0];
+    float sum_w = X3_W(0);
+    float sum_x = sum_w * x[0];
+    for (int i = 1; i < n; ++i) {
+        if (x[i] < min) min = x[i];
+        if (x[i] > max) max = x[i];
+        const float w = X3_W(i);
+        sum_w += w;
+        sum_x += w * x[i];
+    }
+    if (min > 0) min = 0;
+    if (max <= min) {
+        memset(L, 0, (size_t)n);
+        *the_min = -min;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / (max - min);
+    float scale = 1 / iscale;
+    float best_mad = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * (x[i] - min));
+        L[i] = (uint8_t)(l < 0 ? 0 : (l > nmax ? nmax : l));
+        float diff = scale * (float)L[i] + min - x[i];
+        diff = use_mad ? fabsf(diff) : diff * diff;
+        best_mad += X3_W(i) * diff;
+    }
+    if (nstep < 1) { *the_min = -min; return scale; }
+    for (int is = 0; is <= nstep; ++is) {
+        iscale = (rmin + rdelta * (float)is + (float)nmax) / (max - min);
+        float sum_l = 0, sum_l2 = 0, sum_xl = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale * (x[i] - min));
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            Laux[i] = (uint8_t)l;
+            const float w = X3_W(i);
+            const float lf = (float)l;
+            sum_l += w * lf;
+            sum_l2 += w * lf * lf;
+            sum_xl += w * lf * x[i];
+        }
+        const float D = sum_w * sum_l2 - sum_l * sum_l;
+        if (D > 0) {
+            float this_scale = (sum_w * sum_xl - sum_x * sum_l) / D;
+            float this_min = (sum_l2 * sum_x - sum_l * sum_xl) / D;
+            if (this_min > 0) { this_min = 0; this_scale = sum_xl / sum_l2; }
+            float mad = 0;
+            for (int i = 0; i < n; ++i) {
+                float diff = this_scale * (float)Laux[i] + this_min - x[i];
+                diff = use_mad ? fabsf(diff) : diff * diff;
+                mad += X3_W(i) * diff;
+            }
+            if (mad < best_mad) {
+                for (int i = 0; i < n; ++i) L[i] = Laux[i];
+                best_mad = mad;
+                scale = this_scale;
+                min = this_min;
+            }
+        }
+    }
+#undef X3_W
+    *the_min = -min;
+    return scale;
+}
+
+/* makeQpQuants, helpers.zig:525-610. */
+static float make_qp_quants(int n, int nmax, const float *x, uint8_t *L, const float *quant_weights) {
+    float max = 0;
+    for (int i = 0; i < n; ++i) max = x[i] > max ? x[i] : max;
+    if (max < GROUP_MAX_EPS) {
+        for (int i = 0; i < n; ++i) L[i] = 0;
+        return 0.0f;
+    }
+    float iscale = (float)nmax / max;
+    for (int i = 0; i < n; ++i) L[i] = (uint8_t)(uint32_t)nearest_int(iscale * x[i]);
+    const float scale = 1 / iscale;
+    float best_mse = 0;
+    for (int i = 0; i < n; ++i) {
+        const float diff = x[i] - scale * (float)L[i];
+        best_mse += quant_weights[i] * diff * diff;
+    }
+    for (int is = -4; is <= 4; ++is) {
+        if (is == 0) continue;
+        const float iscale_is = (0.1f * (float)is + (float)nmax) / max;
+        const float scale_is = 1 / iscale_is;
+        float mse = 0;
+        for (int i = 0; i < n; ++i) {
+            int l = nearest_int(iscale_is * x[i]);
+            l = l < nmax ? l : nmax;
+            const float diff = x[i] - scale_is * (float)l;
+            mse += quant_weights[i] * diff * diff;
+        }
+        if (mse < best_mse) { best_mse = mse; iscale = iscale_is; }
+    }
+    float sumlx = 0, suml2 = 0;
+    for (int i = 0; i < n; ++i) {
+        int l = nearest_int(iscale * x[i]);
+        l = l < nmax ? l : nmax;
+        L[i] = (uint8_t)(uint32_t)l;
+        const float w = quant_weights[i];
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    for (int itry = 0; itry < 5; ++itry) {
+        int n_changed = 0;
+        for (int i = 0; i < n; ++i) {
+            const float w = quant_weights[i];
+            float slx = sumlx - w * x[i] * (float)L[i];
+            float sl2 = suml2 - w * (float)L[i] * (float)L[i];
+            if (slx > 0 && sl2 > 0) {
+                int new_l = nearest_int(x[i] * sl2 / slx);
+                new_l = new_l < nmax ? new_l : nmax;
+                if (new_l != (int)L[i]) {
+                    slx += w * x[i] * (float)new_l;
+                    sl2 += w * (float)new_l * (float)new_l;
+                    if (slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        L[i] = (uint8_t)(uint32_t)new_l;
+                        sumlx = slx;
+                        suml2 = sl2;
+                        ++n_changed;
+                    }
+                }
+            }
+        }
+        if (!n_changed) break;
+    }
+    return suml2 > 0.0f ? sumlx / suml2 : 0.0f;
+}
+
+/* getScaleMinK4, helpers.zig:621-629. */
+static inline void get_scale_min_k4(int j, const uint8_t *q, uint8_t *d, uint8_t *m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t)((q[j + 4] & 0xF) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t)((q[j + 4] >> 4) | ((q[j - 0] >> 6) << 4));
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q4_K: src/ggml/quants/k.zig:330-470 */
+
+/* packScalesK / packScalePair, k.zig:372-390, chunks.zig:614-624. */
+static inline void pack_scale_pair(uint8_t *s, int j, uint8_t ls, uint8_t lm) {
+    if (j < 4) {
+        s[j] = ls;
+        s[j + 4] = lm;
+    } else {
+        s[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+        s[j - 4] |= (uint8_t)((ls >> 4) << 6);
+        s[j - 0] |= (uint8_t)((lm >> 4) << 6);
+    }
+}
+
+void orc_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q4_K *y = (blk_q4_K *)vy;
+    const int64_t nb = k / QK_K;
+    uint8_t L[QK_K], Laux[32];
+    float mins[QK_K / 32], scales[QK_K / 32], weights[32];
+    for (int64_t i = 0; i < nb; ++i) {
+        float max_scale = 0, max_min = 0;
+        for (int j = 0; j < QK_K / 32; ++j) {           /* fitScalesK, k.zig:338-363 */
+            float sum_x2 = 0;
+            for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+            const float av_x = sqrtf(sum_x2 / 32);
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+            scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
+                                         -1.0f, 0.1f, 20, 0);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
+        }
+        memset(y[i].scales, 0, K_SCALE_SIZE);
+        const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t ls = (uint8_t)(uint32_t)nearest_int(inv_scale * scales[j]);
+            uint8_t lm = (uint8_t)(uint32_t)nearest_int(inv_min * mins[j]);
+            ls = ls < 63 ? ls : 63;
+            lm = lm < 63 ? lm : 63;
+            pack_scale_pair(y[i].scales, j, ls, lm);
+        }
+        y[i].d = FP16(max_scale / 63.0f);
+        y[i].dmin = FP16(max_min / 63.0f);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t sc, m;
+            get_scale_min_k4(j, y[i].scales, &sc, &m);
+            const float d = F32(y[i].d) * (float)sc;
+            if (d == 0) continue;
+            const float dm = F32(y[i].dmin) * (float)m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = nearest_int((x[32 * j + ii] + dm) / d);
+                l = l < 0 ? 0 : (l > 15 ? 15 : l);
+                L[32 * j + ii] = (uint8_t)l;
+            }
+        }
+        uint8_t *q = y[i].qs;
+        for (int j = 0; j < QK_K; j += 64) {
+            for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+            q += 32;
+        }
+        x += QK_K;
+    }
+}
+
+void orc_dequantize_row_q4_K(const void *vx, float *y, int64_t k) {
+    const blk_q4_K *x = (const blk_q4_K *)vx;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+        const uint8_t *q = x[i].qs;
+        const float d = F32(x[i].d);
+        const float min = F32(x[i].dmin);
+        int is = 0;
+        uint8_t sc, m;
+        for (int j = 0; j < QK_K; j += 64) {
+            get_scale_min_k4(is + 0, x[i].scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = min * (float)m;
+            get_scale_min_k4(is + 1, x[i].scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = min * (float)m;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)(q[l] & 0xF) - m1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (float)(q[l] >> 4) - m2;
+            q += 32;
+            is += 2;
+        }
+    }
+}
+
+/* quantize_row_q4_K_impl with imatrix: chunks.zig:478-552 (fitScalesKImpl,
+ * q4_KImpl, requantizeK). */
+static void q4_K_impl(const float *x, blk_q4_K *y, int64_t n_per_row, const float *qw_all) {
+    const int64_t nb = n_per_row / QK_K;
+    uint8_t L[QK_K], Laux[32], ls[QK_K / 32], lm[QK_K / 32];
+    float sw[QK_K / 32], mins[QK_K / 32], scales[QK_K / 32], weights[32];
+    for (int64_t i = 0; i < nb; ++i) {
+        float sum_x2 = 0;
+        for (int l = 0; l < QK_K; ++l) sum_x2 += x[l] * x[l];
+        const float sigma2 = 2 * sum_x2 / QK_K;
+        const float av_x = sqrtf(sigma2);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            if (qw_all) {
+                const float *qw = qw_all + QK_K * i + 32 * j;
+                for (int l = 0; l < 32; ++l)
+                    weights[l] = qw[l] * sqrtf(sigma2 + x[32 * j + l] * x[32 * j + l]);
+            } else {
+                for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+            }
+            float sumw = 0;
+            for (int l = 0; l < 32; ++l) sumw += weights[l];
+            sw[j] = sumw;
+            scales[j] = make_qkx3_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
+                                         -0.9f, 0.05f, 36, 0);
+        }
+        const float d_block = make_qp_quants(QK_K / 32, 63, scales, ls, sw);
+        const float m_block = make_qp_quants(QK_K / 32, 63, mins, lm, sw);
+        memset(y[i].scales, 0, K_SCALE_SIZE);
+        for (int j = 0; j < QK_K / 32; ++j) pack_scale_pair(y[i].scales, j, ls[j], lm[j]);
+        y[i].d = FP16(d_block);
+        y[i].dmin = FP16(m_block);
+        const float d_all = F32(y[i].d), dmin_all = F32(y[i].dmin);
+        for (int j = 0; j < QK_K / 32; ++j) {
+            uint8_t sc, m;
+            get_scale_min_k4(j, y[i].scales, &sc, &m);
+            const float d = d_all * (float)sc;
+            if (d == 0) continue;
+            const float dm = dmin_all * (float)m;
+            for (int ii = 0; ii < 32; ++ii) {
+                int l = nearest_int((x[32 * j + ii] + dm) / d);
+                l = l < 0 ? 0 : (l > 15 ? 15 : l);
+                L[32 * j + ii] = (uint8_t)l;
+            }
+        }
+        uint8_t *q = y[i].qs;
+        for (int j = 0; j < QK_K; j += 64) {
+            for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+            q += 32;
+        }
+        x += QK_K;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q6_K: k.zig:585-696, chunks.zig:642-712 */
+
+static void q6_K_common(const float *x, blk_q6_K *y, int64_t k, const float *qw_all) {
+    const int64_t nb = k / QK_K;
+    int8_t L[QK_K];
+    float scales[QK_K / 16];
+    for (int64_t i = 0; i < nb; ++i) {
+        float max_scale = 0, max_abs_scale = 0;
+        for (int ib = 0; ib < QK_K / 16; ++ib) {
+            const float scale = make_qx_quants(16, 32, x + 16 * ib, L + 16 * ib, 1,
+                                               qw_all ? qw_all + QK_K * i + 16 * ib : NULL);
+            scales[ib] = scale;
+            const float abs_scale = fabsf(scale);
+            if (abs_scale > max_abs_scale) { max_abs_scale = abs_scale; max_scale = scale; }
+        }
+        if (max_abs_scale < GROUP_MAX_EPS) {
+            memset(&y[i], 0, sizeof(blk_q6_K));
+            y[i].d = FP16(0.0f);
+            x += QK_K;
+            continue;
+        }
+        const float iscale = -128.0f / max_scale;
+        y[i].d = FP16(1 / iscale);
+        for (int ib = 0; ib < QK_K / 16; ++ib) {
+            const int v = nearest_int(iscale * scales[ib]);
+            y[i].scales[ib] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < QK_K / 16; ++j) {
+            const float d = F32(y[i].d) * (float)y[i].scales[j];
+            if (d == 0) continue;
+            for (int ii = 0; ii < 16; ++ii) {
+                int l = nearest_int(x[16 * j + ii] / d);
+                l = l < -32 ? -32 : (l > 31 ? 31 : l);
+                L[16 * j + ii] = (int8_t)(l + 32);
+            }
+        }
+        uint8_t *ql = y[i].ql, *qh = y[i].qh;
+        for (int j = 0; j < QK_K; j += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t q1 = (uint8_t)L[j + l + 0] & 0xF;
+                const uint8_t q2 = (uint8_t)L[j + l + 32] & 0xF;
+                const uint8_t q3 = (uint8_t)L[j + l + 64] & 0xF;
+                const uint8_t q4 = (uint8_t)L[j + l + 96] & 0xF;
+                ql[l + 0] = (uint8_t)(q1 | (q3 << 4));
+                ql[l + 32] = (uint8_t)(q2 | (q4 << 4));
+                qh[l] = (uint8_t)(((uint8_t)L[j + l] >> 4) | (((uint8_t)L[j + l + 32] >> 4) << 2) |
+                                  (((uint8_t)L[j + l + 64] >> 4) << 4) | (((uint8_t)L[j + l + 96] >> 4) << 6));
+            }
+            ql += 64;
+            qh += 32;
+        }
+        x += QK_K;
+    }
+}
+
+void orc_quantize_row_q6_K_ref(const float *x, void *y, int64_t k) { q6_K_common(x, (blk_q6_K *)y, k, NULL); }
+
+void orc_dequantize_row_q6_K(const void *vx, float *y, int64_t k) {
+    const blk_q6_K *x = (const blk_q6_K *)vx;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = F32(x[i].d);
+        const uint8_t *ql = x[i].ql, *qh = x[i].qh;
+        const int8_t *sc = x[i].scales;
+        for (int n = 0; n < QK_K; n += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int8_t q1 = (int8_t)((ql[l + 0] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int8_t q2 = (int8_t)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int8_t q3 = (int8_t)((ql[l + 0] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int8_t q4 = (int8_t)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                y[l + 0] = d * (float)sc[is + 0] * (float)q1;
+                y[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                y[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                y[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0 / Q8_1: src/ggml/quants/legacy.zig:407-484 */
+
+void orc_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    const int64_t nb = k / QK8_0;
+    for (int64_t i = 0; i < nb; ++i) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_0; ++j) amax = fmaxf(amax, fabsf(x[i * QK8_0 + j]));
+        const float d = amax / (float)((1 << 7) - 1);
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = FP16(d);
+        for (int j = 0; j < QK8_0; ++j) y[i].qs[j] = trunc_i8(roundf(x[i * QK8_0 + j] * id));
+    }
+}
+
+void orc_dequantize_row_q8_0(const void *vx, float *y, int64_t k) {
+    const blk_q8_0 *x = (const blk_q8_0 *)vx;
+    const int64_t nb = k / QK8_0;
+    for (int64_t i = 0; i < nb; ++i) {
+        const float d = F32(x[i].d);
+        for (int j = 0; j < QK8_0; ++j) y[i * QK8_0 + j] = (float)x[i].qs[j] * d;
+    }
+}
+
+void orc_quantize_row_q8_1_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_1 *y = (blk_q8_1 *)vy;
+    const int64_t nb = k / QK8_1;
+    for (int64_t i = 0; i < nb; ++i) {
+        float amax = 0.0f;
+        for (int j = 0; j < QK8_1; ++j) amax = fmaxf(amax, fabsf(x[i * QK8_1 + j]));
+        const float d = amax / (float)((1 << 7) - 1);
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = FP16(d);
+        int sum = 0;
+        for (int j = 0; j < QK8_1 / 2; ++j) {
+            const float v0 = x[i * QK8_1 + j] * id;
+            const float v1 = x[i * QK8_1 + QK8_1 / 2 + j] * id;
+            y[i].qs[j] = trunc_i8(roundf(v0));
+            y[i].qs[QK8_1 / 2 + j] = trunc_i8(roundf(v1));
+            sum += y[i].qs[j];
+            sum += y[i].qs[QK8_1 / 2 + j];
+        }
+        y[i].s = FP16((float)sum * d);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_K: k.zig:710-760 */
+
+void orc_quantize_row_q8_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q8_K *y = (blk_q8_K *)vy;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i) {
+        float max = 0, amax = 0;
+        for (int j = 0; j < QK_K; ++j) {
+            const float ax = fabsf(x[j]);
+            if (ax > amax) { amax = ax; max = x[j]; }
+        }
+        if (amax == 0) {
+            /* bsums left untouched, as the reference does (k.zig:727-733) */
+            y[i].d = 0;
+            memset(y[i].qs, 0, QK_K);
+            x += QK_K;
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < QK_K; ++j) {
+            const int v = nearest_int(iscale * x[j]);
+            y[i].qs[j] = (int8_t)(v < 127 ? v : 127);
+        }
+        for (int j = 0; j < QK_K / 16; ++j) {
+            int sum = 0;
+            for (int ii = 0; ii < 16; ++ii) sum += y[i].qs[j * 16 + ii];
+            y[i].bsums[j] = (int16_t)sum;
+        }
+        y[i].d = 1 / iscale;
+        x += QK_K;
+    }
+}
+
+void orc_dequantize_row_q8_K(const void *vx, float *y, int64_t k) {
+    const blk_q8_K *x = (const blk_q8_K *)vx;
+    const int64_t nb = k / QK_K;
+    for (int64_t i = 0; i < nb; ++i)
+        for (int j = 0; j < QK_K; ++j) *y++ = x[i].d * (float)x[i].qs[j];
+}
+
+/* ggml_quantize_chunk for the three weight types (chunks.zig:99-128, 289-305,
+ * 716-724): without an imatrix the whole buffer goes through the reference
+ * quantizer; with one, q4_K / q6_K run their impls row by row.  q8_0 ignores it. */
+size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, int64_t nrows,
+                          int64_t n_per_row, const float *imatrix) {
+    const size_t row_size = orc_row_size(type, n_per_row);
+    const int64_t start_row = start / n_per_row;
+    uint8_t *out = (uint8_t *)dst + (size_t)start_row * row_size;
+    src += start;
+    switch (type) {
+    case ORC_TYPE_Q8_0:
+        orc_quantize_row_q8_0_ref(src, out, nrows * n_per_row);
+        break;
+    case ORC_TYPE_Q4_K:
+        if (!imatrix) orc_quantize_row_q4_K_ref(src, out, nrows * n_per_row);
+        else for (int64_t r = 0; r < nrows; ++r)
+            q4_K_impl(src + r * n_per_row, (blk_q4_K *)(out + (size_t)r * row_size), n_per_row, imatrix);
+        break;
+    case ORC_TYPE_Q6_K:
+        if (!imatrix) orc_quantize_row_q6_K_ref(src, out, nrows * n_per_row);
+        else for (int64_t r = 0; r < nrows; ++r)
+            q6_K_common(src + r * n_per_row, (blk_q6_K *)(out + (size_t)r * row_size), n_per_row, imatrix);
+        break;
+    default:
+        return 0;
+    }
+    return (size_t)nrows * row_size;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Generic dot products: src/ggml/cpu/quants/k.zig:146-177, 269-353, 377-438;
+ * cpu/quants/legacy.zig:563-599. */
+
+typedef struct {
+    int8_t aux8[QK_K];
+    int16_t aux16[8];
+    int32_t aux32[8];
+    float sums[8]; /* not reset between super-blocks */
+} dot_scratch;
+
+static inline void scratch_accumulate(dot_scratch *s, int32_t scale, const int8_t *q8, const int8_t *a) {
+    for (int l = 0; l < 8; ++l) s->aux16[l] = (int16_t)(q8[l] * a[l]);
+    for (int l = 0; l < 8; ++l) s->aux32[l] += scale * s->aux16[l];
+}
+
+static float vec_dot_q4_K_q8_K_generic(int n, const void *vx, const void *vy) {
+    const blk_q4_K *x = (const blk_q4_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    dot_scratch sc;
+    memset(&sc, 0, sizeof sc);
+    float sumf = 0;
+    for (int i = 0; i < nb; ++i) {
+        memset(sc.aux32, 0, sizeof sc.aux32);
+        int a = 0, q4 = 0;
+        for (int c = 0; c < QK_K / 64; ++c) {
+            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(x[i].qs[q4 + l] & 0xF);
+            a += 32;
+            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(x[i].qs[q4 + l] >> 4);
+            a += 32;
+            q4 += 32;
+        }
+        uint8_t scales[8], mins[8];
+        for (int j = 0; j < 8; ++j) get_scale_min_k4(j, x[i].scales, &scales[j], &mins[j]);
+        int32_t sumi = 0;
+        for (int j = 0; j < QK_K / 16; ++j) sumi += (int32_t)y[i].bsums[j] * mins[j / 2];
+        a = 0;
+        int q8 = 0;
+        for (int j = 0; j < QK_K / 32; ++j) {
+            const int32_t scale = scales[j];
+            for (int l = 0; l < 4; ++l) { scratch_accumulate(&sc, scale, y[i].qs + q8, sc.aux8 + a); q8 += 8; a += 8; }
+        }
+        const float d = F32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sc.sums[l] += d * (float)sc.aux32[l];
+        const float dmin = F32(x[i].dmin) * y[i].d;
+        sumf -= dmin * (float)sumi;
+    }
+    for (int l = 0; l < 8; ++l) sumf += sc.sums[l];
+    return sumf;
+}
+
+static float vec_dot_q6_K_q8_K_generic(int n, const void *vx, const void *vy) {
+    const blk_q6_K *x = (const blk_q6_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    dot_scratch sc;
+    memset(&sc, 0, sizeof sc);
+    for (int i = 0; i < nb; ++i) {
+        memset(sc.aux32, 0, sizeof sc.aux32);
+        int a = 0, q4 = 0, qh = 0;
+        for (int j = 0; j < QK_K; j += 128) {
+            for (int l = 0; l < 32; ++l) {
+                const uint8_t h = x[i].qh[qh + l];
+                sc.aux8[a + l + 0] = (int8_t)((x[i].ql[q4 + l + 0] & 0xF) | (((h >> 0) & 3) << 4)) - 32;
+                sc.aux8[a + l + 32] = (int8_t)((x[i].ql[q4 + l + 32] & 0xF) | (((h >> 2) & 3) << 4)) - 32;
+                sc.aux8[a + l + 64] = (int8_t)((x[i].ql[q4 + l + 0] >> 4) | (((h >> 4) & 3) << 4)) - 32;
+                sc.aux8[a + l + 96] = (int8_t)((x[i].ql[q4 + l + 32] >> 4) | (((h >> 6) & 3) << 4)) - 32;
+            }
+            a += 128;
+            q4 += 64;
+            qh += 32;
+        }
+        a = 0;
+        int q8 = 0;
+        for (int is = 0; is < QK_K / 16; ++is) {
+            const int32_t scale = x[i].scales[is];
+            scratch_accumulate(&sc, scale, y[i].qs + q8, sc.aux8 + a); q8 += 8; a += 8;
+            scratch_accumulate(&sc, scale, y[i].qs + q8, sc.aux8 + a); q8 += 8; a += 8;
+        }
+        const float d = F32(x[i].d) * y[i].d;
+        for (int l = 0; l < 8; ++l) sc.sums[l] += d * (float)sc.aux32[l];
+    }
+    float sumf = 0;
+    for (int l = 0; l < 8; ++l) sumf += sc.sums[l];
+    return sumf;
+}
+
+static float vec_dot_q8_0_q8_0_generic(int n, const void *vx, const void *vy) {
+    const blk_q8_0 *x = (const blk_q8_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    const int nb = n / QK8_0;
+    float sumf = 0;
+    for (int ib = 0; ib < nb; ++ib) {
+        int32_t sumi = 0;
+        for (int j = 0; j < QK8_0; ++j) sumi += (int32_t)x[ib].qs[j] * y[ib].qs[j];
+        sumf += (float)sumi * (F32(x[ib].d) * F32(y[ib].d));
+    }
+    return sumf;
+}
+
+/* ------------------------------------------------------------------------ */
+/* x86 AVX2 kernels: src/ggml/cpu/quants/x86/{k,legacy,rows,common}.zig.
+ * Compiled with target attributes so the file still builds for hosts without
+ * AVX2; orc_has_avx2() gates their use. */
+#if ORC_X86
+#define AVX2_FN __attribute__((target("avx2,fma,f16c")))
+
+/* hsum_float_8, x86/common.zig:36-42 */
+AVX2_FN static inline float hsum_float_8(__m256 x) {
+    __m128 res = _mm256_extractf128_ps(x, 1);
+    res = _mm_add_ps(res, _mm256_castps256_ps128(x));
+    res = _mm_add_ps(res, _mm_movehl_ps(res, res));
+    res = _mm_add_ss(res, _mm_movehdup_ps(res));
+    return _mm_cvtss_f32(res);
+}
+
+/* get_scale_shuffle_k4 (x86/common.zig:64-77): control bytes 2i,2i+1 repeated. */
+AVX2_FN static inline __m256i scale_shuffle_k4(int i) {
+    return _mm256_set1_epi16((short)((2 * i) | ((2 * i + 1) << 8)));
+}
+
+/* get_scale_shuffle (x86/common.zig:153-163): byte i repeated 8 times, twice (i=2r, 2r+1). */
+AVX2_FN static inline __m128i scale_shuffle_q6(int i) {
+    return _mm_set_epi8((char)(2 * i + 1), (char)(2 * i + 1), (char)(2 * i + 1), (char)(2 * i + 1),
+                        (char)(2 * i + 1), (char)(2 * i + 1), (char)(2 * i + 1), (char)(2 * i + 1),
+                        (char)(2 * i), (char)(2 * i), (char)(2 * i), (char)(2 * i),
+                        (char)(2 * i), (char)(2 * i), (char)(2 * i), (char)(2 * i));
+}
+
+/* unpackScales, x86/common.zig:168-182 */
+static inline void unpack_scales_k4(const uint8_t *packed, uint32_t utmp[4]) {
+    const uint32_t kmask1 = 0x3f3f3f3f, kmask2 = 0x0f0f0f0f, kmask3 = 0x03030303;
+    memcpy(utmp, packed, 12);
+    utmp[3] = ((utmp[2] >> 4) & kmask2) | (((utmp[1] >> 6) & kmask3) << 4);
+    const uint32_t uaux = utmp[1] & kmask1;
+    utmp[1] = (utmp[2] & kmask2) | (((utmp[0] >> 6) & kmask3) << 4);
+    utmp[2] = uaux;
+    utmp[0] &= kmask1;
+}
+
+/* ggml_vec_dot_q4_K_q8_K AVX2 arm, x86/k.zig:256-343 */
+AVX2_FN static float vec_dot_q4_K_q8_K_avx2(int n, const void *vx, const void *vy) {
+    const blk_q4_K *x = (const blk_q4_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m256i m4 = _mm256_set1_epi8(0xF);
+    __m256 acc = _mm256_setzero_ps();
+    __m128 acc_m = _mm_setzero_ps();
+    for (int i = 0; i < nb; ++i) {
+        const float d = y[i].d * F32(x[i].d);
+        const float dmin = -y[i].d * F32(x[i].dmin);
+        uint32_t utmp[4];
+        unpack_scales_k4(x[i].scales, utmp);
+        const uint8_t *q4 = x[i].qs;
+        const int8_t *q8 = y[i].qs;
+        const __m256i mins_and_scales = _mm256_cvtepu8_epi16(
+            _mm_set_epi32((int)utmp[3], (int)utmp[2], (int)utmp[1], (int)utmp[0]));
+        const __m256i q8sums = _mm256_loadu_si256((const __m256i *)y[i].bsums);
+        const __m128i q8s = _mm_hadd_epi16(_mm256_extracti128_si256(q8sums, 0), _mm256_extracti128_si256(q8sums, 1));
+        const __m128i prod = _mm_madd_epi16(_mm256_extracti128_si256(mins_and_scales, 1), q8s);
+        acc_m = _mm_fmadd_ps(_mm_set1_ps(dmin), _mm_cvtepi32_ps(prod), acc_m);
+        const __m128i sc128 = _mm256_extracti128_si256(mins_and_scales, 0);
+        const __m256i scales = _mm256_set_m128i(sc128, sc128);
+        __m256i sumi = _mm256_setzero_si256();
+        for (int j = 0; j < QK_K / 64; ++j) {
+            const __m256i scale_l = _mm256_shuffle_epi8(scales, scale_shuffle_k4(2 * j + 0));
+            const __m256i scale_h = _mm256_shuffle_epi8(scales, scale_shuffle_k4(2 * j + 1));
+            const __m256i q4bits = _mm256_loadu_si256((const __m256i *)q4); q4 += 32;
+            const __m256i q4l = _mm256_and_si256(q4bits, m4);
+            const __m256i q4h = _mm256_and_si256(_mm256_srli_epi16(q4bits, 4), m4);
+            const __m256i q8l = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            __m256i p16l = _mm256_maddubs_epi16(q4l, q8l);
+            p16l = _mm256_madd_epi16(scale_l, p16l);
+            const __m256i q8h = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            __m256i p16h = _mm256_maddubs_epi16(q4h, q8h);
+            p16h = _mm256_madd_epi16(scale_h, p16h);
+            sumi = _mm256_add_epi32(sumi, _mm256_add_epi32(p16l, p16h));
+        }
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(sumi), acc);
+    }
+    acc_m = _mm_add_ps(acc_m, _mm_movehl_ps(acc_m, acc_m));
+    acc_m = _mm_add_ss(acc_m, _mm_movehdup_ps(acc_m));
+    return hsum_float_8(acc) + _mm_cvtss_f32(acc_m);
+}
+
+/* ggml_vec_dot_q6_K_q8_K AVX2 arm, x86/k.zig:454-552 */
+AVX2_FN static float vec_dot_q6_K_q8_K_avx2(int n, const void *vx, const void *vy) {
+    const blk_q6_K *x = (const blk_q6_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m256i m3 = _mm256_set1_epi8(3);
+    const __m256i m15 = _mm256_set1_epi8(15);
+    __m256 acc = _mm256_setzero_ps();
+    for (int i = 0; i < nb; ++i) {
+        const float d = y[i].d * F32(x[i].d);
+        const uint8_t *q4 = x[i].ql, *qh = x[i].qh;
+        const int8_t *q8 = y[i].qs;
+        const __m256i q8sums = _mm256_loadu_si256((const __m256i *)y[i].bsums);
+        const __m128i scales = _mm_loadu_si128((const __m128i *)x[i].scales);
+        const __m256i scales_16 = _mm256_cvtepi8_epi16(scales);
+        const __m256i q8sclsub = _mm256_slli_epi32(_mm256_madd_epi16(q8sums, scales_16), 5);
+        __m256i sumi = _mm256_setzero_si256();
+        int is = 0;
+        for (int j = 0; j < QK_K / 128; ++j) {
+            const __m256i q4bits1 = _mm256_loadu_si256((const __m256i *)q4); q4 += 32;
+            const __m256i q4bits2 = _mm256_loadu_si256((const __m256i *)q4); q4 += 32;
+            const __m256i q4bitsH = _mm256_loadu_si256((const __m256i *)qh); qh += 32;
+            const __m256i q4h_0 = _mm256_slli_epi16(_mm256_and_si256(q4bitsH, m3), 4);
+            const __m256i q4h_1 = _mm256_slli_epi16(_mm256_and_si256(q4bitsH, _mm256_set1_epi8(12)), 2);
+            const __m256i q4h_2 = _mm256_and_si256(q4bitsH, _mm256_set1_epi8(48));
+            const __m256i q4h_3 = _mm256_srli_epi16(_mm256_and_si256(q4bitsH, _mm256_set1_epi8(-64)), 2);
+            const __m256i q4_0 = _mm256_or_si256(_mm256_and_si256(q4bits1, m15), q4h_0);
+            const __m256i q4_1 = _mm256_or_si256(_mm256_and_si256(q4bits2, m15), q4h_1);
+            const __m256i q4_2 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(q4bits1, 4), m15), q4h_2);
+            const __m256i q4_3 = _mm256_or_si256(_mm256_and_si256(_mm256_srli_epi16(q4bits2, 4), m15), q4h_3);
+            const __m256i q8_0 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q8_1 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q8_2 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q8_3 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            __m256i p16_0 = _mm256_maddubs_epi16(q4_0, q8_0);
+            __m256i p16_1 = _mm256_maddubs_epi16(q4_1, q8_1);
+            __m256i p16_2 = _mm256_maddubs_epi16(q4_2, q8_2);
+            __m256i p16_3 = _mm256_maddubs_epi16(q4_3, q8_3);
+            const __m128i scale_0 = _mm_shuffle_epi8(scales, scale_shuffle_q6(is + 0));
+            const __m128i scale_1 = _mm_shuffle_epi8(scales, scale_shuffle_q6(is + 1));
+            const __m128i scale_2 = _mm_shuffle_epi8(scales, scale_shuffle_q6(is + 2));
+            const __m128i scale_3 = _mm_shuffle_epi8(scales, scale_shuffle_q6(is + 3));
+            is += 4;
+            p16_0 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(scale_0), p16_0);
+            p16_1 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(scale_1), p16_1);
+            p16_2 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(scale_2), p16_2);
+            p16_3 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(scale_3), p16_3);
+            sumi = _mm256_add_epi32(sumi, _mm256_add_epi32(p16_0, p16_1));
+            sumi = _mm256_add_epi32(sumi, _mm256_add_epi32(p16_2, p16_3));
+        }
+        sumi = _mm256_sub_epi32(sumi, q8sclsub);
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(sumi), acc);
+    }
+    return hsum_float_8(acc);
+}
+
+/* ggml_vec_dot_q8_0_q8_0 AVX2 arm, x86/legacy.zig:537-572 with
+ * mul_sum_i8_pairs_float (x86/common.zig:120-150, non-VNNI arm). */
+AVX2_FN static float vec_dot_q8_0_q8_0_avx2(int n, const void *vx, const void *vy) {
+    const blk_q8_0 *x = (const blk_q8_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    const int nb = n / QK8_0;
+    __m256 acc = _mm256_setzero_ps();
+    for (int ib = 0; ib < nb; ++ib) {
+        const __m256 d = _mm256_set1_ps(F32(x[ib].d) * F32(y[ib].d));
+        const __m256i qx = _mm256_loadu_si256((const __m256i *)x[ib].qs);
+        const __m256i qy = _mm256_loadu_si256((const __m256i *)y[ib].qs);
+        const __m256i ax = _mm256_sign_epi8(qx, qx);
+        const __m256i sy = _mm256_sign_epi8(qy, qx);
+        const __m256i dot = _mm256_maddubs_epi16(ax, sy);
+        const __m256 q = _mm256_cvtepi32_ps(_mm256_madd_epi16(_mm256_set1_epi16(1), dot));
+        acc = _mm256_fmadd_ps(d, q, acc);
+    }
+    return hsum_float_8(acc);
+}
+
+/* quantize_row_q8_0 AVX2 arm, x86/rows.zig:27-105: id = 127/max and
+ * round-half-even, saturating packs. */
+AVX2_FN static void quantize_row_q8_0_avx2_impl(const float *x, void *vy, int64_t k) {
+    blk_q8_0 *y = (blk_q8_0 *)vy;
+    const int64_t nb = k / 32;
+    for (int64_t i = 0; i < nb; ++i) {
+        __m256 v0 = _mm256_loadu_ps(x), v1 = _mm256_loadu_ps(x + 8);
+        __m256 v2 = _mm256_loadu_ps(x + 16), v3 = _mm256_loadu_ps(x + 24);
+        x += 32;
+        const __m256 signBit = _mm256_set1_ps(-0.0f);
+        __m256 maxAbs = _mm256_andnot_ps(signBit, v0);
+        maxAbs = _mm256_max_ps(maxAbs, _mm256_andnot_ps(signBit, v1));
+        maxAbs = _mm256_max_ps(maxAbs, _mm256_andnot_ps(signBit, v2));
+        maxAbs = _mm256_max_ps(maxAbs, _mm256_andnot_ps(signBit, v3));
+        __m128 max4 = _mm_max_ps(_mm256_extractf128_ps(maxAbs, 1), _mm256_castps256_ps128(maxAbs));
+        max4 = _mm_max_ps(max4, _mm_movehl_ps(max4, max4));
+        max4 = _mm_max_ss(max4, _mm_movehdup_ps(max4));
+        const float max_scalar = _mm_cvtss_f32(max4);
+        const float d = max_scalar / 127.f;
+        y[i].d = FP16(d);
+        const float id = (max_scalar != 0.0f) ? 127.f / max_scalar : 0.0f;
+        const __m256 mul = _mm256_set1_ps(id);
+        v0 = _mm256_round_ps(_mm256_mul_ps(v0, mul), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        v1 = _mm256_round_ps(_mm256_mul_ps(v1, mul), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        v2 = _mm256_round_ps(_mm256_mul_ps(v2, mul), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        v3 = _mm256_round_ps(_mm256_mul_ps(v3, mul), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC);
+        __m256i i0 = _mm256_cvtps_epi32(v0);
+        const __m256i i1 = _mm256_cvtps_epi32(v1);
+        __m256i i2 = _mm256_cvtps_epi32(v2);
+        const __m256i i3 = _mm256_cvtps_epi32(v3);
+        i0 = _mm256_packs_epi32(i0, i1);
+        i2 = _mm256_packs_epi32(i2, i3);
+        i0 = _mm256_packs_epi16(i0, i2);
+        const __m256i perm = _mm256_setr_epi32(0, 4, 1, 5, 2, 6, 3, 7);
+        i0 = _mm256_permutevar8x32_epi32(i0, perm);
+        _mm256_storeu_si256((__m256i *)y[i].qs, i0);
+    }
+}
+#endif /* ORC_X86 */
+
+int orc_has_avx2(void) {
+#if ORC_X86
+    __builtin_cpu_init();
+    return __builtin_cpu_supports("avx2") && __builtin_cpu_supports("fma") && __builtin_cpu_supports("f16c");
+#else
+    return 0;
+#endif
+}
+
+void orc_quantize_row_q8_0_avx2(const float *x, void *y, int64_t k) {
+#if ORC_X86
+    if (orc_has_avx2()) { quantize_row_q8_0_avx2_impl(x, y, k); return; }
+#endif
+    orc_quantize_row_q8_0_ref(x, y, k);
+}
+
+typedef float (*dot_fn)(int, const void *, const void *);
+typedef void (*from_float_fn)(const float *, void *, int64_t);
+
+static dot_fn pick_dot(int type, int impl) {
+#if ORC_X86
+    if (impl == ORC_IMPL_AVX2 && orc_has_avx2()) {
+        switch (type) {
+        case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_avx2;
+        case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_avx2;
+        case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_avx2;
+        }
+    }
+#endif
+    (void)impl;
+    switch (type) {
+    case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_generic;
+    case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_generic;
+    case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_generic;
+    }
+    return NULL;
+}
+
+/* vec_dot_type and from_float per cpu/traits.zig:158-201 and x86/rows.zig:
+ * K-quants take Q8_K (scalar ref on x86 too); Q8_0 takes Q8_0 (AVX2 row
+ * quantizer on x86, the reference quantizer in the generic build). */
+static int vec_dot_type(int type) { return type == ORC_TYPE_Q8_0 ? ORC_TYPE_Q8_0 : ORC_TYPE_Q8_K; }
+static from_float_fn pick_from_float(int type, int impl) {
+    if (type == ORC_TYPE_Q8_0) return impl == ORC_IMPL_AVX2 ? orc_quantize_row_q8_0_avx2 : orc_quantize_row_q8_0_ref;
+    return orc_quantize_row_q8_K_ref;
+}
+
+float orc_vec_dot(int type, int impl, int n, const void *vx, const void *vy) {
+    dot_fn f = pick_dot(type, impl);
+    return f ? f(n, vx, vy) : NAN;
+}
+
+/* ------------------------------------------------------------------------ */
+/* GPU semantics against Q8_1 activations (the device kernels' contract). */
+
+void orc_block_dots_q8_1(int type, const void *w, int64_t nrows, int64_t K, const void *vy, int32_t *out) {
+    const blk_q8_1 *y = (const blk_q8_1 *)vy;
+    const size_t rs = orc_row_size(type, K);
+    for (int64_t r = 0; r < nrows; ++r) {
+        const uint8_t *row = (const uint8_t *)w + (size_t)r * rs;
+        if (type == ORC_TYPE_Q4_K) {
+            const blk_q4_K *x = (const blk_q4_K *)row;
+            for (int64_t b = 0; b < K / QK_K; ++b)
+                for (int j = 0; j < 8; ++j) {
+                    const blk_q8_1 *yb = &y[b * 8 + j];
+                    int32_t s = 0;
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t byte = x[b].qs[32 * (j / 2) + l];
+                        const int q = (j & 1) ? (byte >> 4) : (byte & 0xF);
+                        s += q * yb->qs[l];
+                    }
+                    *out++ = s;
+                }
+        } else if (type == ORC_TYPE_Q6_K) {
+            const blk_q6_K *x = (const blk_q6_K *)row;
+            for (int64_t b = 0; b < K / QK_K; ++b) {
+                int8_t q6[QK_K];
+                for (int n = 0; n < 2; ++n)
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t *ql = x[b].ql + 64 * n, *qh = x[b].qh + 32 * n;
+                        q6[128 * n + l + 0] = (int8_t)(((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32);
+                        q6[128 * n + l + 32] = (int8_t)(((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32);
+                        q6[128 * n + l + 64] = (int8_t)(((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32);
+                        q6[128 * n + l + 96] = (int8_t)(((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32);
+                    }
+                for (int k = 0; k < 16; ++k) {
+                    const blk_q8_1 *yb = &y[b * 8 + k / 2];
+                    int32_t s = 0;
+                    for (int l = 0; l < 16; ++l) s += q6[16 * k + l] * yb->qs[16 * (k & 1) + l];
+                    *out++ = s;
+                }
+            }
+        } else if (type == ORC_TYPE_Q8_0) {
+            const blk_q8_0 *x = (const blk_q8_0 *)row;
+            for (int64_t b = 0; b < K / 32; ++b) {
+                int32_t s = 0;
+                for (int l = 0; l < 32; ++l) s += x[b].qs[l] * y[b].qs[l];
+                *out++ = s;
+            }
+        }
+    }
+}
+
+void orc_mul_mat_q8_1_f64(int type, const void *w, int64_t nrows, int64_t K, const void *vy,
+                          int64_t ncols, double *dst) {
+    const size_t rs = orc_row_size(type, K);
+    const int64_t nsub = type == ORC_TYPE_Q6_K ? K / 16 : K / 32;
+    int32_t *S = (int32_t *)malloc(sizeof(int32_t) * (size_t)nsub);
+    for (int64_t c = 0; c < ncols; ++c) {
+        const blk_q8_1 *y = (const blk_q8_1 *)vy + c * (K / 32);
+        for (int64_t r = 0; r < nrows; ++r) {
+            const uint8_t *row = (const uint8_t *)w + (size_t)r * rs;
+            orc_block_dots_q8_1(type, row, 1, K, y, S);
+            double acc = 0.0;
+            if (type == ORC_TYPE_Q4_K) {
+                const blk_q4_K *x = (const blk_q4_K *)row;
+                for (int64_t b = 0; b < K / QK_K; ++b)
+                    for (int j = 0; j < 8; ++j) {
+                        uint8_t sc, m;
+                        get_scale_min_k4(j, x[b].scales, &sc, &m);
+                        const blk_q8_1 *yb = &y[b * 8 + j];
+                        acc += (double)F32(x[b].d) * sc * F32(yb->d) * S[b * 8 + j] -
+                               (double)F32(x[b].dmin) * m * F32(yb->s);
+                    }
+            } else if (type == ORC_TYPE_Q6_K) {
+                const blk_q6_K *x = (const blk_q6_K *)row;
+                for (int64_t b = 0; b < K / QK_K; ++b)
+                    for (int k = 0; k < 16; ++k)
+                        acc += (double)F32(x[b].d) * x[b].scales[k] * F32(y[b * 8 + k / 2].d) * S[b * 16 + k];
+            } else {
+                const blk_q8_0 *x = (const blk_q8_0 *)row;
+                for (int64_t b = 0; b < K / 32; ++b) acc += (double)F32(x[b].d) * F32(y[b].d) * S[b];
+            }
+            dst[c * nrows + r] = acc;
+        }
+    }
+    free(S);
+}
+
+/* ------------------------------------------------------------------------ */
+/* mul_mat driver: src/ggml/cpu/mulmat.zig:92-423 (oneChunk + chunking). */
+
+typedef struct {
+    int type, impl, nth;
+    const uint8_t *w;
+    int64_t nrows, K, ncols;
+    const float *x;
+    float *dst;
+    uint8_t *wdata;
+    size_t wrow; /* bytes per staged src1 row */
+    atomic_long current_chunk;
+    int64_t nchunk0, nchunk1, dr0, dr1;
+} mm_ctx;
+
+typedef struct { mm_ctx *ctx; int ith; } mm_thread;
+
+static void one_chunk(mm_ctx *c, int64_t ir0_start, int64_t ir0_end, int64_t ir1_start, int64_t ir1_end) {
+    if (ir0_start >= ir0_end || ir1_start >= ir1_end) return;
+    dot_fn dot = pick_dot(c->type, c->impl);
+    const size_t rs = orc_row_size(c->type, c->K);
+    const int64_t blck_0 = 16, blck_1 = 16;
+    float tmp[32];
+    for (int64_t iir1 = ir1_start; iir1 < ir1_end; iir1 += blck_1)
+        for (int64_t iir0 = ir0_start; iir0 < ir0_end; iir0 += blck_0)
+            for (int64_t ir1 = iir1; ir1 < iir1 + blck_1 && ir1 < ir1_end; ++ir1) {
+                const uint8_t *src1_col = c->wdata + (size_t)ir1 * c->wrow;
+                float *dst_col = c->dst + ir1 * c->nrows;
+                for (int64_t ir0 = iir0; ir0 < iir0 + blck_0 && ir0 < ir0_end; ++ir0)
+                    tmp[ir0 - iir0] = dot((int)c->K, c->w + (size_t)ir0 * rs, src1_col);
+                const int64_t end = iir0 + blck_0 < ir0_end ? iir0 + blck_0 : ir0_end;
+                memcpy(dst_col + iir0, tmp, sizeof(float) * (size_t)(end - iir0));
+            }
+}
+
+static void *mm_stage_worker(void *arg) {
+    mm_thread *t = (mm_thread *)arg;
+    mm_ctx *c = t->ctx;
+    const int vdt = vec_dot_type(c->type);
+    from_float_fn ff = pick_from_float(c->type, c->impl);
+    const int64_t bs = orc_blck_size(vdt);
+    const size_t nbw0 = orc_type_size(vdt);
+    const int64_t block_start = (int64_t)t->ith * (c->K / bs) / c->nth;
+    const int64_t block_end = ((int64_t)t->ith + 1) * (c->K / bs) / c->nth;
+    for (int64_t j11 = 0; j11 < c->ncols; ++j11)
+        ff(c->x + j11 * c->K + block_start * bs, c->wdata + (size_t)j11 * c->wrow + (size_t)block_start * nbw0,
+           (block_end - block_start) * bs);
+    return NULL;
+}
+
+static void *mm_compute_worker(void *arg) {
+    mm_thread *t = (mm_thread *)arg;
+    mm_ctx *c = t->ctx;
+    long current_chunk = t->ith;
+    const int64_t nr0 = c->nrows, nr1 = c->ncols;
+    while (current_chunk < c->nchunk0 * c->nchunk1) {
+        const int64_t ith0 = current_chunk % c->nchunk0, ith1 = current_chunk / c->nchunk0;
+        const int64_t ir0_start = c->dr0 * ith0, ir1_start = c->dr1 * ith1;
+        const int64_t ir0_end = ir0_start + c->dr0 < nr0 ? ir0_start + c->dr0 : nr0;
+        const int64_t ir1_end = ir1_start + c->dr1 < nr1 ? ir1_start + c->dr1 : nr1;
+        one_chunk(c, ir0_start, ir0_end, ir1_start, ir1_end);
+        if (c->nth >= c->nchunk0 * c->nchunk1) break;
+        current_chunk = atomic_fetch_add(&c->current_chunk, 1);
+    }
+    return NULL;
+}
+
+static void run_threads(int nth, void *ts, size_t stride, void *(*fn)(void *)) {
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nth);
+    for (int i = 1; i < nth; ++i) pthread_create(&th[i], NULL, fn, (char *)ts + (size_t)i * stride);
+    fn(ts);
+    for (int i = 1; i < nth; ++i) pthread_join(th[i], NULL);
+    free(th);
+}
+
+void orc_mul_mat(int type, int impl, const void *w, int64_t nrows, int64_t K, const float *x,
+                 int64_t ncols, float *dst, int nth) {
+    if (nth < 1) nth = 1;
+    mm_ctx c;
+    memset(&c, 0, sizeof c);
+    c.type = type; c.impl = impl; c.nth = nth; c.w = (const uint8_t *)w;
+    c.nrows = nrows; c.K = K; c.ncols = ncols; c.x = x; c.dst = dst;
+    c.wrow = orc_row_size(vec_dot_type(type), K);
+    c.wdata = (uint8_t *)calloc((size_t)ncols, c.wrow);
+    mm_thread *ts = (mm_thread *)malloc(sizeof(mm_thread) * (size_t)nth);
+    for (int i = 0; i < nth; ++i) { ts[i].ctx = &c; ts[i].ith = i; }
+    run_threads(nth, ts, sizeof *ts, mm_stage_worker);
+    const int64_t nr0 = nrows, nr1 = ncols;
+    int64_t chunk_size = (nr0 == 1 || nr1 == 1) ? 64 : 16;
+    int64_t nchunk0 = (nr0 + chunk_size - 1) / chunk_size;
+    int64_t nchunk1 = (nr1 + chunk_size - 1) / chunk_size;
+    if (nchunk0 * nchunk1 < (int64_t)nth * 4) {
+        nchunk0 = nr0 > nr1 ? nth : 1;
+        nchunk1 = nr0 > nr1 ? 1 : nth;
+    }
+    c.nchunk0 = nchunk0; c.nchunk1 = nchunk1;
+    c.dr0 = (nr0 + nchunk0 - 1) / nchunk0;
+    c.dr1 = (nr1 + nchunk1 - 1) / nchunk1;
+    atomic_store(&c.current_chunk, nth);
+    run_threads(nth, ts, sizeof *ts, mm_compute_worker);
+    free(ts);
+    free(c.wdata);
+}
+
+/* mul_mat_id driver: mulmat.zig:429-777 (grouping by expert, -1 -> zero row). */
+
+typedef struct { int32_t i1, i2; } row_mapping;
+
+typedef struct {
+    int type, impl, nth;
+    const uint8_t *w;
+    int64_t n_as, nrows, K, ne11, n_tokens, n_ids;
+    const float *x;
+    const int32_t *ids;
+    float *dst;
+    uint8_t *wdata;
+    size_t wrow;
+    int64_t *counts;
+    row_mapping *rows;
+    atomic_long *chunk;
+} mmid_ctx;
+
+typedef struct { mmid_ctx *ctx; int ith; } mmid_thread;
+
+static void *mmid_stage_worker(void *arg) {
+    mmid_thread *t = (mmid_thread *)arg;
+    mmid_ctx *c = t->ctx;
+    const int vdt = vec_dot_type(c->type);
+    from_float_fn ff = pick_from_float(c->type, c->impl);
+    const int64_t bs = orc_blck_size(vdt);
+    const size_t nbw0 = orc_type_size(vdt);
+    const int64_t block_start = (int64_t)t->ith * (c->K / bs) / c->nth;
+    const int64_t block_end = ((int64_t)t->ith + 1) * (c->K / bs) / c->nth;
+    for (int64_t r = 0; r < c->ne11 * c->n_tokens; ++r)
+        ff(c->x + r * c->K + block_start * bs, c->wdata + (size_t)r * c->wrow + (size_t)block_start * nbw0,
+           (block_end - block_start) * bs);
+    return NULL;
+}
+
+static void *mmid_compute_worker(void *arg) {
+    mmid_thread *t = (mmid_thread *)arg;
+    mmid_ctx *c = t->ctx;
+    dot_fn dot = pick_dot(c->type, c->impl);
+    const size_t rs = orc_row_size(c->type, c->K);
+    const int nth = c->nth;
+    for (int64_t cur_a = 0; cur_a < c->n_as; ++cur_a) {
+        const int64_t cne1 = c->counts[cur_a];
+        if (cne1 == 0) continue;
+        const uint8_t *src0_cur = c->w + (size_t)cur_a * (size_t)c->nrows * rs;
+        const int64_t nr0 = c->nrows, nr1 = cne1;
+        int64_t chunk_size = (nr0 == 1 || nr1 == 1) ? 64 : 16;
+        int64_t nchunk0 = (nr0 + chunk_size - 1) / chunk_size;
+        int64_t nchunk1 = (nr1 + chunk_size - 1) / chunk_size;
+        if (nchunk0 * nchunk1 < (int64_t)nth * 4) {
+            nchunk0 = nr0 > nr1 ? nth : 1;
+            nchunk1 = nr0 > nr1 ? 1 : nth;
+        }
+        const int64_t dr0 = (nr0 + nchunk0 - 1) / nchunk0, dr1 = (nr1 + nchunk1 - 1) / nchunk1;
+        long current_chunk = t->ith;
+        while (current_chunk < nchunk0 * nchunk1) {
+            const int64_t ith0 = current_chunk % nchunk0, ith1 = current_chunk / nchunk0;
+            const int64_t ir0_start = dr0 * ith0, ir1_start = dr1 * ith1;
+            const int64_t ir0_end = ir0_start + dr0 < nr0 ? ir0_start + dr0 : nr0;
+            const int64_t ir1_end = ir1_start + dr1 < nr1 ? ir1_start + dr1 : nr1;
+            for (int64_t ir1 = ir1_start; ir1 < ir1_end; ++ir1) {
+                const row_mapping rm = c->rows[cur_a * c->n_ids * c->n_tokens + ir1];
+                const int64_t j11 = rm.i1 % c->ne11, j12 = rm.i2;
+                const uint8_t *src1_col = c->wdata + (size_t)(j11 + j12 * c->ne11) * c->wrow;
+                float *dst_col = c->dst + ((int64_t)rm.i2 * c->n_ids + rm.i1) * c->nrows;
+                for (int64_t ir0 = ir0_start; ir0 < ir0_end; ++ir0)
+                    dst_col[ir0] = dot((int)c->K, src0_cur + (size_t)ir0 * rs, src1_col);
+            }
+            if (nth >= nchunk0 * nchunk1) break;
+            current_chunk = atomic_fetch_add(&c->chunk[cur_a], 1);
+        }
+    }
+    return NULL;
+}
+
+void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nrows, int64_t K,
+                    const float *x, int64_t ne11, int64_t n_tokens, const int32_t *ids, int64_t n_ids,
+                    float *dst, int nth) {
+    if (nth < 1) nth = 1;
+    mmid_ctx c;
+    memset(&c, 0, sizeof c);
+    c.type = type; c.impl = impl; c.nth = nth; c.w = (const uint8_t *)w;
+    c.n_as = n_as; c.nrows = nrows; c.K = K; c.ne11 = ne11; c.n_tokens = n_tokens; c.n_ids = n_ids;
+    c.x = x; c.ids = ids; c.dst = dst;
+    c.wrow = orc_row_size(vec_dot_type(type), K);
+    c.wdata = (uint8_t *)calloc((size_t)(ne11 * n_tokens), c.wrow);
+    c.counts = (int64_t *)calloc((size_t)n_as, sizeof(int64_t));
+    c.rows = (row_mapping *)calloc((size_t)(n_as * n_ids * n_tokens), sizeof(row_mapping));
+    c.chunk = (atomic_long *)calloc((size_t)n_as, sizeof(atomic_long));
+    mmid_thread *ts = (mmid_thread *)malloc(sizeof(mmid_thread) * (size_t)nth);
+    for (int i = 0; i < nth; ++i) { ts[i].ctx = &c; ts[i].ith = i; }
+    run_threads(nth, ts, sizeof *ts, mmid_stage_worker);
+    for (int64_t t = 0; t < n_tokens; ++t)
+        for (int64_t s = 0; s < n_ids; ++s) {
+            const int32_t e = ids[t * n_ids + s];
+            if (e == -1) {
+                memset(dst + (t * n_ids + s) * nrows, 0, sizeof(float) * (size_t)nrows);
+                continue;
+            }
+            c.rows[e * n_ids * n_tokens + c.counts[e]] = (row_mapping){(int32_t)s, (int32_t)t};
+            c.counts[e] += 1;
+        }
+    for (int64_t a = 0; a < n_as; ++a) atomic_store(&c.chunk[a], nth);
+    run_threads(nth, ts, sizeof *ts, mmid_compute_worker);
+    free(ts);
+    free(c.chunk);
+    free(c.rows);
+    free(c.counts);
+    free(c.wdata);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Synthetic inputs: SplitMix64 (public-domain generator by S. Vigna) feeding
+ * Box-Muller in double precision, rounded to f32. */
+
+static uint64_t splitmix64(uint64_t *s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out) {
+    uint64_t s = seed;
+    const double two_pi = 6.283185307179586476925286766559;
+    for (int64_t i = 0; i < n; i += 2) {
+        const double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740992.0); /* (0,1] */
+        const double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);       /* [0,1) */
+        const double r = sqrt(-2.0 * log(u1));
+        out[i] = (float)(mean + stddev * r * cos(two_pi * u2));
+        if (i + 1 < n) out[i + 1] = (float)(mean + stddev * r * sin(two_pi * u2));
+    }
+}

@@ -1,0 +1,100 @@
+/*
+ * qmm_oracle.h -- CPU restatement of the reference's quantized-matmul path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
+ * backend, the Python host mirror) may link, load or call this.  Only the
+ * tests, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and
+ * only as the checker / CPU baseline.
+ *
+ * Every function restates, in plain C, the algorithm of the reference file
+ * named in its comment (paths relative to the mlavergn/llama.zig root).  The
+ * reference is Zig-only and its C headers come from an empty submodule, so it
+ * cannot be built here; the restatement is pinned instead against the golden
+ * vectors the reference's own tests hold (src/ggml/quants/golden.zig and
+ * src/ggml/cpu/quants/golden.zig), reproduced bit-for-bit by tests/.
+ */
+#ifndef QMM_ORACLE_H
+#define QMM_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids used on this path (values as the reference's goldens record
+ * them: quants/golden.zig:74-133 `.type = ...`). */
+enum {
+    ORC_TYPE_F32  = 0,
+    ORC_TYPE_Q8_0 = 8,
+    ORC_TYPE_Q8_1 = 9,
+    ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q6_K = 14,
+    ORC_TYPE_Q8_K = 15,
+};
+
+/* Implementation selector for the dot-product drivers. */
+enum {
+    ORC_IMPL_GENERIC = 0, /* ggml_vec_dot_*_generic + reference row quantizers */
+    ORC_IMPL_AVX2    = 1, /* the reference's x86 AVX2 kernels (arch/x86)       */
+};
+
+size_t   orc_type_size(int type);   /* bytes per block */
+int64_t  orc_blck_size(int type);   /* elements per block */
+size_t   orc_row_size(int type, int64_t ne);
+
+uint16_t orc_fp32_to_fp16(float f);
+float    orc_fp16_to_fp32(uint16_t h);
+int      orc_nearest_int(float f);
+uint64_t orc_fnv1a(const void *p, size_t n);
+
+/* reference quantizers / dequantizers */
+void orc_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_1_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q8_K_ref(const float *x, void *y, int64_t k);
+void orc_dequantize_row_q4_K(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q6_K(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q8_0(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q8_K(const void *x, float *y, int64_t k);
+size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start,
+                          int64_t nrows, int64_t n_per_row, const float *imatrix);
+
+/* x86 row quantizer (round-half-even, id = 127/max) */
+void orc_quantize_row_q8_0_avx2(const float *x, void *y, int64_t k);
+
+/* dot products, reference signature without the nrc/stride arguments */
+float orc_vec_dot(int type, int impl, int n, const void *vx, const void *vy);
+
+/* GPU-semantics block dot: the integer sums the device kernels form against
+ * Q8_1 activations.  Q4_K: one int per 32-sub-block (K/32 per row); Q6_K: one
+ * per 16-sub-block (K/16 per row); Q8_0: one per 32-block. */
+void orc_block_dots_q8_1(int type, const void *w, int64_t nrows, int64_t K,
+                         const void *y_q8_1, int32_t *out);
+/* f64 evaluation of out = sum_b d*sc*d8*S - dmin*m*s8 (Q4_K), d*sc*d8*T (Q6_K),
+ * d*d8*S (Q8_0) against Q8_1 activations (AoS block_q8_1, ncols columns of K). */
+void orc_mul_mat_q8_1_f64(int type, const void *w, int64_t nrows, int64_t K,
+                          const void *y_q8_1, int64_t ncols, double *dst);
+
+/* ggml_compute_forward_mul_mat restated: W [K x nrows] quantized, X [K x ncols]
+ * f32 column-major (x[c*K + k]), dst[c*nrows + r]. */
+void orc_mul_mat(int type, int impl, const void *w, int64_t nrows, int64_t K,
+                 const float *x, int64_t ncols, float *dst, int nth);
+
+/* ggml_compute_forward_mul_mat_id restated.  w: n_as experts, each nrows rows;
+ * x[(t*ne11 + i11)*K + k]; ids[t*n_ids + s]; dst[(t*n_ids + s)*nrows + r]. */
+void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nrows,
+                    int64_t K, const float *x, int64_t ne11, int64_t n_tokens,
+                    const int32_t *ids, int64_t n_ids, float *dst, int nth);
+
+/* synthetic inputs: SplitMix64 -> Box-Muller (double) -> f32 */
+void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out);
+
+int orc_has_avx2(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,163 @@
+"""ctypes wrapper around oracle/liborc_qmm.so -- the CPU checker.
+
+Test infrastructure: imported by tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg only.
+"""
+import ctypes
+import pathlib
+import subprocess
+
+import numpy as np
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+LIB_PATH = ROOT / "oracle" / "liborc_qmm.so"
+
+TYPE_F32, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 8, 9, 12, 14, 15
+TYPE_IDS = {"Q8_0": TYPE_Q8_0, "Q8_1": TYPE_Q8_1, "Q4_K": TYPE_Q4_K, "Q6_K": TYPE_Q6_K, "Q8_K": TYPE_Q8_K}
+BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q8_1: (32, 36), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210), TYPE_Q8_K: (256, 292)}
+IMPL_GENERIC, IMPL_AVX2 = 0, 1
+
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", str(ROOT / "oracle")], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, f32p = ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p
+        L.orc_fp32_to_fp16.restype = ctypes.c_uint16
+        L.orc_fp32_to_fp16.argtypes = [ctypes.c_float]
+        L.orc_fp16_to_fp32.restype = ctypes.c_float
+        L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
+        L.orc_nearest_int.restype = ctypes.c_int
+        L.orc_nearest_int.argtypes = [ctypes.c_float]
+        for n in ("q4_K", "q6_K", "q8_0", "q8_1", "q8_K"):
+            f = getattr(L, f"orc_quantize_row_{n}_ref")
+            f.restype = None
+            f.argtypes = [vp, vp, i64]
+        for n in ("q4_K", "q6_K", "q8_0", "q8_K"):
+            f = getattr(L, f"orc_dequantize_row_{n}")
+            f.restype = None
+            f.argtypes = [vp, vp, i64]
+        L.orc_quantize_row_q8_0_avx2.restype = None
+        L.orc_quantize_row_q8_0_avx2.argtypes = [vp, vp, i64]
+        L.orc_quantize_chunk.restype = ctypes.c_size_t
+        L.orc_quantize_chunk.argtypes = [ctypes.c_int, vp, vp, i64, i64, i64, vp]
+        L.orc_vec_dot.restype = ctypes.c_float
+        L.orc_vec_dot.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        L.orc_block_dots_q8_1.restype = None
+        L.orc_block_dots_q8_1.argtypes = [ctypes.c_int, vp, i64, i64, vp, vp]
+        L.orc_mul_mat_q8_1_f64.restype = None
+        L.orc_mul_mat_q8_1_f64.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, vp]
+        L.orc_mul_mat.restype = None
+        L.orc_mul_mat.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
+        L.orc_mul_mat_id.restype = None
+        L.orc_mul_mat_id.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, i64, f32p, i64, i64, vp, i64,
+                                     f32p, ctypes.c_int]
+        L.orc_fill_normal.restype = None
+        L.orc_fill_normal.argtypes = [ctypes.c_uint64, i64, ctypes.c_float, ctypes.c_float, f32p]
+        L.orc_fnv1a.restype = ctypes.c_uint64
+        L.orc_fnv1a.argtypes = [vp, ctypes.c_size_t]
+        L.orc_has_avx2.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def fnv1a(buf):
+    b = np.ascontiguousarray(buf).view(np.uint8)
+    return int(lib().orc_fnv1a(_p(b), b.nbytes))
+
+
+def row_bytes(t, k):
+    bs, ts = BLOCK[t]
+    assert k % bs == 0
+    return (k // bs) * ts
+
+
+def quantize_ref(t, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(row_bytes(t, x.size), dtype=np.uint8)
+    name = {TYPE_Q4_K: "q4_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_1: "q8_1", TYPE_Q8_K: "q8_K"}[t]
+    getattr(lib(), f"orc_quantize_row_{name}_ref")(_p(x), _p(out), x.size)
+    return out
+
+
+def quantize_rows(t, w):
+    """Quantize a [nrows, K] f32 matrix row by row (quantize_row_*_ref)."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    return quantize_ref(t, w.reshape(-1)).reshape(w.shape[0], -1)
+
+
+def dequantize(t, q, k):
+    out = np.zeros(k, dtype=np.float32)
+    name = {TYPE_Q4_K: "q4_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_K"}[t]
+    q = np.ascontiguousarray(q)
+    getattr(lib(), f"orc_dequantize_row_{name}")(_p(q), _p(out), k)
+    return out
+
+
+def quantize_chunk(t, src, nrows, n_per_row, imatrix=None):
+    src = np.ascontiguousarray(src, dtype=np.float32)
+    out = np.zeros(nrows * row_bytes(t, n_per_row), dtype=np.uint8)
+    im = None if imatrix is None else np.ascontiguousarray(imatrix, dtype=np.float32)
+    n = lib().orc_quantize_chunk(t, _p(src), _p(out), 0, nrows, n_per_row, None if im is None else _p(im))
+    return out[:n]
+
+
+def vec_dot(t, impl, n, xq, yq):
+    return float(lib().orc_vec_dot(t, impl, n, _p(np.ascontiguousarray(xq)), _p(np.ascontiguousarray(yq))))
+
+
+def block_dots_q8_1(t, wq, nrows, K, yq8_1):
+    nsub = K // 16 if t == TYPE_Q6_K else K // 32
+    out = np.zeros(nrows * nsub, dtype=np.int32)
+    lib().orc_block_dots_q8_1(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(np.ascontiguousarray(yq8_1)), _p(out))
+    return out.reshape(nrows, nsub)
+
+
+def mul_mat_q8_1_f64(t, wq, nrows, K, yq8_1, ncols):
+    out = np.zeros(ncols * nrows, dtype=np.float64)
+    lib().orc_mul_mat_q8_1_f64(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(np.ascontiguousarray(yq8_1)), ncols,
+                               _p(out))
+    return out.reshape(ncols, nrows)
+
+
+def mul_mat(t, wq, nrows, K, x, nth=4, impl=IMPL_GENERIC):
+    """x: [ncols, K] f32 -> [ncols, nrows] f32 (ggml's dst with ne0 = nrows)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ncols = x.shape[0]
+    out = np.zeros((ncols, nrows), dtype=np.float32)
+    lib().orc_mul_mat(t, impl, _p(np.ascontiguousarray(wq)), nrows, K, _p(x), ncols, _p(out), nth)
+    return out
+
+
+def mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=4, impl=IMPL_GENERIC):
+    """x: [n_tokens, ne11, K]; ids: [n_tokens, n_ids] int32 -> [n_tokens, n_ids, nrows]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ids = np.ascontiguousarray(ids, dtype=np.int32)
+    n_tokens, ne11, _ = x.shape
+    n_ids = ids.shape[1]
+    out = np.full((n_tokens, n_ids, nrows), np.nan, dtype=np.float32)
+    lib().orc_mul_mat_id(t, impl, _p(np.ascontiguousarray(wq)), n_as, nrows, K, _p(x), ne11, n_tokens, _p(ids),
+                         n_ids, _p(out), nth)
+    return out
+
+
+def fill_normal(seed, n, mean=0.0, std=1.0):
+    out = np.zeros(n, dtype=np.float32)
+    lib().orc_fill_normal(seed, n, mean, std, _p(out))
+    return out
+
+
+def has_avx2():
+    return bool(lib().orc_has_avx2())
