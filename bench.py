@@ -1,0 +1,212 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X quantized-matmul path (one GPU).
+
+Metric: "Q4_K GEMV GB/s (% HBM peak) @14336x4096 b=1; MMQ
+int8 TOPS @b=512".  A step is one ggml_mul_mat of the headline decode shape:
+Q4_K weight 14336x4096 times one f32 activation column, i.e. the Q8_1
+activation quantizer followed by the GEMV.  Inputs are resident in HBM; the
+weight is rotated over enough distinct copies (> 2x the 256 MB Infinity
+Cache) that every step streams it from HBM.  Steps are replayed from a HIP
+graph (one node per kernel) so the measurement is of the GPU, not of Python
+launch overhead.
+
+Printed JSON (one line): value = whole-step GB/s (algorithmic bytes /
+wall-clock per step); roofline = the GEMV kernel alone (algorithmic bytes /
+its average duration from HIP events); mmq = the T=512 MMQ figure (TOPS and
+fraction of the int8 dense peak); cpu_baseline = the reference CPU path
+(restated AVX2 vec_dot_q4_K_q8_K in ggml's mul_mat chunking) on a bounded
+sample, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "llama.zig_amd"))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
+INFINITY_CACHE = 256 << 20
+
+M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
+T_MMQ = 512
+
+
+def q4k_row_bytes(k):
+    return k // 256 * 144
+
+
+def random_q4k(torch, nrows, k, gen, device):
+    """Random but valid Q4_K blocks: random nibbles and 6-bit scale/min bytes,
+    f16 d/dmin at the magnitude N(0, 0.02) weights quantize to."""
+    nb = nrows * (k // 256)
+    blocks = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, generator=gen, device="cpu")
+    d = torch.full((nb,), 2.5e-4, dtype=torch.float16).view(torch.uint8).view(nb, 2)
+    dmin = torch.full((nb,), 4.0e-4, dtype=torch.float16).view(torch.uint8).view(nb, 2)
+    blocks[:, 0:2] = d
+    blocks[:, 2:4] = dmin
+    return blocks.view(nrows, q4k_row_bytes(k)).to(device)
+
+
+def event_time_kernel(torch, launch, n):
+    """Average device duration of `launch(i)` over n launches, from HIP event
+    pairs on the launching stream.  A spin kernel first fills the queue so the
+    events bracket back-to-back GPU work, not host launch gaps."""
+    s = torch.cuda.current_stream()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+    torch.cuda.synchronize()
+    torch.cuda._sleep(20_000_000)
+    for i in range(n):
+        starts[i].record(s)
+        launch(i)
+        ends[i].record(s)
+    torch.cuda.synchronize()
+    ts = sorted(a.elapsed_time(b) for a, b in zip(starts, ends))
+    return sum(ts) / len(ts), ts[len(ts) // 2]
+
+
+def cpu_baseline(w_host, x_host):
+    """Reference CPU path on a bounded sample: the restated x86 AVX2
+    vec_dot_q4_K_q8_K with quantize_row_q8_K_ref staging, in ggml's mul_mat
+    chunking, on up to 16 host threads."""
+    sys.path.insert(0, str(ROOT / "tests"))
+    import oracle_lib as O  # noqa: E402  (test infrastructure: the checker / baseline only)
+    nth = max(1, min(16, os.cpu_count() or 1))
+    impl = O.IMPL_AVX2 if O.has_avx2() else O.IMPL_GENERIC
+    O.mul_mat(O.TYPE_Q4_K, w_host, M, K, x_host, nth=nth, impl=impl)  # warm-up
+    runs, t_total, t0 = 0, 0.0, time.perf_counter()
+    times = []
+    while (time.perf_counter() - t0 < 10.0 and runs < 2000) or runs < 20:
+        t1 = time.perf_counter()
+        O.mul_mat(O.TYPE_Q4_K, w_host, M, K, x_host, nth=nth, impl=impl)
+        times.append(time.perf_counter() - t1)
+        runs += 1
+    times.sort()
+    med = times[len(times) // 2]
+    bytes_alg = M * q4k_row_bytes(K) + K * 4 + M * 4
+    return {
+        "value": round(bytes_alg / med / 1e9, 3), "unit": "GB/s", "cores": nth,
+        "kind": "port",
+        "sample": f"Q4_K {M}x{K} b=1 mul_mat, {'AVX2' if impl == O.IMPL_AVX2 else 'generic'} vec_dot path, "
+                  f"median of {runs} runs ({med * 1e3:.3f} ms each)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import ggml_hip as G
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    G.lib()
+
+    gen = torch.Generator().manual_seed(42)
+    w_bytes = M * q4k_row_bytes(K)
+    ncopy = max(4, -(-2 * INFINITY_CACHE // w_bytes))
+    weights = [random_q4k(torch, M, K, gen, dev) for _ in range(ncopy)]
+    xg = torch.Generator(device="cpu").manual_seed(43)
+    x = torch.randn((1, K), generator=xg, dtype=torch.float32).to(dev)
+    out = torch.empty((1, M), dtype=torch.float32, device=dev)
+    ws = torch.empty(G.workspace_size("Q4_K", K, 1), dtype=torch.uint8, device=dev)
+    qs = ws[: G.padded_k(K)].view(torch.int8).view(1, -1)
+    ds = ws[G.padded_k(K):].view(torch.int32).view(1, -1)
+
+    def step(i):
+        G.mul_mat("Q4_K", weights[i % ncopy], x, out=out, workspace=ws)
+
+    for i in range(max(args.warmup, ncopy)):
+        step(i)
+    torch.cuda.synchronize()
+
+    # one graph replay = ncopy steps (each step: quantize + GEMV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(ncopy):
+                step(i)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    reps = max(1, -(-args.steps // ncopy))
+    steps = reps * ncopy
+    for _ in range(max(1, args.warmup // ncopy)):
+        graph.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        graph.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / steps
+
+    bytes_alg = w_bytes + K * 4 + M * 4
+    value = bytes_alg / (ms_per_step * 1e-3) / 1e9
+
+    # dominant kernel alone: GEMV against the already-quantized activation
+    n_ev = 4 * ncopy
+    gemv_avg_ms, gemv_med_ms = event_time_kernel(
+        torch, lambda i: G.mul_mat_vec("Q4_K", weights[i % ncopy], K, qs, ds, out=out), n_ev)
+    quant_avg_ms, _ = event_time_kernel(torch, lambda i: G.quantize_q8_1_planar(x), n_ev)
+    achieved = bytes_alg / (gemv_avg_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": "Q4_K GEMV GB/s (% HBM peak) @14336x4096 b=1; MMQ int8 TOPS @b=512",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 dot products, fp32 epilogue (Q4_K weights x Q8_1 activations)",
+        "data": "synthetic: random valid Q4_K blocks (f16 d/dmin at N(0,0.02) scale), N(0,1) f32 activations",
+        "config": {"workload": "Llama-3-8B ffn_gate/up Q4_K decode GEMV (config 1)", "rows": M, "K": K,
+                   "batch": 1, "weight_copies": ncopy, "step": "quantize_q8_1 + GEMV, HIP-graph replay"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "gemv_kernel<Q4_K,NC=1>", "avg_us": round(gemv_avg_ms * 1e3, 3),
+                     "median_us": round(gemv_med_ms * 1e3, 3), "quantize_avg_us": round(quant_avg_ms * 1e3, 3)},
+    }
+
+    if not args.no_mmq:
+        xt = torch.randn((T_MMQ, K), generator=xg, dtype=torch.float32).to(dev)
+        qst, dst_ = G.quantize_q8_1_planar(xt)
+        outt = torch.empty((T_MMQ, M), dtype=torch.float32, device=dev)
+        n_m = 2 * ncopy
+        mmq_avg_ms, mmq_med_ms = event_time_kernel(
+            torch, lambda i: G.mmq("Q4_K", weights[i % ncopy], K, qst, dst_, out=outt), n_m)
+        ops = 2.0 * M * K * T_MMQ
+        tops = ops / (mmq_avg_ms * 1e-3) / 1e12
+        result["mmq"] = {"workload": "Q4_K 14336x4096 x T=512 (config 2)", "tops": round(tops, 2),
+                         "peak_tops": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
+                         "avg_us": round(mmq_avg_ms * 1e3, 2), "median_us": round(mmq_med_ms * 1e3, 2)}
+
+    if not args.no_cpu:
+        w_host = weights[0].cpu().numpy()
+        x_host = x.cpu().numpy()
+        result["cpu_baseline"] = cpu_baseline(w_host, x_host)
+
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

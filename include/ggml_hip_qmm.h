@@ -1,0 +1,103 @@
+/*
+ * ggml_hip_qmm.h -- kernel-level C ABI of the MI355X (gfx950) quantized
+ * matmul library, libggml_hip_qmm.so.
+ *
+ * These are the entry points a ggml HIP backend host layer (e.g. a Zig
+ * src/ggml/hip/ next to the reference's src/ggml/cuda/) calls where the
+ * reference's CUDA host layer launches its kernels.  Each declaration names
+ * the reference call site whose launch arguments it mirrors (paths relative
+ * to the mlavergn/llama.zig root).
+ *
+ * Conventions:
+ *  - every pointer except `stream` and host-side scalars is a device pointer;
+ *  - `type` is the ggml type id: GGML_TYPE_Q8_0 = 8, Q4_K = 12, Q6_K = 14;
+ *  - weights are ggml rows: `nrows` rows of `K` elements, each row
+ *    `row_stride` bytes (ggml nb01); blocks in the reference layout
+ *    (block_q4_K 144 B, block_q6_K 210 B, block_q8_0 34 B);
+ *  - activations / outputs are column-major f32 (ggml ne0 contiguous);
+ *  - calls are asynchronous on `stream` (a hipStream_t; NULL = default
+ *    stream), allocate nothing, and return 0 (hipSuccess) or a hipError_t
+ *    (hipErrorInvalidValue = 1 for rejected shapes);
+ *  - scratch is caller-owned (`workspace`), sized by the *_workspace_size
+ *    functions, as the reference's host pool provides it (mmvq.zig:633-643).
+ */
+#ifndef GGML_HIP_QMM_H
+#define GGML_HIP_QMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GGML_HIP_QMM_TYPE_Q8_0 8
+#define GGML_HIP_QMM_TYPE_Q4_K 12
+#define GGML_HIP_QMM_TYPE_Q6_K 14
+
+/* Library version: (major << 16) | minor. */
+int hip_qmm_version(void);
+
+/* Row padding of quantized activations, in elements (cuda/common.zig:50-53,
+ * MATRIX_ROW_PADDING = 512). */
+int64_t hip_qmm_row_padding(void);
+
+/*
+ * f32 -> block_q8_1, bit-exact with quantize_row_q8_1_ref
+ * (src/ggml/quants/legacy.zig:451-484).  Replaces quantize_row_q8_1_cuda
+ * (src/ggml/cuda/quantize.zig:43-54), same arguments: x is [ne00, ne1, ne2,
+ * ne3] with element strides s01/s02/s03; y receives ne1*ne2*ne3 rows of
+ * ne0_padded/32 blocks (36 B each); elements ne00..ne0_padded-1 are
+ * quantized as zeros.  ne0_padded must be a multiple of 32 and >= ne00.
+ */
+int hip_qmm_quantize_q8_1(const float *x, void *y_q8_1, int64_t ne00, int64_t s01, int64_t s02,
+                          int64_t s03, int64_t ne0_padded, int64_t ne1, int64_t ne2, int64_t ne3,
+                          void *stream);
+
+/*
+ * The same quantization written in the library's planar activation layout,
+ * used between its kernels: for column c (of ncols), int8 values at
+ * qs[c*Kp + k] and the block header (d, s) as two halves at
+ * ((uint32_t*)ds)[c*Kp/32 + k/32], Kp = K rounded up to 512.  Per 32-block
+ * the bytes equal quantize_row_q8_1_ref's.  x[c*x_col_stride + k].
+ * Replaces the per-layout quantize_mmq_q8_1 variants (quantize.zig:61-118).
+ */
+int hip_qmm_quantize_q8_1_planar(const float *x, int64_t K, int64_t ncols, int64_t x_col_stride,
+                                 int8_t *qs, void *ds, void *stream);
+
+/* Bytes of workspace hip_qmm_mul_mat / _mul_mat_vec / _mmq need for ncols
+ * activation columns of K (the planar Q8_1 copy). */
+size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t ncols);
+
+/*
+ * Decode GEMV against planar Q8_1 activations, 1..8 columns: dst[c*dst_col_stride + r]
+ * = sum_k W[r,k] * y[c,k].  Replaces mul_mat_vec_q_switch_type
+ * (src/ggml/cuda/mmvq.zig:275-300, 349-493; the MMVQ path chosen for
+ * ncols_dst <= 8 at mmvq.zig:128-173).
+ */
+int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                        const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
+                        int64_t dst_col_stride, void *stream);
+
+/*
+ * Op-level MUL_MAT: quantizes x to Q8_1 into `workspace` and runs the GEMV
+ * (ncols <= 8) or the int8-MFMA MMQ (ncols > 8).  Mirrors the dispatch in
+ * ggml_cuda_mul_mat (src/ggml/cuda/mulmat.zig:576-639).
+ * x[c*x_col_stride + k] f32, dst[c*dst_col_stride + r] f32.
+ */
+int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                    const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
+                    int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
+
+/*
+ * Test hook: the integer block dot products the GEMV forms, written out
+ * instead of scaled.  out[c][r][i] int32 with i over K/32 sub-blocks (Q4_K,
+ * Q8_0) or K/16 (Q6_K).  Shares the device code of hip_qmm_mul_mat_vec.
+ */
+int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                       const int8_t *y_qs, int64_t ncols, int32_t *out, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

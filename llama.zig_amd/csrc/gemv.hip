@@ -1,0 +1,385 @@
+// gemv.hip -- decode GEMV (1..8 activation columns) of Q4_K / Q6_K / Q8_0
+// weights against planar Q8_1 activations, for gfx950.
+//
+// Replaces the reference's MMVQ path (src/ggml/cuda/mmvq.zig:275-300, chosen
+// for ncols_dst <= 8 at mmvq.zig:128-173).  Semantics (integer block dots and
+// their float combination) follow the formats' definitions:
+//   Q4_K x Q8_1: S_bj = sum_{l<32} q4 * q8 per 32-sub-block j of super-block b,
+//                out += d_b*sc_bj*d8 * S_bj - dmin_b*m_bj * s8
+//   Q6_K x Q8_1: T_bk = sum_{l<16} (q6 - 32) * q8 per 16-sub-block k,
+//                out += d_b*sc_bk*d8 * T_bk
+//   Q8_0 x Q8_1: S_b = sum_{l<32} q * q8, out += d_b*d8 * S_b
+//
+// Mapping: one 64-lane wavefront owns RPW consecutive weight rows and walks K
+// in steps of 64 lanes x W weights (W = 64 for the K-quants, 32 for Q8_0).
+// Within a step every lane owns a fixed K-slice: it loads that slice of the
+// NC activation columns once (registers) and reuses it for all RPW rows,
+// whose weight slices are loaded back to back before any arithmetic so the
+// wave keeps RPW x 48 B per lane in flight.  Integer dots use v_dot4_i32_i8;
+// each lane's partial sums are exactly the sub-block dots defined above.  One
+// butterfly reduction per (row, column) at the end.
+#include "../../include/ggml_hip_qmm.h"
+#include "qmm_device.h"
+
+using namespace qmm;
+
+namespace {
+
+template <int TYPE>
+struct Fmt;
+
+template <>
+struct Fmt<TYPE_Q4_K> {
+    static constexpr int W = 64;  // weights per lane per step
+    static constexpr int NSUB = 2;  // integer block dots per lane per step
+};
+template <>
+struct Fmt<TYPE_Q6_K> {
+    static constexpr int W = 64;
+    static constexpr int NSUB = 4;
+};
+template <>
+struct Fmt<TYPE_Q8_0> {
+    static constexpr int W = 32;
+    static constexpr int NSUB = 1;
+};
+
+// Activation slice of one column for one lane and step.
+template <int TYPE>
+struct Act;
+
+template <>
+struct Act<TYPE_Q4_K> {
+    uint4 q[4];      // 64 int8: weights kl..kl+63
+    uint32_t ds[2];  // (d, s) of the two Q8_1 blocks
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + kl);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ld_u128(p + 16 * i);
+        const uint2 t = *reinterpret_cast<const uint2 *>(dsp + kl / QK8);
+        ds[0] = t.x;
+        ds[1] = t.y;
+    }
+};
+
+// Q6_K lane (sb, n, h) covers weights 256sb + 128n + 32g + 16h + [0,16), g=0..3.
+template <>
+struct Act<TYPE_Q6_K> {
+    uint4 q[4];
+    uint32_t ds[4];
+    uint32_t asum[4];  // sum of the 16 int8 activations of group g (for the -32 bias)
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+        // kl = 256sb + 64q (q = lane % 4) -> n = q / 2, h = q % 2
+        const int64_t sb = kl / QK_K;
+        const int qq = (int)((kl % QK_K) / 64);
+        const int n = qq >> 1, h = qq & 1;
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + sb * QK_K + 128 * n + 16 * h);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) q[g] = ld_u128(p + 32 * g);
+        const uint4 t = *reinterpret_cast<const uint4 *>(dsp + sb * 8 + 4 * n);
+        ds[0] = t.x;
+        ds[1] = t.y;
+        ds[2] = t.z;
+        ds[3] = t.w;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            int s = dot4(q[g].x, 0x01010101u, 0);
+            s = dot4(q[g].y, 0x01010101u, s);
+            s = dot4(q[g].z, 0x01010101u, s);
+            s = dot4(q[g].w, 0x01010101u, s);
+            asum[g] = (uint32_t)s;
+        }
+    }
+};
+
+template <>
+struct Act<TYPE_Q8_0> {
+    uint4 q[2];
+    uint32_t ds;
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+        const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + kl);
+        q[0] = ld_u128(p);
+        q[1] = ld_u128(p + 16);
+        ds = dsp[kl / QK8];
+    }
+};
+
+// Weight slice of one row for one lane and step.
+template <int TYPE>
+struct Wt;
+
+template <>
+struct Wt<TYPE_Q4_K> {
+    uint4 hdr;   // d, dmin, scales[12]
+    uint4 q[2];  // qs[32c .. 32c+32)
+    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+        const uint8_t *blk = row + (kl / QK_K) * Q4K_BYTES;
+        const int c = (int)((kl % QK_K) / 64);
+        hdr = ld_stream_u128(blk);
+        q[0] = ld_stream_u128(blk + 16 + 32 * c);
+        q[1] = ld_stream_u128(blk + 16 + 32 * c + 16);
+    }
+    // Integer dots of the two 32-sub-blocks (j = 2c low nibbles, 2c+1 high).
+    __device__ __forceinline__ void dots(const Act<TYPE_Q4_K> &a, int S[2]) const {
+        const uint32_t w[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+        const uint32_t av[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
+                                 a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            s0 = dot4(w[i] & 0x0F0F0F0Fu, av[i], s0);
+            s1 = dot4((w[i] >> 4) & 0x0F0F0F0Fu, av[8 + i], s1);
+        }
+        S[0] = s0;
+        S[1] = s1;
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_Q4_K> &a, const int S[2], int64_t kl) const {
+        const int c = (int)((kl % QK_K) / 64);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+        q4k_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+        const float d80 = h2f(a.ds[0]), s80 = h2f(a.ds[0] >> 16);
+        const float d81 = h2f(a.ds[1]), s81 = h2f(a.ds[1] >> 16);
+        const float t = (float)S[0] * d80 * (float)sc0 + (float)S[1] * d81 * (float)sc1;
+        const float u = (float)m0 * s80 + (float)m1 * s81;
+        return d * t - dmin * u;
+    }
+};
+
+template <>
+struct Wt<TYPE_Q6_K> {
+    uint4 ql0, ql1, qh, sc;  // ql[64n+16h..], ql[64n+32+16h..], qh[32n+16h..], scales[16]
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+        const uint8_t *blk = row + (kl / QK_K) * Q6K_BYTES;
+        const int qq = (int)((kl % QK_K) / 64);
+        const int n = qq >> 1, h = qq & 1;
+        ql0 = ld16_a2(blk + 64 * n + 16 * h);
+        ql1 = ld16_a2(blk + 64 * n + 32 + 16 * h);
+        qh = ld16_a2(blk + 128 + 32 * n + 16 * h);
+        sc = ld16_a2(blk + 192);
+        d = ld_u16(blk + 208);
+    }
+    __device__ __forceinline__ void dots(const Act<TYPE_Q6_K> &a, int T[4]) const {
+        const uint32_t l0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
+        const uint32_t l1[4] = {ql1.x, ql1.y, ql1.z, ql1.w};
+        const uint32_t hh[4] = {qh.x, qh.y, qh.z, qh.w};
+        int t0 = 0, t1 = 0, t2 = 0, t3 = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t a0 = i == 0 ? a.q[0].x : i == 1 ? a.q[0].y : i == 2 ? a.q[0].z : a.q[0].w;
+            const uint32_t a1 = i == 0 ? a.q[1].x : i == 1 ? a.q[1].y : i == 2 ? a.q[1].z : a.q[1].w;
+            const uint32_t a2 = i == 0 ? a.q[2].x : i == 1 ? a.q[2].y : i == 2 ? a.q[2].z : a.q[2].w;
+            const uint32_t a3 = i == 0 ? a.q[3].x : i == 1 ? a.q[3].y : i == 2 ? a.q[3].z : a.q[3].w;
+            // unbiased 6-bit values 0..63, the -32 is applied through asum
+            const uint32_t v0 = (l0[i] & 0x0F0F0F0Fu) | ((hh[i] << 4) & 0x30303030u);
+            const uint32_t v1 = (l1[i] & 0x0F0F0F0Fu) | ((hh[i] << 2) & 0x30303030u);
+            const uint32_t v2 = ((l0[i] >> 4) & 0x0F0F0F0Fu) | (hh[i] & 0x30303030u);
+            const uint32_t v3 = ((l1[i] >> 4) & 0x0F0F0F0Fu) | ((hh[i] >> 2) & 0x30303030u);
+            t0 = dot4(v0, a0, t0);
+            t1 = dot4(v1, a1, t1);
+            t2 = dot4(v2, a2, t2);
+            t3 = dot4(v3, a3, t3);
+        }
+        T[0] = t0 - 32 * (int)a.asum[0];
+        T[1] = t1 - 32 * (int)a.asum[1];
+        T[2] = t2 - 32 * (int)a.asum[2];
+        T[3] = t3 - 32 * (int)a.asum[3];
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_Q6_K> &a, const int T[4], int64_t kl) const {
+        const int qq = (int)((kl % QK_K) / 64);
+        const int n = qq >> 1, h = qq & 1;
+        float t = 0.0f;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int idx = 8 * n + h + 2 * g;  // scales[8n + l/16 + 2g], l/16 = h
+            const float s = (float)(int8_t)byte_of(sc, idx);
+            t += (float)T[g] * h2f(a.ds[g]) * s;
+        }
+        return h2f(d) * t;
+    }
+};
+
+template <>
+struct Wt<TYPE_Q8_0> {
+    uint4 q0, q1;
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+        const uint8_t *blk = row + (kl / QK8) * Q80_BYTES;
+        d = ld_u16(blk);
+        q0 = ld16_a2(blk + 2);
+        q1 = ld16_a2(blk + 18);
+    }
+    __device__ __forceinline__ void dots(const Act<TYPE_Q8_0> &a, int S[1]) const {
+        int s = 0;
+        s = dot4(q0.x, a.q[0].x, s);
+        s = dot4(q0.y, a.q[0].y, s);
+        s = dot4(q0.z, a.q[0].z, s);
+        s = dot4(q0.w, a.q[0].w, s);
+        s = dot4(q1.x, a.q[1].x, s);
+        s = dot4(q1.y, a.q[1].y, s);
+        s = dot4(q1.z, a.q[1].z, s);
+        s = dot4(q1.w, a.q[1].w, s);
+        S[0] = s;
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_Q8_0> &a, const int S[1], int64_t) const {
+        return h2f(d) * h2f(a.ds) * (float)S[0];
+    }
+};
+
+constexpr int WAVES_PER_BLOCK = 4;
+
+// MODE 0: scaled GEMV into dst; MODE 1: write the integer block dots.
+template <int TYPE, int NC, int RPW, int MODE>
+__global__ __launch_bounds__(64 * WAVES_PER_BLOCK) void gemv_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
+    const uint32_t *__restrict__ yds, int64_t Kp, float *__restrict__ dst, int64_t dst_col_stride,
+    int32_t *__restrict__ dots_out) {
+    using F = Fmt<TYPE>;
+    const int lane = threadIdx.x & 63;
+    const int64_t row0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6)) * RPW;
+    if (row0 >= nrows) return;
+
+    float acc[RPW][NC];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+
+    constexpr int STEP = 64 * F::W;
+    for (int64_t k0 = 0; k0 < K; k0 += STEP) {
+        const int64_t kl = k0 + (int64_t)lane * F::W;
+        if (kl < K) {
+            Act<TYPE> a[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) a[c].load(yqs + c * Kp, yds + c * (Kp / QK8), kl);
+            Wt<TYPE> wt[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+                if (row0 + r < nrows) wt[r].load(w + (row0 + r) * row_stride, kl);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                if (row0 + r >= nrows) continue;
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    int S[F::NSUB];
+                    wt[r].dots(a[c], S);
+                    if constexpr (MODE == 0) {
+                        acc[r][c] += wt[r].combine(a[c], S, kl);
+                    } else {
+                        // sub-block index of this lane's first dot
+                        const int64_t nsub_row = TYPE == TYPE_Q6_K ? K / 16 : K / 32;
+                        int64_t i0;
+                        if constexpr (TYPE == TYPE_Q4_K) {
+                            i0 = kl / 32;  // 2 consecutive
+                        } else if constexpr (TYPE == TYPE_Q8_0) {
+                            i0 = kl / 32;
+                        } else {
+                            i0 = 0;  // Q6_K handled below
+                        }
+                        int32_t *o = dots_out + ((int64_t)c * nrows + row0 + r) * nsub_row;
+                        if constexpr (TYPE == TYPE_Q6_K) {
+                            const int64_t sb = kl / QK_K;
+                            const int qq = (int)((kl % QK_K) / 64);
+                            const int n = qq >> 1, h = qq & 1;
+#pragma unroll
+                            for (int g = 0; g < 4; ++g) o[sb * 16 + 8 * n + 2 * g + h] = S[g];
+                        } else {
+#pragma unroll
+                            for (int s = 0; s < F::NSUB; ++s) o[i0 + s] = S[s];
+                        }
+                    }
+                }
+            }
+        }
+    }
+    if constexpr (MODE == 0) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r)
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                const float v = wave_sum(acc[r][c]);
+                if (lane == r * NC + c && row0 + r < nrows) dst[(int64_t)c * dst_col_stride + row0 + r] = v;
+            }
+    }
+}
+
+template <int TYPE, int NC, int MODE>
+int launch_nc(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+              const uint32_t *yds, float *dst, int64_t dst_col_stride, int32_t *dots, hipStream_t s) {
+    const int64_t Kp = pad_k(K);
+    constexpr int RPW = NC <= 2 ? 4 : 2;
+    const int64_t rows_per_block = (int64_t)WAVES_PER_BLOCK * RPW;
+    const int64_t nblocks = (nrows + rows_per_block - 1) / rows_per_block;
+    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_kernel<TYPE, NC, RPW, MODE>), dim3((unsigned)nblocks), dim3(64 * WAVES_PER_BLOCK), 0,
+                       s, w, K, nrows, row_stride, yqs, yds, Kp, dst, dst_col_stride, dots);
+    return (int)hipGetLastError();
+}
+
+template <int TYPE, int MODE>
+int launch_type(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                const uint32_t *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int32_t *dots,
+                hipStream_t s) {
+    switch (ncols) {
+    case 1: return launch_nc<TYPE, 1, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 2: return launch_nc<TYPE, 2, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 3: return launch_nc<TYPE, 3, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 4: return launch_nc<TYPE, 4, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 5: return launch_nc<TYPE, 5, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 6: return launch_nc<TYPE, 6, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 7: return launch_nc<TYPE, 7, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    case 8: return launch_nc<TYPE, 8, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
+    default: return (int)hipErrorInvalidValue;
+    }
+}
+
+int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
+    if (K <= 0 || nrows <= 0) return (int)hipErrorInvalidValue;
+    int64_t bs, bb;
+    switch (type) {
+    case TYPE_Q4_K: bs = QK_K; bb = Q4K_BYTES; break;
+    case TYPE_Q6_K: bs = QK_K; bb = Q6K_BYTES; break;
+    case TYPE_Q8_0: bs = QK8; bb = Q80_BYTES; break;
+    default: return (int)hipErrorInvalidValue;
+    }
+    if (K % bs != 0 || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
+    // row bases keep the blocks' natural alignment: 16 bytes for Q4_K (144-byte
+    // blocks, read as dwordx4), 2 bytes for Q6_K / Q8_0 (read by ld16_a2)
+    if (type == TYPE_Q4_K ? (row_stride % 16) : (row_stride % 2)) return (int)hipErrorInvalidValue;
+    return 0;
+}
+
+template <int MODE>
+int dispatch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+             const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int32_t *dots, void *stream) {
+    if (int e = check_shape(type, K, nrows, row_stride)) return e;
+    if (!w || !yqs || ncols < 1 || ncols > 8) return (int)hipErrorInvalidValue;
+    if (MODE == 0 && (!yds || !dst || dst_col_stride < nrows)) return (int)hipErrorInvalidValue;
+    if (MODE == 1 && !dots) return (int)hipErrorInvalidValue;
+    if (type == TYPE_Q4_K && ((uintptr_t)w % 16)) return (int)hipErrorInvalidValue;
+    if (type != TYPE_Q4_K && ((uintptr_t)w % 2)) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *wb = (const uint8_t *)w;
+    const uint32_t *ds = (const uint32_t *)yds;
+    switch (type) {
+    case TYPE_Q4_K: return launch_type<TYPE_Q4_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    case TYPE_Q6_K: return launch_type<TYPE_Q6_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    default: return launch_type<TYPE_Q8_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    }
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                   const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
+                                   int64_t dst_col_stride, void *stream) {
+    return dispatch<0>(type, w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, nullptr, stream);
+}
+
+extern "C" int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                  const int8_t *y_qs, int64_t ncols, int32_t *out, void *stream) {
+    // The Q8_1 scales are not read in this mode; pass the qs plane for both.
+    return dispatch<1>(type, w, K, nrows, row_stride, y_qs, y_qs, ncols, nullptr, 0, out, stream);
+}

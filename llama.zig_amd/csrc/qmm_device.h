@@ -1,0 +1,95 @@
+// qmm_device.h -- device-side building blocks shared by the gfx950 kernels.
+//
+// Block layouts follow the reference's ggml-common.h restatement
+// (src/ggml/quants/blocks.zig:67-222): block_q4_K {d, dmin, scales[12],
+// qs[128]} 144 B; block_q6_K {ql[128], qh[64], scales[16], d} 210 B;
+// block_q8_0 {d, qs[32]} 34 B.  Q6_K and Q8_0 blocks sit at 2-byte alignment
+// inside a row, so they are read with dword-aligned loads plus a byte funnel
+// shift (v_alignbyte_b32); nothing here relies on unaligned memory access.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmm {
+
+constexpr int QK_K = 256;
+constexpr int QK8 = 32;
+constexpr int Q4K_BYTES = 144;
+constexpr int Q6K_BYTES = 210;
+constexpr int Q80_BYTES = 34;
+constexpr int64_t ROW_PAD = 512;  // activation row padding (MATRIX_ROW_PADDING)
+
+constexpr int TYPE_Q8_0 = 8;
+constexpr int TYPE_Q4_K = 12;
+constexpr int TYPE_Q6_K = 14;
+
+__host__ __device__ constexpr int64_t pad_k(int64_t k) { return (k + ROW_PAD - 1) / ROW_PAD * ROW_PAD; }
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+    return __half2float(__ushort_as_half((unsigned short)(bits16 & 0xFFFFu)));
+}
+
+__device__ __forceinline__ uint32_t ld_u32(const uint8_t *p) { return *reinterpret_cast<const uint32_t *>(p); }
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) { return *reinterpret_cast<const uint16_t *>(p); }
+__device__ __forceinline__ uint4 ld_u128(const uint8_t *p) { return *reinterpret_cast<const uint4 *>(p); }
+
+// Weights are streamed once: read them past L2's most-recently-used slots.
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream_u128(const uint8_t *p) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// 16 bytes at a 2-byte-aligned address, read without touching any byte
+// outside [p, p+16): four dwords from the dword below p, plus a 16-bit load
+// of the last two bytes (redundant when p is 4-aligned), then funnel-shifted.
+__device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 2u);
+    const uint8_t *base = p - sh;
+    const uint32_t a0 = ld_u32(base + 0), a1 = ld_u32(base + 4), a2 = ld_u32(base + 8), a3 = ld_u32(base + 12);
+    const uint32_t t = ld_u16(p + 14);
+    uint4 r;
+    r.x = __builtin_amdgcn_alignbyte(a1, a0, sh);
+    r.y = __builtin_amdgcn_alignbyte(a2, a1, sh);
+    r.z = __builtin_amdgcn_alignbyte(a3, a2, sh);
+    r.w = __builtin_amdgcn_alignbyte(t, a3, sh);
+    return r;
+}
+
+__device__ __forceinline__ int dot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+__device__ __forceinline__ uint32_t byte_of(uint4 v, int i) {
+    const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
+    return (w >> (8 * (i & 3))) & 0xFFu;
+}
+
+// Sub-block j's 6-bit scale and min from block_q4_K.scales (getScaleMinK4,
+// src/ggml/quants/helpers.zig:621-629).  `s` holds the 12 scale bytes in
+// its low three words (.x = bytes 0..3).
+__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                              uint32_t &m) {
+    if (j < 4) {
+        sc = (s0 >> (8 * j)) & 63u;
+        m = (s1 >> (8 * j)) & 63u;
+    } else {
+        const int jj = j - 4;
+        const uint32_t b8 = (s2 >> (8 * jj)) & 0xFFu;     // scales[j + 4]
+        const uint32_t blo = (s0 >> (8 * jj)) & 0xFFu;    // scales[j - 4]
+        const uint32_t bhi = (s1 >> (8 * jj)) & 0xFFu;    // scales[j]
+        sc = (b8 & 0xFu) | ((blo >> 6) << 4);
+        m = (b8 >> 4) | ((bhi >> 6) << 4);
+    }
+}
+
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+}  // namespace qmm

@@ -1,0 +1,107 @@
+// quantize_q8_1.hip -- f32 activations -> Q8_1, bit-exact with the
+// reference's quantize_row_q8_1_ref (src/ggml/quants/legacy.zig:451-484):
+//   amax over 32 values; d = amax / 127 (IEEE division); id = d ? 1/d : 0
+//   (IEEE division, not v_rcp); q = trunc-to-int8(roundf(x * id)) with
+//   roundf = half away from zero; d and s = fp16(sum(q) * d) rounded to
+//   nearest-even.  Built without fast-math so '/' stays correctly rounded.
+//
+// One 32-lane half-wave per Q8_1 block: lane i owns element i of the block;
+// amax and sum(q) are butterfly reductions inside the half-wave.
+//
+// The f32 product `(float)sum * d` is pinned in a register before its f16
+// conversion: the AMDGPU backend otherwise folds multiply + convert into
+// v_fma_mixlo_f16 (one rounding, where the reference rounds to f32 first and
+// then to f16), which changes `s` whenever the f32 product is an exact f16
+// tie.  `#pragma clang fp contract(off)` does not stop that fold.
+#include "../../include/ggml_hip_qmm.h"
+#include "qmm_device.h"
+
+using namespace qmm;
+
+namespace {
+
+struct Q8_1Val {
+    int8_t q;
+    float d;
+    int sum;
+};
+
+__device__ __forceinline__ Q8_1Val quantize_lane32(float x) {
+    float amax = fabsf(x);
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    const float r = roundf(x * id);
+    // The reference's C cast with clamping (src/ggml/impl.zig:744-752).
+    const int8_t q = r != r ? (int8_t)0 : r <= -128.0f ? (int8_t)-128 : r >= 127.0f ? (int8_t)127 : (int8_t)r;
+    int sum = q;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
+    return {q, d, sum};
+}
+
+__device__ __forceinline__ uint32_t pack_ds(float d, int sum) {
+    float sd = (float)sum * d;
+    asm volatile("" : "+v"(sd));  // materialise the f32-rounded product (no fold into the f16 convert)
+    const uint32_t hd = __half_as_ushort(__float2half_rn(d));
+    const uint32_t hs = __half_as_ushort(__float2half_rn(sd));
+    return hd | (hs << 16);
+}
+
+// Reference-layout output: one block_q8_1 {d, s, qs[32]} per 32 values.
+__global__ __launch_bounds__(256) void quantize_q8_1_aos(const float *__restrict__ x, uint8_t *__restrict__ y,
+                                                         int64_t ne00, int64_t s01, int64_t s02, int64_t s03,
+                                                         int64_t ne0_padded, int64_t ne1, int64_t ne2) {
+    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t i1 = blockIdx.y;
+    const int64_t i23 = blockIdx.z;
+    const int64_t i2 = i23 % ne2, i3 = i23 / ne2;
+    if (i0 >= ne0_padded) return;  // whole half-waves: ne0_padded % 32 == 0
+    const float xv = i0 < ne00 ? x[i3 * s03 + i2 * s02 + i1 * s01 + i0] : 0.0f;
+    const Q8_1Val v = quantize_lane32(xv);
+    const int64_t row = (i23 * ne1 + i1);
+    uint8_t *blk = y + (row * (ne0_padded / QK8) + i0 / QK8) * 36;
+    blk[4 + (i0 & 31)] = (uint8_t)v.q;
+    if ((i0 & 31) == 0) *reinterpret_cast<uint32_t *>(blk) = pack_ds(v.d, v.sum);
+}
+
+// Planar output: qs[c*Kp + k], ds[c*Kp/32 + k/32].
+__global__ __launch_bounds__(256) void quantize_q8_1_planar(const float *__restrict__ x, int64_t K,
+                                                            int64_t x_col_stride, int64_t Kp,
+                                                            int8_t *__restrict__ qs, uint32_t *__restrict__ ds) {
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t c = blockIdx.y;
+    if (k >= Kp) return;
+    const float xv = k < K ? x[c * x_col_stride + k] : 0.0f;
+    const Q8_1Val v = quantize_lane32(xv);
+    qs[c * Kp + k] = v.q;
+    if ((k & 31) == 0) ds[c * (Kp / QK8) + k / QK8] = pack_ds(v.d, v.sum);
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_quantize_q8_1(const float *x, void *y_q8_1, int64_t ne00, int64_t s01, int64_t s02,
+                                     int64_t s03, int64_t ne0_padded, int64_t ne1, int64_t ne2, int64_t ne3,
+                                     void *stream) {
+    if (!x || !y_q8_1 || ne00 < 0 || ne0_padded < ne00 || ne0_padded % QK8 != 0 || ne1 < 0 || ne2 < 1 ||
+        ne3 < 1 || ne1 > 65535 || ne2 * ne3 > 65535)
+        return (int)hipErrorInvalidValue;
+    if (ne0_padded == 0 || ne1 == 0) return 0;
+    const dim3 grid((unsigned)((ne0_padded + 255) / 256), (unsigned)ne1, (unsigned)(ne2 * ne3));
+    hipLaunchKernelGGL(quantize_q8_1_aos, grid, dim3(256), 0, (hipStream_t)stream, x, (uint8_t *)y_q8_1, ne00,
+                       s01, s02, s03, ne0_padded, ne1, ne2);
+    return (int)hipGetLastError();
+}
+
+extern "C" int hip_qmm_quantize_q8_1_planar(const float *x, int64_t K, int64_t ncols, int64_t x_col_stride,
+                                            int8_t *qs, void *ds, void *stream) {
+    if (!x || !qs || !ds || K <= 0 || K % QK8 != 0 || ncols < 0 || ncols > 65535 || x_col_stride < K)
+        return (int)hipErrorInvalidValue;
+    if (ncols == 0) return 0;
+    const int64_t Kp = pad_k(K);
+    const dim3 grid((unsigned)((Kp + 255) / 256), (unsigned)ncols);
+    hipLaunchKernelGGL(quantize_q8_1_planar, grid, dim3(256), 0, (hipStream_t)stream, x, K, x_col_stride, Kp, qs,
+                       (uint32_t *)ds);
+    return (int)hipGetLastError();
+}

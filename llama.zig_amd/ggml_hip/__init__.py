@@ -1,0 +1,173 @@
+"""Host-side mirror of the ggml quantized-matmul path, over libggml_hip_qmm.so.
+
+The functions mirror the reference's operator interface for this path:
+``mul_mat(w, x)`` is ``ggml_mul_mat(a, b)`` (src/ggml/ops.zig:1072-1083: a is
+the [K, M] quantized weight, b the [K, N] f32 activation, result [M, N] f32)
+and ``mul_mat_id(as_, x, ids)`` is ``ggml_mul_mat_id`` (ops.zig:1104-1125).
+Compute runs only in the HIP library; there is no CPU fallback.  If the
+library is missing or no GPU is present the calls raise.
+
+Tensors are torch tensors on the GPU (torch provides device memory and
+streams); weights are uint8 tensors holding ggml blocks row by row.
+"""
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+import torch
+
+from .qtypes import BLOCK, TYPE_IDS, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_0, row_size  # noqa: F401
+
+PKG_DIR = pathlib.Path(__file__).resolve().parents[1]
+LIB_PATH = PKG_DIR / "libggml_hip_qmm.so"
+
+_lib = None
+
+
+class HipQmmError(RuntimeError):
+    pass
+
+
+def lib():
+    """Load the HIP library; raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise HipQmmError(f"{LIB_PATH} not built: run `make -C {PKG_DIR}` (or __graft_entry__.build())")
+        L = ctypes.CDLL(str(LIB_PATH))
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.hip_qmm_version.restype = i32
+        L.hip_qmm_row_padding.restype = i64
+        L.hip_qmm_quantize_q8_1.restype = i32
+        L.hip_qmm_quantize_q8_1.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, i64, i64, vp]
+        L.hip_qmm_quantize_q8_1_planar.restype = i32
+        L.hip_qmm_quantize_q8_1_planar.argtypes = [vp, i64, i64, i64, vp, vp, vp]
+        L.hip_qmm_mul_mat_workspace_size.restype = ctypes.c_size_t
+        L.hip_qmm_mul_mat_workspace_size.argtypes = [i32, i64, i64]
+        L.hip_qmm_mul_mat_vec.restype = i32
+        L.hip_qmm_mul_mat_vec.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
+        L.hip_qmm_mmq.restype = i32
+        L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
+        L.hip_qmm_mul_mat.restype = i32
+        L.hip_qmm_mul_mat.argtypes = [i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, ctypes.c_size_t, vp]
+        L.hip_qmm_block_dots.restype = i32
+        L.hip_qmm_block_dots.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, vp]
+        _lib = L
+    return _lib
+
+
+def _check(err, what):
+    if err != 0:
+        raise HipQmmError(f"{what} failed with hipError {err}")
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _require_cuda(*ts):
+    for t in ts:
+        if not t.is_cuda:
+            raise HipQmmError("tensors must live on the GPU")
+        if not t.is_contiguous():
+            raise HipQmmError("tensors must be contiguous")
+
+
+def padded_k(K: int) -> int:
+    pad = int(lib().hip_qmm_row_padding())
+    return (K + pad - 1) // pad * pad
+
+
+def quantize_q8_1(x: torch.Tensor, ne0_padded: int | None = None) -> torch.Tensor:
+    """f32 [N, K] -> uint8 [N, ne0_padded/32*36] in block_q8_1 layout, bit-exact
+    with quantize_row_q8_1_ref (src/ggml/quants/legacy.zig:451-484)."""
+    _require_cuda(x)
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise HipQmmError("x must be a 2-D float32 tensor [ncols, K]")
+    n, K = x.shape
+    ne0_padded = padded_k(K) if ne0_padded is None else ne0_padded
+    y = torch.empty((n, ne0_padded // 32 * 36), dtype=torch.uint8, device=x.device)
+    _check(lib().hip_qmm_quantize_q8_1(_ptr(x), _ptr(y), K, K, K * n, K * n, ne0_padded, n, 1, 1, _stream()),
+           "hip_qmm_quantize_q8_1")
+    return y
+
+
+def quantize_q8_1_planar(x: torch.Tensor):
+    """f32 [N, K] -> (qs int8 [N, Kp], ds int32 [N, Kp/32]) in the library's planar layout."""
+    _require_cuda(x)
+    n, K = x.shape
+    Kp = padded_k(K)
+    qs = torch.empty((n, Kp), dtype=torch.int8, device=x.device)
+    ds = torch.empty((n, Kp // 32), dtype=torch.int32, device=x.device)
+    _check(lib().hip_qmm_quantize_q8_1_planar(_ptr(x), K, n, K, _ptr(qs), _ptr(ds), _stream()),
+           "hip_qmm_quantize_q8_1_planar")
+    return qs, ds
+
+
+def _weight_args(qtype, w, K):
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    _require_cuda(w)
+    if w.dtype != torch.uint8 or w.dim() != 2:
+        raise HipQmmError("weights must be a 2-D uint8 tensor [nrows, row_bytes]")
+    if w.shape[1] < row_size(t, K):
+        raise HipQmmError("weight rows are shorter than K elements of this type")
+    return t, w.shape[0], w.stride(0)
+
+
+def mul_mat_vec(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=None):
+    """GEMV against planar Q8_1 activations (1..8 columns)."""
+    t, nrows, rs = _weight_args(qtype, w, K)
+    n = qs.shape[0]
+    out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_vec(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
+                                     _stream()), "hip_qmm_mul_mat_vec")
+    return out
+
+
+def mmq(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=None):
+    """int8-MFMA GEMM against planar Q8_1 activations (any column count)."""
+    t, nrows, rs = _weight_args(qtype, w, K)
+    n = qs.shape[0]
+    out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_mmq(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
+                             _stream()), "hip_qmm_mmq")
+    return out
+
+
+def block_dots(qtype, w: torch.Tensor, K: int, qs: torch.Tensor):
+    """The GEMV's integer block dot products: int32 [N, nrows, K/32 or K/16]."""
+    t, nrows, rs = _weight_args(qtype, w, K)
+    n = qs.shape[0]
+    nsub = K // 16 if t == TYPE_Q6_K else K // 32
+    out = torch.empty((n, nrows, nsub), dtype=torch.int32, device=w.device)
+    _check(lib().hip_qmm_block_dots(t, _ptr(w), K, nrows, rs, _ptr(qs), n, _ptr(out), _stream()),
+           "hip_qmm_block_dots")
+    return out
+
+
+def workspace_size(qtype, K: int, ncols: int) -> int:
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    return int(lib().hip_qmm_mul_mat_workspace_size(t, K, ncols))
+
+
+def mul_mat(qtype, w: torch.Tensor, x: torch.Tensor, out=None, workspace=None):
+    """ggml_mul_mat(w, x): w quantized [nrows, row_bytes], x f32 [N, K] -> f32 [N, nrows]."""
+    _require_cuda(x)
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise HipQmmError("x must be a 2-D float32 tensor [ncols, K]")
+    n, K = x.shape
+    t, nrows, rs = _weight_args(qtype, w, K)
+    need = workspace_size(t, K, n)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() < need:
+        raise HipQmmError(f"workspace too small: {workspace.numel()} < {need}")
+    out = torch.empty((n, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat(t, _ptr(w), K, nrows, rs, _ptr(x), n, x.stride(0), _ptr(out), out.stride(0),
+                                 _ptr(workspace), workspace.numel(), _stream()), "hip_qmm_mul_mat")
+    return out

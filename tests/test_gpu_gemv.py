@@ -1,0 +1,70 @@
+"""Decode GEMV (1..8 columns) parity: integer block dots exact, fp32 outputs
+within NMSE < 5e-4 of the CPU ggml path (and within 1e-5 relative of the
+f64 evaluation of the same Q8_1 formula)."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, max_rel, nmse, weights_q
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4  # test-backend-ops' gate for mul_mat
+F64_TOL = 2e-6    # fp32 epilogue vs exact f64 of the same Q8_1 formula, / max|out|
+
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+
+
+def _run(tname, nrows, K, ncols):
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    got = G.mul_mat_vec(tname, w_d, K, qs, ds).cpu().numpy()
+    return t, wq, x, w_d, x_d, qs, got
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("ncols", [1, 2, 3, 8])
+def test_block_dots_exact(tname, ncols):
+    import ggml_hip as G
+    nrows, K = 64, 2048
+    t, wq, x, w_d, x_d, qs, _ = _run(tname, nrows, K, ncols)
+    got = G.block_dots(tname, w_d, K, qs).cpu().numpy()
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    for c in range(ncols):
+        want = O.block_dots_q8_1(t, wq, nrows, K, y[c])
+        np.testing.assert_array_equal(got[c], want)
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("nrows,K,ncols", [(4096, 4096, 1), (1024, 4096, 2), (1024, 4096, 4), (1000, 4096, 8),
+                                           (333, 14336, 3), (96, 768, 5)])
+def test_gemv_parity(tname, nrows, K, ncols):
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, ncols)
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    assert nmse(got, ideal) < 1e-11
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    e = nmse(got, cpu)
+    assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {max_rel(got, cpu):.3g}"
+
+
+def test_gemv_config0_op_level():
+    """Config 0: 4096x4096 Q4_K (seed 42) times a 4096x1 activation through the
+    op-level entry point, against the CPU ggml path."""
+    import ggml_hip as G
+    K = nrows = 4096
+    wq = weights_q(O.TYPE_Q4_K, nrows, K)
+    x = acts(1, K)
+    got = G.mul_mat("Q4_K", torch.from_numpy(np.array(wq)).cuda(),
+                    torch.from_numpy(np.array(x)).cuda()).cpu().numpy()
+    cpu = O.mul_mat(O.TYPE_Q4_K, wq, nrows, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    assert np.all(np.isfinite(got))

@@ -1,0 +1,50 @@
+"""MMQ (int8 MFMA) parity: fp32 outputs within NMSE < 5e-4 of the CPU ggml
+path and within 1e-5 relative of the f64 evaluation of the Q8_1 formula."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, max_rel, nmse, weights_q
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4
+F64_TOL = 2e-6  # vs the f64 Q8_1 formula, error / max|out|
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("nrows,K,ncols", [(256, 4096, 128), (200, 2048, 77), (128, 14336, 9), (384, 768, 300)])
+def test_mmq_parity(tname, nrows, K, ncols):
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    got = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+
+
+def test_mmq_config2_rows_subset():
+    """Config 2 shape (Q4_K 14336x4096, T=512) at full size on the GPU, checked
+    on a row subset against the oracle, plus the op-level entry point."""
+    import ggml_hip as G
+    nrows, K, T = 14336, 4096, 512
+    wq = weights_q(O.TYPE_Q4_K, nrows, K)
+    x = acts(T, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    got = G.mul_mat("Q4_K", w_d, x_d).cpu().numpy()
+    rows = np.r_[0:64, 7000:7064, nrows - 64:nrows]
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(O.TYPE_Q4_K, wq[rows], len(rows), K, y, T)
+    assert max_err_scaled(got[:, rows], ideal) < F64_TOL
+    cpu = O.mul_mat(O.TYPE_Q4_K, wq[rows], len(rows), K, x, nth=8)
+    assert nmse(got[:, rows], cpu) < NMSE_GATE
