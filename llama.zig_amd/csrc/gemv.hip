@@ -17,7 +17,8 @@
 // whose weight slices are loaded back to back before any arithmetic so the
 // wave keeps RPW x 48 B per lane in flight.  Integer dots use v_dot4_i32_i8;
 // each lane's partial sums are exactly the sub-block dots defined above.  One
-// butterfly reduction per (row, column) at the end.
+// DPP reduction per (row, column) at the end.  Weights are read with plain
+// loads: the nontemporal variant measured ~30% slower on gfx950.
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
@@ -52,7 +53,7 @@ template <>
 struct Act<TYPE_Q4_K> {
     uint4 q[4];      // 64 int8: weights kl..kl+63
     uint32_t ds[2];  // (d, s) of the two Q8_1 blocks
-    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int kl) {
         const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + kl);
 #pragma unroll
         for (int i = 0; i < 4; ++i) q[i] = ld_u128(p + 16 * i);
@@ -68,10 +69,10 @@ struct Act<TYPE_Q6_K> {
     uint4 q[4];
     uint32_t ds[4];
     uint32_t asum[4];  // sum of the 16 int8 activations of group g (for the -32 bias)
-    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int kl) {
         // kl = 256sb + 64q (q = lane % 4) -> n = q / 2, h = q % 2
-        const int64_t sb = kl / QK_K;
-        const int qq = (int)((kl % QK_K) / 64);
+        const int sb = kl / QK_K;
+        const int qq = (kl % QK_K) / 64;
         const int n = qq >> 1, h = qq & 1;
         const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + sb * QK_K + 128 * n + 16 * h);
 #pragma unroll
@@ -96,7 +97,7 @@ template <>
 struct Act<TYPE_Q8_0> {
     uint4 q[2];
     uint32_t ds;
-    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int64_t kl) {
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int kl) {
         const uint8_t *p = reinterpret_cast<const uint8_t *>(qs + kl);
         q[0] = ld_u128(p);
         q[1] = ld_u128(p + 16);
@@ -112,12 +113,12 @@ template <>
 struct Wt<TYPE_Q4_K> {
     uint4 hdr;   // d, dmin, scales[12]
     uint4 q[2];  // qs[32c .. 32c+32)
-    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
         const uint8_t *blk = row + (kl / QK_K) * Q4K_BYTES;
-        const int c = (int)((kl % QK_K) / 64);
-        hdr = ld_stream_u128(blk);
-        q[0] = ld_stream_u128(blk + 16 + 32 * c);
-        q[1] = ld_stream_u128(blk + 16 + 32 * c + 16);
+        const int c = (kl % QK_K) / 64;
+        hdr = ld_u128(blk);
+        q[0] = ld_u128(blk + 16 + 32 * c);
+        q[1] = ld_u128(blk + 16 + 32 * c + 16);
     }
     // Integer dots of the two 32-sub-blocks (j = 2c low nibbles, 2c+1 high).
     __device__ __forceinline__ void dots(const Act<TYPE_Q4_K> &a, int S[2]) const {
@@ -133,8 +134,8 @@ struct Wt<TYPE_Q4_K> {
         S[0] = s0;
         S[1] = s1;
     }
-    __device__ __forceinline__ float combine(const Act<TYPE_Q4_K> &a, const int S[2], int64_t kl) const {
-        const int c = (int)((kl % QK_K) / 64);
+    __device__ __forceinline__ float combine(const Act<TYPE_Q4_K> &a, const int S[2], int kl) const {
+        const int c = (kl % QK_K) / 64;
         uint32_t sc0, m0, sc1, m1;
         q4k_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
         q4k_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
@@ -151,9 +152,9 @@ template <>
 struct Wt<TYPE_Q6_K> {
     uint4 ql0, ql1, qh, sc;  // ql[64n+16h..], ql[64n+32+16h..], qh[32n+16h..], scales[16]
     uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
         const uint8_t *blk = row + (kl / QK_K) * Q6K_BYTES;
-        const int qq = (int)((kl % QK_K) / 64);
+        const int qq = (kl % QK_K) / 64;
         const int n = qq >> 1, h = qq & 1;
         ql0 = ld16_a2(blk + 64 * n + 16 * h);
         ql1 = ld16_a2(blk + 64 * n + 32 + 16 * h);
@@ -187,8 +188,8 @@ struct Wt<TYPE_Q6_K> {
         T[2] = t2 - 32 * (int)a.asum[2];
         T[3] = t3 - 32 * (int)a.asum[3];
     }
-    __device__ __forceinline__ float combine(const Act<TYPE_Q6_K> &a, const int T[4], int64_t kl) const {
-        const int qq = (int)((kl % QK_K) / 64);
+    __device__ __forceinline__ float combine(const Act<TYPE_Q6_K> &a, const int T[4], int kl) const {
+        const int qq = (kl % QK_K) / 64;
         const int n = qq >> 1, h = qq & 1;
         float t = 0.0f;
 #pragma unroll
@@ -205,7 +206,7 @@ template <>
 struct Wt<TYPE_Q8_0> {
     uint4 q0, q1;
     uint32_t d;
-    __device__ __forceinline__ void load(const uint8_t *row, int64_t kl) {
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
         const uint8_t *blk = row + (kl / QK8) * Q80_BYTES;
         d = ld_u16(blk);
         q0 = ld16_a2(blk + 2);
@@ -223,7 +224,7 @@ struct Wt<TYPE_Q8_0> {
         s = dot4(q1.w, a.q[1].w, s);
         S[0] = s;
     }
-    __device__ __forceinline__ float combine(const Act<TYPE_Q8_0> &a, const int S[1], int64_t) const {
+    __device__ __forceinline__ float combine(const Act<TYPE_Q8_0> &a, const int S[1], int) const {
         return h2f(d) * h2f(a.ds) * (float)S[0];
     }
 };
@@ -231,15 +232,29 @@ struct Wt<TYPE_Q8_0> {
 constexpr int WAVES_PER_BLOCK = 4;
 
 // MODE 0: scaled GEMV into dst; MODE 1: write the integer block dots.
+// Rows past nrows are clamped to the last row for loading (branch-free) and
+// masked at the store.  K < 2^31 (checked on the host), so in-row offsets are
+// 32-bit.
+// Occupancy target: one column of Q4_K / Q8_0 fits in 64 VGPRs without
+// spilling, which keeps 8 waves per SIMD so a 14336-row grid (7168 waves) is
+// resident in one round.  Q6_K and wider GEMVs would spill at that bound.
+template <int TYPE, int NC>
+constexpr int gemv_min_waves() { return NC == 1 && TYPE != TYPE_Q6_K ? 8 : 1; }
+
 template <int TYPE, int NC, int RPW, int MODE>
-__global__ __launch_bounds__(64 * WAVES_PER_BLOCK) void gemv_kernel(
+__global__ __launch_bounds__(64 * WAVES_PER_BLOCK, (gemv_min_waves<TYPE, NC>())) void gemv_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t Kp, float *__restrict__ dst, int64_t dst_col_stride,
     int32_t *__restrict__ dots_out) {
     using F = Fmt<TYPE>;
     const int lane = threadIdx.x & 63;
-    const int64_t row0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + (threadIdx.x >> 6)) * RPW;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: row math in SGPRs
+    const int64_t row0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + wave) * RPW;
     if (row0 >= nrows) return;
+
+    const uint8_t *rowp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rowp[r] = w + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride;
 
     float acc[RPW][NC];
 #pragma unroll
@@ -248,19 +263,22 @@ __global__ __launch_bounds__(64 * WAVES_PER_BLOCK) void gemv_kernel(
         for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
 
     constexpr int STEP = 64 * F::W;
-    for (int64_t k0 = 0; k0 < K; k0 += STEP) {
-        const int64_t kl = k0 + (int64_t)lane * F::W;
-        if (kl < K) {
+    const int K32 = (int)K;
+    for (int k0 = 0; k0 < K32; k0 += STEP) {
+        const int kl = k0 + lane * F::W;
+        if (kl < K32) {
+            Wt<TYPE> wt[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) wt[r].load(rowp[r], kl);
             Act<TYPE> a[NC];
 #pragma unroll
             for (int c = 0; c < NC; ++c) a[c].load(yqs + c * Kp, yds + c * (Kp / QK8), kl);
-            Wt<TYPE> wt[RPW];
-#pragma unroll
-            for (int r = 0; r < RPW; ++r)
-                if (row0 + r < nrows) wt[r].load(w + (row0 + r) * row_stride, kl);
+            // Keep every load of this step above the arithmetic: left alone, the
+            // scheduler sinks row r+1's loads below row r's dots, which costs a
+            // second memory round trip per wave.
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
-                if (row0 + r >= nrows) continue;
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
                     int S[F::NSUB];
@@ -268,26 +286,18 @@ __global__ __launch_bounds__(64 * WAVES_PER_BLOCK) void gemv_kernel(
                     if constexpr (MODE == 0) {
                         acc[r][c] += wt[r].combine(a[c], S, kl);
                     } else {
-                        // sub-block index of this lane's first dot
+                        if (row0 + r >= nrows) continue;
                         const int64_t nsub_row = TYPE == TYPE_Q6_K ? K / 16 : K / 32;
-                        int64_t i0;
-                        if constexpr (TYPE == TYPE_Q4_K) {
-                            i0 = kl / 32;  // 2 consecutive
-                        } else if constexpr (TYPE == TYPE_Q8_0) {
-                            i0 = kl / 32;
-                        } else {
-                            i0 = 0;  // Q6_K handled below
-                        }
                         int32_t *o = dots_out + ((int64_t)c * nrows + row0 + r) * nsub_row;
                         if constexpr (TYPE == TYPE_Q6_K) {
-                            const int64_t sb = kl / QK_K;
-                            const int qq = (int)((kl % QK_K) / 64);
+                            const int sb = kl / QK_K;
+                            const int qq = (kl % QK_K) / 64;
                             const int n = qq >> 1, h = qq & 1;
 #pragma unroll
                             for (int g = 0; g < 4; ++g) o[sb * 16 + 8 * n + 2 * g + h] = S[g];
                         } else {
 #pragma unroll
-                            for (int s = 0; s < F::NSUB; ++s) o[i0 + s] = S[s];
+                            for (int s = 0; s < F::NSUB; ++s) o[kl / 32 + s] = S[s];
                         }
                     }
                 }
@@ -309,7 +319,9 @@ template <int TYPE, int NC, int MODE>
 int launch_nc(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
               const uint32_t *yds, float *dst, int64_t dst_col_stride, int32_t *dots, hipStream_t s) {
     const int64_t Kp = pad_k(K);
-    constexpr int RPW = NC <= 2 ? 4 : 2;
+    // rows per wave: 2 measured best for one column (more waves in flight);
+    // with more columns the activation registers grow and fewer rows fit
+    constexpr int RPW = 2;
     const int64_t rows_per_block = (int64_t)WAVES_PER_BLOCK * RPW;
     const int64_t nblocks = (nrows + rows_per_block - 1) / rows_per_block;
     if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
@@ -344,7 +356,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     case TYPE_Q8_0: bs = QK8; bb = Q80_BYTES; break;
     default: return (int)hipErrorInvalidValue;
     }
-    if (K % bs != 0 || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
+    if (K % bs != 0 || K > (1 << 30) || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
     // row bases keep the blocks' natural alignment: 16 bytes for Q4_K (144-byte
     // blocks, read as dwordx4), 2 bytes for Q6_K / Q8_0 (read by ld16_a2)
     if (type == TYPE_Q4_K ? (row_stride % 16) : (row_stride % 2)) return (int)hipErrorInvalidValue;
