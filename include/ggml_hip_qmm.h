@@ -90,6 +90,51 @@ int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t r
                     int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
 
 /*
+ * int8-MFMA GEMM against planar Q8_1 activations for any column count
+ * (K a multiple of 256).  Replaces launch_mul_mat_q (src/ggml/cuda/mmq.zig:282-408).
+ */
+int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *y_qs,
+                const void *y_ds, int64_t ncols, float *dst, int64_t dst_col_stride, void *stream);
+
+/* Column-tile width hip_qmm_mmq picks for `ncols` columns (32 or 64). */
+int hip_qmm_mmq_tile_n(int64_t ncols);
+
+/*
+ * Expert-grouped MMQ over device-side tile tables (see hip_qmm_mul_mat_id):
+ * tiles[2*i] = expert, tiles[2*i+1] = first routed column of the tile;
+ * *n_tiles live entries; expert_off[e]..expert_off[e+1] are expert e's
+ * columns; col_src / col_dst map a routed column to its activation row and
+ * its dst row.  Mirrors mul_mat_q's ids path (src/ggml/cuda/mmq.zig:750-855).
+ */
+int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                        int64_t expert_stride, const int8_t *y_qs, const void *y_ds, float *dst,
+                        int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
+                        const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
+                        const int32_t *col_dst, void *stream);
+
+/* Bytes of workspace hip_qmm_mul_mat_id needs. */
+size_t hip_qmm_mul_mat_id_workspace_size(int type, int64_t K, int64_t n_as, int64_t ne11, int64_t n_tokens,
+                                         int64_t n_ids);
+
+/*
+ * Op-level MUL_MAT_ID (ggml_mul_mat_id, src/ggml/ops.zig:1104-1125; CPU
+ * semantics src/ggml/cpu/mulmat.zig:555-777): n_as experts of nrows x K
+ * weights, expert e at w + e*expert_stride; activations x row (t, i11) at
+ * x + (t*ne11 + i11)*x_row_stride (ne11 = 1 broadcasts one row per token,
+ * ne11 = n_ids gives one per slot); ids[t*ids_stride + s] selects the expert
+ * of slot s of token t; dst row (t, s) at dst + (t*n_ids + s)*dst_row_stride.
+ * An id of -1 (or any id outside [0, n_as)) yields a zero row.  Expert
+ * grouping runs on the device (no host synchronisation); replaces
+ * ggml_cuda_mul_mat_id (src/ggml/cuda/mulmat.zig:669-800) and
+ * mm_ids_helper (src/ggml/cuda/mmid.zig:32-90).  K a multiple of 256; at
+ * most 1024 experts.
+ */
+int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                       int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
+                       int64_t x_row_stride, const int32_t *ids, int64_t n_ids, int64_t ids_stride, float *dst,
+                       int64_t dst_row_stride, void *workspace, size_t workspace_size, void *stream);
+
+/*
  * Test hook: the integer block dot products the GEMV forms, written out
  * instead of scaled.  out[c][r][i] int32 with i over K/32 sub-blocks (Q4_K,
  * Q8_0) or K/16 (Q6_K).  Shares the device code of hip_qmm_mul_mat_vec.

@@ -1,29 +1,36 @@
-// mmq.hip -- prefill GEMM (more than 8 activation columns) of Q4_K / Q6_K /
-// Q8_0 weights against planar Q8_1 activations on CDNA4 int8 MFMA.
+// mmq.hip -- prefill GEMM (more than 8 activation columns) and the
+// expert-grouped MoE GEMM of Q4_K / Q6_K / Q8_0 weights against planar Q8_1
+// activations, on CDNA4 int8 MFMA.
 //
 // Replaces the reference's MMQ path (mul_mat_q, src/ggml/cuda/mmq.zig:282-408,
-// chosen at mmq.zig:865-917).  Integer block dots are formed exactly by
-// v_mfma_i32_32x32x32_i8 (one 32-deep Q8_1 block: Q4_K sub-blocks, Q8_0
-// blocks) or v_mfma_i32_32x32x16_i8 (Q6_K's 16-deep sub-blocks) and then
-// scaled per (row, column, block) in fp32:
-//   Q4_K: out = sum_j d*sc_j*d8_j*S_j - sum_j dmin*m_j*s8_j
-//   Q6_K: out = sum_k d*sc_k*d8_{k/2}*T_k      (T over q6-32)
-//   Q8_0: out = sum_b d_b*d8_b*S_b
-// The Q4_K min term is itself a small GEMM over K/32: per super-block the f16
-// MFMA (v_mfma_f32_32x32x8_f16, K = its 8 sub-blocks) forms sum_j m_j*s8_j
-// exactly (6-bit integers times f16 values), and dmin scales it in fp32.
+// chosen at mmq.zig:865-917) and its mul_mat_id form (mmq.zig:750-855 with the
+// mm_ids_helper tile specs, src/ggml/cuda/mmid.zig:32-90).
 //
-// Tiling: a 256-thread workgroup computes a 128x128 output tile; each wave a
-// 64x64 quarter as 2x2 MFMA tiles of 32x32.  K advances one 256-element
-// super-block at a time: the workgroup unpacks the 128 weight rows' nibbles
-// / 6-bit values to int8 in LDS (with their fp32 sub-block scales) and stages
-// the 128 activation columns' int8 values and (d8, s8) beside them.
+// Arithmetic.  Integer block dots are formed exactly on the MFMA:
+// v_mfma_i32_32x32x32_i8 for one 32-deep Q8_1 block (Q4_K sub-blocks, Q8_0
+// blocks), v_mfma_i32_32x32x16_i8 for Q6_K's 16-deep sub-blocks.  Each dot is
+// then scaled per (row, column, block):
+//   Q4_K: out = sum_b d_b * sum_j (sc_bj*d8_j) * S_bj  -  sum_b dmin_b * sum_j m_bj*s8_j
+//   Q6_K: out = sum_b d_b * sum_k (sc_bk*d8_{k/2}) * T_bk
+//   Q8_0: out = sum_b (d_b*d8_b) * S_b
+// The per-(row, column) factor in parentheses is an outer product of exactly
+// representable f16 values (6-bit / int8 scales, f16 d8 and d), formed exactly
+// in fp32 by one v_mfma_f32_32x32x8_f16 with a single live K slot.  The VALU
+// then spends one convert and one FMA per output and block; d_b and the Q4_K
+// min term (a K=8 f16 MFMA of m_j x s8_j) are applied once per super-block.
+//
+// Tiling: a 256-thread workgroup computes a BM=128 x BN output tile (BN = 32
+// or 64); the four waves split it into 32x32 MFMA tiles.  K advances one
+// 256-element super-block at a time.  While the MFMAs of step kb run, the
+// workgroup's global loads for step kb+1 are already in flight into
+// registers; they are unpacked into LDS (weights as int8, scales as f16)
+// after the step.
 //
 // MFMA operand convention: for a 32x32xK tile, lane l supplies row (l % 32)
 // of A and column (l % 32) of B over the K-slice [(l / 32) * K/2, +K/2).  A and
 // B use the same slice, so the sum over K is formed whatever order the
-// hardware assigns to the slices.  Results use the 32x32 accumulator layout:
-// value v of lane l is row 8*(v/4) + 4*(l/32) + v%4, column l%32.
+// hardware gives the slices.  Results: value v of lane l is row
+// 8*(v/4) + 4*(l/32) + v%4, column l%32.
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
@@ -37,9 +44,8 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
-constexpr int BN = 128;
 constexpr int BK = 256;
-constexpr int LDA = BK + 16;  // int8 row stride in LDS (pad breaks bank aliasing)
+constexpr int LDA = BK + 16;  // int8 row stride in LDS (the pad staggers banks)
 constexpr int NTHREADS = 256;
 
 template <int TYPE>
@@ -48,253 +54,382 @@ struct MmqFmt {
     static constexpr int NG = BK / GK;                      // scale groups per K-step
 };
 
-template <int TYPE>
+template <int TYPE, int BN>
 struct Smem {
     int8_t a[BM * LDA];
     int8_t b[BN * LDA];
-    float ascale[MmqFmt<TYPE>::NG][BM];  // d * sc per (group, row)
-    float bd[8][BN];                      // d8 per (Q8_1 block, column)
-    _Float16 amin[BM][8];                 // m_j as f16 (Q4_K)
-    float admin[BM];                      // dmin       (Q4_K)
-    _Float16 bs8[BN][8];                  // s8          (Q4_K)
+    _Float16 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
+    _Float16 bd8[8][BN];                 // d8 per (Q8_1 block, column)
+    float ad[BM];                        // d per row (Q4_K, Q6_K)
+    float admin[BM];                     // dmin per row (Q4_K)
+    _Float16 am[BM][8];                  // m_j per row (Q4_K)
+    _Float16 bs8[BN][8];                 // s8 per column (Q4_K)
 };
 
-// ---- staging of one K-step (256 elements) of the 128 weight rows ----------
+// Global data of one K-step, held in registers between the load and the LDS
+// write.  Each thread owns one (row, half) of the A tile.
+template <int TYPE>
+struct AReg;
 
-__device__ __forceinline__ void store16(int8_t *dst, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+template <>
+struct AReg<TYPE_Q4_K> {
+    uint4 hdr, q[4];  // block header and this half's 64 qs bytes
+    __device__ __forceinline__ void load(const uint8_t *blk, int half) {
+        hdr = ld_u128(blk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ld_u128(blk + 16 + 64 * half + 16 * i);
+    }
+    __device__ __forceinline__ void zero() {
+        hdr = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = make_uint4(0, 0, 0, 0);
+    }
+};
+
+template <>
+struct AReg<TYPE_Q6_K> {
+    uint4 l0[2], l1[2], qh[2], sc;
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *blk, int n) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            l0[hh] = ld16_a2(blk + 64 * n + 16 * hh);
+            l1[hh] = ld16_a2(blk + 64 * n + 32 + 16 * hh);
+            qh[hh] = ld16_a2(blk + 128 + 32 * n + 16 * hh);
+        }
+        sc = ld16_a2(blk + 192);
+        d = ld_u16(blk + 208);
+    }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) l0[hh] = l1[hh] = qh[hh] = make_uint4(0, 0, 0, 0);
+        sc = make_uint4(0, 0, 0, 0);
+        d = 0;
+    }
+};
+
+// Q8_0: thread t owns blocks (row t/2, blocks 4*(t%2) .. +4) of the step
+template <>
+struct AReg<TYPE_Q8_0> {
+    uint4 q[4][2];
+    uint32_t d[4];
+    __device__ __forceinline__ void load(const uint8_t *blk0, int) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint8_t *blk = blk0 + b * Q80_BYTES;
+            d[b] = ld_u16(blk);
+            q[b][0] = ld16_a2(blk + 2);
+            q[b][1] = ld16_a2(blk + 18);
+        }
+    }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            d[b] = 0;
+            q[b][0] = q[b][1] = make_uint4(0, 0, 0, 0);
+        }
+    }
+};
+
+__device__ __forceinline__ void st16(int8_t *dst, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     *reinterpret_cast<uint4 *>(dst) = make_uint4(a, b, c, d);
 }
 
-template <int TYPE>
-__device__ void stage_a(Smem<TYPE> &sm, const uint8_t *w, int64_t row_stride, int64_t nrows, int64_t row0,
-                        int64_t kb) {
+__device__ __forceinline__ uint32_t minus32(uint32_t u) {
+    // bytewise u - 32 for bytes in [0, 63], without borrows between bytes
+    return ((u | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+template <int TYPE, int BN>
+__device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar) {
     const int t = threadIdx.x;
+    const int r = t >> 1, half = t & 1;
     if constexpr (TYPE == TYPE_Q4_K) {
-        const int r = t >> 1, half = t & 1;
         int8_t *arow = sm.a + r * LDA;
-        if (row0 + r < nrows) {
-            const uint8_t *blk = w + (row0 + r) * row_stride + kb * Q4K_BYTES;
-            const uint4 hdr = ld_u128(blk);
-            const float d = h2f(hdr.x);
-            if (half == 0) sm.admin[r] = h2f(hdr.x >> 16);
+        const uint32_t m = 0x0F0F0F0Fu;
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const int c = 2 * half + cc;
-                const uint4 q0 = ld_u128(blk + 16 + 32 * c);
-                const uint4 q1 = ld_u128(blk + 16 + 32 * c + 16);
-                const uint32_t m = 0x0F0F0F0Fu;
-                store16(arow + 64 * c + 0, q0.x & m, q0.y & m, q0.z & m, q0.w & m);
-                store16(arow + 64 * c + 16, q1.x & m, q1.y & m, q1.z & m, q1.w & m);
-                store16(arow + 64 * c + 32, (q0.x >> 4) & m, (q0.y >> 4) & m, (q0.z >> 4) & m, (q0.w >> 4) & m);
-                store16(arow + 64 * c + 48, (q1.x >> 4) & m, (q1.y >> 4) & m, (q1.z >> 4) & m, (q1.w >> 4) & m);
+        for (int cc = 0; cc < 2; ++cc) {
+            const int c = 2 * half + cc;
+            const uint4 q0 = ar.q[2 * cc], q1 = ar.q[2 * cc + 1];
+            st16(arow + 64 * c + 0, q0.x & m, q0.y & m, q0.z & m, q0.w & m);
+            st16(arow + 64 * c + 16, q1.x & m, q1.y & m, q1.z & m, q1.w & m);
+            st16(arow + 64 * c + 32, (q0.x >> 4) & m, (q0.y >> 4) & m, (q0.z >> 4) & m, (q0.w >> 4) & m);
+            st16(arow + 64 * c + 48, (q1.x >> 4) & m, (q1.y >> 4) & m, (q1.z >> 4) & m, (q1.w >> 4) & m);
 #pragma unroll
-                for (int jj = 0; jj < 2; ++jj) {
-                    const int j = 2 * c + jj;
-                    uint32_t sc, mn;
-                    q4k_scale_min(j, hdr.y, hdr.z, hdr.w, sc, mn);
-                    sm.ascale[j][r] = d * (float)sc;
-                    sm.amin[r][j] = (_Float16)(float)mn;
-                }
+            for (int jj = 0; jj < 2; ++jj) {
+                const int j = 2 * c + jj;
+                uint32_t sc, mn;
+                q4k_scale_min(j, ar.hdr.y, ar.hdr.z, ar.hdr.w, sc, mn);
+                sm.asc[j][r] = (_Float16)(float)sc;
+                sm.am[r][j] = (_Float16)(float)mn;
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) store16(arow + 128 * half + 16 * i, 0, 0, 0, 0);
-#pragma unroll
-            for (int jj = 0; jj < 4; ++jj) {
-                sm.ascale[4 * half + jj][r] = 0.0f;
-                sm.amin[r][4 * half + jj] = (_Float16)0.0f;
-            }
-            if (half == 0) sm.admin[r] = 0.0f;
+        }
+        if (half == 0) {
+            sm.ad[r] = h2f(ar.hdr.x);
+            sm.admin[r] = h2f(ar.hdr.x >> 16);
         }
     } else if constexpr (TYPE == TYPE_Q6_K) {
-        const int r = t >> 1, n = t & 1;
+        const int n = half;
         int8_t *arow = sm.a + r * LDA + 128 * n;
-        if (row0 + r < nrows) {
-            const uint8_t *blk = w + (row0 + r) * row_stride + kb * Q6K_BYTES;
-            const float d = h2f(ld_u16(blk + 208));
-            const uint4 sc = ld16_a2(blk + 192);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) sm.ascale[8 * n + i][r] = d * (float)(int8_t)byte_of(sc, 8 * n + i);
+        for (int hh = 0; hh < 2; ++hh) {
+            const uint32_t L0[4] = {ar.l0[hh].x, ar.l0[hh].y, ar.l0[hh].z, ar.l0[hh].w};
+            const uint32_t L1[4] = {ar.l1[hh].x, ar.l1[hh].y, ar.l1[hh].z, ar.l1[hh].w};
+            const uint32_t H[4] = {ar.qh[hh].x, ar.qh[hh].y, ar.qh[hh].z, ar.qh[hh].w};
+            uint32_t v[4][4];
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const uint4 l0 = ld16_a2(blk + 64 * n + 16 * hh);
-                const uint4 l1 = ld16_a2(blk + 64 * n + 32 + 16 * hh);
-                const uint4 qh = ld16_a2(blk + 128 + 32 * n + 16 * hh);
-                const uint32_t L0[4] = {l0.x, l0.y, l0.z, l0.w}, L1[4] = {l1.x, l1.y, l1.z, l1.w};
-                const uint32_t H[4] = {qh.x, qh.y, qh.z, qh.w};
-                uint32_t v[4][4];
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t m = 0x0F0F0F0Fu, hm = 0x30303030u;
-                    const uint32_t u0 = (L0[i] & m) | ((H[i] << 4) & hm);
-                    const uint32_t u1 = (L1[i] & m) | ((H[i] << 2) & hm);
-                    const uint32_t u2 = ((L0[i] >> 4) & m) | (H[i] & hm);
-                    const uint32_t u3 = ((L1[i] >> 4) & m) | ((H[i] >> 2) & hm);
-                    // bytewise -32 without borrows: (u | 0x80) - 0x20, then flip the top bit back
-                    v[0][i] = ((u0 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                    v[1][i] = ((u1 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                    v[2][i] = ((u2 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                    v[3][i] = ((u3 | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
-                }
-#pragma unroll
-                for (int g = 0; g < 4; ++g) store16(arow + 32 * g + 16 * hh, v[g][0], v[g][1], v[g][2], v[g][3]);
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t m = 0x0F0F0F0Fu, hm = 0x30303030u;
+                v[0][i] = minus32((L0[i] & m) | ((H[i] << 4) & hm));
+                v[1][i] = minus32((L1[i] & m) | ((H[i] << 2) & hm));
+                v[2][i] = minus32(((L0[i] >> 4) & m) | (H[i] & hm));
+                v[3][i] = minus32(((L1[i] >> 4) & m) | ((H[i] >> 2) & hm));
             }
-        } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) store16(arow + 16 * i, 0, 0, 0, 0);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) sm.ascale[8 * n + i][r] = 0.0f;
+            for (int g = 0; g < 4; ++g) st16(arow + 32 * g + 16 * hh, v[g][0], v[g][1], v[g][2], v[g][3]);
         }
-    } else {  // Q8_0: 8 blocks of 34 B per row per K-step
 #pragma unroll
-        for (int it = 0; it < 4; ++it) {
-            const int idx = t + NTHREADS * it;  // 0..1023 = row * 8 + block
-            const int r = idx >> 3, b = idx & 7;
-            int8_t *dst = sm.a + r * LDA + 32 * b;
-            if (row0 + r < nrows) {
-                const uint8_t *blk = w + (row0 + r) * row_stride + (kb * 8 + b) * Q80_BYTES;
-                const uint4 q0 = ld16_a2(blk + 2), q1 = ld16_a2(blk + 18);
-                store16(dst, q0.x, q0.y, q0.z, q0.w);
-                store16(dst + 16, q1.x, q1.y, q1.z, q1.w);
-                sm.ascale[b][r] = h2f(ld_u16(blk));
-            } else {
-                store16(dst, 0, 0, 0, 0);
-                store16(dst + 16, 0, 0, 0, 0);
-                sm.ascale[b][r] = 0.0f;
-            }
-        }
-    }
-}
-
-template <int TYPE>
-__device__ void stage_b(Smem<TYPE> &sm, const int8_t *yqs, const uint32_t *yds, int64_t Kp, int64_t ncols,
-                        int64_t col0, int64_t kb) {
-    const int t = threadIdx.x;
-    const int c = t >> 1, half = t & 1;
-    int8_t *brow = sm.b + c * LDA + 128 * half;
-    if (col0 + c < ncols) {
-        const uint8_t *src = reinterpret_cast<const uint8_t *>(yqs + (col0 + c) * Kp + kb * BK + 128 * half);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(brow + 16 * i) = ld_u128(src + 16 * i);
-        const uint4 ds = *reinterpret_cast<const uint4 *>(yds + (col0 + c) * (Kp / QK8) + kb * 8 + 4 * half);
-        const uint32_t dv[4] = {ds.x, ds.y, ds.z, ds.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sm.bd[4 * half + i][c] = h2f(dv[i]);
-            if constexpr (TYPE == TYPE_Q4_K) sm.bs8[c][4 * half + i] = __builtin_bit_cast(_Float16, (uint16_t)(dv[i] >> 16));
-        }
+        for (int i = 0; i < 8; ++i) sm.asc[8 * n + i][r] = (_Float16)(float)(int8_t)byte_of(ar.sc, 8 * n + i);
+        if (half == 0) sm.ad[r] = h2f(ar.d);
     } else {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) *reinterpret_cast<uint4 *>(brow + 16 * i) = make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sm.bd[4 * half + i][c] = 0.0f;
-            if constexpr (TYPE == TYPE_Q4_K) sm.bs8[c][4 * half + i] = (_Float16)0.0f;
+        for (int b = 0; b < 4; ++b) {
+            const int blk = 4 * half + b;
+            int8_t *dst = sm.a + r * LDA + 32 * blk;
+            st16(dst, ar.q[b][0].x, ar.q[b][0].y, ar.q[b][0].z, ar.q[b][0].w);
+            st16(dst + 16, ar.q[b][1].x, ar.q[b][1].y, ar.q[b][1].z, ar.q[b][1].w);
+            sm.asc[blk][r] = __builtin_bit_cast(_Float16, (uint16_t)ar.d[b]);
         }
     }
 }
 
-template <int TYPE>
-__global__ __launch_bounds__(NTHREADS) void mmq_kernel(const uint8_t *__restrict__ w, int64_t K, int64_t nrows,
-                                                       int64_t row_stride, const int8_t *__restrict__ yqs,
-                                                       const uint32_t *__restrict__ yds, int64_t ncols,
-                                                       float *__restrict__ dst, int64_t dst_col_stride) {
+// B: BN columns x (256 int8 + 8 (d, s)) per step, split into PARTS pieces of
+// BYTES bytes per thread.
+template <int BN>
+struct BReg {
+    static constexpr int BYTES = BN >= 128 ? 128 : BN * 256 / NTHREADS;  // bytes per part
+    static constexpr int PARTS = BN * 256 / (NTHREADS * BYTES);           // parts per thread
+    uint4 q[PARTS][BYTES / 16];
+    uint32_t ds[PARTS][BYTES / 32];
+};
+
+template <int BN>
+__device__ __forceinline__ void bpart(int p, int &c, int &off) {
+    constexpr int BYTES = BReg<BN>::BYTES;
+    constexpr int PER_COL = 256 / BYTES;
+    const int idx = threadIdx.x + NTHREADS * p;
+    c = idx / PER_COL;
+    off = (idx % PER_COL) * BYTES;
+}
+
+template <int TYPE, int BN>
+__global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+    const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
+    int64_t dst_col_stride,
+    // expert-grouped mode (tiles != nullptr): column tile table and gather/scatter maps
+    const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles, const int32_t *__restrict__ expert_off,
+    const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst) {
     using F = MmqFmt<TYPE>;
-    __shared__ Smem<TYPE> sm;
+    __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
     const int64_t row0 = (int64_t)blockIdx.x * BM;
-    const int64_t col0 = (int64_t)blockIdx.y * BN;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;  // wave's sub-tile
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
 
-    v16f acc[2][2], accm[2][2];
+    // column tile: dense (col0 .. col0+BN of ncols) or one expert's routed columns
+    int64_t col0 = (int64_t)blockIdx.y * BN, col_end = ncols;
+    const uint8_t *wexp = w;
+    if (tiles) {
+        if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup
+        const int e = tiles[2 * blockIdx.y], cs = tiles[2 * blockIdx.y + 1];
+        wexp = w + (int64_t)e * expert_stride;
+        col0 = cs;
+        const int64_t ce = expert_off[e + 1];
+        col_end = ce < col0 + BN ? ce : col0 + BN;
+    }
+
+    // wave -> sub-tile: TI x TJ MFMA tiles of 32x32 at (wr, wc)
+    constexpr int TI = BN == 128 ? 2 : 1;
+    constexpr int TJ = BN == 32 ? 1 : 2;
+    const int wr = BN == 128 ? (wave >> 1) * 64 : wave * 32;
+    const int wc = BN == 128 ? (wave & 1) * 64 : 0;
+
+    v16f acc[TI][TJ], accb[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) acc[i][j][v] = accm[i][j][v] = 0.0f;
+            for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+    // ---- register staging of one K-step ----
+    const int ar_row = threadIdx.x >> 1, ar_half = threadIdx.x & 1;
+    const bool a_ok = row0 + ar_row < nrows;
+    const uint8_t *a_row = wexp + (a_ok ? row0 + ar_row : 0) * row_stride;
+    AReg<TYPE> areg;
+    BReg<BN> breg;
+    auto gload = [&](int64_t kb) {
+        if (a_ok) {
+            if constexpr (TYPE == TYPE_Q4_K) areg.load(a_row + kb * Q4K_BYTES, ar_half);
+            else if constexpr (TYPE == TYPE_Q6_K) areg.load(a_row + kb * Q6K_BYTES, ar_half);
+            else areg.load(a_row + (kb * 8 + 4 * ar_half) * Q80_BYTES, 0);
+        } else {
+            areg.zero();
+        }
+#pragma unroll
+        for (int p = 0; p < BReg<BN>::PARTS; ++p) {
+            int c, off;
+            bpart<BN>(p, c, off);
+            const int64_t cc = col0 + c;
+            if (cc < col_end) {
+                const int64_t src = tiles ? (int64_t)col_src[cc] : cc;
+                const uint8_t *q = reinterpret_cast<const uint8_t *>(yqs + src * Kp + kb * BK + off);
+#pragma unroll
+                for (int i = 0; i < BReg<BN>::BYTES / 16; ++i) breg.q[p][i] = ld_u128(q + 16 * i);
+                const uint32_t *d = yds + src * (Kp / QK8) + kb * 8 + off / 32;
+#pragma unroll
+                for (int i = 0; i < BReg<BN>::BYTES / 32; ++i) breg.ds[p][i] = d[i];
+            } else {
+#pragma unroll
+                for (int i = 0; i < BReg<BN>::BYTES / 16; ++i) breg.q[p][i] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < BReg<BN>::BYTES / 32; ++i) breg.ds[p][i] = 0;
+            }
+        }
+    };
+    auto lstore = [&]() {
+        store_a<TYPE, BN>(sm, areg);
+#pragma unroll
+        for (int p = 0; p < BReg<BN>::PARTS; ++p) {
+            int c, off;
+            bpart<BN>(p, c, off);
+            int8_t *brow = sm.b + c * LDA + off;
+#pragma unroll
+            for (int i = 0; i < BReg<BN>::BYTES / 16; ++i) *reinterpret_cast<uint4 *>(brow + 16 * i) = breg.q[p][i];
+#pragma unroll
+            for (int i = 0; i < BReg<BN>::BYTES / 32; ++i) {
+                const uint32_t v = breg.ds[p][i];
+                sm.bd8[off / 32 + i][c] = __builtin_bit_cast(_Float16, (uint16_t)v);
+                if constexpr (TYPE == TYPE_Q4_K) sm.bs8[c][off / 32 + i] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+            }
+        }
+    };
 
     const int64_t nkb = K / BK;
+    gload(0);
     for (int64_t kb = 0; kb < nkb; ++kb) {
-        stage_a<TYPE>(sm, w, row_stride, nrows, row0, kb);
-        stage_b<TYPE>(sm, yqs, yds, Kp, ncols, col0, kb);
+        lstore();
         __syncthreads();
+        if (kb + 1 < nkb) gload(kb + 1);  // in flight during this step's MFMAs
+
+        if constexpr (TYPE != TYPE_Q8_0) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) accb[i][j][v] = 0.0f;
+        }
 
 #pragma unroll 2
         for (int g = 0; g < F::NG; ++g) {
-            v16i S[2][2];
-            if constexpr (F::GK == 32) {
-                v4i a[2], b[2];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    a[i] = *reinterpret_cast<const v4i *>(sm.a + (wr + 32 * i + li) * LDA + 32 * g + 16 * lh);
-                    b[i] = *reinterpret_cast<const v4i *>(sm.b + (wc + 32 * i + li) * LDA + 32 * g + 16 * lh);
-                }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const v16i z = {0};
-                        S[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], z, 0, 0, 0);
-                    }
-            } else {
-                long a[2], b[2];
-#pragma unroll
-                for (int i = 0; i < 2; ++i) {
-                    a[i] = *reinterpret_cast<const long *>(sm.a + (wr + 32 * i + li) * LDA + 16 * g + 8 * lh);
-                    b[i] = *reinterpret_cast<const long *>(sm.b + (wc + 32 * i + li) * LDA + 16 * g + 8 * lh);
-                }
-#pragma unroll
-                for (int i = 0; i < 2; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j) {
-                        const v16i z = {0};
-                        S[i][j] = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[i], b[j], z, 0, 0, 0);
-                    }
-            }
             const int qb = F::GK == 32 ? g : g >> 1;  // Q8_1 block of this group
+            // f16 outer-product operands: one live K slot (lanes 0..31, element 0)
+            v4h sa[TI], sb[TJ];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const float d8 = sm.bd[qb][wc + 32 * j + li];
+            for (int i = 0; i < TI; ++i) {
+                const _Float16 v = lh == 0 ? sm.asc[g][wr + 32 * i + li] : (_Float16)0.0f;
+                sa[i] = v4h{v, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            }
 #pragma unroll
-                for (int i = 0; i < 2; ++i) {
+            for (int j = 0; j < TJ; ++j) {
+                const _Float16 v = lh == 0 ? sm.bd8[qb][wc + 32 * j + li] : (_Float16)0.0f;
+                sb[j] = v4h{v, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            }
+            if constexpr (F::GK == 32) {
+                v4i a[TI], b[TJ];
 #pragma unroll
-                    for (int v4 = 0; v4 < 4; ++v4) {
-                        const int rr = wr + 32 * i + 8 * v4 + 4 * lh;
-                        const float4 sc = *reinterpret_cast<const float4 *>(&sm.ascale[g][rr]);
-                        const float scv[4] = {sc.x, sc.y, sc.z, sc.w};
+                for (int i = 0; i < TI; ++i)
+                    a[i] = *reinterpret_cast<const v4i *>(sm.a + (wr + 32 * i + li) * LDA + 32 * g + 16 * lh);
 #pragma unroll
-                        for (int u = 0; u < 4; ++u) {
-                            const int v = 4 * v4 + u;
-                            acc[i][j][v] += (float)S[i][j][v] * (d8 * scv[u]);
+                for (int j = 0; j < TJ; ++j)
+                    b[j] = *reinterpret_cast<const v4i *>(sm.b + (wc + 32 * j + li) * LDA + 32 * g + 16 * lh);
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) {
+                        const v16i z = {0};
+                        const v16f zf = {0};
+                        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], z, 0, 0, 0);
+                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sb[j], zf, 0, 0, 0);
+                        if constexpr (TYPE == TYPE_Q8_0) {
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf((float)S[v], sc[v], acc[i][j][v]);
+                        } else {
+#pragma unroll
+                            for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], sc[v], accb[i][j][v]);
                         }
                     }
-                }
+            } else {
+                long a[TI], b[TJ];
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+                    a[i] = *reinterpret_cast<const long *>(sm.a + (wr + 32 * i + li) * LDA + 16 * g + 8 * lh);
+#pragma unroll
+                for (int j = 0; j < TJ; ++j)
+                    b[j] = *reinterpret_cast<const long *>(sm.b + (wc + 32 * j + li) * LDA + 16 * g + 8 * lh);
+#pragma unroll
+                for (int i = 0; i < TI; ++i)
+#pragma unroll
+                    for (int j = 0; j < TJ; ++j) {
+                        const v16i z = {0};
+                        const v16f zf = {0};
+                        const v16i S = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[i], b[j], z, 0, 0, 0);
+                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sb[j], zf, 0, 0, 0);
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], sc[v], accb[i][j][v]);
+                    }
             }
         }
-        if constexpr (TYPE == TYPE_Q4_K) {
-            // min term: dmin[r] * sum_j m_j[r] * s8_j[c] over the 8 sub-blocks (K = 8, f16 MFMA)
+
+        if constexpr (TYPE != TYPE_Q8_0) {
+            // acc += d[r] * accb; Q4_K also subtracts dmin[r] * sum_j m_j[r] * s8_j[c]
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const v4h am = *reinterpret_cast<const v4h *>(&sm.amin[wr + 32 * i + li][4 * lh]);
-                float dm[16];
+            for (int i = 0; i < TI; ++i) {
+                float dr[16], dm[16];
 #pragma unroll
                 for (int v4 = 0; v4 < 4; ++v4) {
-                    const float4 t = *reinterpret_cast<const float4 *>(&sm.admin[wr + 32 * i + 8 * v4 + 4 * lh]);
-                    dm[4 * v4 + 0] = t.x;
-                    dm[4 * v4 + 1] = t.y;
-                    dm[4 * v4 + 2] = t.z;
-                    dm[4 * v4 + 3] = t.w;
+                    const int rr = wr + 32 * i + 8 * v4 + 4 * lh;
+                    const float4 t = *reinterpret_cast<const float4 *>(&sm.ad[rr]);
+                    dr[4 * v4 + 0] = t.x;
+                    dr[4 * v4 + 1] = t.y;
+                    dr[4 * v4 + 2] = t.z;
+                    dr[4 * v4 + 3] = t.w;
+                    if constexpr (TYPE == TYPE_Q4_K) {
+                        const float4 u = *reinterpret_cast<const float4 *>(&sm.admin[rr]);
+                        dm[4 * v4 + 0] = u.x;
+                        dm[4 * v4 + 1] = u.y;
+                        dm[4 * v4 + 2] = u.z;
+                        dm[4 * v4 + 3] = u.w;
+                    }
                 }
+                v4h am;
+                if constexpr (TYPE == TYPE_Q4_K) am = *reinterpret_cast<const v4h *>(&sm.am[wr + 32 * i + li][4 * lh]);
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    const v4h bm = *reinterpret_cast<const v4h *>(&sm.bs8[wc + 32 * j + li][4 * lh]);
-                    const v16f z = {0};
-                    const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm, z, 0, 0, 0);
+                for (int j = 0; j < TJ; ++j) {
+                    if constexpr (TYPE == TYPE_Q4_K) {
+                        const v4h bm = *reinterpret_cast<const v4h *>(&sm.bs8[wc + 32 * j + li][4 * lh]);
+                        const v16f zf = {0};
+                        const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm, zf, 0, 0, 0);
 #pragma unroll
-                    for (int v = 0; v < 16; ++v) accm[i][j][v] += dm[v] * P[v];
+                        for (int v = 0; v < 16; ++v)
+                            acc[i][j][v] = fmaf(dr[v], accb[i][j][v], fmaf(-dm[v], P[v], acc[i][j][v]));
+                    } else {
+#pragma unroll
+                        for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf(dr[v], accb[i][j][v], acc[i][j][v]);
+                    }
                 }
             }
         }
@@ -302,50 +437,100 @@ __global__ __launch_bounds__(NTHREADS) void mmq_kernel(const uint8_t *__restrict
     }
 
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             const int64_t c = col0 + wc + 32 * j + li;
-            if (c >= ncols) continue;
+            if (c >= col_end) continue;
+            const int64_t drow = tiles ? (int64_t)col_dst[c] : c;
+            float *o = dst + drow * dst_col_stride;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t r = row0 + wr + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (r < nrows) dst[c * dst_col_stride + r] = acc[i][j][v] - accm[i][j][v];
+                if (r < nrows) o[r] = acc[i][j][v];
             }
         }
 }
 
-template <int TYPE>
-int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs, const void *yds,
-           int64_t ncols, float *dst, int64_t dst_col_stride, hipStream_t s) {
-    const int64_t gx = (nrows + BM - 1) / BM, gy = (ncols + BN - 1) / BN;
-    if (gx > 0x7FFFFFFF || gy > 65535) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(mmq_kernel<TYPE>, dim3((unsigned)gx, (unsigned)gy), dim3(NTHREADS), 0, s,
-                       (const uint8_t *)w, K, nrows, row_stride, yqs, (const uint32_t *)yds, ncols, dst,
-                       dst_col_stride);
+template <int TYPE, int BN>
+int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride, const int8_t *yqs,
+           const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy, const int32_t *tiles,
+           const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src, const int32_t *col_dst,
+           hipStream_t s) {
+    const int64_t gx = (nrows + BM - 1) / BM;
+    if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), dim3((unsigned)gx, (unsigned)gy), dim3(NTHREADS), 0, s,
+                       (const uint8_t *)w, K, nrows, row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols, dst,
+                       dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst);
     return (int)hipGetLastError();
 }
 
+template <int TYPE>
+int launch_bn(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+              const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy,
+              const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
+              const int32_t *col_dst, hipStream_t s) {
+    // A 128-column tile needs more than the 256 registers per lane that two
+    // workgroups per CU leave (its two accumulator sets alone take 128), so
+    // tiles stop at 64 columns.
+    if (bn == 32)
+        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, s);
+    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, s);
+}
+
+int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
+    switch (type) {
+    case TYPE_Q4_K:
+        return (row_stride < K / QK_K * Q4K_BYTES || row_stride % 16 || (uintptr_t)w % 16) ? (int)hipErrorInvalidValue : 0;
+    case TYPE_Q6_K:
+        return (row_stride < K / QK_K * Q6K_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
+    case TYPE_Q8_0:
+        return (row_stride < K / QK8 * Q80_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
+    default:
+        return (int)hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
+
+// Column-tile width for a dense problem with `ncols` columns: the widest tile
+// that does not leave most of a tile empty.
+extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64; }
 
 extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                            const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
                            int64_t dst_col_stride, void *stream) {
     if (!w || !y_qs || !y_ds || !dst || K <= 0 || nrows <= 0 || ncols <= 0 || dst_col_stride < nrows)
         return (int)hipErrorInvalidValue;
-    if (K % BK != 0) return (int)hipErrorInvalidValue;  // Q8_0 rows of K % 256 != 0: not supported here
+    if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
+    if (int e = check_weights(type, w, K, row_stride)) return e;
+    const int bn = hip_qmm_mmq_tile_n(ncols);
+    const int64_t gy = (ncols + bn - 1) / bn;
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
-    case TYPE_Q4_K:
-        if (row_stride < K / QK_K * Q4K_BYTES || row_stride % 16 || (uintptr_t)w % 16) return (int)hipErrorInvalidValue;
-        return launch<TYPE_Q4_K>(w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, s);
-    case TYPE_Q6_K:
-        if (row_stride < K / QK_K * Q6K_BYTES || row_stride % 2 || (uintptr_t)w % 2) return (int)hipErrorInvalidValue;
-        return launch<TYPE_Q6_K>(w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, s);
-    case TYPE_Q8_0:
-        if (row_stride < K / QK8 * Q80_BYTES || row_stride % 2 || (uintptr_t)w % 2) return (int)hipErrorInvalidValue;
-        return launch<TYPE_Q8_0>(w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, s);
-    default:
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
+    }
+}
+
+// Expert-grouped form used by hip_qmm_mul_mat_id: column tiles come from the
+// device tile table written by the grouping kernel; `max_tiles` bounds the
+// grid (workgroups past the table's count exit at once).
+extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                   int64_t expert_stride, const int8_t *y_qs, const void *y_ds, float *dst,
+                                   int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
+                                   const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
+                                   const int32_t *col_dst, void *stream) {
+    if (!w || !y_qs || !y_ds || !dst || !tiles || !n_tiles || !expert_off || !col_src || !col_dst || K <= 0 ||
+        nrows <= 0 || dst_row_stride < nrows || max_tiles < 1)
         return (int)hipErrorInvalidValue;
+    if (K % BK != 0 || K > (1 << 30) || (bn != 32 && bn != 64)) return (int)hipErrorInvalidValue;
+    if (int e = check_weights(type, w, K, row_stride)) return e;
+    hipStream_t s = (hipStream_t)stream;
+    switch (type) {
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
     }
 }

@@ -51,6 +51,13 @@ def lib():
         L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_mul_mat.restype = i32
         L.hip_qmm_mul_mat.argtypes = [i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, ctypes.c_size_t, vp]
+        L.hip_qmm_mmq_tile_n.restype = i32
+        L.hip_qmm_mmq_tile_n.argtypes = [i64]
+        L.hip_qmm_mul_mat_id_workspace_size.restype = ctypes.c_size_t
+        L.hip_qmm_mul_mat_id_workspace_size.argtypes = [i32, i64, i64, i64, i64, i64]
+        L.hip_qmm_mul_mat_id.restype = i32
+        L.hip_qmm_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, i64,
+                                         vp, ctypes.c_size_t, vp]
         L.hip_qmm_block_dots.restype = i32
         L.hip_qmm_block_dots.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, vp]
         _lib = L
@@ -170,4 +177,39 @@ def mul_mat(qtype, w: torch.Tensor, x: torch.Tensor, out=None, workspace=None):
     out = torch.empty((n, nrows), dtype=torch.float32, device=x.device) if out is None else out
     _check(lib().hip_qmm_mul_mat(t, _ptr(w), K, nrows, rs, _ptr(x), n, x.stride(0), _ptr(out), out.stride(0),
                                  _ptr(workspace), workspace.numel(), _stream()), "hip_qmm_mul_mat")
+    return out
+
+
+def mul_mat_id(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, out=None, workspace=None):
+    """ggml_mul_mat_id(as, b, ids) (src/ggml/ops.zig:1104-1125).
+
+    w: uint8 [n_as, nrows, row_bytes] stacked expert weights; x: f32
+    [n_tokens, ne11, K] with ne11 = 1 (one row per token) or n_ids (one per
+    slot); ids: int32 [n_tokens, n_ids] expert per slot (-1: zero row).
+    Returns f32 [n_tokens, n_ids, nrows].
+    """
+    _require_cuda(w, x, ids)
+    if w.dtype != torch.uint8 or w.dim() != 3:
+        raise HipQmmError("w must be a 3-D uint8 tensor [n_as, nrows, row_bytes]")
+    if x.dtype != torch.float32 or x.dim() != 3:
+        raise HipQmmError("x must be a 3-D float32 tensor [n_tokens, ne11, K]")
+    if ids.dtype != torch.int32 or ids.dim() != 2:
+        raise HipQmmError("ids must be a 2-D int32 tensor [n_tokens, n_ids]")
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    n_as, nrows, rb = w.shape
+    n_tokens, ne11, K = x.shape
+    n_ids = ids.shape[1]
+    if ids.shape[0] != n_tokens:
+        raise HipQmmError("ids and x disagree on the token count")
+    if rb < row_size(t, K):
+        raise HipQmmError("weight rows are shorter than K elements of this type")
+    need = int(lib().hip_qmm_mul_mat_id_workspace_size(t, K, n_as, ne11, n_tokens, n_ids))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() < need:
+        raise HipQmmError(f"workspace too small: {workspace.numel()} < {need}")
+    out = torch.empty((n_tokens, n_ids, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_id(t, _ptr(w), K, nrows, w.stride(1), w.stride(0), n_as, _ptr(x), ne11, n_tokens,
+                                    K, _ptr(ids), n_ids, n_ids, _ptr(out), nrows, _ptr(workspace),
+                                    workspace.numel(), _stream()), "hip_qmm_mul_mat_id")
     return out

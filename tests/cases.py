@@ -54,3 +54,29 @@ def max_err_scaled(got, want):
     got = np.asarray(got, dtype=np.float64)
     want = np.asarray(want, dtype=np.float64)
     return float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-30))
+
+
+def route_top_k(n_tokens, n_experts, k, seed=SEED_ROUTER):
+    """Softmax over seeded N(0,1) router logits, top-k experts per token
+    (the ids of ggml's argsort_top_k, src/llama/graph.zig:3265-3318), and the
+    renormalised weights (norm_w, graph.zig:3343-3362)."""
+    logits = O.fill_normal(seed, n_tokens * n_experts).reshape(n_tokens, n_experts).astype(np.float64)
+    p = np.exp(logits - logits.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :k].astype(np.int32)
+    w = np.take_along_axis(p, ids, axis=1)
+    return ids, (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+
+
+def mul_mat_id_f64(t, wq_experts, nrows, K, y_q8_1_rows, ne11, ids):
+    """f64 evaluation of the GPU's Q8_1 formula for mul_mat_id, expert by expert.
+    y_q8_1_rows: AoS Q8_1 blocks of every activation row (n_tokens*ne11 rows)."""
+    n_tokens, n_ids = ids.shape
+    out = np.zeros((n_tokens, n_ids, nrows))
+    rb = y_q8_1_rows.shape[1]
+    for e in np.unique(ids[ids >= 0]):
+        ts, ss = np.nonzero(ids == e)
+        cols = np.stack([y_q8_1_rows[t * ne11 + s % ne11] for t, s in zip(ts, ss)]).reshape(len(ts), rb)
+        res = O.mul_mat_q8_1_f64(t, wq_experts[e], nrows, K, cols, len(ts))
+        out[ts, ss] = res
+    return out

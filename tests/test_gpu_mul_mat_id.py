@@ -1,0 +1,99 @@
+"""MUL_MAT_ID (expert-grouped MMQ) parity against the CPU ggml path
+(ggml_compute_forward_mul_mat_id restated) and the f64 Q8_1 formula."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, mul_mat_id_f64, nmse, route_top_k, weights_f32
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4
+F64_TOL = 2e-6
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+
+
+def _experts(t, n_as, nrows, K):
+    w = weights_f32(n_as * nrows, K)
+    return O.quantize_rows(t, w).reshape(n_as, nrows, -1)
+
+
+def _run(tname, n_as, nrows, K, x, ids):
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = _experts(t, n_as, nrows, K)
+    got = G.mul_mat_id(tname, torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(),
+                       torch.from_numpy(ids).cuda()).cpu().numpy()
+    return t, wq, got
+
+
+def _check(tname, n_as, nrows, K, x, ids):
+    import ggml_hip as G
+    t, wq, got = _run(tname, n_as, nrows, K, x, ids)
+    n_tokens, ne11, _ = x.shape
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=8)
+    assert np.all(got[ids < 0] == 0.0)
+    assert nmse(got, cpu) < NMSE_GATE, nmse(got, cpu)
+    y = G.quantize_q8_1(torch.from_numpy(x.reshape(-1, K)).cuda(), K).cpu().numpy()
+    ideal = mul_mat_id_f64(t, wq, nrows, K, y, ne11, ids)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    return got
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("ne11", [1, 3])
+def test_mul_mat_id_random_ids(tname, ne11):
+    n_as, nrows, K, n_tokens, n_ids = 8, 160, 512, 37, 3
+    rng = np.random.default_rng(5)
+    ids = rng.integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    x = np.array(acts(n_tokens * ne11, K)).reshape(n_tokens, ne11, K)
+    _check(tname, n_as, nrows, K, x, ids)
+
+
+def test_mul_mat_id_uneven_and_single_expert():
+    """Every slot routed to one expert (one long column list, many tiles)."""
+    n_as, nrows, K, n_tokens, n_ids = 16, 128, 256, 150, 2
+    ids = np.full((n_tokens, n_ids), 11, dtype=np.int32)
+    ids[::7, 1] = -1
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    _check("Q4_K", n_as, nrows, K, x, ids)
+
+
+def test_mul_mat_id_decode_one_token():
+    n_as, nrows, K = 32, 256, 1024
+    ids = np.array([[3, 17, 31, 0, 9, 22, 5, 30]], dtype=np.int32)
+    x = np.array(acts(1, K)).reshape(1, 1, K)
+    _check("Q4_K", n_as, nrows, K, x, ids)
+
+
+def test_mul_mat_id_all_ids_negative():
+    import ggml_hip as G
+    n_as, nrows, K, n_tokens, n_ids = 4, 64, 256, 5, 2
+    ids = np.full((n_tokens, n_ids), -1, dtype=np.int32)
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    wq = _experts(O.TYPE_Q4_K, n_as, nrows, K)
+    out = torch.full((n_tokens, n_ids, nrows), float("nan"), device="cuda")
+    got = G.mul_mat_id("Q4_K", torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(),
+                       torch.from_numpy(ids).cuda(), out=out).cpu().numpy()
+    assert np.all(got == 0.0)
+
+
+def test_mul_mat_id_config4_qwen3_moe_gate():
+    """Config 4 (Qwen3-30B-A3B shape): 128 experts of Q4_K 768x2048, 512 tokens
+    routed top-8 by softmax over seeded N(0,1) logits; broadcast activations
+    (gate/up projection).  Full size on the GPU, oracle on a token subset."""
+    import ggml_hip as G
+    n_as, nrows, K, n_tokens, k = 128, 768, 2048, 512, 8
+    ids, _ = route_top_k(n_tokens, n_as, k)
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    t = O.TYPE_Q4_K
+    wq = _experts(t, n_as, nrows, K)
+    got = G.mul_mat_id("Q4_K", torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(),
+                       torch.from_numpy(ids).cuda()).cpu().numpy()
+    sub = np.arange(0, n_tokens, 16)
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x[sub], ids[sub], nth=8)
+    assert nmse(got[sub], cpu) < NMSE_GATE
+    y = G.quantize_q8_1(torch.from_numpy(x[sub].reshape(-1, K)).cuda(), K).cpu().numpy()
+    ideal = mul_mat_id_f64(t, wq, nrows, K, y, 1, ids[sub])
+    assert max_err_scaled(got[sub], ideal) < F64_TOL
