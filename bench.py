@@ -40,20 +40,40 @@ M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
 T_MMQ = 512
 
 
+BLOCKS = {"Q4_K": (256, 144), "Q6_K": (256, 210), "Q8_0": (32, 34)}
+
+
 def q4k_row_bytes(k):
     return k // 256 * 144
 
 
+def row_bytes(qtype, k):
+    bs, bb = BLOCKS[qtype]
+    return k // bs * bb
+
+
+def random_blocks(torch, qtype, nrows, k, gen, device):
+    """Random but valid blocks of a weight type: random quant / scale bytes and
+    f16 super-block scales at the magnitude N(0, 0.02) weights quantize to.
+    Throughput does not depend on the values; parity tests use quantized
+    N(0, 0.02) weights instead."""
+    bs, bb = BLOCKS[qtype]
+    nb = nrows * (k // bs)
+    blocks = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, generator=gen, device="cpu")
+    def f16(v):
+        return torch.full((nb,), v, dtype=torch.float16).view(torch.uint8).view(nb, 2)
+    if qtype == "Q4_K":
+        blocks[:, 0:2] = f16(2.5e-4)
+        blocks[:, 2:4] = f16(4.0e-4)
+    elif qtype == "Q6_K":
+        blocks[:, 208:210] = f16(2.5e-4)
+    else:
+        blocks[:, 0:2] = f16(5.0e-4)
+    return blocks.view(nrows, row_bytes(qtype, k)).to(device)
+
+
 def random_q4k(torch, nrows, k, gen, device):
-    """Random but valid Q4_K blocks: random nibbles and 6-bit scale/min bytes,
-    f16 d/dmin at the magnitude N(0, 0.02) weights quantize to."""
-    nb = nrows * (k // 256)
-    blocks = torch.randint(0, 256, (nb, 144), dtype=torch.uint8, generator=gen, device="cpu")
-    d = torch.full((nb,), 2.5e-4, dtype=torch.float16).view(torch.uint8).view(nb, 2)
-    dmin = torch.full((nb,), 4.0e-4, dtype=torch.float16).view(torch.uint8).view(nb, 2)
-    blocks[:, 0:2] = d
-    blocks[:, 2:4] = dmin
-    return blocks.view(nrows, q4k_row_bytes(k)).to(device)
+    return random_blocks(torch, "Q4_K", nrows, k, gen, device)
 
 
 def event_time_kernel(torch, launch, n):
@@ -125,6 +145,80 @@ def cpu_baseline(w_host, x_host):
     }
 
 
+def run_suite(name, torch, G, dev, reps):
+    """Kernel-level measurements over the configs of BASELINE.json, one JSON
+    line per case (device time from a HIP graph of launches between events,
+    weights rotated over > 2 x the Infinity Cache)."""
+    gen = torch.Generator().manual_seed(42)
+    xg = torch.Generator().manual_seed(43)
+
+    def copies(qtype, nrows, k):
+        wb = nrows * row_bytes(qtype, k)
+        n = max(3, -(-2 * INFINITY_CACHE // wb))
+        return [random_blocks(torch, qtype, nrows, k, gen, dev) for _ in range(n)], wb
+
+    def emit(rec):
+        print(json.dumps(rec), flush=True)
+
+    if name in ("decode", "crossquant", "mmq"):
+        if name == "decode":
+            shapes = [("Q4_K", 4096, 4096, "attn_q/o"), ("Q4_K", 1024, 4096, "attn_k"), ("Q6_K", 1024, 4096, "attn_v"),
+                      ("Q4_K", 14336, 4096, "ffn_gate/up"), ("Q6_K", 4096, 14336, "ffn_down")]
+            batches = (1, 2, 4, 8)
+        elif name == "mmq":
+            shapes = [("Q4_K", 14336, 4096, "ffn_gate/up")]
+            batches = (128, 512, 2048)
+        else:
+            shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K") for k in (4096, 14336)]
+            batches = (1, 32, 512)
+        for qtype, M, Kx, label in shapes:
+            ws, wb = copies(qtype, M, Kx)
+            for T in batches:
+                x = torch.randn((T, Kx), generator=xg, dtype=torch.float32).to(dev)
+                qs, ds = G.quantize_q8_1_planar(x)
+                out = torch.empty((T, M), dtype=torch.float32, device=dev)
+                n = len(ws) * reps
+                if T <= 8:
+                    fn = lambda i: G.mul_mat_vec(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
+                    kern = "gemv"
+                else:
+                    fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
+                    kern = "mmq"
+                ms = event_time_batch(torch, fn, n)
+                alg = wb + Kx * 4 * T + M * 4 * T
+                ops = 2.0 * M * Kx * T
+                emit({"suite": name, "kernel": kern, "type": qtype, "shape": f"{M}x{Kx}", "label": label, "T": T,
+                      "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
+                      "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2),
+                      "int8_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)})
+            del ws
+            torch.cuda.empty_cache()
+    elif name == "moe":
+        n_as, n_tokens, k = 128, 512, 8
+        logits = torch.randn((n_tokens, n_as), generator=torch.Generator().manual_seed(44))
+        ids = torch.topk(torch.softmax(logits, dim=1), k, dim=1).indices.to(torch.int32).to(dev)
+        for label, M, Kx, ne11 in (("gate/up", 768, 2048, 1), ("down", 2048, 768, k)):
+            wb = n_as * M * row_bytes("Q4_K", Kx)
+            n = max(2, -(-2 * INFINITY_CACHE // wb))
+            ws = [random_blocks(torch, "Q4_K", n_as * M, Kx, gen, dev).view(n_as, M, -1) for _ in range(n)]
+            x = torch.randn((n_tokens, ne11, Kx), generator=xg, dtype=torch.float32).to(dev)
+            out = torch.empty((n_tokens, k, M), dtype=torch.float32, device=dev)
+            wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_id_workspace_size(12, Kx, n_as, ne11, n_tokens, k)),
+                              dtype=torch.uint8, device=dev)
+            fn = lambda i: G.mul_mat_id("Q4_K", ws[i % len(ws)], x, ids, out=out, workspace=wsp)  # noqa: E731
+            ms = event_time_batch(torch, fn, n * reps)
+            alg = wb + n_tokens * ne11 * Kx * 4 + n_tokens * k * M * 4
+            ops = 2.0 * M * Kx * n_tokens * k
+            emit({"suite": name, "kernel": "mul_mat_id (quantize + group + grouped MMQ)", "type": "Q4_K",
+                  "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": n_tokens, "top_k": k,
+                  "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
+                  "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2)})
+            del ws
+            torch.cuda.empty_cache()
+    else:
+        raise SystemExit(f"unknown suite {name}")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -132,6 +226,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe"],
+                    help="instead of the headline line, measure every case of one BASELINE config")
+    ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -142,6 +239,9 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     G.lib()
+    if args.suite:
+        run_suite(args.suite, torch, G, dev, args.reps)
+        return
 
     gen = torch.Generator().manual_seed(42)
     w_bytes = M * q4k_row_bytes(K)

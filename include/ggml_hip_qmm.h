@@ -65,9 +65,10 @@ int hip_qmm_quantize_q8_1(const float *x, void *y_q8_1, int64_t ne00, int64_t s0
 int hip_qmm_quantize_q8_1_planar(const float *x, int64_t K, int64_t ncols, int64_t x_col_stride,
                                  int8_t *qs, void *ds, void *stream);
 
-/* Bytes of workspace hip_qmm_mul_mat / _mul_mat_vec / _mmq need for ncols
- * activation columns of K (the planar Q8_1 copy). */
-size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t ncols);
+/* Bytes of workspace hip_qmm_mul_mat needs for an nrows x K weight and ncols
+ * activation columns: the planar Q8_1 copy, plus split-K partials when the
+ * MMQ spreads K over several workgroups. */
+size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
 /*
  * Decode GEMV against planar Q8_1 activations, 1..8 columns: dst[c*dst_col_stride + r]
@@ -92,12 +93,21 @@ int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t r
 /*
  * int8-MFMA GEMM against planar Q8_1 activations for any column count
  * (K a multiple of 256).  Replaces launch_mul_mat_q (src/ggml/cuda/mmq.zig:282-408).
+ * When the output tiles alone would leave the GPU under-filled, K is split
+ * over several workgroups (the reference's stream-k fixup, mmq.zig:359-407)
+ * and the partials, kept in `workspace`, are summed in a fixed order; with
+ * no or too small a workspace the GEMM runs unsplit.
  */
 int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *y_qs,
-                const void *y_ds, int64_t ncols, float *dst, int64_t dst_col_stride, void *stream);
+                const void *y_ds, int64_t ncols, float *dst, int64_t dst_col_stride, void *workspace,
+                size_t workspace_size, void *stream);
 
-/* Column-tile width hip_qmm_mmq picks for `ncols` columns (32 or 64). */
+/* Bytes of split-K workspace hip_qmm_mmq uses for this shape (0: no split). */
+size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
+
+/* Column-tile width (32 or 64) and K-split factor hip_qmm_mmq picks. */
 int hip_qmm_mmq_tile_n(int64_t ncols);
+int hip_qmm_mmq_split_k(int64_t K, int64_t nrows, int64_t ncols);
 
 /*
  * Expert-grouped MMQ over device-side tile tables (see hip_qmm_mul_mat_id):

@@ -9,25 +9,33 @@ using namespace qmm;
 
 extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                            const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
-                           int64_t dst_col_stride, void *stream);
+                           int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
+extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
+
+namespace {
+size_t q8_1_bytes(int64_t K, int64_t ncols) {
+    const int64_t Kp = pad_k(K);
+    return (size_t)(ncols * Kp) + (size_t)(ncols * (Kp / QK8)) * 4u;  // qs plane, then ds plane
+}
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+}  // namespace
 
 extern "C" int hip_qmm_version(void) { return (0 << 16) | 1; }
 
 extern "C" int64_t hip_qmm_row_padding(void) { return ROW_PAD; }
 
-extern "C" size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t ncols) {
-    (void)type;
+extern "C" size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || ncols <= 0) return 0;
-    const int64_t Kp = pad_k(K);
-    // qs plane (ncols * Kp bytes, a multiple of 512) followed by the ds plane
-    return (size_t)(ncols * Kp) + (size_t)(ncols * (Kp / QK8)) * 4u;
+    size_t n = q8_1_bytes(K, ncols);
+    if (ncols > 8 && K % 256 == 0 && nrows > 0) n = align256(n) + hip_qmm_mmq_workspace_size(type, K, nrows, ncols);
+    return n;
 }
 
 extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
                                int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream) {
     if (ncols <= 0 || !workspace || !x || !dst) return (int)hipErrorInvalidValue;
-    if (workspace_size < hip_qmm_mul_mat_workspace_size(type, K, ncols)) return (int)hipErrorInvalidValue;
+    if (workspace_size < hip_qmm_mul_mat_workspace_size(type, K, nrows, ncols)) return (int)hipErrorInvalidValue;
     if ((uintptr_t)workspace % 16) return (int)hipErrorInvalidValue;
     const int64_t Kp = pad_k(K);
     int8_t *qs = (int8_t *)workspace;
@@ -35,8 +43,11 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     if (int e = hip_qmm_quantize_q8_1_planar(x, K, ncols, x_col_stride, qs, ds, stream)) return e;
     if (ncols <= 8)
         return hip_qmm_mul_mat_vec(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, stream);
-    if (K % 256 == 0)
-        return hip_qmm_mmq(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, stream);
+    if (K % 256 == 0) {
+        const size_t off = align256(q8_1_bytes(K, ncols));
+        return hip_qmm_mmq(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, (uint8_t *)workspace + off,
+                           workspace_size - off, stream);
+    }
     // Q8_0 rows whose length is not a multiple of 256 (the MMQ K-step): GEMV
     // over column groups of 8.
     for (int64_t c0 = 0; c0 < ncols; c0 += 8) {

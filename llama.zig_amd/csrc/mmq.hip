@@ -31,6 +31,8 @@
 // B use the same slice, so the sum over K is formed whatever order the
 // hardware gives the slices.  Results: value v of lane l is row
 // 8*(v/4) + 4*(l/32) + v%4, column l%32.
+#include <type_traits>
+
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
@@ -54,16 +56,20 @@ struct MmqFmt {
     static constexpr int NG = BK / GK;                      // scale groups per K-step
 };
 
+// Every member is 16-byte aligned so the compiler can prove it and read the
+// MFMA operands with ds_read_b128 (conflict-free with the 272-byte row
+// stride); unproven alignment degrades them to ds_read2_b32 pairs, whose
+// rows r and r+16 share banks.
 template <int TYPE, int BN>
 struct Smem {
-    int8_t a[BM * LDA];
-    int8_t b[BN * LDA];
-    _Float16 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
-    _Float16 bd8[8][BN];                 // d8 per (Q8_1 block, column)
-    float ad[BM];                        // d per row (Q4_K, Q6_K)
-    float admin[BM];                     // dmin per row (Q4_K)
-    _Float16 am[BM][8];                  // m_j per row (Q4_K)
-    _Float16 bs8[BN][8];                 // s8 per column (Q4_K)
+    alignas(16) int8_t a[BM * LDA];
+    alignas(16) int8_t b[BN * LDA];
+    alignas(16) _Float16 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
+    alignas(16) _Float16 bd8[8][BN];                 // d8 per (Q8_1 block, column)
+    alignas(16) float ad[BM];                        // d per row (Q4_K, Q6_K)
+    alignas(16) float admin[BM];                     // dmin per row (Q4_K)
+    alignas(16) _Float16 am[BM][8];                  // m_j per row (Q4_K)
+    alignas(16) _Float16 bs8[BN][8];                 // s8 per column (Q4_K)
 };
 
 // Global data of one K-step, held in registers between the load and the LDS
@@ -229,7 +235,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     int64_t dst_col_stride,
     // expert-grouped mode (tiles != nullptr): column tile table and gather/scatter maps
     const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles, const int32_t *__restrict__ expert_off,
-    const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst) {
+    const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst,
+    // split-K (gridDim.z > 1): this workgroup's share of the K-steps goes to
+    // partial[z][col][row] instead of dst
+    float *__restrict__ partial) {
     using F = MmqFmt<TYPE>;
     __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
@@ -317,80 +326,69 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         }
     };
 
-    const int64_t nkb = K / BK;
-    gload(0);
-    for (int64_t kb = 0; kb < nkb; ++kb) {
+    const int64_t nkb_all = K / BK;
+    const int64_t kb_begin = nkb_all * blockIdx.z / gridDim.z;
+    const int64_t nkb = nkb_all * (blockIdx.z + 1) / gridDim.z;
+    gload(kb_begin);
+    for (int64_t kb = kb_begin; kb < nkb; ++kb) {
         lstore();
         __syncthreads();
         if (kb + 1 < nkb) gload(kb + 1);  // in flight during this step's MFMAs
 
-        if constexpr (TYPE != TYPE_Q8_0) {
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-#pragma unroll
-                    for (int v = 0; v < 16; ++v) accb[i][j][v] = 0.0f;
-        }
-
-#pragma unroll 2
-        for (int g = 0; g < F::NG; ++g) {
+        // One step is NG x (TI*TJ) (scale group, tile) pairs.  Each pair is an
+        // int8 MFMA (the exact block dots) plus an f16 MFMA (the exact scale
+        // outer product); its VALU epilogue is one convert and one FMA per
+        // output.  The pairs are software-pipelined one deep: pair p+1's MFMAs
+        // are issued before pair p's epilogue so the matrix core runs under the
+        // VALU work.  The first pair of a super-block writes accb instead of
+        // accumulating into it.
+        constexpr int NT = TI * TJ;
+        constexpr int NP = F::NG * NT;
+        using SType = typename std::conditional<F::GK == 32, v4i, long>::type;
+        auto issue = [&](int p, v16i &S, v16f &SC) {
+            const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
             const int qb = F::GK == 32 ? g : g >> 1;  // Q8_1 block of this group
-            // f16 outer-product operands: one live K slot (lanes 0..31, element 0)
-            v4h sa[TI], sb[TJ];
+            // f16 outer-product operands: one live K slot (lanes 0..31, element 0);
+            // read unconditionally, then zero the upper half-wave's slot
+            const _Float16 va = sm.asc[g][wr + 32 * i + li];
+            const _Float16 vb = sm.bd8[qb][wc + 32 * j + li];
+            const v4h sa = v4h{lh == 0 ? va : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            const v4h sb = v4h{lh == 0 ? vb : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            const v16i z = {0};
+            const v16f zf = {0};
+            const SType a = *reinterpret_cast<const SType *>(sm.a + (wr + 32 * i + li) * LDA + F::GK * g + (F::GK / 2) * lh);
+            const SType b = *reinterpret_cast<const SType *>(sm.b + (wc + 32 * j + li) * LDA + F::GK * g + (F::GK / 2) * lh);
+            if constexpr (F::GK == 32) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
+            else S = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, zf, 0, 0, 0);
+        };
+        auto consume = [&](int p, const v16i &S, const v16f &SC) {
+            const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
+            if constexpr (TYPE == TYPE_Q8_0) {
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const _Float16 v = lh == 0 ? sm.asc[g][wr + 32 * i + li] : (_Float16)0.0f;
-                sa[i] = v4h{v, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-            }
+                for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf((float)S[v], SC[v], acc[i][j][v]);
+            } else if (g == 0) {
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const _Float16 v = lh == 0 ? sm.bd8[qb][wc + 32 * j + li] : (_Float16)0.0f;
-                sb[j] = v4h{v, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-            }
-            if constexpr (F::GK == 32) {
-                v4i a[TI], b[TJ];
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-                    a[i] = *reinterpret_cast<const v4i *>(sm.a + (wr + 32 * i + li) * LDA + 32 * g + 16 * lh);
-#pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    b[j] = *reinterpret_cast<const v4i *>(sm.b + (wc + 32 * j + li) * LDA + 32 * g + 16 * lh);
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j) {
-                        const v16i z = {0};
-                        const v16f zf = {0};
-                        const v16i S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[i], b[j], z, 0, 0, 0);
-                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sb[j], zf, 0, 0, 0);
-                        if constexpr (TYPE == TYPE_Q8_0) {
-#pragma unroll
-                            for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf((float)S[v], sc[v], acc[i][j][v]);
-                        } else {
-#pragma unroll
-                            for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], sc[v], accb[i][j][v]);
-                        }
-                    }
+                for (int v = 0; v < 16; ++v) accb[i][j][v] = (float)S[v] * SC[v];
             } else {
-                long a[TI], b[TJ];
 #pragma unroll
-                for (int i = 0; i < TI; ++i)
-                    a[i] = *reinterpret_cast<const long *>(sm.a + (wr + 32 * i + li) * LDA + 16 * g + 8 * lh);
+                for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], SC[v], accb[i][j][v]);
+            }
+        };
+        // The 64-column K-quant tiles have no registers left for a second
+        // pair in flight (it would spill), so they issue and consume in turn.
+        constexpr bool PIPE = !(BN == 64 && TYPE != TYPE_Q8_0);
+        v16i Sbuf[2];
+        v16f SCbuf[2];
+        if constexpr (PIPE) issue(0, Sbuf[0], SCbuf[0]);
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
-                    b[j] = *reinterpret_cast<const long *>(sm.b + (wc + 32 * j + li) * LDA + 16 * g + 8 * lh);
-#pragma unroll
-                for (int i = 0; i < TI; ++i)
-#pragma unroll
-                    for (int j = 0; j < TJ; ++j) {
-                        const v16i z = {0};
-                        const v16f zf = {0};
-                        const v16i S = __builtin_amdgcn_mfma_i32_32x32x16_i8(a[i], b[j], z, 0, 0, 0);
-                        const v16f sc = __builtin_amdgcn_mfma_f32_32x32x8f16(sa[i], sb[j], zf, 0, 0, 0);
-#pragma unroll
-                        for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], sc[v], accb[i][j][v]);
-                    }
+        for (int p = 0; p < NP; ++p) {
+            if constexpr (PIPE) {
+                if (p + 1 < NP) issue(p + 1, Sbuf[(p + 1) & 1], SCbuf[(p + 1) & 1]);
+                consume(p, Sbuf[p & 1], SCbuf[p & 1]);
+            } else {
+                issue(p, Sbuf[0], SCbuf[0]);
+                consume(p, Sbuf[0], SCbuf[0]);
             }
         }
 
@@ -443,7 +441,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
             const int64_t c = col0 + wc + 32 * j + li;
             if (c >= col_end) continue;
             const int64_t drow = tiles ? (int64_t)col_dst[c] : c;
-            float *o = dst + drow * dst_col_stride;
+            float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + drow * dst_col_stride;
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t r = row0 + wr + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
@@ -452,30 +450,48 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         }
 }
 
+// dst[c][r] = sum over z of partial[z][c][r], in z order (deterministic)
+__global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial, int split, int64_t nrows,
+                                                     int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= nrows * ncols) return;
+    const int64_t c = i / nrows, r = i % nrows;
+    float acc = 0.0f;
+    for (int z = 0; z < split; ++z) acc += partial[(int64_t)z * nrows * ncols + i];
+    dst[c * dst_col_stride + r] = acc;
+}
+
 template <int TYPE, int BN>
 int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride, const int8_t *yqs,
            const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy, const int32_t *tiles,
            const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src, const int32_t *col_dst,
-           hipStream_t s) {
+           int split, float *partial, hipStream_t s) {
     const int64_t gx = (nrows + BM - 1) / BM;
-    if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), dim3((unsigned)gx, (unsigned)gy), dim3(NTHREADS), 0, s,
-                       (const uint8_t *)w, K, nrows, row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols, dst,
-                       dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst);
-    return (int)hipGetLastError();
+    if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), dim3((unsigned)gx, (unsigned)gy, (unsigned)split), dim3(NTHREADS), 0,
+                       s, (const uint8_t *)w, K, nrows, row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols,
+                       dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, split > 1 ? partial : nullptr);
+    if (int e = (int)hipGetLastError()) return e;
+    if (split > 1) {
+        const int64_t n = nrows * ncols;
+        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, split, nrows,
+                           ncols, dst, dst_col_stride);
+        return (int)hipGetLastError();
+    }
+    return 0;
 }
 
 template <int TYPE>
 int launch_bn(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
               const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy,
               const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
-              const int32_t *col_dst, hipStream_t s) {
+              const int32_t *col_dst, int split, float *partial, hipStream_t s) {
     // A 128-column tile needs more than the 256 registers per lane that two
     // workgroups per CU leave (its two accumulator sets alone take 128), so
     // tiles stop at 64 columns.
     if (bn == 32)
-        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, s);
-    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, s);
+        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, split, partial, s);
+    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, split, partial, s);
 }
 
 int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
@@ -497,20 +513,45 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
 // that does not leave most of a tile empty.
 extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64; }
 
+// K-split factor: spread the K-steps over more workgroups until about two
+// workgroups per CU exist (256 CUs on MI355X), at least one K-step each.
+extern "C" int hip_qmm_mmq_split_k(int64_t K, int64_t nrows, int64_t ncols) {
+    if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
+    const int64_t bn = hip_qmm_mmq_tile_n(ncols);
+    const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
+    const int64_t nkb = K / BK;
+    int64_t split = (512 + wgs - 1) / wgs;
+    if (split > nkb) split = nkb;
+    if (split > 16) split = 16;
+    return split < 1 ? 1 : (int)split;
+}
+
+extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    (void)type;
+    const int split = hip_qmm_mmq_split_k(K, nrows, ncols);
+    return split > 1 ? (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) : 0;
+}
+
 extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                            const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
-                           int64_t dst_col_stride, void *stream) {
+                           int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream) {
     if (!w || !y_qs || !y_ds || !dst || K <= 0 || nrows <= 0 || ncols <= 0 || dst_col_stride < nrows)
         return (int)hipErrorInvalidValue;
     if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
     const int bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
+    // split K only when the caller's workspace holds the partials
+    int split = hip_qmm_mmq_split_k(K, nrows, ncols);
+    if (split > 1 && (!workspace || workspace_size < hip_qmm_mmq_workspace_size(type, K, nrows, ncols) ||
+                      (uintptr_t)workspace % 16))
+        split = 1;
+    float *partial = (float *)workspace;
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, s);
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     }
 }
 
@@ -529,8 +570,8 @@ extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t n
     if (int e = check_weights(type, w, K, row_stride)) return e;
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, s);
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     }
 }

@@ -44,11 +44,15 @@ def lib():
         L.hip_qmm_quantize_q8_1_planar.restype = i32
         L.hip_qmm_quantize_q8_1_planar.argtypes = [vp, i64, i64, i64, vp, vp, vp]
         L.hip_qmm_mul_mat_workspace_size.restype = ctypes.c_size_t
-        L.hip_qmm_mul_mat_workspace_size.argtypes = [i32, i64, i64]
+        L.hip_qmm_mul_mat_workspace_size.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mul_mat_vec.restype = i32
         L.hip_qmm_mul_mat_vec.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_mmq.restype = i32
-        L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
+        L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp, ctypes.c_size_t, vp]
+        L.hip_qmm_mmq_workspace_size.restype = ctypes.c_size_t
+        L.hip_qmm_mmq_workspace_size.argtypes = [i32, i64, i64, i64]
+        L.hip_qmm_mmq_split_k.restype = i32
+        L.hip_qmm_mmq_split_k.argtypes = [i64, i64, i64]
         L.hip_qmm_mul_mat.restype = i32
         L.hip_qmm_mul_mat.argtypes = [i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mmq_tile_n.restype = i32
@@ -136,12 +140,17 @@ def mul_mat_vec(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tens
     return out
 
 
-def mmq(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=None):
-    """int8-MFMA GEMM against planar Q8_1 activations (any column count)."""
+def mmq(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=None, workspace=None):
+    """int8-MFMA GEMM against planar Q8_1 activations (any column count).
+    `workspace` (uint8, >= mmq_workspace_size) enables the K split."""
     t, nrows, rs = _weight_args(qtype, w, K)
     n = qs.shape[0]
     out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
-    _check(lib().hip_qmm_mmq(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
+    need = int(lib().hip_qmm_mmq_workspace_size(t, K, nrows, n))
+    if workspace is None and need:
+        workspace = torch.empty(need, dtype=torch.uint8, device=w.device)
+    wp, wn = (_ptr(workspace), workspace.numel()) if workspace is not None else (None, 0)
+    _check(lib().hip_qmm_mmq(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0), wp, wn,
                              _stream()), "hip_qmm_mmq")
     return out
 
@@ -157,9 +166,9 @@ def block_dots(qtype, w: torch.Tensor, K: int, qs: torch.Tensor):
     return out
 
 
-def workspace_size(qtype, K: int, ncols: int) -> int:
+def workspace_size(qtype, K: int, ncols: int, nrows: int = 0) -> int:
     t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
-    return int(lib().hip_qmm_mul_mat_workspace_size(t, K, ncols))
+    return int(lib().hip_qmm_mul_mat_workspace_size(t, K, nrows, ncols))
 
 
 def mul_mat(qtype, w: torch.Tensor, x: torch.Tensor, out=None, workspace=None):
@@ -169,7 +178,7 @@ def mul_mat(qtype, w: torch.Tensor, x: torch.Tensor, out=None, workspace=None):
         raise HipQmmError("x must be a 2-D float32 tensor [ncols, K]")
     n, K = x.shape
     t, nrows, rs = _weight_args(qtype, w, K)
-    need = workspace_size(t, K, n)
+    need = workspace_size(t, K, n, nrows)
     if workspace is None:
         workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
     elif workspace.numel() < need:

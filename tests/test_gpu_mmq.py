@@ -48,3 +48,30 @@ def test_mmq_config2_rows_subset():
     assert max_err_scaled(got[:, rows], ideal) < F64_TOL
     cpu = O.mul_mat(O.TYPE_Q4_K, wq[rows], len(rows), K, x, nth=8)
     assert nmse(got[:, rows], cpu) < NMSE_GATE
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("nrows,K,ncols", [(128, 14336, 9), (256, 4096, 40), (2048, 14336, 32)])
+def test_mmq_split_k(tname, nrows, K, ncols):
+    """Under-filled grids split K over workgroups; the partials are summed in a
+    fixed order, so two runs agree bit for bit, and split and unsplit results
+    both match the f64 formula."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    split = G.lib().hip_qmm_mmq_split_k(K, nrows, ncols)
+    assert split > 1
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    a = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    b = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    assert np.array_equal(a, b)
+    # a workspace too small for the partials runs the GEMM unsplit
+    tiny = torch.empty(16, dtype=torch.uint8, device="cuda")
+    u = G.mmq(tname, w_d, K, qs, ds, workspace=tiny).cpu().numpy()
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(a, ideal) < F64_TOL, max_err_scaled(a, ideal)
+    assert max_err_scaled(u, ideal) < F64_TOL, max_err_scaled(u, ideal)
