@@ -64,8 +64,14 @@ template <int TYPE, int BN>
 struct Smem {
     alignas(16) int8_t a[BM * LDA];
     alignas(16) int8_t b[BN * LDA];
-    alignas(16) _Float16 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
-    alignas(16) _Float16 bd8[8][BN];                 // d8 per (Q8_1 block, column)
+    // Scale operands of the f16 outer-product MFMA, stored as the 8-byte
+    // (4 x f16) operand each lane hands the MFMA, so reading one is a single
+    // ds_read_b64 with no VALU work.  asc holds {s, 0, 0, 0}; bd8[h] holds
+    // the column's d8 in K slot h: lanes 0-31 (K slots 0-3) read bd8[0],
+    // lanes 32-63 (slots 4-7) read bd8[1], so only slot 0 pairs two nonzero
+    // values and the MFMA returns exactly s_r * d8_c.
+    alignas(16) uint2 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
+    alignas(16) uint2 bd8[2][8][BN];              // d8 per (Q8_1 block, column)
     alignas(16) float ad[BM];                        // d per row (Q4_K, Q6_K)
     alignas(16) float admin[BM];                     // dmin per row (Q4_K)
     alignas(16) _Float16 am[BM][8];                  // m_j per row (Q4_K)
@@ -137,6 +143,10 @@ struct AReg<TYPE_Q8_0> {
     }
 };
 
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
 __device__ __forceinline__ void st16(int8_t *dst, uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
     *reinterpret_cast<uint4 *>(dst) = make_uint4(a, b, c, d);
 }
@@ -166,7 +176,7 @@ __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar
                 const int j = 2 * c + jj;
                 uint32_t sc, mn;
                 q4k_scale_min(j, ar.hdr.y, ar.hdr.z, ar.hdr.w, sc, mn);
-                sm.asc[j][r] = (_Float16)(float)sc;
+                sm.asc[j][r] = make_uint2(f16_bits((float)sc), 0u);
                 sm.am[r][j] = (_Float16)(float)mn;
             }
         }
@@ -195,7 +205,7 @@ __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar
             for (int g = 0; g < 4; ++g) st16(arow + 32 * g + 16 * hh, v[g][0], v[g][1], v[g][2], v[g][3]);
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) sm.asc[8 * n + i][r] = (_Float16)(float)(int8_t)byte_of(ar.sc, 8 * n + i);
+        for (int i = 0; i < 8; ++i) sm.asc[8 * n + i][r] = make_uint2(f16_bits((float)(int8_t)byte_of(ar.sc, 8 * n + i)), 0u);
         if (half == 0) sm.ad[r] = h2f(ar.d);
     } else {
 #pragma unroll
@@ -204,7 +214,7 @@ __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar
             int8_t *dst = sm.a + r * LDA + 32 * blk;
             st16(dst, ar.q[b][0].x, ar.q[b][0].y, ar.q[b][0].z, ar.q[b][0].w);
             st16(dst + 16, ar.q[b][1].x, ar.q[b][1].y, ar.q[b][1].z, ar.q[b][1].w);
-            sm.asc[blk][r] = __builtin_bit_cast(_Float16, (uint16_t)ar.d[b]);
+            sm.asc[blk][r] = make_uint2(ar.d[b] & 0xFFFFu, 0u);
         }
     }
 }
@@ -320,7 +330,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
 #pragma unroll
             for (int i = 0; i < BReg<BN>::BYTES / 32; ++i) {
                 const uint32_t v = breg.ds[p][i];
-                sm.bd8[off / 32 + i][c] = __builtin_bit_cast(_Float16, (uint16_t)v);
+                sm.bd8[0][off / 32 + i][c] = make_uint2(v & 0xFFFFu, 0u);
+                sm.bd8[1][off / 32 + i][c] = make_uint2(v << 16, 0u);
                 if constexpr (TYPE == TYPE_Q4_K) sm.bs8[c][off / 32 + i] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
             }
         }
@@ -345,22 +356,24 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         constexpr int NT = TI * TJ;
         constexpr int NP = F::NG * NT;
         using SType = typename std::conditional<F::GK == 32, v4i, long>::type;
-        auto issue = [&](int p, v16i &S, v16f &SC) {
+        struct Ops {
+            SType a, b;
+            v4h sa, sb;
+        };
+        auto load_ops = [&](int p, Ops &o) {
             const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
             const int qb = F::GK == 32 ? g : g >> 1;  // Q8_1 block of this group
-            // f16 outer-product operands: one live K slot (lanes 0..31, element 0);
-            // read unconditionally, then zero the upper half-wave's slot
-            const _Float16 va = sm.asc[g][wr + 32 * i + li];
-            const _Float16 vb = sm.bd8[qb][wc + 32 * j + li];
-            const v4h sa = v4h{lh == 0 ? va : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
-            const v4h sb = v4h{lh == 0 ? vb : (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f, (_Float16)0.0f};
+            o.sa = __builtin_bit_cast(v4h, sm.asc[g][wr + 32 * i + li]);
+            o.sb = __builtin_bit_cast(v4h, sm.bd8[lh][qb][wc + 32 * j + li]);
+            o.a = *reinterpret_cast<const SType *>(sm.a + (wr + 32 * i + li) * LDA + F::GK * g + (F::GK / 2) * lh);
+            o.b = *reinterpret_cast<const SType *>(sm.b + (wc + 32 * j + li) * LDA + F::GK * g + (F::GK / 2) * lh);
+        };
+        auto issue = [&](const Ops &o, v16i &S, v16f &SC) {
             const v16i z = {0};
             const v16f zf = {0};
-            const SType a = *reinterpret_cast<const SType *>(sm.a + (wr + 32 * i + li) * LDA + F::GK * g + (F::GK / 2) * lh);
-            const SType b = *reinterpret_cast<const SType *>(sm.b + (wc + 32 * j + li) * LDA + F::GK * g + (F::GK / 2) * lh);
-            if constexpr (F::GK == 32) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, z, 0, 0, 0);
-            else S = __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
-            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(sa, sb, zf, 0, 0, 0);
+            if constexpr (F::GK == 32) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b, z, 0, 0, 0);
+            else S = __builtin_amdgcn_mfma_i32_32x32x16_i8(o.a, o.b, z, 0, 0, 0);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(o.sa, o.sb, zf, 0, 0, 0);
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
@@ -375,22 +388,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
                 for (int v = 0; v < 16; ++v) accb[i][j][v] = fmaf((float)S[v], SC[v], accb[i][j][v]);
             }
         };
-        // The 64-column K-quant tiles have no registers left for a second
-        // pair in flight (it would spill), so they issue and consume in turn.
-        constexpr bool PIPE = !(BN == 64 && TYPE != TYPE_Q8_0);
-        v16i Sbuf[2];
-        v16f SCbuf[2];
-        if constexpr (PIPE) issue(0, Sbuf[0], SCbuf[0]);
+        // Software pipeline over the NP (scale group, tile) pairs: while the
+        // VALU scales pair p, the matrix core runs pair p+1 and the LDS
+        // delivers the operands of pair p+2.  The scheduling fences pin that
+        // order; left alone the scheduler consumes each MFMA result right
+        // after issuing it and stalls on the MFMA latency.
+        Ops ops[2];
+        v16i Sb[2];
+        v16f SCb[2];
+        load_ops(0, ops[0]);
+        if (NP > 1) load_ops(1, ops[1]);
+        issue(ops[0], Sb[0], SCb[0]);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
-            if constexpr (PIPE) {
-                if (p + 1 < NP) issue(p + 1, Sbuf[(p + 1) & 1], SCbuf[(p + 1) & 1]);
-                consume(p, Sbuf[p & 1], SCbuf[p & 1]);
-            } else {
-                issue(p, Sbuf[0], SCbuf[0]);
-                consume(p, Sbuf[0], SCbuf[0]);
-            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + 1 < NP) issue(ops[(p + 1) & 1], Sb[(p + 1) & 1], SCb[(p + 1) & 1]);
+            if (p + 2 < NP) load_ops(p + 2, ops[p & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(p, Sb[p & 1], SCb[p & 1]);
         }
+        __builtin_amdgcn_sched_barrier(0);
 
         if constexpr (TYPE != TYPE_Q8_0) {
             // acc += d[r] * accb; Q4_K also subtracts dmin[r] * sum_j m_j[r] * s8_j[c]
