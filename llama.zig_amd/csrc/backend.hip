@@ -1,0 +1,830 @@
+// backend.hip -- the ggml backend plugin layer: registry, devices, device and
+// pinned-host buffer types, buffers and backends, behind the vtables of
+// ggml_hip_ggml_abi.h, with graph_compute running MUL_MAT / MUL_MAT_ID on
+// the kernels of this library.
+//
+// It fills the same interfaces the reference's CUDA backend fills
+// (src/ggml/cuda/backend.zig: buffer 56-265, buffer type 277-383, pinned host
+// 511-590, backend 594-739, device 742-1048, registry 1060-1236) so that
+// ggml_backend_sched routes a MUL_MAT whose weight lives in a HIP buffer to
+// this device (src/ggml/backend_sched.zig:288-396).  Host code only: plain
+// HIP runtime calls; every device call is checked and a failing one aborts
+// with the call named, as the reference's cudaCheck does.
+#include <hip/hip_runtime.h>
+
+#include <cctype>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <new>
+
+#include "../../include/ggml_hip_backend.h"
+#include "../../include/ggml_hip_qmm.h"
+
+// Present when the library is loaded into a ggml host (the core owns buffer
+// structs and frees them with its own allocator); absent in standalone use.
+extern "C" __attribute__((weak)) ggml_backend_buffer_t ggml_backend_buffer_init(ggml_backend_buffer_type_t buft,
+                                                                                struct ggml_backend_buffer_i iface,
+                                                                                void *context, size_t size);
+
+namespace {
+
+[[noreturn]] void hip_fail(hipError_t e, const char *what, const char *file, int line) {
+    std::fprintf(stderr, "ggml-hip: %s failed: %s (%s:%d)\n", what, hipGetErrorString(e), file, line);
+    std::abort();
+}
+#define HIP_CHECK(call)                                                          \
+    do {                                                                         \
+        hipError_t e_ = (call);                                                  \
+        if (e_ != hipSuccess) hip_fail(e_, #call, __FILE__, __LINE__);           \
+    } while (0)
+
+constexpr int64_t ROW_PADDING = 512;  // MATRIX_ROW_PADDING (cuda/common.zig:50-53)
+constexpr size_t ALIGNMENT = 128;     // cuda/backend.zig:315-318
+
+// ---------------------------------------------------------------- type table
+
+struct TypeInfo {
+    int64_t blck;
+    size_t size;
+    bool quantized;
+};
+
+TypeInfo type_info(int t) {
+    switch (t) {
+    case GGML_TYPE_F32: return {1, 4, false};
+    case GGML_TYPE_F16: return {1, 2, false};
+    case GGML_TYPE_I32: return {1, 4, false};
+    case GGML_TYPE_Q8_0: return {32, 34, true};
+    case GGML_TYPE_Q8_1: return {32, 36, true};
+    case GGML_TYPE_Q4_K: return {256, 144, true};
+    case GGML_TYPE_Q6_K: return {256, 210, true};
+    case GGML_TYPE_Q8_K: return {256, 292, true};
+    default: return {0, 0, false};
+    }
+}
+
+bool weight_type(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0; }
+
+size_t row_size(int t, int64_t ne) {
+    const TypeInfo ti = type_info(t);
+    return ti.blck ? ti.size * (size_t)(ne / ti.blck) : 0;
+}
+
+// Bytes spanned by a tensor's elements (ggml_nbytes).
+size_t nbytes(const ggml_tensor *t) {
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (t->ne[i] <= 0) return 0;
+    const TypeInfo ti = type_info(t->type);
+    if (!ti.blck) return 0;
+    size_t n;
+    if (ti.blck == 1) {
+        n = ti.size;
+        for (int i = 0; i < GGML_MAX_DIMS; ++i) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    } else {
+        n = (size_t)t->ne[0] * t->nb[0] / (size_t)ti.blck;
+        for (int i = 1; i < GGML_MAX_DIMS; ++i) n += (size_t)(t->ne[i] - 1) * t->nb[i];
+    }
+    return n;
+}
+
+// Rows dense and in order, dims of extent 1 ignored (ggml_is_contiguous).
+bool contiguous(const ggml_tensor *t) {
+    const TypeInfo ti = type_info(t->type);
+    if (!ti.blck) return false;
+    size_t next = ti.size;
+    if (t->ne[0] != ti.blck && t->nb[0] != next) return false;
+    next *= (size_t)(t->ne[0] / ti.blck);
+    for (int i = 1; i < GGML_MAX_DIMS; ++i) {
+        if (t->ne[i] != 1) {
+            if (t->nb[i] != next) return false;
+            next *= (size_t)t->ne[i];
+        }
+    }
+    return true;
+}
+
+const ggml_tensor *backing(const ggml_tensor *t) { return t->view_src ? t->view_src : t; }
+
+// ---------------------------------------------------------------- devices
+
+struct DeviceCtx {
+    int device;
+    char name[16];
+    char description[256];
+    char pci_bus_id[64];
+};
+
+struct BufferTypeCtx {
+    int device;
+    char name[16];
+};
+
+struct BufferCtx {
+    int device;
+    void *dev_ptr;
+    bool own_struct;  // allocated here because no ggml core is linked
+};
+
+struct HostBufferCtx {
+    void *ptr;
+    bool own_struct;
+};
+
+struct BackendCtx {
+    int device;
+    char name[16];
+    hipStream_t stream;
+    void *ws;
+    size_t ws_size;
+};
+
+int device_count_probe() {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return n < GGML_HIP_MAX_DEVICES ? n : GGML_HIP_MAX_DEVICES;
+}
+
+int device_count() {
+    static int n = device_count_probe();
+    return n;
+}
+
+// One guid per backend kind (a random 16-byte tag).
+ggml_guid hip_guid = {0x5e, 0x1a, 0x7c, 0x93, 0x0b, 0xd4, 0x46, 0x2f, 0x9a, 0x31, 0xe2, 0x58, 0x77, 0x0c, 0xa6, 0x1d};
+
+ggml_backend_buffer_t make_buffer(ggml_backend_buffer_type_t buft, const ggml_backend_buffer_i &iface, void *ctx,
+                                  size_t size, bool *own_struct) {
+    if (ggml_backend_buffer_init) {
+        *own_struct = false;
+        return ggml_backend_buffer_init(buft, iface, ctx, size);
+    }
+    auto *b = new ggml_backend_buffer{};
+    b->iface = iface;
+    b->buft = buft;
+    b->context = ctx;
+    b->size = size;
+    b->usage = GGML_BACKEND_BUFFER_USAGE_ANY;
+    *own_struct = true;
+    return b;
+}
+
+char *at(void *p, size_t off) { return static_cast<char *>(p) + off; }
+const char *at(const void *p, size_t off) { return static_cast<const char *>(p) + off; }
+
+// ---------------------------------------------------------------- device buffer
+
+BufferCtx *buf_ctx(ggml_backend_buffer_t b) { return static_cast<BufferCtx *>(b->context); }
+
+void buf_free(ggml_backend_buffer_t b) {
+    BufferCtx *ctx = buf_ctx(b);
+    HIP_CHECK(hipSetDevice(ctx->device));
+    HIP_CHECK(hipFree(ctx->dev_ptr));
+    const bool own = ctx->own_struct;
+    delete ctx;
+    if (own) delete b;
+}
+
+void *buf_base(ggml_backend_buffer_t b) { return buf_ctx(b)->dev_ptr; }
+
+ggml_status buf_init_tensor(ggml_backend_buffer_t b, ggml_tensor *t) {
+    if (t->view_src) return GGML_STATUS_SUCCESS;
+    // zero the row padding of quantized weights so the kernels read no NaNs
+    if (type_info(t->type).quantized && b->usage != GGML_BACKEND_BUFFER_USAGE_COMPUTE) {
+        const size_t orig = nbytes(t);
+        const size_t padded = ggml_backend_hip_tensor_alloc_size(t);
+        if (padded > orig) {
+            HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+            HIP_CHECK(hipMemsetAsync(at(t->data, orig), 0, padded - orig, hipStreamPerThread));
+            HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+        }
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+void buf_memset_tensor(ggml_backend_buffer_t b, ggml_tensor *t, uint8_t value, size_t offset, size_t size) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemsetAsync(at(t->data, offset), value, size, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_set_tensor(ggml_backend_buffer_t b, ggml_tensor *t, const void *data, size_t offset, size_t size) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemcpyAsync(at(t->data, offset), data, size, hipMemcpyHostToDevice, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_get_tensor(ggml_backend_buffer_t b, const ggml_tensor *t, void *data, size_t offset, size_t size) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemcpyAsync(data, at(t->data, offset), size, hipMemcpyDeviceToHost, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_set_tensor_2d(ggml_backend_buffer_t b, ggml_tensor *t, const void *data, size_t offset, size_t size,
+                       size_t n_copies, size_t stride_tensor, size_t stride_data) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemcpy2DAsync(at(t->data, offset), stride_tensor, data, stride_data, size, n_copies,
+                               hipMemcpyHostToDevice, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_get_tensor_2d(ggml_backend_buffer_t b, const ggml_tensor *t, void *data, size_t offset, size_t size,
+                       size_t n_copies, size_t stride_tensor, size_t stride_data) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemcpy2DAsync(data, stride_data, at(t->data, offset), stride_tensor, size, n_copies,
+                               hipMemcpyDeviceToHost, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+bool buffer_is_hip(ggml_backend_buffer_t b);
+
+void copy_device(const ggml_tensor *src, ggml_tensor *dst, hipStream_t s) {
+    const int sd = buf_ctx(backing(src)->buffer)->device, dd = buf_ctx(backing(dst)->buffer)->device;
+    if (sd == dd)
+        HIP_CHECK(hipMemcpyAsync(dst->data, src->data, nbytes(src), hipMemcpyDeviceToDevice, s));
+    else
+        HIP_CHECK(hipMemcpyPeerAsync(dst->data, dd, src->data, sd, nbytes(src), s));
+}
+
+bool buf_cpy_tensor(ggml_backend_buffer_t b, const ggml_tensor *src, ggml_tensor *dst) {
+    if (!src->buffer || !buffer_is_hip(backing(src)->buffer)) return false;
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    copy_device(src, dst, hipStreamPerThread);
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+    return true;
+}
+
+void buf_clear(ggml_backend_buffer_t b, uint8_t value) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    HIP_CHECK(hipMemsetAsync(buf_ctx(b)->dev_ptr, value, b->size, hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_set_tensor_n(ggml_backend_buffer_t b, ggml_tensor *const *ts, const void *const *data, const size_t *offs,
+                      const size_t *sizes, size_t n) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    for (size_t i = 0; i < n; ++i)
+        if (sizes[i])
+            HIP_CHECK(hipMemcpyAsync(at(ts[i]->data, offs[i]), data[i], sizes[i], hipMemcpyHostToDevice,
+                                     hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+void buf_get_tensor_n(ggml_backend_buffer_t b, const ggml_tensor *const *ts, void *const *data, const size_t *offs,
+                      const size_t *sizes, size_t n) {
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    for (size_t i = 0; i < n; ++i)
+        if (sizes[i])
+            HIP_CHECK(hipMemcpyAsync(data[i], at(ts[i]->data, offs[i]), sizes[i], hipMemcpyDeviceToHost,
+                                     hipStreamPerThread));
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+}
+
+bool buf_cpy_tensor_n(ggml_backend_buffer_t b, const ggml_tensor *const *srcs, ggml_tensor *const *dsts, size_t n) {
+    for (size_t i = 0; i < n; ++i)
+        if (!backing(srcs[i])->buffer || !buffer_is_hip(backing(srcs[i])->buffer)) return false;
+    HIP_CHECK(hipSetDevice(buf_ctx(b)->device));
+    for (size_t i = 0; i < n; ++i) copy_device(srcs[i], dsts[i], hipStreamPerThread);
+    HIP_CHECK(hipStreamSynchronize(hipStreamPerThread));
+    return true;
+}
+
+const ggml_backend_buffer_i buffer_iface = {
+    buf_free,          buf_base,          buf_init_tensor, buf_memset_tensor, buf_set_tensor,
+    buf_get_tensor,    buf_set_tensor_2d, buf_get_tensor_2d, buf_cpy_tensor,  buf_clear,
+    nullptr,           buf_set_tensor_n,  buf_get_tensor_n,  buf_cpy_tensor_n,
+};
+
+bool buffer_is_hip(ggml_backend_buffer_t b) { return b && b->iface.free_buffer == buf_free; }
+
+// ---------------------------------------------------------------- device buffer type
+
+const char *buft_name(ggml_backend_buffer_type_t buft) {
+    return static_cast<BufferTypeCtx *>(buft->context)->name;
+}
+
+ggml_backend_buffer_t buft_alloc(ggml_backend_buffer_type_t buft, size_t size) {
+    const int device = static_cast<BufferTypeCtx *>(buft->context)->device;
+    HIP_CHECK(hipSetDevice(device));
+    void *p = nullptr;
+    const hipError_t e = hipMalloc(&p, size ? size : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        std::fprintf(stderr, "ggml-hip: allocating %.2f MiB on device %d: hipMalloc failed: %s\n",
+                     (double)size / 1048576.0, device, hipGetErrorString(e));
+        return nullptr;
+    }
+    auto *ctx = new BufferCtx{device, p, false};
+    return make_buffer(buft, buffer_iface, ctx, size, &ctx->own_struct);
+}
+
+size_t buft_alignment(ggml_backend_buffer_type_t) { return ALIGNMENT; }
+
+size_t buft_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor *t) {
+    return ggml_backend_hip_tensor_alloc_size(t);
+}
+
+const ggml_backend_buffer_type_i buffer_type_iface = {
+    buft_name, buft_alloc, nullptr, buft_alignment, nullptr, buft_alloc_size, nullptr, nullptr,
+};
+
+bool buft_is_hip(ggml_backend_buffer_type_t buft) { return buft && buft->iface.get_name == buft_name; }
+
+// ---------------------------------------------------------------- pinned host buffer type
+
+HostBufferCtx *hbuf_ctx(ggml_backend_buffer_t b) { return static_cast<HostBufferCtx *>(b->context); }
+
+void hbuf_free(ggml_backend_buffer_t b) {
+    HostBufferCtx *ctx = hbuf_ctx(b);
+    HIP_CHECK(hipHostFree(ctx->ptr));
+    const bool own = ctx->own_struct;
+    delete ctx;
+    if (own) delete b;
+}
+void *hbuf_base(ggml_backend_buffer_t b) { return hbuf_ctx(b)->ptr; }
+void hbuf_memset_tensor(ggml_backend_buffer_t, ggml_tensor *t, uint8_t v, size_t off, size_t size) {
+    std::memset(at(t->data, off), v, size);
+}
+void hbuf_set_tensor(ggml_backend_buffer_t, ggml_tensor *t, const void *d, size_t off, size_t size) {
+    std::memcpy(at(t->data, off), d, size);
+}
+void hbuf_get_tensor(ggml_backend_buffer_t, const ggml_tensor *t, void *d, size_t off, size_t size) {
+    std::memcpy(d, at(t->data, off), size);
+}
+void hbuf_clear(ggml_backend_buffer_t b, uint8_t v) { std::memset(hbuf_ctx(b)->ptr, v, b->size); }
+
+const ggml_backend_buffer_i host_buffer_iface = {
+    hbuf_free, hbuf_base, nullptr, hbuf_memset_tensor, hbuf_set_tensor, hbuf_get_tensor, nullptr,
+    nullptr,   nullptr,   hbuf_clear, nullptr,          nullptr,         nullptr,         nullptr,
+};
+
+const char *hbuft_name(ggml_backend_buffer_type_t) { return GGML_HIP_NAME "_Host"; }
+
+ggml_backend_buffer_t hbuft_alloc(ggml_backend_buffer_type_t buft, size_t size) {
+    void *p = nullptr;
+    const hipError_t e = hipHostMalloc(&p, size ? size : 1, hipHostMallocDefault);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        std::fprintf(stderr, "ggml-hip: failed to allocate %.2f MiB of pinned memory: %s\n",
+                     (double)size / 1048576.0, hipGetErrorString(e));
+        return nullptr;
+    }
+    auto *ctx = new HostBufferCtx{p, false};
+    return make_buffer(buft, host_buffer_iface, ctx, size, &ctx->own_struct);
+}
+
+size_t hbuft_alignment(ggml_backend_buffer_type_t) { return 64; }
+size_t hbuft_max_size(ggml_backend_buffer_type_t) { return (size_t)4 << 30; }
+size_t hbuft_alloc_size(ggml_backend_buffer_type_t, const ggml_tensor *t) { return nbytes(t); }
+bool hbuft_is_host(ggml_backend_buffer_type_t) { return true; }
+
+// ---------------------------------------------------------------- backend
+
+BackendCtx *be_ctx(ggml_backend_t be) { return static_cast<BackendCtx *>(be->context); }
+
+const char *be_name(ggml_backend_t be) { return be_ctx(be)->name; }
+
+void be_free(ggml_backend_t be) {
+    BackendCtx *ctx = be_ctx(be);
+    HIP_CHECK(hipSetDevice(ctx->device));
+    HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) HIP_CHECK(hipFree(ctx->ws));
+    HIP_CHECK(hipStreamDestroy(ctx->stream));
+    delete ctx;
+    delete be;
+}
+
+void check_own_buffer(BackendCtx *ctx, const ggml_tensor *t) {
+    const ggml_backend_buffer_t b = backing(t)->buffer;
+    if (!buffer_is_hip(b) || buf_ctx(b)->device != ctx->device) {
+        std::fprintf(stderr, "ggml-hip: tensor '%s' is not in a buffer of device %d\n", t->name, ctx->device);
+        std::abort();
+    }
+}
+
+void be_set_tensor_async(ggml_backend_t be, ggml_tensor *t, const void *data, size_t off, size_t size) {
+    BackendCtx *ctx = be_ctx(be);
+    check_own_buffer(ctx, t);
+    HIP_CHECK(hipMemcpyAsync(at(t->data, off), data, size, hipMemcpyHostToDevice, ctx->stream));
+}
+
+void be_get_tensor_async(ggml_backend_t be, const ggml_tensor *t, void *data, size_t off, size_t size) {
+    BackendCtx *ctx = be_ctx(be);
+    check_own_buffer(ctx, t);
+    HIP_CHECK(hipMemcpyAsync(data, at(t->data, off), size, hipMemcpyDeviceToHost, ctx->stream));
+}
+
+void be_set_tensor_2d_async(ggml_backend_t be, ggml_tensor *t, const void *data, size_t off, size_t size,
+                            size_t n_copies, size_t stride_tensor, size_t stride_data) {
+    BackendCtx *ctx = be_ctx(be);
+    check_own_buffer(ctx, t);
+    HIP_CHECK(hipMemcpy2DAsync(at(t->data, off), stride_tensor, data, stride_data, size, n_copies,
+                               hipMemcpyHostToDevice, ctx->stream));
+}
+
+void be_get_tensor_2d_async(ggml_backend_t be, const ggml_tensor *t, void *data, size_t off, size_t size,
+                            size_t n_copies, size_t stride_tensor, size_t stride_data) {
+    BackendCtx *ctx = be_ctx(be);
+    check_own_buffer(ctx, t);
+    HIP_CHECK(hipMemcpy2DAsync(data, stride_data, at(t->data, off), stride_tensor, size, n_copies,
+                               hipMemcpyDeviceToHost, ctx->stream));
+}
+
+bool be_cpy_tensor_async(ggml_backend_t src_be, ggml_backend_t dst_be, const ggml_tensor *src, ggml_tensor *dst) {
+    if (!ggml_backend_is_hip(src_be) || !ggml_backend_is_hip(dst_be)) return false;
+    const ggml_backend_buffer_t bs = backing(src)->buffer, bd = backing(dst)->buffer;
+    if (!buffer_is_hip(bs) || !buffer_is_hip(bd)) return false;
+    BackendCtx *cs = be_ctx(src_be), *cd = be_ctx(dst_be);
+    if (cs->device != buf_ctx(bs)->device || cd->device != buf_ctx(bd)->device) return false;
+    copy_device(src, dst, cs->stream);
+    if (src_be != dst_be) {
+        // the destination stream waits for the copy
+        hipEvent_t ev;
+        HIP_CHECK(hipSetDevice(cs->device));
+        HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+        HIP_CHECK(hipEventRecord(ev, cs->stream));
+        HIP_CHECK(hipStreamWaitEvent(cd->stream, ev, 0));
+        HIP_CHECK(hipEventDestroy(ev));
+    }
+    return true;
+}
+
+void be_synchronize(ggml_backend_t be) { HIP_CHECK(hipStreamSynchronize(be_ctx(be)->stream)); }
+
+// Grow-only workspace of the backend (the reference's per-device pool,
+// mmvq.zig:633-643).  Growing waits for the stream, so no queued kernel
+// still uses the old block when it is freed.
+void *workspace(BackendCtx *ctx, size_t need) {
+    if (need <= ctx->ws_size) return ctx->ws;
+    HIP_CHECK(hipStreamSynchronize(ctx->stream));
+    if (ctx->ws) HIP_CHECK(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_size = 0;
+    size_t sz = need + need / 4;
+    sz = (sz + 255) & ~(size_t)255;
+    HIP_CHECK(hipMalloc(&ctx->ws, sz));
+    ctx->ws_size = sz;
+    return ctx->ws;
+}
+
+bool report(int rc, const char *what, const ggml_tensor *node) {
+    if (rc == 0) return true;
+    std::fprintf(stderr, "ggml-hip: %s for node '%s' failed: %s\n", what, node->name,
+                 hipGetErrorString((hipError_t)rc));
+    return false;
+}
+
+// dst[M, N, ne2, ne3] = src0[K, M, ne02, ne03] x src1[K, N, ne2, ne3], src0
+// broadcast over dims 2 and 3 (ggml_mul_mat, src/ggml/ops.zig:1072-1083).
+bool run_mul_mat(BackendCtx *ctx, const ggml_tensor *node) {
+    const ggml_tensor *a = node->src[0], *b = node->src[1];
+    const int64_t K = a->ne[0], M = a->ne[1], N = b->ne[1];
+    const int64_t r2 = b->ne[2] / a->ne[2], r3 = b->ne[3] / a->ne[3];
+    const size_t need = hip_qmm_mul_mat_workspace_size(a->type, K, M, N);
+    void *ws = workspace(ctx, need);
+    for (int64_t i3 = 0; i3 < b->ne[3]; ++i3)
+        for (int64_t i2 = 0; i2 < b->ne[2]; ++i2) {
+            const char *w = at(a->data, (size_t)(i2 / r2) * a->nb[2] + (size_t)(i3 / r3) * a->nb[3]);
+            const float *x = reinterpret_cast<const float *>(at(b->data, (size_t)i2 * b->nb[2] + (size_t)i3 * b->nb[3]));
+            float *d = reinterpret_cast<float *>(at(node->data, (size_t)i2 * node->nb[2] + (size_t)i3 * node->nb[3]));
+            const int rc = hip_qmm_mul_mat(a->type, w, K, M, (int64_t)a->nb[1], x, N, (int64_t)(b->nb[1] / 4), d,
+                                           (int64_t)(node->nb[1] / 4), ws, ctx->ws_size, ctx->stream);
+            if (!report(rc, "hip_qmm_mul_mat", node)) return false;
+        }
+    return true;
+}
+
+// dst[M, n_used, n_tokens]: row (s, t) = src0[:, :, ids[s, t]] x src1[:, s % ne11, t]
+// (ggml_mul_mat_id, src/ggml/ops.zig:1104-1125).
+bool run_mul_mat_id(BackendCtx *ctx, const ggml_tensor *node) {
+    const ggml_tensor *as = node->src[0], *b = node->src[1], *ids = node->src[2];
+    const int64_t K = as->ne[0], M = as->ne[1], n_as = as->ne[2];
+    const int64_t ne11 = b->ne[1], n_tokens = b->ne[2], n_ids = ids->ne[0];
+    const size_t need = hip_qmm_mul_mat_id_workspace_size(as->type, K, n_as, ne11, n_tokens, n_ids);
+    void *ws = workspace(ctx, need);
+    const int rc = hip_qmm_mul_mat_id(as->type, as->data, K, M, (int64_t)as->nb[1], (int64_t)as->nb[2], n_as,
+                                      static_cast<const float *>(b->data), ne11, n_tokens, (int64_t)(b->nb[1] / 4),
+                                      static_cast<const int32_t *>(ids->data), n_ids, (int64_t)(ids->nb[1] / 4),
+                                      static_cast<float *>(node->data), (int64_t)(node->nb[1] / 4), ws, ctx->ws_size,
+                                      ctx->stream);
+    return report(rc, "hip_qmm_mul_mat_id", node);
+}
+
+bool is_noop(int op) {
+    return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
+           op == GGML_OP_TRANSPOSE;
+}
+
+ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
+    BackendCtx *ctx = be_ctx(be);
+    HIP_CHECK(hipSetDevice(ctx->device));
+    for (int i = 0; i < g->n_nodes; ++i) {
+        const ggml_tensor *node = g->nodes[i];
+        if (is_noop(node->op) || nbytes(node) == 0) continue;
+        if (!ggml_backend_hip_op_supported(node)) {
+            std::fprintf(stderr, "ggml-hip: node '%s' (op %d) is not supported by this backend\n", node->name,
+                         (int)node->op);
+            return GGML_STATUS_FAILED;
+        }
+        const bool ok = node->op == GGML_OP_MUL_MAT ? run_mul_mat(ctx, node) : run_mul_mat_id(ctx, node);
+        if (!ok) return GGML_STATUS_FAILED;
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+void be_event_record(ggml_backend_t be, ggml_backend_event_t ev) {
+    HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev->context), be_ctx(be)->stream));
+}
+
+void be_event_wait(ggml_backend_t be, ggml_backend_event_t ev) {
+    if (!ggml_backend_is_hip(be)) {
+        std::fprintf(stderr, "ggml-hip: event_wait on a foreign backend\n");
+        std::abort();
+    }
+    HIP_CHECK(hipStreamWaitEvent(be_ctx(be)->stream, static_cast<hipEvent_t>(ev->context), 0));
+}
+
+const ggml_backend_i backend_iface = {
+    be_name,
+    be_free,
+    be_set_tensor_async,
+    be_get_tensor_async,
+    be_set_tensor_2d_async,
+    be_get_tensor_2d_async,
+    be_cpy_tensor_async,
+    be_synchronize,
+    nullptr,
+    nullptr,
+    nullptr,
+    nullptr,
+    be_graph_compute,
+    be_event_record,
+    be_event_wait,
+    nullptr,
+};
+
+// ---------------------------------------------------------------- device vtable
+
+DeviceCtx *dev_ctx(ggml_backend_dev_t dev) { return static_cast<DeviceCtx *>(dev->context); }
+
+const char *dev_name(ggml_backend_dev_t dev) { return dev_ctx(dev)->name; }
+const char *dev_description(ggml_backend_dev_t dev) { return dev_ctx(dev)->description; }
+void dev_memory(ggml_backend_dev_t dev, size_t *free, size_t *total) {
+    ggml_backend_hip_get_device_memory(dev_ctx(dev)->device, free, total);
+}
+ggml_backend_dev_type dev_type(ggml_backend_dev_t) { return GGML_BACKEND_DEVICE_TYPE_GPU; }
+
+void dev_props(ggml_backend_dev_t dev, ggml_backend_dev_props *p) {
+    p->name = dev_name(dev);
+    p->description = dev_description(dev);
+    p->type = dev_type(dev);
+    p->device_id = dev_ctx(dev)->pci_bus_id[0] ? dev_ctx(dev)->pci_bus_id : nullptr;
+    dev_memory(dev, &p->memory_free, &p->memory_total);
+    p->caps.async = true;
+    p->caps.host_buffer = true;
+    p->caps.buffer_from_host_ptr = false;
+    p->caps.events = true;
+    p->caps.mmap_support = true;
+}
+
+ggml_backend_t dev_init_backend(ggml_backend_dev_t dev, const char *) {
+    return ggml_backend_hip_init(dev_ctx(dev)->device);
+}
+ggml_backend_buffer_type_t dev_buffer_type(ggml_backend_dev_t dev) {
+    return ggml_backend_hip_buffer_type(dev_ctx(dev)->device);
+}
+ggml_backend_buffer_type_t dev_host_buffer_type(ggml_backend_dev_t) { return ggml_backend_hip_host_buffer_type(); }
+bool dev_supports_op(ggml_backend_dev_t, const ggml_tensor *op) { return ggml_backend_hip_op_supported(op); }
+bool dev_supports_buft(ggml_backend_dev_t dev, ggml_backend_buffer_type_t buft) {
+    return buft_is_hip(buft) && buft->device == dev;
+}
+
+// Ops whose weights sit in host memory are worth shipping to the GPU from a
+// batch of 32 columns on (get_op_batch_size / offload_op,
+// cuda/backend.zig:992-1006, the default GGML_OP_OFFLOAD_MIN_BATCH).
+bool dev_offload_op(ggml_backend_dev_t, const ggml_tensor *op) {
+    const int64_t batch = op->op == GGML_OP_MUL_MAT ? op->ne[1] : op->op == GGML_OP_MUL_MAT_ID ? op->ne[2] : 0;
+    return batch >= 32 && ggml_backend_hip_op_supported(op);
+}
+
+ggml_backend_event_t dev_event_new(ggml_backend_dev_t dev) {
+    HIP_CHECK(hipSetDevice(dev_ctx(dev)->device));
+    hipEvent_t e;
+    HIP_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return new ggml_backend_event{dev, e};
+}
+void dev_event_free(ggml_backend_dev_t, ggml_backend_event_t ev) {
+    HIP_CHECK(hipEventDestroy(static_cast<hipEvent_t>(ev->context)));
+    delete ev;
+}
+void dev_event_synchronize(ggml_backend_dev_t, ggml_backend_event_t ev) {
+    HIP_CHECK(hipEventSynchronize(static_cast<hipEvent_t>(ev->context)));
+}
+
+const ggml_backend_device_i device_iface = {
+    dev_name,      dev_description,      dev_memory,       dev_type,       dev_props,
+    dev_init_backend, dev_buffer_type,   dev_host_buffer_type, nullptr,    dev_supports_op,
+    dev_supports_buft, dev_offload_op,   dev_event_new,    dev_event_free, dev_event_synchronize,
+};
+
+// ---------------------------------------------------------------- registry
+
+struct Registry {
+    std::mutex mu;
+    bool ready = false;
+    ggml_backend_reg reg{};
+    ggml_backend_device devices[GGML_HIP_MAX_DEVICES]{};
+    DeviceCtx dev_ctx[GGML_HIP_MAX_DEVICES]{};
+    int count = 0;
+    bool buft_ready = false;
+    ggml_backend_buffer_type bufts[GGML_HIP_MAX_DEVICES]{};
+    BufferTypeCtx buft_ctx[GGML_HIP_MAX_DEVICES]{};
+    bool host_ready = false;
+    ggml_backend_buffer_type host_buft{};
+};
+
+Registry &registry() {
+    static Registry r;
+    return r;
+}
+
+const char *reg_name(ggml_backend_reg_t) { return GGML_HIP_NAME; }
+size_t reg_device_count(ggml_backend_reg_t) { return (size_t)registry().count; }
+ggml_backend_dev_t reg_device(ggml_backend_reg_t, size_t i) {
+    Registry &r = registry();
+    if (i >= (size_t)r.count) {
+        std::fprintf(stderr, "ggml-hip: device index %zu out of range\n", i);
+        std::abort();
+    }
+    return &r.devices[i];
+}
+void *reg_proc_address(ggml_backend_reg_t, const char *name) {
+    if (!name) return nullptr;
+    if (!std::strcmp(name, "ggml_backend_register_host_buffer"))
+        return reinterpret_cast<void *>(&ggml_backend_hip_register_host_buffer);
+    if (!std::strcmp(name, "ggml_backend_unregister_host_buffer"))
+        return reinterpret_cast<void *>(&ggml_backend_hip_unregister_host_buffer);
+    return nullptr;
+}
+
+const ggml_backend_reg_i reg_iface = {reg_name, reg_device_count, reg_device, reg_proc_address};
+
+void describe(int device, char *out, size_t n) {
+    hipDeviceProp_t prop;
+    HIP_CHECK(hipGetDeviceProperties(&prop, device));
+    std::snprintf(out, n, "%s", prop.name);
+}
+
+}  // namespace
+
+// ================================================================ C ABI
+
+extern "C" {
+
+bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
+    if (!op) return false;
+    if (is_noop(op->op)) return true;
+    if (op->op != GGML_OP_MUL_MAT && op->op != GGML_OP_MUL_MAT_ID) return false;
+    const ggml_tensor *a = op->src[0], *b = op->src[1];
+    if (!a || !b || !weight_type(a->type) || b->type != GGML_TYPE_F32 || op->type != GGML_TYPE_F32) return false;
+    const TypeInfo ta = type_info(a->type);
+    // rows of elements, each row read with its own stride (cuda/supports.zig:111-114)
+    if (a->nb[0] != ta.size || b->nb[0] != 4 || op->nb[0] != 4) return false;
+    if (a->ne[0] % ta.blck != 0 || a->ne[0] > ((int64_t)1 << 30) || b->ne[0] != a->ne[0]) return false;
+    if (b->nb[1] % 4 != 0 || op->nb[1] % 4 != 0) return false;
+    if (op->op == GGML_OP_MUL_MAT) {
+        if (a->ne[2] <= 0 || a->ne[3] <= 0 || b->ne[2] % a->ne[2] != 0 || b->ne[3] % a->ne[3] != 0) return false;
+        return op->ne[0] == a->ne[1] && op->ne[1] == b->ne[1];
+    }
+    // MUL_MAT_ID: src2 = ids [n_used, n_tokens] I32
+    const ggml_tensor *ids = op->src[2];
+    if (!ids || ids->type != GGML_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4 != 0) return false;
+    if (a->ne[0] % 256 != 0 || a->ne[2] > 1024 || a->ne[3] != 1) return false;
+    const int64_t n_ids = ids->ne[0], n_tokens = ids->ne[1];
+    if (b->ne[1] != 1 && b->ne[1] != n_ids) return false;
+    if (b->ne[2] != n_tokens || b->ne[3] != 1 || op->ne[1] != n_ids || op->ne[2] != n_tokens) return false;
+    // activations and results as dense rows: (token, slot) at (t*rows + s) * row stride
+    if (b->nb[2] != (size_t)b->ne[1] * b->nb[1] || op->nb[2] != (size_t)op->ne[1] * op->nb[1]) return false;
+    return n_tokens * n_ids <= 0x7FFFFFFF;
+}
+
+size_t ggml_backend_hip_tensor_alloc_size(const ggml_tensor *t) {
+    size_t size = nbytes(t);
+    const int64_t ne0 = t->ne[0];
+    // pad quantized rows to 512 elements (cuda/backend.zig:321-338)
+    if (type_info(t->type).quantized && ne0 % ROW_PADDING != 0) size += row_size(t->type, ROW_PADDING - ne0 % ROW_PADDING);
+    return size;
+}
+
+int ggml_backend_hip_get_device_count(void) { return device_count(); }
+
+void ggml_backend_hip_get_device_description(int device, char *description, size_t description_size) {
+    if (!description || !description_size) return;
+    if (device < 0 || device >= device_count()) {
+        description[0] = 0;
+        return;
+    }
+    describe(device, description, description_size);
+}
+
+void ggml_backend_hip_get_device_memory(int device, size_t *free, size_t *total) {
+    HIP_CHECK(hipSetDevice(device));
+    HIP_CHECK(hipMemGetInfo(free, total));
+}
+
+bool ggml_backend_hip_register_host_buffer(void *, size_t) { return false; }
+void ggml_backend_hip_unregister_host_buffer(void *) {}
+
+ggml_backend_reg_t ggml_backend_hip_reg(void) {
+    Registry &r = registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (!r.ready) {
+        r.count = device_count();
+        for (int i = 0; i < r.count; ++i) {
+            DeviceCtx &c = r.dev_ctx[i];
+            c.device = i;
+            std::snprintf(c.name, sizeof c.name, GGML_HIP_NAME "%d", i);
+            describe(i, c.description, sizeof c.description);
+            char bus[64] = {0};
+            if (hipDeviceGetPCIBusId(bus, sizeof bus, i) == hipSuccess) {
+                for (char *p = bus; *p; ++p) *p = (char)std::tolower((unsigned char)*p);
+                std::snprintf(c.pci_bus_id, sizeof c.pci_bus_id, "%s", bus);
+            } else {
+                (void)hipGetLastError();
+            }
+            r.devices[i].iface = device_iface;
+            r.devices[i].reg = &r.reg;
+            r.devices[i].context = &c;
+        }
+        r.reg.api_version = GGML_BACKEND_API_VERSION;
+        r.reg.iface = reg_iface;
+        r.reg.context = nullptr;
+        r.ready = true;
+    }
+    return &r.reg;
+}
+
+ggml_backend_buffer_type_t ggml_backend_hip_buffer_type(int device) {
+    ggml_backend_reg_t reg = ggml_backend_hip_reg();
+    Registry &r = registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (device < 0 || device >= r.count) return nullptr;
+    if (!r.buft_ready) {
+        for (int i = 0; i < r.count; ++i) {
+            r.buft_ctx[i].device = i;
+            std::snprintf(r.buft_ctx[i].name, sizeof r.buft_ctx[i].name, GGML_HIP_NAME "%d", i);
+            r.bufts[i].iface = buffer_type_iface;
+            r.bufts[i].device = reg_device(reg, (size_t)i);
+            r.bufts[i].context = &r.buft_ctx[i];
+        }
+        r.buft_ready = true;
+    }
+    return &r.bufts[device];
+}
+
+ggml_backend_buffer_type_t ggml_backend_hip_host_buffer_type(void) {
+    ggml_backend_reg_t reg = ggml_backend_hip_reg();
+    Registry &r = registry();
+    std::lock_guard<std::mutex> lock(r.mu);
+    if (!r.host_ready) {
+        r.host_buft.iface = {hbuft_name, hbuft_alloc, nullptr, hbuft_alignment, hbuft_max_size,
+                             hbuft_alloc_size, nullptr, hbuft_is_host};
+        r.host_buft.device = r.count > 0 ? reg_device(reg, 0) : nullptr;
+        r.host_buft.context = nullptr;
+        r.host_ready = true;
+    }
+    return &r.host_buft;
+}
+
+ggml_backend_t ggml_backend_hip_init(int device) {
+    if (device < 0 || device >= device_count()) {
+        std::fprintf(stderr, "ggml-hip: invalid device %d\n", device);
+        return nullptr;
+    }
+    ggml_backend_reg_t reg = ggml_backend_hip_reg();
+    HIP_CHECK(hipSetDevice(device));
+    auto *ctx = new BackendCtx{};
+    ctx->device = device;
+    std::snprintf(ctx->name, sizeof ctx->name, GGML_HIP_NAME "%d", device);
+    HIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+    auto *be = new ggml_backend{};
+    be->guid = &hip_guid;
+    be->iface = backend_iface;
+    be->device = reg_device(reg, (size_t)device);
+    be->context = ctx;
+    return be;
+}
+
+bool ggml_backend_is_hip(ggml_backend_t backend) {
+    return backend && backend->guid && std::memcmp(*backend->guid, hip_guid, sizeof(ggml_guid)) == 0;
+}
+
+int ggml_backend_score(void) { return device_count() > 0 ? 100 : 0; }
+
+ggml_backend_reg_t ggml_backend_init(void) { return ggml_backend_hip_reg(); }
+
+}  // extern "C"

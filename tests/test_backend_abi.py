@@ -1,0 +1,155 @@
+"""CPU checks of the C ABI and the backend plugin layer: every function the
+include/ headers declare is exported, the ctypes layouts agree with the
+reference's layout facts, and the device-independent vtable answers
+(supports_op, get_alloc_size, the registry without a device) behave as the
+reference's CUDA backend does.  Nothing here launches GPU work."""
+import ctypes as C
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def declared_functions(path):
+    text = re.sub(r"/\*.*?\*/", " ", path.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", " ", text)
+    text = re.sub(r"#[^\n]*", " ", text)
+    # the extern "C" wrapper: its opening line and its lone closing brace
+    text = text.replace('extern "C" {', " ")
+    text = re.sub(r"(?m)^\s*\}\s*$", " ", text)
+    # drop struct / enum bodies (function-pointer members live there)
+    prev = None
+    while prev != text:
+        prev = text
+        text = re.sub(r"\{[^{}]*\}", " ", text)
+    names = []
+    for stmt in text.split(";"):
+        stmt = " ".join(stmt.split())
+        if not stmt or "(*" in stmt or stmt.startswith(("typedef", "struct", "enum", "extern \"C\"")):
+            continue
+        m = re.match(r"^(?:const )?[A-Za-z_][\w ]*[\s\*]+([A-Za-z_]\w*)\s*\(", stmt)
+        if m:
+            names.append(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def L():
+    import ggml_hip.backend as B
+    return B.lib()
+
+
+def test_headers_declare_functions():
+    names = {h.name: declared_functions(h) for h in HEADERS}
+    assert len(names["ggml_hip_qmm.h"]) >= 14
+    assert "ggml_backend_hip_reg" in names["ggml_hip_backend.h"]
+    assert names["ggml_hip_ggml_abi.h"] == []
+
+
+def test_every_declared_function_is_exported(L):
+    missing = [n for h in HEADERS for n in declared_functions(h) if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_ten_hip_exports_mirror_the_cuda_header(L):
+    # cuda/backend.zig:1225-1236 with `cuda` -> `hip`, plus the dynamic-loading pair
+    for n in ["ggml_backend_hip_reg", "ggml_backend_hip_init", "ggml_backend_is_hip", "ggml_backend_hip_buffer_type",
+              "ggml_backend_hip_host_buffer_type", "ggml_backend_hip_get_device_count",
+              "ggml_backend_hip_get_device_description", "ggml_backend_hip_get_device_memory",
+              "ggml_backend_hip_register_host_buffer", "ggml_backend_hip_unregister_host_buffer",
+              "ggml_backend_init", "ggml_backend_score"]:
+        assert hasattr(L, n), n
+
+
+def test_layouts():
+    from ggml_hip import abi
+    # the trailing 8-byte padding member ends the tensor (backend_meta.zig:3221-3222)
+    assert C.sizeof(abi.ggml_tensor) - 8 == abi.ggml_tensor.padding.offset
+    assert C.sizeof(abi.ggml_tensor) == 336
+    assert abi.ggml_tensor.data.offset == 248 and abi.ggml_tensor.src.offset == 152
+    # cgraph: three ints then the node array (impl.zig:469-485)
+    assert abi.ggml_cgraph.nodes.offset == 16
+    # vtables: one pointer per member in the CUDA backend's order
+    assert C.sizeof(abi.buffer_i) == 14 * 8 and C.sizeof(abi.buffer_type_i) == 8 * 8
+    assert C.sizeof(abi.backend_i) == 16 * 8 and C.sizeof(abi.device_i) == 15 * 8 and C.sizeof(abi.reg_i) == 4 * 8
+
+
+def test_registry_answers(L):
+    import ggml_hip.backend as B
+    n = L.ggml_backend_hip_get_device_count()
+    r = B.registry()
+    rp = L.ggml_backend_hip_reg()
+    assert r.api_version == 2
+    assert r.iface.get_name(rp) == b"HIP"
+    assert r.iface.get_device_count(rp) == n
+    assert L.ggml_backend_init() == rp
+    assert r.iface.get_proc_address(rp, b"no_such_symbol") is None
+    assert r.iface.get_proc_address(rp, b"ggml_backend_register_host_buffer")
+    assert L.ggml_backend_hip_register_host_buffer(None, 0) is False
+    if n == 0:
+        assert L.ggml_backend_score() == 0
+        assert not L.ggml_backend_hip_init(0)
+        assert not L.ggml_backend_hip_buffer_type(0)
+        assert not L.ggml_backend_is_hip(None)
+    assert not L.ggml_backend_hip_init(-1)
+    assert not L.ggml_backend_hip_buffer_type(n)
+
+
+def mm(a_type, K, M, N, batch=(1, 1, 1, 1)):
+    from ggml_hip import abi
+    a = abi.make_tensor(a_type, [K, M, batch[0], batch[1]])
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [K, N, batch[2], batch[3]])
+    d = abi.make_tensor(abi.GGML_TYPE_F32, [M, N, batch[2], batch[3]], op=abi.GGML_OP_MUL_MAT, srcs=(a, b))
+    return a, b, d
+
+
+def mmid(a_type, K, M, n_as, n_used, n_tokens, ne11=None):
+    from ggml_hip import abi
+    ne11 = n_used if ne11 is None else ne11
+    a = abi.make_tensor(a_type, [K, M, n_as])
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [K, ne11, n_tokens])
+    ids = abi.make_tensor(abi.GGML_TYPE_I32, [n_used, n_tokens])
+    d = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_used, n_tokens], op=abi.GGML_OP_MUL_MAT_ID, srcs=(a, b, ids))
+    return a, b, ids, d
+
+
+def test_supports_op(L):
+    from ggml_hip import abi
+    ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))  # noqa: E731
+    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0):
+        assert ok(mm(t, 4096, 4096, 1)[2])
+        assert ok(mm(t, 4096, 1024, 512, batch=(2, 1, 4, 1))[2])  # broadcast over dim 2
+        assert ok(mmid(t, 2048, 768, 128, 8, 512)[3])
+    assert ok(mm(abi.GGML_TYPE_Q8_0, 96, 64, 3)[2])  # Q8_0 rows need only whole 32-blocks
+    assert not ok(mm(abi.GGML_TYPE_F16, 4096, 4096, 1)[2])  # only the quantized weight types
+    assert not ok(mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 1, batch=(3, 1, 4, 1))[2])  # 4 % 3: no broadcast
+    a, b, d = mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 2)
+    b.nb[0] = 8  # strided elements
+    assert not ok(d)
+    a, b, d = mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 2)
+    d.type = abi.GGML_TYPE_F16
+    assert not ok(d)
+    assert not ok(mmid(abi.GGML_TYPE_Q8_0, 96, 64, 4, 2, 3)[3])  # grouped MMQ needs K % 256
+    assert not ok(mmid(abi.GGML_TYPE_Q4_K, 256, 64, 2000, 2, 3)[3])  # more than 1024 experts
+    assert ok(mmid(abi.GGML_TYPE_Q4_K, 256, 64, 16, 4, 3, ne11=1)[3])  # one row broadcast per token
+    assert not ok(mmid(abi.GGML_TYPE_Q4_K, 256, 64, 16, 4, 3, ne11=2)[3])
+    other = abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=abi.GGML_OP_ADD)
+    assert not ok(other)
+    for op in (abi.GGML_OP_NONE, abi.GGML_OP_VIEW, abi.GGML_OP_RESHAPE, abi.GGML_OP_PERMUTE, abi.GGML_OP_TRANSPOSE):
+        assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=op))
+
+
+def test_alloc_size_pads_quantized_rows(L):
+    from ggml_hip import abi
+    size = lambda t: L.ggml_backend_hip_tensor_alloc_size(C.pointer(t))  # noqa: E731
+    t = abi.make_tensor(abi.GGML_TYPE_Q4_K, [4096, 14336])
+    assert size(t) == 14336 * 16 * 144  # rows already a multiple of 512
+    t = abi.make_tensor(abi.GGML_TYPE_Q4_K, [4352, 3])  # 4352 % 512 = 256 -> one extra Q4_K block
+    assert size(t) == 3 * 17 * 144 + 144
+    t = abi.make_tensor(abi.GGML_TYPE_Q8_0, [544, 2])  # 32 past 512 -> 480 elements = 15 blocks
+    assert size(t) == 2 * 17 * 34 + 15 * 34
+    t = abi.make_tensor(abi.GGML_TYPE_F32, [100, 3])
+    assert size(t) == 1200

@@ -1,0 +1,135 @@
+"""The backend plugin path end to end on the GPU: tensors placed in a HIP
+buffer through the buffer-type vtable, a graph of MUL_MAT / MUL_MAT_ID nodes
+run by the backend's graph_compute, results read back with get_tensor and
+checked against the CPU ggml path (NMSE gate) and against the kernel-level
+entry points (same kernels, so the bytes must agree)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, mul_mat_id_f64, nmse, weights_f32, weights_q
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+
+
+@pytest.fixture(scope="module")
+def hb():
+    from ggml_hip.backend import HipBackend
+    with HipBackend(0) as b:
+        yield b
+
+
+def test_registry_and_device(hb):
+    import ggml_hip.backend as B
+    from ggml_hip import abi
+    L = B.lib()
+    rp = L.ggml_backend_hip_reg()
+    r = B.registry()
+    n = r.iface.get_device_count(rp)
+    assert n >= 1 and n == L.ggml_backend_hip_get_device_count()
+    assert L.ggml_backend_score() > 0
+    dp = r.iface.get_device(rp, 0)
+    dev = abi.deref(dp, abi.device)
+    assert dev.iface.get_name(dp) == b"HIP0"
+    props = abi.dev_props()
+    dev.iface.get_props(dp, C.pointer(props))
+    assert props.type == abi.GGML_BACKEND_DEVICE_TYPE_GPU and props.memory_total > props.memory_free > 0
+    assert props.caps.async_ and props.caps.events
+    desc = C.create_string_buffer(256)
+    L.ggml_backend_hip_get_device_description(0, desc, 256)
+    assert desc.value and desc.value == props.description
+    assert L.ggml_backend_is_hip(hb.be_ptr)
+    assert dev.iface.supports_buft(dp, hb.buft_ptr)
+    assert not dev.iface.supports_buft(dp, L.ggml_backend_hip_host_buffer_type())
+    # events: record on the backend stream, wait, synchronize
+    ev = dev.iface.event_new(dp)
+    hb.be.iface.event_record(hb.be_ptr, ev)
+    hb.be.iface.event_wait(hb.be_ptr, ev)
+    dev.iface.event_synchronize(dp, ev)
+    dev.iface.event_free(dp, ev)
+
+
+def _mul_mat_graph(hb, t, wq, K, M, x, batch_w=1, batch_x=1):
+    from ggml_hip import abi
+    N = x.shape[-2]
+    a = abi.make_tensor(t, [K, M, batch_w], name=b"w")
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [K, N, batch_x], name=b"x")
+    d = abi.make_tensor(abi.GGML_TYPE_F32, [M, N, batch_x], op=abi.GGML_OP_MUL_MAT, srcs=(a, b), name=b"out")
+    hb.alloc([a], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([b, d], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(a, wq)
+    hb.set(b, x.astype(np.float32))
+    hb.set(d, np.full((batch_x, N, M), np.nan, dtype=np.float32))
+    view = abi.make_tensor(abi.GGML_TYPE_F32, [M, N, batch_x], op=abi.GGML_OP_VIEW, srcs=(d,))
+    assert hb.compute([d, view]) == abi.GGML_STATUS_SUCCESS
+    return hb.get(d, np.float32, (batch_x, N, M))
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("N", [1, 5, 40])
+def test_graph_mul_mat(hb, tname, N):
+    import ggml_hip as G
+    t = TYPES[tname]
+    M, K = 256, 1024
+    wq, x = weights_q(t, M, K), np.array(acts(N, K))
+    got = _mul_mat_graph(hb, t, wq, K, M, x)[0]
+    cpu = O.mul_mat(t, wq, M, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    direct = G.mul_mat(tname, torch.from_numpy(np.array(wq)).cuda(), torch.from_numpy(x).cuda()).cpu().numpy()
+    assert np.array_equal(got, direct)
+
+
+def test_graph_mul_mat_broadcast_and_padding(hb):
+    """src0 broadcast over dim 2 (2 weight slices for 4 activation slices) with
+    a Q8_0 row length that is not a multiple of 512 (init_tensor zero-fills
+    the padding get_alloc_size adds)."""
+    t, M, K, N = O.TYPE_Q8_0, 96, 544, 3
+    w = np.stack([O.quantize_rows(t, weights_f32(M, K, idx=i)) for i in range(2)])
+    x = np.stack([np.array(acts(N, K, idx=i)) for i in range(4)])
+    got = _mul_mat_graph(hb, t, w, K, M, x, batch_w=2, batch_x=4)
+    for i in range(4):
+        cpu = O.mul_mat(t, w[i // 2], M, K, x[i], nth=8)
+        assert nmse(got[i], cpu) < NMSE_GATE, i
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K"])
+def test_graph_mul_mat_id(hb, tname):
+    import ggml_hip as G
+    from ggml_hip import abi
+    t = TYPES[tname]
+    n_as, M, K, n_tokens, n_ids = 8, 128, 512, 21, 3
+    wq = O.quantize_rows(t, weights_f32(n_as * M, K)).reshape(n_as, M, -1)
+    rng = np.random.default_rng(11)
+    ids = rng.integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    x = np.array(acts(n_tokens * n_ids, K)).reshape(n_tokens, n_ids, K)
+    a = abi.make_tensor(t, [K, M, n_as], name=b"experts")
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [K, n_ids, n_tokens], name=b"x")
+    it = abi.make_tensor(abi.GGML_TYPE_I32, [n_ids, n_tokens], name=b"ids")
+    d = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_ids, n_tokens], op=abi.GGML_OP_MUL_MAT_ID, srcs=(a, b, it))
+    hb.alloc([a], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([b, it, d], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(a, wq)
+    hb.set(b, x.astype(np.float32))
+    hb.set(it, ids)
+    assert hb.compute([d]) == abi.GGML_STATUS_SUCCESS
+    got = hb.get(d, np.float32, (n_tokens, n_ids, M))
+    assert np.all(got[ids < 0] == 0.0)
+    cpu = O.mul_mat_id(t, wq, n_as, M, K, x, ids, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    y = G.quantize_q8_1(torch.from_numpy(x.reshape(-1, K)).cuda(), K).cpu().numpy()
+    assert max_err_scaled(got, mul_mat_id_f64(t, wq, M, K, y, n_ids, ids)) < 2e-6
+
+
+def test_graph_rejects_unsupported_node(hb):
+    from ggml_hip import abi
+    a = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4], name=b"a")
+    hb.alloc([a])
+    add = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4], op=abi.GGML_OP_ADD, srcs=(a, a), name=b"add")
+    hb.alloc([add])
+    assert hb.compute([add]) == abi.GGML_STATUS_FAILED
