@@ -1,0 +1,220 @@
+"""Pins for the oracle functions the reference's golden vectors do not cover
+directly.  Each check ties a function to golden-pinned ones (the reference
+quantizers, dequantizers and generic dot products, test_oracle_golden.py) or
+to a closed form, so that a wrong index, a transposed operand or a dropped
+term fails here:
+
+- orc_block_dots_q8_1: on blocks whose super-block scale is 1 and whose
+  minimum is 0, the golden-pinned dequantizer returns sc * q exactly, so each
+  integer block dot is (sum of dequantized weight * q8) / sc;
+- orc_mul_mat_q8_1_f64: with activations whose Q8_1 block sums are zero it is
+  the f64 dot of the dequantized weights and dequantized activations; with
+  d = 0 weights only the min term remains, equal up to the f16 rounding of s;
+- orc_mul_mat (generic): each output is the golden-pinned vec_dot of the
+  weight row with the activation column quantized by the golden-pinned
+  quantize_row_q8_K_ref / q8_0_ref, and no output depends on the thread count;
+- orc_mul_mat_id: every (token, slot) row is orc_mul_mat of the routed expert
+  and the routed activation row; ids of -1 give zero rows;
+- the AVX2 restatements (no x86 goldens exist in the reference): checked
+  against the generic ones, integers exact and floats within rounding;
+- orc_fill_normal: moments of the distribution and a committed fingerprint of
+  the seeded stream (determinism across machines).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+
+RNG = np.random.default_rng(1234)
+F16_ONE = np.float16(1.0).view(np.uint16)
+
+
+def _q8_1(x):
+    """AoS Q8_1 blocks of one row and the int8 values, per 32."""
+    y = O.quantize_ref(O.TYPE_Q8_1, x).reshape(-1, 36)
+    q = y[:, 4:].view(np.int8).astype(np.int64)
+    d = y[:, 0:2].copy().view(np.float16).astype(np.float64)[:, 0]
+    return y.reshape(-1), q, d
+
+
+def _unit_q4_k_blocks(nblocks):
+    """Q4_K blocks with d = 1, dmin = 0, random 6-bit scales and random
+    nibbles: dequantized weight = sc_j * q."""
+    b = RNG.integers(0, 256, size=(nblocks, 144), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    b[:, 2:4] = 0
+    return b
+
+
+def _unit_q6_k_blocks(nblocks):
+    b = RNG.integers(0, 256, size=(nblocks, 210), dtype=np.uint8)
+    b[:, 208:210] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    return b
+
+
+def _unit_q8_0_blocks(nblocks):
+    b = RNG.integers(0, 256, size=(nblocks, 34), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    return b
+
+
+@pytest.mark.parametrize("t,maker,group", [(O.TYPE_Q4_K, _unit_q4_k_blocks, 32),
+                                           (O.TYPE_Q6_K, _unit_q6_k_blocks, 16),
+                                           (O.TYPE_Q8_0, _unit_q8_0_blocks, 32)])
+def test_block_dots_against_unit_scale_dequantization(t, maker, group):
+    nrows, K = 3, 512
+    bs = 256 if t != O.TYPE_Q8_0 else 32
+    w = maker(nrows * K // bs).reshape(nrows, -1)
+    x = RNG.standard_normal(K).astype(np.float32) * 3
+    y, q8, _ = _q8_1(x)
+    got = O.block_dots_q8_1(t, w, nrows, K, np.tile(y, 1))
+    q8 = q8.reshape(-1)
+    checked = 0
+    for r in range(nrows):
+        deq = O.dequantize(t, w[r], K).astype(np.float64)  # = scale * q, exactly
+        for j in range(K // group):
+            sl = slice(group * j, group * (j + 1))
+            # the sub-block's integer scale: deq / q for any nonzero code; the
+            # scale itself comes from the golden-pinned dequantizer
+            prod = float(np.dot(deq[sl], q8[sl]))
+            if t == O.TYPE_Q8_0:
+                assert got[r, j] == prod
+                checked += 1
+                continue
+            sc = _scale_of(t, w[r], j)
+            if sc == 0:
+                continue
+            assert prod == sc * got[r, j], (r, j)
+            checked += 1
+    assert checked > nrows * (K // group) // 2
+
+
+def _scale_of(t, row, j):
+    """Sub-block scale of a unit-scale block, read back through the
+    dequantizer: a block whose codes are all 1 (Q4_K) or all 33 (Q6_K)
+    dequantizes to the scale itself."""
+    bs = 144 if t == O.TYPE_Q4_K else 210
+    blk = row.reshape(-1, bs)[j // (8 if t == O.TYPE_Q4_K else 16)].copy()
+    if t == O.TYPE_Q4_K:
+        blk[16:] = 0x11  # every nibble 1
+        deq = O.dequantize(t, blk, 256)
+        return deq[32 * (j % 8)]
+    blk[0:128] = 0x11  # low 4 bits 1
+    blk[128:192] = 0xAA  # high 2 bits 2 -> code 33, value sc * 1
+    deq = O.dequantize(t, blk, 256)
+    sub = j % 16
+    return deq[16 * sub]
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+def test_mul_mat_q8_1_f64_is_the_dequantized_dot(t):
+    nrows, K, ncols = 5, 768, 3
+    w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    # pairwise-negated activations: every Q8_1 block sum is 0, so s = 0 exactly
+    half = RNG.standard_normal((ncols, K // 2)).astype(np.float32)
+    x = np.empty((ncols, K), dtype=np.float32)
+    x[:, 0::2], x[:, 1::2] = half, -half
+    ys, deq_y = [], []
+    for c in range(ncols):
+        y, q8, d = _q8_1(x[c])
+        assert np.all(q8.sum(axis=1) == 0)
+        ys.append(y)
+        deq_y.append((q8 * d[:, None]).reshape(-1))
+    got = O.mul_mat_q8_1_f64(t, w, nrows, K, np.stack(ys), ncols)
+    deq_w = np.stack([O.dequantize(t, w[r], K).astype(np.float64) for r in range(nrows)])
+    want = np.stack(deq_y) @ deq_w.T
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
+
+
+def test_mul_mat_q8_1_f64_min_term():
+    """d = 0: a Q4_K weight is -dmin*m_j on its sub-block, and the formula's
+    min term uses s = f16(d8 * sum q) in place of d8 * sum q."""
+    nrows, K = 4, 512
+    w = O.quantize_rows(O.TYPE_Q4_K, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    w = w.reshape(nrows, -1, 144).copy()
+    w[:, :, 0:2] = 0  # d = 0
+    w = w.reshape(nrows, -1)
+    x = RNG.standard_normal(K).astype(np.float32) + 0.3
+    y, q8, d = _q8_1(x)
+    got = O.mul_mat_q8_1_f64(O.TYPE_Q4_K, w, nrows, K, y[None, :], 1)[0]
+    deq_y = (q8 * d[:, None]).reshape(-1)
+    for r in range(nrows):
+        deq = O.dequantize(O.TYPE_Q4_K, w[r], K).astype(np.float64)
+        per_block = (deq * deq_y).reshape(-1, 32).sum(axis=1)
+        want = per_block.sum()
+        bound = 2.0 ** -11 * np.abs(per_block).sum() + 1e-30
+        assert abs(got[r] - want) <= bound, (r, got[r], want, bound)
+        assert abs(want) > 10 * bound  # the min term is really there
+
+
+VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0}
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+def test_mul_mat_generic_is_vec_dot_per_output(t):
+    nrows, K, ncols = 7, 512, 4
+    w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    x = RNG.standard_normal((ncols, K)).astype(np.float32)
+    got = O.mul_mat(t, w, nrows, K, x, nth=3)
+    for c in range(ncols):
+        yq = O.quantize_ref(VDT[t], x[c])
+        for r in range(nrows):
+            assert got[c, r] == np.float32(O.vec_dot(t, O.IMPL_GENERIC, K, w[r], yq)), (c, r)
+    for nth in (1, 2, 8):
+        assert np.array_equal(O.mul_mat(t, w, nrows, K, x, nth=nth), got)
+
+
+@pytest.mark.parametrize("ne11", [1, 2])
+def test_mul_mat_id_is_mul_mat_per_slot(ne11):
+    t, n_as, nrows, K, n_tokens, n_ids = O.TYPE_Q4_K, 5, 6, 256, 4, 2
+    w = O.quantize_rows(t, RNG.standard_normal((n_as * nrows, K)).astype(np.float32) * 0.02).reshape(n_as, nrows, -1)
+    x = RNG.standard_normal((n_tokens, ne11, K)).astype(np.float32)
+    ids = RNG.integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    ids[0, 0] = -1
+    got = O.mul_mat_id(t, w, n_as, nrows, K, x, ids, nth=3)
+    for tok in range(n_tokens):
+        for s in range(n_ids):
+            e = ids[tok, s]
+            if e < 0:
+                assert np.all(got[tok, s] == 0)
+                continue
+            want = O.mul_mat(t, w[e], nrows, K, x[tok, s % ne11][None, :], nth=1)[0]
+            assert np.array_equal(got[tok, s], want), (tok, s)
+
+
+@pytest.mark.skipif(not O.has_avx2(), reason="host has no AVX2")
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+def test_avx2_restatement_agrees_with_generic(t):
+    """Parity unpinned against the reference (no x86 goldens): the AVX2 path
+    is held to the golden-pinned generic one, up to float summation order."""
+    nrows, K, ncols = 16, 1024, 3
+    w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    x = RNG.standard_normal((ncols, K)).astype(np.float32)
+    g = O.mul_mat(t, w, nrows, K, x, nth=2, impl=O.IMPL_GENERIC).astype(np.float64)
+    a = O.mul_mat(t, w, nrows, K, x, nth=2, impl=O.IMPL_AVX2).astype(np.float64)
+    assert np.max(np.abs(a - g)) <= 1e-5 * np.max(np.abs(g))
+
+
+def test_q8_0_avx2_row_quantizer_against_ref():
+    x = RNG.standard_normal(4096).astype(np.float32)
+    ref = O.quantize_ref(O.TYPE_Q8_0, x).reshape(-1, 34)
+    avx = np.zeros_like(ref)
+    lib = O.lib()
+    lib.orc_quantize_row_q8_0_avx2(x.ctypes.data, avx.ctypes.data, x.size)
+    assert np.array_equal(ref[:, 0:2], avx[:, 0:2])  # same scale d = amax / 127
+    dq = ref[:, 2:].view(np.int8).astype(int) - avx[:, 2:].view(np.int8).astype(int)
+    assert np.abs(dq).max() <= 1 and np.count_nonzero(dq) <= x.size // 100  # rounding ties only
+
+
+def test_fill_normal_moments_and_fingerprint():
+    v = O.fill_normal(42, 1 << 20).astype(np.float64)
+    assert abs(v.mean()) < 5 / np.sqrt(v.size)
+    assert abs(v.std() - 1.0) < 5 / np.sqrt(2 * v.size)
+    assert abs((v ** 3).mean()) < 0.02 and abs((v ** 4).mean() - 3.0) < 0.05
+    assert O.fill_normal(42, 8, 0.0, 0.02)[0] == np.float32(O.fill_normal(42, 8)[0] * np.float32(0.02))
+    # fingerprints of the seeded streams the configs use (weights 42, activations 43, router 44)
+    fp = {s: O.fnv1a(O.fill_normal(s, 4096)) for s in (42, 43, 44)}
+    assert fp == FINGERPRINTS
+
+
+FINGERPRINTS = {42: 3664293373807877317, 43: 7632513219039429954, 44: 984130064333561219}
