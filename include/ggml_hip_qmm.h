@@ -81,6 +81,16 @@ int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64
                         int64_t dst_col_stride, void *stream);
 
 /*
+ * Small-batch GEMV on int8 MFMA, 1..16 columns, K a multiple of 256: 16 rows
+ * per workgroup contracted against all columns at once (v_mfma_i32_16x16x32_i8),
+ * same arguments and result as hip_qmm_mul_mat_vec.  The MMVQ path of
+ * mmvq.zig:275-300 for 2..8 columns and the small-column MMQ tiles of
+ * mmq.zig:865-917 for 9..16.
+ */
+int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *y_qs,
+                      const void *y_ds, int64_t ncols, float *dst, int64_t dst_col_stride, void *stream);
+
+/*
  * Op-level MUL_MAT: quantizes x to Q8_1 into `workspace` and runs the GEMV
  * (ncols <= 8) or the int8-MFMA MMQ (ncols > 8).  Mirrors the dispatch in
  * ggml_cuda_mul_mat (src/ggml/cuda/mulmat.zig:576-639).

@@ -384,9 +384,21 @@ int dispatch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stri
 
 }  // namespace
 
+extern "C" int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                 const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
+                                 int64_t dst_col_stride, void *stream);
+
+// The int8-MFMA GEMV takes 8 columns of K-quant weights on large matrices,
+// where the v_dot4 GEMV's activation re-reads dominate.
+static bool use_gemv_mfma(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return (type == TYPE_Q4_K || type == TYPE_Q6_K) && ncols >= 8 && nrows >= 2048 && K % QK_K == 0;
+}
+
 extern "C" int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                    const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
                                    int64_t dst_col_stride, void *stream) {
+    if (use_gemv_mfma(type, K, nrows, ncols))
+        return hip_qmm_gemv_mfma(type, w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, stream);
     return dispatch<0>(type, w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, nullptr, stream);
 }
 

@@ -79,6 +79,36 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
     }
 }
 
+// Q8_1 code of one value (quantize_row_q8_1_ref, src/ggml/quants/legacy.zig:
+// 451-484): roundf (half away from zero) of x * id, narrowed with the
+// reference's clamping C cast (src/ggml/impl.zig:744-752).
+// Branch-free.  roundf(v) is computed as trunc(v + copysign(h, v)) with h the
+// float just below 0.5: the two agree for every float (checked for all
+// non-negative floats below 2^24, the formula is odd in v, and above 2^24
+// every float is an integer that v + h rounds back to).  The clamp is one
+// v_med3_f32, NaN maps to 0 by a select, and the clamped value is integral,
+// so the convert is exact.
+__device__ __forceinline__ int8_t q8_1_code(float x, float id) {
+    const float v = x * id;
+    const float r = __builtin_truncf(v + __builtin_copysignf(0.49999997f, v));
+    const float c = __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
+    return (int8_t)(int)(r == r ? c : 0.0f);
+}
+
+// Q8_1 block header: f16 d in the low half, f16 s = fp16(f32(sum * d)) in the
+// high half.  The f32 product is pinned in a register before its f16
+// conversion: the AMDGPU backend otherwise folds multiply + convert into
+// v_fma_mixlo_f16 (one rounding, where the reference rounds to f32 first and
+// then to f16), which changes `s` whenever the f32 product is an exact f16
+// tie.  `#pragma clang fp contract(off)` does not stop that fold.
+__device__ __forceinline__ uint32_t q8_1_pack_ds(float d, int sum) {
+    float sd = (float)sum * d;
+    asm volatile("" : "+v"(sd));
+    const uint32_t hd = __half_as_ushort(__float2half_rn(d));
+    const uint32_t hs = __half_as_ushort(__float2half_rn(sd));
+    return hd | (hs << 16);
+}
+
 // Sum over the 64 lanes of a wavefront with DPP: an inclusive prefix sum
 // inside each row of 16 lanes (row_shr 1, 2, 4, 8), then row_bcast:15 and
 // row_bcast:31 carry the row totals forward, leaving the total in lane 63,

@@ -3,16 +3,11 @@
 //   amax over 32 values; d = amax / 127 (IEEE division); id = d ? 1/d : 0
 //   (IEEE division, not v_rcp); q = trunc-to-int8(roundf(x * id)) with
 //   roundf = half away from zero; d and s = fp16(sum(q) * d) rounded to
-//   nearest-even.  Built without fast-math so '/' stays correctly rounded.
+//   nearest-even (q8_1_code / q8_1_pack_ds in qmm_device.h).  Built without
+//   fast-math so '/' stays correctly rounded.
 //
 // One 32-lane half-wave per Q8_1 block: lane i owns element i of the block;
 // amax and sum(q) are butterfly reductions inside the half-wave.
-//
-// The f32 product `(float)sum * d` is pinned in a register before its f16
-// conversion: the AMDGPU backend otherwise folds multiply + convert into
-// v_fma_mixlo_f16 (one rounding, where the reference rounds to f32 first and
-// then to f16), which changes `s` whenever the f32 product is an exact f16
-// tie.  `#pragma clang fp contract(off)` does not stop that fold.
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
@@ -32,21 +27,11 @@ __device__ __forceinline__ Q8_1Val quantize_lane32(float x) {
     for (int off = 16; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, 32));
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    const float r = roundf(x * id);
-    // The reference's C cast with clamping (src/ggml/impl.zig:744-752).
-    const int8_t q = r != r ? (int8_t)0 : r <= -128.0f ? (int8_t)-128 : r >= 127.0f ? (int8_t)127 : (int8_t)r;
+    const int8_t q = q8_1_code(x, id);
     int sum = q;
 #pragma unroll
     for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
     return {q, d, sum};
-}
-
-__device__ __forceinline__ uint32_t pack_ds(float d, int sum) {
-    float sd = (float)sum * d;
-    asm volatile("" : "+v"(sd));  // materialise the f32-rounded product (no fold into the f16 convert)
-    const uint32_t hd = __half_as_ushort(__float2half_rn(d));
-    const uint32_t hs = __half_as_ushort(__float2half_rn(sd));
-    return hd | (hs << 16);
 }
 
 // Reference-layout output: one block_q8_1 {d, s, qs[32]} per 32 values.
@@ -63,7 +48,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_aos(const float *__restrict
     const int64_t row = (i23 * ne1 + i1);
     uint8_t *blk = y + (row * (ne0_padded / QK8) + i0 / QK8) * 36;
     blk[4 + (i0 & 31)] = (uint8_t)v.q;
-    if ((i0 & 31) == 0) *reinterpret_cast<uint32_t *>(blk) = pack_ds(v.d, v.sum);
+    if ((i0 & 31) == 0) *reinterpret_cast<uint32_t *>(blk) = q8_1_pack_ds(v.d, v.sum);
 }
 
 // Planar output: qs[c*Kp + k], ds[c*Kp/32 + k/32].
@@ -76,7 +61,7 @@ __global__ __launch_bounds__(256) void quantize_q8_1_planar(const float *__restr
     const float xv = k < K ? x[c * x_col_stride + k] : 0.0f;
     const Q8_1Val v = quantize_lane32(xv);
     qs[c * Kp + k] = v.q;
-    if ((k & 31) == 0) ds[c * (Kp / QK8) + k / QK8] = pack_ds(v.d, v.sum);
+    if ((k & 31) == 0) ds[c * (Kp / QK8) + k / QK8] = q8_1_pack_ds(v.d, v.sum);
 }
 
 }  // namespace

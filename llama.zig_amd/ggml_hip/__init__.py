@@ -47,6 +47,8 @@ def lib():
         L.hip_qmm_mul_mat_workspace_size.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mul_mat_vec.restype = i32
         L.hip_qmm_mul_mat_vec.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
+        L.hip_qmm_gemv_mfma.restype = i32
+        L.hip_qmm_gemv_mfma.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_mmq.restype = i32
         L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mmq_workspace_size.restype = ctypes.c_size_t
@@ -137,6 +139,16 @@ def mul_mat_vec(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tens
     out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
     _check(lib().hip_qmm_mul_mat_vec(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
                                      _stream()), "hip_qmm_mul_mat_vec")
+    return out
+
+
+def gemv_mfma(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=None):
+    """Small-batch GEMV on int8 MFMA against planar Q8_1 activations (1..16 columns)."""
+    t, nrows, rs = _weight_args(qtype, w, K)
+    n = qs.shape[0]
+    out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_gemv_mfma(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
+                                   _stream()), "hip_qmm_gemv_mfma")
     return out
 
 
