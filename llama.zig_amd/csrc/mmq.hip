@@ -356,24 +356,36 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         constexpr int NT = TI * TJ;
         constexpr int NP = F::NG * NT;
         using SType = typename std::conditional<F::GK == 32, v4i, long>::type;
-        struct Ops {
-            SType a, b;
-            v4h sa, sb;
+        // The A-side operands (weights and the row scale) depend on the scale
+        // group only: they are read once per group and shared by the TJ
+        // column tiles (2 buffers, by group parity).
+        static_assert(TI == 1, "one 32-row strip per wave");
+        struct AOps {
+            SType a;
+            v4h sa;
         };
-        auto load_ops = [&](int p, Ops &o) {
-            const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
+        struct BOps {
+            SType b;
+            v4h sb;
+        };
+        AOps aops[2];
+        auto load_ops = [&](int p, BOps &o) {
+            const int g = p / NT, j = p % NT;
             const int qb = F::GK == 32 ? g : g >> 1;  // Q8_1 block of this group
-            o.sa = __builtin_bit_cast(v4h, sm.asc[g][wr + 32 * i + li]);
+            if (j == 0) {
+                aops[g & 1].sa = __builtin_bit_cast(v4h, sm.asc[g][wr + li]);
+                aops[g & 1].a = *reinterpret_cast<const SType *>(sm.a + (wr + li) * LDA + F::GK * g + (F::GK / 2) * lh);
+            }
             o.sb = __builtin_bit_cast(v4h, sm.bd8[lh][qb][wc + 32 * j + li]);
-            o.a = *reinterpret_cast<const SType *>(sm.a + (wr + 32 * i + li) * LDA + F::GK * g + (F::GK / 2) * lh);
             o.b = *reinterpret_cast<const SType *>(sm.b + (wc + 32 * j + li) * LDA + F::GK * g + (F::GK / 2) * lh);
         };
-        auto issue = [&](const Ops &o, v16i &S, v16f &SC) {
+        auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
+            const AOps &ao = aops[(p / NT) & 1];
             const v16i z = {0};
             const v16f zf = {0};
-            if constexpr (F::GK == 32) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.b, z, 0, 0, 0);
-            else S = __builtin_amdgcn_mfma_i32_32x32x16_i8(o.a, o.b, z, 0, 0, 0);
-            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(o.sa, o.sb, zf, 0, 0, 0);
+            if constexpr (F::GK == 32) S = __builtin_amdgcn_mfma_i32_32x32x32_i8(ao.a, o.b, z, 0, 0, 0);
+            else S = __builtin_amdgcn_mfma_i32_32x32x16_i8(ao.a, o.b, z, 0, 0, 0);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(ao.sa, o.sb, zf, 0, 0, 0);
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
@@ -393,16 +405,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         // delivers the operands of pair p+2.  The scheduling fences pin that
         // order; left alone the scheduler consumes each MFMA result right
         // after issuing it and stalls on the MFMA latency.
-        Ops ops[2];
+        BOps ops[2];
         v16i Sb[2];
         v16f SCb[2];
         load_ops(0, ops[0]);
         if (NP > 1) load_ops(1, ops[1]);
-        issue(ops[0], Sb[0], SCb[0]);
+        issue(0, ops[0], Sb[0], SCb[0]);
 #pragma unroll
         for (int p = 0; p < NP; ++p) {
             __builtin_amdgcn_sched_barrier(0);
-            if (p + 1 < NP) issue(ops[(p + 1) & 1], Sb[(p + 1) & 1], SCb[(p + 1) & 1]);
+            if (p + 1 < NP) issue(p + 1, ops[(p + 1) & 1], Sb[(p + 1) & 1], SCb[(p + 1) & 1]);
             if (p + 2 < NP) load_ops(p + 2, ops[p & 1]);
             __builtin_amdgcn_sched_barrier(0);
             consume(p, Sb[p & 1], SCb[p & 1]);
