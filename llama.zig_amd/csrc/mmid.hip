@@ -27,11 +27,49 @@ namespace {
 constexpr int GROUP_THREADS = 1024;
 constexpr int MAX_EXPERTS = 1024;
 
-// One workgroup.  Pass 1 counts the pairs routed to each expert (LDS
-// atomics); an exclusive scan gives each expert its column range; pass 2
-// places every pair at its expert's cursor.  The order of pairs inside an
-// expert's range is whatever the atomics give: each pair writes its own
-// output row, so the order does not change any result.
+constexpr int IDS_PER_THREAD = 16;  // ids held in registers between the passes
+
+// Exclusive prefix sums of two per-thread values over the workgroup (thread i
+// holds the values of expert i), with the totals.
+__device__ __forceinline__ void block_excl_scan2(int &a, int &b, int &tot_a, int &tot_b) {
+    __shared__ int wa[GROUP_THREADS / 64], wb[GROUP_THREADS / 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int ia = a, ib = b;  // inclusive scans inside the wave
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int ua = __shfl_up(ia, off), ub = __shfl_up(ib, off);
+        if (lane >= off) {
+            ia += ua;
+            ib += ub;
+        }
+    }
+    if (lane == 63) {
+        wa[wave] = ia;
+        wb[wave] = ib;
+    }
+    __syncthreads();
+    int pa = 0, pb = 0;
+    tot_a = 0;
+    tot_b = 0;
+    for (int w = 0; w < GROUP_THREADS / 64; ++w) {
+        if (w < wave) {
+            pa += wa[w];
+            pb += wb[w];
+        }
+        tot_a += wa[w];
+        tot_b += wb[w];
+    }
+    a = pa + ia - a;
+    b = pb + ib - b;
+}
+
+// One workgroup.  Every thread first loads its ids into registers (all loads
+// in flight at once); pass 1 counts the pairs routed to each expert (LDS
+// atomics); parallel exclusive scans give each expert its column range and
+// its tile range, and thread e writes expert e's tiles; pass 2 places every
+// pair at its expert's cursor.  The order of pairs inside an expert's range is
+// whatever the atomics give: each pair writes its own output row, so the
+// order does not change any result.
 __global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
     const int32_t *__restrict__ ids, int64_t ids_stride, int64_t n_tokens, int64_t n_ids, int n_as, int64_t ne11,
     int bn, int32_t *__restrict__ col_src, int32_t *__restrict__ col_dst, int32_t *__restrict__ expert_off,
@@ -40,42 +78,64 @@ __global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
     __shared__ int count[MAX_EXPERTS];
     __shared__ int cursor[MAX_EXPERTS];
     const int64_t npairs = n_tokens * n_ids;
-    for (int e = threadIdx.x; e < n_as; e += GROUP_THREADS) count[e] = 0;
+    const int tid = threadIdx.x;
+    auto id_of = [&](int64_t p) -> int {
+        const int e = ids[(p / n_ids) * ids_stride + p % n_ids];
+        return e >= 0 && e < n_as ? e : -1;
+    };
+    int eid[IDS_PER_THREAD];
+#pragma unroll
+    for (int k = 0; k < IDS_PER_THREAD; ++k) {
+        const int64_t p = tid + (int64_t)k * GROUP_THREADS;
+        eid[k] = p < npairs ? id_of(p) : -1;
+    }
+    for (int e = tid; e < n_as; e += GROUP_THREADS) count[e] = 0;
     __syncthreads();
-    for (int64_t p = threadIdx.x; p < npairs; p += GROUP_THREADS) {
-        const int64_t t = p / n_ids, s = p % n_ids;
-        const int e = ids[t * ids_stride + s];
-        if (e >= 0 && e < n_as) atomicAdd(&count[e], 1);
+#pragma unroll
+    for (int k = 0; k < IDS_PER_THREAD; ++k)
+        if (eid[k] >= 0) atomicAdd(&count[eid[k]], 1);
+    for (int64_t p = tid + (int64_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) {
+        const int e = id_of(p);
+        if (e >= 0) atomicAdd(&count[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int off = 0, nt = 0;
-        for (int e = 0; e < n_as; ++e) {
-            cursor[e] = off;
-            expert_off[e] = off;
-            for (int c = 0; c < count[e]; c += bn) {
-                tiles[2 * nt] = e;
-                tiles[2 * nt + 1] = off + c;
-                ++nt;
+    {
+        int c = tid < n_as ? count[tid] : 0;
+        int nt = (c + bn - 1) / bn;
+        const int nt_own = nt;
+        int total_c, total_t;
+        block_excl_scan2(c, nt, total_c, total_t);
+        if (tid < n_as) {
+            cursor[tid] = c;
+            expert_off[tid] = c;
+            for (int i = 0; i < nt_own; ++i) {
+                tiles[2 * (nt + i)] = tid;
+                tiles[2 * (nt + i) + 1] = c + i * bn;
             }
-            off += count[e];
         }
-        expert_off[n_as] = off;
-        *n_tiles = nt;
+        if (tid == 0) {
+            expert_off[n_as] = total_c;
+            *n_tiles = total_t;
+        }
     }
     __syncthreads();
-    for (int64_t p = threadIdx.x; p < npairs; p += GROUP_THREADS) {
-        const int64_t t = p / n_ids, s = p % n_ids;
-        const int e = ids[t * ids_stride + s];
-        if (e >= 0 && e < n_as) {
+    auto place = [&](int64_t p, int e) {
+        if (e >= 0) {
             const int pos = atomicAdd(&cursor[e], 1);
+            const int64_t t = p / n_ids, s = p % n_ids;
             col_src[pos] = (int32_t)(t * ne11 + s % ne11);
             col_dst[pos] = (int32_t)p;
         } else {
             float *row = dst + p * dst_row_stride;
             for (int64_t r = 0; r < nrows; ++r) row[r] = 0.0f;
         }
+    };
+#pragma unroll
+    for (int k = 0; k < IDS_PER_THREAD; ++k) {
+        const int64_t p = tid + (int64_t)k * GROUP_THREADS;
+        if (p < npairs) place(p, eid[k]);
     }
+    for (int64_t p = tid + (int64_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) place(p, id_of(p));
 }
 
 struct MmidLayout {

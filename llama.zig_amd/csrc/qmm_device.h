@@ -89,7 +89,12 @@ __device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, u
 // v_med3_f32, NaN maps to 0 by a select, and the clamped value is integral,
 // so the convert is exact.
 __device__ __forceinline__ int8_t q8_1_code(float x, float id) {
-    const float v = x * id;
+    // The product is pinned in a register so that it is rounded to f32 on its
+    // own, as the reference's x * id is: HIP's default contraction otherwise
+    // fuses it with the add below into one FMA (one rounding of the sum),
+    // which moves ties such as x * id = 63.5 - 5e-7 from 64 to 63.
+    float v = x * id;
+    asm volatile("" : "+v"(v));
     const float r = __builtin_truncf(v + __builtin_copysignf(0.49999997f, v));
     const float c = __builtin_amdgcn_fmed3f(r, -128.0f, 127.0f);
     return (int8_t)(int)(r == r ? c : 0.0f);

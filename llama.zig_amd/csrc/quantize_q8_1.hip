@@ -64,6 +64,61 @@ __global__ __launch_bounds__(256) void quantize_q8_1_planar(const float *__restr
     if ((k & 31) == 0) ds[c * (Kp / QK8) + k / QK8] = q8_1_pack_ds(v.d, v.sum);
 }
 
+// Lane values of the quad partner (lane ^ 1, lane ^ 2): DPP quad_perm
+// [1,0,3,2] and [2,3,0,1].
+__device__ __forceinline__ float quad_x1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_x2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int quad_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+
+// Planar output, 8 consecutive values per lane: a 32-block is the 4 lanes of
+// one quad, so amax and sum(q) take two DPP exchanges instead of five
+// shuffles, and x is read with 16-byte loads.  The max and the integer sum do
+// not depend on the order, so the bytes equal the one-value-per-lane
+// kernel's.  Needs x 16-byte aligned and x_col_stride a multiple of 4.
+__global__ __launch_bounds__(256) void quantize_q8_1_planar8(const float *__restrict__ x, int64_t K,
+                                                             int64_t x_col_stride, int64_t Kp,
+                                                             int8_t *__restrict__ qs, uint32_t *__restrict__ ds) {
+    const int64_t k = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    const int64_t c = blockIdx.y;
+    // whole quads stay active: Kp is a multiple of 512, so k < Kp for all 4 lanes or none
+    if (k >= Kp) return;
+    float v[8];
+    if (k < K) {  // K % 32 == 0: a 32-block is wholly inside or wholly past K
+        const float4 a = *reinterpret_cast<const float4 *>(x + c * x_col_stride + k);
+        const float4 b = *reinterpret_cast<const float4 *>(x + c * x_col_stride + k + 4);
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+        v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, quad_x1(amax));
+    amax = fmaxf(amax, quad_x2(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t lo = 0, hi = 0;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int8_t q = q8_1_code(v[i], id);
+        sum += q;
+        if (i < 4) lo |= (uint32_t)(uint8_t)q << (8 * i);
+        else hi |= (uint32_t)(uint8_t)q << (8 * (i - 4));
+    }
+    sum += quad_x1(sum);
+    sum += quad_x2(sum);
+    *reinterpret_cast<uint2 *>(qs + c * Kp + k) = make_uint2(lo, hi);
+    if ((threadIdx.x & 3) == 0) ds[c * (Kp / QK8) + k / QK8] = q8_1_pack_ds(d, sum);
+}
+
 }  // namespace
 
 extern "C" int hip_qmm_quantize_q8_1(const float *x, void *y_q8_1, int64_t ne00, int64_t s01, int64_t s02,
@@ -85,8 +140,14 @@ extern "C" int hip_qmm_quantize_q8_1_planar(const float *x, int64_t K, int64_t n
         return (int)hipErrorInvalidValue;
     if (ncols == 0) return 0;
     const int64_t Kp = pad_k(K);
-    const dim3 grid((unsigned)((Kp + 255) / 256), (unsigned)ncols);
-    hipLaunchKernelGGL(quantize_q8_1_planar, grid, dim3(256), 0, (hipStream_t)stream, x, K, x_col_stride, Kp, qs,
-                       (uint32_t *)ds);
+    if ((uintptr_t)x % 16 == 0 && x_col_stride % 4 == 0 && (uintptr_t)qs % 8 == 0) {
+        const dim3 grid((unsigned)((Kp / 8 + 255) / 256), (unsigned)ncols);
+        hipLaunchKernelGGL(quantize_q8_1_planar8, grid, dim3(256), 0, (hipStream_t)stream, x, K, x_col_stride, Kp, qs,
+                           (uint32_t *)ds);
+    } else {
+        const dim3 grid((unsigned)((Kp + 255) / 256), (unsigned)ncols);
+        hipLaunchKernelGGL(quantize_q8_1_planar, grid, dim3(256), 0, (hipStream_t)stream, x, K, x_col_stride, Kp, qs,
+                           (uint32_t *)ds);
+    }
     return (int)hipGetLastError();
 }

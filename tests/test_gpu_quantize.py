@@ -74,3 +74,35 @@ def test_planar_layout_holds_the_same_bytes():
     qs, ds = qs.cpu().numpy(), ds.cpu().numpy()
     np.testing.assert_array_equal(aos[:, :, 4:].reshape(n, K).view(np.int8), qs[:, :K])
     np.testing.assert_array_equal(aos[:, :, :4].copy().view(np.int32).reshape(n, K // 32), ds)
+
+
+@pytest.mark.parametrize("K,pad", [(768, 0), (4096, 4), (1024, 1)])
+def test_planar_matches_reference_on_ties_and_strides(K, pad):
+    """The planar quantizer (8 values per lane with quad reductions for
+    16-byte-aligned x, one value per lane otherwise) against
+    quantize_row_q8_1_ref, on tie-heavy and extreme rows, with and without
+    the 512-padding and with row strides that do and do not allow 16-byte
+    loads.  Padding blocks must come out as zero blocks."""
+    import ggml_hip as G
+    rng = np.random.default_rng(9)
+    n = 6
+    rows = [np.array(acts(1, K))[0],
+            (rng.integers(-254, 255, size=K) * np.float32(0.5)).astype(np.float32),  # x.5 ties after scaling
+            np.full(K, 3.0, dtype=np.float32),
+            np.where(np.arange(K) % 3 == 0, 1e-30, -7.5).astype(np.float32),
+            (rng.standard_normal(K) * 1e4).astype(np.float32),
+            np.zeros(K, dtype=np.float32)]
+    x = np.zeros((n, K + pad), dtype=np.float32)
+    x[:, :K] = np.stack(rows)
+    xd = torch.from_numpy(x).cuda()[:, :K]
+    Kp = G.padded_k(K)
+    qs = torch.empty((n, Kp), dtype=torch.int8, device="cuda")
+    ds = torch.empty((n, Kp // 32), dtype=torch.int32, device="cuda")
+    L = G.lib()
+    assert L.hip_qmm_quantize_q8_1_planar(G._ptr(xd), K, n, K + pad, G._ptr(qs), G._ptr(ds), G._stream()) == 0
+    qs, ds = qs.cpu().numpy(), ds.cpu().numpy()
+    for r in range(n):
+        ref = O.quantize_ref(O.TYPE_Q8_1, x[r, :K]).reshape(-1, 36)
+        np.testing.assert_array_equal(qs[r, :K], ref[:, 4:].reshape(-1).view(np.int8))
+        np.testing.assert_array_equal(ds[r, :K // 32], ref[:, :4].copy().view(np.int32).reshape(-1))
+        assert not qs[r, K:].any() and not ds[r, K // 32:].any()
