@@ -38,6 +38,12 @@
 
 using namespace qmm;
 
+// mmq_q4k_dma.hip: the Q4_K kernel fed by direct global->LDS loads
+int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+                       const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
+                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
+                       const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s);
+
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -497,10 +503,20 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
            int split, float *partial, hipStream_t s) {
     const int64_t gx = (nrows + BM - 1) / BM;
     if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64) return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), dim3((unsigned)gx, (unsigned)gy, (unsigned)split), dim3(NTHREADS), 0,
-                       s, (const uint8_t *)w, K, nrows, row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols,
-                       dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, split > 1 ? partial : nullptr);
-    if (int e = (int)hipGetLastError()) return e;
+    const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)split);
+    // Q4_K with 16-byte aligned operands (the transfer unit of the direct
+    // global->LDS loads; the weight rows are checked by check_weights)
+    if (TYPE == TYPE_Q4_K && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+        if (int e = mmq_q4k_dma_launch(BN, w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst,
+                                       dst_col_stride, grid, tiles, n_tiles, expert_off, col_src, col_dst,
+                                       split > 1 ? partial : nullptr, s))
+            return e;
+    } else {
+        hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,
+                           row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols, dst, dst_col_stride, tiles,
+                           n_tiles, expert_off, col_src, col_dst, split > 1 ? partial : nullptr);
+        if (int e = (int)hipGetLastError()) return e;
+    }
     if (split > 1) {
         const int64_t n = nrows * ncols;
         hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, split, nrows,

@@ -1,0 +1,306 @@
+// mmq_q4k_dma.hip -- the Q4_K MMQ with direct global->LDS loads.
+//
+// Same arithmetic as mmq.hip's kernel: exact int8 block dots on
+// v_mfma_i32_32x32x32_i8, the per-(row, column, block) scale sc_j * d8_j as an
+// exact f16 outer product (v_mfma_f32_32x32x8_f16, one live K slot), one
+// convert + FMA per output and block, d and the min term (K=8 f16 MFMA of
+// m_j x s8_j) once per super-block:
+//   out = sum_b d_b * sum_j (sc_bj*d8_j) * S_bj - dmin_b * sum_j m_bj*s8_j
+//
+// What differs is the data path.  The staged kernel loads each K-step into
+// registers, unpacks it and writes it to LDS between two barriers, so every
+// wave stalls on that phase.  Here the step's raw bytes go straight from
+// global memory into LDS with global_load_lds_dwordx4 (no registers, no
+// VALU), into a second LDS buffer while the current one is contracted:
+//   - A: the 128 rows' Q4_K blocks of the step, 144 B per row, as stored;
+//     nibbles are unpacked when the MFMA operands are read (each 16-byte read
+//     serves sub-blocks 2c and 2c+1);
+//   - B: the BN columns' Q8_1 int8 values, 256 B per column, with the 16-byte
+//     chunk c of column n stored at chunk position c ^ (n % 16) so that the
+//     operand reads of 32 columns spread over all banks;
+//   - the columns' raw (d8 | s8 << 16) headers.
+// One barrier per K-step.  A wave waits only for its own transfers
+// (vmcnt(0)) before that barrier; the barrier publishes every wave's.
+// Rows past nrows and columns past the tile load duplicates of a valid row /
+// column, whose results are never stored.
+#include "../../include/ggml_hip_qmm.h"
+#include "qmm_device.h"
+
+using namespace qmm;
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+constexpr int BM = 128;
+constexpr int NTHREADS = 256;
+constexpr int ABYTES = BM * Q4K_BYTES;  // 18432: 18 transfers of 1 KiB
+
+__device__ __forceinline__ uint32_t f16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
+}
+
+// 16 bytes per lane from global memory to LDS at base + 16 * lane (base is
+// wave-uniform).
+__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
+}
+
+template <int BN>
+__global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+    const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
+    int64_t dst_col_stride, const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles,
+    const int32_t *__restrict__ expert_off, const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst,
+    float *__restrict__ partial) {
+    constexpr int TJ = BN / 32;
+    constexpr int NQB = BN / 4;    // 1 KiB transfers of B int8 per step
+    constexpr int NQD = BN / 32;   // 1 KiB transfers of B headers per step
+    __shared__ alignas(16) uint8_t sA0[ABYTES], sA1[ABYTES];
+    __shared__ alignas(16) uint8_t sB0[BN * 256], sB1[BN * 256];
+    __shared__ alignas(16) uint32_t sD0[BN * 8], sD1[BN * 8];
+    __shared__ alignas(16) float rowd[4][2][32];
+
+    const int64_t Kp = pad_k(K);
+    const int64_t row0 = (int64_t)blockIdx.x * BM;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 31, lh = lane >> 5;
+    const int wr = wave * 32;
+
+    int64_t col0 = (int64_t)blockIdx.y * BN, col_end = ncols;
+    const uint8_t *wexp = w;
+    if (tiles) {
+        if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup
+        const int e = tiles[2 * blockIdx.y], cs = tiles[2 * blockIdx.y + 1];
+        wexp = w + (int64_t)e * expert_stride;
+        col0 = cs;
+        const int64_t ce = expert_off[e + 1];
+        col_end = ce < col0 + BN ? ce : col0 + BN;
+    }
+    auto src_col = [&](int n) -> int64_t {  // activation row of tile column n
+        int64_t cc = col0 + n;
+        if (cc >= col_end) cc = col0;
+        return tiles ? (int64_t)col_src[cc] : cc;
+    };
+
+    // per-lane sources of this wave's transfers (fixed over the K-steps)
+    const uint8_t *a_src[(18 + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (18 + 3) / 4; ++i) {
+        const int q = wave + 4 * i;
+        const int pos = (q < 18 ? q : 0) * 1024 + lane * 16;
+        const int r = pos / Q4K_BYTES, ch = (pos - r * Q4K_BYTES) / 16;
+        const int64_t grow = row0 + r < nrows ? row0 + r : nrows - 1;
+        a_src[i] = wexp + grow * row_stride + ch * 16;
+    }
+    const int8_t *b_src[(NQB + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (NQB + 3) / 4; ++i) {
+        const int q = wave + 4 * i;
+        const int pos = (q < NQB ? q : 0) * 1024 + lane * 16;
+        const int n = pos >> 8, p = (pos >> 4) & 15;
+        b_src[i] = yqs + src_col(n) * Kp + 16 * (p ^ (n & 15));
+    }
+    const uint32_t *d_src = yds;
+    if (wave < NQD) {
+        const int pos = wave * 1024 + lane * 16;
+        d_src = yds + src_col(pos >> 5) * (Kp / QK8) + 4 * ((pos >> 4) & 1);
+    }
+
+    auto dma = [&](int64_t kb, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
+#pragma unroll
+        for (int i = 0; i < (18 + 3) / 4; ++i)
+            if (wave + 4 * i < 18) dma16(a_src[i] + kb * Q4K_BYTES, sA + (wave + 4 * i) * 1024);
+#pragma unroll
+        for (int i = 0; i < (NQB + 3) / 4; ++i)
+            if (wave + 4 * i < NQB) dma16(b_src[i] + kb * 256, sB + (wave + 4 * i) * 1024);
+        if (wave < NQD) dma16(d_src + kb * 8, reinterpret_cast<uint8_t *>(sD) + wave * 1024);
+    };
+
+    v16f acc[TJ], accb[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+
+    // Scale outer product per group g on the f16 MFMA with one live K slot:
+    // groups 0-3 live in slot 0 of lane half 0, groups 4-7 in slot 4 (slot 0
+    // of lane half 1).  A lane of half h decodes only sub-blocks 4h..4h+3
+    // (their scales and mins); its A operand for group g is sc_{4h + g%4},
+    // live when h == g/4 and otherwise paired with a zero B slot.
+    const uint32_t mask_hi = (0u - (uint32_t)lh) & 0xFFFFu, mask_lo = mask_hi ^ 0xFFFFu;
+    const uint32_t sel_s8 = 0x07060302u;  // s8 halves of two headers -> one dword
+
+    auto compute = [&](const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
+        const uint8_t *arow = sA + (wr + li) * Q4K_BYTES;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(arow);
+        // getScaleMinK4 for sub-blocks 4*lh .. 4*lh+3, four at a time (bytes)
+        const uint32_t hsel = 0u - (uint32_t)lh;  // all ones in lane half 1
+        const uint32_t scb = (hsel & ((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u))) |
+                             (~hsel & hdr.y & 0x3F3F3F3Fu);
+        const uint32_t mnb = (hsel & (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u))) |
+                             (~hsel & hdr.z & 0x3F3F3F3Fu);
+        uint32_t sa[4], mh[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sa[t] = f16_bits((float)((scb >> (8 * t)) & 0xFFu));
+            mh[t] = f16_bits((float)((mnb >> (8 * t)) & 0xFFu));
+        }
+        // row d / dmin into this wave's table (the two lanes of a row store the same values)
+        rowd[wave][0][li] = h2f(hdr.x);
+        rowd[wave][1][li] = h2f(hdr.x >> 16);
+        // the tile columns' (d8 | s8 << 16) headers of the step
+        uint4 hd[TJ][2];
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const uint32_t *h = sD + (32 * j + li) * 8;
+            hd[j][0] = *reinterpret_cast<const uint4 *>(h);
+            hd[j][1] = *reinterpret_cast<const uint4 *>(h + 4);
+        }
+        auto hword = [&](int j, int g) -> uint32_t {
+            const uint4 &v = hd[j][g >> 2];
+            const int t = g & 3;
+            return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;
+        };
+
+        struct BOps {
+            v4i b;
+            v4h sb;
+        };
+        v4i aop[2];
+        uint4 qa;
+        auto load_ops = [&](int p, BOps &o) {
+            const int g = p / TJ, j = p % TJ;
+            if (j == 0) {
+                if ((g & 1) == 0) qa = *reinterpret_cast<const uint4 *>(arow + 16 + 32 * (g >> 1) + 16 * lh);
+                const uint32_t m4 = 0x0F0F0F0Fu;
+                const int sh = 4 * (g & 1);
+                aop[g & 1] = v4i{(int)((qa.x >> sh) & m4), (int)((qa.y >> sh) & m4), (int)((qa.z >> sh) & m4),
+                                 (int)((qa.w >> sh) & m4)};
+            }
+            const int n = 32 * j + li;
+            o.b = *reinterpret_cast<const v4i *>(sB + n * 256 + 16 * ((2 * g + lh) ^ (n & 15)));
+            o.sb = __builtin_bit_cast(v4h, make_uint2(hword(j, g) & (g < 4 ? mask_lo : mask_hi), 0u));
+        };
+        auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
+            const int g = p / TJ;
+            const v16i z = {0};
+            const v16f zf = {0};
+            S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[g & 1], o.b, z, 0, 0, 0);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, make_uint2(sa[g & 3], 0u)), o.sb, zf, 0,
+                                                      0, 0);
+        };
+        auto consume = [&](int p, const v16i &S, const v16f &SC) {
+            const int g = p / TJ, j = p % TJ;
+            if (g == 0) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) accb[j][v] = (float)S[v] * SC[v];
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) accb[j][v] = fmaf((float)S[v], SC[v], accb[j][v]);
+            }
+        };
+        // pair p+1's MFMAs and pair p+2's LDS reads are issued before pair p's
+        // epilogue; the fences keep the scheduler from collapsing that
+        constexpr int NP = 8 * TJ;
+        BOps ops[2];
+        v16i Sb[2];
+        v16f SCb[2];
+        load_ops(0, ops[0]);
+        load_ops(1, ops[1]);
+        issue(0, ops[0], Sb[0], SCb[0]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + 1 < NP) issue(p + 1, ops[(p + 1) & 1], Sb[(p + 1) & 1], SCb[(p + 1) & 1]);
+            if (p + 2 < NP) load_ops(p + 2, ops[p & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(p, Sb[p & 1], SCb[p & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+
+        // acc += d[r] * accb - dmin[r] * sum_j m_j[r] * s8_j[c]; lane half h
+        // supplies K slots 4h..4h+3 of the K=8 MFMA: sub-blocks 4h..4h+3
+        float dr[16], dm[16];
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+            const float4 t = *reinterpret_cast<const float4 *>(&rowd[wave][0][8 * v4 + 4 * lh]);
+            const float4 u = *reinterpret_cast<const float4 *>(&rowd[wave][1][8 * v4 + 4 * lh]);
+            dr[4 * v4 + 0] = t.x; dr[4 * v4 + 1] = t.y; dr[4 * v4 + 2] = t.z; dr[4 * v4 + 3] = t.w;
+            dm[4 * v4 + 0] = u.x; dm[4 * v4 + 1] = u.y; dm[4 * v4 + 2] = u.z; dm[4 * v4 + 3] = u.w;
+        }
+        const v4h am = __builtin_bit_cast(v4h, make_uint2(mh[0] | (mh[1] << 16), mh[2] | (mh[3] << 16)));
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const uint4 s = *reinterpret_cast<const uint4 *>(sD + (32 * j + li) * 8 + 4 * lh);
+            const v4h bm = __builtin_bit_cast(
+                v4h, make_uint2(__builtin_amdgcn_perm(s.y, s.x, sel_s8), __builtin_amdgcn_perm(s.w, s.z, sel_s8)));
+            const v16f zf = {0};
+            const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[j][v] = fmaf(dr[v], accb[j][v], fmaf(-dm[v], P[v], acc[j][v]));
+        }
+    };
+
+    const int64_t nkb_all = K / QK_K;
+    const int64_t kb_begin = nkb_all * blockIdx.z / gridDim.z;
+    const int64_t nkb = nkb_all * (blockIdx.z + 1) / gridDim.z;
+    if (kb_begin < nkb) {
+        dma(kb_begin, sA0, sB0, sD0);
+        wait_vmem();
+        __syncthreads();
+    }
+    for (int64_t kb = kb_begin; kb < nkb; kb += 2) {
+        if (kb + 1 < nkb) dma(kb + 1, sA1, sB1, sD1);
+        compute(sA0, sB0, sD0);
+        wait_vmem();
+        __syncthreads();
+        if (kb + 1 < nkb) {
+            if (kb + 2 < nkb) dma(kb + 2, sA0, sB0, sD0);
+            compute(sA1, sB1, sD1);
+            wait_vmem();
+            __syncthreads();
+        }
+    }
+
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int64_t c = col0 + 32 * j + li;
+        if (c >= col_end) continue;
+        const int64_t drow = tiles ? (int64_t)col_dst[c] : c;
+        float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + drow * dst_col_stride;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t r = row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
+            if (r < nrows) o[r] = acc[j][v];
+        }
+    }
+}
+
+}  // namespace
+
+// Launch for mmq.hip's dispatch (same arguments as its kernel; Q4_K rows and
+// the activation planes 16-byte aligned, which the caller checks).
+int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+                       const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
+                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
+                       const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s) {
+    const uint8_t *wb = (const uint8_t *)w;
+    const uint32_t *ds = (const uint32_t *)yds;
+    if (bn == 32)
+        hipLaunchKernelGGL(mmq_q4k_dma_kernel<32>, grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, expert_stride,
+                           yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, partial);
+    else
+        hipLaunchKernelGGL(mmq_q4k_dma_kernel<64>, grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, expert_stride,
+                           yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, partial);
+    return (int)hipGetLastError();
+}
