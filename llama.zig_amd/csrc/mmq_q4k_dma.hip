@@ -177,22 +177,25 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             v4h sb;
         };
         v4i aop[2];
-        uint4 qa;
+        uint4 qa, qc;  // weight bytes as read (two pairs ahead) and in use
         auto load_ops = [&](int p, BOps &o) {
             const int g = p / TJ, j = p % TJ;
-            if (j == 0) {
-                if ((g & 1) == 0) qa = *reinterpret_cast<const uint4 *>(arow + 16 + 32 * (g >> 1) + 16 * lh);
-                const uint32_t m4 = 0x0F0F0F0Fu;
-                const int sh = 4 * (g & 1);
-                aop[g & 1] = v4i{(int)((qa.x >> sh) & m4), (int)((qa.y >> sh) & m4), (int)((qa.z >> sh) & m4),
-                                 (int)((qa.w >> sh) & m4)};
-            }
+            // the weight bytes are only read here; unpacking them at issue time
+            // keeps the LDS latency off the critical path
+            if (j == 0 && (g & 1) == 0) qa = *reinterpret_cast<const uint4 *>(arow + 16 + 32 * (g >> 1) + 16 * lh);
             const int n = 32 * j + li;
             o.b = *reinterpret_cast<const v4i *>(sB + n * 256 + 16 * ((2 * g + lh) ^ (n & 15)));
             o.sb = __builtin_bit_cast(v4h, make_uint2(hword(j, g) & (g < 4 ? mask_lo : mask_hi), 0u));
         };
         auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
-            const int g = p / TJ;
+            const int g = p / TJ, j = p % TJ;
+            if (j == 0) {
+                if ((g & 1) == 0) qc = qa;
+                const uint32_t m4 = 0x0F0F0F0Fu;
+                const int sh = 4 * (g & 1);
+                aop[g & 1] = v4i{(int)((qc.x >> sh) & m4), (int)((qc.y >> sh) & m4), (int)((qc.z >> sh) & m4),
+                                 (int)((qc.w >> sh) & m4)};
+            }
             const v16i z = {0};
             const v16f zf = {0};
             S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[g & 1], o.b, z, 0, 0, 0);
