@@ -315,6 +315,164 @@ __global__ __launch_bounds__(64 * WAVES_PER_BLOCK, (gemv_min_waves<TYPE, NC>()))
     }
 }
 
+// Row-streaming GEMV (2..8 columns on large Q4_K matrices).  The v_dot4
+// GEMV above re-loads every column's activation slice for each pair of rows,
+// and at 4-8 columns those loads, not the weights, occupy the texture
+// addresser.  Here a wave owns R rows: per K-step it loads the activation
+// slice once, streams the R rows' weight slices through a queue of D loads in
+// flight, and keeps per-lane partial sums of all R x NC outputs.  The sums
+// across the 64 lanes go through LDS, 64 outputs at a time: lane o adds
+// output o of every lane in lane order.
+template <int TYPE, int NC, int R, int D>
+__global__ __launch_bounds__(256) void gemv_rows_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
+    const uint32_t *__restrict__ yds, int64_t Kp, float *__restrict__ dst, int64_t dst_col_stride) {
+    using F = Fmt<TYPE>;
+    constexpr int NO = R * NC;  // outputs per wave
+    constexpr int LD = 65;      // padded LDS row of one lane's 64 partial sums
+    __shared__ float red[WAVES_PER_BLOCK][64 * LD];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t r0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + wave) * R;
+    if (r0 >= nrows) return;  // uniform per wave; no workgroup barrier follows
+    const uint8_t *rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rowp[r] = w + (r0 + r < nrows ? r0 + r : nrows - 1) * row_stride;
+    float acc[R][NC];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+    constexpr int STEP = 64 * F::W;
+    const int K32 = (int)K;
+    for (int k0 = 0; k0 < K32; k0 += STEP) {
+        const int kl = k0 + lane * F::W;
+        const bool live = kl < K32;
+        const int klc = live ? kl : k0;  // lanes past K load a valid slice and add nothing
+        Act<TYPE> a[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) a[c].load(yqs + c * Kp, yds + c * (Kp / QK8), klc);
+        Wt<TYPE> q[D];
+#pragma unroll
+        for (int i = 0; i < D && i < R; ++i) q[i].load(rowp[i], klc);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const Wt<TYPE> cur = q[r % D];
+            if (r + D < R) q[r % D].load(rowp[r + D], klc);
+            // the next row's loads stay above this row's arithmetic
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                int S[F::NSUB];
+                cur.dots(a[c], S);
+                const float v = cur.combine(a[c], S, klc);
+                acc[r][c] += live ? v : 0.0f;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    float *buf = red[wave];
+#pragma unroll
+    for (int o0 = 0; o0 < NO; o0 += 64) {
+#pragma unroll
+        for (int o = o0; o < o0 + 64 && o < NO; ++o) buf[lane * LD + (o - o0)] = acc[o / NC][o % NC];
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's partial sums are in LDS
+        const int o = o0 + lane;
+        float sum = 0.0f;
+        if (o < NO) {
+#pragma unroll 16
+            for (int i = 0; i < 64; ++i) sum += buf[i * LD + lane];
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_s_waitcnt(0xc07f);  // every lane has read before the next chunk is written
+        const int r = o / NC, c = o % NC;
+        if (o < NO && r0 + r < nrows) dst[(int64_t)c * dst_col_stride + r0 + r] = sum;
+    }
+}
+
+// K-split GEMV (small row counts and long rows): the four waves of a
+// workgroup share RPW rows and take a quarter of the K-steps each; their
+// partial sums meet in LDS and are added in wave order.
+template <int TYPE, int NC, int RPW>
+__global__ __launch_bounds__(256) void gemv_ks_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
+    const uint32_t *__restrict__ yds, int64_t Kp, float *__restrict__ dst, int64_t dst_col_stride) {
+    using F = Fmt<TYPE>;
+    __shared__ float part[WAVES_PER_BLOCK][RPW * NC];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = (int64_t)blockIdx.x * RPW;
+    const uint8_t *rowp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rowp[r] = w + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride;
+    float acc[RPW][NC];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+    constexpr int STEP = 64 * F::W;
+    const int K32 = (int)K;
+    const int nsteps = (K32 + STEP - 1) / STEP;
+    const int s0 = nsteps * wave / WAVES_PER_BLOCK, s1 = nsteps * (wave + 1) / WAVES_PER_BLOCK;
+    for (int st = s0; st < s1; ++st) {
+        const int kl = st * STEP + lane * F::W;
+        if (kl < K32) {
+            Wt<TYPE> wt[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) wt[r].load(rowp[r], kl);
+            Act<TYPE> a[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) a[c].load(yqs + c * Kp, yds + c * (Kp / QK8), kl);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    int S[F::NSUB];
+                    wt[r].dots(a[c], S);
+                    acc[r][c] += wt[r].combine(a[c], S, kl);
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float v = wave_sum(acc[r][c]);
+            if (lane == 0) part[wave][r * NC + c] = v;
+        }
+    __syncthreads();
+    if (wave == 0 && lane < RPW * NC) {
+        float v = part[0][lane];
+#pragma unroll
+        for (int i = 1; i < WAVES_PER_BLOCK; ++i) v += part[i][lane];
+        const int r = lane / NC, c = lane % NC;
+        if (row0 + r < nrows) dst[(int64_t)c * dst_col_stride + row0 + r] = v;
+    }
+}
+
+template <int TYPE, int NC, int R, int D>
+int launch_rows(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
+    const int64_t units = (nrows + R - 1) / R;
+    const int64_t nblocks = (units + WAVES_PER_BLOCK - 1) / WAVES_PER_BLOCK;
+    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_rows_kernel<TYPE, NC, R, D>), dim3((unsigned)nblocks), dim3(64 * WAVES_PER_BLOCK), 0,
+                       s, w, K, nrows, row_stride, yqs, yds, pad_k(K), dst, dst_col_stride);
+    return (int)hipGetLastError();
+}
+
+template <int TYPE, int NC, int RPW>
+int launch_ks(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+              const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
+    const int64_t nblocks = (nrows + RPW - 1) / RPW;
+    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL((gemv_ks_kernel<TYPE, NC, RPW>), dim3((unsigned)nblocks), dim3(64 * WAVES_PER_BLOCK), 0, s,
+                       w, K, nrows, row_stride, yqs, yds, pad_k(K), dst, dst_col_stride);
+    return (int)hipGetLastError();
+}
+
 template <int TYPE, int NC, int MODE>
 int launch_nc(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
               const uint32_t *yds, float *dst, int64_t dst_col_stride, int32_t *dots, hipStream_t s) {
@@ -330,10 +488,64 @@ int launch_nc(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, co
     return (int)hipGetLastError();
 }
 
+// Kernel choice for the scaled GEMV (measured on MI355X over the decode and
+// cross-quant shapes of bench.py):
+//   - Q4_K, K <= 4096, 2..8 columns, >= 4096 rows (>= 8192 at 2 columns):
+//     row-streaming, 16 rows per wave from 8192 rows (8 at 2 columns), else 4;
+//   - at most 2048 rows, or (K-quants) K >= 8192 with at most 4096 rows: the
+//     K-split kernel (1 row per workgroup at <= 2048 rows -- 2 for Q4_K at
+//     5-8 columns -- and 4 otherwise);
+//   - everything else: the two-rows-per-wave kernel.
+enum class GemvKind { pairs, rows16, rows8, rows4, ks1, ks2, ks4 };
+
+GemvKind choose(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    if (type == TYPE_Q4_K && K <= 4096 && ncols >= 2 && nrows >= (ncols == 2 ? 8192 : 4096))
+        return nrows >= 8192 ? (ncols == 2 ? GemvKind::rows8 : GemvKind::rows16) : GemvKind::rows4;
+    if (nrows <= 2048) return type == TYPE_Q4_K && ncols >= 5 ? GemvKind::ks2 : GemvKind::ks1;
+    if (type != TYPE_Q8_0 && K >= 8192 && nrows <= 4096) return GemvKind::ks4;
+    return GemvKind::pairs;
+}
+
+template <int TYPE, int NC>
+int launch_scaled(GemvKind kind, const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                  const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
+    constexpr int D = NC <= 4 ? 4 : 2;  // weight loads in flight (register budget)
+    if constexpr (TYPE == TYPE_Q4_K && NC >= 2) {
+        switch (kind) {
+        case GemvKind::rows16: return launch_rows<TYPE, NC, 16, D>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+        case GemvKind::rows8: return launch_rows<TYPE, NC, 8, 4>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+        case GemvKind::rows4: return launch_rows<TYPE, NC, 4, 4>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+        default: break;
+        }
+    }
+    switch (kind) {
+    case GemvKind::ks1: return launch_ks<TYPE, NC, 1>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+    case GemvKind::ks2: return launch_ks<TYPE, NC, 2>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+    case GemvKind::ks4: return launch_ks<TYPE, NC, 4>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+    default: return launch_nc<TYPE, NC, 0>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, nullptr, s);
+    }
+}
+
 template <int TYPE, int MODE>
 int launch_type(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                 const uint32_t *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int32_t *dots,
                 hipStream_t s) {
+    if constexpr (MODE == 0) {
+        const GemvKind kind = choose(TYPE, K, nrows, ncols);
+        {
+            switch (ncols) {
+            case 1: return launch_scaled<TYPE, 1>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 2: return launch_scaled<TYPE, 2>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 3: return launch_scaled<TYPE, 3>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 4: return launch_scaled<TYPE, 4>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 5: return launch_scaled<TYPE, 5>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 6: return launch_scaled<TYPE, 6>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 7: return launch_scaled<TYPE, 7>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            case 8: return launch_scaled<TYPE, 8>(kind, w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, s);
+            default: return (int)hipErrorInvalidValue;
+            }
+        }
+    }
     switch (ncols) {
     case 1: return launch_nc<TYPE, 1, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
     case 2: return launch_nc<TYPE, 2, MODE>(w, K, nrows, row_stride, yqs, yds, dst, dst_col_stride, dots, s);
@@ -388,10 +600,11 @@ extern "C" int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nro
                                  const int8_t *y_qs, const void *y_ds, int64_t ncols, float *dst,
                                  int64_t dst_col_stride, void *stream);
 
-// The int8-MFMA GEMV takes 8 columns of K-quant weights on large matrices,
-// where the v_dot4 GEMV's activation re-reads dominate.
+// The int8-MFMA GEMV takes 8 columns of K-quant weights on large matrices
+// that the row-streaming GEMV does not cover (Q6_K, or rows longer than 4096).
 static bool use_gemv_mfma(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    return (type == TYPE_Q4_K || type == TYPE_Q6_K) && ncols >= 8 && nrows >= 2048 && K % QK_K == 0;
+    const bool rows = type == TYPE_Q4_K && K <= 4096 && nrows >= 4096;
+    return (type == TYPE_Q4_K || type == TYPE_Q6_K) && !rows && ncols >= 8 && nrows > 2048 && K % QK_K == 0;
 }
 
 extern "C" int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,

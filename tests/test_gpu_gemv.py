@@ -56,6 +56,25 @@ def test_gemv_parity(tname, nrows, K, ncols):
     assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {max_rel(got, cpu):.3g}"
 
 
+# Shapes that reach each GEMV kernel of hip_qmm_mul_mat_vec's shape-based
+# choice: Q4_K row-streaming with 4 / 8 / 16 rows per wave (ragged row counts,
+# 7 columns = more outputs per wave than lanes), the K-split kernel with 4
+# rows per workgroup (long rows, at most 4096 rows), and the int8-MFMA GEMV
+# beside them.
+@pytest.mark.parametrize("tname,nrows,K,ncols", [
+    ("Q4_K", 4100, 4096, 3), ("Q4_K", 4096, 2048, 8), ("Q4_K", 8195, 1024, 2), ("Q4_K", 8195, 1024, 7),
+    ("Q4_K", 2500, 8192, 2), ("Q6_K", 2500, 8192, 4), ("Q6_K", 3000, 8192, 8), ("Q8_0", 2500, 8192, 3)])
+def test_gemv_kernel_paths(tname, nrows, K, ncols):
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, ncols)
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    e = nmse(got, cpu)
+    assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {max_rel(got, cpu):.3g}"
+
+
 def test_gemv_config0_op_level():
     """Config 0: 4096x4096 Q4_K (seed 42) times a 4096x1 activation through the
     op-level entry point, against the CPU ggml path."""
