@@ -77,16 +77,19 @@ __global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
     int64_t nrows) {
     __shared__ int count[MAX_EXPERTS];
     __shared__ int cursor[MAX_EXPERTS];
-    const int64_t npairs = n_tokens * n_ids;
+    // pair indices fit in 32 bits (checked by the host): 32-bit division
+    // instead of the much longer 64-bit sequence
+    const uint32_t npairs = (uint32_t)(n_tokens * n_ids), nid = (uint32_t)n_ids;
     const int tid = threadIdx.x;
-    auto id_of = [&](int64_t p) -> int {
-        const int e = ids[(p / n_ids) * ids_stride + p % n_ids];
+    auto id_of = [&](uint32_t p) -> int {
+        const uint32_t t = p / nid;
+        const int e = ids[(int64_t)t * ids_stride + (p - t * nid)];
         return e >= 0 && e < n_as ? e : -1;
     };
     int eid[IDS_PER_THREAD];
 #pragma unroll
     for (int k = 0; k < IDS_PER_THREAD; ++k) {
-        const int64_t p = tid + (int64_t)k * GROUP_THREADS;
+        const uint32_t p = tid + (uint32_t)k * GROUP_THREADS;
         eid[k] = p < npairs ? id_of(p) : -1;
     }
     for (int e = tid; e < n_as; e += GROUP_THREADS) count[e] = 0;
@@ -94,7 +97,7 @@ __global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
 #pragma unroll
     for (int k = 0; k < IDS_PER_THREAD; ++k)
         if (eid[k] >= 0) atomicAdd(&count[eid[k]], 1);
-    for (int64_t p = tid + (int64_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) {
+    for (uint32_t p = tid + (uint32_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) {
         const int e = id_of(p);
         if (e >= 0) atomicAdd(&count[e], 1);
     }
@@ -119,23 +122,24 @@ __global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
         }
     }
     __syncthreads();
-    auto place = [&](int64_t p, int e) {
+    const uint32_t n11 = (uint32_t)ne11;  // 1 or n_ids
+    auto place = [&](uint32_t p, int e) {
         if (e >= 0) {
             const int pos = atomicAdd(&cursor[e], 1);
-            const int64_t t = p / n_ids, s = p % n_ids;
-            col_src[pos] = (int32_t)(t * ne11 + s % ne11);
+            const uint32_t t = p / nid, sl = p - t * nid;
+            col_src[pos] = (int32_t)(t * n11 + (n11 == 1 ? 0u : sl));
             col_dst[pos] = (int32_t)p;
         } else {
-            float *row = dst + p * dst_row_stride;
+            float *row = dst + (int64_t)p * dst_row_stride;
             for (int64_t r = 0; r < nrows; ++r) row[r] = 0.0f;
         }
     };
 #pragma unroll
     for (int k = 0; k < IDS_PER_THREAD; ++k) {
-        const int64_t p = tid + (int64_t)k * GROUP_THREADS;
+        const uint32_t p = tid + (uint32_t)k * GROUP_THREADS;
         if (p < npairs) place(p, eid[k]);
     }
-    for (int64_t p = tid + (int64_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) place(p, id_of(p));
+    for (uint32_t p = tid + (uint32_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) place(p, id_of(p));
 }
 
 struct MmidLayout {

@@ -54,13 +54,13 @@ __device__ __forceinline__ void wait_vmem() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
 }
 
-template <int BN>
+template <int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
     const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
     int64_t dst_col_stride, const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles,
     const int32_t *__restrict__ expert_off, const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst,
-    float *__restrict__ partial) {
+    float *__restrict__ partial, int gx, int gy, int gz) {
     constexpr int TJ = BN / 32;
     constexpr int NQB = BN / 4;    // 1 KiB transfers of B int8 per step
     constexpr int NQD = BN / 32;   // 1 KiB transfers of B headers per step
@@ -70,51 +70,73 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     __shared__ alignas(16) float rowd[4][2][32];
 
     const int64_t Kp = pad_k(K);
-    const int64_t row0 = (int64_t)blockIdx.x * BM;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int wr = wave * 32;
 
-    int64_t col0 = (int64_t)blockIdx.y * BN, col_end = ncols;
-    const uint8_t *wexp = w;
-    if (tiles) {
-        if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup
-        const int e = tiles[2 * blockIdx.y], cs = tiles[2 * blockIdx.y + 1];
-        wexp = w + (int64_t)e * expert_stride;
-        col0 = cs;
-        const int64_t ce = expert_off[e + 1];
-        col_end = ce < col0 + BN ? ce : col0 + BN;
-    }
-    auto src_col = [&](int n) -> int64_t {  // activation row of tile column n
-        int64_t cc = col0 + n;
-        if (cc >= col_end) cc = col0;
-        return tiles ? (int64_t)col_src[cc] : cc;
+    // Work items (row tile, column tile, K part), row tiles fastest; the
+    // workgroups take items blockIdx.x, +gridDim.x, ...  Grouped mode has
+    // *n_tiles live column tiles.
+    const int gy_live = GROUPED ? (*n_tiles < gy ? *n_tiles : gy) : gy;  // uniform
+    const int nitems = gx * gy_live * gz;  // < 2^31, checked by the host
+    const int nkb_all = (int)(K / QK_K);
+    // one item's tile, as 32-bit values (the host bounds rows, columns and
+    // K-steps below 2^31); wexp is the expert's weights in grouped mode
+    struct Item {
+        int row0, col0, col_end, kb0, kb1, z;
+        const uint8_t *wexp;
     };
+    auto item_xyz = [&](int bx, int by, int bz) {
+        Item I;
+        I.row0 = bx * BM;
+        I.z = bz;
+        I.kb0 = nkb_all * bz / gz;
+        I.kb1 = nkb_all * (bz + 1) / gz;
+        I.col0 = by * BN;
+        I.col_end = (int)ncols;
+        I.wexp = w;
+        if constexpr (GROUPED) {
+            const int e = tiles[2 * by], cs = tiles[2 * by + 1];
+            I.wexp = w + (int64_t)e * expert_stride;
+            I.col0 = cs;
+            const int ce = expert_off[e + 1];
+            I.col_end = ce < I.col0 + BN ? ce : I.col0 + BN;
+        }
+        return I;
+    };
+    auto item = [&](int it) { return item_xyz(it % gx, (it / gx) % gy_live, it / (gx * gy_live)); };
 
-    // per-lane sources of this wave's transfers (fixed over the K-steps)
+    // per-lane sources of this wave's transfers for one item (fixed over its K-steps)
     const uint8_t *a_src[(18 + 3) / 4];
-#pragma unroll
-    for (int i = 0; i < (18 + 3) / 4; ++i) {
-        const int q = wave + 4 * i;
-        const int pos = (q < 18 ? q : 0) * 1024 + lane * 16;
-        const int r = pos / Q4K_BYTES, ch = (pos - r * Q4K_BYTES) / 16;
-        const int64_t grow = row0 + r < nrows ? row0 + r : nrows - 1;
-        a_src[i] = wexp + grow * row_stride + ch * 16;
-    }
     const int8_t *b_src[(NQB + 3) / 4];
-#pragma unroll
-    for (int i = 0; i < (NQB + 3) / 4; ++i) {
-        const int q = wave + 4 * i;
-        const int pos = (q < NQB ? q : 0) * 1024 + lane * 16;
-        const int n = pos >> 8, p = (pos >> 4) & 15;
-        b_src[i] = yqs + src_col(n) * Kp + 16 * (p ^ (n & 15));
-    }
     const uint32_t *d_src = yds;
-    if (wave < NQD) {
-        const int pos = wave * 1024 + lane * 16;
-        d_src = yds + src_col(pos >> 5) * (Kp / QK8) + 4 * ((pos >> 4) & 1);
-    }
+    auto set_sources = [&](const Item &I) {
+        auto src_col = [&](int n) -> int64_t {  // activation row of tile column n
+            int64_t cc = (int64_t)I.col0 + n;
+            if (cc >= I.col_end) cc = I.col0;
+            return GROUPED ? (int64_t)col_src[cc] : cc;
+        };
+#pragma unroll
+        for (int i = 0; i < (18 + 3) / 4; ++i) {
+            const int q = wave + 4 * i;
+            const int pos = (q < 18 ? q : 0) * 1024 + lane * 16;
+            const int r = pos / Q4K_BYTES, ch = (pos - r * Q4K_BYTES) / 16;
+            const int64_t grow = (int64_t)I.row0 + r < nrows ? (int64_t)I.row0 + r : nrows - 1;
+            a_src[i] = I.wexp + grow * row_stride + ch * 16;
+        }
+#pragma unroll
+        for (int i = 0; i < (NQB + 3) / 4; ++i) {
+            const int q = wave + 4 * i;
+            const int pos = (q < NQB ? q : 0) * 1024 + lane * 16;
+            const int n = pos >> 8, p = (pos >> 4) & 15;
+            b_src[i] = yqs + src_col(n) * Kp + 16 * (p ^ (n & 15));
+        }
+        if (wave < NQD) {
+            const int pos = wave * 1024 + lane * 16;
+            d_src = yds + src_col(pos >> 5) * (Kp / QK8) + 4 * ((pos >> 4) & 1);
+        }
+    };
 
     auto dma = [&](int64_t kb, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
 #pragma unroll
@@ -254,37 +276,115 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
         }
     };
 
-    const int64_t nkb_all = K / QK_K;
-    const int64_t kb_begin = nkb_all * blockIdx.z / gridDim.z;
-    const int64_t nkb = nkb_all * (blockIdx.z + 1) / gridDim.z;
-    if (kb_begin < nkb) {
-        dma(kb_begin, sA0, sB0, sD0);
+    // Grouped 32-column tiles (the MoE case: a few K-steps per tile) are
+    // walked by persistent workgroups; everything else takes one tile per
+    // workgroup (the persistent loop's extra state spills at 64 columns).
+    constexpr bool PERSIST = GROUPED && BN == 32;
+    if constexpr (!PERSIST) {
+        // one tile per workgroup: grid (row tiles, column tiles, K parts)
+        if ((int)blockIdx.y >= gy_live) return;  // grouped: past the live tiles (uniform)
+        const Item C = item_xyz((int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
+        set_sources(C);
+        dma(C.kb0, sA0, sB0, sD0);
         wait_vmem();
         __syncthreads();
-    }
-    for (int64_t kb = kb_begin; kb < nkb; kb += 2) {
-        if (kb + 1 < nkb) dma(kb + 1, sA1, sB1, sD1);
-        compute(sA0, sB0, sD0);
+        for (int kb = C.kb0; kb < C.kb1; kb += 2) {
+            if (kb + 1 < C.kb1) dma(kb + 1, sA1, sB1, sD1);
+            compute(sA0, sB0, sD0);
+            wait_vmem();
+            __syncthreads();
+            if (kb + 1 < C.kb1) {
+                if (kb + 2 < C.kb1) dma(kb + 2, sA0, sB0, sD0);
+                compute(sA1, sB1, sD1);
+                wait_vmem();
+                __syncthreads();
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < TJ; ++j) {
+            const int64_t c = (int64_t)C.col0 + 32 * j + li;
+            if (c >= C.col_end) continue;
+            float *o;
+            if constexpr (GROUPED) o = dst + (int64_t)col_dst[c] * dst_col_stride;
+            else o = partial ? partial + ((int64_t)C.z * ncols + c) * nrows : dst + c * dst_col_stride;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int64_t r = (int64_t)C.row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
+                if (r < nrows) o[r] = acc[j][v];
+            }
+        }
+    } else {
+    int it_c = (int)blockIdx.x;
+        if (it_c >= nitems) return;  // uniform per workgroup
+        // The transfer cursor (item it_n, step kb_n) runs one step ahead of the
+        // contraction (item it_c, step kb_c) and crosses into the next item while
+        // the current one finishes, so a tile's first transfer is not exposed.
+        Item C = item(it_c);
+        int it_n = it_c;
+        int kb_n = C.kb0, kb1_n = C.kb1, kb_c = C.kb0;
+        bool dma_live = true;
+        set_sources(C);
+        auto advance = [&]() {
+            if (++kb_n < kb1_n) return;
+            it_n += (int)gridDim.x;
+            if (it_n < nitems) {
+                const Item N = item(it_n);
+                kb_n = N.kb0;
+                kb1_n = N.kb1;
+                set_sources(N);
+            } else {
+                dma_live = false;
+            }
+        };
+        auto store = [&]() {
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int64_t c = (int64_t)C.col0 + 32 * j + li;
+                if (c >= C.col_end) continue;
+                float *o = dst + (int64_t)col_dst[c] * dst_col_stride;
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int64_t r = (int64_t)C.row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
+                    if (r < nrows) o[r] = acc[j][v];
+                }
+            }
+        };
+        // after a step's contraction: at an item's last step store it and move on
+        auto finish_step = [&]() -> bool {
+            if (++kb_c < C.kb1) return true;
+            store();
+#pragma unroll
+            for (int j = 0; j < TJ; ++j)
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+            it_c += (int)gridDim.x;
+            if (it_c >= nitems) return false;
+            C = item(it_c);
+            kb_c = C.kb0;
+            return true;
+        };
+
+        dma(kb_n, sA0, sB0, sD0);
+        advance();
         wait_vmem();
         __syncthreads();
-        if (kb + 1 < nkb) {
-            if (kb + 2 < nkb) dma(kb + 2, sA0, sB0, sD0);
+        for (;;) {
+            if (dma_live) {
+                dma(kb_n, sA1, sB1, sD1);
+                advance();
+            }
+            compute(sA0, sB0, sD0);
+            wait_vmem();
+            __syncthreads();
+            if (!finish_step()) break;
+            if (dma_live) {
+                dma(kb_n, sA0, sB0, sD0);
+                advance();
+            }
             compute(sA1, sB1, sD1);
             wait_vmem();
             __syncthreads();
-        }
-    }
-
-#pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        const int64_t c = col0 + 32 * j + li;
-        if (c >= col_end) continue;
-        const int64_t drow = tiles ? (int64_t)col_dst[c] : c;
-        float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + drow * dst_col_stride;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t r = row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
-            if (r < nrows) o[r] = acc[j][v];
+            if (!finish_step()) break;
         }
     }
 }
@@ -292,18 +392,43 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
 }  // namespace
 
 // Launch for mmq.hip's dispatch (same arguments as its kernel; Q4_K rows and
-// the activation planes 16-byte aligned, which the caller checks).
+// the activation planes 16-byte aligned, which the caller checks).  `grid` is
+// the tile grid (row tiles, column tiles, K parts).  Grouped 32-column tiles
+// are walked by at most two workgroups per CU (the kernel's register and LDS
+// budget); otherwise each workgroup takes one tile.
 int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
                        const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s) {
+    static int resident = 0;  // workgroups resident at once: 2 per CU
+    if (!resident) {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        resident = 2 * cus;
+    }
+    const int64_t items = (int64_t)grid.x * grid.y * grid.z;
+    if (items > 0x7FFFFFFF || K / QK_K > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
+        return (int)hipErrorInvalidValue;
+    // grouped mode walks its tiles with the resident workgroups; a dense
+    // launch takes one tile per workgroup
+    const dim3 pgrid((unsigned)(items < resident ? items : resident));
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
-    if (bn == 32)
-        hipLaunchKernelGGL(mmq_q4k_dma_kernel<32>, grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, expert_stride,
-                           yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, partial);
-    else
-        hipLaunchKernelGGL(mmq_q4k_dma_kernel<64>, grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, expert_stride,
-                           yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src, col_dst, partial);
+    const int gx = (int)grid.x, gy = (int)grid.y, gz = (int)grid.z;
+#define MMQ_DMA_LAUNCH(BNV, GR)                                                                                        \
+    hipLaunchKernelGGL((mmq_q4k_dma_kernel<BNV, GR>), GR && BNV == 32 ? pgrid : grid, dim3(NTHREADS), 0, s, wb, K,   \
+                       nrows,                                                                                          \
+                       row_stride,                                                                                     \
+                       expert_stride, yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src,       \
+                       col_dst, partial, gx, gy, gz)
+    if (tiles) {
+        if (bn == 32) MMQ_DMA_LAUNCH(32, true);
+        else MMQ_DMA_LAUNCH(64, true);
+    } else {
+        if (bn == 32) MMQ_DMA_LAUNCH(32, false);
+        else MMQ_DMA_LAUNCH(64, false);
+    }
+#undef MMQ_DMA_LAUNCH
     return (int)hipGetLastError();
 }
