@@ -3,15 +3,15 @@
 
 Metric: "Q4_K GEMV GB/s (% HBM peak) @14336x4096 b=1; MMQ
 int8 TOPS @b=512".  A step is one ggml_mul_mat of the headline decode shape:
-Q4_K weight 14336x4096 times one f32 activation column, i.e. the Q8_1
-activation quantizer followed by the GEMV.  Inputs are resident in HBM; the
+Q4_K weight 14336x4096 times one f32 activation column; for one column the
+op runs a single kernel, the GEMV with the Q8_1 quantization fused in.  Inputs are resident in HBM; the
 weight is rotated over enough distinct copies (> 2x the 256 MB Infinity
 Cache) that every step streams it from HBM.  Steps are replayed from a HIP
 graph (one node per kernel) so the measurement is of the GPU, not of Python
 launch overhead.
 
 Printed JSON (one line): value = whole-step GB/s (algorithmic bytes /
-wall-clock per step); roofline = the GEMV kernel alone (algorithmic bytes /
+wall-clock per step); roofline = the step's kernel alone (algorithmic bytes /
 its average duration from HIP events); mmq = the T=512 MMQ figure (TOPS and
 fraction of the int8 dense peak); cpu_baseline = the reference CPU path
 (restated AVX2 vec_dot_q4_K_q8_K in ggml's mul_mat chunking) on a bounded
@@ -30,9 +30,10 @@ ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "llama.zig_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-# HBM bytes per GEMV launch measured with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE,
-# scaled by a 64 MiB copy's readings (x1.9993 / x1.0): profiles/gemv_q4_K_14336x4096_b1.md
-GEMV_TRAFFIC_BYTES = 33_146_531
+# HBM bytes per launch of the op's kernel (the fused GEMV) measured with
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a 64 MiB copy's readings
+# (x1.9993 / x1.0): profiles/gemv_q4_K_14336x4096_b1.md
+GEMV_TRAFFIC_BYTES = 33_261_179
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 INFINITY_CACHE = 256 << 20
 
@@ -286,18 +287,21 @@ def main():
     bytes_alg = w_bytes + K * 4 + M * 4
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
 
-    # dominant kernel alone: GEMV against the already-quantized activation,
-    # n back-to-back launches between two events (agrees with rocprofv3's
-    # per-dispatch average); per-launch event pairs are reported beside it but
-    # carry ~2 us of event overhead on a ~8 us kernel.
+    # dominant kernel alone: the step is one kernel here (the GEMV with the
+    # Q8_1 quantization fused in); n back-to-back launches between two events
+    # (agrees with rocprofv3's per-dispatch average); per-launch event pairs
+    # are reported beside it but carry ~2 us of event overhead.  The unfused
+    # pair (quantizer + GEMV on the quantized column) is timed for reference.
     n_ev = 8 * ncopy
+    fused = lambda i: G.mul_mat_vec_f32("Q4_K", weights[i % ncopy], K, x, out=out)  # noqa: E731
+    fused_batch_ms = event_time_batch(torch, fused, n_ev)
+    fused_pair_ms, fused_pair_med_ms = event_time_kernel(torch, fused, n_ev)
     gemv = lambda i: G.mul_mat_vec("Q4_K", weights[i % ncopy], K, qs, ds, out=out)  # noqa: E731
     gemv_batch_ms = event_time_batch(torch, gemv, n_ev)
-    gemv_pair_ms, gemv_pair_med_ms = event_time_kernel(torch, gemv, n_ev)
     quant_batch_ms = event_time_batch(
         torch, lambda i: G.lib().hip_qmm_quantize_q8_1_planar(
             G._ptr(x), K, 1, K, G._ptr(qs), G._ptr(ds), G._stream()), n_ev)
-    achieved = bytes_alg / (gemv_batch_ms * 1e-3) / 1e9
+    achieved = bytes_alg / (fused_batch_ms * 1e-3) / 1e9
 
     result = {
         "metric": "Q4_K GEMV GB/s (% HBM peak) @14336x4096 b=1; MMQ int8 TOPS @b=512",
@@ -313,16 +317,18 @@ def main():
         "dtype": "int8 dot products, fp32 epilogue (Q4_K weights x Q8_1 activations)",
         "data": "synthetic: random valid Q4_K blocks (f16 d/dmin at N(0,0.02) scale), N(0,1) f32 activations",
         "config": {"workload": "Llama-3-8B ffn_gate/up Q4_K decode GEMV (config 1)", "rows": M, "K": K,
-                   "batch": 1, "weight_copies": ncopy, "step": "quantize_q8_1 + GEMV, HIP-graph replay"},
+                   "batch": 1, "weight_copies": ncopy,
+                   "step": "mul_mat: GEMV with the Q8_1 quantization fused (one kernel), HIP-graph replay"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated (profiles/)",
                      "algorithmic_bytes": bytes_alg,
-                     "kernel": "gemv_kernel<Q4_K,NC=1>", "avg_us": round(gemv_batch_ms * 1e3, 3),
+                     "kernel": "gemv_fused_kernel<Q4_K> (quantize-in-GEMV)", "avg_us": round(fused_batch_ms * 1e3, 3),
                      "timing": f"HIP graph of {n_ev} launches between HIP events, weights rotated over {ncopy} copies",
-                     "event_pair_avg_us": round(gemv_pair_ms * 1e3, 3),
-                     "event_pair_median_us": round(gemv_pair_med_ms * 1e3, 3),
-                     "quantize_avg_us": round(quant_batch_ms * 1e3, 3)},
+                     "event_pair_avg_us": round(fused_pair_ms * 1e3, 3),
+                     "event_pair_median_us": round(fused_pair_med_ms * 1e3, 3),
+                     "unfused_gemv_avg_us": round(gemv_batch_ms * 1e3, 3),
+                     "unfused_quantize_avg_us": round(quant_batch_ms * 1e3, 3)},
     }
 
     if not args.no_mmq:

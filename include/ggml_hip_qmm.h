@@ -81,6 +81,18 @@ int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64
                         int64_t dst_col_stride, void *stream);
 
 /*
+ * Decode GEMV of one f32 activation column with the Q8_1 quantization fused
+ * in: dst[r] = sum_k W[r,k] * q8_1(x)[k], bit-identical to
+ * hip_qmm_quantize_q8_1_planar followed by hip_qmm_mul_mat_vec on one column
+ * (two-rows-per-wave kernel).  x 16-byte aligned, K a multiple of 32 and at
+ * most 4096 (2048 for Q8_0).  The MMVQ path of mmvq.zig:275-300 with the
+ * quantizer launch of mmvq.zig:633-643 folded in (the quantize-in-GEMV
+ * prologue of the fusion arguments, mmvq.zig:552-622).
+ */
+int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                            const float *x, float *dst, void *stream);
+
+/*
  * Small-batch GEMV on int8 MFMA, 1..16 columns, K a multiple of 256: 16 rows
  * per workgroup contracted against all columns at once (v_mfma_i32_16x16x32_i8),
  * same arguments and result as hip_qmm_mul_mat_vec.  The MMVQ path of

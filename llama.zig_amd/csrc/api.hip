@@ -37,6 +37,10 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     if (ncols <= 0 || !workspace || !x || !dst) return (int)hipErrorInvalidValue;
     if (workspace_size < hip_qmm_mul_mat_workspace_size(type, K, nrows, ncols)) return (int)hipErrorInvalidValue;
     if ((uintptr_t)workspace % 16) return (int)hipErrorInvalidValue;
+    // one column on a large matrix: the quantization runs inside the GEMV
+    if (ncols == 1 && nrows >= 4096 && K <= (type == TYPE_Q8_0 ? 2048 : 4096) && K % QK8 == 0 &&
+        (uintptr_t)x % 16 == 0)
+        return hip_qmm_mul_mat_vec_f32(type, w, K, nrows, row_stride, x, dst, stream);
     const int64_t Kp = pad_k(K);
     int8_t *qs = (int8_t *)workspace;
     void *ds = (uint8_t *)workspace + ncols * Kp;

@@ -452,6 +452,77 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
     }
 }
 
+// Decode GEMV of one f32 column with the Q8_1 quantization fused in (the
+// quantize-in-GEMV prologue of mmvq.zig:552-622's fusion arguments).  Each
+// workgroup issues its activation loads, then its rows' weight loads,
+// quantizes the whole column into LDS with the same per-quad code as the
+// standalone quantizer (so the Q8_1 bytes are identical) while the weights
+// are in flight, and then runs the two-rows-per-wave arithmetic against LDS.
+// One
+// K-step per lane: K <= 64 * W.  FW waves per workgroup: 8 (512 threads, one
+// 8-value quad slice each), or 16 on large matrices, where half as many
+// workgroups repeat the quantization (measured 8.5 vs 8.9 us at 14336 rows,
+// but 5.4 vs 4.2 us at 4096 rows, whose 128 workgroups are too few).
+constexpr int FUSED_MAXK = 4096;
+
+template <int TYPE, int FW>
+__global__ __launch_bounds__(64 * FW) void gemv_fused_kernel(const uint8_t *__restrict__ w, int64_t K,
+                                                                      int64_t nrows, int64_t row_stride,
+                                                                      const float *x, float *__restrict__ dst) {
+    using F = Fmt<TYPE>;
+    constexpr int RPW = 2;
+    static_assert(FUSED_MAXK <= 8 * 64 * FW, "one activation pass: 8 values per thread");
+    __shared__ alignas(16) int8_t aq[FUSED_MAXK];
+    __shared__ alignas(16) uint32_t ad[FUSED_MAXK / QK8];
+    const int K32 = (int)K;
+    // The activation loads go out first: loads complete in issue order, so
+    // the quantization then waits only for them while the weights stay in
+    // flight.  K % 32 == 0, so the 4 lanes of a quad (one 32-block) are all
+    // in or all out.  Unconditional loads (a valid address past K): with no
+    // branch around them the wait counts only the loads before it.
+    const int kq = 8 * (int)threadIdx.x;
+    const int kqc = kq < K32 ? kq : 0;
+    const float4 xa = *reinterpret_cast<const float4 *>(x + kqc);
+    const float4 xb = *reinterpret_cast<const float4 *>(x + kqc + 4);
+    asm volatile("" ::: "memory");  // keep them ahead of the weight loads
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * RPW;
+    const int kl = lane * F::W;
+    const bool live = kl < K32;
+    const int klc = live ? kl : 0;  // lanes past K load a valid slice and add nothing
+    Wt<TYPE> wt[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) wt[r].load(w + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride, klc);
+    if (kq < K32) {
+        const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const Q8Quad q = q8_1_quantize_quad(v);
+        *reinterpret_cast<uint2 *>(aq + kq) = make_uint2(q.lo, q.hi);
+        if ((threadIdx.x & 3) == 0) ad[kq / QK8] = q.ds;
+    }
+    __syncthreads();
+    if (row0 >= nrows) return;  // uniform per wave, after the workgroup's last barrier
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+    {
+        Act<TYPE> a;
+        a.load(aq, ad, klc);
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            int S[F::NSUB];
+            wt[r].dots(a, S);
+            const float v = wt[r].combine(a, S, klc);
+            acc[r] += live ? v : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const float v = wave_sum(acc[r]);
+        if (lane == r && row0 + r < nrows) dst[row0 + r] = v;
+    }
+}
+
 template <int TYPE, int NC, int R, int D>
 int launch_rows(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                 const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
@@ -619,4 +690,33 @@ extern "C" int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nr
                                   const int8_t *y_qs, int64_t ncols, int32_t *out, void *stream) {
     // The Q8_1 scales are not read in this mode; pass the qs plane for both.
     return dispatch<1>(type, w, K, nrows, row_stride, y_qs, y_qs, ncols, nullptr, 0, out, stream);
+}
+
+// One f32 activation column, quantized to Q8_1 inside the GEMV (no separate
+// quantizer launch, no Q8_1 copy in memory).  Same result as
+// hip_qmm_quantize_q8_1_planar followed by hip_qmm_mul_mat_vec with one
+// column on the two-rows-per-wave kernel.
+extern "C" int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                       const float *x, float *dst, void *stream) {
+    if (int e = check_shape(type, K, nrows, row_stride)) return e;
+    if (!w || !x || !dst || K % QK8 != 0 || (uintptr_t)x % 16) return (int)hipErrorInvalidValue;
+    if (K > (type == TYPE_Q8_0 ? 64 * Fmt<TYPE_Q8_0>::W : FUSED_MAXK)) return (int)hipErrorInvalidValue;
+    if (type == TYPE_Q4_K ? ((uintptr_t)w % 16) : ((uintptr_t)w % 2)) return (int)hipErrorInvalidValue;
+    const int fw = nrows >= 8192 ? 16 : 8;
+    const int64_t rows_per_block = 2 * fw;
+    const int64_t nblocks = (nrows + rows_per_block - 1) / rows_per_block;
+    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *wb = (const uint8_t *)w;
+    const dim3 grid((unsigned)nblocks), block(64 * fw);
+#define FUSED_LAUNCH(T)                                                                                              \
+    if (fw == 16) hipLaunchKernelGGL((gemv_fused_kernel<T, 16>), grid, block, 0, s, wb, K, nrows, row_stride, x, dst); \
+    else hipLaunchKernelGGL((gemv_fused_kernel<T, 8>), grid, block, 0, s, wb, K, nrows, row_stride, x, dst)
+    switch (type) {
+    case TYPE_Q4_K: FUSED_LAUNCH(TYPE_Q4_K); break;
+    case TYPE_Q6_K: FUSED_LAUNCH(TYPE_Q6_K); break;
+    default: FUSED_LAUNCH(TYPE_Q8_0); break;
+    }
+#undef FUSED_LAUNCH
+    return (int)hipGetLastError();
 }

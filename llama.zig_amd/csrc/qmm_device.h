@@ -114,6 +114,51 @@ __device__ __forceinline__ uint32_t q8_1_pack_ds(float d, int sum) {
     return hd | (hs << 16);
 }
 
+// Lane values of the quad partner (lane ^ 1, lane ^ 2): DPP quad_perm
+// [1,0,3,2] and [2,3,0,1].
+__device__ __forceinline__ float quad_x1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float quad_x2(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ int quad_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
+__device__ __forceinline__ int quad_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
+
+// One Q8_1 block held by the 4 lanes of a quad, 8 consecutive values per lane
+// (quantize_row_q8_1_ref, src/ggml/quants/legacy.zig:451-484): amax and the
+// code sum take two DPP exchanges each; the max and the integer sum do not
+// depend on the order, so the bytes equal a one-value-per-lane quantizer's.
+// lo / hi pack this lane's 8 codes; ds is the block header (every lane).  All
+// 4 lanes of the quad must be active.
+struct Q8Quad {
+    uint32_t lo, hi, ds;
+};
+__device__ __forceinline__ Q8Quad q8_1_quantize_quad(const float v[8]) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, quad_x1(amax));
+    amax = fmaxf(amax, quad_x2(amax));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    Q8Quad r;
+    r.lo = 0;
+    r.hi = 0;
+    int sum = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int8_t q = q8_1_code(v[i], id);
+        sum += q;
+        if (i < 4) r.lo |= (uint32_t)(uint8_t)q << (8 * i);
+        else r.hi |= (uint32_t)(uint8_t)q << (8 * (i - 4));
+    }
+    sum += quad_x1(sum);
+    sum += quad_x2(sum);
+    r.ds = q8_1_pack_ds(d, sum);
+    return r;
+}
+
 // Sum over the 64 lanes of a wavefront with DPP: an inclusive prefix sum
 // inside each row of 16 lanes (row_shr 1, 2, 4, 8), then row_bcast:15 and
 // row_bcast:31 carry the row totals forward, leaving the total in lane 63,

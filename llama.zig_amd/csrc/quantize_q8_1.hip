@@ -64,17 +64,6 @@ __global__ __launch_bounds__(256) void quantize_q8_1_planar(const float *__restr
     if ((k & 31) == 0) ds[c * (Kp / QK8) + k / QK8] = q8_1_pack_ds(v.d, v.sum);
 }
 
-// Lane values of the quad partner (lane ^ 1, lane ^ 2): DPP quad_perm
-// [1,0,3,2] and [2,3,0,1].
-__device__ __forceinline__ float quad_x1(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, false));
-}
-__device__ __forceinline__ float quad_x2(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, false));
-}
-__device__ __forceinline__ int quad_x1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false); }
-__device__ __forceinline__ int quad_x2(int v) { return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false); }
-
 // Planar output, 8 consecutive values per lane: a 32-block is the 4 lanes of
 // one quad, so amax and sum(q) take two DPP exchanges instead of five
 // shuffles, and x is read with 16-byte loads.  The max and the integer sum do
@@ -97,26 +86,9 @@ __global__ __launch_bounds__(256) void quantize_q8_1_planar8(const float *__rest
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    float amax = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, quad_x1(amax));
-    amax = fmaxf(amax, quad_x2(amax));
-    const float d = amax / 127.0f;
-    const float id = d != 0.0f ? 1.0f / d : 0.0f;
-    uint32_t lo = 0, hi = 0;
-    int sum = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int8_t q = q8_1_code(v[i], id);
-        sum += q;
-        if (i < 4) lo |= (uint32_t)(uint8_t)q << (8 * i);
-        else hi |= (uint32_t)(uint8_t)q << (8 * (i - 4));
-    }
-    sum += quad_x1(sum);
-    sum += quad_x2(sum);
-    *reinterpret_cast<uint2 *>(qs + c * Kp + k) = make_uint2(lo, hi);
-    if ((threadIdx.x & 3) == 0) ds[c * (Kp / QK8) + k / QK8] = q8_1_pack_ds(d, sum);
+    const Q8Quad r = q8_1_quantize_quad(v);
+    *reinterpret_cast<uint2 *>(qs + c * Kp + k) = make_uint2(r.lo, r.hi);
+    if ((threadIdx.x & 3) == 0) ds[c * (Kp / QK8) + k / QK8] = r.ds;
 }
 
 }  // namespace

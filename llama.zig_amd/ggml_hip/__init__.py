@@ -49,6 +49,8 @@ def lib():
         L.hip_qmm_mul_mat_vec.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_gemv_mfma.restype = i32
         L.hip_qmm_gemv_mfma.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
+        L.hip_qmm_mul_mat_vec_f32.restype = i32
+        L.hip_qmm_mul_mat_vec_f32.argtypes = [i32, vp, i64, i64, i64, vp, vp, vp]
         L.hip_qmm_mmq.restype = i32
         L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mmq_workspace_size.restype = ctypes.c_size_t
@@ -139,6 +141,19 @@ def mul_mat_vec(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tens
     out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
     _check(lib().hip_qmm_mul_mat_vec(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0),
                                      _stream()), "hip_qmm_mul_mat_vec")
+    return out
+
+
+def mul_mat_vec_f32(qtype, w: torch.Tensor, K: int, x: torch.Tensor, out=None):
+    """GEMV of one f32 column [1, K] with the Q8_1 quantization fused into the kernel."""
+    _require_cuda(x)
+    t, nrows, rs = _weight_args(qtype, w, K)
+    x = x.reshape(-1)
+    if x.numel() != K or not x.is_contiguous():
+        raise ValueError("x must be one contiguous column of K values")
+    out = torch.empty((1, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_vec_f32(t, _ptr(w), K, nrows, rs, _ptr(x), _ptr(out), _stream()),
+           "hip_qmm_mul_mat_vec_f32")
     return out
 
 

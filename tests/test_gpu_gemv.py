@@ -75,6 +75,28 @@ def test_gemv_kernel_paths(tname, nrows, K, ncols):
     assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {max_rel(got, cpu):.3g}"
 
 
+@pytest.mark.parametrize("tname,nrows,K", [("Q4_K", 4096, 4096), ("Q4_K", 5000, 1024), ("Q6_K", 4100, 4096),
+                                           ("Q8_0", 4096, 2048), ("Q8_0", 333, 96)])
+def test_gemv_fused_quantize(tname, nrows, K):
+    """Quantize-in-GEMV for one column: bit-identical to the separate Q8_1
+    quantizer followed by the two-rows-per-wave GEMV (which the unfused path
+    takes for one column on >= 4096 rows), and within the gates of the CPU
+    path."""
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, 1)
+    fused = G.mul_mat_vec_f32(tname, w_d, K, x_d[0]).cpu().numpy()
+    if nrows >= 4096:
+        np.testing.assert_array_equal(fused, got)
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, 1)
+    assert max_err_scaled(fused, ideal) < F64_TOL, max_err_scaled(fused, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    assert nmse(fused, cpu) < NMSE_GATE
+    # the op-level entry point takes the fused kernel for this shape
+    op = G.mul_mat(tname, w_d, x_d).cpu().numpy()
+    np.testing.assert_array_equal(op.reshape(fused.shape), fused)
+
+
 def test_gemv_config0_op_level():
     """Config 0: 4096x4096 Q4_K (seed 42) times a 4096x1 activation through the
     op-level entry point, against the CPU ggml path."""
