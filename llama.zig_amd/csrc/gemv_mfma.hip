@@ -52,14 +52,11 @@ constexpr int WAVES = 8;
 constexpr int ROWS = 16;  // rows per workgroup (one MFMA tile)
 constexpr int MAXCOLS = 16; // columns per MFMA tile
 
-// 8 bytes at a 2-byte-aligned address without touching bytes outside
-// [p, p+8): two dwords from the dword below p and a 16-bit tail.
+// 8 bytes at a 2-byte-aligned address: one global_load_dwordx2 (see ld16_u).
 __device__ __forceinline__ uint2 ld8_a2(const uint8_t *p) {
-    const uint32_t sh = (uint32_t)((uintptr_t)p & 2u);
-    const uint8_t *base = p - sh;
-    const uint32_t a0 = ld_u32(base), a1 = ld_u32(base + 4);
-    const uint32_t t = ld_u16(p + 6);
-    return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(t, a1, sh));
+    uint2 r;
+    __builtin_memcpy(&r, __builtin_assume_aligned(p, 2), 8);
+    return r;
 }
 
 __device__ __forceinline__ long as_long(uint2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }

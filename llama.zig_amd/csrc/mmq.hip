@@ -111,11 +111,11 @@ struct AReg<TYPE_Q6_K> {
     __device__ __forceinline__ void load(const uint8_t *blk, int n) {
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            l0[hh] = ld16_a2(blk + 64 * n + 16 * hh);
-            l1[hh] = ld16_a2(blk + 64 * n + 32 + 16 * hh);
-            qh[hh] = ld16_a2(blk + 128 + 32 * n + 16 * hh);
+            l0[hh] = ld16_u(blk + 64 * n + 16 * hh);
+            l1[hh] = ld16_u(blk + 64 * n + 32 + 16 * hh);
+            qh[hh] = ld16_u(blk + 128 + 32 * n + 16 * hh);
         }
-        sc = ld16_a2(blk + 192);
+        sc = ld16_u(blk + 192);
         d = ld_u16(blk + 208);
     }
     __device__ __forceinline__ void zero() {
@@ -136,8 +136,8 @@ struct AReg<TYPE_Q8_0> {
         for (int b = 0; b < 4; ++b) {
             const uint8_t *blk = blk0 + b * Q80_BYTES;
             d[b] = ld_u16(blk);
-            q[b][0] = ld16_a2(blk + 2);
-            q[b][1] = ld16_a2(blk + 18);
+            q[b][0] = ld16_u(blk + 2);
+            q[b][1] = ld16_u(blk + 18);
         }
     }
     __device__ __forceinline__ void zero() {

@@ -4,8 +4,10 @@
 // (src/ggml/quants/blocks.zig:67-222): block_q4_K {d, dmin, scales[12],
 // qs[128]} 144 B; block_q6_K {ql[128], qh[64], scales[16], d} 210 B;
 // block_q8_0 {d, qs[32]} 34 B.  Q6_K and Q8_0 blocks sit at 2-byte alignment
-// inside a row, so they are read with dword-aligned loads plus a byte funnel
-// shift (v_alignbyte_b32); nothing here relies on unaligned memory access.
+// inside a row.  The GEMV kernels read them with dword-aligned loads plus a
+// byte funnel shift (v_alignbyte_b32, ld16_a2); the MMQ staging loads use one
+// unaligned vector load (ld16_u), which measured faster there.  Neither reads
+// outside the block.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -49,6 +51,17 @@ __device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
     r.y = __builtin_amdgcn_alignbyte(a2, a1, sh);
     r.z = __builtin_amdgcn_alignbyte(a3, a2, sh);
     r.w = __builtin_amdgcn_alignbyte(t, a3, sh);
+    return r;
+}
+
+// The same 16 bytes with one instruction: a memcpy from a pointer known to be
+// 2-byte aligned compiles to a single global_load_dwordx4 (global memory
+// accepts unaligned vector loads on gfx950).  It reads exactly [p, p+16).
+// Measured faster for the MMQ's Q6_K staging loads, slower for the GEMV's
+// Q8_0 loads (where the aligned dwords above stay).
+__device__ __forceinline__ uint4 ld16_u(const uint8_t *p) {
+    uint4 r;
+    __builtin_memcpy(&r, __builtin_assume_aligned(p, 2), 16);
     return r;
 }
 
