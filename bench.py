@@ -216,6 +216,49 @@ def run_suite(name, torch, G, dev, reps):
                   "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2)})
             del ws
             torch.cuda.empty_cache()
+    elif name == "ffn":
+        # Decode FFN gate + up + SWIGLU on one f32 column: the fused kernel
+        # (hip_qmm_mul_mat_vec_fused with a gate) against the unfused
+        # sequence it replaces (two one-column quantizing GEMVs and the GLU
+        # kernel), and the bias lane (GEMV + bias) against the plain GEMV.
+        for M, Kx, label in ((14336, 4096, "llama3-8b ffn_gate/up"), (768, 2048, "qwen3-30b-a3b expert gate/up")):
+            wb = M * row_bytes("Q4_K", Kx)
+            n = max(3, -(-2 * INFINITY_CACHE // (2 * wb)))
+            wu = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+            wg = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+            x = torch.randn((1, Kx), generator=xg, dtype=torch.float32).to(dev)
+            bias = torch.randn((M,), generator=xg, dtype=torch.float32).to(dev)
+            u = torch.empty((1, M), dtype=torch.float32, device=dev)
+            g = torch.empty((1, M), dtype=torch.float32, device=dev)
+            out = torch.empty((1, M), dtype=torch.float32, device=dev)
+            reps_n = n * reps
+
+            def fused(i):
+                G.mul_mat_vec_fused("Q4_K", wu[i % n], Kx, x, w_gate=wg[i % n], glu="SWIGLU", out=out)
+
+            def unfused(i):
+                G.mul_mat_vec_f32("Q4_K", wu[i % n], Kx, x, out=u)
+                G.mul_mat_vec_f32("Q4_K", wg[i % n], Kx, x, out=g)
+                G.glu_f32(g, u, "SWIGLU", out=out)
+
+            def lane_bias(i):
+                G.mul_mat_vec_fused("Q4_K", wu[i % n], Kx, x, bias=bias, out=out)
+
+            def lane_plain(i):
+                G.mul_mat_vec_f32("Q4_K", wu[i % n], Kx, x, out=out)
+
+            alg2 = 2 * wb + Kx * 4 + M * 4
+            alg1 = wb + Kx * 4 + M * 4
+            for kern, fn, alg in (("gate+up+swiglu fused", fused, alg2), ("gate+up+swiglu unfused (3 launches)",
+                                                                         unfused, alg2),
+                                  ("gemv+bias fused", lane_bias, alg1 + M * 4), ("gemv (one column)", lane_plain,
+                                                                                  alg1)):
+                ms = event_time_batch(torch, fn, reps_n)
+                emit({"suite": name, "kernel": kern, "type": "Q4_K", "shape": f"{M}x{Kx}", "label": label, "T": 1,
+                      "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
+                      "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4)})
+            del wu, wg
+            torch.cuda.empty_cache()
     else:
         raise SystemExit(f"unknown suite {name}")
 
@@ -227,7 +270,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
-    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe"],
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()

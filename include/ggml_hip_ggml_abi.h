@@ -12,13 +12,14 @@
  *     op, op_params, flags, src, view_src, view_offs, data, name, extra) with
  *     the trailing 8-byte `padding` member src/ggml/backend_meta.zig:3221-3222
  *     checks;
- *   - ggml_cgraph: src/ggml/impl.zig:469-485 (the reference's own extern
- *     declaration);
+ *   - ggml_cgraph and ggml_hash_set: src/ggml/impl.zig:422-435, 469-485
+ *     (the reference's own extern declarations);
  *   - vtable members: in the order the CUDA backend initialises them
  *     (src/ggml/cuda/backend.zig:250-265 buffer, :343-352 buffer type,
  *     :714-731 backend, :1032-1048 device, :1141-1146 registry);
  *   - enum ggml_op values: the position of each name in op_name
- *     (src/ggml/types.zig:25-48).
+ *     (src/ggml/types.zig:25-51); ggml_glu_op values likewise from
+ *     glu_op_name (types.zig:103-106), read from op_params[0].
  * Numeric ggml_type ids follow ggml.h (GGML_TYPE_Q8_0 = 8, Q4_K = 12, Q6_K =
  * 14, I32 = 26); the kernel-level ABI (ggml_hip_qmm.h) uses the same ids.
  *
@@ -61,13 +62,19 @@ enum ggml_type {
 
 enum ggml_op {
     GGML_OP_NONE = 0,
+    GGML_OP_ADD = 2,
     GGML_OP_MUL_MAT = 28,
     GGML_OP_MUL_MAT_ID = 29,
     GGML_OP_RESHAPE = 35,
     GGML_OP_VIEW = 36,
     GGML_OP_PERMUTE = 37,
     GGML_OP_TRANSPOSE = 38,
+    GGML_OP_GLU = 98,
 };
+
+/* ggml_tensor.flags bit a graph output carries (the scheduler and the
+ * allocator keep such a tensor alive: src/ggml/alloc.zig:635-637, 684) */
+#define GGML_TENSOR_FLAG_OUTPUT 2
 
 enum ggml_status {
     GGML_STATUS_ALLOC_FAILED = -2,
@@ -122,7 +129,19 @@ struct ggml_tensor {
     char padding[8];
 };
 
-/* only the members before visited_hash_set are read */
+/* ggml_hash_set (src/ggml/impl.zig:422-435): open addressing over tensor
+ * pointers, slot of p = (p >> 4) % size with linear probing
+ * (impl.zig:509-557), occupancy in a bitset of 32-bit words. */
+struct ggml_hash_set {
+    size_t size;
+    uint32_t *used;
+    struct ggml_tensor **keys;
+};
+
+/* Members up to visited_hash_set are read: use_counts[slot] is the number of
+ * times the tensor in that slot is a source of a graph node
+ * (src/ggml/graph.zig:1262-1268).  A graph view shares both with its parent
+ * graph (graph.zig:252-266), so the counts include uses outside the view. */
 struct ggml_cgraph {
     int size;
     int n_nodes;
@@ -132,6 +151,8 @@ struct ggml_cgraph {
     struct ggml_tensor **grad_accs;
     struct ggml_tensor **leafs;
     int32_t *use_counts;
+    struct ggml_hash_set visited_hash_set;
+    int order;
 };
 
 struct ggml_backend_buffer_type_i {

@@ -92,6 +92,53 @@ int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64
 int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                             const float *x, float *dst, void *stream);
 
+/* ggml_glu_op values (positions in GGML_GLU_OP_NAME, src/ggml/types.zig:103-106)
+ * the fused and standalone GLU entry points accept. */
+#define HIP_QMM_GLU_REGLU 0
+#define HIP_QMM_GLU_GEGLU 1
+#define HIP_QMM_GLU_SWIGLU 2
+#define HIP_QMM_GLU_SWIGLU_OAI 3
+#define HIP_QMM_GLU_SWIGLU_CLAMP 6
+
+/*
+ * One f32 activation column through the Q8_1-quantizing GEMV with the
+ * reference's mul_mat_vec fusion epilogue (ggml_cuda_mm_fusion_args_device,
+ * src/ggml/cuda/common.zig:1448-1459, applied by mulMatVecQ at
+ * src/ggml/cuda/mmvq.zig:571-622; the graph patterns that reach it are
+ * src/ggml/cuda/fusion.zig:1308-1390 and 1482-1520):
+ *   u[r] = sum_k W[r,k] * q8_1(x)[k]  (+ bias[r] when bias != NULL)
+ *   w_gate == NULL:  dst[r] = u[r]
+ *   otherwise:       g[r] = sum_k Wg[r,k] * q8_1(x)[k] (+ gate_bias[r]),
+ *                    dst[r] = glu(glu_op, g[r], u[r])
+ * glu is the CPU op (src/ggml/cpu/ops/activation.zig:434-556): REGLU, GEGLU
+ * (f16-table gelu), SWIGLU, SWIGLU_OAI (alpha = op param 2, limit = op param
+ * 3) or SWIGLU_CLAMP (limit).  W and Wg share type, shape and row stride.
+ * u and g equal hip_qmm_mul_mat_vec_f32's output bit for bit.  K a multiple
+ * of the block size and of 32, at most 32768; x 16-byte aligned.  No
+ * workspace.  hipErrorInvalidValue for anything else.
+ */
+int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                              int64_t row_stride, const float *x, const float *bias, const float *gate_bias,
+                              int glu_op, float glu_alpha, float glu_limit, float *dst, void *stream);
+
+/*
+ * Standalone GLU over rows of f32 (ggml_compute_forward_glu,
+ * src/ggml/cpu/ops/activation.zig:594-608, per element as above):
+ * dst[r*dst_stride + i] = glu(op, gate[r*gate_stride + i], up[r*up_stride + i])
+ * for i < nc, r < nrows; strides in floats.
+ */
+int hip_qmm_glu_f32(int glu_op, float alpha, float limit, int64_t nc, int64_t nrows, const float *gate,
+                    int64_t gate_stride, const float *up, int64_t up_stride, float *dst, int64_t dst_stride,
+                    void *stream);
+
+/*
+ * Elementwise f32 add of two same-shape row sets (ggml_add without
+ * broadcasting, the bias add the fused GEMV epilogue replaces):
+ * dst[r*dst_stride + i] = a[r*a_stride + i] + b[r*b_stride + i].
+ */
+int hip_qmm_add_f32(int64_t nc, int64_t nrows, const float *a, int64_t a_stride, const float *b, int64_t b_stride,
+                    float *dst, int64_t dst_stride, void *stream);
+
 /*
  * Small-batch GEMV on int8 MFMA, 1..16 columns, K a multiple of 256: 16 rows
  * per workgroup contracted against all columns at once (v_mfma_i32_16x16x32_i8),

@@ -519,6 +519,226 @@ bool is_noop(int op) {
            op == GGML_OP_TRANSPOSE;
 }
 
+// ---------------------------------------------------------------- GLU and ADD nodes
+
+float op_param_f32(const ggml_tensor *t, int i) {
+    float f;
+    std::memcpy(&f, &t->op_params[i], sizeof f);
+    return f;
+}
+
+// GLU ops with a device implementation (glu_apply): REGLU, GEGLU, SWIGLU,
+// SWIGLU_OAI, SWIGLU_CLAMP.  GEGLU_ERF and GEGLU_QUICK stay on the CPU.
+bool glu_op_supported(int op) {
+    return op == HIP_QMM_GLU_REGLU || op == HIP_QMM_GLU_GEGLU || op == HIP_QMM_GLU_SWIGLU ||
+           op == HIP_QMM_GLU_SWIGLU_OAI || op == HIP_QMM_GLU_SWIGLU_CLAMP;
+}
+
+bool same_shape(const ggml_tensor *a, const ggml_tensor *b) {
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (a->ne[i] != b->ne[i]) return false;
+    return true;
+}
+
+bool f32_rows(const ggml_tensor *t) {
+    return t->type == GGML_TYPE_F32 && t->nb[0] == 4 && t->nb[1] % 4 == 0 && t->nb[2] % 4 == 0 && t->nb[3] % 4 == 0;
+}
+
+// dst = glu(gate, value) row by row (ggml_compute_forward_glu,
+// src/ggml/cpu/ops/activation.zig:594-608).  Split form: src0 gates, src1 is
+// the value.  One tensor: the halves of each src0 row, the first gating
+// unless op_params[1] (swapped) is set (GluRows.halves, activation.zig:365-376).
+bool run_glu(BackendCtx *ctx, const ggml_tensor *node) {
+    const ggml_tensor *a = node->src[0], *b = node->src[1];
+    const int64_t nc = node->ne[0];
+    const ggml_tensor *gt = a, *ut = b ? b : a;
+    size_t goff = 0, uoff = 0;
+    if (!b) (node->op_params[1] ? goff : uoff) = (size_t)nc * 4;
+    for (int64_t i3 = 0; i3 < node->ne[3]; ++i3)
+        for (int64_t i2 = 0; i2 < node->ne[2]; ++i2) {
+            const float *g = reinterpret_cast<const float *>(at(gt->data, i2 * gt->nb[2] + i3 * gt->nb[3] + goff));
+            const float *u = reinterpret_cast<const float *>(at(ut->data, i2 * ut->nb[2] + i3 * ut->nb[3] + uoff));
+            float *d = reinterpret_cast<float *>(at(node->data, i2 * node->nb[2] + i3 * node->nb[3]));
+            const int rc = hip_qmm_glu_f32(node->op_params[0], op_param_f32(node, 2), op_param_f32(node, 3), nc,
+                                           node->ne[1], g, (int64_t)(gt->nb[1] / 4), u, (int64_t)(ut->nb[1] / 4), d,
+                                           (int64_t)(node->nb[1] / 4), ctx->stream);
+            if (!report(rc, "hip_qmm_glu_f32", node)) return false;
+        }
+    return true;
+}
+
+// dst = src0 + src1, all of one shape (ggml_add without broadcasting).
+bool run_add(BackendCtx *ctx, const ggml_tensor *node) {
+    const ggml_tensor *a = node->src[0], *b = node->src[1];
+    for (int64_t i3 = 0; i3 < node->ne[3]; ++i3)
+        for (int64_t i2 = 0; i2 < node->ne[2]; ++i2) {
+            const float *pa = reinterpret_cast<const float *>(at(a->data, i2 * a->nb[2] + i3 * a->nb[3]));
+            const float *pb = reinterpret_cast<const float *>(at(b->data, i2 * b->nb[2] + i3 * b->nb[3]));
+            float *d = reinterpret_cast<float *>(at(node->data, i2 * node->nb[2] + i3 * node->nb[3]));
+            const int rc = hip_qmm_add_f32(node->ne[0], node->ne[1], pa, (int64_t)(a->nb[1] / 4), pb,
+                                           (int64_t)(b->nb[1] / 4), d, (int64_t)(node->nb[1] / 4), ctx->stream);
+            if (!report(rc, "hip_qmm_add_f32", node)) return false;
+        }
+    return true;
+}
+
+// ---------------------------------------------------------------- fusion
+//
+// The mul_mat_vec fusions of the reference's CUDA backend
+// (ggml_cuda_try_fuse, src/ggml/cuda/fusion.zig:1153-1390, 1482-1520), for
+// one activation column:
+//   {MUL_MAT, MUL_MAT, GLU}            gate and up GEMVs + GLU, one kernel
+//   {MUL_MAT, ADD, MUL_MAT, ADD, GLU}  the same with a bias on each lane
+//   {MUL_MAT, ADD}                     GEMV + bias
+// A run fuses only when every node in it but the last is read only inside
+// the run and is not a graph output (ggml_can_fuse_subgraph_ext,
+// src/ggml/graph.zig:1207-1250), with use counts from the graph's hash set.
+// Graphs without use counts, and GGML_HIP_DISABLE_FUSION=1, run unfused.
+
+bool fusion_disabled() {
+    static const bool off = [] {
+        const char *e = std::getenv("GGML_HIP_DISABLE_FUSION");
+        return e && *e && std::strcmp(e, "0") != 0;
+    }();
+    return off;
+}
+
+// ggml_node_get_use_count (src/ggml/graph.zig:1262-1268) through the hash
+// lookup of impl.zig:549-557; -1 when the graph carries no use counts.
+int use_count(const ggml_cgraph *g, const ggml_tensor *t) {
+    const ggml_hash_set &h = g->visited_hash_set;
+    if (!g->use_counts || !h.size || !h.used || !h.keys) return -1;
+    auto used = [&](size_t i) { return (h.used[i >> 5] >> (i & 31)) & 1u; };
+    const size_t start = ((uintptr_t)t >> 4) % h.size;
+    size_t i = start;
+    while (used(i) && h.keys[i] != t) {
+        i = (i + 1) % h.size;
+        if (i == start) return -1;
+    }
+    return used(i) ? g->use_counts[i] : 0;
+}
+
+// Nodes i0 .. i0+n-1 but `out` are read only inside the run, are not graph
+// outputs and are not views.
+bool run_is_closed(const ggml_cgraph *g, int i0, int n, const ggml_tensor *out) {
+    for (int i = i0; i < i0 + n; ++i) {
+        const ggml_tensor *t = g->nodes[i];
+        if (t == out) continue;
+        if ((t->flags & GGML_TENSOR_FLAG_OUTPUT) || t->view_src) return false;
+        int uses = 0;
+        for (int j = i + 1; j < i0 + n; ++j)
+            for (int s = 0; s < GGML_MAX_SRC; ++s) uses += g->nodes[j]->src[s] == t;
+        if (use_count(g, t) != uses) return false;
+    }
+    return true;
+}
+
+bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+    const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
+    return pa < pb + nb && pb < pa + na;
+}
+
+// A supported MUL_MAT the fused one-column entry point takes
+// (ggml_cuda_should_fuse_mul_mat_vec_q, src/ggml/cuda/mulmat.zig:443-462:
+// one destination column, f32 in and out; plus the entry point's limits).
+bool vec_fusable(const ggml_tensor *mm) {
+    const ggml_tensor *w = mm->src[0], *x = mm->src[1];
+    for (int i = 1; i < GGML_MAX_DIMS; ++i)
+        if (x->ne[i] != 1 || mm->ne[i] != 1 || (i > 1 && w->ne[i] != 1)) return false;
+    const int64_t K = w->ne[0];
+    if (K % 32 != 0 || K > 32768 || (uintptr_t)x->data % 16 != 0) return false;
+    const size_t walign = w->type == GGML_TYPE_Q4_K ? 16 : 2;
+    return (uintptr_t)w->data % walign == 0 && w->nb[1] % walign == 0 && mm->nb[0] == 4;
+}
+
+// A bias of a MUL_MAT output: f32, the output's shape, dense.
+bool bias_ok(const ggml_tensor *b, const ggml_tensor *mm) {
+    return b && b->type == GGML_TYPE_F32 && same_shape(b, mm) && b->nb[0] == 4;
+}
+
+// The other operand of an ADD that reads mm (getBiasTensor, fusion.zig:910-919).
+const ggml_tensor *bias_of(const ggml_tensor *add, const ggml_tensor *mm) {
+    if (add->op != GGML_OP_ADD || !same_shape(add->src[0], add->src[1])) return nullptr;
+    if (add->src[0] == mm) return add->src[1];
+    if (add->src[1] == mm) return add->src[0];
+    return nullptr;
+}
+
+// ggml_cuda_should_fuse_mul_mat (src/ggml/cuda/mulmat.zig:355-410) for the
+// one-column kernel: same weight type, shape and strides, the same
+// activation tensor, a split non-swapped GLU of a fused op.
+bool gate_up_fusable(const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *glu) {
+    const ggml_tensor *wu = up->src[0], *wg = gate->src[0];
+    const int op = glu->op_params[0];
+    if (op != HIP_QMM_GLU_GEGLU && op != HIP_QMM_GLU_SWIGLU && op != HIP_QMM_GLU_SWIGLU_OAI &&
+        op != HIP_QMM_GLU_SWIGLU_CLAMP)
+        return false;
+    if (glu->op_params[1] != 0 || !glu->src[1] || glu->type != GGML_TYPE_F32 || glu->nb[0] != 4) return false;
+    if (wu->type != wg->type || !same_shape(wu, wg)) return false;
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (wu->nb[i] != wg->nb[i]) return false;
+    if (up->src[1] != gate->src[1]) return false;
+    return vec_fusable(up) && vec_fusable(gate) && same_shape(glu, up);
+}
+
+bool launch_fused(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *ubias,
+                  const ggml_tensor *gbias, const ggml_tensor *out, bool *ok) {
+    const ggml_tensor *w = up->src[0], *x = up->src[1];
+    const int64_t K = w->ne[0], M = w->ne[1];
+    // the result must not land on an input (checkFusionMemoryRanges, fusion.zig)
+    const size_t ob = (size_t)M * 4;
+    if (overlaps(out->data, ob, x->data, (size_t)K * 4)) return false;
+    if (ubias && overlaps(out->data, ob, ubias->data, ob)) return false;
+    if (gbias && overlaps(out->data, ob, gbias->data, ob)) return false;
+    const int op = gate ? out->op_params[0] : 0;
+    const float alpha = gate ? op_param_f32(out, 2) : 0.0f, limit = gate ? op_param_f32(out, 3) : 0.0f;
+    const int rc = hip_qmm_mul_mat_vec_fused(w->type, w->data, gate ? gate->src[0]->data : nullptr, K, M,
+                                             (int64_t)w->nb[1], static_cast<const float *>(x->data),
+                                             ubias ? static_cast<const float *>(ubias->data) : nullptr,
+                                             gbias ? static_cast<const float *>(gbias->data) : nullptr, op, alpha,
+                                             limit, static_cast<float *>(out->data), ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_vec_fused", out);
+    return true;
+}
+
+// Nodes consumed by a fused launch at node i (0: none); *ok false on a failed launch.
+int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
+    if (fusion_disabled() || g->nodes[i]->op != GGML_OP_MUL_MAT) return 0;
+    auto node = [&](int k) { return k < g->n_nodes ? g->nodes[k] : nullptr; };
+    auto is = [&](int k, int op) { return node(k) && node(k)->op == op && ggml_backend_hip_op_supported(node(k)); };
+    if (is(i + 1, GGML_OP_ADD) && is(i + 2, GGML_OP_MUL_MAT) && is(i + 3, GGML_OP_ADD) && is(i + 4, GGML_OP_GLU)) {
+        const ggml_tensor *glu = node(i + 4);
+        const ggml_tensor *ma = node(i), *aa = node(i + 1), *mb = node(i + 2), *ab = node(i + 3);
+        const ggml_tensor *ba = bias_of(aa, ma), *bb = bias_of(ab, mb);
+        // which lane gates follows from the GLU's sources (fusion.zig:1313-1325)
+        const bool a_gates = glu->src[0] == aa && glu->src[1] == ab;
+        const bool b_gates = glu->src[0] == ab && glu->src[1] == aa;
+        if (bias_ok(ba, ma) && bias_ok(bb, mb) && (a_gates || b_gates)) {
+            const ggml_tensor *gate = a_gates ? ma : mb, *up = a_gates ? mb : ma;
+            const ggml_tensor *gb = a_gates ? ba : bb, *ub = a_gates ? bb : ba;
+            if (gate_up_fusable(up, gate, glu) && run_is_closed(g, i, 5, glu) &&
+                launch_fused(ctx, up, gate, ub, gb, glu, ok))
+                return 5;
+        }
+    }
+    if (is(i + 1, GGML_OP_MUL_MAT) && is(i + 2, GGML_OP_GLU)) {
+        const ggml_tensor *glu = node(i + 2);
+        const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
+        const bool pair = (gate == node(i) && up == node(i + 1)) || (gate == node(i + 1) && up == node(i));
+        if (pair && gate_up_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
+            launch_fused(ctx, up, gate, nullptr, nullptr, glu, ok))
+            return 3;
+    }
+    if (is(i + 1, GGML_OP_ADD)) {
+        const ggml_tensor *mm = node(i), *add = node(i + 1);
+        const ggml_tensor *b = bias_of(add, mm);
+        if (bias_ok(b, mm) && vec_fusable(mm) && same_shape(add, mm) && run_is_closed(g, i, 2, add) &&
+            launch_fused(ctx, mm, nullptr, b, nullptr, add, ok))
+            return 2;
+    }
+    return 0;
+}
+
 ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
     BackendCtx *ctx = be_ctx(be);
     HIP_CHECK(hipSetDevice(ctx->device));
@@ -530,7 +750,18 @@ ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
                          (int)node->op);
             return GGML_STATUS_FAILED;
         }
-        const bool ok = node->op == GGML_OP_MUL_MAT ? run_mul_mat(ctx, node) : run_mul_mat_id(ctx, node);
+        bool ok = true;
+        if (const int n = try_fuse(ctx, g, i, &ok)) {
+            if (!ok) return GGML_STATUS_FAILED;
+            i += n - 1;
+            continue;
+        }
+        switch (node->op) {
+        case GGML_OP_MUL_MAT: ok = run_mul_mat(ctx, node); break;
+        case GGML_OP_MUL_MAT_ID: ok = run_mul_mat_id(ctx, node); break;
+        case GGML_OP_GLU: ok = run_glu(ctx, node); break;
+        default: ok = run_add(ctx, node); break;
+        }
         if (!ok) return GGML_STATUS_FAILED;
     }
     return GGML_STATUS_SUCCESS;
@@ -688,6 +919,21 @@ extern "C" {
 bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
     if (!op) return false;
     if (is_noop(op->op)) return true;
+    if (op->op == GGML_OP_GLU) {
+        // f32 GLU of a device op (glu_op_supported), split or one-tensor form
+        const ggml_tensor *a = op->src[0], *b = op->src[1];
+        if (!a || !f32_rows(a) || !f32_rows(op) || !glu_op_supported(op->op_params[0])) return false;
+        if (b) return f32_rows(b) && same_shape(a, b) && same_shape(op, a);
+        if (a->ne[0] != 2 * op->ne[0]) return false;
+        for (int i = 1; i < GGML_MAX_DIMS; ++i)
+            if (a->ne[i] != op->ne[i]) return false;
+        return true;
+    }
+    if (op->op == GGML_OP_ADD) {
+        // same-shape f32 add (the bias add of the GEMV fusion); no broadcasting
+        const ggml_tensor *a = op->src[0], *b = op->src[1];
+        return a && b && f32_rows(a) && f32_rows(b) && f32_rows(op) && same_shape(a, b) && same_shape(a, op);
+    }
     if (op->op != GGML_OP_MUL_MAT && op->op != GGML_OP_MUL_MAT_ID) return false;
     const ggml_tensor *a = op->src[0], *b = op->src[1];
     if (!a || !b || !weight_type(a->type) || b->type != GGML_TYPE_F32 || op->type != GGML_TYPE_F32) return false;

@@ -523,6 +523,122 @@ __global__ __launch_bounds__(64 * FW) void gemv_fused_kernel(const uint8_t *__re
     }
 }
 
+// One f32 column with the reference's mul_mat_vec fusion epilogue
+// (ggml_cuda_mm_fusion_args_device, src/ggml/cuda/common.zig:1448-1459):
+//   u[r] = W[r] . x (+ bias[r]);  GATE: g[r] = Wg[r] . x (+ gate_bias[r]),
+//   dst[r] = glu(g[r], u[r]);  otherwise dst[r] = u[r].
+// The column is quantized to Q8_1 in the prologue, as in gemv_fused_kernel
+// (identical bytes), into dynamic LDS of K + K/8 bytes; each wave then owns R
+// rows of W (and the same R rows of Wg), one K-step of 64 lanes x W weights
+// at a time; the first step's weights are in flight during the prologue.
+// The dots and their combination are the two-rows-per-wave kernel's, in the
+// same order, so u and g equal that kernel's outputs bit for bit.  Biases are read at the start, from a valid address when absent (the
+// value is then unused), so no load sits behind a branch.
+constexpr int FX_MAXK = 32768;
+
+template <int TYPE, int FW, int R, bool GATE>
+__global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restrict__ w,
+                                                             const uint8_t *__restrict__ wg, int K32, int64_t nrows,
+                                                             int64_t row_stride, const float *x,
+                                                             const float *bias, const float *gbias, int glu_op,
+                                                             float alpha, float limit, float *__restrict__ dst) {
+    using F = Fmt<TYPE>;
+    constexpr int NM = GATE ? 2 : 1;
+    constexpr int CH = 8 * 64 * FW;  // activation values per prologue pass
+    constexpr int STEP = 64 * F::W;
+    extern __shared__ __align__(16) uint8_t fx_lds[];
+    int8_t *aq = reinterpret_cast<int8_t *>(fx_lds);
+    uint32_t *ad = reinterpret_cast<uint32_t *>(fx_lds + K32);  // K32 % 32 == 0
+    // First pass of activation loads, then the biases, then the weights:
+    // loads complete in issue order, so the quantization waits only for the
+    // activations.
+    const int kq = 8 * (int)threadIdx.x;
+    const int kqc = kq < K32 ? kq : 0;
+    const float4 xa = *reinterpret_cast<const float4 *>(x + kqc);
+    const float4 xb = *reinterpret_cast<const float4 *>(x + kqc + 4);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * R;
+    const int64_t brow = row0 + (lane < R ? lane : 0);
+    const int64_t browc = brow < nrows ? brow : nrows - 1;
+    const float bu = *(bias ? bias + browc : x);
+    const float bg = GATE ? *(gbias ? gbias + browc : x) : 0.0f;
+    asm volatile("" ::: "memory");  // keep them ahead of the weight loads
+    const uint8_t *rows[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+            rows[m][r] = (m ? wg : w) + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride;
+    int kl = lane * F::W;
+    bool live = kl < K32;
+    int klc = live ? kl : 0;  // lanes past K load a valid slice and add nothing
+    Wt<TYPE> wt[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) wt[m][r].load(rows[m][r], klc);
+    if (kq < K32) {
+        const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+        const Q8Quad q = q8_1_quantize_quad(v);
+        *reinterpret_cast<uint2 *>(aq + kq) = make_uint2(q.lo, q.hi);
+        if ((threadIdx.x & 3) == 0) ad[kq / QK8] = q.ds;
+    }
+    for (int k = kq + CH; k < K32; k += CH) {  // columns longer than one pass
+        const float4 ya = *reinterpret_cast<const float4 *>(x + k);
+        const float4 yb = *reinterpret_cast<const float4 *>(x + k + 4);
+        const float v[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+        const Q8Quad q = q8_1_quantize_quad(v);
+        *reinterpret_cast<uint2 *>(aq + k) = make_uint2(q.lo, q.hi);
+        if ((threadIdx.x & 3) == 0) ad[k / QK8] = q.ds;
+    }
+    __syncthreads();
+    if (row0 >= nrows) return;  // uniform per wave, after the workgroup's last barrier
+    float acc[NM][R];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[m][r] = 0.0f;
+    auto contract = [&](const Wt<TYPE> (&cur)[NM][R]) {
+        Act<TYPE> a;
+        a.load(aq, ad, klc);
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                int S[F::NSUB];
+                cur[m][r].dots(a, S);
+                const float v = cur[m][r].combine(a, S, klc);
+                acc[m][r] += live ? v : 0.0f;
+            }
+    };
+    contract(wt);
+    // Rows longer than one step: load, then contract.  No prefetch into a
+    // second register set: that would cost the occupancy the single-step
+    // case runs on, and with many waves per SIMD the other waves cover the
+    // latency.
+    for (int k0 = STEP; k0 < K32; k0 += STEP) {
+        kl = k0 + lane * F::W;
+        live = kl < K32;
+        klc = live ? kl : 0;
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < R; ++r) wt[m][r].load(rows[m][r], klc);
+        contract(wt);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float u = wave_sum(acc[0][r]);
+        const float g = GATE ? wave_sum(acc[NM - 1][r]) : 0.0f;
+        if (lane == r && row0 + r < nrows) {
+            if (bias) u += bu;
+            if constexpr (GATE) u = glu_apply(glu_op, gbias ? g + bg : g, u, alpha, limit);
+            dst[row0 + r] = u;
+        }
+    }
+}
+
 template <int TYPE, int NC, int R, int D>
 int launch_rows(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                 const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
@@ -718,5 +834,64 @@ extern "C" int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64
     default: FUSED_LAUNCH(TYPE_Q8_0); break;
     }
 #undef FUSED_LAUNCH
+    return (int)hipGetLastError();
+}
+
+namespace {
+
+template <int TYPE, int FW, int R, bool GATE>
+void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
+               const float *bias, const float *gbias, int op, float alpha, float limit, float *dst, hipStream_t s) {
+    const int64_t nblocks = (nrows + (int64_t)FW * R - 1) / ((int64_t)FW * R);
+    const size_t lds = (size_t)K + (size_t)(K / QK8) * 4;
+    hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE>), dim3((unsigned)nblocks), dim3(64 * FW), lds, s, w, wg,
+                       (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst);
+}
+
+template <int TYPE>
+void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride,
+                    const float *x, const float *bias, const float *gbias, int op, float alpha, float limit,
+                    float *dst, hipStream_t s) {
+    // 16 waves per workgroup on large matrices, 8 otherwise (the plain
+    // fused GEMV's measured choice); the gated form keeps two weight rows
+    // in flight per wave (one of each matrix).
+    const bool big = nrows >= 8192;
+    if (wg) {
+        if (big) launch_fx<TYPE, 16, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        else launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+    } else {
+        if (big) launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        else launch_fx<TYPE, 8, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+    }
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                         int64_t row_stride, const float *x, const float *bias,
+                                         const float *gate_bias, int glu_op, float glu_alpha, float glu_limit,
+                                         float *dst, void *stream) {
+    if (int e = check_shape(type, K, nrows, row_stride)) return e;
+    if (!w || !x || !dst || K % QK8 != 0 || K > FX_MAXK || (uintptr_t)x % 16) return (int)hipErrorInvalidValue;
+    const uintptr_t walign = type == TYPE_Q4_K ? 16 : 2;
+    if ((uintptr_t)w % walign || (uintptr_t)w_gate % walign) return (int)hipErrorInvalidValue;
+    if (!w_gate && gate_bias) return (int)hipErrorInvalidValue;
+    if (w_gate && glu_op != GLU_REGLU && glu_op != GLU_GEGLU && glu_op != GLU_SWIGLU && glu_op != GLU_SWIGLU_OAI &&
+        glu_op != GLU_SWIGLU_CLAMP)
+        return (int)hipErrorInvalidValue;
+    if ((nrows + 7) / 8 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *wb = (const uint8_t *)w, *gb = (const uint8_t *)w_gate;
+    switch (type) {
+    case TYPE_Q4_K:
+        launch_fx_type<TYPE_Q4_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        break;
+    case TYPE_Q6_K:
+        launch_fx_type<TYPE_Q6_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        break;
+    default:
+        launch_fx_type<TYPE_Q8_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        break;
+    }
     return (int)hipGetLastError();
 }

@@ -192,4 +192,44 @@ __device__ __forceinline__ float wave_sum(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
+// ggml_glu_op values: positions in GGML_GLU_OP_NAME (src/ggml/types.zig:103-106).
+enum : int {
+    GLU_REGLU = 0,
+    GLU_GEGLU = 1,
+    GLU_SWIGLU = 2,
+    GLU_SWIGLU_OAI = 3,
+    GLU_SWIGLU_CLAMP = 6,
+};
+
+// out = glu(gate g, value u) for one element, as the CPU ops define it:
+//   REGLU         g > 0 ? g*u : 0                      (vecinline.zig:507-511)
+//   GEGLU         gelu from the f16 table: g rounded to f16, gelu of that,
+//                 rounded to f16, times u; 0 at g <= -10, g*u at g >= 10
+//                 (vecinline.zig:522-536; table entries convert.zig:224-260,
+//                 gelu = 0.5x(1 + tanh(sqrt(2/pi) x (1 + 0.044715 x^2))) with
+//                 the inner 1 + a*x*x as one fused multiply-add)
+//   SWIGLU        g / (1 + exp(-g)) * u                (vec.zig:658-668)
+//   SWIGLU_OAI    x = min(g, limit), y = clamp(u, -limit, limit),
+//                 x / (1 + exp(alpha * -x)) * (y + 1)  (activation.zig:475-503)
+//   SWIGLU_CLAMP  x = min(g, limit), y = clamp(u, -limit, limit),
+//                 x / (1 + exp(-x)) * y                (activation.zig:523-548)
+// min and clamp keep the C++ library's NaN behaviour (a NaN g or u passes
+// through).  The host validates op.
+__device__ __forceinline__ float glu_apply(int op, float g, float u, float alpha, float limit) {
+    if (op == GLU_REGLU) return g > 0.0f ? g * u : 0.0f;
+    if (op == GLU_GEGLU) {
+        if (g <= -10.0f) return 0.0f;
+        if (g >= 10.0f) return g * u;
+        const float t = (float)(_Float16)g;
+        const float inner = 0.79788456080286535587989211986876f * t * __builtin_fmaf(0.044715f * t, t, 1.0f);
+        const float gl = 0.5f * t * (1.0f + tanhf(inner));
+        return (float)(_Float16)gl * u;
+    }
+    if (op == GLU_SWIGLU) return g / (1.0f + expf(-g)) * u;
+    const float x = limit < g ? limit : g;
+    const float y = u < -limit ? -limit : (limit < u ? limit : u);
+    if (op == GLU_SWIGLU_OAI) return x / (1.0f + expf(alpha * (-x))) * (y + 1.0f);
+    return x / (1.0f + expf(-x)) * y;  // GLU_SWIGLU_CLAMP
+}
+
 }  // namespace qmm

@@ -51,6 +51,13 @@ def lib():
         L.hip_qmm_gemv_mfma.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_mul_mat_vec_f32.restype = i32
         L.hip_qmm_mul_mat_vec_f32.argtypes = [i32, vp, i64, i64, i64, vp, vp, vp]
+        L.hip_qmm_mul_mat_vec_fused.restype = i32
+        L.hip_qmm_mul_mat_vec_fused.argtypes = [i32, vp, vp, i64, i64, i64, vp, vp, vp, i32, ctypes.c_float,
+                                                ctypes.c_float, vp, vp]
+        L.hip_qmm_glu_f32.restype = i32
+        L.hip_qmm_glu_f32.argtypes = [i32, ctypes.c_float, ctypes.c_float, i64, i64, vp, i64, vp, i64, vp, i64, vp]
+        L.hip_qmm_add_f32.restype = i32
+        L.hip_qmm_add_f32.argtypes = [i64, i64, vp, i64, vp, i64, vp, i64, vp]
         L.hip_qmm_mmq.restype = i32
         L.hip_qmm_mmq.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mmq_workspace_size.restype = ctypes.c_size_t
@@ -154,6 +161,67 @@ def mul_mat_vec_f32(qtype, w: torch.Tensor, K: int, x: torch.Tensor, out=None):
     out = torch.empty((1, nrows), dtype=torch.float32, device=w.device) if out is None else out
     _check(lib().hip_qmm_mul_mat_vec_f32(t, _ptr(w), K, nrows, rs, _ptr(x), _ptr(out), _stream()),
            "hip_qmm_mul_mat_vec_f32")
+    return out
+
+
+GLU_OPS = {"REGLU": 0, "GEGLU": 1, "SWIGLU": 2, "SWIGLU_OAI": 3, "SWIGLU_CLAMP": 6}
+
+
+def _vec(t, n, name):
+    if t is None:
+        return None
+    _require_cuda(t)
+    if t.dtype != torch.float32 or t.numel() != n or not t.is_contiguous():
+        raise ValueError(f"{name} must be {n} contiguous float32 values")
+    return t
+
+
+def mul_mat_vec_fused(qtype, w: torch.Tensor, K: int, x: torch.Tensor, w_gate=None, bias=None, gate_bias=None,
+                      glu="SWIGLU", alpha=1.702, limit=7.0, out=None):
+    """One f32 column through the quantizing GEMV with the fusion epilogue:
+    u = W x (+ bias); with w_gate, out = glu(Wg x (+ gate_bias), u), else u."""
+    _require_cuda(x)
+    t, nrows, rs = _weight_args(qtype, w, K)
+    if w_gate is not None:
+        tg, ng, rg = _weight_args(qtype, w_gate, K)
+        if (ng, rg) != (nrows, rs):
+            raise ValueError("w_gate must match w")
+    x = x.reshape(-1)
+    if x.numel() != K or not x.is_contiguous():
+        raise ValueError("x must be one contiguous column of K values")
+    _vec(bias, nrows, "bias")
+    _vec(gate_bias, nrows, "gate_bias")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty((1, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_vec_fused(t, _ptr(w), _ptr(w_gate) if w_gate is not None else None, K, nrows, rs,
+                                           _ptr(x), _ptr(bias) if bias is not None else None,
+                                           _ptr(gate_bias) if gate_bias is not None else None, op, alpha, limit,
+                                           _ptr(out), _stream()), "hip_qmm_mul_mat_vec_fused")
+    return out
+
+
+def glu_f32(gate: torch.Tensor, up: torch.Tensor, glu="SWIGLU", alpha=1.702, limit=7.0, out=None):
+    """Standalone GLU over [rows, n] f32 tensors (rows may be strided)."""
+    if not (gate.is_cuda and up.is_cuda):
+        raise HipQmmError("tensors must live on the GPU")
+    if gate.shape != up.shape or gate.dim() != 2 or gate.stride(1) != 1 or up.stride(1) != 1:
+        raise ValueError("gate and up must be [rows, n] with contiguous rows")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty(gate.shape, dtype=torch.float32, device=gate.device) if out is None else out
+    _check(lib().hip_qmm_glu_f32(op, alpha, limit, gate.shape[1], gate.shape[0], _ptr(gate), gate.stride(0),
+                                 _ptr(up), up.stride(0), _ptr(out), out.stride(0), _stream()), "hip_qmm_glu_f32")
+    return out
+
+
+def add_f32(a: torch.Tensor, b: torch.Tensor, out=None):
+    """Same-shape f32 add over [rows, n] tensors (rows may be strided)."""
+    if not (a.is_cuda and b.is_cuda):
+        raise HipQmmError("tensors must live on the GPU")
+    if a.shape != b.shape or a.dim() != 2 or a.stride(1) != 1 or b.stride(1) != 1:
+        raise ValueError("a and b must be [rows, n] with contiguous rows")
+    out = torch.empty(a.shape, dtype=torch.float32, device=a.device) if out is None else out
+    _check(lib().hip_qmm_add_f32(a.shape[1], a.shape[0], _ptr(a), a.stride(0), _ptr(b), b.stride(0), _ptr(out),
+                                 out.stride(0), _stream()), "hip_qmm_add_f32")
     return out
 
 

@@ -3,12 +3,14 @@ and backend vtable layouts the HIP backend layer fills, for Python hosts and
 tests that drive the backend through the plugin interface.
 
 Layout sources (reference paths): ggml_tensor as read throughout src/ggml and
-checked at src/ggml/backend_meta.zig:3221-3222; ggml_cgraph at
-src/ggml/impl.zig:469-485; vtable member order as the CUDA backend fills them
-(src/ggml/cuda/backend.zig:250-265, 343-352, 714-731, 1032-1048, 1141-1146);
-op ids from op_name (src/ggml/types.zig:25-48).
+checked at src/ggml/backend_meta.zig:3221-3222; ggml_cgraph and
+ggml_hash_set at src/ggml/impl.zig:422-435, 469-485; vtable member order as
+the CUDA backend fills them (src/ggml/cuda/backend.zig:250-265, 343-352,
+714-731, 1032-1048, 1141-1146); op ids from op_name
+(src/ggml/types.zig:25-51), GLU op ids from glu_op_name (types.zig:103-106).
 """
 import ctypes as C
+import struct
 
 GGML_MAX_DIMS = 4
 GGML_MAX_SRC = 10
@@ -21,6 +23,11 @@ GGML_TYPE_Q4_K, GGML_TYPE_Q6_K, GGML_TYPE_Q8_K, GGML_TYPE_I32 = 12, 14, 15, 26
 # ggml_op ids (position in op_name)
 GGML_OP_NONE, GGML_OP_ADD, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT_ID = 0, 2, 28, 29
 GGML_OP_RESHAPE, GGML_OP_VIEW, GGML_OP_PERMUTE, GGML_OP_TRANSPOSE = 35, 36, 37, 38
+GGML_OP_GLU = 98
+# ggml_glu_op ids
+GGML_GLU_OP_REGLU, GGML_GLU_OP_GEGLU, GGML_GLU_OP_SWIGLU, GGML_GLU_OP_SWIGLU_OAI = 0, 1, 2, 3
+GGML_GLU_OP_GEGLU_ERF, GGML_GLU_OP_GEGLU_QUICK, GGML_GLU_OP_SWIGLU_CLAMP = 4, 5, 6
+GGML_TENSOR_FLAG_OUTPUT = 2
 GGML_STATUS_SUCCESS, GGML_STATUS_FAILED = 0, -1
 GGML_BACKEND_BUFFER_USAGE_ANY, GGML_BACKEND_BUFFER_USAGE_WEIGHTS, GGML_BACKEND_BUFFER_USAGE_COMPUTE = 0, 1, 2
 GGML_BACKEND_DEVICE_TYPE_GPU = 1
@@ -63,6 +70,10 @@ class ggml_cgraph(C.Structure):
         ("grad_accs", C.c_void_p),
         ("leafs", C.POINTER(C.POINTER(ggml_tensor))),
         ("use_counts", C.c_void_p),
+        ("hash_size", C.c_size_t),  # visited_hash_set
+        ("hash_used", C.c_void_p),
+        ("hash_keys", C.c_void_p),
+        ("order", C.c_int),
     ]
 
 
@@ -208,6 +219,21 @@ def make_tensor(gtype, ne, name=b"", op=GGML_OP_NONE, srcs=(), data=None, nb=Non
         t.src[i] = C.pointer(s)
     t.data = data
     t.name = name
+    return t
+
+
+def set_op_param_f32(t, i, v):
+    t.op_params[i] = struct.unpack("<i", struct.pack("<f", v))[0]
+
+
+def make_glu(op, gate, up, ne, alpha=0.0, limit=0.0, name=b"glu"):
+    """ggml_glu_split(gate, up) with op params as ggml_swiglu_oai /
+    ggml_swiglu_clamp write them (src/ggml/ops.zig:727-751, 3779-3798)."""
+    t = make_tensor(GGML_TYPE_F32, ne, name=name, op=GGML_OP_GLU, srcs=(gate, up))
+    t.op_params[0] = op
+    t.op_params[1] = 0
+    set_op_param_f32(t, 2, alpha)
+    set_op_param_f32(t, 3, limit)
     return t
 
 

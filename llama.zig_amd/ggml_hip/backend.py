@@ -114,15 +114,54 @@ class HipBackend:
         buf.iface.get_tensor(t.buffer, C.pointer(t), out.ctypes.data, 0, out.nbytes)
         return out
 
-    def compute(self, nodes):
+    def compute(self, nodes, use_counts=True):
+        """Run `nodes` as one graph.  With use_counts, the graph carries the
+        visited hash set and per-tensor use counts ggml_build_forward fills
+        (every node and source keyed at (addr >> 4) % size with linear
+        probing, src/ggml/impl.zig:509-557; the count of a tensor is the
+        number of node source slots naming it, src/ggml/graph.zig:472-520),
+        which the backend's fusion reads."""
         arr = (abi.PT * len(nodes))(*[C.pointer(n) for n in nodes])
         g = abi.ggml_cgraph()
         g.size = len(nodes)
         g.n_nodes = len(nodes)
         g.n_leafs = 0
         g.nodes = arr
+        keep = []
+        if use_counts:
+            tensors = []
+            for n in nodes:
+                tensors.append(C.addressof(n))
+                for s in n.src:
+                    if s:
+                        tensors.append(C.addressof(s.contents))
+            size = 2 * len(tensors) + 1
+            used = (C.c_uint32 * ((size + 31) // 32))()
+            keys = (C.c_void_p * size)()
+            counts = (C.c_int32 * size)()
+
+            def slot(a):
+                i = (a >> 4) % size
+                while used[i >> 5] >> (i & 31) & 1 and keys[i] != a:
+                    i = (i + 1) % size
+                return i
+
+            for a in tensors:
+                i = slot(a)
+                used[i >> 5] |= 1 << (i & 31)
+                keys[i] = a
+            for n in nodes:
+                for s in n.src:
+                    if s:
+                        counts[slot(C.addressof(s.contents))] += 1
+            g.use_counts = C.cast(counts, C.c_void_p)
+            g.hash_size = size
+            g.hash_used = C.cast(used, C.c_void_p)
+            g.hash_keys = C.cast(keys, C.c_void_p)
+            keep = [used, keys, counts]
         st = self.be.iface.graph_compute(self.be_ptr, C.pointer(g))
         self.be.iface.synchronize(self.be_ptr)
+        del keep
         return st
 
     def close(self):

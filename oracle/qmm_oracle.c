@@ -1430,6 +1430,54 @@ void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nro
 /* Synthetic inputs: SplitMix64 (public-domain generator by S. Vigna) feeding
  * Box-Muller in double precision, rounded to f32. */
 
+/* ---------------------------------------------------------------- GLU
+ * The CPU GLU ops on f32 rows (ggml_compute_forward_glu,
+ * src/ggml/cpu/ops/activation.zig:594-608), split form (gate and value in
+ * separate rows, gluRows / GluRows.halves at :365-376, :391-403):
+ *   REGLU        ggml_vec_reglu_f32        (vecinline.zig:507-511)
+ *   GEGLU        ggml_vec_geglu_f32, the GGML_GELU_FP16 arm (vecinline.zig:522-536):
+ *                0 at x <= -10, x*g at x >= 10, else table[f16(x)] * g with
+ *                table[t] = f16(gelu(f32(t))) (cpu/convert.zig:224-228)
+ *   SWIGLU       ggml_vec_swiglu_f32's scalar arm: silu(x)*g, silu = x/(1+exp(-x))
+ *                (vec.zig:658-668, vecinline.zig:617-620).  The vector arm
+ *                evaluates exp with its own polynomial; the two agree to a few
+ *                ulp, which the tests allow.
+ *   SWIGLU_OAI   swigluOaiRows f32 (activation.zig:475-503)
+ *   SWIGLU_CLAMP swigluClampRows f32 (activation.zig:523-548)
+ * std::min(a, b) = b < a ? b : a and std::clamp(v, lo, hi) =
+ * v < lo ? lo : (hi < v ? hi : v) (activation.zig:458-463). */
+float orc_gelu_f32(float x) {
+    const float a = 0.044715f;                          /* GELU_COEF_A, convert.zig:242 */
+    const float s = 0.79788456080286535587989211986876f; /* SQRT_2_OVER_PI, convert.zig:248 */
+    return 0.5f * x * (1.0f + tanhf(s * x * fmaf(a * x, x, 1.0f)));
+}
+
+static float glu_one(int op, float x, float g, float alpha, float limit) {
+    switch (op) {
+    case ORC_GLU_REGLU: return x > 0.0f ? x * g : 0.0f;
+    case ORC_GLU_GEGLU:
+        if (x <= -10.0f) return 0.0f;
+        if (x >= 10.0f) return x * g;
+        return orc_fp16_to_fp32(orc_fp32_to_fp16(orc_gelu_f32(orc_fp16_to_fp32(orc_fp32_to_fp16(x))))) * g;
+    case ORC_GLU_SWIGLU: return (x / (1.0f + expf(-x))) * g;
+    case ORC_GLU_SWIGLU_OAI: {
+        const float xm = limit < x ? limit : x;
+        const float y = g < -limit ? -limit : (limit < g ? limit : g);
+        const float out_glu = xm / (1.0f + expf(alpha * (-xm)));
+        return out_glu * (y + 1.0f);
+    }
+    default: { /* ORC_GLU_SWIGLU_CLAMP */
+        const float gate = limit < x ? limit : x;
+        const float up = g < -limit ? -limit : (limit < g ? limit : g);
+        return gate / (1.0f + expf(-gate)) * up;
+    }
+    }
+}
+
+void orc_glu_f32(int op, int64_t n, const float *gate, const float *up, float alpha, float limit, float *out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = glu_one(op, gate[i], up[i], alpha, limit);
+}
+
 static uint64_t splitmix64(uint64_t *s) {
     uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;

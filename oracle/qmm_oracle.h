@@ -89,6 +89,21 @@ void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nro
                     int64_t K, const float *x, int64_t ne11, int64_t n_tokens,
                     const int32_t *ids, int64_t n_ids, float *dst, int nth);
 
+/* GLU ops (ggml_glu_op: positions in GGML_GLU_OP_NAME, src/ggml/types.zig:103-106) */
+#define ORC_GLU_REGLU 0
+#define ORC_GLU_GEGLU 1
+#define ORC_GLU_SWIGLU 2
+#define ORC_GLU_SWIGLU_OAI 3
+#define ORC_GLU_SWIGLU_CLAMP 6
+
+/* ggml_gelu_f32 as the CPU's f16 gelu table is built from it
+ * (src/ggml/cpu/convert.zig:250-260): 0.5x(1 + tanh(sqrt(2/pi) x (1 + a x^2)))
+ * with the inner 1 + a*x*x as one fused multiply-add. */
+float orc_gelu_f32(float x);
+/* ggml_compute_forward_glu, split form, one row of n:
+ * out[i] = glu(gate[i], up[i]); alpha / limit are op params 2 / 3. */
+void orc_glu_f32(int op, int64_t n, const float *gate, const float *up, float alpha, float limit, float *out);
+
 /* synthetic inputs: SplitMix64 -> Box-Muller (double) -> f32 */
 void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out);
 

@@ -65,6 +65,10 @@ def lib():
         L.orc_fnv1a.restype = ctypes.c_uint64
         L.orc_fnv1a.argtypes = [vp, ctypes.c_size_t]
         L.orc_has_avx2.restype = ctypes.c_int
+        L.orc_gelu_f32.restype = ctypes.c_float
+        L.orc_gelu_f32.argtypes = [ctypes.c_float]
+        L.orc_glu_f32.restype = None
+        L.orc_glu_f32.argtypes = [ctypes.c_int, i64, f32p, f32p, ctypes.c_float, ctypes.c_float, f32p]
         _lib = L
     return _lib
 
@@ -150,6 +154,23 @@ def mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=4, impl=IMPL_GENERIC):
     out = np.full((n_tokens, n_ids, nrows), np.nan, dtype=np.float32)
     lib().orc_mul_mat_id(t, impl, _p(np.ascontiguousarray(wq)), n_as, nrows, K, _p(x), ne11, n_tokens, _p(ids),
                          n_ids, _p(out), nth)
+    return out
+
+
+GLU_REGLU, GLU_GEGLU, GLU_SWIGLU, GLU_SWIGLU_OAI, GLU_SWIGLU_CLAMP = 0, 1, 2, 3, 6
+
+
+def gelu_f32(x):
+    return float(lib().orc_gelu_f32(x))
+
+
+def glu(op, gate, up, alpha=0.0, limit=0.0):
+    """The CPU GLU op, split form: out = glu(gate, up), elementwise."""
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    assert gate.shape == up.shape
+    out = np.empty_like(gate)
+    lib().orc_glu_f32(op, gate.size, _p(gate), _p(up), alpha, limit, _p(out))
     return out
 
 

@@ -137,7 +137,29 @@ def test_supports_op(L):
     assert ok(mmid(abi.GGML_TYPE_Q4_K, 256, 64, 16, 4, 3, ne11=1)[3])  # one row broadcast per token
     assert not ok(mmid(abi.GGML_TYPE_Q4_K, 256, 64, 16, 4, 3, ne11=2)[3])
     other = abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=abi.GGML_OP_ADD)
-    assert not ok(other)
+    assert not ok(other)  # an ADD without sources
+    # GLU: f32, the device's five ops, split (same shapes) or one tensor of two halves
+    g = abi.make_tensor(abi.GGML_TYPE_F32, [14336, 1], name=b"g")
+    u = abi.make_tensor(abi.GGML_TYPE_F32, [14336, 1], name=b"u")
+    for op in (abi.GGML_GLU_OP_REGLU, abi.GGML_GLU_OP_GEGLU, abi.GGML_GLU_OP_SWIGLU, abi.GGML_GLU_OP_SWIGLU_OAI,
+               abi.GGML_GLU_OP_SWIGLU_CLAMP):
+        assert ok(abi.make_glu(op, g, u, [14336, 1]))
+    for op in (abi.GGML_GLU_OP_GEGLU_ERF, abi.GGML_GLU_OP_GEGLU_QUICK, 7):
+        assert not ok(abi.make_glu(op, g, u, [14336, 1]))
+    assert not ok(abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g, u, [14336, 2]))  # dst shape differs
+    half = abi.make_tensor(abi.GGML_TYPE_F32, [64, 3], name=b"gu")
+    single = abi.make_tensor(abi.GGML_TYPE_F32, [32, 3], op=abi.GGML_OP_GLU, srcs=(half,))
+    single.op_params[0] = abi.GGML_GLU_OP_SWIGLU
+    assert ok(single)
+    single.ne[0] = 31
+    assert not ok(single)
+    h16 = abi.make_tensor(abi.GGML_TYPE_F16, [14336, 1])
+    assert not ok(abi.make_glu(abi.GGML_GLU_OP_SWIGLU, h16, h16, [14336, 1]))
+    # ADD: same-shape f32 only (no broadcasting)
+    assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [14336, 1], op=abi.GGML_OP_ADD, srcs=(g, u)))
+    row = abi.make_tensor(abi.GGML_TYPE_F32, [14336, 1])
+    mat = abi.make_tensor(abi.GGML_TYPE_F32, [14336, 4])
+    assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [14336, 4], op=abi.GGML_OP_ADD, srcs=(mat, row)))
     for op in (abi.GGML_OP_NONE, abi.GGML_OP_VIEW, abi.GGML_OP_RESHAPE, abi.GGML_OP_PERMUTE, abi.GGML_OP_TRANSPOSE):
         assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=op))
 
@@ -153,3 +175,44 @@ def test_alloc_size_pads_quantized_rows(L):
     assert size(t) == 2 * 17 * 34 + 15 * 34
     t = abi.make_tensor(abi.GGML_TYPE_F32, [100, 3])
     assert size(t) == 1200
+
+
+def test_fused_and_elementwise_entry_points_reject_bad_arguments(L):
+    """Argument checks of the fused-epilogue GEMV and the GLU / ADD entry
+    points: each rejected call returns hipErrorInvalidValue (1) before any
+    device work, so this runs without a GPU."""
+    import ctypes as C
+    vp, i64, f = C.c_void_p, C.c_int64, C.c_float
+    L.hip_qmm_mul_mat_vec_fused.restype = C.c_int
+    L.hip_qmm_mul_mat_vec_fused.argtypes = [C.c_int, vp, vp, i64, i64, i64, vp, vp, vp, C.c_int, f, f, vp, vp]
+    L.hip_qmm_glu_f32.restype = C.c_int
+    L.hip_qmm_glu_f32.argtypes = [C.c_int, f, f, i64, i64, vp, i64, vp, i64, vp, i64, vp]
+    L.hip_qmm_add_f32.restype = C.c_int
+    L.hip_qmm_add_f32.argtypes = [i64, i64, vp, i64, vp, i64, vp, i64, vp]
+    Q4K, F16 = 12, 1
+    w, x, d = 0x100000, 0x200000, 0x300000  # aligned placeholders, never dereferenced
+    rs = 16 * 144
+
+    def fused(**kw):
+        a = dict(type=Q4K, w=w, wg=None, K=4096, M=64, rs=rs, x=x, b=None, gb=None, op=2, dst=d)
+        a.update(kw)
+        return L.hip_qmm_mul_mat_vec_fused(a["type"], a["w"], a["wg"], a["K"], a["M"], a["rs"], a["x"], a["b"],
+                                           a["gb"], a["op"], 1.702, 7.0, a["dst"], None)
+
+    assert fused(type=F16) == 1                      # not a weight type
+    assert fused(K=4000) == 1                         # Q4_K rows are whole super-blocks
+    assert fused(K=65536, rs=256 * 144) == 1          # beyond the 32768-element column
+    assert fused(w=None) == 1 and fused(x=None) == 1 and fused(dst=None) == 1
+    assert fused(x=x + 4) == 1                        # column not 16-byte aligned
+    assert fused(w=w + 2) == 1                        # Q4_K blocks are read 16 bytes at a time
+    assert fused(wg=w + 2) == 1
+    assert fused(gb=x) == 1                           # a gate bias without a gate
+    assert fused(wg=w, op=4) == 1 and fused(wg=w, op=5) == 1 and fused(wg=w, op=7) == 1  # no device op
+    assert fused(rs=rs - 1) == 1                      # rows shorter than K
+    assert L.hip_qmm_glu_f32(4, 0.0, 0.0, 8, 2, x, 8, x, 8, d, 8, None) == 1
+    assert L.hip_qmm_glu_f32(2, 0.0, 0.0, -1, 2, x, 8, x, 8, d, 8, None) == 1
+    assert L.hip_qmm_glu_f32(2, 0.0, 0.0, 8, 2, x, 4, x, 8, d, 8, None) == 1  # stride below the row
+    assert L.hip_qmm_glu_f32(2, 0.0, 0.0, 8, 2, None, 8, x, 8, d, 8, None) == 1
+    assert L.hip_qmm_glu_f32(2, 0.0, 0.0, 0, 2, x, 8, x, 8, d, 8, None) == 0   # nothing to do
+    assert L.hip_qmm_add_f32(8, 2, x, 8, x, 8, None, 8, None) == 1
+    assert L.hip_qmm_add_f32(8, 0, x, 8, x, 8, d, 8, None) == 0

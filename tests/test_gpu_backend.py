@@ -130,6 +130,13 @@ def test_graph_rejects_unsupported_node(hb):
     from ggml_hip import abi
     a = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4], name=b"a")
     hb.alloc([a])
-    add = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4], op=abi.GGML_OP_ADD, srcs=(a, a), name=b"add")
+    # a broadcasting ADD (a row added to every row) stays on the CPU
+    row = abi.make_tensor(abi.GGML_TYPE_F32, [64, 1], name=b"row")
+    hb.alloc([row])
+    add = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4], op=abi.GGML_OP_ADD, srcs=(a, row), name=b"add")
     hb.alloc([add])
     assert hb.compute([add]) == abi.GGML_STATUS_FAILED
+    # so does a GLU the device has no kernel for (GEGLU_ERF)
+    glu = abi.make_glu(abi.GGML_GLU_OP_GEGLU_ERF, a, a, [64, 4])
+    hb.alloc([glu])
+    assert hb.compute([glu]) == abi.GGML_STATUS_FAILED

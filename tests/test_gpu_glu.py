@@ -1,0 +1,312 @@
+"""The GEMV fusion epilogue on the GPU: gate + up GEMVs + GLU in one kernel,
+GEMV + bias, and the standalone GLU / ADD kernels the backend runs when it
+does not fuse.
+
+Checks, per case:
+  - fused output == the unfused composition on the GPU (GEMV per lane, bias
+    add, GLU kernel) bit for bit: the same dots, the same combination order,
+    the same glu_apply;
+  - the lanes' GEMVs (no gate) == hip_qmm_mul_mat_vec_f32 bit for bit, and
+    within 2e-6 of the f64 evaluation of the Q8_1 formula;
+  - fused output vs the CPU ggml path (Q8_K vec_dot + f32 bias add + the CPU
+    GLU op) within NMSE < 5e-4;
+  - standalone GLU vs the CPU GLU op: REGLU exact; SWIGLU / SWIGLU_OAI /
+    SWIGLU_CLAMP within 8 f32 ulp (the device and libm exp differ in the last
+    bits); GEGLU exact but for rare one-f16-step moves of the gelu factor
+    where 1 + tanh cancels (the device and libm tanhf differ in the last bit);
+  - through the plugin: {MUL_MAT, MUL_MAT, GLU}, {MUL_MAT, ADD, MUL_MAT, ADD,
+    GLU} and {MUL_MAT, ADD} fuse (their intermediates, pre-filled with NaN,
+    stay untouched) unless a use count or an output flag forbids it, and the
+    fused and unfused graphs agree."""
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, max_rel, nmse, weights_q
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4  # test-backend-ops' gate for mul_mat
+F64_TOL = 2e-6    # fp32 epilogue vs exact f64 of the same Q8_1 formula, / max|out|
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+OPS = {"REGLU": O.GLU_REGLU, "GEGLU": O.GLU_GEGLU, "SWIGLU": O.GLU_SWIGLU, "SWIGLU_OAI": O.GLU_SWIGLU_OAI,
+       "SWIGLU_CLAMP": O.GLU_SWIGLU_CLAMP}
+ALPHA, LIMIT = 1.702, 7.0  # ggml_swiglu_oai's defaults as gpt-oss uses them
+
+
+def _dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def glu_matches(op, g, u, got, want):
+    """The standalone and fused GLU against the CPU op, per element."""
+    got = np.asarray(got, np.float32).reshape(-1)
+    want = np.asarray(want, np.float32).reshape(-1)
+    g = np.asarray(g, np.float32).reshape(-1)
+    u = np.asarray(u, np.float32).reshape(-1)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    ok = ~np.isnan(want)
+    got, want, g, u = got[ok], want[ok], g[ok], u[ok]
+    if op == O.GLU_REGLU:
+        np.testing.assert_array_equal(got, want)
+        return
+    if op == O.GLU_GEGLU:
+        diff = got != want
+        assert diff.mean() < 2e-3, diff.mean()
+        # one f16 step of the gelu factor, times |u|
+        gl = np.abs(want / np.where(u == 0, 1, u)).astype(np.float16)
+        step = np.spacing(gl).astype(np.float32) * np.abs(u)
+        assert np.all(np.abs(got - want)[diff] <= step[diff] * 1.001 + 1e-30)
+        return
+    tol = 8 * np.spacing(np.abs(want).astype(np.float32)) + 1e-37
+    bad = np.abs(got - want) > tol
+    assert not bad.any(), (got[bad][:5], want[bad][:5])
+
+
+def glu_inputs(n, seed):
+    rng = np.random.default_rng(seed)
+    g = (rng.standard_normal(n) * 4).astype(np.float32)
+    u = (rng.standard_normal(n) * 4).astype(np.float32)
+    special = np.float32([0.0, -0.0, 10.0, -10.0, 9.99, -9.99, LIMIT, -LIMIT, 30.0, -30.0, 90.0, -90.0])
+    g[:special.size] = special
+    u[:special.size] = special[::-1]
+    return g, u
+
+
+@pytest.mark.parametrize("opname", list(OPS))
+def test_glu_kernel_vs_cpu(opname):
+    import ggml_hip as G
+    op = OPS[opname]
+    g, u = glu_inputs(3 * 5000, 11 + op)
+    gd, ud = _dev(g.reshape(3, 5000)), _dev(u.reshape(3, 5000))
+    got = G.glu_f32(gd, ud, opname, ALPHA, LIMIT).cpu().numpy()
+    glu_matches(op, g, u, got, O.glu(op, g, u, ALPHA, LIMIT))
+    # strided rows: every other row of a [6, 5000] buffer, into a strided output
+    big = torch.zeros((6, 5000), dtype=torch.float32, device="cuda")
+    big[::2] = gd
+    out = torch.full((3, 6000), float("nan"), dtype=torch.float32, device="cuda")
+    G.glu_f32(big[::2], ud, opname, ALPHA, LIMIT, out=out[:, :5000])
+    np.testing.assert_array_equal(out[:, :5000].cpu().numpy(), got)
+    assert torch.isnan(out[:, 5000:]).all()
+
+
+def test_add_kernel_exact():
+    import ggml_hip as G
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((7, 1234)).astype(np.float32)
+    b = rng.standard_normal((7, 1234)).astype(np.float32)
+    np.testing.assert_array_equal(G.add_f32(_dev(a), _dev(b)).cpu().numpy(), a + b)
+
+
+def _fused_case(tname, M, K, opname, with_bias):
+    import ggml_hip as G
+    t = TYPES[tname]
+    wu, wg = weights_q(t, M, K, 0), weights_q(t, M, K, 1)
+    x = acts(1, K)
+    wu_d, wg_d, x_d = _dev(wu), _dev(wg), _dev(x)
+    rng = np.random.default_rng(M + K)
+    bu = (rng.standard_normal(M) * 0.5).astype(np.float32) if with_bias else None
+    bg = (rng.standard_normal(M) * 0.5).astype(np.float32) if with_bias else None
+    bu_d = _dev(bu) if with_bias else None
+    bg_d = _dev(bg) if with_bias else None
+    op = OPS[opname]
+    fused = G.mul_mat_vec_fused(tname, wu_d, K, x_d, w_gate=wg_d, bias=bu_d, gate_bias=bg_d, glu=opname,
+                                alpha=ALPHA, limit=LIMIT)
+    u = G.mul_mat_vec_fused(tname, wu_d, K, x_d, bias=bu_d)
+    g = G.mul_mat_vec_fused(tname, wg_d, K, x_d, bias=bg_d)
+    unfused = G.glu_f32(g, u, opname, ALPHA, LIMIT)
+    torch.cuda.synchronize()
+    return t, wu, wg, x, bu, bg, op, fused.cpu().numpy(), u.cpu().numpy(), g.cpu().numpy(), unfused.cpu().numpy()
+
+
+@pytest.mark.parametrize("tname,M,K", [("Q4_K", 14336, 4096), ("Q4_K", 768, 2048), ("Q4_K", 3000, 8192),
+                                       ("Q6_K", 4100, 4096), ("Q8_0", 2048, 4096), ("Q8_0", 333, 96)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_fused_gate_up_swiglu(tname, M, K, with_bias):
+    import ggml_hip as G
+    t, wu, wg, x, bu, bg, op, fused, u, g, unfused = _fused_case(tname, M, K, "SWIGLU", with_bias)
+    np.testing.assert_array_equal(fused, unfused)
+    x_d = _dev(x)
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    for wq, lane, b in ((wu, u, bu), (wg, g, bg)):
+        plain = lane - b if b is not None else lane
+        if b is None and K <= (2048 if tname == "Q8_0" else 4096):
+            # the lanes' GEMV is the one-column fused GEMV's arithmetic
+            ref = G.mul_mat_vec_f32(tname, _dev(wq), K, x_d[0]).cpu().numpy()
+            np.testing.assert_array_equal(lane, ref)
+        ideal = O.mul_mat_q8_1_f64(t, wq, M, K, y, 1)
+        assert max_err_scaled(plain, ideal) < F64_TOL * 2, max_err_scaled(plain, ideal)
+    cu = O.mul_mat(t, wu, M, K, x, nth=8)
+    cg = O.mul_mat(t, wg, M, K, x, nth=8)
+    if bu is not None:
+        cu, cg = cu + bu, cg + bg
+    cpu = O.glu(op, cg, cu, ALPHA, LIMIT)
+    e = nmse(fused, cpu)
+    assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {max_rel(fused, cpu):.3g}"
+
+
+@pytest.mark.parametrize("opname", ["REGLU", "GEGLU", "SWIGLU_OAI", "SWIGLU_CLAMP"])
+def test_fused_gate_up_other_glu(opname):
+    t, wu, wg, x, bu, bg, op, fused, u, g, unfused = _fused_case("Q4_K", 768, 2048, opname, True)
+    np.testing.assert_array_equal(fused, unfused)
+    glu_matches(op, g, u, fused, O.glu(op, g, u, ALPHA, LIMIT))  # the epilogue on the GPU's own lanes
+    cu = O.mul_mat(t, wu, 768, 2048, x, nth=8) + bu
+    cg = O.mul_mat(t, wg, 768, 2048, x, nth=8) + bg
+    assert nmse(fused, O.glu(op, cg, cu, ALPHA, LIMIT)) < NMSE_GATE
+
+
+def test_fused_bias_only():
+    import ggml_hip as G
+    M, K = 5000, 4096
+    wq = weights_q(O.TYPE_Q4_K, M, K)
+    x = acts(1, K)
+    b = np.linspace(-1, 1, M, dtype=np.float32)
+    got = G.mul_mat_vec_fused("Q4_K", _dev(wq), K, _dev(x), bias=_dev(b)).cpu().numpy()
+    plain = G.mul_mat_vec_f32("Q4_K", _dev(wq), K, _dev(x)[0]).cpu().numpy()
+    np.testing.assert_array_equal(got, plain + b)
+    assert nmse(got, O.mul_mat(O.TYPE_Q4_K, wq, M, K, x, nth=8) + b) < NMSE_GATE
+
+
+# ---------------------------------------------------------------- through the plugin
+
+@pytest.fixture(scope="module")
+def hb():
+    from ggml_hip.backend import HipBackend
+    with HipBackend(0) as b:
+        yield b
+
+
+def _ffn_graph(hb, M, K, with_bias, opname="SWIGLU", gate_first=True):
+    """x -> up/gate MUL_MATs (+ bias ADDs) -> GLU, as llama's FFN builds it."""
+    from ggml_hip import abi
+    t = abi.GGML_TYPE_Q4_K
+    wu, wg = weights_q(O.TYPE_Q4_K, M, K, 0), weights_q(O.TYPE_Q4_K, M, K, 1)
+    x = acts(1, K)
+    tw_u = abi.make_tensor(t, [K, M], name=b"ffn_up")
+    tw_g = abi.make_tensor(t, [K, M], name=b"ffn_gate")
+    tx = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1], name=b"x")
+    up = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(tw_u, tx), name=b"up")
+    gate = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(tw_g, tx), name=b"gate")
+    leaves, inter = [tw_u, tw_g], [up, gate]
+    u_out, g_out, biases = up, gate, None
+    if with_bias:
+        tb_u = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], name=b"b_up")
+        tb_g = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], name=b"b_gate")
+        u_out = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_ADD, srcs=(up, tb_u), name=b"up_b")
+        g_out = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_ADD, srcs=(tb_g, gate), name=b"gate_b")
+        inter += [u_out, g_out]
+        rng = np.random.default_rng(3)
+        biases = (tb_u, tb_g, (rng.standard_normal(M) * 0.5).astype(np.float32),
+                  (rng.standard_normal(M) * 0.5).astype(np.float32))
+    glu = abi.make_glu(OPS[opname], g_out, u_out, [M, 1], ALPHA, LIMIT)
+    hb.alloc(leaves, usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([tx] + inter + [glu] + ([biases[0], biases[1]] if biases else []),
+             usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(tw_u, wu)
+    hb.set(tw_g, wg)
+    hb.set(tx, x)
+    if biases:
+        hb.set(biases[0], biases[2])
+        hb.set(biases[1], biases[3])
+    if with_bias:
+        nodes = [gate, g_out, up, u_out, glu] if gate_first else [up, u_out, gate, g_out, glu]
+    else:
+        nodes = [gate, up, glu] if gate_first else [up, gate, glu]
+    return nodes, inter, glu, (wu, wg, x, biases)
+
+
+def _run(hb, nodes, inter, glu, M, use_counts=True):
+    for t in inter + [glu]:
+        hb.set(t, np.full(M, np.nan, dtype=np.float32))
+    from ggml_hip import abi
+    assert hb.compute(nodes, use_counts=use_counts) == abi.GGML_STATUS_SUCCESS
+    return hb.get(glu, np.float32, (M,)), [hb.get(t, np.float32, (M,)) for t in inter]
+
+
+@pytest.mark.parametrize("with_bias", [False, True])
+@pytest.mark.parametrize("gate_first", [True, False])
+def test_plugin_fuses_ffn_gate_up_glu(hb, with_bias, gate_first):
+    import ggml_hip as G
+    M, K = 4096, 4096
+    nodes, inter, glu, (wu, wg, x, biases) = _ffn_graph(hb, M, K, with_bias, gate_first=gate_first)
+    out, mids = _run(hb, nodes, inter, glu, M)
+    assert all(np.isnan(m).all() for m in mids)  # fused: no intermediate written
+    want = G.mul_mat_vec_fused("Q4_K", _dev(wu), K, _dev(x), w_gate=_dev(wg),
+                               bias=_dev(biases[2]) if biases else None,
+                               gate_bias=_dev(biases[3]) if biases else None, glu="SWIGLU").cpu().numpy()
+    np.testing.assert_array_equal(out, want.reshape(-1))
+    # the same graph without use counts runs node by node: the intermediates
+    # are written, and at 4096 rows the one-column MUL_MAT is the same GEMV
+    out2, mids2 = _run(hb, nodes, inter, glu, M, use_counts=False)
+    assert not any(np.isnan(m).any() for m in mids2)
+    np.testing.assert_array_equal(out2, out)
+    cu = O.mul_mat(O.TYPE_Q4_K, wu, M, K, x, nth=8).reshape(-1)
+    cg = O.mul_mat(O.TYPE_Q4_K, wg, M, K, x, nth=8).reshape(-1)
+    if biases:
+        cu, cg = cu + biases[2], cg + biases[3]
+    assert nmse(out, O.glu(O.GLU_SWIGLU, cg, cu)) < NMSE_GATE
+
+
+def test_plugin_does_not_fuse_an_output_intermediate(hb):
+    from ggml_hip import abi
+    M, K = 4096, 4096
+    nodes, inter, glu, _ = _ffn_graph(hb, M, K, False)
+    up = nodes[1]
+    up.flags |= abi.GGML_TENSOR_FLAG_OUTPUT
+    try:
+        out, mids = _run(hb, nodes, inter, glu, M)
+    finally:
+        up.flags &= ~abi.GGML_TENSOR_FLAG_OUTPUT
+    assert not any(np.isnan(m).any() for m in mids)
+    out_f, _ = _run(hb, nodes, inter, glu, M)
+    np.testing.assert_array_equal(out, out_f)
+
+
+def test_plugin_does_not_fuse_a_shared_intermediate(hb):
+    """The up result is also read by a node outside the run: no fusion."""
+    from ggml_hip import abi
+    M, K = 4096, 4096
+    nodes, inter, glu, _ = _ffn_graph(hb, M, K, False)
+    up = nodes[1]
+    extra = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_ADD, srcs=(up, up), name=b"reuse")
+    hb.alloc([extra], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    out, mids = _run(hb, nodes + [extra], inter, glu, M)
+    assert not any(np.isnan(m).any() for m in mids)
+    np.testing.assert_array_equal(hb.get(extra, np.float32, (M,)), mids[0] + mids[0])
+
+
+def test_plugin_fuses_mul_mat_bias_and_runs_glu_alone(hb):
+    import ggml_hip as G
+    from ggml_hip import abi
+    M, K = 5000, 4096
+    wq = weights_q(O.TYPE_Q4_K, M, K)
+    x = acts(1, K)
+    b = np.linspace(-1, 1, M, dtype=np.float32)
+    tw = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M], name=b"w")
+    tx = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1], name=b"x")
+    tb = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], name=b"b")
+    mm = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(tw, tx), name=b"mm")
+    add = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_ADD, srcs=(mm, tb), name=b"mm_b")
+    # a one-tensor swapped GEGLU over [2*M/2 ...]: halves of `add`'s rows are
+    # not a GLU shape, so use a fresh [2n, 3] input for the standalone node
+    h = abi.make_tensor(abi.GGML_TYPE_F32, [64, 3], name=b"h")
+    gl = abi.make_tensor(abi.GGML_TYPE_F32, [32, 3], op=abi.GGML_OP_GLU, srcs=(h,), name=b"geglu_swapped")
+    gl.op_params[0] = abi.GGML_GLU_OP_GEGLU
+    gl.op_params[1] = 1
+    hb.alloc([tw], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([tx, tb, mm, add, h, gl], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(tw, wq)
+    hb.set(tx, x)
+    hb.set(tb, b)
+    hb.set(mm, np.full(M, np.nan, dtype=np.float32))
+    hv = np.random.default_rng(9).standard_normal((3, 64)).astype(np.float32) * 3
+    hb.set(h, hv)
+    assert hb.compute([mm, add, gl]) == abi.GGML_STATUS_SUCCESS
+    assert np.isnan(hb.get(mm, np.float32, (M,))).all()
+    got = hb.get(add, np.float32, (M,))
+    plain = G.mul_mat_vec_f32("Q4_K", _dev(wq), K, _dev(x)[0]).cpu().numpy().reshape(-1)
+    np.testing.assert_array_equal(got, plain + b)
+    # swapped: the second half of each row gates
+    want = O.glu(O.GLU_GEGLU, hv[:, 32:], hv[:, :32])
+    glu_matches(O.GLU_GEGLU, hv[:, 32:], hv[:, :32], hb.get(gl, np.float32, (3, 32)), want)
