@@ -452,83 +452,15 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
     }
 }
 
-// Decode GEMV of one f32 column with the Q8_1 quantization fused in (the
-// quantize-in-GEMV prologue of mmvq.zig:552-622's fusion arguments).  Each
-// workgroup issues its activation loads, then its rows' weight loads,
-// quantizes the whole column into LDS with the same per-quad code as the
-// standalone quantizer (so the Q8_1 bytes are identical) while the weights
-// are in flight, and then runs the two-rows-per-wave arithmetic against LDS.
-// One
-// K-step per lane: K <= 64 * W.  FW waves per workgroup: 8 (512 threads, one
-// 8-value quad slice each), or 16 on large matrices, where half as many
-// workgroups repeat the quantization (measured 8.5 vs 8.9 us at 14336 rows,
-// but 5.4 vs 4.2 us at 4096 rows, whose 128 workgroups are too few).
-constexpr int FUSED_MAXK = 4096;
-
-template <int TYPE, int FW>
-__global__ __launch_bounds__(64 * FW) void gemv_fused_kernel(const uint8_t *__restrict__ w, int64_t K,
-                                                                      int64_t nrows, int64_t row_stride,
-                                                                      const float *x, float *__restrict__ dst) {
-    using F = Fmt<TYPE>;
-    constexpr int RPW = 2;
-    static_assert(FUSED_MAXK <= 8 * 64 * FW, "one activation pass: 8 values per thread");
-    __shared__ alignas(16) int8_t aq[FUSED_MAXK];
-    __shared__ alignas(16) uint32_t ad[FUSED_MAXK / QK8];
-    const int K32 = (int)K;
-    // The activation loads go out first: loads complete in issue order, so
-    // the quantization then waits only for them while the weights stay in
-    // flight.  K % 32 == 0, so the 4 lanes of a quad (one 32-block) are all
-    // in or all out.  Unconditional loads (a valid address past K): with no
-    // branch around them the wait counts only the loads before it.
-    const int kq = 8 * (int)threadIdx.x;
-    const int kqc = kq < K32 ? kq : 0;
-    const float4 xa = *reinterpret_cast<const float4 *>(x + kqc);
-    const float4 xb = *reinterpret_cast<const float4 *>(x + kqc + 4);
-    asm volatile("" ::: "memory");  // keep them ahead of the weight loads
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * RPW;
-    const int kl = lane * F::W;
-    const bool live = kl < K32;
-    const int klc = live ? kl : 0;  // lanes past K load a valid slice and add nothing
-    Wt<TYPE> wt[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) wt[r].load(w + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride, klc);
-    if (kq < K32) {
-        const float v[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
-        const Q8Quad q = q8_1_quantize_quad(v);
-        *reinterpret_cast<uint2 *>(aq + kq) = make_uint2(q.lo, q.hi);
-        if ((threadIdx.x & 3) == 0) ad[kq / QK8] = q.ds;
-    }
-    __syncthreads();
-    if (row0 >= nrows) return;  // uniform per wave, after the workgroup's last barrier
-    float acc[RPW];
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    {
-        Act<TYPE> a;
-        a.load(aq, ad, klc);
-#pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            int S[F::NSUB];
-            wt[r].dots(a, S);
-            const float v = wt[r].combine(a, S, klc);
-            acc[r] += live ? v : 0.0f;
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < RPW; ++r) {
-        const float v = wave_sum(acc[r]);
-        if (lane == r && row0 + r < nrows) dst[row0 + r] = v;
-    }
-}
-
 // One f32 column with the reference's mul_mat_vec fusion epilogue
 // (ggml_cuda_mm_fusion_args_device, src/ggml/cuda/common.zig:1448-1459):
 //   u[r] = W[r] . x (+ bias[r]);  GATE: g[r] = Wg[r] . x (+ gate_bias[r]),
 //   dst[r] = glu(g[r], u[r]);  otherwise dst[r] = u[r].
-// The column is quantized to Q8_1 in the prologue, as in gemv_fused_kernel
-// (identical bytes), into dynamic LDS of K + K/8 bytes; each wave then owns R
+// The quantize-in-GEMV prologue (the fusion arguments of mmvq.zig:552-622):
+// each workgroup issues its activation loads, then its rows' weight loads, and
+// quantizes the column to Q8_1 with the standalone quantizer's per-quad code
+// (identical bytes) into dynamic LDS of K + K/8 bytes while the weights are in
+// flight; one barrier, and the Q8_1 copy never reaches memory.  Each wave owns R
 // rows of W (and the same R rows of Wg), one K-step of 64 lanes x W weights
 // at a time; the first step's weights are in flight during the prologue.
 // The dots and their combination are the two-rows-per-wave kernel's, in the
@@ -809,32 +741,13 @@ extern "C" int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nr
 }
 
 // One f32 activation column, quantized to Q8_1 inside the GEMV (no separate
-// quantizer launch, no Q8_1 copy in memory).  Same result as
-// hip_qmm_quantize_q8_1_planar followed by hip_qmm_mul_mat_vec with one
-// column on the two-rows-per-wave kernel.
+// quantizer launch, no Q8_1 copy in memory): the fused entry point without a
+// gate or a bias.  Same result as hip_qmm_quantize_q8_1_planar followed by
+// hip_qmm_mul_mat_vec with one column on the two-rows-per-wave kernel.
 extern "C" int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                        const float *x, float *dst, void *stream) {
-    if (int e = check_shape(type, K, nrows, row_stride)) return e;
-    if (!w || !x || !dst || K % QK8 != 0 || (uintptr_t)x % 16) return (int)hipErrorInvalidValue;
-    if (K > (type == TYPE_Q8_0 ? 64 * Fmt<TYPE_Q8_0>::W : FUSED_MAXK)) return (int)hipErrorInvalidValue;
-    if (type == TYPE_Q4_K ? ((uintptr_t)w % 16) : ((uintptr_t)w % 2)) return (int)hipErrorInvalidValue;
-    const int fw = nrows >= 8192 ? 16 : 8;
-    const int64_t rows_per_block = 2 * fw;
-    const int64_t nblocks = (nrows + rows_per_block - 1) / rows_per_block;
-    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-    hipStream_t s = (hipStream_t)stream;
-    const uint8_t *wb = (const uint8_t *)w;
-    const dim3 grid((unsigned)nblocks), block(64 * fw);
-#define FUSED_LAUNCH(T)                                                                                              \
-    if (fw == 16) hipLaunchKernelGGL((gemv_fused_kernel<T, 16>), grid, block, 0, s, wb, K, nrows, row_stride, x, dst); \
-    else hipLaunchKernelGGL((gemv_fused_kernel<T, 8>), grid, block, 0, s, wb, K, nrows, row_stride, x, dst)
-    switch (type) {
-    case TYPE_Q4_K: FUSED_LAUNCH(TYPE_Q4_K); break;
-    case TYPE_Q6_K: FUSED_LAUNCH(TYPE_Q6_K); break;
-    default: FUSED_LAUNCH(TYPE_Q8_0); break;
-    }
-#undef FUSED_LAUNCH
-    return (int)hipGetLastError();
+    return hip_qmm_mul_mat_vec_fused(type, w, nullptr, K, nrows, row_stride, x, nullptr, nullptr, 0, 0.0f, 0.0f, dst,
+                                     stream);
 }
 
 namespace {
@@ -852,13 +765,22 @@ template <int TYPE>
 void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride,
                     const float *x, const float *bias, const float *gbias, int op, float alpha, float limit,
                     float *dst, hipStream_t s) {
-    // 16 waves per workgroup on large matrices, 8 otherwise (the plain
-    // fused GEMV's measured choice); the gated form keeps two weight rows
-    // in flight per wave (one of each matrix).
+    // Without a gate: 16 waves per workgroup on large matrices, 8 otherwise
+    // (the plain fused GEMV's measured choice).  Gated, measured on Q4_K
+    // (K = 2048..8192): from 8192 rows 8 waves of 2 rows of each matrix
+    // (15.4 vs 15.9 us for 16 waves of 1 at 14336x4096), from 2048 rows 8
+    // waves of 1, below that 4 waves of 1 (3.1 vs 3.4 us at 768x2048: more
+    // workgroups on a small grid).  Q6_K and Q8_0 keep 16 waves of 1 row on
+    // large matrices: two rows of each matrix would cost Q6_K 131 VGPRs.
     const bool big = nrows >= 8192;
     if (wg) {
-        if (big) launch_fx<TYPE, 16, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
-        else launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        if (big && TYPE == TYPE_Q4_K)
+            launch_fx<TYPE, 8, 2, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        else if (big)
+            launch_fx<TYPE, 16, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        else if (nrows >= 2048)
+            launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        else launch_fx<TYPE, 4, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
     } else {
         if (big) launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
         else launch_fx<TYPE, 8, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);

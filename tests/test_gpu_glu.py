@@ -121,7 +121,8 @@ def _fused_case(tname, M, K, opname, with_bias):
 
 
 @pytest.mark.parametrize("tname,M,K", [("Q4_K", 14336, 4096), ("Q4_K", 768, 2048), ("Q4_K", 3000, 8192),
-                                       ("Q6_K", 4100, 4096), ("Q8_0", 2048, 4096), ("Q8_0", 333, 96)])
+                                       ("Q6_K", 4100, 4096), ("Q6_K", 8200, 1024), ("Q8_0", 2048, 4096),
+                                       ("Q8_0", 333, 96)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_fused_gate_up_swiglu(tname, M, K, with_bias):
     import ggml_hip as G
