@@ -186,10 +186,16 @@ def run_suite(name, torch, G, dev, reps):
                     fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
                     kern = "mmq"
                 ms = event_time_batch(torch, fn, n)
+                # the op on f32 activations (hip_qmm_mul_mat: quantizer + kernel,
+                # or for one column the GEMV that quantizes in its prologue)
+                wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_workspace_size(G.TYPE_IDS[qtype], Kx, M, T)),
+                                  dtype=torch.uint8, device=dev)
+                op_fn = lambda i: G.mul_mat(qtype, ws[i % len(ws)], x, out=out, workspace=wsp)  # noqa: E731
+                ms_op = event_time_batch(torch, op_fn, n)
                 alg = wb + Kx * 4 * T + M * 4 * T
                 ops = 2.0 * M * Kx * T
                 emit({"suite": name, "kernel": kern, "type": qtype, "shape": f"{M}x{Kx}", "label": label, "T": T,
-                      "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
+                      "us": round(ms * 1e3, 3), "op_us": round(ms_op * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2),
                       "int8_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)})
             del ws
@@ -214,6 +220,38 @@ def run_suite(name, torch, G, dev, reps):
                   "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": n_tokens, "top_k": k,
                   "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
                   "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2)})
+            # decode: one token's 8 experts through the one-launch GEMV over
+            # (token, slot) pairs; bytes = the 8 selected experts' weights
+            x1 = torch.randn((1, ne11, Kx), generator=xg, dtype=torch.float32).to(dev)
+            ids1 = ids[:1].contiguous()
+            out1 = torch.empty((1, k, M), dtype=torch.float32, device=dev)
+            fn1 = lambda i: G.mul_mat_id("Q4_K", ws[i % len(ws)], x1, ids1, out=out1, workspace=wsp)  # noqa: E731
+            ms1 = event_time_batch(torch, fn1, n * reps * 4)
+            alg1 = k * M * row_bytes("Q4_K", Kx) + ne11 * Kx * 4 + k * M * 4
+            emit({"suite": name, "kernel": "mul_mat_id decode (GEMV over token/slot pairs)", "type": "Q4_K",
+                  "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": 1, "top_k": k,
+                  "us": round(ms1 * 1e3, 3), "GB/s": round(alg1 / ms1 / 1e6, 1),
+                  "hbm_frac": round(alg1 / ms1 / 1e6 / HBM_PEAK_GBS, 4)})
+            if label == "gate/up":
+                gs = [random_blocks(torch, "Q4_K", n_as * M, Kx, gen, dev).view(n_as, M, -1) for _ in range(n)]
+                fz = lambda i: G.mul_mat_id_vec_fused("Q4_K", ws[i % n], x1, ids1, w_gate=gs[i % n],  # noqa: E731
+                                                      glu="SWIGLU", out=out1)
+                msf = event_time_batch(torch, fz, n * reps * 4)
+                u1 = torch.empty_like(out1)
+                g1 = torch.empty_like(out1)
+
+                def unf(i):
+                    G.mul_mat_id("Q4_K", ws[i % n], x1, ids1, out=u1, workspace=wsp)
+                    G.mul_mat_id("Q4_K", gs[i % n], x1, ids1, out=g1, workspace=wsp)
+                    G.glu_f32(g1.view(k, M), u1.view(k, M), "SWIGLU", out=out1.view(k, M))
+
+                msu = event_time_batch(torch, unf, n * reps * 4)
+                algf = 2 * k * M * row_bytes("Q4_K", Kx) + Kx * 4 + k * M * 4
+                emit({"suite": name, "kernel": "mul_mat_id decode gate+up+swiglu fused", "type": "Q4_K",
+                      "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": 1, "top_k": k,
+                      "us": round(msf * 1e3, 3), "GB/s": round(algf / msf / 1e6, 1),
+                      "unfused_3_launches_us": round(msu * 1e3, 3)})
+                del gs
             del ws
             torch.cuda.empty_cache()
     elif name == "ffn":

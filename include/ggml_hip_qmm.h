@@ -84,8 +84,9 @@ int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64
  * Decode GEMV of one f32 activation column with the Q8_1 quantization fused
  * in: dst[r] = sum_k W[r,k] * q8_1(x)[k], bit-identical to
  * hip_qmm_quantize_q8_1_planar followed by hip_qmm_mul_mat_vec on one column
- * (two-rows-per-wave kernel).  x 16-byte aligned, K a multiple of 32 and at
- * most 4096 (2048 for Q8_0).  The MMVQ path of mmvq.zig:275-300 with the
+ * (two-rows-per-wave kernel).  x 16-byte aligned, K a multiple of the block
+ * size and at most 32768; hip_qmm_mul_mat_vec_fused without a gate or a
+ * bias.  The MMVQ path of mmvq.zig:275-300 with the
  * quantizer launch of mmvq.zig:633-643 folded in (the quantize-in-GEMV
  * prologue of the fusion arguments, mmvq.zig:552-622).
  */
@@ -120,6 +121,24 @@ int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64_t nrows, i
 int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
                               int64_t row_stride, const float *x, const float *bias, const float *gate_bias,
                               int glu_op, float glu_alpha, float glu_limit, float *dst, void *stream);
+
+/*
+ * hip_qmm_mul_mat_vec_fused over the (token, slot) pairs of a MUL_MAT_ID
+ * with few tokens: the reference's MMVQ with ids and its fusion arguments
+ * (src/ggml/cuda/mmvq.zig:531-622; MUL_MAT_ID gate/up/GLU fusion,
+ * src/ggml/cuda/fusion.zig:1153-1306, 1308-1390).  For pair (t, s) with
+ * expert e = ids[t*ids_stride + s] and column x + (t*ne11 + s % ne11)*x_row_stride:
+ *   u = W_e . q8_1(x);  w_gate == NULL: row = u;  else row = glu(glu_op, Wg_e . q8_1(x), u)
+ * written at dst + (t*n_ids + s)*dst_row_stride; an id outside [0, n_as) writes
+ * a zero row.  W_e = w + e*expert_stride (Wg_e likewise).  n_tokens*n_ids at most
+ * 65535; x 16-byte aligned with x_row_stride a multiple of 4; the limits of
+ * hip_qmm_mul_mat_vec_fused otherwise.  No workspace.
+ */
+int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                 int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
+                                 int64_t ne11, int64_t n_tokens, int64_t x_row_stride, const int32_t *ids,
+                                 int64_t n_ids, int64_t ids_stride, int glu_op, float glu_alpha, float glu_limit,
+                                 float *dst, int64_t dst_row_stride, void *stream);
 
 /*
  * Standalone GLU over rows of f32 (ggml_compute_forward_glu,
@@ -202,11 +221,15 @@ size_t hip_qmm_mul_mat_id_workspace_size(int type, int64_t K, int64_t n_as, int6
  * x + (t*ne11 + i11)*x_row_stride (ne11 = 1 broadcasts one row per token,
  * ne11 = n_ids gives one per slot); ids[t*ids_stride + s] selects the expert
  * of slot s of token t; dst row (t, s) at dst + (t*n_ids + s)*dst_row_stride.
- * An id of -1 (or any id outside [0, n_as)) yields a zero row.  Expert
- * grouping runs on the device (no host synchronisation); replaces
- * ggml_cuda_mul_mat_id (src/ggml/cuda/mulmat.zig:669-800) and
- * mm_ids_helper (src/ggml/cuda/mmid.zig:32-90).  K a multiple of 256; at
- * most 1024 experts.
+ * An id of -1 (or any id outside [0, n_as)) yields a zero row.  Up to 8
+ * tokens (the reference's MMVQ-with-ids batch limit on AMD,
+ * src/ggml/cuda/mmvq.zig:116-125) it runs hip_qmm_mul_mat_id_vec_fused
+ * without a gate: one launch, no workspace touched.  Above that, expert
+ * grouping runs on the device (no host synchronisation) and feeds the
+ * grouped MMQ; replaces ggml_cuda_mul_mat_id
+ * (src/ggml/cuda/mulmat.zig:669-800) and mm_ids_helper
+ * (src/ggml/cuda/mmid.zig:32-90).  K a multiple of 256; at most 1024
+ * experts.
  */
 int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                        int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,

@@ -701,11 +701,61 @@ bool launch_fused(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gat
     return true;
 }
 
+// The MUL_MAT_ID pair of an MoE FFN over at most 8 tokens (the reference's
+// MMVQ-with-ids limit, mmvq.zig:116-125): same expert weights' type, shape
+// and strides, the same activations and ids, a split non-swapped GLU of a
+// fused op, dense rows the ids entry point addresses.
+bool gate_up_id_fusable(const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *glu) {
+    const ggml_tensor *wu = up->src[0], *wg = gate->src[0], *x = up->src[1];
+    const int op = glu->op_params[0];
+    if (op != HIP_QMM_GLU_GEGLU && op != HIP_QMM_GLU_SWIGLU && op != HIP_QMM_GLU_SWIGLU_OAI &&
+        op != HIP_QMM_GLU_SWIGLU_CLAMP)
+        return false;
+    if (glu->op_params[1] != 0 || !glu->src[1] || glu->type != GGML_TYPE_F32 || glu->nb[0] != 4) return false;
+    if (wu->type != wg->type || !same_shape(wu, wg)) return false;
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (wu->nb[i] != wg->nb[i]) return false;
+    if (up->src[1] != gate->src[1] || up->src[2] != gate->src[2] || !same_shape(glu, up)) return false;
+    if (glu->nb[2] != (size_t)glu->ne[1] * glu->nb[1] || glu->nb[1] % 4) return false;
+    const int64_t K = wu->ne[0], n_tokens = x->ne[2];
+    const size_t walign = wu->type == GGML_TYPE_Q4_K ? 16 : 2;
+    return n_tokens <= 8 && n_tokens * glu->ne[1] <= 65535 && K % 32 == 0 && K <= 32768 &&
+           (uintptr_t)x->data % 16 == 0 && x->nb[1] % 16 == 0 && (uintptr_t)wu->data % walign == 0 &&
+           (uintptr_t)wg->data % walign == 0 && wu->nb[1] % walign == 0 && wu->nb[2] % walign == 0;
+}
+
+bool launch_fused_id(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *out,
+                     bool *ok) {
+    const ggml_tensor *w = up->src[0], *x = up->src[1], *ids = up->src[2];
+    const int64_t K = w->ne[0], M = w->ne[1];
+    const size_t ob = nbytes(out);
+    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids))) return false;
+    const int rc = hip_qmm_mul_mat_id_vec_fused(
+        w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
+        static_cast<const float *>(x->data), x->ne[1], x->ne[2], (int64_t)(x->nb[1] / 4),
+        static_cast<const int32_t *>(ids->data), ids->ne[0], (int64_t)(ids->nb[1] / 4), out->op_params[0],
+        op_param_f32(out, 2), op_param_f32(out, 3), static_cast<float *>(out->data), (int64_t)(out->nb[1] / 4),
+        ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_id_vec_fused", out);
+    return true;
+}
+
 // Nodes consumed by a fused launch at node i (0: none); *ok false on a failed launch.
 int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
-    if (fusion_disabled() || g->nodes[i]->op != GGML_OP_MUL_MAT) return 0;
+    if (fusion_disabled()) return 0;
     auto node = [&](int k) { return k < g->n_nodes ? g->nodes[k] : nullptr; };
     auto is = [&](int k, int op) { return node(k) && node(k)->op == op && ggml_backend_hip_op_supported(node(k)); };
+    if (g->nodes[i]->op == GGML_OP_MUL_MAT_ID) {
+        if (!is(i + 1, GGML_OP_MUL_MAT_ID) || !is(i + 2, GGML_OP_GLU)) return 0;
+        const ggml_tensor *glu = node(i + 2);
+        const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
+        const bool pair = (gate == node(i) && up == node(i + 1)) || (gate == node(i + 1) && up == node(i));
+        if (pair && gate_up_id_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
+            launch_fused_id(ctx, up, gate, glu, ok))
+            return 3;
+        return 0;
+    }
+    if (g->nodes[i]->op != GGML_OP_MUL_MAT) return 0;
     if (is(i + 1, GGML_OP_ADD) && is(i + 2, GGML_OP_MUL_MAT) && is(i + 3, GGML_OP_ADD) && is(i + 4, GGML_OP_GLU)) {
         const ggml_tensor *glu = node(i + 4);
         const ggml_tensor *ma = node(i), *aa = node(i + 1), *mb = node(i + 2), *ab = node(i + 3);

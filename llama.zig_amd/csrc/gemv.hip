@@ -466,18 +466,41 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
 // The dots and their combination are the two-rows-per-wave kernel's, in the
 // same order, so u and g equal that kernel's outputs bit for bit.  Biases are read at the start, from a valid address when absent (the
 // value is then unused), so no load sits behind a branch.
+//
+// IDS (MUL_MAT_ID with few tokens, the reference's MMVQ-with-ids path,
+// mmvq.zig:116-125, 531-622): grid y enumerates the (token t, slot s) pairs;
+// the pair's expert e = ids[t, s] selects the weights (w + e * expert_stride),
+// its column is x row t * ne11 + s % ne11, its result dst row t * n_ids + s.
+// An id outside [0, n_as) yields a zero row, as the CPU path's -1 does
+// (src/ggml/cpu/mulmat.zig:555-777).
 constexpr int FX_MAXK = 32768;
 
-template <int TYPE, int FW, int R, bool GATE>
+struct FxIds {
+    const int32_t *ids;
+    int64_t ids_stride, x_row_stride, expert_stride, dst_row_stride;
+    int n_ids, ne11, n_as, n_pairs;
+};
+
+template <int TYPE, int FW, int R, bool GATE, bool IDS, int SEG>
 __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restrict__ w,
                                                              const uint8_t *__restrict__ wg, int K32, int64_t nrows,
                                                              int64_t row_stride, const float *x,
                                                              const float *bias, const float *gbias, int glu_op,
-                                                             float alpha, float limit, float *__restrict__ dst) {
+                                                             float alpha, float limit, float *__restrict__ dst,
+                                                             FxIds fi) {
     using F = Fmt<TYPE>;
+    int expert = 0;
+    if constexpr (IDS) {
+        const int p = blockIdx.y;
+        const int t = p / fi.n_ids, slot = p - t * fi.n_ids;
+        x += (int64_t)(t * fi.ne11 + slot % fi.ne11) * fi.x_row_stride;
+        dst += (int64_t)p * fi.dst_row_stride;
+        expert = __builtin_amdgcn_readfirstlane(fi.ids[(int64_t)t * fi.ids_stride + slot]);
+    }
     constexpr int NM = GATE ? 2 : 1;
-    constexpr int CH = 8 * 64 * FW;  // activation values per prologue pass
-    constexpr int STEP = 64 * F::W;
+    constexpr int NSEG = 64 / SEG;            // weight rows side by side in a wave
+    constexpr int CH = 8 * 64 * FW;           // activation values per prologue pass
+    constexpr int STEP = SEG * F::W;          // K per step of a segment
     extern __shared__ __align__(16) uint8_t fx_lds[];
     int8_t *aq = reinterpret_cast<int8_t *>(fx_lds);
     uint32_t *ad = reinterpret_cast<uint32_t *>(fx_lds + K32);  // K32 % 32 == 0
@@ -489,20 +512,36 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     const float4 xa = *reinterpret_cast<const float4 *>(x + kqc);
     const float4 xb = *reinterpret_cast<const float4 *>(x + kqc + 4);
     const int lane = threadIdx.x & 63;
+    const int seg = lane / SEG, sl = lane % SEG;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * R;
-    const int64_t brow = row0 + (lane < R ? lane : 0);
-    const int64_t browc = brow < nrows ? brow : nrows - 1;
-    const float bu = *(bias ? bias + browc : x);
-    const float bg = GATE ? *(gbias ? gbias + browc : x) : 0.0f;
+    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * (R * NSEG);  // the wave's first row
+    // lane rows: row0 + r * NSEG + seg, clamped for loading
+    int64_t rowc[R];
+    float bu[R], bg[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int64_t row = row0 + r * NSEG + seg;
+        rowc[r] = row < nrows ? row : nrows - 1;
+        bu[r] = *(bias ? bias + rowc[r] : x);
+        bg[r] = GATE ? *(gbias ? gbias + rowc[r] : x) : 0.0f;
+    }
     asm volatile("" ::: "memory");  // keep them ahead of the weight loads
+    if constexpr (IDS) {
+        if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its only barrier
+#pragma unroll
+            for (int r = 0; r < R; ++r)
+                if (sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
+            return;
+        }
+        w += (int64_t)expert * fi.expert_stride;
+        if constexpr (GATE) wg += (int64_t)expert * fi.expert_stride;
+    }
     const uint8_t *rows[NM][R];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-            rows[m][r] = (m ? wg : w) + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride;
-    int kl = lane * F::W;
+        for (int r = 0; r < R; ++r) rows[m][r] = (m ? wg : w) + rowc[r] * row_stride;
+    int kl = sl * F::W;
     bool live = kl < K32;
     int klc = live ? kl : 0;  // lanes past K load a valid slice and add nothing
     Wt<TYPE> wt[NM][R];
@@ -550,7 +589,7 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     // case runs on, and with many waves per SIMD the other waves cover the
     // latency.
     for (int k0 = STEP; k0 < K32; k0 += STEP) {
-        kl = k0 + lane * F::W;
+        kl = k0 + sl * F::W;
         live = kl < K32;
         klc = live ? kl : 0;
 #pragma unroll
@@ -559,14 +598,16 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
             for (int r = 0; r < R; ++r) wt[m][r].load(rows[m][r], klc);
         contract(wt);
     }
+    // Segment sums land in each segment's last lane, which writes its rows.
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float u = wave_sum(acc[0][r]);
-        const float g = GATE ? wave_sum(acc[NM - 1][r]) : 0.0f;
-        if (lane == r && row0 + r < nrows) {
-            if (bias) u += bu;
-            if constexpr (GATE) u = glu_apply(glu_op, gbias ? g + bg : g, u, alpha, limit);
-            dst[row0 + r] = u;
+        float u = seg_sum<SEG>(acc[0][r]);
+        const float g = GATE ? seg_sum<SEG>(acc[NM - 1][r]) : 0.0f;
+        const int64_t row = row0 + r * NSEG + seg;
+        if (sl == SEG - 1 && row < nrows) {
+            if (bias) u += bu[r];
+            if constexpr (GATE) u = glu_apply(glu_op, gbias ? g + bg[r] : g, u, alpha, limit);
+            dst[row] = u;
         }
     }
 }
@@ -752,19 +793,26 @@ extern "C" int hip_qmm_mul_mat_vec_f32(int type, const void *w, int64_t K, int64
 
 namespace {
 
-template <int TYPE, int FW, int R, bool GATE>
+template <int TYPE, int FW, int R, bool GATE, int SEG = 64>
 void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
-               const float *bias, const float *gbias, int op, float alpha, float limit, float *dst, hipStream_t s) {
-    const int64_t nblocks = (nrows + (int64_t)FW * R - 1) / ((int64_t)FW * R);
+               const float *bias, const float *gbias, int op, float alpha, float limit, float *dst, const FxIds *fi,
+               hipStream_t s) {
+    constexpr int64_t ROWS = (int64_t)FW * R * (64 / SEG);  // rows per workgroup
+    const int64_t nblocks = (nrows + ROWS - 1) / ROWS;
     const size_t lds = (size_t)K + (size_t)(K / QK8) * 4;
-    hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE>), dim3((unsigned)nblocks), dim3(64 * FW), lds, s, w, wg,
-                       (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst);
+    if (fi)
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, true, SEG>),
+                           dim3((unsigned)nblocks, (unsigned)fi->n_pairs), dim3(64 * FW), lds, s, w, wg, (int)K, nrows,
+                           row_stride, x, bias, gbias, op, alpha, limit, dst, *fi);
+    else
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, false, SEG>), dim3((unsigned)nblocks), dim3(64 * FW), lds,
+                           s, w, wg, (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, FxIds{});
 }
 
 template <int TYPE>
 void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride,
                     const float *x, const float *bias, const float *gbias, int op, float alpha, float limit,
-                    float *dst, hipStream_t s) {
+                    float *dst, const FxIds *fi, hipStream_t s) {
     // Without a gate: 16 waves per workgroup on large matrices, 8 otherwise
     // (the plain fused GEMV's measured choice).  Gated, measured on Q4_K
     // (K = 2048..8192): from 8192 rows 8 waves of 2 rows of each matrix
@@ -772,27 +820,43 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
     // waves of 1, below that 4 waves of 1 (3.1 vs 3.4 us at 768x2048: more
     // workgroups on a small grid).  Q6_K and Q8_0 keep 16 waves of 1 row on
     // large matrices: two rows of each matrix would cost Q6_K 131 VGPRs.
+    // Rows of at most 16 (32) lane slices share a wave 4 (2) to a wave, one
+    // segment of lanes each, so short rows do not leave most lanes idle.
+    const int64_t lanes = (K + Fmt<TYPE>::W - 1) / Fmt<TYPE>::W;
+    if (lanes <= 16) {
+        if (wg) launch_fx<TYPE, 4, 1, true, 16>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        else launch_fx<TYPE, 8, 1, false, 16>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        return;
+    }
+    if (lanes <= 32) {
+        if (wg) launch_fx<TYPE, 4, 1, true, 32>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        else launch_fx<TYPE, 8, 1, false, 32>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        return;
+    }
     const bool big = nrows >= 8192;
     if (wg) {
         if (big && TYPE == TYPE_Q4_K)
-            launch_fx<TYPE, 8, 2, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+            launch_fx<TYPE, 8, 2, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
         else if (big)
-            launch_fx<TYPE, 16, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+            launch_fx<TYPE, 16, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
         else if (nrows >= 2048)
-            launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
-        else launch_fx<TYPE, 4, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+            launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        else launch_fx<TYPE, 4, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
     } else {
-        if (big) launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
-        else launch_fx<TYPE, 8, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, s);
+        if (big) launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        else launch_fx<TYPE, 8, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
     }
 }
 
 }  // namespace
 
-extern "C" int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
-                                         int64_t row_stride, const float *x, const float *bias,
-                                         const float *gate_bias, int glu_op, float glu_alpha, float glu_limit,
-                                         float *dst, void *stream) {
+namespace {
+
+// Shared checks and launch of the fusion-epilogue GEMV; fi selects the ids
+// mode (one grid row per (token, slot) pair).
+int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows, int64_t row_stride,
+                 const float *x, const float *bias, const float *gate_bias, int glu_op, float glu_alpha,
+                 float glu_limit, float *dst, const FxIds *fi, void *stream) {
     if (int e = check_shape(type, K, nrows, row_stride)) return e;
     if (!w || !x || !dst || K % QK8 != 0 || K > FX_MAXK || (uintptr_t)x % 16) return (int)hipErrorInvalidValue;
     const uintptr_t walign = type == TYPE_Q4_K ? 16 : 2;
@@ -806,14 +870,45 @@ extern "C" int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_
     const uint8_t *wb = (const uint8_t *)w, *gb = (const uint8_t *)w_gate;
     switch (type) {
     case TYPE_Q4_K:
-        launch_fx_type<TYPE_Q4_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        launch_fx_type<TYPE_Q4_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                                  fi, s);
         break;
     case TYPE_Q6_K:
-        launch_fx_type<TYPE_Q6_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        launch_fx_type<TYPE_Q6_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                                  fi, s);
         break;
     default:
-        launch_fx_type<TYPE_Q8_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst, s);
+        launch_fx_type<TYPE_Q8_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                                  fi, s);
         break;
     }
     return (int)hipGetLastError();
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                         int64_t row_stride, const float *x, const float *bias,
+                                         const float *gate_bias, int glu_op, float glu_alpha, float glu_limit,
+                                         float *dst, void *stream) {
+    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                        nullptr, stream);
+}
+
+extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                            int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
+                                            int64_t ne11, int64_t n_tokens, int64_t x_row_stride, const int32_t *ids,
+                                            int64_t n_ids, int64_t ids_stride, int glu_op, float glu_alpha,
+                                            float glu_limit, float *dst, int64_t dst_row_stride, void *stream) {
+    if (!ids || n_as <= 0 || n_as > 0x7FFFFFFF || n_tokens <= 0 || n_ids <= 0 || ids_stride < n_ids ||
+        (ne11 != 1 && ne11 != n_ids) || x_row_stride < K || x_row_stride % 4 || dst_row_stride < nrows)
+        return (int)hipErrorInvalidValue;
+    if (n_tokens * n_ids > 65535 || n_tokens * ne11 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    const int64_t walign = type == TYPE_Q4_K ? 16 : 2;
+    if (expert_stride < nrows * row_stride || expert_stride % walign || expert_stride > ((int64_t)1 << 40))
+        return (int)hipErrorInvalidValue;
+    const FxIds fi{ids, ids_stride, x_row_stride, expert_stride, dst_row_stride,
+                   (int)n_ids, (int)ne11, (int)n_as, (int)(n_tokens * n_ids)};
+    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op, glu_alpha, glu_limit, dst,
+                        &fi, stream);
 }

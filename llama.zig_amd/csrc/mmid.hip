@@ -193,6 +193,15 @@ extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nr
         return (int)hipErrorInvalidValue;
     if (ne11 != 1 && ne11 != n_ids) return (int)hipErrorInvalidValue;  // ggml_mul_mat_id's b.ne1 rule
     if (n_tokens * n_ids > 0x7FFFFFFF || n_tokens * ne11 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    // Up to 8 tokens (the reference's MMVQ-with-ids limit on AMD,
+    // mmvq.zig:116-125): one GEMV launch over the (token, slot) pairs, each
+    // quantizing its own column in LDS; no grouping, no workspace used.
+    const int64_t walign = type == TYPE_Q4_K ? 16 : 2;
+    if (n_tokens <= 8 && n_tokens * n_ids <= 65535 && K % 32 == 0 && K <= 32768 && (uintptr_t)x % 16 == 0 &&
+        x_row_stride % 4 == 0 && expert_stride % walign == 0)
+        return hip_qmm_mul_mat_id_vec_fused(type, w, nullptr, K, nrows, row_stride, expert_stride, n_as, x, ne11,
+                                            n_tokens, x_row_stride, ids, n_ids, ids_stride, 0, 0.0f, 0.0f, dst,
+                                            dst_row_stride, stream);
     const int bn = grouped_bn(n_tokens * n_ids, n_as);
     const MmidLayout L = layout(K, n_as, ne11, n_tokens, n_ids, bn);
     if (workspace_size < L.total || (uintptr_t)workspace % 256) return (int)hipErrorInvalidValue;

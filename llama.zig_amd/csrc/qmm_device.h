@@ -192,6 +192,22 @@ __device__ __forceinline__ float wave_sum(float x) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), 63));
 }
 
+// Sums over segments of SEG consecutive lanes (16, 32 or 64) with wave_sum's
+// first steps: the total of segment q lands in its last lane, (q+1)*SEG - 1,
+// with the same additions in the same order as wave_sum for those lanes (at
+// SEG = 64, lane 63 holds exactly wave_sum's result).
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float x) {
+    static_assert(SEG == 16 || SEG == 32 || SEG == 64, "segments of 16, 32 or 64 lanes");
+    x += dpp_or_zero<0x111, 0xf>(x);  // row_shr:1
+    x += dpp_or_zero<0x112, 0xf>(x);  // row_shr:2
+    x += dpp_or_zero<0x114, 0xf>(x);  // row_shr:4
+    x += dpp_or_zero<0x118, 0xf>(x);  // row_shr:8
+    if constexpr (SEG >= 32) x += dpp_or_zero<0x142, 0xa>(x);  // row_bcast:15 into rows 1 and 3
+    if constexpr (SEG == 64) x += dpp_or_zero<0x143, 0xc>(x);  // row_bcast:31 into rows 2 and 3
+    return x;
+}
+
 // ggml_glu_op values: positions in GGML_GLU_OP_NAME (src/ggml/types.zig:103-106).
 enum : int {
     GLU_REGLU = 0,

@@ -54,6 +54,9 @@ def lib():
         L.hip_qmm_mul_mat_vec_fused.restype = i32
         L.hip_qmm_mul_mat_vec_fused.argtypes = [i32, vp, vp, i64, i64, i64, vp, vp, vp, i32, ctypes.c_float,
                                                 ctypes.c_float, vp, vp]
+        L.hip_qmm_mul_mat_id_vec_fused.restype = i32
+        L.hip_qmm_mul_mat_id_vec_fused.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64,
+                                                   i64, i32, ctypes.c_float, ctypes.c_float, vp, i64, vp]
         L.hip_qmm_glu_f32.restype = i32
         L.hip_qmm_glu_f32.argtypes = [i32, ctypes.c_float, ctypes.c_float, i64, i64, vp, i64, vp, i64, vp, i64, vp]
         L.hip_qmm_add_f32.restype = i32
@@ -197,6 +200,32 @@ def mul_mat_vec_fused(qtype, w: torch.Tensor, K: int, x: torch.Tensor, w_gate=No
                                            _ptr(x), _ptr(bias) if bias is not None else None,
                                            _ptr(gate_bias) if gate_bias is not None else None, op, alpha, limit,
                                            _ptr(out), _stream()), "hip_qmm_mul_mat_vec_fused")
+    return out
+
+
+def mul_mat_id_vec_fused(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, w_gate=None, glu="SWIGLU",
+                         alpha=1.702, limit=7.0, out=None):
+    """MUL_MAT_ID over few tokens in one launch: row (t, s) = W_e x[t, s % ne11]
+    with e = ids[t, s], or glu(Wg_e x, W_e x) with w_gate; zero rows for ids
+    outside [0, n_as).  w / w_gate: uint8 [n_as, nrows, row_bytes]; x: f32
+    [n_tokens, ne11, K]; ids: int32 [n_tokens, n_ids]."""
+    _require_cuda(w, x, ids)
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    n_as, nrows, rb = w.shape
+    n_tokens, ne11, K = x.shape
+    n_ids = ids.shape[1]
+    if rb < row_size(t, K) or ids.shape[0] != n_tokens or ids.dtype != torch.int32:
+        raise HipQmmError("bad mul_mat_id shapes")
+    if w_gate is not None:
+        _require_cuda(w_gate)
+        if w_gate.shape != w.shape:
+            raise HipQmmError("w_gate must match w")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty((n_tokens, n_ids, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_id_vec_fused(t, _ptr(w), _ptr(w_gate) if w_gate is not None else None, K, nrows,
+                                              w.stride(1), w.stride(0), n_as, _ptr(x), ne11, n_tokens, K, _ptr(ids),
+                                              n_ids, n_ids, op, alpha, limit, _ptr(out), nrows, _stream()),
+           "hip_qmm_mul_mat_id_vec_fused")
     return out
 
 

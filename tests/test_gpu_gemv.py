@@ -76,12 +76,14 @@ def test_gemv_kernel_paths(tname, nrows, K, ncols):
 
 
 @pytest.mark.parametrize("tname,nrows,K", [("Q4_K", 4096, 4096), ("Q4_K", 5000, 1024), ("Q6_K", 4100, 4096),
-                                           ("Q8_0", 4096, 2048), ("Q8_0", 333, 96)])
+                                           ("Q8_0", 4096, 2048), ("Q8_0", 333, 96), ("Q4_K", 4096, 768),
+                                           ("Q6_K", 4100, 1536), ("Q8_0", 4097, 1024)])
 def test_gemv_fused_quantize(tname, nrows, K):
     """Quantize-in-GEMV for one column: bit-identical to the separate Q8_1
     quantizer followed by the two-rows-per-wave GEMV (which the unfused path
     takes for one column on >= 4096 rows), and within the gates of the CPU
-    path."""
+    path.  Short rows (at most 16 or 32 lane slices) run several rows per
+    wave in lane segments; their sums must still match bit for bit."""
     import ggml_hip as G
     t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, 1)
     fused = G.mul_mat_vec_f32(tname, w_d, K, x_d[0]).cpu().numpy()

@@ -311,3 +311,73 @@ def test_plugin_fuses_mul_mat_bias_and_runs_glu_alone(hb):
     # swapped: the second half of each row gates
     want = O.glu(O.GLU_GEGLU, hv[:, 32:], hv[:, :32])
     glu_matches(O.GLU_GEGLU, hv[:, 32:], hv[:, :32], hb.get(gl, np.float32, (3, 32)), want)
+
+
+# ---------------------------------------------------------------- MUL_MAT_ID (MoE decode)
+
+def _moe(tname, n_as, M, K, n_tokens, n_ids, seed):
+    t = TYPES[tname]
+    wu = O.quantize_rows(t, O.fill_normal(100 + seed, n_as * M * K, 0.0, 0.02).reshape(n_as * M, K)).reshape(n_as, M, -1)
+    wg = O.quantize_rows(t, O.fill_normal(200 + seed, n_as * M * K, 0.0, 0.02).reshape(n_as * M, K)).reshape(n_as, M, -1)
+    rng = np.random.default_rng(seed)
+    ids = np.stack([rng.choice(n_as, n_ids, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    x = O.fill_normal(300 + seed, n_tokens * K).reshape(n_tokens, 1, K)
+    return t, wu, wg, ids, x
+
+
+@pytest.mark.parametrize("tname,n_tokens,opname", [("Q4_K", 1, "SWIGLU"), ("Q4_K", 5, "GEGLU"),
+                                                    ("Q6_K", 2, "SWIGLU_OAI"), ("Q8_0", 8, "SWIGLU_CLAMP")])
+def test_fused_gate_up_glu_with_ids(tname, n_tokens, opname):
+    """MoE decode's gate / up / GLU over the selected experts in one launch:
+    every (token, slot) row equals the one-column fused kernel on its expert
+    bit for bit, and the whole passes the CPU gate (mul_mat_id twice + GLU)."""
+    import ggml_hip as G
+    n_as, M, K, n_ids = 16, 768, 1024, 4
+    t, wu, wg, ids, x = _moe(tname, n_as, M, K, n_tokens, n_ids, n_tokens)
+    wu_d, wg_d, x_d, ids_d = _dev(wu), _dev(wg), _dev(x), _dev(ids)
+    got = G.mul_mat_id_vec_fused(tname, wu_d, x_d, ids_d, w_gate=wg_d, glu=opname, alpha=ALPHA,
+                                 limit=LIMIT).cpu().numpy()
+    for tt in range(n_tokens):
+        for s in range(n_ids):
+            e = ids[tt, s]
+            one = G.mul_mat_vec_fused(tname, wu_d[e], K, x_d[tt, 0], w_gate=wg_d[e], glu=opname, alpha=ALPHA,
+                                      limit=LIMIT).cpu().numpy().reshape(-1)
+            np.testing.assert_array_equal(got[tt, s], one)
+    cu = O.mul_mat_id(t, wu, n_as, M, K, x, ids, nth=8)
+    cg = O.mul_mat_id(t, wg, n_as, M, K, x, ids, nth=8)
+    assert nmse(got, O.glu(OPS[opname], cg, cu, ALPHA, LIMIT)) < NMSE_GATE
+
+
+def test_plugin_fuses_moe_gate_up_glu(hb):
+    """{MUL_MAT_ID, MUL_MAT_ID, GLU} of one decode token fuses (intermediates
+    stay NaN) and equals the kernel-level fused call; unfused, the same."""
+    import ggml_hip as G
+    from ggml_hip import abi
+    n_as, M, K, n_tokens, n_ids = 16, 768, 1024, 1, 4
+    t, wu, wg, ids, x = _moe("Q4_K", n_as, M, K, n_tokens, n_ids, 7)
+    tw_u = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M, n_as], name=b"ffn_up_exps")
+    tw_g = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M, n_as], name=b"ffn_gate_exps")
+    tx = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1, n_tokens], name=b"x")
+    tids = abi.make_tensor(abi.GGML_TYPE_I32, [n_ids, n_tokens], name=b"ids")
+    up = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_ids, n_tokens], op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_u, tx, tids),
+                         name=b"up")
+    gate = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_ids, n_tokens], op=abi.GGML_OP_MUL_MAT_ID,
+                           srcs=(tw_g, tx, tids), name=b"gate")
+    glu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, gate, up, [M, n_ids, n_tokens])
+    hb.alloc([tw_u, tw_g], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([tx, tids, up, gate, glu], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(tw_u, wu)
+    hb.set(tw_g, wg)
+    hb.set(tx, x)
+    hb.set(tids, ids)
+    shape = (n_tokens, n_ids, M)
+    for tns in (up, gate, glu):
+        hb.set(tns, np.full(shape, np.nan, dtype=np.float32))
+    assert hb.compute([gate, up, glu]) == abi.GGML_STATUS_SUCCESS
+    assert np.isnan(hb.get(up, np.float32, shape)).all() and np.isnan(hb.get(gate, np.float32, shape)).all()
+    out = hb.get(glu, np.float32, shape)
+    want = G.mul_mat_id_vec_fused("Q4_K", _dev(wu), _dev(x), _dev(ids), w_gate=_dev(wg), glu="SWIGLU").cpu().numpy()
+    np.testing.assert_array_equal(out, want)
+    assert hb.compute([gate, up, glu], use_counts=False) == abi.GGML_STATUS_SUCCESS
+    assert not np.isnan(hb.get(up, np.float32, shape)).any()
+    np.testing.assert_array_equal(hb.get(glu, np.float32, shape), out)

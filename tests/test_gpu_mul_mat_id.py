@@ -97,3 +97,46 @@ def test_mul_mat_id_config4_qwen3_moe_gate():
     y = G.quantize_q8_1(torch.from_numpy(x[sub].reshape(-1, K)).cuda(), K).cpu().numpy()
     ideal = mul_mat_id_f64(t, wq, nrows, K, y, 1, ids[sub])
     assert max_err_scaled(got[sub], ideal) < F64_TOL
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("n_tokens,ne11", [(1, 1), (3, 1), (8, 1), (2, 4)])
+def test_mul_mat_id_few_tokens(tname, n_tokens, ne11):
+    """Up to 8 tokens run the one-launch GEMV over (token, slot) pairs: each
+    row equals the one-column fused GEMV of its expert bit for bit, ids of -1
+    or past n_as give zero rows, and the result passes the CPU gates."""
+    import ggml_hip as G
+    n_as, nrows, K, n_ids = 12, 320, 1024, 4
+    rng = np.random.default_rng(n_tokens * 10 + ne11)
+    ids = rng.integers(0, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    ids[0, 1] = -1
+    if n_tokens > 1:
+        ids[1, 2] = n_as + 3  # out of range: a zero row, like -1
+    x = np.array(acts(n_tokens * ne11, K)).reshape(n_tokens, ne11, K)
+    t = TYPES[tname]
+    wq = _experts(t, n_as, nrows, K)
+    w_d, x_d = torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda()
+    out = torch.full((n_tokens, n_ids, nrows), float("nan"), device="cuda")
+    got = G.mul_mat_id(tname, w_d, x_d, torch.from_numpy(ids).cuda(), out=out).cpu().numpy()
+    bad = (ids < 0) | (ids >= n_as)
+    assert np.all(got[bad] == 0.0)
+    for tt in range(n_tokens):
+        for s in range(n_ids):
+            if bad[tt, s]:
+                continue
+            one = G.mul_mat_vec_f32(tname, w_d[ids[tt, s]], K, x_d[tt, s % ne11]).cpu().numpy().reshape(-1)
+            np.testing.assert_array_equal(got[tt, s], one)
+    ok_ids = np.where(bad, -1, ids).astype(np.int32)
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x, ok_ids, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    y = G.quantize_q8_1(x_d.reshape(-1, K), K).cpu().numpy()
+    ideal = mul_mat_id_f64(t, wq, nrows, K, y, ne11, ok_ids)
+    assert max_err_scaled(got, ideal) < F64_TOL
+
+
+def test_mul_mat_id_nine_tokens_take_the_grouped_path():
+    """The boundary: 9 tokens go through grouping + grouped MMQ, with the same gates."""
+    n_as, nrows, K, n_tokens, n_ids = 8, 256, 512, 9, 2
+    ids = np.random.default_rng(3).integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    _check("Q4_K", n_as, nrows, K, x, ids)
