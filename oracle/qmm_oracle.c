@@ -48,12 +48,14 @@
 typedef struct { uint16_t d; int8_t qs[QK8_0]; } blk_q8_0;                  /* 34 B */
 typedef struct { uint16_t d; uint16_t s; int8_t qs[QK8_1]; } blk_q8_1;      /* 36 B */
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qs[QK_K / 2]; } blk_q4_K; /* 144 B */
+typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; } blk_q5_K; /* 176 B */
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_K;  /* 210 B */
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;                               /* 292 B */
 
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
 _Static_assert(sizeof(blk_q8_1) == 36, "q8_1");
 _Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
+_Static_assert(sizeof(blk_q5_K) == 176, "q5_K");
 _Static_assert(sizeof(blk_q6_K) == 210, "q6_K");
 _Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
 
@@ -63,6 +65,7 @@ size_t orc_type_size(int type) {
     case ORC_TYPE_Q8_0: return sizeof(blk_q8_0);
     case ORC_TYPE_Q8_1: return sizeof(blk_q8_1);
     case ORC_TYPE_Q4_K: return sizeof(blk_q4_K);
+    case ORC_TYPE_Q5_K: return sizeof(blk_q5_K);
     case ORC_TYPE_Q6_K: return sizeof(blk_q6_K);
     case ORC_TYPE_Q8_K: return sizeof(blk_q8_K);
     default: return 0;
@@ -73,7 +76,7 @@ int64_t orc_blck_size(int type) {
     switch (type) {
     case ORC_TYPE_F32: return 1;
     case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_1: return 32;
-    case ORC_TYPE_Q4_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
+    case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
     default: return 0;
     }
 }
@@ -443,52 +446,95 @@ static inline void pack_scale_pair(uint8_t *s, int j, uint8_t ls, uint8_t lm) {
     }
 }
 
+/* The body quantize_row_q4_K_ref and quantize_row_q5_K_ref share
+ * (k.zig:331-390 fitScalesK + packScalesK, then the levels against the
+ * rounded scales, :393-434 and :472-535): nmax 15, rmin -1, 20 steps for
+ * q4_K; nmax 31, rmin -0.5, 15 steps for q5_K.  Leaves d, dmin, the packed
+ * scales and the per-weight levels L. */
+static void k45_ref_levels(const float *x, int nmax, float rmin, int nstep, uint16_t *d_out, uint16_t *dmin_out,
+                           uint8_t *scales_out, uint8_t L[QK_K]) {
+    uint8_t Laux[32];
+    float mins[QK_K / 32], scales[QK_K / 32], weights[32];
+    float max_scale = 0, max_min = 0;
+    for (int j = 0; j < QK_K / 32; ++j) {           /* fitScalesK, k.zig:338-363 */
+        float sum_x2 = 0;
+        for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
+        const float av_x = sqrtf(sum_x2 / 32);
+        for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        scales[j] = make_qkx2_quants(32, nmax, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, rmin, 0.1f, nstep, 0);
+        if (scales[j] > max_scale) max_scale = scales[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    memset(scales_out, 0, K_SCALE_SIZE);
+    const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
+    const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
+    for (int j = 0; j < QK_K / 32; ++j) {
+        uint8_t ls = (uint8_t)(uint32_t)nearest_int(inv_scale * scales[j]);
+        uint8_t lm = (uint8_t)(uint32_t)nearest_int(inv_min * mins[j]);
+        ls = ls < 63 ? ls : 63;
+        lm = lm < 63 ? lm : 63;
+        pack_scale_pair(scales_out, j, ls, lm);
+    }
+    *d_out = FP16(max_scale / 63.0f);
+    *dmin_out = FP16(max_min / 63.0f);
+    for (int j = 0; j < QK_K / 32; ++j) {
+        uint8_t sc, m;
+        get_scale_min_k4(j, scales_out, &sc, &m);
+        const float d = F32(*d_out) * (float)sc;
+        if (d == 0) continue;
+        const float dm = F32(*dmin_out) * (float)m;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = nearest_int((x[32 * j + ii] + dm) / d);
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            L[32 * j + ii] = (uint8_t)l;
+        }
+    }
+}
+
+/* q4_K: level j and j+32 of each 64-weight span share a byte (k.zig:426-431). */
+static void pack_q4_levels(const uint8_t L[QK_K], uint8_t *q) {
+    for (int j = 0; j < QK_K; j += 64) {
+        for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
+        q += 32;
+    }
+}
+
+/* q5_K: the low four bits as q4_K, the fifth in qh, two bits per 64-weight
+ * span (k.zig:508-532; chunks.zig:586-609). */
+static void pack_q5_levels(const uint8_t L[QK_K], uint8_t *qh, uint8_t *ql) {
+    memset(qh, 0, QK_K / 8);
+    uint8_t m1 = 1, m2 = 2;
+    for (int n = 0; n < QK_K; n += 64) {
+        for (int j = 0; j < 32; ++j) {
+            int l1 = L[n + j];
+            if (l1 > 15) { l1 -= 16; qh[j] |= m1; }
+            int l2 = L[n + j + 32];
+            if (l2 > 15) { l2 -= 16; qh[j] |= m2; }
+            ql[j] = (uint8_t)(l1 | (l2 << 4));
+        }
+        m1 = (uint8_t)(m1 << 2);
+        m2 = (uint8_t)(m2 << 2);
+        ql += 32;
+    }
+}
+
 void orc_quantize_row_q4_K_ref(const float *x, void *vy, int64_t k) {
     blk_q4_K *y = (blk_q4_K *)vy;
-    const int64_t nb = k / QK_K;
-    uint8_t L[QK_K], Laux[32];
-    float mins[QK_K / 32], scales[QK_K / 32], weights[32];
-    for (int64_t i = 0; i < nb; ++i) {
-        float max_scale = 0, max_min = 0;
-        for (int j = 0; j < QK_K / 32; ++j) {           /* fitScalesK, k.zig:338-363 */
-            float sum_x2 = 0;
-            for (int l = 0; l < 32; ++l) sum_x2 += x[32 * j + l] * x[32 * j + l];
-            const float av_x = sqrtf(sum_x2 / 32);
-            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-            scales[j] = make_qkx2_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
-                                         -1.0f, 0.1f, 20, 0);
-            if (scales[j] > max_scale) max_scale = scales[j];
-            if (mins[j] > max_min) max_min = mins[j];
-        }
-        memset(y[i].scales, 0, K_SCALE_SIZE);
-        const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
-        const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
-        for (int j = 0; j < QK_K / 32; ++j) {
-            uint8_t ls = (uint8_t)(uint32_t)nearest_int(inv_scale * scales[j]);
-            uint8_t lm = (uint8_t)(uint32_t)nearest_int(inv_min * mins[j]);
-            ls = ls < 63 ? ls : 63;
-            lm = lm < 63 ? lm : 63;
-            pack_scale_pair(y[i].scales, j, ls, lm);
-        }
-        y[i].d = FP16(max_scale / 63.0f);
-        y[i].dmin = FP16(max_min / 63.0f);
-        for (int j = 0; j < QK_K / 32; ++j) {
-            uint8_t sc, m;
-            get_scale_min_k4(j, y[i].scales, &sc, &m);
-            const float d = F32(y[i].d) * (float)sc;
-            if (d == 0) continue;
-            const float dm = F32(y[i].dmin) * (float)m;
-            for (int ii = 0; ii < 32; ++ii) {
-                int l = nearest_int((x[32 * j + ii] + dm) / d);
-                l = l < 0 ? 0 : (l > 15 ? 15 : l);
-                L[32 * j + ii] = (uint8_t)l;
-            }
-        }
-        uint8_t *q = y[i].qs;
-        for (int j = 0; j < QK_K; j += 64) {
-            for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
-            q += 32;
-        }
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        k45_ref_levels(x, 15, -1.0f, 20, &y[i].d, &y[i].dmin, y[i].scales, L);
+        pack_q4_levels(L, y[i].qs);
+        x += QK_K;
+    }
+}
+
+/* quantize_row_q5_K_ref, k.zig:472-535. */
+void orc_quantize_row_q5_K_ref(const float *x, void *vy, int64_t k) {
+    blk_q5_K *y = (blk_q5_K *)vy;
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        k45_ref_levels(x, 31, -0.5f, 15, &y[i].d, &y[i].dmin, y[i].scales, L);
+        pack_q5_levels(L, y[i].qh, y[i].qs);
         x += QK_K;
     }
 }
@@ -515,55 +561,90 @@ void orc_dequantize_row_q4_K(const void *vx, float *y, int64_t k) {
     }
 }
 
-/* quantize_row_q4_K_impl with imatrix: chunks.zig:478-552 (fitScalesKImpl,
- * q4_KImpl, requantizeK). */
-static void q4_K_impl(const float *x, blk_q4_K *y, int64_t n_per_row, const float *qw_all) {
-    const int64_t nb = n_per_row / QK_K;
-    uint8_t L[QK_K], Laux[32], ls[QK_K / 32], lm[QK_K / 32];
-    float sw[QK_K / 32], mins[QK_K / 32], scales[QK_K / 32], weights[32];
-    for (int64_t i = 0; i < nb; ++i) {
-        float sum_x2 = 0;
-        for (int l = 0; l < QK_K; ++l) sum_x2 += x[l] * x[l];
-        const float sigma2 = 2 * sum_x2 / QK_K;
-        const float av_x = sqrtf(sigma2);
-        for (int j = 0; j < QK_K / 32; ++j) {
-            if (qw_all) {
-                const float *qw = qw_all + QK_K * i + 32 * j;
-                for (int l = 0; l < 32; ++l)
-                    weights[l] = qw[l] * sqrtf(sigma2 + x[32 * j + l] * x[32 * j + l]);
-            } else {
-                for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
-            }
-            float sumw = 0;
-            for (int l = 0; l < 32; ++l) sumw += weights[l];
-            sw[j] = sumw;
-            scales[j] = make_qkx3_quants(32, 15, x + 32 * j, weights, L + 32 * j, &mins[j], Laux,
-                                         -0.9f, 0.05f, 36, 0);
-        }
-        const float d_block = make_qp_quants(QK_K / 32, 63, scales, ls, sw);
-        const float m_block = make_qp_quants(QK_K / 32, 63, mins, lm, sw);
-        memset(y[i].scales, 0, K_SCALE_SIZE);
-        for (int j = 0; j < QK_K / 32; ++j) pack_scale_pair(y[i].scales, j, ls[j], lm[j]);
-        y[i].d = FP16(d_block);
-        y[i].dmin = FP16(m_block);
-        const float d_all = F32(y[i].d), dmin_all = F32(y[i].dmin);
-        for (int j = 0; j < QK_K / 32; ++j) {
-            uint8_t sc, m;
-            get_scale_min_k4(j, y[i].scales, &sc, &m);
-            const float d = d_all * (float)sc;
-            if (d == 0) continue;
-            const float dm = dmin_all * (float)m;
-            for (int ii = 0; ii < 32; ++ii) {
-                int l = nearest_int((x[32 * j + ii] + dm) / d);
-                l = l < 0 ? 0 : (l > 15 ? 15 : l);
-                L[32 * j + ii] = (uint8_t)l;
-            }
-        }
-        uint8_t *q = y[i].qs;
+/* dequantize_row_q5_K, k.zig:538-575. */
+void orc_dequantize_row_q5_K(const void *vx, float *y, int64_t k) {
+    const blk_q5_K *x = (const blk_q5_K *)vx;
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        const uint8_t *ql = x[i].qs, *qh = x[i].qh;
+        const float d = F32(x[i].d), min = F32(x[i].dmin);
+        int is = 0;
+        uint8_t sc, m, u1 = 1, u2 = 2;
         for (int j = 0; j < QK_K; j += 64) {
-            for (int l = 0; l < 32; ++l) q[l] = (uint8_t)(L[j + l] | (L[j + l + 32] << 4));
-            q += 32;
+            get_scale_min_k4(is + 0, x[i].scales, &sc, &m);
+            const float d1 = d * (float)sc, m1 = min * (float)m;
+            get_scale_min_k4(is + 1, x[i].scales, &sc, &m);
+            const float d2 = d * (float)sc, m2 = min * (float)m;
+            for (int l = 0; l < 32; ++l) *y++ = d1 * (float)((ql[l] & 0xF) + (qh[l] & u1 ? 16 : 0)) - m1;
+            for (int l = 0; l < 32; ++l) *y++ = d2 * (float)((ql[l] >> 4) + (qh[l] & u2 ? 16 : 0)) - m2;
+            ql += 32;
+            is += 2;
+            u1 = (uint8_t)(u1 << 2);
+            u2 = (uint8_t)(u2 << 2);
         }
+    }
+}
+
+/* quantize_row_q{4,5}_K_impl with imatrix: chunks.zig:478-626
+ * (fitScalesKImpl, q4_KImpl / q5_KImpl, requantizeK).  q5_K clamps the packed
+ * levels to 63 where q4_K does not (chunks.zig:535-538 vs 572-575). */
+static void k45_impl_levels(const float *x, int64_t i, const float *qw_all, int nmax, int clamp63,
+                            uint16_t *d_out, uint16_t *dmin_out, uint8_t *scales_out, uint8_t L[QK_K]) {
+    uint8_t Laux[32], ls[QK_K / 32], lm[QK_K / 32];
+    float sw[QK_K / 32], mins[QK_K / 32], scales[QK_K / 32], weights[32];
+    float sum_x2 = 0;
+    for (int l = 0; l < QK_K; ++l) sum_x2 += x[l] * x[l];
+    const float sigma2 = 2 * sum_x2 / QK_K;
+    const float av_x = sqrtf(sigma2);
+    for (int j = 0; j < QK_K / 32; ++j) {
+        if (qw_all) {
+            const float *qw = qw_all + QK_K * i + 32 * j;
+            for (int l = 0; l < 32; ++l) weights[l] = qw[l] * sqrtf(sigma2 + x[32 * j + l] * x[32 * j + l]);
+        } else {
+            for (int l = 0; l < 32; ++l) weights[l] = av_x + fabsf(x[32 * j + l]);
+        }
+        float sumw = 0;
+        for (int l = 0; l < 32; ++l) sumw += weights[l];
+        sw[j] = sumw;
+        scales[j] = make_qkx3_quants(32, nmax, x + 32 * j, weights, L + 32 * j, &mins[j], Laux, -0.9f, 0.05f, 36, 0);
+    }
+    const float d_block = make_qp_quants(QK_K / 32, 63, scales, ls, sw);
+    const float m_block = make_qp_quants(QK_K / 32, 63, mins, lm, sw);
+    memset(scales_out, 0, K_SCALE_SIZE);
+    for (int j = 0; j < QK_K / 32; ++j) {
+        const uint8_t a = clamp63 && ls[j] > 63 ? 63 : ls[j], b = clamp63 && lm[j] > 63 ? 63 : lm[j];
+        pack_scale_pair(scales_out, j, a, b);
+    }
+    *d_out = FP16(d_block);
+    *dmin_out = FP16(m_block);
+    const float d_all = F32(*d_out), dmin_all = F32(*dmin_out);
+    for (int j = 0; j < QK_K / 32; ++j) {            /* requantizeK */
+        uint8_t sc, m;
+        get_scale_min_k4(j, scales_out, &sc, &m);
+        const float d = d_all * (float)sc;
+        if (d == 0) continue;
+        const float dm = dmin_all * (float)m;
+        for (int ii = 0; ii < 32; ++ii) {
+            int l = nearest_int((x[32 * j + ii] + dm) / d);
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            L[32 * j + ii] = (uint8_t)l;
+        }
+    }
+}
+
+static void q4_K_impl(const float *x, blk_q4_K *y, int64_t n_per_row, const float *qw_all) {
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < n_per_row / QK_K; ++i) {
+        k45_impl_levels(x, i, qw_all, 15, 0, &y[i].d, &y[i].dmin, y[i].scales, L);
+        pack_q4_levels(L, y[i].qs);
+        x += QK_K;
+    }
+}
+
+static void q5_K_impl(const float *x, blk_q5_K *y, int64_t n_per_row, const float *qw_all) {
+    uint8_t L[QK_K];
+    for (int64_t i = 0; i < n_per_row / QK_K; ++i) {
+        k45_impl_levels(x, i, qw_all, 31, 1, &y[i].d, &y[i].dmin, y[i].scales, L);
+        pack_q5_levels(L, y[i].qh, y[i].qs);
         x += QK_K;
     }
 }
@@ -759,6 +840,11 @@ size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
         else for (int64_t r = 0; r < nrows; ++r)
             q4_K_impl(src + r * n_per_row, (blk_q4_K *)(out + (size_t)r * row_size), n_per_row, imatrix);
         break;
+    case ORC_TYPE_Q5_K:
+        if (!imatrix) orc_quantize_row_q5_K_ref(src, out, nrows * n_per_row);
+        else for (int64_t r = 0; r < nrows; ++r)
+            q5_K_impl(src + r * n_per_row, (blk_q5_K *)(out + (size_t)r * row_size), n_per_row, imatrix);
+        break;
     case ORC_TYPE_Q6_K:
         if (!imatrix) orc_quantize_row_q6_K_ref(src, out, nrows * n_per_row);
         else for (int64_t r = 0; r < nrows; ++r)
@@ -786,25 +872,42 @@ static inline void scratch_accumulate(dot_scratch *s, int32_t scale, const int8_
     for (int l = 0; l < 8; ++l) s->aux32[l] += scale * s->aux16[l];
 }
 
-static float vec_dot_q4_K_q8_K_generic(int n, const void *vx, const void *vy) {
-    const blk_q4_K *x = (const blk_q4_K *)vx;
+/* The body ggml_vec_dot_q4_K_q8_K_generic and _q5_K_ share (k.zig:262-353):
+ * q5_K adds 16 to a level whose qh bit is set.  `x` walks blocks of `bsize`
+ * bytes laid out as {d, dmin, scales[12], [qh[32]], qs[128]}. */
+static float vec_dot_q45_K_q8_K_generic(int n, const uint8_t *x, size_t bsize, int q5, const void *vy) {
     const blk_q8_K *y = (const blk_q8_K *)vy;
     const int nb = n / QK_K;
     dot_scratch sc;
     memset(&sc, 0, sizeof sc);
     float sumf = 0;
-    for (int i = 0; i < nb; ++i) {
+    for (int i = 0; i < nb; ++i, x += bsize) {
+        uint16_t xd, xdmin;
+        memcpy(&xd, x, 2);
+        memcpy(&xdmin, x + 2, 2);
+        const uint8_t *scales_p = x + 4;
+        const uint8_t *qh = q5 ? x + 16 : NULL;
+        const uint8_t *qs = x + (q5 ? 48 : 16);
         memset(sc.aux32, 0, sizeof sc.aux32);
         int a = 0, q4 = 0;
+        uint8_t m = 1;
         for (int c = 0; c < QK_K / 64; ++c) {
-            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(x[i].qs[q4 + l] & 0xF);
+            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(qs[q4 + l] & 0xF);
+            if (q5) {
+                for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(sc.aux8[a + l] + (qh[l] & m ? 16 : 0));
+                m = (uint8_t)(m << 1);
+            }
             a += 32;
-            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(x[i].qs[q4 + l] >> 4);
+            for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(qs[q4 + l] >> 4);
+            if (q5) {
+                for (int l = 0; l < 32; ++l) sc.aux8[a + l] = (int8_t)(sc.aux8[a + l] + (qh[l] & m ? 16 : 0));
+                m = (uint8_t)(m << 1);
+            }
             a += 32;
             q4 += 32;
         }
         uint8_t scales[8], mins[8];
-        for (int j = 0; j < 8; ++j) get_scale_min_k4(j, x[i].scales, &scales[j], &mins[j]);
+        for (int j = 0; j < 8; ++j) get_scale_min_k4(j, scales_p, &scales[j], &mins[j]);
         int32_t sumi = 0;
         for (int j = 0; j < QK_K / 16; ++j) sumi += (int32_t)y[i].bsums[j] * mins[j / 2];
         a = 0;
@@ -813,13 +916,22 @@ static float vec_dot_q4_K_q8_K_generic(int n, const void *vx, const void *vy) {
             const int32_t scale = scales[j];
             for (int l = 0; l < 4; ++l) { scratch_accumulate(&sc, scale, y[i].qs + q8, sc.aux8 + a); q8 += 8; a += 8; }
         }
-        const float d = F32(x[i].d) * y[i].d;
+        const float d = F32(xd) * y[i].d;
         for (int l = 0; l < 8; ++l) sc.sums[l] += d * (float)sc.aux32[l];
-        const float dmin = F32(x[i].dmin) * y[i].d;
+        const float dmin = F32(xdmin) * y[i].d;
         sumf -= dmin * (float)sumi;
     }
     for (int l = 0; l < 8; ++l) sumf += sc.sums[l];
     return sumf;
+}
+
+static float vec_dot_q4_K_q8_K_generic(int n, const void *vx, const void *vy) {
+    return vec_dot_q45_K_q8_K_generic(n, (const uint8_t *)vx, sizeof(blk_q4_K), 0, vy);
+}
+
+/* ggml_vec_dot_q5_K_q8_K_generic, k.zig:355-375. */
+static float vec_dot_q5_K_q8_K_generic(int n, const void *vx, const void *vy) {
+    return vec_dot_q45_K_q8_K_generic(n, (const uint8_t *)vx, sizeof(blk_q5_K), 1, vy);
 }
 
 static float vec_dot_q6_K_q8_K_generic(int n, const void *vx, const void *vy) {
@@ -1104,6 +1216,7 @@ static dot_fn pick_dot(int type, int impl) {
     (void)impl;
     switch (type) {
     case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_generic;
+    case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
     case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_generic;
     case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_generic;
     }
@@ -1141,6 +1254,19 @@ void orc_block_dots_q8_1(int type, const void *w, int64_t nrows, int64_t K, cons
                     for (int l = 0; l < 32; ++l) {
                         const uint8_t byte = x[b].qs[32 * (j / 2) + l];
                         const int q = (j & 1) ? (byte >> 4) : (byte & 0xF);
+                        s += q * yb->qs[l];
+                    }
+                    *out++ = s;
+                }
+        } else if (type == ORC_TYPE_Q5_K) {
+            const blk_q5_K *x = (const blk_q5_K *)row;
+            for (int64_t b = 0; b < K / QK_K; ++b)
+                for (int j = 0; j < 8; ++j) {
+                    const blk_q8_1 *yb = &y[b * 8 + j];
+                    int32_t s = 0;
+                    for (int l = 0; l < 32; ++l) {
+                        const uint8_t byte = x[b].qs[32 * (j / 2) + l];
+                        const int q = ((j & 1) ? (byte >> 4) : (byte & 0xF)) + ((x[b].qh[l] >> j) & 1) * 16;
                         s += q * yb->qs[l];
                     }
                     *out++ = s;
@@ -1188,6 +1314,16 @@ void orc_mul_mat_q8_1_f64(int type, const void *w, int64_t nrows, int64_t K, con
             double acc = 0.0;
             if (type == ORC_TYPE_Q4_K) {
                 const blk_q4_K *x = (const blk_q4_K *)row;
+                for (int64_t b = 0; b < K / QK_K; ++b)
+                    for (int j = 0; j < 8; ++j) {
+                        uint8_t sc, m;
+                        get_scale_min_k4(j, x[b].scales, &sc, &m);
+                        const blk_q8_1 *yb = &y[b * 8 + j];
+                        acc += (double)F32(x[b].d) * sc * F32(yb->d) * S[b * 8 + j] -
+                               (double)F32(x[b].dmin) * m * F32(yb->s);
+                    }
+            } else if (type == ORC_TYPE_Q5_K) {
+                const blk_q5_K *x = (const blk_q5_K *)row;
                 for (int64_t b = 0; b < K / QK_K; ++b)
                     for (int j = 0; j < 8; ++j) {
                         uint8_t sc, m;

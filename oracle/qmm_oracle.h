@@ -30,6 +30,7 @@ enum {
     ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q8_1 = 9,
     ORC_TYPE_Q4_K = 12,
+    ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
     ORC_TYPE_Q8_K = 15,
 };
@@ -51,11 +52,13 @@ uint64_t orc_fnv1a(const void *p, size_t n);
 
 /* reference quantizers / dequantizers */
 void orc_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_q5_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_1_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_K_ref(const float *x, void *y, int64_t k);
 void orc_dequantize_row_q4_K(const void *x, float *y, int64_t k);
+void orc_dequantize_row_q5_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q8_0(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q8_K(const void *x, float *y, int64_t k);

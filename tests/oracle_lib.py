@@ -12,9 +12,13 @@ import numpy as np
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 LIB_PATH = ROOT / "oracle" / "liborc_qmm.so"
 
-TYPE_F32, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q6_K, TYPE_Q8_K = 0, 8, 9, 12, 14, 15
-TYPE_IDS = {"Q8_0": TYPE_Q8_0, "Q8_1": TYPE_Q8_1, "Q4_K": TYPE_Q4_K, "Q6_K": TYPE_Q6_K, "Q8_K": TYPE_Q8_K}
-BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q8_1: (32, 36), TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210), TYPE_Q8_K: (256, 292)}
+TYPE_F32, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_K = 0, 8, 9, 12, 13, 14, 15
+TYPE_IDS = {"Q8_0": TYPE_Q8_0, "Q8_1": TYPE_Q8_1, "Q4_K": TYPE_Q4_K, "Q5_K": TYPE_Q5_K, "Q6_K": TYPE_Q6_K,
+            "Q8_K": TYPE_Q8_K}
+BLOCK = {TYPE_Q8_0: (32, 34), TYPE_Q8_1: (32, 36), TYPE_Q4_K: (256, 144), TYPE_Q5_K: (256, 176), TYPE_Q6_K: (256, 210),
+         TYPE_Q8_K: (256, 292)}
+_NAMES = {TYPE_Q4_K: "q4_K", TYPE_Q5_K: "q5_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_1: "q8_1",
+          TYPE_Q8_K: "q8_K"}
 IMPL_GENERIC, IMPL_AVX2 = 0, 1
 
 _lib = None
@@ -37,11 +41,11 @@ def lib():
         L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         L.orc_nearest_int.restype = ctypes.c_int
         L.orc_nearest_int.argtypes = [ctypes.c_float]
-        for n in ("q4_K", "q6_K", "q8_0", "q8_1", "q8_K"):
+        for n in ("q4_K", "q5_K", "q6_K", "q8_0", "q8_1", "q8_K"):
             f = getattr(L, f"orc_quantize_row_{n}_ref")
             f.restype = None
             f.argtypes = [vp, vp, i64]
-        for n in ("q4_K", "q6_K", "q8_0", "q8_K"):
+        for n in ("q4_K", "q5_K", "q6_K", "q8_0", "q8_K"):
             f = getattr(L, f"orc_dequantize_row_{n}")
             f.restype = None
             f.argtypes = [vp, vp, i64]
@@ -91,8 +95,7 @@ def row_bytes(t, k):
 def quantize_ref(t, x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.zeros(row_bytes(t, x.size), dtype=np.uint8)
-    name = {TYPE_Q4_K: "q4_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_1: "q8_1", TYPE_Q8_K: "q8_K"}[t]
-    getattr(lib(), f"orc_quantize_row_{name}_ref")(_p(x), _p(out), x.size)
+    getattr(lib(), f"orc_quantize_row_{_NAMES[t]}_ref")(_p(x), _p(out), x.size)
     return out
 
 
@@ -104,9 +107,8 @@ def quantize_rows(t, w):
 
 def dequantize(t, q, k):
     out = np.zeros(k, dtype=np.float32)
-    name = {TYPE_Q4_K: "q4_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_K: "q8_K"}[t]
     q = np.ascontiguousarray(q)
-    getattr(lib(), f"orc_dequantize_row_{name}")(_p(q), _p(out), k)
+    getattr(lib(), f"orc_dequantize_row_{_NAMES[t]}")(_p(q), _p(out), k)
     return out
 
 

@@ -46,6 +46,14 @@ def _unit_q4_k_blocks(nblocks):
     return b
 
 
+def _unit_q5_k_blocks(nblocks):
+    """Q5_K likewise: dequantized weight = sc_j * (q + 16 h)."""
+    b = RNG.integers(0, 256, size=(nblocks, 176), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    b[:, 2:4] = 0
+    return b
+
+
 def _unit_q6_k_blocks(nblocks):
     b = RNG.integers(0, 256, size=(nblocks, 210), dtype=np.uint8)
     b[:, 208:210] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
@@ -59,6 +67,7 @@ def _unit_q8_0_blocks(nblocks):
 
 
 @pytest.mark.parametrize("t,maker,group", [(O.TYPE_Q4_K, _unit_q4_k_blocks, 32),
+                                           (O.TYPE_Q5_K, _unit_q5_k_blocks, 32),
                                            (O.TYPE_Q6_K, _unit_q6_k_blocks, 16),
                                            (O.TYPE_Q8_0, _unit_q8_0_blocks, 32)])
 def test_block_dots_against_unit_scale_dequantization(t, maker, group):
@@ -91,12 +100,17 @@ def test_block_dots_against_unit_scale_dequantization(t, maker, group):
 
 def _scale_of(t, row, j):
     """Sub-block scale of a unit-scale block, read back through the
-    dequantizer: a block whose codes are all 1 (Q4_K) or all 33 (Q6_K)
+    dequantizer: a block whose codes are all 1 (Q4_K, Q5_K) or all 33 (Q6_K)
     dequantizes to the scale itself."""
-    bs = 144 if t == O.TYPE_Q4_K else 210
-    blk = row.reshape(-1, bs)[j // (8 if t == O.TYPE_Q4_K else 16)].copy()
+    bs = {O.TYPE_Q4_K: 144, O.TYPE_Q5_K: 176, O.TYPE_Q6_K: 210}[t]
+    blk = row.reshape(-1, bs)[j // (16 if t == O.TYPE_Q6_K else 8)].copy()
     if t == O.TYPE_Q4_K:
         blk[16:] = 0x11  # every nibble 1
+        deq = O.dequantize(t, blk, 256)
+        return deq[32 * (j % 8)]
+    if t == O.TYPE_Q5_K:
+        blk[16:48] = 0  # no fifth bits
+        blk[48:] = 0x11  # every nibble 1
         deq = O.dequantize(t, blk, 256)
         return deq[32 * (j % 8)]
     blk[0:128] = 0x11  # low 4 bits 1
@@ -106,7 +120,7 @@ def _scale_of(t, row, j):
     return deq[16 * sub]
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
 def test_mul_mat_q8_1_f64_is_the_dequantized_dot(t):
     nrows, K, ncols = 5, 768, 3
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
@@ -126,20 +140,21 @@ def test_mul_mat_q8_1_f64_is_the_dequantized_dot(t):
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12 * np.abs(want).max())
 
 
-def test_mul_mat_q8_1_f64_min_term():
-    """d = 0: a Q4_K weight is -dmin*m_j on its sub-block, and the formula's
-    min term uses s = f16(d8 * sum q) in place of d8 * sum q."""
+@pytest.mark.parametrize("t,bs", [(O.TYPE_Q4_K, 144), (O.TYPE_Q5_K, 176)])
+def test_mul_mat_q8_1_f64_min_term(t, bs):
+    """d = 0: a Q4_K / Q5_K weight is -dmin*m_j on its sub-block, and the
+    formula's min term uses s = f16(d8 * sum q) in place of d8 * sum q."""
     nrows, K = 4, 512
-    w = O.quantize_rows(O.TYPE_Q4_K, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
-    w = w.reshape(nrows, -1, 144).copy()
+    w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    w = w.reshape(nrows, -1, bs).copy()
     w[:, :, 0:2] = 0  # d = 0
     w = w.reshape(nrows, -1)
     x = RNG.standard_normal(K).astype(np.float32) + 0.3
     y, q8, d = _q8_1(x)
-    got = O.mul_mat_q8_1_f64(O.TYPE_Q4_K, w, nrows, K, y[None, :], 1)[0]
+    got = O.mul_mat_q8_1_f64(t, w, nrows, K, y[None, :], 1)[0]
     deq_y = (q8 * d[:, None]).reshape(-1)
     for r in range(nrows):
-        deq = O.dequantize(O.TYPE_Q4_K, w[r], K).astype(np.float64)
+        deq = O.dequantize(t, w[r], K).astype(np.float64)
         per_block = (deq * deq_y).reshape(-1, 32).sum(axis=1)
         want = per_block.sum()
         bound = 2.0 ** -11 * np.abs(per_block).sum() + 1e-30
@@ -147,10 +162,10 @@ def test_mul_mat_q8_1_f64_min_term():
         assert abs(want) > 10 * bound  # the min term is really there
 
 
-VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0}
+VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q5_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0}
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
 def test_mul_mat_generic_is_vec_dot_per_output(t):
     nrows, K, ncols = 7, 512, 4
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
