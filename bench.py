@@ -41,7 +41,7 @@ M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
 T_MMQ = 512
 
 
-BLOCKS = {"Q4_K": (256, 144), "Q6_K": (256, 210), "Q8_0": (32, 34)}
+BLOCKS = {"Q4_K": (256, 144), "Q5_K": (256, 176), "Q6_K": (256, 210), "Q8_0": (32, 34)}
 
 
 def q4k_row_bytes(k):
@@ -63,8 +63,8 @@ def random_blocks(torch, qtype, nrows, k, gen, device):
     blocks = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, generator=gen, device="cpu")
     def f16(v):
         return torch.full((nb,), v, dtype=torch.float16).view(torch.uint8).view(nb, 2)
-    if qtype == "Q4_K":
-        blocks[:, 0:2] = f16(2.5e-4)
+    if qtype in ("Q4_K", "Q5_K"):
+        blocks[:, 0:2] = f16(2.5e-4 if qtype == "Q4_K" else 1.2e-4)
         blocks[:, 2:4] = f16(4.0e-4)
     elif qtype == "Q6_K":
         blocks[:, 208:210] = f16(2.5e-4)
@@ -170,7 +170,7 @@ def run_suite(name, torch, G, dev, reps):
             shapes = [("Q4_K", 14336, 4096, "ffn_gate/up")]
             batches = (128, 512, 2048)
         else:
-            shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K") for k in (4096, 14336)]
+            shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K", "Q5_K") for k in (4096, 14336)]
             batches = (1, 32, 512)
         for qtype, M, Kx, label in shapes:
             ws, wb = copies(qtype, M, Kx)

@@ -55,6 +55,7 @@ enum ggml_type {
     GGML_TYPE_Q8_0 = 8,
     GGML_TYPE_Q8_1 = 9,
     GGML_TYPE_Q4_K = 12,
+    GGML_TYPE_Q5_K = 13,
     GGML_TYPE_Q6_K = 14,
     GGML_TYPE_Q8_K = 15,
     GGML_TYPE_I32 = 26,

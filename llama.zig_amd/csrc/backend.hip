@@ -59,13 +59,20 @@ TypeInfo type_info(int t) {
     case GGML_TYPE_Q8_0: return {32, 34, true};
     case GGML_TYPE_Q8_1: return {32, 36, true};
     case GGML_TYPE_Q4_K: return {256, 144, true};
+    case GGML_TYPE_Q5_K: return {256, 176, true};
     case GGML_TYPE_Q6_K: return {256, 210, true};
     case GGML_TYPE_Q8_K: return {256, 292, true};
     default: return {0, 0, false};
     }
 }
 
-bool weight_type(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0; }
+bool weight_type(int t) {
+    return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K || t == GGML_TYPE_Q8_0;
+}
+
+// Alignment the kernels read a weight type's blocks at (16 for the K-quants
+// with 144- / 176-byte blocks, 2 otherwise).
+size_t weight_align(int t) { return t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K ? 16 : 2; }
 
 size_t row_size(int t, int64_t ne) {
     const TypeInfo ti = type_info(t);
@@ -647,7 +654,7 @@ bool vec_fusable(const ggml_tensor *mm) {
         if (x->ne[i] != 1 || mm->ne[i] != 1 || (i > 1 && w->ne[i] != 1)) return false;
     const int64_t K = w->ne[0];
     if (K % 32 != 0 || K > 32768 || (uintptr_t)x->data % 16 != 0) return false;
-    const size_t walign = w->type == GGML_TYPE_Q4_K ? 16 : 2;
+    const size_t walign = weight_align(w->type);
     return (uintptr_t)w->data % walign == 0 && w->nb[1] % walign == 0 && mm->nb[0] == 4;
 }
 
@@ -718,7 +725,7 @@ bool gate_up_id_fusable(const ggml_tensor *up, const ggml_tensor *gate, const gg
     if (up->src[1] != gate->src[1] || up->src[2] != gate->src[2] || !same_shape(glu, up)) return false;
     if (glu->nb[2] != (size_t)glu->ne[1] * glu->nb[1] || glu->nb[1] % 4) return false;
     const int64_t K = wu->ne[0], n_tokens = x->ne[2];
-    const size_t walign = wu->type == GGML_TYPE_Q4_K ? 16 : 2;
+    const size_t walign = weight_align(wu->type);
     return n_tokens <= 8 && n_tokens * glu->ne[1] <= 65535 && K % 32 == 0 && K <= 32768 &&
            (uintptr_t)x->data % 16 == 0 && x->nb[1] % 16 == 0 && (uintptr_t)wu->data % walign == 0 &&
            (uintptr_t)wg->data % walign == 0 && wu->nb[1] % walign == 0 && wu->nb[2] % walign == 0;

@@ -10,6 +10,8 @@
 //                out += d_b*sc_bk*d8 * T_bk
 //   Q8_0 x Q8_1: S_b = sum_{l<32} q * q8, out += d_b*d8 * S_b
 //
+//   Q5_K x Q8_1: as Q4_K with q5 = nibble + 16 * (qh bit j of the element)
+//
 // Mapping: one 64-lane wavefront owns RPW consecutive weight rows and walks K
 // in steps of 64 lanes x W weights (W = 64 for the K-quants, 32 for Q8_0).
 // Within a step every lane owns a fixed K-slice: it loads that slice of the
@@ -33,6 +35,11 @@ template <>
 struct Fmt<TYPE_Q4_K> {
     static constexpr int W = 64;  // weights per lane per step
     static constexpr int NSUB = 2;  // integer block dots per lane per step
+};
+template <>
+struct Fmt<TYPE_Q5_K> {
+    static constexpr int W = 64;
+    static constexpr int NSUB = 2;
 };
 template <>
 struct Fmt<TYPE_Q6_K> {
@@ -62,6 +69,10 @@ struct Act<TYPE_Q4_K> {
         ds[1] = t.y;
     }
 };
+
+// Q5_K takes the activation slice as Q4_K does (64 values, two Q8_1 blocks).
+template <>
+struct Act<TYPE_Q5_K> : Act<TYPE_Q4_K> {};
 
 // Q6_K lane (sb, n, h) covers weights 256sb + 128n + 32g + 16h + [0,16), g=0..3.
 template <>
@@ -121,7 +132,7 @@ struct Wt<TYPE_Q4_K> {
         q[1] = ld_u128(blk + 16 + 32 * c + 16);
     }
     // Integer dots of the two 32-sub-blocks (j = 2c low nibbles, 2c+1 high).
-    __device__ __forceinline__ void dots(const Act<TYPE_Q4_K> &a, int S[2]) const {
+    __device__ __forceinline__ void dots(const Act<TYPE_Q4_K> &a, int S[2], int = 0) const {
         const uint32_t w[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
         const uint32_t av[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
                                  a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
@@ -135,6 +146,53 @@ struct Wt<TYPE_Q4_K> {
         S[1] = s1;
     }
     __device__ __forceinline__ float combine(const Act<TYPE_Q4_K> &a, const int S[2], int kl) const {
+        const int c = (kl % QK_K) / 64;
+        uint32_t sc0, m0, sc1, m1;
+        q4k_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
+        q4k_scale_min(2 * c + 1, hdr.y, hdr.z, hdr.w, sc1, m1);
+        const float d = h2f(hdr.x), dmin = h2f(hdr.x >> 16);
+        const float d80 = h2f(a.ds[0]), s80 = h2f(a.ds[0] >> 16);
+        const float d81 = h2f(a.ds[1]), s81 = h2f(a.ds[1] >> 16);
+        const float t = (float)S[0] * d80 * (float)sc0 + (float)S[1] * d81 * (float)sc1;
+        const float u = (float)m0 * s80 + (float)m1 * s81;
+        return d * t - dmin * u;
+    }
+};
+
+// Q5_K (block_q5_K {d, dmin, scales[12], qh[32], qs[128]}, 176 B): the lane's
+// 64-weight slice c reads the 16-byte header, its 32 qs bytes and all 32 qh
+// bytes, whose bits 2c and 2c+1 are the fifth bits of sub-blocks 2c and 2c+1
+// (quantize_row_q5_K_ref's packing, src/ggml/quants/k.zig:508-532).
+template <>
+struct Wt<TYPE_Q5_K> {
+    uint4 hdr, q[2], h[2];
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
+        const uint8_t *blk = row + (kl / QK_K) * Q5K_BYTES;
+        const int c = (kl % QK_K) / 64;
+        hdr = ld_u128(blk);
+        h[0] = ld_u128(blk + 16);
+        h[1] = ld_u128(blk + 32);
+        q[0] = ld_u128(blk + 48 + 32 * c);
+        q[1] = ld_u128(blk + 48 + 32 * c + 16);
+    }
+    __device__ __forceinline__ void dots(const Act<TYPE_Q5_K> &a, int S[2], int kl) const {
+        const int c = (kl % QK_K) / 64;
+        const uint32_t w[8] = {q[0].x, q[0].y, q[0].z, q[0].w, q[1].x, q[1].y, q[1].z, q[1].w};
+        const uint32_t hb[8] = {h[0].x, h[0].y, h[0].z, h[0].w, h[1].x, h[1].y, h[1].z, h[1].w};
+        const uint32_t av[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
+                                 a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t lo = (w[i] & 0x0F0F0F0Fu) | (((hb[i] >> (2 * c)) & 0x01010101u) << 4);
+            const uint32_t hi = ((w[i] >> 4) & 0x0F0F0F0Fu) | (((hb[i] >> (2 * c + 1)) & 0x01010101u) << 4);
+            s0 = dot4(lo, av[i], s0);
+            s1 = dot4(hi, av[8 + i], s1);
+        }
+        S[0] = s0;
+        S[1] = s1;
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_Q5_K> &a, const int S[2], int kl) const {
         const int c = (kl % QK_K) / 64;
         uint32_t sc0, m0, sc1, m1;
         q4k_scale_min(2 * c, hdr.y, hdr.z, hdr.w, sc0, m0);
@@ -162,7 +220,7 @@ struct Wt<TYPE_Q6_K> {
         sc = ld16_a2(blk + 192);
         d = ld_u16(blk + 208);
     }
-    __device__ __forceinline__ void dots(const Act<TYPE_Q6_K> &a, int T[4]) const {
+    __device__ __forceinline__ void dots(const Act<TYPE_Q6_K> &a, int T[4], int = 0) const {
         const uint32_t l0[4] = {ql0.x, ql0.y, ql0.z, ql0.w};
         const uint32_t l1[4] = {ql1.x, ql1.y, ql1.z, ql1.w};
         const uint32_t hh[4] = {qh.x, qh.y, qh.z, qh.w};
@@ -212,7 +270,7 @@ struct Wt<TYPE_Q8_0> {
         q0 = ld16_a2(blk + 2);
         q1 = ld16_a2(blk + 18);
     }
-    __device__ __forceinline__ void dots(const Act<TYPE_Q8_0> &a, int S[1]) const {
+    __device__ __forceinline__ void dots(const Act<TYPE_Q8_0> &a, int S[1], int = 0) const {
         int s = 0;
         s = dot4(q0.x, a.q[0].x, s);
         s = dot4(q0.y, a.q[0].y, s);
@@ -237,9 +295,9 @@ constexpr int WAVES_PER_BLOCK = 4;
 // 32-bit.
 // Occupancy target: one column of Q4_K / Q8_0 fits in 64 VGPRs without
 // spilling, which keeps 8 waves per SIMD so a 14336-row grid (7168 waves) is
-// resident in one round.  Q6_K and wider GEMVs would spill at that bound.
+// resident in one round.  Q5_K, Q6_K and wider GEMVs would spill at that bound.
 template <int TYPE, int NC>
-constexpr int gemv_min_waves() { return NC == 1 && TYPE != TYPE_Q6_K ? 8 : 1; }
+constexpr int gemv_min_waves() { return NC == 1 && TYPE != TYPE_Q6_K && TYPE != TYPE_Q5_K ? 8 : 1; }
 
 template <int TYPE, int NC, int RPW, int MODE>
 __global__ __launch_bounds__(64 * WAVES_PER_BLOCK, (gemv_min_waves<TYPE, NC>())) void gemv_kernel(
@@ -282,7 +340,7 @@ __global__ __launch_bounds__(64 * WAVES_PER_BLOCK, (gemv_min_waves<TYPE, NC>()))
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
                     int S[F::NSUB];
-                    wt[r].dots(a[c], S);
+                    wt[r].dots(a[c], S, kl);
                     if constexpr (MODE == 0) {
                         acc[r][c] += wt[r].combine(a[c], S, kl);
                     } else {
@@ -364,7 +422,7 @@ __global__ __launch_bounds__(256) void gemv_rows_kernel(
 #pragma unroll
             for (int c = 0; c < NC; ++c) {
                 int S[F::NSUB];
-                cur.dots(a[c], S);
+                cur.dots(a[c], S, klc);
                 const float v = cur.combine(a[c], S, klc);
                 acc[r][c] += live ? v : 0.0f;
             }
@@ -430,7 +488,7 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
 #pragma unroll
                 for (int c = 0; c < NC; ++c) {
                     int S[F::NSUB];
-                    wt[r].dots(a[c], S);
+                    wt[r].dots(a[c], S, kl);
                     acc[r][c] += wt[r].combine(a[c], S, kl);
                 }
         }
@@ -578,7 +636,7 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 int S[F::NSUB];
-                cur[m][r].dots(a, S);
+                cur[m][r].dots(a, S, klc);
                 const float v = cur[m][r].combine(a, S, klc);
                 acc[m][r] += live ? v : 0.0f;
             }
@@ -724,6 +782,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     int64_t bs, bb;
     switch (type) {
     case TYPE_Q4_K: bs = QK_K; bb = Q4K_BYTES; break;
+    case TYPE_Q5_K: bs = QK_K; bb = Q5K_BYTES; break;
     case TYPE_Q6_K: bs = QK_K; bb = Q6K_BYTES; break;
     case TYPE_Q8_0: bs = QK8; bb = Q80_BYTES; break;
     default: return (int)hipErrorInvalidValue;
@@ -731,7 +790,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     if (K % bs != 0 || K > (1 << 30) || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
     // row bases keep the blocks' natural alignment: 16 bytes for Q4_K (144-byte
     // blocks, read as dwordx4), 2 bytes for Q6_K / Q8_0 (read by ld16_a2)
-    if (type == TYPE_Q4_K ? (row_stride % 16) : (row_stride % 2)) return (int)hipErrorInvalidValue;
+    if (row_stride % block_align(type)) return (int)hipErrorInvalidValue;
     return 0;
 }
 
@@ -742,13 +801,13 @@ int dispatch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stri
     if (!w || !yqs || ncols < 1 || ncols > 8) return (int)hipErrorInvalidValue;
     if (MODE == 0 && (!yds || !dst || dst_col_stride < nrows)) return (int)hipErrorInvalidValue;
     if (MODE == 1 && !dots) return (int)hipErrorInvalidValue;
-    if (type == TYPE_Q4_K && ((uintptr_t)w % 16)) return (int)hipErrorInvalidValue;
-    if (type != TYPE_Q4_K && ((uintptr_t)w % 2)) return (int)hipErrorInvalidValue;
+    if ((uintptr_t)w % block_align(type)) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     switch (type) {
     case TYPE_Q4_K: return launch_type<TYPE_Q4_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    case TYPE_Q5_K: return launch_type<TYPE_Q5_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     case TYPE_Q6_K: return launch_type<TYPE_Q6_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     default: return launch_type<TYPE_Q8_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     }
@@ -859,7 +918,7 @@ int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t
                  float glu_limit, float *dst, const FxIds *fi, void *stream) {
     if (int e = check_shape(type, K, nrows, row_stride)) return e;
     if (!w || !x || !dst || K % QK8 != 0 || K > FX_MAXK || (uintptr_t)x % 16) return (int)hipErrorInvalidValue;
-    const uintptr_t walign = type == TYPE_Q4_K ? 16 : 2;
+    const uintptr_t walign = (uintptr_t)block_align(type);
     if ((uintptr_t)w % walign || (uintptr_t)w_gate % walign) return (int)hipErrorInvalidValue;
     if (!w_gate && gate_bias) return (int)hipErrorInvalidValue;
     if (w_gate && glu_op != GLU_REGLU && glu_op != GLU_GEGLU && glu_op != GLU_SWIGLU && glu_op != GLU_SWIGLU_OAI &&
@@ -871,6 +930,10 @@ int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t
     switch (type) {
     case TYPE_Q4_K:
         launch_fx_type<TYPE_Q4_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                                  fi, s);
+        break;
+    case TYPE_Q5_K:
+        launch_fx_type<TYPE_Q5_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
                                   fi, s);
         break;
     case TYPE_Q6_K:
@@ -904,7 +967,7 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void 
         (ne11 != 1 && ne11 != n_ids) || x_row_stride < K || x_row_stride % 4 || dst_row_stride < nrows)
         return (int)hipErrorInvalidValue;
     if (n_tokens * n_ids > 65535 || n_tokens * ne11 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-    const int64_t walign = type == TYPE_Q4_K ? 16 : 2;
+    const int64_t walign = block_align(type);
     if (expert_stride < nrows * row_stride || expert_stride % walign || expert_stride > ((int64_t)1 << 40))
         return (int)hipErrorInvalidValue;
     const FxIds fi{ids, ids_stride, x_row_stride, expert_stride, dst_row_stride,

@@ -196,7 +196,7 @@ extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nr
     // Up to 8 tokens (the reference's MMVQ-with-ids limit on AMD,
     // mmvq.zig:116-125): one GEMV launch over the (token, slot) pairs, each
     // quantizing its own column in LDS; no grouping, no workspace used.
-    const int64_t walign = type == TYPE_Q4_K ? 16 : 2;
+    const int64_t walign = block_align(type);
     if (n_tokens <= 8 && n_tokens * n_ids <= 65535 && K % 32 == 0 && K <= 32768 && (uintptr_t)x % 16 == 0 &&
         x_row_stride % 4 == 0 && expert_stride % walign == 0)
         return hip_qmm_mul_mat_id_vec_fused(type, w, nullptr, K, nrows, row_stride, expert_stride, n_as, x, ne11,

@@ -104,6 +104,25 @@ struct AReg<TYPE_Q4_K> {
     }
 };
 
+// Q5_K: the Q4_K registers plus the block's 32 qh bytes, whose bits 4h..4h+3
+// are the fifth bits of the half's four sub-blocks.
+template <>
+struct AReg<TYPE_Q5_K> {
+    uint4 hdr, q[4], h[2];
+    __device__ __forceinline__ void load(const uint8_t *blk, int half) {
+        hdr = ld_u128(blk);
+        h[0] = ld_u128(blk + 16);
+        h[1] = ld_u128(blk + 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ld_u128(blk + 48 + 64 * half + 16 * i);
+    }
+    __device__ __forceinline__ void zero() {
+        hdr = h[0] = h[1] = make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = make_uint4(0, 0, 0, 0);
+    }
+};
+
 template <>
 struct AReg<TYPE_Q6_K> {
     uint4 l0[2], l1[2], qh[2], sc;
@@ -166,17 +185,34 @@ template <int TYPE, int BN>
 __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar) {
     const int t = threadIdx.x;
     const int r = t >> 1, half = t & 1;
-    if constexpr (TYPE == TYPE_Q4_K) {
+    if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) {
         int8_t *arow = sm.a + r * LDA;
         const uint32_t m = 0x0F0F0F0Fu;
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
             const int c = 2 * half + cc;
             const uint4 q0 = ar.q[2 * cc], q1 = ar.q[2 * cc + 1];
-            st16(arow + 64 * c + 0, q0.x & m, q0.y & m, q0.z & m, q0.w & m);
-            st16(arow + 64 * c + 16, q1.x & m, q1.y & m, q1.z & m, q1.w & m);
-            st16(arow + 64 * c + 32, (q0.x >> 4) & m, (q0.y >> 4) & m, (q0.z >> 4) & m, (q0.w >> 4) & m);
-            st16(arow + 64 * c + 48, (q1.x >> 4) & m, (q1.y >> 4) & m, (q1.z >> 4) & m, (q1.w >> 4) & m);
+            // Q5_K: bit j of qh[l] is the fifth bit of sub-block j's element l
+            uint4 f0 = make_uint4(0, 0, 0, 0), f1 = f0, g0 = f0, g1 = f0;
+            if constexpr (TYPE == TYPE_Q5_K) {
+                const uint32_t one = 0x01010101u;
+                const uint4 h0 = ar.h[0], h1 = ar.h[1];
+                const int j0 = 2 * c, j1 = 2 * c + 1;
+                f0 = make_uint4(((h0.x >> j0) & one) << 4, ((h0.y >> j0) & one) << 4, ((h0.z >> j0) & one) << 4,
+                                ((h0.w >> j0) & one) << 4);
+                f1 = make_uint4(((h1.x >> j0) & one) << 4, ((h1.y >> j0) & one) << 4, ((h1.z >> j0) & one) << 4,
+                                ((h1.w >> j0) & one) << 4);
+                g0 = make_uint4(((h0.x >> j1) & one) << 4, ((h0.y >> j1) & one) << 4, ((h0.z >> j1) & one) << 4,
+                                ((h0.w >> j1) & one) << 4);
+                g1 = make_uint4(((h1.x >> j1) & one) << 4, ((h1.y >> j1) & one) << 4, ((h1.z >> j1) & one) << 4,
+                                ((h1.w >> j1) & one) << 4);
+            }
+            st16(arow + 64 * c + 0, (q0.x & m) | f0.x, (q0.y & m) | f0.y, (q0.z & m) | f0.z, (q0.w & m) | f0.w);
+            st16(arow + 64 * c + 16, (q1.x & m) | f1.x, (q1.y & m) | f1.y, (q1.z & m) | f1.z, (q1.w & m) | f1.w);
+            st16(arow + 64 * c + 32, ((q0.x >> 4) & m) | g0.x, ((q0.y >> 4) & m) | g0.y, ((q0.z >> 4) & m) | g0.z,
+                 ((q0.w >> 4) & m) | g0.w);
+            st16(arow + 64 * c + 48, ((q1.x >> 4) & m) | g1.x, ((q1.y >> 4) & m) | g1.y, ((q1.z >> 4) & m) | g1.z,
+                 ((q1.w >> 4) & m) | g1.w);
 #pragma unroll
             for (int jj = 0; jj < 2; ++jj) {
                 const int j = 2 * c + jj;
@@ -256,6 +292,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     // partial[z][col][row] instead of dst
     float *__restrict__ partial) {
     using F = MmqFmt<TYPE>;
+    constexpr bool KMIN = TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K;  // scales with a min term
     __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
     const int64_t row0 = (int64_t)blockIdx.x * BM;
@@ -298,6 +335,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     auto gload = [&](int64_t kb) {
         if (a_ok) {
             if constexpr (TYPE == TYPE_Q4_K) areg.load(a_row + kb * Q4K_BYTES, ar_half);
+            else if constexpr (TYPE == TYPE_Q5_K) areg.load(a_row + kb * Q5K_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q6_K) areg.load(a_row + kb * Q6K_BYTES, ar_half);
             else areg.load(a_row + (kb * 8 + 4 * ar_half) * Q80_BYTES, 0);
         } else {
@@ -338,7 +376,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
                 const uint32_t v = breg.ds[p][i];
                 sm.bd8[0][off / 32 + i][c] = make_uint2(v & 0xFFFFu, 0u);
                 sm.bd8[1][off / 32 + i][c] = make_uint2(v << 16, 0u);
-                if constexpr (TYPE == TYPE_Q4_K) sm.bs8[c][off / 32 + i] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
+                if constexpr (KMIN) sm.bs8[c][off / 32 + i] = __builtin_bit_cast(_Float16, (uint16_t)(v >> 16));
             }
         }
     };
@@ -428,7 +466,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         __builtin_amdgcn_sched_barrier(0);
 
         if constexpr (TYPE != TYPE_Q8_0) {
-            // acc += d[r] * accb; Q4_K also subtracts dmin[r] * sum_j m_j[r] * s8_j[c]
+            // acc += d[r] * accb; Q4_K / Q5_K also subtract dmin[r] * sum_j m_j[r] * s8_j[c]
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
                 float dr[16], dm[16];
@@ -440,7 +478,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
                     dr[4 * v4 + 1] = t.y;
                     dr[4 * v4 + 2] = t.z;
                     dr[4 * v4 + 3] = t.w;
-                    if constexpr (TYPE == TYPE_Q4_K) {
+                    if constexpr (KMIN) {
                         const float4 u = *reinterpret_cast<const float4 *>(&sm.admin[rr]);
                         dm[4 * v4 + 0] = u.x;
                         dm[4 * v4 + 1] = u.y;
@@ -449,10 +487,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
                     }
                 }
                 v4h am;
-                if constexpr (TYPE == TYPE_Q4_K) am = *reinterpret_cast<const v4h *>(&sm.am[wr + 32 * i + li][4 * lh]);
+                if constexpr (KMIN) am = *reinterpret_cast<const v4h *>(&sm.am[wr + 32 * i + li][4 * lh]);
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {
-                    if constexpr (TYPE == TYPE_Q4_K) {
+                    if constexpr (KMIN) {
                         const v4h bm = *reinterpret_cast<const v4h *>(&sm.bs8[wc + 32 * j + li][4 * lh]);
                         const v16f zf = {0};
                         const v16f P = __builtin_amdgcn_mfma_f32_32x32x8f16(am, bm, zf, 0, 0, 0);
@@ -543,6 +581,8 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
     switch (type) {
     case TYPE_Q4_K:
         return (row_stride < K / QK_K * Q4K_BYTES || row_stride % 16 || (uintptr_t)w % 16) ? (int)hipErrorInvalidValue : 0;
+    case TYPE_Q5_K:
+        return (row_stride < K / QK_K * Q5K_BYTES || row_stride % 16 || (uintptr_t)w % 16) ? (int)hipErrorInvalidValue : 0;
     case TYPE_Q6_K:
         return (row_stride < K / QK_K * Q6K_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
     case TYPE_Q8_0:
@@ -595,6 +635,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
     case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     }
@@ -616,6 +657,7 @@ extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t n
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
     case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     }
