@@ -45,6 +45,7 @@
 #define K_SCALE_SIZE 12
 
 /* Block layouts: src/ggml/quants/blocks.zig:67-222 (ggml-common.h). */
+typedef struct { uint16_t d; uint8_t qs[16]; } blk_q4_0;                     /* 18 B */
 typedef struct { uint16_t d; int8_t qs[QK8_0]; } blk_q8_0;                  /* 34 B */
 typedef struct { uint16_t d; uint16_t s; int8_t qs[QK8_1]; } blk_q8_1;      /* 36 B */
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qs[QK_K / 2]; } blk_q4_K; /* 144 B */
@@ -52,6 +53,7 @@ typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_K;  /* 210 B */
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;                               /* 292 B */
 
+_Static_assert(sizeof(blk_q4_0) == 18, "q4_0");
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
 _Static_assert(sizeof(blk_q8_1) == 36, "q8_1");
 _Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
@@ -62,6 +64,7 @@ _Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
 size_t orc_type_size(int type) {
     switch (type) {
     case ORC_TYPE_F32: return 4;
+    case ORC_TYPE_Q4_0: return sizeof(blk_q4_0);
     case ORC_TYPE_Q8_0: return sizeof(blk_q8_0);
     case ORC_TYPE_Q8_1: return sizeof(blk_q8_1);
     case ORC_TYPE_Q4_K: return sizeof(blk_q4_K);
@@ -75,7 +78,7 @@ size_t orc_type_size(int type) {
 int64_t orc_blck_size(int type) {
     switch (type) {
     case ORC_TYPE_F32: return 1;
-    case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_1: return 32;
+    case ORC_TYPE_Q4_0: case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_1: return 32;
     case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
     default: return 0;
     }
@@ -737,6 +740,63 @@ void orc_dequantize_row_q6_K(const void *vx, float *y, int64_t k) {
 /* ------------------------------------------------------------------------ */
 /* Q8_0 / Q8_1: src/ggml/quants/legacy.zig:407-484 */
 
+/* quantize_row_q4_0_ref, legacy.zig:151-184: d = max / -8 (max the element of
+ * largest magnitude, with its sign), q = min(15, trunc-narrow(x / d + 8.5));
+ * element j and j + 16 share byte j. */
+void orc_quantize_row_q4_0_ref(const float *x, void *vy, int64_t k) {
+    blk_q4_0 *y = (blk_q4_0 *)vy;
+    for (int64_t i = 0; i < k / 32; ++i) {
+        float amax = 0.0f, max = 0.0f;
+        for (int j = 0; j < 32; ++j) {
+            const float v = x[i * 32 + j];
+            if (amax < fabsf(v)) {
+                amax = fabsf(v);
+                max = v;
+            }
+        }
+        const float d = max / -8.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = FP16(d);
+        for (int j = 0; j < 16; ++j) {
+            const float x0 = x[i * 32 + j] * id, x1 = x[i * 32 + 16 + j] * id;
+            int xi0 = trunc_i8(x0 + 8.5f), xi1 = trunc_i8(x1 + 8.5f);
+            xi0 = xi0 < 15 ? xi0 : 15;
+            xi1 = xi1 < 15 ? xi1 : 15;
+            y[i].qs[j] = (uint8_t)((uint8_t)xi0 | ((uint8_t)xi1 << 4));
+        }
+    }
+}
+
+/* dequantize_row_q4_0, legacy.zig:187-202. */
+void orc_dequantize_row_q4_0(const void *vx, float *y, int64_t k) {
+    const blk_q4_0 *x = (const blk_q4_0 *)vx;
+    for (int64_t i = 0; i < k / 32; ++i) {
+        const float d = F32(x[i].d);
+        for (int j = 0; j < 16; ++j) {
+            y[i * 32 + j] = (float)((x[i].qs[j] & 0x0F) - 8) * d;
+            y[i * 32 + j + 16] = (float)((x[i].qs[j] >> 4) - 8) * d;
+        }
+    }
+}
+
+/* quantize_row_q4_0_impl with an imatrix, chunks.zig:164-186: weights
+ * qw * sqrt(sigma2 + x^2) with sigma2 = mean x^2 over the row, levels from
+ * makeQxQuants(32, 8, ..., rmse_type 1). */
+static void q4_0_impl(const float *x, blk_q4_0 *y, int64_t n_per_row, const float *qw_all) {
+    float weight[32];
+    int8_t L[32];
+    float sum_x2 = 0;
+    for (int64_t j = 0; j < n_per_row; ++j) sum_x2 += x[j] * x[j];
+    const float sigma2 = sum_x2 / (float)n_per_row;
+    for (int64_t ib = 0; ib < n_per_row / 32; ++ib) {
+        const float *xb = x + 32 * ib, *qw = qw_all + 32 * ib;
+        for (int j = 0; j < 32; ++j) weight[j] = qw[j] * sqrtf(sigma2 + xb[j] * xb[j]);
+        const float d = make_qx_quants(32, 8, xb, L, 1, weight);
+        y[ib].d = FP16(d);
+        for (int j = 0; j < 16; ++j) y[ib].qs[j] = (uint8_t)((uint8_t)L[j] | ((uint8_t)L[j + 16] << 4));
+    }
+}
+
 void orc_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
     blk_q8_0 *y = (blk_q8_0 *)vy;
     const int64_t nb = k / QK8_0;
@@ -832,6 +892,11 @@ size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
     uint8_t *out = (uint8_t *)dst + (size_t)start_row * row_size;
     src += start;
     switch (type) {
+    case ORC_TYPE_Q4_0:
+        if (!imatrix) orc_quantize_row_q4_0_ref(src, out, nrows * n_per_row);
+        else for (int64_t r = 0; r < nrows; ++r)
+            q4_0_impl(src + r * n_per_row, (blk_q4_0 *)(out + (size_t)r * row_size), n_per_row, imatrix);
+        break;
     case ORC_TYPE_Q8_0:
         orc_quantize_row_q8_0_ref(src, out, nrows * n_per_row);
         break;
@@ -967,6 +1032,24 @@ static float vec_dot_q6_K_q8_K_generic(int n, const void *vx, const void *vy) {
     }
     float sumf = 0;
     for (int l = 0; l < 8; ++l) sumf += sc.sums[l];
+    return sumf;
+}
+
+/* ggml_vec_dot_q4_0_q8_0_generic, cpu/quants/legacy.zig:174-212. */
+static float vec_dot_q4_0_q8_0_generic(int n, const void *vx, const void *vy) {
+    const blk_q4_0 *x = (const blk_q4_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    float sumf = 0;
+    for (int ib = 0; ib < n / 32; ++ib) {
+        int32_t sumi0 = 0, sumi1 = 0;
+        for (int j = 0; j < 16; ++j) {
+            const int32_t v0 = (int32_t)(x[ib].qs[j] & 0x0F) - 8, v1 = (int32_t)(x[ib].qs[j] >> 4) - 8;
+            sumi0 += v0 * y[ib].qs[j];
+            sumi1 += v1 * y[ib].qs[j + 16];
+        }
+        const int32_t sumi = sumi0 + sumi1;
+        sumf += (float)sumi * F32(x[ib].d) * F32(y[ib].d);
+    }
     return sumf;
 }
 
@@ -1215,6 +1298,7 @@ static dot_fn pick_dot(int type, int impl) {
 #endif
     (void)impl;
     switch (type) {
+    case ORC_TYPE_Q4_0: return vec_dot_q4_0_q8_0_generic;  /* no AVX2 restatement: generic on every impl */
     case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_generic;
     case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
     case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_generic;
@@ -1226,9 +1310,12 @@ static dot_fn pick_dot(int type, int impl) {
 /* vec_dot_type and from_float per cpu/traits.zig:158-201 and x86/rows.zig:
  * K-quants take Q8_K (scalar ref on x86 too); Q8_0 takes Q8_0 (AVX2 row
  * quantizer on x86, the reference quantizer in the generic build). */
-static int vec_dot_type(int type) { return type == ORC_TYPE_Q8_0 ? ORC_TYPE_Q8_0 : ORC_TYPE_Q8_K; }
+static int vec_dot_type(int type) {
+    return type == ORC_TYPE_Q8_0 || type == ORC_TYPE_Q4_0 ? ORC_TYPE_Q8_0 : ORC_TYPE_Q8_K;
+}
 static from_float_fn pick_from_float(int type, int impl) {
-    if (type == ORC_TYPE_Q8_0) return impl == ORC_IMPL_AVX2 ? orc_quantize_row_q8_0_avx2 : orc_quantize_row_q8_0_ref;
+    if (vec_dot_type(type) == ORC_TYPE_Q8_0)
+        return impl == ORC_IMPL_AVX2 ? orc_quantize_row_q8_0_avx2 : orc_quantize_row_q8_0_ref;
     return orc_quantize_row_q8_K_ref;
 }
 
@@ -1297,6 +1384,17 @@ void orc_block_dots_q8_1(int type, const void *w, int64_t nrows, int64_t K, cons
                 for (int l = 0; l < 32; ++l) s += x[b].qs[l] * y[b].qs[l];
                 *out++ = s;
             }
+        } else if (type == ORC_TYPE_Q4_0) {
+            /* S = sum (q - 8) * q8 over the block: the offset applied in integers */
+            const blk_q4_0 *x = (const blk_q4_0 *)row;
+            for (int64_t b = 0; b < K / 32; ++b) {
+                int32_t s = 0;
+                for (int l = 0; l < 16; ++l) {
+                    s += ((x[b].qs[l] & 0x0F) - 8) * y[b].qs[l];
+                    s += ((x[b].qs[l] >> 4) - 8) * y[b].qs[l + 16];
+                }
+                *out++ = s;
+            }
         }
     }
 }
@@ -1337,6 +1435,9 @@ void orc_mul_mat_q8_1_f64(int type, const void *w, int64_t nrows, int64_t K, con
                 for (int64_t b = 0; b < K / QK_K; ++b)
                     for (int k = 0; k < 16; ++k)
                         acc += (double)F32(x[b].d) * x[b].scales[k] * F32(y[b * 8 + k / 2].d) * S[b * 16 + k];
+            } else if (type == ORC_TYPE_Q4_0) {
+                const blk_q4_0 *x = (const blk_q4_0 *)row;
+                for (int64_t b = 0; b < K / 32; ++b) acc += (double)F32(x[b].d) * F32(y[b].d) * S[b];
             } else {
                 const blk_q8_0 *x = (const blk_q8_0 *)row;
                 for (int64_t b = 0; b < K / 32; ++b) acc += (double)F32(x[b].d) * F32(y[b].d) * S[b];

@@ -27,6 +27,7 @@ extern "C" {
  * them: quants/golden.zig:74-133 `.type = ...`). */
 enum {
     ORC_TYPE_F32  = 0,
+    ORC_TYPE_Q4_0 = 2,
     ORC_TYPE_Q8_0 = 8,
     ORC_TYPE_Q8_1 = 9,
     ORC_TYPE_Q4_K = 12,
@@ -51,12 +52,14 @@ int      orc_nearest_int(float f);
 uint64_t orc_fnv1a(const void *p, size_t n);
 
 /* reference quantizers / dequantizers */
+void orc_quantize_row_q4_0_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q4_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q5_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_1_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_K_ref(const float *x, void *y, int64_t k);
+void orc_dequantize_row_q4_0(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q4_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q5_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q6_K(const void *x, float *y, int64_t k);

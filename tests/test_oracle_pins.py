@@ -60,6 +60,13 @@ def _unit_q6_k_blocks(nblocks):
     return b
 
 
+def _unit_q4_0_blocks(nblocks):
+    """Q4_0 with d = 1: dequantized weight = q - 8, the block dot's operand."""
+    b = RNG.integers(0, 256, size=(nblocks, 18), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    return b
+
+
 def _unit_q8_0_blocks(nblocks):
     b = RNG.integers(0, 256, size=(nblocks, 34), dtype=np.uint8)
     b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
@@ -69,10 +76,11 @@ def _unit_q8_0_blocks(nblocks):
 @pytest.mark.parametrize("t,maker,group", [(O.TYPE_Q4_K, _unit_q4_k_blocks, 32),
                                            (O.TYPE_Q5_K, _unit_q5_k_blocks, 32),
                                            (O.TYPE_Q6_K, _unit_q6_k_blocks, 16),
-                                           (O.TYPE_Q8_0, _unit_q8_0_blocks, 32)])
+                                           (O.TYPE_Q8_0, _unit_q8_0_blocks, 32),
+                                           (O.TYPE_Q4_0, _unit_q4_0_blocks, 32)])
 def test_block_dots_against_unit_scale_dequantization(t, maker, group):
     nrows, K = 3, 512
-    bs = 256 if t != O.TYPE_Q8_0 else 32
+    bs = 32 if t in (O.TYPE_Q8_0, O.TYPE_Q4_0) else 256
     w = maker(nrows * K // bs).reshape(nrows, -1)
     x = RNG.standard_normal(K).astype(np.float32) * 3
     y, q8, _ = _q8_1(x)
@@ -86,7 +94,7 @@ def test_block_dots_against_unit_scale_dequantization(t, maker, group):
             # the sub-block's integer scale: deq / q for any nonzero code; the
             # scale itself comes from the golden-pinned dequantizer
             prod = float(np.dot(deq[sl], q8[sl]))
-            if t == O.TYPE_Q8_0:
+            if t in (O.TYPE_Q8_0, O.TYPE_Q4_0):
                 assert got[r, j] == prod
                 checked += 1
                 continue
@@ -120,7 +128,7 @@ def _scale_of(t, row, j):
     return deq[16 * sub]
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0])
 def test_mul_mat_q8_1_f64_is_the_dequantized_dot(t):
     nrows, K, ncols = 5, 768, 3
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
@@ -162,10 +170,11 @@ def test_mul_mat_q8_1_f64_min_term(t, bs):
         assert abs(want) > 10 * bound  # the min term is really there
 
 
-VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q5_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0}
+VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q5_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0,
+       O.TYPE_Q4_0: O.TYPE_Q8_0}
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0])
 def test_mul_mat_generic_is_vec_dot_per_output(t):
     nrows, K, ncols = 7, 512, 4
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
