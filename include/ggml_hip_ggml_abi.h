@@ -52,6 +52,7 @@ extern "C" {
 enum ggml_type {
     GGML_TYPE_F32 = 0,
     GGML_TYPE_F16 = 1,
+    GGML_TYPE_Q4_0 = 2,
     GGML_TYPE_Q8_0 = 8,
     GGML_TYPE_Q8_1 = 9,
     GGML_TYPE_Q4_K = 12,

@@ -56,8 +56,8 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
         return hip_qmm_mmq(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, (uint8_t *)workspace + off,
                            workspace_size - off, stream);
     }
-    // Q8_0 rows whose length is not a multiple of 256 (the MMQ K-step): GEMV
-    // over column groups of 8.
+    // Q8_0 / Q4_0 rows whose length is not a multiple of 256 (the MMQ K-step):
+    // GEMV over column groups of 8.
     for (int64_t c0 = 0; c0 < ncols; c0 += 8) {
         const int64_t nc = ncols - c0 < 8 ? ncols - c0 : 8;
         const uint8_t *dsb = (const uint8_t *)ds + c0 * (Kp / QK8) * 4;

@@ -11,6 +11,7 @@
 //   Q8_0 x Q8_1: S_b = sum_{l<32} q * q8, out += d_b*d8 * S_b
 //
 //   Q5_K x Q8_1: as Q4_K with q5 = nibble + 16 * (qh bit j of the element)
+//   Q4_0 x Q8_1: S_b = sum_{l<32} (q - 8) * q8, out += d_b*d8 * S_b
 //
 // Mapping: one 64-lane wavefront owns RPW consecutive weight rows and walks K
 // in steps of 64 lanes x W weights (W = 64 for the K-quants, 32 for Q8_0).
@@ -48,6 +49,11 @@ struct Fmt<TYPE_Q6_K> {
 };
 template <>
 struct Fmt<TYPE_Q8_0> {
+    static constexpr int W = 32;
+    static constexpr int NSUB = 1;
+};
+template <>
+struct Fmt<TYPE_Q4_0> {
     static constexpr int W = 32;
     static constexpr int NSUB = 1;
 };
@@ -113,6 +119,24 @@ struct Act<TYPE_Q8_0> {
         q[0] = ld_u128(p);
         q[1] = ld_u128(p + 16);
         ds = dsp[kl / QK8];
+    }
+};
+
+// Q4_0: the Q8_0 slice plus its integer sum, which turns the dot of the raw
+// nibbles into the dot of q - 8 (computed once, shared by the wave's rows).
+template <>
+struct Act<TYPE_Q4_0> : Act<TYPE_Q8_0> {
+    int asum;
+    __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int kl) {
+        Act<TYPE_Q8_0>::load(qs, dsp, kl);
+        int s = dot4(q[0].x, 0x01010101u, 0);
+        s = dot4(q[0].y, 0x01010101u, s);
+        s = dot4(q[0].z, 0x01010101u, s);
+        s = dot4(q[0].w, 0x01010101u, s);
+        s = dot4(q[1].x, 0x01010101u, s);
+        s = dot4(q[1].y, 0x01010101u, s);
+        s = dot4(q[1].z, 0x01010101u, s);
+        asum = dot4(q[1].w, 0x01010101u, s);
     }
 };
 
@@ -257,6 +281,36 @@ struct Wt<TYPE_Q6_K> {
             t += (float)T[g] * h2f(a.ds[g]) * s;
         }
         return h2f(d) * t;
+    }
+};
+
+// Q4_0 (block_q4_0 {d, qs[16]}, 18 B): byte j holds element j (low nibble)
+// and element j + 16 (high nibble) (quantize_row_q4_0_ref,
+// src/ggml/quants/legacy.zig:151-184).
+template <>
+struct Wt<TYPE_Q4_0> {
+    uint4 q;
+    uint32_t d;
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
+        const uint8_t *blk = row + (kl / QK8) * Q40_BYTES;
+        d = ld_u16(blk);
+        q = ld16_a2(blk + 2);
+    }
+    __device__ __forceinline__ void dots(const Act<TYPE_Q4_0> &a, int S[1], int = 0) const {
+        const uint32_t m = 0x0F0F0F0Fu;
+        int s = 0;
+        s = dot4(q.x & m, a.q[0].x, s);
+        s = dot4(q.y & m, a.q[0].y, s);
+        s = dot4(q.z & m, a.q[0].z, s);
+        s = dot4(q.w & m, a.q[0].w, s);
+        s = dot4((q.x >> 4) & m, a.q[1].x, s);
+        s = dot4((q.y >> 4) & m, a.q[1].y, s);
+        s = dot4((q.z >> 4) & m, a.q[1].z, s);
+        s = dot4((q.w >> 4) & m, a.q[1].w, s);
+        S[0] = s - 8 * a.asum;
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_Q4_0> &a, const int S[1], int) const {
+        return h2f(d) * h2f(a.ds) * (float)S[0];
     }
 };
 
@@ -720,7 +774,7 @@ GemvKind choose(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (type == TYPE_Q4_K && K <= 4096 && ncols >= 2 && nrows >= (ncols == 2 ? 8192 : 4096))
         return nrows >= 8192 ? (ncols == 2 ? GemvKind::rows8 : GemvKind::rows16) : GemvKind::rows4;
     if (nrows <= 2048) return type == TYPE_Q4_K && ncols >= 5 ? GemvKind::ks2 : GemvKind::ks1;
-    if (type != TYPE_Q8_0 && K >= 8192 && nrows <= 4096) return GemvKind::ks4;
+    if (type != TYPE_Q8_0 && type != TYPE_Q4_0 && K >= 8192 && nrows <= 4096) return GemvKind::ks4;
     return GemvKind::pairs;
 }
 
@@ -785,6 +839,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     case TYPE_Q5_K: bs = QK_K; bb = Q5K_BYTES; break;
     case TYPE_Q6_K: bs = QK_K; bb = Q6K_BYTES; break;
     case TYPE_Q8_0: bs = QK8; bb = Q80_BYTES; break;
+    case TYPE_Q4_0: bs = QK8; bb = Q40_BYTES; break;
     default: return (int)hipErrorInvalidValue;
     }
     if (K % bs != 0 || K > (1 << 30) || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
@@ -809,6 +864,7 @@ int dispatch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stri
     case TYPE_Q4_K: return launch_type<TYPE_Q4_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     case TYPE_Q5_K: return launch_type<TYPE_Q5_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     case TYPE_Q6_K: return launch_type<TYPE_Q6_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    case TYPE_Q4_0: return launch_type<TYPE_Q4_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     default: return launch_type<TYPE_Q8_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     }
 }
@@ -938,6 +994,10 @@ int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t
         break;
     case TYPE_Q6_K:
         launch_fx_type<TYPE_Q6_K>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
+                                  fi, s);
+        break;
+    case TYPE_Q4_0:
+        launch_fx_type<TYPE_Q4_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
                                   fi, s);
         break;
     default:

@@ -76,7 +76,7 @@ struct Smem {
     // the column's d8 in K slot h: lanes 0-31 (K slots 0-3) read bd8[0],
     // lanes 32-63 (slots 4-7) read bd8[1], so only slot 0 pairs two nonzero
     // values and the MFMA returns exactly s_r * d8_c.
-    alignas(16) uint2 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K), sc_k (Q6_K) or d_b (Q8_0), exact in f16
+    alignas(16) uint2 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K, Q5_K), sc_k (Q6_K) or d_b (Q8_0, Q4_0), exact in f16
     alignas(16) uint2 bd8[2][8][BN];              // d8 per (Q8_1 block, column)
     alignas(16) float ad[BM];                        // d per row (Q4_K, Q6_K)
     alignas(16) float admin[BM];                     // dmin per row (Q4_K)
@@ -168,6 +168,28 @@ struct AReg<TYPE_Q8_0> {
     }
 };
 
+// Q4_0: as Q8_0, thread t owns blocks 4*(t%2) .. +4 of row t/2 in the step
+template <>
+struct AReg<TYPE_Q4_0> {
+    uint4 q[4];
+    uint32_t d[4];
+    __device__ __forceinline__ void load(const uint8_t *blk0, int) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const uint8_t *blk = blk0 + b * Q40_BYTES;
+            d[b] = ld_u16(blk);
+            q[b] = ld16_u(blk + 2);
+        }
+    }
+    __device__ __forceinline__ void zero() {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            d[b] = 0;
+            q[b] = make_uint4(0, 0, 0, 0);
+        }
+    }
+};
+
 __device__ __forceinline__ uint32_t f16_bits(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
@@ -179,6 +201,11 @@ __device__ __forceinline__ void st16(int8_t *dst, uint32_t a, uint32_t b, uint32
 __device__ __forceinline__ uint32_t minus32(uint32_t u) {
     // bytewise u - 32 for bytes in [0, 63], without borrows between bytes
     return ((u | 0x80808080u) - 0x20202020u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ uint32_t minus8(uint32_t u) {
+    // bytewise u - 8 for bytes in [0, 15], without borrows between bytes
+    return ((u | 0x80808080u) - 0x08080808u) ^ 0x80808080u;
 }
 
 template <int TYPE, int BN>
@@ -249,6 +276,19 @@ __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar
 #pragma unroll
         for (int i = 0; i < 8; ++i) sm.asc[8 * n + i][r] = make_uint2(f16_bits((float)(int8_t)byte_of(ar.sc, 8 * n + i)), 0u);
         if (half == 0) sm.ad[r] = h2f(ar.d);
+    } else if constexpr (TYPE == TYPE_Q4_0) {
+        // q - 8 as int8: low nibbles are elements 0..15, high nibbles 16..31
+        const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int blk = 4 * half + b;
+            int8_t *dst = sm.a + r * LDA + 32 * blk;
+            const uint4 q = ar.q[b];
+            st16(dst, minus8(q.x & m), minus8(q.y & m), minus8(q.z & m), minus8(q.w & m));
+            st16(dst + 16, minus8((q.x >> 4) & m), minus8((q.y >> 4) & m), minus8((q.z >> 4) & m),
+                 minus8((q.w >> 4) & m));
+            sm.asc[blk][r] = make_uint2(ar.d[b] & 0xFFFFu, 0u);
+        }
     } else {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
@@ -293,6 +333,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     float *__restrict__ partial) {
     using F = MmqFmt<TYPE>;
     constexpr bool KMIN = TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K;  // scales with a min term
+    constexpr bool LEGACY = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0;  // one scale per 32-block, no super-block
     __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
     const int64_t row0 = (int64_t)blockIdx.x * BM;
@@ -337,6 +378,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
             if constexpr (TYPE == TYPE_Q4_K) areg.load(a_row + kb * Q4K_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q5_K) areg.load(a_row + kb * Q5K_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q6_K) areg.load(a_row + kb * Q6K_BYTES, ar_half);
+            else if constexpr (TYPE == TYPE_Q4_0) areg.load(a_row + (kb * 8 + 4 * ar_half) * Q40_BYTES, 0);
             else areg.load(a_row + (kb * 8 + 4 * ar_half) * Q80_BYTES, 0);
         } else {
             areg.zero();
@@ -433,7 +475,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / NT, t = p % NT, i = t / TJ, j = t % TJ;
-            if constexpr (TYPE == TYPE_Q8_0) {
+            if constexpr (LEGACY) {
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[i][j][v] = fmaf((float)S[v], SC[v], acc[i][j][v]);
             } else if (g == 0) {
@@ -465,7 +507,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         }
         __builtin_amdgcn_sched_barrier(0);
 
-        if constexpr (TYPE != TYPE_Q8_0) {
+        if constexpr (!LEGACY) {
             // acc += d[r] * accb; Q4_K / Q5_K also subtract dmin[r] * sum_j m_j[r] * s8_j[c]
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
@@ -587,6 +629,8 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
         return (row_stride < K / QK_K * Q6K_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
     case TYPE_Q8_0:
         return (row_stride < K / QK8 * Q80_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
+    case TYPE_Q4_0:
+        return (row_stride < K / QK8 * Q40_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
     default:
         return (int)hipErrorInvalidValue;
     }
@@ -637,6 +681,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     }
 }
@@ -659,6 +704,7 @@ extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t n
     case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     }
 }

@@ -22,8 +22,10 @@ constexpr int Q4K_BYTES = 144;
 constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
 constexpr int Q80_BYTES = 34;
+constexpr int Q40_BYTES = 18;
 constexpr int64_t ROW_PAD = 512;  // activation row padding (MATRIX_ROW_PADDING)
 
+constexpr int TYPE_Q4_0 = 2;
 constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q4_K = 12;
 constexpr int TYPE_Q5_K = 13;
@@ -33,7 +35,7 @@ __host__ __device__ constexpr int64_t pad_k(int64_t k) { return (k + ROW_PAD - 1
 
 // Alignment of a weight type's blocks inside its rows, which the kernels read
 // at: 16 bytes for the 144- and 176-byte K-quant blocks (dwordx4 loads), 2 for
-// Q6_K's 210 and Q8_0's 34.
+// Q6_K's 210, Q8_0's 34 and Q4_0's 18.
 __host__ __device__ constexpr int64_t block_align(int type) {
     return type == TYPE_Q4_K || type == TYPE_Q5_K ? 16 : 2;
 }

@@ -18,7 +18,7 @@ GGML_MAX_OP_PARAMS = 64
 GGML_MAX_NAME = 64
 
 # ggml_type ids
-GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q8_0, GGML_TYPE_Q8_1 = 0, 1, 8, 9
+GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q4_0, GGML_TYPE_Q8_0, GGML_TYPE_Q8_1 = 0, 1, 2, 8, 9
 GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K, GGML_TYPE_Q8_K, GGML_TYPE_I32 = 12, 13, 14, 15, 26
 # ggml_op ids (position in op_name)
 GGML_OP_NONE, GGML_OP_ADD, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT_ID = 0, 2, 28, 29
@@ -33,7 +33,8 @@ GGML_BACKEND_BUFFER_USAGE_ANY, GGML_BACKEND_BUFFER_USAGE_WEIGHTS, GGML_BACKEND_B
 GGML_BACKEND_DEVICE_TYPE_GPU = 1
 
 # (block elements, block bytes) per type
-TYPE_BLOCK = {GGML_TYPE_F32: (1, 4), GGML_TYPE_F16: (1, 2), GGML_TYPE_I32: (1, 4), GGML_TYPE_Q8_0: (32, 34),
+TYPE_BLOCK = {GGML_TYPE_F32: (1, 4), GGML_TYPE_F16: (1, 2), GGML_TYPE_I32: (1, 4), GGML_TYPE_Q4_0: (32, 18),
+              GGML_TYPE_Q8_0: (32, 34),
               GGML_TYPE_Q8_1: (32, 36), GGML_TYPE_Q4_K: (256, 144), GGML_TYPE_Q5_K: (256, 176), GGML_TYPE_Q6_K: (256, 210),
               GGML_TYPE_Q8_K: (256, 292)}
 

@@ -119,11 +119,12 @@ def mmid(a_type, K, M, n_as, n_used, n_tokens, ne11=None):
 def test_supports_op(L):
     from ggml_hip import abi
     ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))  # noqa: E731
-    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q5_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0):
+    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q5_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0, abi.GGML_TYPE_Q4_0):
         assert ok(mm(t, 4096, 4096, 1)[2])
         assert ok(mm(t, 4096, 1024, 512, batch=(2, 1, 4, 1))[2])  # broadcast over dim 2
         assert ok(mmid(t, 2048, 768, 128, 8, 512)[3])
-    assert ok(mm(abi.GGML_TYPE_Q8_0, 96, 64, 3)[2])  # Q8_0 rows need only whole 32-blocks
+    assert ok(mm(abi.GGML_TYPE_Q8_0, 96, 64, 3)[2])  # Q8_0 / Q4_0 rows need only whole 32-blocks
+    assert ok(mm(abi.GGML_TYPE_Q4_0, 96, 64, 3)[2])
     assert not ok(mm(abi.GGML_TYPE_F16, 4096, 4096, 1)[2])  # only the quantized weight types
     assert not ok(mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 1, batch=(3, 1, 4, 1))[2])  # 4 % 3: no broadcast
     a, b, d = mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 2)
