@@ -197,9 +197,10 @@ int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_s
 /* Bytes of split-K workspace hip_qmm_mmq uses for this shape (0: no split). */
 size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
-/* Column-tile width (32 or 64) and K-split factor hip_qmm_mmq picks. */
+/* Column-tile width (32 or 64) and K-split factor hip_qmm_mmq picks (1: no
+ * split; otherwise a divisor of K / 256). */
 int hip_qmm_mmq_tile_n(int64_t ncols);
-int hip_qmm_mmq_split_k(int64_t K, int64_t nrows, int64_t ncols);
+int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols);
 
 /*
  * Expert-grouped MMQ over device-side tile tables (see hip_qmm_mul_mat_id):

@@ -565,15 +565,50 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
         }
 }
 
-// dst[c][r] = sum over z of partial[z][c][r], in z order (deterministic)
+// dst[c][r] = sum over z of partial[z][c][r], in z order (deterministic).
+// Each thread sums 4 consecutive partial values with 16-byte loads (the
+// planes are 16-byte aligned when nrows * ncols % 4 == 0; the workspace is)
+// and keeps 4 planes' loads in flight.
+constexpr int RED_V = 4;
 __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ partial, int split, int64_t nrows,
                                                      int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride) {
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= nrows * ncols) return;
-    const int64_t c = i / nrows, r = i % nrows;
-    float acc = 0.0f;
-    for (int z = 0; z < split; ++z) acc += partial[(int64_t)z * nrows * ncols + i];
-    dst[c * dst_col_stride + r] = acc;
+    const int64_t n = nrows * ncols;
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * RED_V;
+    if (i0 >= n) return;
+    float a[RED_V] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (n % RED_V == 0) {
+        const float *p = partial + i0;
+        int z = 0;
+        for (; z + 4 <= split; z += 4) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) v[u] = *reinterpret_cast<const float4 *>(p + (int64_t)(z + u) * n);
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                a[0] += v[u].x;
+                a[1] += v[u].y;
+                a[2] += v[u].z;
+                a[3] += v[u].w;
+            }
+        }
+        for (; z < split; ++z) {
+            const float4 v = *reinterpret_cast<const float4 *>(p + (int64_t)z * n);
+            a[0] += v.x;
+            a[1] += v.y;
+            a[2] += v.z;
+            a[3] += v.w;
+        }
+    } else {
+        for (int z = 0; z < split; ++z)
+#pragma unroll
+            for (int e = 0; e < RED_V; ++e)
+                if (i0 + e < n) a[e] += partial[(int64_t)z * n + i0 + e];
+    }
+#pragma unroll
+    for (int e = 0; e < RED_V; ++e) {
+        const int64_t i = i0 + e;
+        if (i < n) dst[(i / nrows) * dst_col_stride + i % nrows] = a[e];
+    }
 }
 
 template <int TYPE, int BN>
@@ -599,8 +634,9 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
     }
     if (split > 1) {
         const int64_t n = nrows * ncols;
-        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, split, nrows,
-                           ncols, dst, dst_col_stride);
+        const int64_t nthr = (n + RED_V - 1) / RED_V;
+        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, partial, split,
+                           nrows, ncols, dst, dst_col_stride);
         return (int)hipGetLastError();
     }
     return 0;
@@ -642,22 +678,32 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
 // that does not leave most of a tile empty.
 extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64; }
 
-// K-split factor: spread the K-steps over more workgroups until about two
-// workgroups per CU exist (256 CUs on MI355X), at least one K-step each.
-extern "C" int hip_qmm_mmq_split_k(int64_t K, int64_t nrows, int64_t ncols) {
+// K-split factor: spread the K-steps over more workgroups until the grid
+// holds about one workgroup per CU (256 CUs on MI355X) for the Q4_K
+// direct-to-LDS kernel on rows of at most 16 K-steps, about two otherwise;
+// at least 2 K-steps per share and equal shares.  Chosen by a sweep of every
+// split on 1024-14336 rows, K 4096 / 14336 and 9-512 columns: the one-per-CU
+// target won at short K (e.g. Q4_K 4096x4096 at 24 columns 13.5 us against
+// 16.9 us for two per CU), two per CU at K = 14336 (Q4_K 4096 rows at 512
+// columns: 108 us against 135 us unsplit), and unequal shares lost to the
+// next smaller equal split (14336 rows at 24 columns: 3 shares 21.9 us, 2
+// shares 19.3 us).
+extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
     const int64_t bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
-    int64_t split = (512 + wgs - 1) / wgs;
-    if (split > nkb) split = nkb;
-    if (split > 16) split = 16;
-    return split < 1 ? 1 : (int)split;
+    const int64_t target = (type == TYPE_Q4_K && nkb <= 16) ? 256 : 512;
+    int64_t split = (target + wgs - 1) / wgs;
+    const int64_t cap = nkb / 2 < 16 ? nkb / 2 : 16;
+    if (split > cap) split = cap;
+    if (split < 1) split = 1;
+    while (nkb % split) --split;
+    return (int)split;
 }
 
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    (void)type;
-    const int split = hip_qmm_mmq_split_k(K, nrows, ncols);
+    const int split = hip_qmm_mmq_split_k(type, K, nrows, ncols);
     return split > 1 ? (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) : 0;
 }
 
@@ -671,7 +717,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     const int bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
     // split K only when the caller's workspace holds the partials
-    int split = hip_qmm_mmq_split_k(K, nrows, ncols);
+    int split = hip_qmm_mmq_split_k(type, K, nrows, ncols);
     if (split > 1 && (!workspace || workspace_size < hip_qmm_mmq_workspace_size(type, K, nrows, ncols) ||
                       (uintptr_t)workspace % 16))
         split = 1;

@@ -66,7 +66,7 @@ def lib():
         L.hip_qmm_mmq_workspace_size.restype = ctypes.c_size_t
         L.hip_qmm_mmq_workspace_size.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mmq_split_k.restype = i32
-        L.hip_qmm_mmq_split_k.argtypes = [i64, i64, i64]
+        L.hip_qmm_mmq_split_k.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mul_mat.restype = i32
         L.hip_qmm_mul_mat.argtypes = [i32, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mmq_tile_n.restype = i32

@@ -59,8 +59,8 @@ def test_mmq_split_k(tname, nrows, K, ncols):
     both match the f64 formula."""
     import ggml_hip as G
     t = TYPES[tname]
-    split = G.lib().hip_qmm_mmq_split_k(K, nrows, ncols)
-    assert split > 1
+    split = G.lib().hip_qmm_mmq_split_k(t, K, nrows, ncols)
+    assert split > 1 and (K // 256) % split == 0
     wq = weights_q(t, nrows, K)
     x = acts(ncols, K)
     w_d = torch.from_numpy(np.array(wq)).cuda()
