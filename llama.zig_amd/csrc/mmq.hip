@@ -43,6 +43,11 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
                        const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s);
+// mmq_few.hip: the Q4_K kernel for at most 16 columns
+int mmq_few_split_k(int64_t K, int64_t nrows);
+int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
+                       hipStream_t s);
 
 namespace {
 
@@ -611,6 +616,15 @@ __global__ __launch_bounds__(256) void splitk_reduce(const float *__restrict__ p
     }
 }
 
+int launch_reduce(const float *partial, int split, int64_t nrows, int64_t ncols, float *dst, int64_t dst_col_stride,
+                  hipStream_t s) {
+    const int64_t n = nrows * ncols;
+    const int64_t nthr = (n + RED_V - 1) / RED_V;
+    hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, partial, split, nrows,
+                       ncols, dst, dst_col_stride);
+    return (int)hipGetLastError();
+}
+
 template <int TYPE, int BN>
 int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride, const int8_t *yqs,
            const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy, const int32_t *tiles,
@@ -632,14 +646,7 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
                            n_tiles, expert_off, col_src, col_dst, split > 1 ? partial : nullptr);
         if (int e = (int)hipGetLastError()) return e;
     }
-    if (split > 1) {
-        const int64_t n = nrows * ncols;
-        const int64_t nthr = (n + RED_V - 1) / RED_V;
-        hipLaunchKernelGGL(splitk_reduce, dim3((unsigned)((nthr + 255) / 256)), dim3(256), 0, s, partial, split,
-                           nrows, ncols, dst, dst_col_stride);
-        return (int)hipGetLastError();
-    }
-    return 0;
+    return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
 }
 
 template <int TYPE>
@@ -688,8 +695,7 @@ extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64;
 // columns: 108 us against 135 us unsplit), and unequal shares lost to the
 // next smaller equal split (14336 rows at 24 columns: 3 shares 21.9 us, 2
 // shares 19.3 us).
-extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
+int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     const int64_t bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
@@ -702,8 +708,19 @@ extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t n
     return (int)split;
 }
 
+// Q4_K with at most 16 columns runs the few-column kernel (mmq_few.hip) when
+// the activation planes are 16-byte aligned.
+bool few_cols(int type, int64_t ncols) { return type == TYPE_Q4_K && ncols <= 16; }
+
+extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
+    return few_cols(type, ncols) ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
+}
+
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    const int split = hip_qmm_mmq_split_k(type, K, nrows, ncols);
+    if (K <= 0 || nrows <= 0 || ncols <= 0) return 0;
+    int split = split_std(type, K, nrows, ncols);
+    if (few_cols(type, ncols) && mmq_few_split_k(K, nrows) > split) split = mmq_few_split_k(K, nrows);
     return split > 1 ? (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) : 0;
 }
 
@@ -716,13 +733,20 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     if (int e = check_weights(type, w, K, row_stride)) return e;
     const int bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
+    const bool few = few_cols(type, ncols) && (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;
     // split K only when the caller's workspace holds the partials
-    int split = hip_qmm_mmq_split_k(type, K, nrows, ncols);
-    if (split > 1 && (!workspace || workspace_size < hip_qmm_mmq_workspace_size(type, K, nrows, ncols) ||
+    int split = few ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
+    if (split > 1 && (!workspace || workspace_size < (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) ||
                       (uintptr_t)workspace % 16))
         split = 1;
     float *partial = (float *)workspace;
     hipStream_t s = (hipStream_t)stream;
+    if (few) {
+        if (int e = mmq_few_q4k_launch(w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, split, partial,
+                                       s))
+            return e;
+        return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
+    }
     switch (type) {
     case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
