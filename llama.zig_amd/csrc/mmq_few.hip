@@ -41,18 +41,22 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void *lds_ptr;
 
-constexpr int FBM = 64;                    // rows per workgroup
-constexpr int FBN = 16;                    // columns
-constexpr int FNT = 256;                   // threads per workgroup
-constexpr int FA = FBM * Q4K_BYTES;        // 9216 B of weights per step
-constexpr int FB = FBN * QK_K;             // 4096 B of codes per step
-constexpr int FD = FBN * 8 * 4;            // 512 B of headers per step
-constexpr int FNQ = (FA + FB + FD + 1023) / 1024;  // 14 transfers per step
-constexpr int FSTAGE = FNQ * 1024;
+constexpr int FBN = 16;  // columns
 
-// transfers per step issued by wave w (transfer q goes to wave q % 4)
-__host__ __device__ constexpr int transfers_of(int w) { return FNQ / 4 + (w < FNQ % 4 ? 1 : 0); }
-static_assert(transfers_of(0) <= 15 && transfers_of(3) >= 1, "vmcnt immediates below assume 1..15");
+// Workgroup geometry for NW waves of 16 rows each: the step's LDS stage and
+// its 1 KiB transfers (transfer q goes to wave q % NW).
+template <int NW>
+struct FewGeo {
+    static constexpr int BM = 16 * NW;                 // rows per workgroup
+    static constexpr int NT = 64 * NW;                 // threads
+    static constexpr int A = BM * Q4K_BYTES;           // weights per step
+    static constexpr int B = FBN * QK_K;               // codes per step
+    static constexpr int D = FBN * 8 * 4;              // headers per step
+    static constexpr int NQ = (A + B + D + 1023) / 1024;
+    static constexpr int STAGE = NQ * 1024;
+    static constexpr int PER = (NQ + NW - 1) / NW;     // most transfers of one wave
+    static constexpr int transfers_of(int w) { return NQ / NW + (w < NQ % NW ? 1 : 0); }
+};
 
 __device__ __forceinline__ uint32_t f16_bits(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
@@ -77,8 +81,8 @@ __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
 // (vmcnt(n); expcnt and lgkmcnt not waited).
 template <int N>
 __device__ __forceinline__ void wait_vm() {
-    static_assert(N >= 0 && N <= 15, "vmcnt field");
-    __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+    static_assert(N >= 0 && N <= 63, "vmcnt field");
+    __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));  // vmcnt bits 3:0 and 15:14
 }
 
 // Workgroup barrier that orders LDS only.  __syncthreads() also orders
@@ -93,40 +97,56 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// this wave's step k is complete; `ahead`: step k+1 was issued after it
-__device__ __forceinline__ void wait_step(int wave, bool ahead) {
-    if (!ahead) {
-        wait_vm<0>();
-    } else if (wave < FNQ % 4) {
-        wait_vm<transfers_of(0)>();
+// This wave's transfers of step k are complete while those of the `ahead`
+// steps issued after it (0 <= ahead <= A) may still be in flight; `big`:
+// this wave issues NBIG transfers per step, else NSMALL.  Both are uniform
+// over the wave.
+template <int A, int NBIG, int NSMALL>
+__device__ __forceinline__ void wait_step(bool big, int ahead) {
+    if constexpr (A > 0) {
+        if (ahead == A) {
+            if (big) wait_vm<A * NBIG>();
+            else wait_vm<A * NSMALL>();
+            return;
+        }
+        wait_step<A - 1, NBIG, NSMALL>(big, ahead);
     } else {
-        wait_vm<transfers_of(3)>();
+        wait_vm<0>();
     }
 }
 
-__global__ __launch_bounds__(FNT, 3) void mmq_few_q4k_kernel(const uint8_t *__restrict__ w, int64_t K, int64_t nrows,
+// workgroups per CU that the LDS (160 KiB) holds with an NST-stage ring
+template <int NW>
+constexpr int few_occupancy(int nst) { return 163840 / (nst * FewGeo<NW>::STAGE); }
+
+template <int NST, int NW>
+__global__ __launch_bounds__(FewGeo<NW>::NT, few_occupancy<NW>(NST)) void mmq_few_q4k_kernel(const uint8_t *__restrict__ w, int64_t K, int64_t nrows,
                                                             int64_t row_stride, const int8_t *__restrict__ yqs,
                                                             const uint32_t *__restrict__ yds, int ncols,
                                                             float *__restrict__ dst, int64_t dst_col_stride,
                                                             float *__restrict__ partial) {
-    __shared__ alignas(16) uint8_t st0[FSTAGE], st1[FSTAGE], st2[FSTAGE];
+    using G = FewGeo<NW>;
+    constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER;
+    static_assert(NST >= 2 && few_occupancy<NW>(NST) >= 1, "ring depth");
+    static_assert((NST - 2) * G::transfers_of(0) <= 63, "vmcnt field");
+    __shared__ alignas(16) uint8_t st[NST][G::STAGE];
 
     const int64_t Kp = pad_k(K);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 15, kq = lane >> 4;
-    const int64_t row0 = (int64_t)blockIdx.x * FBM;
+    const int64_t row0 = (int64_t)blockIdx.x * G::BM;
     const int nkb = (int)(K / QK_K);
     const int gz = (int)gridDim.z, z = (int)blockIdx.z;
     const int kb0 = (int)((int64_t)nkb * z / gz), kb1 = (int)((int64_t)nkb * (z + 1) / gz);
 
-    // Per-lane sources of this wave's transfers (q = wave + 4i), as a base at
-    // K-step 0 and the bytes one K-step adds.
-    const uint8_t *src[4];
-    int kstep[4];
+    // Per-lane sources of this wave's transfers (q = wave + NW*i), as a base
+    // at K-step 0 and the bytes one K-step adds.
+    const uint8_t *src[PER];
+    int kstep[PER];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int q = wave + 4 * i;
+    for (int i = 0; i < PER; ++i) {
+        const int q = wave + NW * i;
         const int pos = (q < FNQ ? q : 0) * 1024 + lane * 16;
         if (pos < FA) {
             const int r = pos / Q4K_BYTES, off = pos - r * Q4K_BYTES;
@@ -149,8 +169,8 @@ __global__ __launch_bounds__(FNT, 3) void mmq_few_q4k_kernel(const uint8_t *__re
     }
     auto dma = [&](int kb, uint8_t *st) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (wave + 4 * i < FNQ) dma16(src[i] + (int64_t)kb * kstep[i], st + (wave + 4 * i) * 1024);
+        for (int i = 0; i < PER; ++i)
+            if (wave + NW * i < FNQ) dma16(src[i] + (int64_t)kb * kstep[i], st + (wave + NW * i) * 1024);
     };
 
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -213,25 +233,22 @@ __global__ __launch_bounds__(FNT, 3) void mmq_few_q4k_kernel(const uint8_t *__re
         }
     };
 
-    // three-stage ring: step kb + s lives in stage s % 3
-    if (kb0 < kb1) dma(kb0, st0);
-    if (kb0 + 1 < kb1) dma(kb0 + 1, st1);
+    // NST-stage ring: step kb0 + i lives in stage i % NST; while a step is
+    // contracted, the next NST - 2 are in flight and one more is issued
+    const bool big = wave < FNQ % NW || FNQ % NW == 0;
+#pragma unroll
+    for (int i = 0; i < NST - 1; ++i)
+        if (kb0 + i < kb1) dma(kb0 + i, st[i]);
     for (int kb = kb0; kb < kb1;) {
-        wait_step(wave, kb + 1 < kb1);
-        lds_barrier();
-        if (kb + 2 < kb1) dma(kb + 2, st2);
-        compute(st0);
-        if (++kb >= kb1) break;
-        wait_step(wave, kb + 1 < kb1);
-        lds_barrier();
-        if (kb + 2 < kb1) dma(kb + 2, st0);
-        compute(st1);
-        if (++kb >= kb1) break;
-        wait_step(wave, kb + 1 < kb1);
-        lds_barrier();
-        if (kb + 2 < kb1) dma(kb + 2, st1);
-        compute(st2);
-        ++kb;
+#pragma unroll
+        for (int i = 0; i < NST; ++i) {
+            const int left = kb1 - 1 - kb;  // steps after kb already issued: min(left, NST - 2)
+            wait_step<NST - 2, G::transfers_of(0), G::transfers_of(NW - 1)>(big, left < NST - 2 ? left : NST - 2);
+            lds_barrier();
+            if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
+            compute(st[i]);
+            if (++kb >= kb1) break;
+        }
     }
 
     if (li < ncols) {
@@ -246,12 +263,33 @@ __global__ __launch_bounds__(FNT, 3) void mmq_few_q4k_kernel(const uint8_t *__re
 
 }  // namespace
 
-// K-split for the few-column kernel: about three workgroups per CU (the LDS
-// ring holds three per CU), at least 2 K-steps per share, equal shares.
+// Shape of the few-column kernel: ring depth and waves per workgroup.  A
+// sweep of 2-6 stages, 4 or 8 waves and 256-2560 workgroups (Q4_K, 16
+// columns, 1024-14336 rows, K 4096 / 14336) found 3 stages of 4 waves best or
+// within noise everywhere: pure transfer streaming of the same pattern takes
+// ~8 us for 33 MB, and the rest is contraction that a deeper ring or more
+// workgroups per CU did not hide.
+struct FewCfg {
+    int nst, nw;
+};
+FewCfg few_cfg(int64_t K, int64_t nrows) {
+    (void)K;
+    (void)nrows;
+    return {3, 4};
+}
+
+// K-split for the few-column kernel.  From 192 row tiles (3/4 of the CUs)
+// the kernel runs unsplit: the partials' reduction is a second launch of
+// ~3-4 us, more than a fuller grid saves (14336 rows at 16 columns: 14.7 us
+// unsplit, 13.3 + 4.0 us in 2 shares).  Below that, about two workgroups per
+// CU (4096 rows: 8 shares), at least 2 K-steps per share, equal shares.
 int mmq_few_split_k(int64_t K, int64_t nrows) {
-    const int64_t wgs = (nrows + FBM - 1) / FBM;
+    const FewCfg c = few_cfg(K, nrows);
+    const int64_t bm = 16 * c.nw;
+    const int64_t wgs = (nrows + bm - 1) / bm;
     const int64_t nkb = K / QK_K;
-    int64_t split = (768 + wgs - 1) / wgs;
+    if (wgs >= 192) return 1;
+    int64_t split = (512 + wgs - 1) / wgs;
     const int64_t cap = nkb / 2 < 16 ? nkb / 2 : 16;
     if (split > cap) split = cap;
     if (split < 1) split = 1;
@@ -266,11 +304,24 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
 int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                        const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
                        hipStream_t s) {
-    const int64_t gx = (nrows + FBM - 1) / FBM;
+    const FewCfg c = few_cfg(K, nrows);
+    const int64_t gx = (nrows + 16 * c.nw - 1) / (16 * c.nw);
     if (ncols < 1 || ncols > FBN || gx > 0x7FFFFFFF || split < 1 || split > 16 || K / QK_K > 0x7FFFFFFF)
         return (int)hipErrorInvalidValue;
-    hipLaunchKernelGGL(mmq_few_q4k_kernel, dim3((unsigned)gx, 1, (unsigned)split), dim3(FNT), 0, s,
-                       (const uint8_t *)w, K, nrows, row_stride, yqs, (const uint32_t *)yds, (int)ncols, dst,
-                       dst_col_stride, split > 1 ? partial : nullptr);
+    const dim3 grid((unsigned)gx, 1, (unsigned)split);
+    const uint8_t *wb = (const uint8_t *)w;
+    const uint32_t *ds = (const uint32_t *)yds;
+    float *pp = split > 1 ? partial : nullptr;
+#define FEW_LAUNCH(NST, NW)                                                                                            \
+    hipLaunchKernelGGL((mmq_few_q4k_kernel<NST, NW>), grid, dim3(64 * NW), 0, s, wb, K, nrows, row_stride, yqs, ds,    \
+                       (int)ncols, dst, dst_col_stride, pp)
+    if (c.nw == 8) {
+        if (c.nst == 2) FEW_LAUNCH(2, 8);
+        else FEW_LAUNCH(3, 8);
+    } else {
+        if (c.nst == 4) FEW_LAUNCH(4, 4);
+        else FEW_LAUNCH(3, 4);
+    }
+#undef FEW_LAUNCH
     return (int)hipGetLastError();
 }
