@@ -43,7 +43,7 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
                        const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s);
-// mmq_few.hip: the Q4_K kernel for at most 16 columns
+// mmq_few.hip: the Q4_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                        const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
@@ -708,9 +708,9 @@ int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return (int)split;
 }
 
-// Q4_K with at most 16 columns runs the few-column kernel (mmq_few.hip) when
+// Q4_K with at most 32 columns runs the few-column kernel (mmq_few.hip) when
 // the activation planes are 16-byte aligned.
-bool few_cols(int type, int64_t ncols) { return type == TYPE_Q4_K && ncols <= 16; }
+bool few_cols(int type, int64_t ncols) { return type == TYPE_Q4_K && ncols <= 32; }
 
 extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;

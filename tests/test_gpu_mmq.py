@@ -16,7 +16,8 @@ TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": 
 
 
 @pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
-@pytest.mark.parametrize("nrows,K,ncols", [(256, 4096, 128), (200, 2048, 77), (128, 14336, 9), (384, 768, 300)])
+@pytest.mark.parametrize("nrows,K,ncols", [(256, 4096, 128), (200, 2048, 77), (128, 14336, 9), (384, 768, 300),
+                                           (1000, 4096, 17), (200, 2048, 24), (64, 512, 32), (70, 1024, 3)])
 def test_mmq_parity(tname, nrows, K, ncols):
     import ggml_hip as G
     t = TYPES[tname]
