@@ -1,5 +1,6 @@
 // api.hip -- op-level entry points of libggml_hip_qmm.so: workspace sizing and
-// the MUL_MAT dispatch (GEMV for <= 8 columns, MMQ above), mirroring
+// the MUL_MAT dispatch (GEMV for <= 8 columns, MMQ above, and the few-column
+// Q4_K GEMM for 5-8 columns of large matrices), mirroring
 // ggml_cuda_mul_mat's choice between MMVQ and MMQ
 // (src/ggml/cuda/mulmat.zig:576-639; mmvq.zig:128-173; mmq.zig:865-917).
 #include "../../include/ggml_hip_qmm.h"
@@ -18,6 +19,28 @@ size_t q8_1_bytes(int64_t K, int64_t ncols) {
     return (size_t)(ncols * Kp) + (size_t)(ncols * (Kp / QK8)) * 4u;  // qs plane, then ds plane
 }
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+// Whether 2-8 columns go to the MMQ dispatch (the few-column Q4_K kernel,
+// mmq_few.hip) rather than the GEMV.  The GEMV's time grows with the columns
+// (each wave re-reads every column's activation slice), the few-column
+// kernel's hardly does; crossovers measured with device timing on Q4_K: from
+// 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.1 against 15.9 us)
+// and on >= 16384 rows (28672x4096: 22.1 against 21.1 us), from 6 at K >= 8192
+// on >= 2048 rows, from 8 on >= 6144 rows (14336x4096: 18.9 against 16.3 us;
+// 6 columns tie); the GEMV stays ahead on smaller matrices (4096x4096 at 8
+// columns: 9.2 against 10.3 us).
+bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    if (type != TYPE_Q4_K || K % 256 != 0 || ncols > 8) return false;
+    if (K >= 8192 && nrows >= 4096) return ncols >= 5;
+    if (nrows >= 16384) return ncols >= 5;
+    if (K >= 8192 && nrows >= 2048) return ncols >= 6;
+    if (nrows >= 6144) return ncols >= 8;
+    return false;
+}
+
+bool use_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return K % 256 == 0 && (ncols > 8 || few_cols_wins(type, K, nrows, ncols));
+}
 }  // namespace
 
 extern "C" int hip_qmm_version(void) { return (0 << 16) | 1; }
@@ -27,7 +50,7 @@ extern "C" int64_t hip_qmm_row_padding(void) { return ROW_PAD; }
 extern "C" size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || ncols <= 0) return 0;
     size_t n = q8_1_bytes(K, ncols);
-    if (ncols > 8 && K % 256 == 0 && nrows > 0) n = align256(n) + hip_qmm_mmq_workspace_size(type, K, nrows, ncols);
+    if (nrows > 0 && use_mmq(type, K, nrows, ncols)) n = align256(n) + hip_qmm_mmq_workspace_size(type, K, nrows, ncols);
     return n;
 }
 
@@ -49,7 +72,7 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     int8_t *qs = (int8_t *)workspace;
     void *ds = (uint8_t *)workspace + ncols * Kp;
     if (int e = hip_qmm_quantize_q8_1_planar(x, K, ncols, x_col_stride, qs, ds, stream)) return e;
-    if (ncols <= 8)
+    if (ncols <= 8 && !use_mmq(type, K, nrows, ncols))
         return hip_qmm_mul_mat_vec(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, stream);
     if (K % 256 == 0) {
         const size_t off = align256(q8_1_bytes(K, ncols));

@@ -77,3 +77,26 @@ def test_mmq_split_k(tname, nrows, K, ncols):
     ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
     assert max_err_scaled(a, ideal) < F64_TOL, max_err_scaled(a, ideal)
     assert max_err_scaled(u, ideal) < F64_TOL, max_err_scaled(u, ideal)
+
+
+@pytest.mark.parametrize("nrows,K,ncols", [(4096, 8192, 5), (2048, 8192, 6), (6144, 4096, 8), (6150, 4096, 8)])
+def test_op_few_columns(nrows, K, ncols):
+    """The op sends 5-8 columns of large Q4_K matrices to the few-column GEMM
+    instead of the GEMV: same bits as the kernel-level MMQ on the quantized
+    columns, within the f64 and CPU gates, and within rounding of the GEMV."""
+    import ggml_hip as G
+    t = O.TYPE_Q4_K
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    got = G.mul_mat("Q4_K", w_d, x_d).cpu().numpy()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    np.testing.assert_array_equal(got, G.mmq("Q4_K", w_d, K, qs, ds).cpu().numpy())
+    gemv = G.mul_mat_vec("Q4_K", w_d, K, qs, ds).cpu().numpy()
+    assert max_err_scaled(got, gemv) < 1e-6
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
