@@ -161,7 +161,7 @@ def run_suite(name, torch, G, dev, reps):
     def emit(rec):
         print(json.dumps(rec), flush=True)
 
-    if name in ("decode", "crossquant", "mmq"):
+    if name in ("decode", "crossquant", "mmq", "few"):
         if name == "decode":
             shapes = [("Q4_K", 4096, 4096, "attn_q/o"), ("Q4_K", 1024, 4096, "attn_k"), ("Q6_K", 1024, 4096, "attn_v"),
                       ("Q4_K", 14336, 4096, "ffn_gate/up"), ("Q6_K", 4096, 14336, "ffn_down")]
@@ -169,6 +169,12 @@ def run_suite(name, torch, G, dev, reps):
         elif name == "mmq":
             shapes = [("Q4_K", 14336, 4096, "ffn_gate/up")]
             batches = (128, 512, 2048)
+        elif name == "few":
+            # batched decode: the few-column Q4_K GEMM against the GEMV (<= 8
+            # columns) and the 128-row MMQ tile it replaced (9-32 columns)
+            shapes = [("Q4_K", 14336, 4096, "ffn_gate/up"), ("Q4_K", 4096, 14336, "Q4_K 4096x14336"),
+                      ("Q4_K", 4096, 4096, "attn_q/o")]
+            batches = (4, 6, 8, 9, 16, 24, 32)
         else:
             shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K", "Q5_K", "Q4_0")
                       for k in (4096, 14336)]
@@ -180,13 +186,22 @@ def run_suite(name, torch, G, dev, reps):
                 qs, ds = G.quantize_q8_1_planar(x)
                 out = torch.empty((T, M), dtype=torch.float32, device=dev)
                 n = len(ws) * reps
+                mmq_ws = torch.empty(max(1, int(G.lib().hip_qmm_mmq_workspace_size(G.TYPE_IDS[qtype], Kx, M, T))),
+                                     dtype=torch.uint8, device=dev)
                 if T <= 8:
                     fn = lambda i: G.mul_mat_vec(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
                     kern = "gemv"
                 else:
-                    fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
+                    fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
                     kern = "mmq"
                 ms = event_time_batch(torch, fn, n)
+                extra = {}
+                if name == "few":
+                    # the few-column GEMM at every width (next to the GEMV up
+                    # to 8 columns)
+                    few_fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
+                    extra["few_us"] = round(event_time_batch(torch, few_fn, n) * 1e3, 3)
+                    extra["few_split"] = int(G.lib().hip_qmm_mmq_split_k(G.TYPE_IDS[qtype], Kx, M, T))
                 # the op on f32 activations (hip_qmm_mul_mat: quantizer + kernel,
                 # or for one column the GEMV that quantizes in its prologue)
                 wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_workspace_size(G.TYPE_IDS[qtype], Kx, M, T)),
@@ -198,7 +213,7 @@ def run_suite(name, torch, G, dev, reps):
                 emit({"suite": name, "kernel": kern, "type": qtype, "shape": f"{M}x{Kx}", "label": label, "T": T,
                       "us": round(ms * 1e3, 3), "op_us": round(ms_op * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2),
-                      "int8_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4)})
+                      "int8_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4), **extra})
             del ws
             torch.cuda.empty_cache()
     elif name == "moe":
@@ -309,7 +324,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
-    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn"],
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "few"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()
