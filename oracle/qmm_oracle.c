@@ -52,6 +52,7 @@ typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_
 typedef struct { uint16_t d; uint16_t dmin; uint8_t scales[K_SCALE_SIZE]; uint8_t qh[QK_K / 8]; uint8_t qs[QK_K / 2]; } blk_q5_K; /* 176 B */
 typedef struct { uint8_t ql[QK_K / 2]; uint8_t qh[QK_K / 4]; int8_t scales[QK_K / 16]; uint16_t d; } blk_q6_K;  /* 210 B */
 typedef struct { float d; int8_t qs[QK_K]; int16_t bsums[QK_K / 16]; } blk_q8_K;                               /* 292 B */
+typedef struct { uint16_t d; uint16_t scales_h; uint8_t scales_l[QK_K / 64]; uint8_t qs[QK_K / 2]; } blk_iq4_xs; /* 136 B */
 
 _Static_assert(sizeof(blk_q4_0) == 18, "q4_0");
 _Static_assert(sizeof(blk_q8_0) == 34, "q8_0");
@@ -60,6 +61,7 @@ _Static_assert(sizeof(blk_q4_K) == 144, "q4_K");
 _Static_assert(sizeof(blk_q5_K) == 176, "q5_K");
 _Static_assert(sizeof(blk_q6_K) == 210, "q6_K");
 _Static_assert(sizeof(blk_q8_K) == 292, "q8_K");
+_Static_assert(sizeof(blk_iq4_xs) == 136, "iq4_xs");
 
 size_t orc_type_size(int type) {
     switch (type) {
@@ -71,6 +73,7 @@ size_t orc_type_size(int type) {
     case ORC_TYPE_Q5_K: return sizeof(blk_q5_K);
     case ORC_TYPE_Q6_K: return sizeof(blk_q6_K);
     case ORC_TYPE_Q8_K: return sizeof(blk_q8_K);
+    case ORC_TYPE_IQ4_XS: return sizeof(blk_iq4_xs);
     default: return 0;
     }
 }
@@ -79,7 +82,7 @@ int64_t orc_blck_size(int type) {
     switch (type) {
     case ORC_TYPE_F32: return 1;
     case ORC_TYPE_Q4_0: case ORC_TYPE_Q8_0: case ORC_TYPE_Q8_1: return 32;
-    case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: return QK_K;
+    case ORC_TYPE_Q4_K: case ORC_TYPE_Q5_K: case ORC_TYPE_Q6_K: case ORC_TYPE_Q8_K: case ORC_TYPE_IQ4_XS: return QK_K;
     default: return 0;
     }
 }
@@ -797,6 +800,142 @@ static void q4_0_impl(const float *x, blk_q4_0 *y, int64_t n_per_row, const floa
     }
 }
 
+/* ------------------------------------------------------------------------ */
+/* IQ4_XS: src/ggml/quants/iq4.zig, iq_dequant.zig:360-381. */
+
+/* The format's 16 non-linear levels (kvalues_iq4nl, ggml-common.h, which the
+ * reference reaches through @cImport, iq4.zig:12-14); dense near zero. */
+static const int8_t KV_IQ4NL[16] = {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113};
+
+/* best_index_iq4nl, iq4.zig:31-40: 15 minus the midpoints x lies below, so a
+ * tie goes to the higher level. */
+static inline int best_index_iq4nl(const float *mid, float x) {
+    int l = 15;
+    for (int k = 0; k < 15; ++k) l -= x < mid[k];
+    return l;
+}
+
+/* quantize_row_iq4_nl_impl for IQ4_XS (iq4.zig:60-194): super-block 256,
+ * sub-blocks of 32, ntry 7.  Per sub-block: weights x^2 (or qw * sqrt(sigma2 +
+ * x^2)), a least-squares scale over 16 candidate inverse scales, then a 6-bit
+ * scale l = nearest(scale / d) in [-32, 31] against d = -max_scale / 32 and
+ * the levels requantized with the rounded scale; stored as l + 32, four bits
+ * in scales_l and two in scales_h. */
+static void iq4_xs_block(const float *x, blk_iq4_xs *y, const float *qw_all) {
+    const int ntry = 7, nt = 2 * ntry + 2;
+    float sigma2 = 0;
+    for (int j = 0; j < QK_K; ++j) sigma2 += x[j] * x[j];
+    sigma2 *= 2.0f / (float)QK_K;
+    memset(y->qs, 0, sizeof y->qs);
+    float mid[15], fval[16];
+    for (int k = 0; k < 15; ++k) mid[k] = 0.5f * (float)((int)KV_IQ4NL[k] + KV_IQ4NL[k + 1]);
+    for (int k = 0; k < 16; ++k) fval[k] = (float)KV_IQ4NL[k];
+    float scales[QK_K / 32], weight[32];
+    uint8_t L[QK_K];
+    memset(L, 0, sizeof L);
+    float max_scale = 0, amax_scale = 0;
+    for (int ib = 0; ib < QK_K / 32; ++ib) {
+        const float *xb = x + 32 * ib;
+        if (qw_all) {
+            const float *qw = qw_all + 32 * ib;
+            for (int j = 0; j < 32; ++j) weight[j] = qw[j] * sqrtf(sigma2 + xb[j] * xb[j]);
+        } else {
+            for (int j = 0; j < 32; ++j) weight[j] = xb[j] * xb[j];
+        }
+        float amax = 0, max = 0;
+        for (int j = 0; j < 32; ++j) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = xb[j];
+            }
+        }
+        if (amax < GROUP_MAX_EPS) {
+            scales[ib] = 0;
+            continue;
+        }
+        float d = -max / (float)KV_IQ4NL[0];
+        float idt[16], sqx[16], sq2[16];
+        idt[0] = 1 / d;
+        for (int lane = 1; lane < nt; ++lane) idt[lane] = (float)(lane - 1 - ntry + KV_IQ4NL[0]) / max;
+        for (int lane = 0; lane < nt; ++lane) sqx[lane] = sq2[lane] = 0;
+        for (int j = 0; j < 32; ++j) {
+            const float w = weight[j];
+            for (int lane = 0; lane < nt; ++lane) {
+                const float q = fval[best_index_iq4nl(mid, idt[lane] * xb[j])];
+                sqx[lane] += w * q * xb[j];
+                sq2[lane] += w * q * q;
+            }
+        }
+        d = sq2[0] > 0 ? sqx[0] / sq2[0] : 0.0f;
+        float best = d * sqx[0];
+        for (int lane = 1; lane < nt; ++lane)
+            if (sq2[lane] > 0 && sqx[lane] * sqx[lane] > best * sq2[lane]) {
+                d = sqx[lane] / sq2[lane];
+                best = d * sqx[lane];
+            }
+        scales[ib] = d;
+        if (fabsf(d) > amax_scale) {
+            amax_scale = fabsf(d);
+            max_scale = d;
+        }
+    }
+    y->scales_h = 0;
+    const float d = -max_scale / 32;
+    y->d = FP16(d);
+    const float id = d != 0 ? 1 / d : 0.0f;
+    for (int ib = 0; ib < QK_K / 32; ++ib) {
+        int l = nearest_int(id * scales[ib]);
+        l = l < -32 ? -32 : (l > 31 ? 31 : l);
+        const float dl = d * (float)l;
+        const float idl = dl != 0 ? 1 / dl : 0.0f;
+        for (int j = 0; j < 32; ++j) L[32 * ib + j] = (uint8_t)best_index_iq4nl(mid, idl * x[32 * ib + j]);
+        l += 32;
+        const uint8_t l_l = (uint8_t)(l & 0xf), l_h = (uint8_t)(l >> 4);
+        if (ib % 2 == 0) y->scales_l[ib / 2] = l_l;
+        else y->scales_l[ib / 2] |= (uint8_t)(l_l << 4);
+        y->scales_h |= (uint16_t)(l_h << (2 * (ib % 8)));
+    }
+    for (int i = 0; i < QK_K / 32; ++i)
+        for (int j = 0; j < 16; ++j) y->qs[16 * i + j] = (uint8_t)(L[32 * i + j] | (L[32 * i + 16 + j] << 4));
+}
+
+/* quantize_iq4_xs (iq4.zig:283-325) row by row; quantize_row_iq4_xs_ref is
+ * the same without an imatrix (iq4.zig:327-330). */
+static void iq4_xs_rows(const float *x, uint8_t *y, int64_t nrows, int64_t n_per_row, const float *qw) {
+    const int64_t nb = n_per_row / QK_K;
+    for (int64_t r = 0; r < nrows; ++r) {
+        blk_iq4_xs *row = (blk_iq4_xs *)(y + (size_t)r * (size_t)nb * sizeof(blk_iq4_xs));
+        for (int64_t i = 0; i < nb; ++i)
+            iq4_xs_block(x + r * n_per_row + i * QK_K, &row[i], qw ? qw + i * QK_K : NULL);
+    }
+}
+
+void orc_quantize_row_iq4_xs_ref(const float *x, void *vy, int64_t k) { iq4_xs_rows(x, (uint8_t *)vy, 1, k, NULL); }
+
+/* dequantize_row_iq4_xs, iq_dequant.zig:360-381: w = d * (ls - 32) * level. */
+void orc_dequantize_row_iq4_xs(const void *vx, float *y, int64_t k) {
+    const blk_iq4_xs *x = (const blk_iq4_xs *)vx;
+    for (int64_t i = 0; i < k / QK_K; ++i) {
+        const float d = F32(x[i].d);
+        for (int ib = 0; ib < QK_K / 32; ++ib) {
+            const int ls = ((x[i].scales_l[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((x[i].scales_h >> (2 * ib)) & 3) << 4);
+            const float dl = d * (float)(ls - 32);
+            const uint8_t *qs = x[i].qs + 16 * ib;
+            for (int j = 0; j < 16; ++j) {
+                y[j] = dl * (float)KV_IQ4NL[qs[j] & 0xf];
+                y[j + 16] = dl * (float)KV_IQ4NL[qs[j] >> 4];
+            }
+            y += 32;
+        }
+    }
+}
+
+/* the 6-bit scale of sub-block ib, l + 32 */
+static inline int iq4_xs_ls(const blk_iq4_xs *x, int ib) {
+    return ((x->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xf) | (((x->scales_h >> (2 * ib)) & 3) << 4);
+}
+
 void orc_quantize_row_q8_0_ref(const float *x, void *vy, int64_t k) {
     blk_q8_0 *y = (blk_q8_0 *)vy;
     const int64_t nb = k / QK8_0;
@@ -899,6 +1038,9 @@ size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start, 
         break;
     case ORC_TYPE_Q8_0:
         orc_quantize_row_q8_0_ref(src, out, nrows * n_per_row);
+        break;
+    case ORC_TYPE_IQ4_XS:
+        iq4_xs_rows(src, out, nrows, n_per_row, imatrix);
         break;
     case ORC_TYPE_Q4_K:
         if (!imatrix) orc_quantize_row_q4_K_ref(src, out, nrows * n_per_row);
@@ -1049,6 +1191,38 @@ static float vec_dot_q4_0_q8_0_generic(int n, const void *vx, const void *vy) {
         }
         const int32_t sumi = sumi0 + sumi1;
         sumf += (float)sumi * F32(x[ib].d) * F32(y[ib].d);
+    }
+    return sumf;
+}
+
+/* ggml_vec_dot_iq4_xs_q8_K_generic, cpu/quants/iq.zig:526-578: sub-blocks in
+ * pairs, scales from scales_l and two bits of scales_h each. */
+static float vec_dot_iq4_xs_q8_K_generic(int n, const void *vx, const void *vy) {
+    const blk_iq4_xs *x = (const blk_iq4_xs *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    float sumf = 0;
+    for (int ibl = 0; ibl < n / QK_K; ++ibl) {
+        const float d4d8 = F32(x[ibl].d) * y[ibl].d;
+        uint16_t h = x[ibl].scales_h;
+        int qs = 0, q8 = 0;
+        for (int ib = 0; ib < QK_K / 32; ib += 2) {
+            const uint8_t sl = x[ibl].scales_l[ib / 2];
+            const uint8_t ls1 = (uint8_t)((sl & 0xf) | ((h << 4) & 0x30));
+            const uint8_t ls2 = (uint8_t)((sl >> 4) | ((h << 2) & 0x30));
+            h >>= 4;
+            const float d1 = d4d8 * (float)((int)ls1 - 32);
+            const float d2 = d4d8 * (float)((int)ls2 - 32);
+            for (int pass = 0; pass < 2; ++pass) {
+                int32_t sumi1 = 0, sumi2 = 0;
+                for (int j = 0; j < 16; ++j) {
+                    sumi1 += (int32_t)y[ibl].qs[q8 + j] * KV_IQ4NL[x[ibl].qs[qs + j] & 0xf];
+                    sumi2 += (int32_t)y[ibl].qs[q8 + j + 16] * KV_IQ4NL[x[ibl].qs[qs + j] >> 4];
+                }
+                sumf += (pass == 0 ? d1 : d2) * (float)(sumi1 + sumi2);
+                qs += 16;
+                q8 += 32;
+            }
+        }
     }
     return sumf;
 }
@@ -1303,6 +1477,7 @@ static dot_fn pick_dot(int type, int impl) {
     case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
     case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_generic;
     case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_generic;
+    case ORC_TYPE_IQ4_XS: return vec_dot_iq4_xs_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
     }
     return NULL;
 }
@@ -1384,6 +1559,20 @@ void orc_block_dots_q8_1(int type, const void *w, int64_t nrows, int64_t K, cons
                 for (int l = 0; l < 32; ++l) s += x[b].qs[l] * y[b].qs[l];
                 *out++ = s;
             }
+        } else if (type == ORC_TYPE_IQ4_XS) {
+            /* S = sum level[q] * q8 over each 32-value sub-block */
+            const blk_iq4_xs *x = (const blk_iq4_xs *)row;
+            for (int64_t b = 0; b < K / QK_K; ++b)
+                for (int ib = 0; ib < 8; ++ib) {
+                    const blk_q8_1 *yb = &y[b * 8 + ib];
+                    const uint8_t *qs = x[b].qs + 16 * ib;
+                    int32_t s = 0;
+                    for (int l = 0; l < 16; ++l) {
+                        s += KV_IQ4NL[qs[l] & 0xf] * yb->qs[l];
+                        s += KV_IQ4NL[qs[l] >> 4] * yb->qs[l + 16];
+                    }
+                    *out++ = s;
+                }
         } else if (type == ORC_TYPE_Q4_0) {
             /* S = sum (q - 8) * q8 over the block: the offset applied in integers */
             const blk_q4_0 *x = (const blk_q4_0 *)row;
@@ -1438,6 +1627,11 @@ void orc_mul_mat_q8_1_f64(int type, const void *w, int64_t nrows, int64_t K, con
             } else if (type == ORC_TYPE_Q4_0) {
                 const blk_q4_0 *x = (const blk_q4_0 *)row;
                 for (int64_t b = 0; b < K / 32; ++b) acc += (double)F32(x[b].d) * F32(y[b].d) * S[b];
+            } else if (type == ORC_TYPE_IQ4_XS) {
+                const blk_iq4_xs *x = (const blk_iq4_xs *)row;
+                for (int64_t b = 0; b < K / QK_K; ++b)
+                    for (int ib = 0; ib < 8; ++ib)
+                        acc += (double)F32(x[b].d) * (iq4_xs_ls(&x[b], ib) - 32) * F32(y[b * 8 + ib].d) * S[b * 8 + ib];
             } else {
                 const blk_q8_0 *x = (const blk_q8_0 *)row;
                 for (int64_t b = 0; b < K / 32; ++b) acc += (double)F32(x[b].d) * F32(y[b].d) * S[b];

@@ -34,6 +34,7 @@ enum {
     ORC_TYPE_Q5_K = 13,
     ORC_TYPE_Q6_K = 14,
     ORC_TYPE_Q8_K = 15,
+    ORC_TYPE_IQ4_XS = 23,
 };
 
 /* Implementation selector for the dot-product drivers. */
@@ -59,12 +60,14 @@ void orc_quantize_row_q6_K_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_0_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_1_ref(const float *x, void *y, int64_t k);
 void orc_quantize_row_q8_K_ref(const float *x, void *y, int64_t k);
+void orc_quantize_row_iq4_xs_ref(const float *x, void *y, int64_t k);
 void orc_dequantize_row_q4_0(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q4_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q5_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q6_K(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q8_0(const void *x, float *y, int64_t k);
 void orc_dequantize_row_q8_K(const void *x, float *y, int64_t k);
+void orc_dequantize_row_iq4_xs(const void *x, float *y, int64_t k);
 size_t orc_quantize_chunk(int type, const float *src, void *dst, int64_t start,
                           int64_t nrows, int64_t n_per_row, const float *imatrix);
 

@@ -23,7 +23,7 @@ import sys
 REF = pathlib.Path(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
 OUT = pathlib.Path(__file__).with_name("reference_goldens.json")
 
-TYPES = ("Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q8_1", "Q8_K")
+TYPES = ("Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q8_1", "Q8_K", "IQ4_XS")
 
 
 def quant_goldens():
@@ -45,7 +45,7 @@ def quant_goldens():
 def dot_goldens():
     src = (REF / "src/ggml/cpu/quants/golden.zig").read_text()
     out = {}
-    for name in ("q8_0", "q4_0", "q4_K", "q5_K", "q6_K"):
+    for name in ("q8_0", "q4_0", "q4_K", "q5_K", "q6_K", "iq4_xs"):
         m = re.search(r"pub const " + name + r" = Dot\{(.*?)\};", src, re.S)
         out[name] = {k: int(v, 16) for k, v in re.findall(r"\.(\w+) = 0x([0-9A-Fa-f]+)", m.group(1))}
     rows = {}

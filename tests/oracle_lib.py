@@ -13,12 +13,13 @@ ROOT = pathlib.Path(__file__).resolve().parents[1]
 LIB_PATH = ROOT / "oracle" / "liborc_qmm.so"
 
 TYPE_F32, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q8_1, TYPE_Q4_K, TYPE_Q5_K, TYPE_Q6_K, TYPE_Q8_K = 0, 2, 8, 9, 12, 13, 14, 15
+TYPE_IQ4_XS = 23
 TYPE_IDS = {"Q4_0": TYPE_Q4_0, "Q8_0": TYPE_Q8_0, "Q8_1": TYPE_Q8_1, "Q4_K": TYPE_Q4_K, "Q5_K": TYPE_Q5_K, "Q6_K": TYPE_Q6_K,
-            "Q8_K": TYPE_Q8_K}
+            "Q8_K": TYPE_Q8_K, "IQ4_XS": TYPE_IQ4_XS}
 BLOCK = {TYPE_Q4_0: (32, 18), TYPE_Q8_0: (32, 34), TYPE_Q8_1: (32, 36), TYPE_Q4_K: (256, 144), TYPE_Q5_K: (256, 176), TYPE_Q6_K: (256, 210),
-         TYPE_Q8_K: (256, 292)}
+         TYPE_Q8_K: (256, 292), TYPE_IQ4_XS: (256, 136)}
 _NAMES = {TYPE_Q4_0: "q4_0", TYPE_Q4_K: "q4_K", TYPE_Q5_K: "q5_K", TYPE_Q6_K: "q6_K", TYPE_Q8_0: "q8_0", TYPE_Q8_1: "q8_1",
-          TYPE_Q8_K: "q8_K"}
+          TYPE_Q8_K: "q8_K", TYPE_IQ4_XS: "iq4_xs"}
 IMPL_GENERIC, IMPL_AVX2 = 0, 1
 
 _lib = None
@@ -41,11 +42,11 @@ def lib():
         L.orc_fp16_to_fp32.argtypes = [ctypes.c_uint16]
         L.orc_nearest_int.restype = ctypes.c_int
         L.orc_nearest_int.argtypes = [ctypes.c_float]
-        for n in ("q4_0", "q4_K", "q5_K", "q6_K", "q8_0", "q8_1", "q8_K"):
+        for n in ("q4_0", "q4_K", "q5_K", "q6_K", "q8_0", "q8_1", "q8_K", "iq4_xs"):
             f = getattr(L, f"orc_quantize_row_{n}_ref")
             f.restype = None
             f.argtypes = [vp, vp, i64]
-        for n in ("q4_0", "q4_K", "q5_K", "q6_K", "q8_0", "q8_K"):
+        for n in ("q4_0", "q4_K", "q5_K", "q6_K", "q8_0", "q8_K", "iq4_xs"):
             f = getattr(L, f"orc_dequantize_row_{n}")
             f.restype = None
             f.argtypes = [vp, vp, i64]

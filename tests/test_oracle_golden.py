@@ -20,7 +20,7 @@ N_PER_ROW, N_ROWS = G["quant"]["n_per_row"], G["quant"]["n_rows"]
 N_ELEM = N_PER_ROW * N_ROWS
 
 
-@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q8_1", "Q8_K"])
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q8_1", "Q8_K", "IQ4_XS"])
 @pytest.mark.parametrize("pattern", QUANT_PATTERNS)
 def test_quantize_ref_matches_golden(name, pattern):
     """quants/k.zig:774-829 and legacy.zig:682-751 checkK/checkLegacy."""
@@ -35,7 +35,7 @@ def test_quantize_ref_matches_golden(name, pattern):
         assert O.fnv1a(deq) == rec["deq"], f"{name}/{pattern} dequantize floats differ"
 
 
-@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0"])
+@pytest.mark.parametrize("name", ["Q4_0", "Q4_K", "Q5_K", "Q6_K", "Q8_0", "IQ4_XS"])
 @pytest.mark.parametrize("pattern", QUANT_PATTERNS)
 def test_quantize_chunk_matches_golden(name, pattern):
     """quants/chunks.zig:758-790 checkChunk, with and without an importance matrix."""
@@ -60,7 +60,7 @@ def test_row_quantizers_match_golden(row, pattern):
     assert O.fnv1a(q) == want
 
 
-@pytest.mark.parametrize("kern", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K"])
+@pytest.mark.parametrize("kern", ["q8_0", "q4_0", "q4_K", "q5_K", "q6_K", "iq4_xs"])
 @pytest.mark.parametrize("pattern", VECDOT_PATTERNS)
 def test_vec_dot_generic_matches_golden(kern, pattern):
     """cpu/quants/testing.zig check: x via ggml_quantize_chunk(imatrix = ones),

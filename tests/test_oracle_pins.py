@@ -67,6 +67,14 @@ def _unit_q4_0_blocks(nblocks):
     return b
 
 
+def _unit_iq4_xs_blocks(nblocks):
+    """IQ4_XS with d = 1, random 6-bit scales and random level indices:
+    dequantized weight = (ls - 32) * level[q]."""
+    b = RNG.integers(0, 256, size=(nblocks, 136), dtype=np.uint8)
+    b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
+    return b
+
+
 def _unit_q8_0_blocks(nblocks):
     b = RNG.integers(0, 256, size=(nblocks, 34), dtype=np.uint8)
     b[:, 0:2] = np.frombuffer(F16_ONE.tobytes(), dtype=np.uint8)
@@ -77,7 +85,8 @@ def _unit_q8_0_blocks(nblocks):
                                            (O.TYPE_Q5_K, _unit_q5_k_blocks, 32),
                                            (O.TYPE_Q6_K, _unit_q6_k_blocks, 16),
                                            (O.TYPE_Q8_0, _unit_q8_0_blocks, 32),
-                                           (O.TYPE_Q4_0, _unit_q4_0_blocks, 32)])
+                                           (O.TYPE_Q4_0, _unit_q4_0_blocks, 32),
+                                           (O.TYPE_IQ4_XS, _unit_iq4_xs_blocks, 32)])
 def test_block_dots_against_unit_scale_dequantization(t, maker, group):
     nrows, K = 3, 512
     bs = 32 if t in (O.TYPE_Q8_0, O.TYPE_Q4_0) else 256
@@ -108,10 +117,14 @@ def test_block_dots_against_unit_scale_dequantization(t, maker, group):
 
 def _scale_of(t, row, j):
     """Sub-block scale of a unit-scale block, read back through the
-    dequantizer: a block whose codes are all 1 (Q4_K, Q5_K) or all 33 (Q6_K)
-    dequantizes to the scale itself."""
-    bs = {O.TYPE_Q4_K: 144, O.TYPE_Q5_K: 176, O.TYPE_Q6_K: 210}[t]
+    dequantizer: a block whose codes are all 1 (Q4_K, Q5_K), all 33 (Q6_K) or
+    all index 8 (IQ4_XS, level 1) dequantizes to the scale itself."""
+    bs = {O.TYPE_Q4_K: 144, O.TYPE_Q5_K: 176, O.TYPE_Q6_K: 210, O.TYPE_IQ4_XS: 136}[t]
     blk = row.reshape(-1, bs)[j // (16 if t == O.TYPE_Q6_K else 8)].copy()
+    if t == O.TYPE_IQ4_XS:
+        blk[8:] = 0x88  # every index 8, level 1
+        deq = O.dequantize(t, blk, 256)
+        return deq[32 * (j % 8)]
     if t == O.TYPE_Q4_K:
         blk[16:] = 0x11  # every nibble 1
         deq = O.dequantize(t, blk, 256)
@@ -128,7 +141,7 @@ def _scale_of(t, row, j):
     return deq[16 * sub]
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0, O.TYPE_IQ4_XS])
 def test_mul_mat_q8_1_f64_is_the_dequantized_dot(t):
     nrows, K, ncols = 5, 768, 3
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
@@ -171,10 +184,10 @@ def test_mul_mat_q8_1_f64_min_term(t, bs):
 
 
 VDT = {O.TYPE_Q4_K: O.TYPE_Q8_K, O.TYPE_Q5_K: O.TYPE_Q8_K, O.TYPE_Q6_K: O.TYPE_Q8_K, O.TYPE_Q8_0: O.TYPE_Q8_0,
-       O.TYPE_Q4_0: O.TYPE_Q8_0}
+       O.TYPE_Q4_0: O.TYPE_Q8_0, O.TYPE_IQ4_XS: O.TYPE_Q8_K}
 
 
-@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0])
+@pytest.mark.parametrize("t", [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_Q8_0, O.TYPE_Q4_0, O.TYPE_IQ4_XS])
 def test_mul_mat_generic_is_vec_dot_per_output(t):
     nrows, K, ncols = 7, 512, 4
     w = O.quantize_rows(t, RNG.standard_normal((nrows, K)).astype(np.float32) * 0.02)
