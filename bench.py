@@ -41,7 +41,8 @@ M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
 T_MMQ = 512
 
 
-BLOCKS = {"Q4_K": (256, 144), "Q5_K": (256, 176), "Q6_K": (256, 210), "Q8_0": (32, 34), "Q4_0": (32, 18)}
+BLOCKS = {"Q4_K": (256, 144), "Q5_K": (256, 176), "Q6_K": (256, 210), "Q8_0": (32, 34), "Q4_0": (32, 18),
+          "IQ4_XS": (256, 136)}
 
 
 def q4k_row_bytes(k):
@@ -176,7 +177,7 @@ def run_suite(name, torch, G, dev, reps):
                       ("Q4_K", 4096, 4096, "attn_q/o")]
             batches = (4, 6, 8, 9, 16, 24, 32)
         else:
-            shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K", "Q5_K", "Q4_0")
+            shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K", "Q5_K", "Q4_0", "IQ4_XS")
                       for k in (4096, 14336)]
             batches = (1, 32, 512)
         for qtype, M, Kx, label in shapes:

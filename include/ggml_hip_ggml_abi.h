@@ -59,6 +59,7 @@ enum ggml_type {
     GGML_TYPE_Q5_K = 13,
     GGML_TYPE_Q6_K = 14,
     GGML_TYPE_Q8_K = 15,
+    GGML_TYPE_IQ4_XS = 23,
     GGML_TYPE_I32 = 26,
 };
 

@@ -11,11 +11,11 @@
  * Conventions:
  *  - every pointer except `stream` and host-side scalars is a device pointer;
  *  - `type` is the ggml type id: GGML_TYPE_Q4_0 = 2, Q8_0 = 8, Q4_K = 12,
- *    Q5_K = 13, Q6_K = 14;
+ *    Q5_K = 13, Q6_K = 14, IQ4_XS = 23;
  *  - weights are ggml rows: `nrows` rows of `K` elements, each row
  *    `row_stride` bytes (ggml nb01); blocks in the reference layout
  *    (block_q4_K 144 B, block_q5_K 176 B, block_q6_K 210 B, block_q8_0 34 B,
- *    block_q4_0 18 B);
+ *    block_q4_0 18 B, block_iq4_xs 136 B);
  *  - activations / outputs are column-major f32 (ggml ne0 contiguous);
  *  - calls are asynchronous on `stream` (a hipStream_t; NULL = default
  *    stream), allocate nothing, and return 0 (hipSuccess) or a hipError_t
@@ -34,6 +34,7 @@ extern "C" {
 #endif
 
 #define GGML_HIP_QMM_TYPE_Q4_0 2
+#define GGML_HIP_QMM_TYPE_IQ4_XS 23
 #define GGML_HIP_QMM_TYPE_Q8_0 8
 #define GGML_HIP_QMM_TYPE_Q4_K 12
 #define GGML_HIP_QMM_TYPE_Q5_K 13

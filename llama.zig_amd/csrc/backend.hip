@@ -58,6 +58,7 @@ TypeInfo type_info(int t) {
     case GGML_TYPE_I32: return {1, 4, false};
     case GGML_TYPE_Q8_0: return {32, 34, true};
     case GGML_TYPE_Q4_0: return {32, 18, true};
+    case GGML_TYPE_IQ4_XS: return {256, 136, true};
     case GGML_TYPE_Q8_1: return {32, 36, true};
     case GGML_TYPE_Q4_K: return {256, 144, true};
     case GGML_TYPE_Q5_K: return {256, 176, true};
@@ -69,7 +70,7 @@ TypeInfo type_info(int t) {
 
 bool weight_type(int t) {
     return t == GGML_TYPE_Q4_0 || t == GGML_TYPE_Q4_K || t == GGML_TYPE_Q5_K || t == GGML_TYPE_Q6_K ||
-           t == GGML_TYPE_Q8_0;
+           t == GGML_TYPE_Q8_0 || t == GGML_TYPE_IQ4_XS;
 }
 
 // Alignment the kernels read a weight type's blocks at (16 for the K-quants

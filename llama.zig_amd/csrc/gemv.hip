@@ -53,6 +53,11 @@ struct Fmt<TYPE_Q8_0> {
     static constexpr int NSUB = 1;
 };
 template <>
+struct Fmt<TYPE_IQ4_XS> {
+    static constexpr int W = 64;
+    static constexpr int NSUB = 2;
+};
+template <>
 struct Fmt<TYPE_Q4_0> {
     static constexpr int W = 32;
     static constexpr int NSUB = 1;
@@ -76,9 +81,12 @@ struct Act<TYPE_Q4_K> {
     }
 };
 
-// Q5_K takes the activation slice as Q4_K does (64 values, two Q8_1 blocks).
+// Q5_K and IQ4_XS take the activation slice as Q4_K does (64 values, two
+// Q8_1 blocks).
 template <>
 struct Act<TYPE_Q5_K> : Act<TYPE_Q4_K> {};
+template <>
+struct Act<TYPE_IQ4_XS> : Act<TYPE_Q4_K> {};
 
 // Q6_K lane (sb, n, h) covers weights 256sb + 128n + 32g + 16h + [0,16), g=0..3.
 template <>
@@ -281,6 +289,48 @@ struct Wt<TYPE_Q6_K> {
             t += (float)T[g] * h2f(a.ds[g]) * s;
         }
         return h2f(d) * t;
+    }
+};
+
+// IQ4_XS (block_iq4_xs {d, scales_h, scales_l[4], qs[128]}, 136 B, at 8-byte
+// alignment): the lane's 64-weight slice c is sub-blocks 2c and 2c+1, the
+// 8-byte header and qs[32c .. 32c+32).  Byte j of a sub-block's 16 holds the
+// level indices of its elements j (low nibble) and j + 16 (high nibble); the
+// 6-bit scale of sub-block i is scales_l nibble i | scales_h bits 2i..2i+1 << 4,
+// biased by 32 (quantize_row_iq4_nl_impl, src/ggml/quants/iq4.zig:165-193).
+template <>
+struct Wt<TYPE_IQ4_XS> {
+    uint2 hdr;   // d | scales_h << 16, scales_l[4]
+    uint2 q[4];  // qs[32c .. 32c+32)
+    __device__ __forceinline__ void load(const uint8_t *row, int kl) {
+        const uint8_t *blk = row + (kl / QK_K) * IQ4XS_BYTES;
+        const int c = (kl % QK_K) / 64;
+        hdr = *reinterpret_cast<const uint2 *>(blk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = *reinterpret_cast<const uint2 *>(blk + 8 + 32 * c + 8 * i);
+    }
+    __device__ __forceinline__ void dots(const Act<TYPE_IQ4_XS> &a, int S[2], int = 0) const {
+        const uint32_t w[8] = {q[0].x, q[0].y, q[1].x, q[1].y, q[2].x, q[2].y, q[3].x, q[3].y};
+        const uint32_t av[16] = {a.q[0].x, a.q[0].y, a.q[0].z, a.q[0].w, a.q[1].x, a.q[1].y, a.q[1].z, a.q[1].w,
+                                 a.q[2].x, a.q[2].y, a.q[2].z, a.q[2].w, a.q[3].x, a.q[3].y, a.q[3].z, a.q[3].w};
+        const uint32_t m = 0x0F0F0F0Fu;
+        int s0 = 0, s1 = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            s0 = dot4(iq4nl_levels(w[t] & m), av[t], s0);
+            s0 = dot4(iq4nl_levels((w[t] >> 4) & m), av[4 + t], s0);
+            s1 = dot4(iq4nl_levels(w[4 + t] & m), av[8 + t], s1);
+            s1 = dot4(iq4nl_levels((w[4 + t] >> 4) & m), av[12 + t], s1);
+        }
+        S[0] = s0;
+        S[1] = s1;
+    }
+    __device__ __forceinline__ float combine(const Act<TYPE_IQ4_XS> &a, const int S[2], int kl) const {
+        const int c = (kl % QK_K) / 64;
+        const uint32_t sl = (hdr.y >> (8 * c)) & 0xFFu, sh = (hdr.x >> (16 + 4 * c)) & 0xFu;
+        const int ls0 = (int)((sl & 0xFu) | ((sh & 3u) << 4)) - 32, ls1 = (int)((sl >> 4) | ((sh >> 2) << 4)) - 32;
+        const float t = (float)S[0] * h2f(a.ds[0]) * (float)ls0 + (float)S[1] * h2f(a.ds[1]) * (float)ls1;
+        return h2f(hdr.x) * t;
     }
 };
 
@@ -840,6 +890,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     case TYPE_Q6_K: bs = QK_K; bb = Q6K_BYTES; break;
     case TYPE_Q8_0: bs = QK8; bb = Q80_BYTES; break;
     case TYPE_Q4_0: bs = QK8; bb = Q40_BYTES; break;
+    case TYPE_IQ4_XS: bs = QK_K; bb = IQ4XS_BYTES; break;
     default: return (int)hipErrorInvalidValue;
     }
     if (K % bs != 0 || K > (1 << 30) || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
@@ -865,6 +916,7 @@ int dispatch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stri
     case TYPE_Q5_K: return launch_type<TYPE_Q5_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     case TYPE_Q6_K: return launch_type<TYPE_Q6_K, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     case TYPE_Q4_0: return launch_type<TYPE_Q4_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
+    case TYPE_IQ4_XS: return launch_type<TYPE_IQ4_XS, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     default: return launch_type<TYPE_Q8_0, MODE>(wb, K, nrows, row_stride, yqs, ds, ncols, dst, dst_col_stride, dots, s);
     }
 }
@@ -999,6 +1051,10 @@ int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t
     case TYPE_Q4_0:
         launch_fx_type<TYPE_Q4_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
                                   fi, s);
+        break;
+    case TYPE_IQ4_XS:
+        launch_fx_type<TYPE_IQ4_XS>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit,
+                                    dst, fi, s);
         break;
     default:
         launch_fx_type<TYPE_Q8_0>(wb, gb, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,

@@ -81,9 +81,9 @@ struct Smem {
     // the column's d8 in K slot h: lanes 0-31 (K slots 0-3) read bd8[0],
     // lanes 32-63 (slots 4-7) read bd8[1], so only slot 0 pairs two nonzero
     // values and the MFMA returns exactly s_r * d8_c.
-    alignas(16) uint2 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K, Q5_K), sc_k (Q6_K) or d_b (Q8_0, Q4_0), exact in f16
+    alignas(16) uint2 asc[MmqFmt<TYPE>::NG][BM];  // sc_j (Q4_K, Q5_K), sc_k (Q6_K), ls_j - 32 (IQ4_XS) or d_b (Q8_0, Q4_0), exact in f16
     alignas(16) uint2 bd8[2][8][BN];              // d8 per (Q8_1 block, column)
-    alignas(16) float ad[BM];                        // d per row (Q4_K, Q6_K)
+    alignas(16) float ad[BM];                        // d per row (Q4_K, Q5_K, Q6_K, IQ4_XS)
     alignas(16) float admin[BM];                     // dmin per row (Q4_K)
     alignas(16) _Float16 am[BM][8];                  // m_j per row (Q4_K)
     alignas(16) _Float16 bs8[BN][8];                 // s8 per column (Q4_K)
@@ -195,6 +195,24 @@ struct AReg<TYPE_Q4_0> {
     }
 };
 
+// IQ4_XS: the 8-byte header (d, scales_h, scales_l) and this half's 64 qs
+// bytes (sub-blocks 4*half .. +3), at 8-byte alignment.
+template <>
+struct AReg<TYPE_IQ4_XS> {
+    uint2 hdr;
+    uint4 q[4];
+    __device__ __forceinline__ void load(const uint8_t *blk, int half) {
+        hdr = *reinterpret_cast<const uint2 *>(blk);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = ld16_u(blk + 8 + 64 * half + 16 * i);
+    }
+    __device__ __forceinline__ void zero() {
+        hdr = make_uint2(0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = make_uint4(0, 0, 0, 0);
+    }
+};
+
 __device__ __forceinline__ uint32_t f16_bits(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
@@ -281,6 +299,22 @@ __device__ __forceinline__ void store_a(Smem<TYPE, BN> &sm, const AReg<TYPE> &ar
 #pragma unroll
         for (int i = 0; i < 8; ++i) sm.asc[8 * n + i][r] = make_uint2(f16_bits((float)(int8_t)byte_of(ar.sc, 8 * n + i)), 0u);
         if (half == 0) sm.ad[r] = h2f(ar.d);
+    } else if constexpr (TYPE == TYPE_IQ4_XS) {
+        // levels as int8: low nibbles are elements 0..15 of a sub-block, high
+        // nibbles 16..31; scale ls - 32 per sub-block, d per row
+        const uint32_t m = 0x0F0F0F0Fu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int j = 4 * half + i;
+            int8_t *dst = sm.a + r * LDA + 32 * j;
+            const uint4 q = ar.q[i];
+            st16(dst, iq4nl_levels(q.x & m), iq4nl_levels(q.y & m), iq4nl_levels(q.z & m), iq4nl_levels(q.w & m));
+            st16(dst + 16, iq4nl_levels((q.x >> 4) & m), iq4nl_levels((q.y >> 4) & m), iq4nl_levels((q.z >> 4) & m),
+                 iq4nl_levels((q.w >> 4) & m));
+            const uint32_t ls = ((ar.hdr.y >> (4 * j)) & 0xFu) | (((ar.hdr.x >> (16 + 2 * j)) & 3u) << 4);
+            sm.asc[j][r] = make_uint2(f16_bits((float)((int)ls - 32)), 0u);
+        }
+        if (half == 0) sm.ad[r] = h2f(ar.hdr.x);
     } else if constexpr (TYPE == TYPE_Q4_0) {
         // q - 8 as int8: low nibbles are elements 0..15, high nibbles 16..31
         const uint32_t m = 0x0F0F0F0Fu;
@@ -383,6 +417,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
             if constexpr (TYPE == TYPE_Q4_K) areg.load(a_row + kb * Q4K_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q5_K) areg.load(a_row + kb * Q5K_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q6_K) areg.load(a_row + kb * Q6K_BYTES, ar_half);
+            else if constexpr (TYPE == TYPE_IQ4_XS) areg.load(a_row + kb * IQ4XS_BYTES, ar_half);
             else if constexpr (TYPE == TYPE_Q4_0) areg.load(a_row + (kb * 8 + 4 * ar_half) * Q40_BYTES, 0);
             else areg.load(a_row + (kb * 8 + 4 * ar_half) * Q80_BYTES, 0);
         } else {
@@ -674,6 +709,8 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
         return (row_stride < K / QK8 * Q80_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
     case TYPE_Q4_0:
         return (row_stride < K / QK8 * Q40_BYTES || row_stride % 2 || (uintptr_t)w % 2) ? (int)hipErrorInvalidValue : 0;
+    case TYPE_IQ4_XS:
+        return (row_stride < K / QK_K * IQ4XS_BYTES || row_stride % 8 || (uintptr_t)w % 8) ? (int)hipErrorInvalidValue : 0;
     default:
         return (int)hipErrorInvalidValue;
     }
@@ -752,6 +789,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     }
 }
@@ -775,6 +813,7 @@ extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t n
     case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
     }
 }

@@ -23,6 +23,7 @@ constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
 constexpr int Q80_BYTES = 34;
 constexpr int Q40_BYTES = 18;
+constexpr int IQ4XS_BYTES = 136;
 constexpr int64_t ROW_PAD = 512;  // activation row padding (MATRIX_ROW_PADDING)
 
 constexpr int TYPE_Q4_0 = 2;
@@ -30,14 +31,30 @@ constexpr int TYPE_Q8_0 = 8;
 constexpr int TYPE_Q4_K = 12;
 constexpr int TYPE_Q5_K = 13;
 constexpr int TYPE_Q6_K = 14;
+constexpr int TYPE_IQ4_XS = 23;
 
 __host__ __device__ constexpr int64_t pad_k(int64_t k) { return (k + ROW_PAD - 1) / ROW_PAD * ROW_PAD; }
 
 // Alignment of a weight type's blocks inside its rows, which the kernels read
-// at: 16 bytes for the 144- and 176-byte K-quant blocks (dwordx4 loads), 2 for
-// Q6_K's 210, Q8_0's 34 and Q4_0's 18.
+// at: 16 bytes for the 144- and 176-byte K-quant blocks (dwordx4 loads), 8 for
+// IQ4_XS's 136, 2 for Q6_K's 210, Q8_0's 34 and Q4_0's 18.
 __host__ __device__ constexpr int64_t block_align(int type) {
-    return type == TYPE_Q4_K || type == TYPE_Q5_K ? 16 : 2;
+    return type == TYPE_Q4_K || type == TYPE_Q5_K ? 16 : type == TYPE_IQ4_XS ? 8 : 2;
+}
+
+// IQ4_XS / IQ4_NL level lookup: four 4-bit indices (one per byte, 0..15) to
+// their int8 levels {-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38,
+// 53, 69, 89, 113} (kvalues_iq4nl, the format's table, reached by the
+// reference through @cImport, src/ggml/quants/iq4.zig:12-14).  Two byte
+// permutes look the index up in levels 0-7 and 8-15, a third picks per byte
+// by the index's bit 3.
+__device__ __forceinline__ uint32_t iq4nl_levels(uint32_t idx) {
+    constexpr uint32_t T0 = 0xBFAD9881u, T1 = 0xF6EADDCFu, T2 = 0x26190D01u, T3 = 0x71594535u;
+    const uint32_t sel = idx & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(T1, T0, sel);
+    const uint32_t hi = __builtin_amdgcn_perm(T3, T2, sel);
+    const uint32_t pick = ((idx >> 1) & 0x04040404u) | 0x03020100u;
+    return __builtin_amdgcn_perm(hi, lo, pick);
 }
 
 __device__ __forceinline__ float h2f(uint32_t bits16) {

@@ -20,6 +20,7 @@ GGML_MAX_NAME = 64
 # ggml_type ids
 GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q4_0, GGML_TYPE_Q8_0, GGML_TYPE_Q8_1 = 0, 1, 2, 8, 9
 GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K, GGML_TYPE_Q8_K, GGML_TYPE_I32 = 12, 13, 14, 15, 26
+GGML_TYPE_IQ4_XS = 23
 # ggml_op ids (position in op_name)
 GGML_OP_NONE, GGML_OP_ADD, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT_ID = 0, 2, 28, 29
 GGML_OP_RESHAPE, GGML_OP_VIEW, GGML_OP_PERMUTE, GGML_OP_TRANSPOSE = 35, 36, 37, 38
@@ -34,7 +35,7 @@ GGML_BACKEND_DEVICE_TYPE_GPU = 1
 
 # (block elements, block bytes) per type
 TYPE_BLOCK = {GGML_TYPE_F32: (1, 4), GGML_TYPE_F16: (1, 2), GGML_TYPE_I32: (1, 4), GGML_TYPE_Q4_0: (32, 18),
-              GGML_TYPE_Q8_0: (32, 34),
+              GGML_TYPE_Q8_0: (32, 34), GGML_TYPE_IQ4_XS: (256, 136),
               GGML_TYPE_Q8_1: (32, 36), GGML_TYPE_Q4_K: (256, 144), GGML_TYPE_Q5_K: (256, 176), GGML_TYPE_Q6_K: (256, 210),
               GGML_TYPE_Q8_K: (256, 292)}
 

@@ -119,7 +119,8 @@ def mmid(a_type, K, M, n_as, n_used, n_tokens, ne11=None):
 def test_supports_op(L):
     from ggml_hip import abi
     ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))  # noqa: E731
-    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q5_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0, abi.GGML_TYPE_Q4_0):
+    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q5_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0, abi.GGML_TYPE_Q4_0,
+              abi.GGML_TYPE_IQ4_XS):
         assert ok(mm(t, 4096, 4096, 1)[2])
         assert ok(mm(t, 4096, 1024, 512, batch=(2, 1, 4, 1))[2])  # broadcast over dim 2
         assert ok(mmid(t, 2048, 768, 128, 8, 512)[3])

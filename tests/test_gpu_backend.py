@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 NMSE_GATE = 5e-4
 TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0,
-         "Q4_0": O.TYPE_Q4_0}
+         "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}
 
 
 @pytest.fixture(scope="module")
@@ -72,7 +72,7 @@ def _mul_mat_graph(hb, t, wq, K, M, x, batch_w=1, batch_x=1):
     return hb.get(d, np.float32, (batch_x, N, M))
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("N", [1, 5, 40])
 def test_graph_mul_mat(hb, tname, N):
     import ggml_hip as G
@@ -99,7 +99,7 @@ def test_graph_mul_mat_broadcast_and_padding(hb):
         assert nmse(got[i], cpu) < NMSE_GATE, i
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q4_0", "IQ4_XS"])
 def test_graph_mul_mat_id(hb, tname):
     import ggml_hip as G
     from ggml_hip import abi

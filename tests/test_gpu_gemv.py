@@ -14,7 +14,7 @@ NMSE_GATE = 5e-4  # test-backend-ops' gate for mul_mat
 F64_TOL = 2e-6    # fp32 epilogue vs exact f64 of the same Q8_1 formula, / max|out|
 
 TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0,
-         "Q4_0": O.TYPE_Q4_0}
+         "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}
 
 
 def _run(tname, nrows, K, ncols):
@@ -29,7 +29,7 @@ def _run(tname, nrows, K, ncols):
     return t, wq, x, w_d, x_d, qs, got
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("ncols", [1, 2, 3, 8])
 def test_block_dots_exact(tname, ncols):
     import ggml_hip as G
@@ -42,7 +42,7 @@ def test_block_dots_exact(tname, ncols):
         np.testing.assert_array_equal(got[c], want)
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("nrows,K,ncols", [(4096, 4096, 1), (1024, 4096, 2), (1024, 4096, 4), (1000, 4096, 8),
                                            (333, 14336, 3), (96, 768, 5)])
 def test_gemv_parity(tname, nrows, K, ncols):
@@ -66,7 +66,8 @@ def test_gemv_parity(tname, nrows, K, ncols):
     ("Q4_K", 4100, 4096, 3), ("Q4_K", 4096, 2048, 8), ("Q4_K", 8195, 1024, 2), ("Q4_K", 8195, 1024, 7),
     ("Q4_K", 2500, 8192, 2), ("Q6_K", 2500, 8192, 4), ("Q6_K", 3000, 8192, 8), ("Q8_0", 2500, 8192, 3),
     ("Q5_K", 4100, 4096, 3), ("Q5_K", 2500, 8192, 8), ("Q5_K", 8195, 1024, 2), ("Q4_0", 2500, 8192, 3),
-    ("Q4_0", 4100, 4096, 8), ("Q4_0", 8195, 1056, 2)])
+    ("Q4_0", 4100, 4096, 8), ("Q4_0", 8195, 1056, 2), ("IQ4_XS", 4100, 4096, 3), ("IQ4_XS", 2500, 8192, 8),
+    ("IQ4_XS", 8195, 1024, 2)])
 def test_gemv_kernel_paths(tname, nrows, K, ncols):
     import ggml_hip as G
     t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, ncols)
@@ -82,7 +83,8 @@ def test_gemv_kernel_paths(tname, nrows, K, ncols):
                                            ("Q8_0", 4096, 2048), ("Q8_0", 333, 96), ("Q4_K", 4096, 768),
                                            ("Q6_K", 4100, 1536), ("Q8_0", 4097, 1024), ("Q5_K", 4096, 4096),
                                            ("Q5_K", 4100, 768), ("Q4_0", 4096, 4096), ("Q4_0", 4096, 2048),
-                                           ("Q4_0", 333, 96), ("Q4_0", 4097, 1024)])
+                                           ("Q4_0", 333, 96), ("Q4_0", 4097, 1024), ("IQ4_XS", 4096, 4096),
+                                           ("IQ4_XS", 4100, 768)])
 def test_gemv_fused_quantize(tname, nrows, K):
     """Quantize-in-GEMV for one column: bit-identical to the separate Q8_1
     quantizer followed by the two-rows-per-wave GEMV (which the unfused path

@@ -30,7 +30,7 @@ pytestmark = pytest.mark.gpu
 NMSE_GATE = 5e-4  # test-backend-ops' gate for mul_mat
 F64_TOL = 2e-6    # fp32 epilogue vs exact f64 of the same Q8_1 formula, / max|out|
 TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0,
-         "Q4_0": O.TYPE_Q4_0}
+         "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}
 OPS = {"REGLU": O.GLU_REGLU, "GEGLU": O.GLU_GEGLU, "SWIGLU": O.GLU_SWIGLU, "SWIGLU_OAI": O.GLU_SWIGLU_OAI,
        "SWIGLU_CLAMP": O.GLU_SWIGLU_CLAMP}
 ALPHA, LIMIT = 1.702, 7.0  # ggml_swiglu_oai's defaults as gpt-oss uses them
@@ -124,7 +124,8 @@ def _fused_case(tname, M, K, opname, with_bias):
 @pytest.mark.parametrize("tname,M,K", [("Q4_K", 14336, 4096), ("Q4_K", 768, 2048), ("Q4_K", 3000, 8192),
                                        ("Q6_K", 4100, 4096), ("Q6_K", 8200, 1024), ("Q8_0", 2048, 4096),
                                        ("Q8_0", 333, 96), ("Q5_K", 14336, 4096), ("Q5_K", 768, 2048),
-                                       ("Q4_0", 14336, 4096), ("Q4_0", 333, 96)])
+                                       ("Q4_0", 14336, 4096), ("Q4_0", 333, 96), ("IQ4_XS", 14336, 4096),
+                                       ("IQ4_XS", 768, 2048)])
 @pytest.mark.parametrize("with_bias", [False, True])
 def test_fused_gate_up_swiglu(tname, M, K, with_bias):
     import ggml_hip as G
@@ -329,7 +330,8 @@ def _moe(tname, n_as, M, K, n_tokens, n_ids, seed):
 
 @pytest.mark.parametrize("tname,n_tokens,opname", [("Q4_K", 1, "SWIGLU"), ("Q4_K", 5, "GEGLU"),
                                                     ("Q6_K", 2, "SWIGLU_OAI"), ("Q8_0", 8, "SWIGLU_CLAMP"),
-                                                    ("Q5_K", 3, "SWIGLU"), ("Q4_0", 4, "GEGLU")])
+                                                    ("Q5_K", 3, "SWIGLU"), ("Q4_0", 4, "GEGLU"),
+                                                    ("IQ4_XS", 6, "SWIGLU")])
 def test_fused_gate_up_glu_with_ids(tname, n_tokens, opname):
     """MoE decode's gate / up / GLU over the selected experts in one launch:
     every (token, slot) row equals the one-column fused kernel on its expert

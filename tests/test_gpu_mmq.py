@@ -12,10 +12,10 @@ pytestmark = pytest.mark.gpu
 NMSE_GATE = 5e-4
 F64_TOL = 2e-6  # vs the f64 Q8_1 formula, error / max|out|
 TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0,
-         "Q4_0": O.TYPE_Q4_0}
+         "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("nrows,K,ncols", [(256, 4096, 128), (200, 2048, 77), (128, 14336, 9), (384, 768, 300),
                                            (1000, 4096, 17), (200, 2048, 24), (64, 512, 32), (70, 1024, 3)])
 def test_mmq_parity(tname, nrows, K, ncols):
@@ -52,7 +52,7 @@ def test_mmq_config2_rows_subset():
     assert nmse(got[:, rows], cpu) < NMSE_GATE
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("nrows,K,ncols", [(128, 14336, 9), (256, 4096, 40), (2048, 14336, 32)])
 def test_mmq_split_k(tname, nrows, K, ncols):
     """Under-filled grids split K over workgroups; the partials are summed in a

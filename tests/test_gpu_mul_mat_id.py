@@ -12,7 +12,7 @@ pytestmark = pytest.mark.gpu
 NMSE_GATE = 5e-4
 F64_TOL = 2e-6
 TYPES = {"Q4_K": O.TYPE_Q4_K, "Q5_K": O.TYPE_Q5_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0,
-         "Q4_0": O.TYPE_Q4_0}
+         "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}
 
 
 def _experts(t, n_as, nrows, K):
@@ -42,7 +42,7 @@ def _check(tname, n_as, nrows, K, x, ids):
     return got
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("ne11", [1, 3])
 def test_mul_mat_id_random_ids(tname, ne11):
     n_as, nrows, K, n_tokens, n_ids = 8, 160, 512, 37, 3
@@ -100,7 +100,7 @@ def test_mul_mat_id_config4_qwen3_moe_gate():
     assert max_err_scaled(got[sub], ideal) < F64_TOL
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
 @pytest.mark.parametrize("n_tokens,ne11", [(1, 1), (3, 1), (8, 1), (2, 4)])
 def test_mul_mat_id_few_tokens(tname, n_tokens, ne11):
     """Up to 8 tokens run the one-launch GEMV over (token, slot) pairs: each
