@@ -400,13 +400,13 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
                        const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s) {
-    static int resident = 0;  // workgroups resident at once: 2 per CU
-    if (!resident) {
-        int dev = 0, cus = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-            cus = 256;
-        resident = 2 * cus;
-    }
+    // workgroups resident at once: 2 per CU of the current device (queried per
+    // call: a process may drive GPUs of different sizes; the query is a host
+    // attribute read)
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    const int resident = 2 * cus;
     const int64_t items = (int64_t)grid.x * grid.y * grid.z;
     if (items > 0x7FFFFFFF || K / QK_K > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
         return (int)hipErrorInvalidValue;
