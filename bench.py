@@ -441,7 +441,7 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES,
                      "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated (profiles/)",
                      "algorithmic_bytes": bytes_alg,
-                     "kernel": "gemv_fx_kernel<Q4_K, 16 waves, 2 rows per wave> (quantize-in-GEMV)",
+                     "kernel": "gemv_fx_kernel<Q4_K, 14 waves (2 workgroups per CU), 2 rows per wave> (quantize-in-GEMV)",
                      "avg_us": round(fused_batch_ms * 1e3, 3),
                      "timing": f"HIP graph of {n_ev} launches between HIP events, weights rotated over {ncopy} copies",
                      "event_pair_avg_us": round(fused_pair_ms * 1e3, 3),

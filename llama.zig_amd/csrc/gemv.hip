@@ -976,12 +976,36 @@ void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, in
                            s, w, wg, (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, FxIds{});
 }
 
+// CUs of the current device (the host's cached attribute; 256 on MI355X).
+int device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+        cus = 256;
+    return cus;
+}
+
+// Waves per workgroup for the plain one-launch GEMV on large matrices (2 rows
+// per wave): 16 or 14, whichever puts fewer rows on the busiest CU when the
+// workgroups are spread over the CUs (ties: 16, fewer column reads).  At
+// 14336 rows 16 waves make 448 workgroups, 2 on 192 CUs and 1 on 64 (64 rows
+// on the busiest), 14 waves make 512, 2 on every CU (56 rows): 8.15 against
+// 8.35 us, the same bits.
+int fx_plain_waves(int64_t nrows) {
+    const int64_t cus = device_cus();
+    auto busiest = [&](int64_t fw) {
+        const int64_t wgs = (nrows + 2 * fw - 1) / (2 * fw);
+        return (wgs + cus - 1) / cus * 2 * fw;
+    };
+    return busiest(14) < busiest(16) ? 14 : 16;
+}
+
 template <int TYPE>
 void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, int64_t row_stride,
                     const float *x, const float *bias, const float *gbias, int op, float alpha, float limit,
                     float *dst, const FxIds *fi, hipStream_t s) {
-    // Without a gate: 16 waves per workgroup on large matrices, 8 otherwise
-    // (the plain fused GEMV's measured choice).  Gated, measured on Q4_K
+    // Without a gate: 16 or 14 waves per workgroup on large matrices
+    // (fx_plain_waves), 8 otherwise (the plain fused GEMV's measured
+    // choice).  Gated, measured on Q4_K
     // (K = 2048..8192): from 8192 rows 8 waves of 2 rows of each matrix
     // (15.4 vs 15.9 us for 16 waves of 1 at 14336x4096), from 2048 rows 8
     // waves of 1, below that 4 waves of 1 (3.1 vs 3.4 us at 768x2048: more
@@ -1010,7 +1034,10 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
             launch_fx<TYPE, 8, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
         else launch_fx<TYPE, 4, 1, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
     } else {
-        if (big) launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        if (big && fx_plain_waves(nrows) == 14)
+            launch_fx<TYPE, 14, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
+        else if (big)
+            launch_fx<TYPE, 16, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
         else launch_fx<TYPE, 8, 2, false>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);
     }
 }

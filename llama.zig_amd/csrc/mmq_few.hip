@@ -65,6 +65,11 @@ __device__ __forceinline__ uint32_t f16_bits(float x) {
     return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
 }
 
+// f16 bits of byte b of v (an integer 0..255, exact in f16), zero-extended
+__device__ __forceinline__ uint32_t byte_f16(uint32_t v, int b) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)(uint16_t)((v >> (8 * b)) & 0xFFu));
+}
+
 __device__ __forceinline__ long as_long(uint2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
 
 // 16 bytes per lane from global memory to LDS at base + 16 * lane (base is
@@ -214,7 +219,7 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
             const uint2 a = make_uint2((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
             // d8 of block g sits in K slot 0 (g even) or 2 (g odd) of the
             // headers of blocks 2h, 2h+1 (h = g/2) as stored; A puts sc there
-            const uint32_t scf = f16_bits((float)(((g < 4 ? sc_lo : sc_hi) >> (8 * (g & 3))) & 0xFFu));
+            const uint32_t scf = byte_f16(g < 4 ? sc_lo : sc_hi, g & 3);
             const v4h sa = __builtin_bit_cast(v4h, (g & 1) ? make_uint2(0u, scf) : make_uint2(scf, 0u));
             const int c = 2 * g + (kq >> 1);
 #pragma unroll
@@ -234,8 +239,7 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
         // min term: K slot 4*kq + t holds sub-block 4*kq + t for kq < 2
         const uint32_t mb = ((kq & 1) ? mn_hi : mn_lo) & m_mn;
         const v4h am = __builtin_bit_cast(
-            v4h, make_uint2(f16_bits((float)(mb & 0xFFu)) | (f16_bits((float)((mb >> 8) & 0xFFu)) << 16),
-                            f16_bits((float)((mb >> 16) & 0xFFu)) | (f16_bits((float)(mb >> 24)) << 16)));
+            v4h, make_uint2(byte_f16(mb, 0) | (byte_f16(mb, 1) << 16), byte_f16(mb, 2) | (byte_f16(mb, 3) << 16)));
         float dr[4], dn[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {

@@ -84,7 +84,8 @@ def test_gemv_kernel_paths(tname, nrows, K, ncols):
                                            ("Q6_K", 4100, 1536), ("Q8_0", 4097, 1024), ("Q5_K", 4096, 4096),
                                            ("Q5_K", 4100, 768), ("Q4_0", 4096, 4096), ("Q4_0", 4096, 2048),
                                            ("Q4_0", 333, 96), ("Q4_0", 4097, 1024), ("IQ4_XS", 4096, 4096),
-                                           ("IQ4_XS", 4100, 768)])
+                                           ("IQ4_XS", 4100, 768), ("Q4_K", 14336, 4096), ("Q6_K", 11008, 4096),
+                                           ("IQ4_XS", 16390, 2048), ("Q8_0", 8192, 2048)])
 def test_gemv_fused_quantize(tname, nrows, K):
     """Quantize-in-GEMV for one column: bit-identical to the separate Q8_1
     quantizer followed by the two-rows-per-wave GEMV (which the unfused path
