@@ -62,11 +62,9 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     if ((uintptr_t)workspace % 16) return (int)hipErrorInvalidValue;
     // One column: the quantization runs inside the GEMV (one launch), which
     // measured faster than quantizer + GEMV on every decode shape (e.g. Q4_K
-    // 1024x4096 3.3 vs 5.1 us, 14336x4096 8.5 vs 9.6 us) but one: Q6_K rows of
-    // K >= 8192 on at most 4096 rows, where the K-split GEMV keeps the lead
-    // (4096x14336: 15.6 vs 20.8 us).
-    const bool ks_q6k = type == TYPE_Q6_K && K >= 8192 && nrows <= 4096;
-    if (ncols == 1 && !ks_q6k && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
+    // 1024x4096 3.3 vs 5.1 us, 14336x4096 8.5 vs 9.6 us, Q6_K 4096x14336 with
+    // K shares 14.9 vs 15.6 us).
+    if (ncols == 1 && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
         return hip_qmm_mul_mat_vec_f32(type, w, K, nrows, row_stride, x, dst, stream);
     const int64_t Kp = pad_k(K);
     int8_t *qs = (int8_t *)workspace;

@@ -629,6 +629,13 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
 // same order, so u and g equal that kernel's outputs bit for bit.  Biases are read at the start, from a valid address when absent (the
 // value is then unused), so no load sits behind a branch.
 //
+// KS > 1 (long rows): the workgroup's FW waves are FW / KS row groups times KS
+// K shares; share h of a row group contracts K-steps [h n / KS, (h + 1) n / KS)
+// of the n steps of the row, so each wave has its first (often only) step in
+// flight during the prologue.  Shares 1..KS-1 leave their segment sums in LDS
+// behind the Q8_1 copy and share 0 adds them in share order after a second
+// barrier (deterministic; one wave per row group runs the epilogue).
+//
 // IDS (MUL_MAT_ID with few tokens, the reference's MMVQ-with-ids path,
 // mmvq.zig:116-125, 531-622): grid y enumerates the (token t, slot s) pairs;
 // the pair's expert e = ids[t, s] selects the weights (w + e * expert_stride),
@@ -637,13 +644,17 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
 // (src/ggml/cpu/mulmat.zig:555-777).
 constexpr int FX_MAXK = 32768;
 
+// Byte offset of the K-share partial sums in the fused GEMV's dynamic LDS:
+// after the Q8_1 copy (K bytes + K / 32 scale words), 16-aligned.
+__host__ __device__ constexpr int fx_part_offset(int K) { return (K + K / 8 + 15) & ~15; }
+
 struct FxIds {
     const int32_t *ids;
     int64_t ids_stride, x_row_stride, expert_stride, dst_row_stride;
     int n_ids, ne11, n_as, n_pairs;
 };
 
-template <int TYPE, int FW, int R, bool GATE, bool IDS, int SEG>
+template <int TYPE, int FW, int R, bool GATE, bool IDS, int SEG, int KS>
 __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restrict__ w,
                                                              const uint8_t *__restrict__ wg, int K32, int64_t nrows,
                                                              int64_t row_stride, const float *x,
@@ -663,6 +674,8 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     constexpr int NSEG = 64 / SEG;            // weight rows side by side in a wave
     constexpr int CH = 8 * 64 * FW;           // activation values per prologue pass
     constexpr int STEP = SEG * F::W;          // K per step of a segment
+    constexpr int FWR = FW / KS;              // row groups per workgroup
+    static_assert(FW % KS == 0 && (KS == 1 || SEG == 64), "K shares: whole waves, one row per lane group");
     extern __shared__ __align__(16) uint8_t fx_lds[];
     int8_t *aq = reinterpret_cast<int8_t *>(fx_lds);
     uint32_t *ad = reinterpret_cast<uint32_t *>(fx_lds + K32);  // K32 % 32 == 0
@@ -673,10 +686,22 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     const int kqc = kq < K32 ? kq : 0;
     const float4 xa = *reinterpret_cast<const float4 *>(x + kqc);
     const float4 xb = *reinterpret_cast<const float4 *>(x + kqc + 4);
+    // K shares serve long rows: their second pass goes out ahead of the weights too
+    constexpr int PRE = KS > 1 ? 2 : 1;
+    float4 xc{}, xd{};
+    if constexpr (PRE > 1) {
+        const int k2 = kq + CH < K32 ? kq + CH : 0;
+        xc = *reinterpret_cast<const float4 *>(x + k2);
+        xd = *reinterpret_cast<const float4 *>(x + k2 + 4);
+    }
     const int lane = threadIdx.x & 63;
     const int seg = lane / SEG, sl = lane % SEG;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * (R * NSEG);  // the wave's first row
+    const int kh = wave / FWR, wr = wave - kh * FWR;  // K share, row group
+    const int64_t row0 = ((int64_t)blockIdx.x * FWR + wr) * (R * NSEG);  // the wave's first row
+    // the share's K-steps [s0, s1) (KS = 1: all of them)
+    const int nsteps = (K32 + STEP - 1) / STEP;
+    const int s0 = kh * nsteps / KS, s1 = (kh + 1) * nsteps / KS;
     // lane rows: row0 + r * NSEG + seg, clamped for loading
     int64_t rowc[R];
     float bu[R], bg[R];
@@ -692,7 +717,7 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
         if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its only barrier
 #pragma unroll
             for (int r = 0; r < R; ++r)
-                if (sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
+                if (kh == 0 && sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
             return;
         }
         w += (int64_t)expert * fi.expert_stride;
@@ -703,8 +728,8 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int r = 0; r < R; ++r) rows[m][r] = (m ? wg : w) + rowc[r] * row_stride;
-    int kl = sl * F::W;
-    bool live = kl < K32;
+    int kl = s0 * STEP + sl * F::W;
+    bool live = s0 < s1 && kl < K32;
     int klc = live ? kl : 0;  // lanes past K load a valid slice and add nothing
     Wt<TYPE> wt[NM][R];
 #pragma unroll
@@ -717,7 +742,13 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
         *reinterpret_cast<uint2 *>(aq + kq) = make_uint2(q.lo, q.hi);
         if ((threadIdx.x & 3) == 0) ad[kq / QK8] = q.ds;
     }
-    for (int k = kq + CH; k < K32; k += CH) {  // columns longer than one pass
+    if (PRE > 1 && kq + CH < K32) {
+        const float v[8] = {xc.x, xc.y, xc.z, xc.w, xd.x, xd.y, xd.z, xd.w};
+        const Q8Quad q = q8_1_quantize_quad(v);
+        *reinterpret_cast<uint2 *>(aq + kq + CH) = make_uint2(q.lo, q.hi);
+        if ((threadIdx.x & 3) == 0) ad[(kq + CH) / QK8] = q.ds;
+    }
+    for (int k = kq + PRE * CH; k < K32; k += CH) {  // columns longer than the passes above
         const float4 ya = *reinterpret_cast<const float4 *>(x + k);
         const float4 yb = *reinterpret_cast<const float4 *>(x + k + 4);
         const float v[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
@@ -726,7 +757,9 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
         if ((threadIdx.x & 3) == 0) ad[k / QK8] = q.ds;
     }
     __syncthreads();
-    if (row0 >= nrows) return;  // uniform per wave, after the workgroup's last barrier
+    // uniform per wave, after the workgroup's last barrier (K shares meet again
+    // at the end: their waves past the rows compute clamped rows and store nothing)
+    if (KS == 1 && row0 >= nrows) return;
     float acc[NM][R];
 #pragma unroll
     for (int m = 0; m < NM; ++m)
@@ -750,7 +783,7 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     // second register set: that would cost the occupancy the single-step
     // case runs on, and with many waves per SIMD the other waves cover the
     // latency.
-    for (int k0 = STEP; k0 < K32; k0 += STEP) {
+    for (int k0 = (s0 + 1) * STEP; k0 < s1 * STEP; k0 += STEP) {  // s1 <= nsteps: k0 < K32
         kl = k0 + sl * F::W;
         live = kl < K32;
         klc = live ? kl : 0;
@@ -761,10 +794,38 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
         contract(wt);
     }
     // Segment sums land in each segment's last lane, which writes its rows.
+    float us[R], gs[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float u = seg_sum<SEG>(acc[0][r]);
-        const float g = GATE ? seg_sum<SEG>(acc[NM - 1][r]) : 0.0f;
+        us[r] = seg_sum<SEG>(acc[0][r]);
+        gs[r] = GATE ? seg_sum<SEG>(acc[NM - 1][r]) : 0.0f;
+    }
+    if constexpr (KS > 1) {
+        // shares 1..KS-1: part[(h - 1) * FWR + group][m * R + r], behind the Q8_1 copy
+        float *part = reinterpret_cast<float *>(fx_lds + fx_part_offset(K32));
+        if (kh > 0 && sl == SEG - 1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                part[((kh - 1) * FWR + wr) * (NM * R) + r] = us[r];
+                if constexpr (GATE) part[((kh - 1) * FWR + wr) * (NM * R) + R + r] = gs[r];
+            }
+        }
+        __syncthreads();
+        if (kh > 0) return;
+        if (sl == SEG - 1) {
+#pragma unroll
+            for (int h = 1; h < KS; ++h)
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    us[r] += part[((h - 1) * FWR + wr) * (NM * R) + r];
+                    if constexpr (GATE) gs[r] += part[((h - 1) * FWR + wr) * (NM * R) + R + r];
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float u = us[r];
+        const float g = gs[r];
         const int64_t row = row0 + r * NSEG + seg;
         if (sl == SEG - 1 && row < nrows) {
             if (bias) u += bu[r];
@@ -968,12 +1029,24 @@ void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, in
     const int64_t nblocks = (nrows + ROWS - 1) / ROWS;
     const size_t lds = (size_t)K + (size_t)(K / QK8) * 4;
     if (fi)
-        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, true, SEG>),
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, true, SEG, 1>),
                            dim3((unsigned)nblocks, (unsigned)fi->n_pairs), dim3(64 * FW), lds, s, w, wg, (int)K, nrows,
                            row_stride, x, bias, gbias, op, alpha, limit, dst, *fi);
     else
-        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, false, SEG>), dim3((unsigned)nblocks), dim3(64 * FW), lds,
-                           s, w, wg, (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, FxIds{});
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, false, SEG, 1>), dim3((unsigned)nblocks), dim3(64 * FW),
+                           lds, s, w, wg, (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, FxIds{});
+}
+
+// The K-share form (plain, one column, no ids): FW / KS row groups of R rows
+// per workgroup.
+template <int TYPE, int FW, int R, int KS>
+void launch_fx_ks(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, const float *bias,
+                  float *dst, hipStream_t s) {
+    constexpr int64_t ROWS = (int64_t)(FW / KS) * R;
+    const int64_t nblocks = (nrows + ROWS - 1) / ROWS;
+    const size_t lds = (size_t)fx_part_offset((int)K) + (size_t)(KS - 1) * (FW / KS) * R * 4;
+    hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, false, false, 64, KS>), dim3((unsigned)nblocks), dim3(64 * FW),
+                       lds, s, w, nullptr, (int)K, nrows, row_stride, x, bias, nullptr, 0, 0.0f, 0.0f, dst, FxIds{});
 }
 
 // CUs of the current device (the host's cached attribute; 256 on MI355X).
@@ -1025,6 +1098,31 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
         return;
     }
     const bool big = nrows >= 8192;
+    // Rows of two or more K-steps on fewer than 8192 rows (ffn_down and the
+    // like), plain: K shares, sized for about one 16-wave workgroup per CU
+    // (rows / 256 rows each), with no more shares than steps.  Measured at
+    // K = 14336 (op us, against the one-share kernel): Q4_K 4096 rows 8.99 vs
+    // 10.91 (16 rows per workgroup, R = 2), 2048 rows 6.31 vs 8.95 (8 rows,
+    // R = 1), 1024 rows 5.00 vs 8.50 (4 rows, 4 shares); Q6_K 4096 rows 14.95
+    // vs 18.8 (R = 1: Q6_K and Q5_K take 76-84 registers at R = 2, and came
+    // out slower there), 6144 rows 21.3 vs 30.3; Q6_K 1024x8192 4.35 vs 9.1.
+    // Not for K <= 4096 above 2048 rows (Q8_0 / Q4_0, two steps of 2048):
+    // 4096x4096 took 5.80 / 4.94 us against 5.57 / 4.22 with one share.
+    const int64_t nsteps = (K + 64 * Fmt<TYPE>::W - 1) / (64 * Fmt<TYPE>::W);
+    if (!wg && !fi && !big && nsteps >= 2 && (K > 4096 || nrows <= 2048)) {
+        constexpr bool heavy = TYPE == TYPE_Q6_K || TYPE == TYPE_Q5_K;
+        if (nrows <= 1024) {
+            if (nsteps >= 4) launch_fx_ks<TYPE, 16, 1, 4>(w, K, nrows, row_stride, x, bias, dst, s);
+            else launch_fx_ks<TYPE, 8, 1, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+        } else if (nrows <= 2048 || heavy) {
+            launch_fx_ks<TYPE, 16, 1, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+        } else if (nrows <= 4096 || nsteps < 4) {
+            launch_fx_ks<TYPE, 16, 2, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+        } else {
+            launch_fx_ks<TYPE, 16, 2, 4>(w, K, nrows, row_stride, x, bias, dst, s);
+        }
+        return;
+    }
     if (wg) {
         if (big && TYPE == TYPE_Q4_K)
             launch_fx<TYPE, 8, 2, true>(w, wg, K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, fi, s);

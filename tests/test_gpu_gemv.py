@@ -111,6 +111,33 @@ def test_gemv_fused_quantize(tname, nrows, K):
     np.testing.assert_array_equal(op.reshape(fused.shape), fused)
 
 
+# One column on long rows (two or more K-steps of 64 lane slices) below 8192
+# rows: K shares of one workgroup, one case per share layout of the fused
+# GEMV's choice (4 shares of 1 row at <= 1024 rows, 2 shares of 1 row for 2-3
+# steps there, 2 of 1 row up to 2048 rows and for Q6_K / Q5_K, 2 of 2 rows up
+# to 4096 rows or under 4 steps, else 4 of 2 rows), with ragged row counts
+# (row groups past the end), part-filled last steps and a bias.
+@pytest.mark.parametrize("tname,nrows,K", [("Q4_K", 1001, 14336), ("Q8_0", 777, 8192), ("Q6_K", 1023, 8192),
+                                           ("Q4_0", 500, 4096), ("Q4_K", 2047, 11008), ("Q6_K", 4100, 14336),
+                                           ("Q5_K", 3001, 9216), ("IQ4_XS", 4095, 14336), ("Q4_K", 7000, 8192),
+                                           ("Q4_0", 6001, 14336), ("Q4_K", 5000, 16384), ("IQ4_XS", 257, 12288)])
+def test_gemv_fused_k_shares(tname, nrows, K):
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, got = _run(tname, nrows, K, 1)
+    fused = G.mul_mat_vec_f32(tname, w_d, K, x_d[0]).cpu().numpy()
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, 1)
+    assert max_err_scaled(fused, ideal) < F64_TOL, max_err_scaled(fused, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    assert nmse(fused, cpu) < NMSE_GATE
+    op = G.mul_mat(tname, w_d, x_d).cpu().numpy()
+    np.testing.assert_array_equal(op.reshape(fused.shape), fused)
+    # the bias is one fp32 add after the share sums
+    b = np.random.default_rng(nrows).standard_normal(nrows).astype(np.float32)
+    with_b = G.mul_mat_vec_fused(tname, w_d, K, x_d[0], bias=torch.from_numpy(b).cuda()).cpu().numpy()
+    np.testing.assert_array_equal(with_b.reshape(-1), fused.reshape(-1) + b)
+
+
 def test_gemv_config0_op_level():
     """Config 0: 4096x4096 Q4_K (seed 42) times a 4096x1 activation through the
     op-level entry point, against the CPU ggml path."""

@@ -100,6 +100,14 @@ def test_add_kernel_exact():
     np.testing.assert_array_equal(G.add_f32(_dev(a), _dev(b)).cpu().numpy(), a + b)
 
 
+def _one_share(tname, M, K):
+    """Whether the plain one-column GEMV runs M x K in one K share: rows of one
+    K-step of 64 lanes, at least 8192 rows, or at most 4096 columns on more
+    than 2048 rows (the gated kernel always does)."""
+    nsteps = -(-K // (64 * (32 if tname in ("Q8_0", "Q4_0") else 64)))
+    return nsteps < 2 or M >= 8192 or (K <= 4096 and M > 2048)
+
+
 def _fused_case(tname, M, K, opname, with_bias):
     import ggml_hip as G
     t = TYPES[tname]
@@ -130,7 +138,12 @@ def _fused_case(tname, M, K, opname, with_bias):
 def test_fused_gate_up_swiglu(tname, M, K, with_bias):
     import ggml_hip as G
     t, wu, wg, x, bu, bg, op, fused, u, g, unfused = _fused_case(tname, M, K, "SWIGLU", with_bias)
-    np.testing.assert_array_equal(fused, unfused)
+    if _one_share(tname, M, K):
+        np.testing.assert_array_equal(fused, unfused)
+    else:
+        # the plain lanes split their rows into K shares (another summation
+        # order than the gated kernel's): the same values to fp32 rounding
+        assert max_err_scaled(fused, unfused) < F64_TOL * 4, max_err_scaled(fused, unfused)
     x_d = _dev(x)
     y = G.quantize_q8_1(x_d, K).cpu().numpy()
     for wq, lane, b in ((wu, u, bu), (wg, g, bg)):
