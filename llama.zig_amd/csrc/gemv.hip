@@ -714,7 +714,7 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     }
     asm volatile("" ::: "memory");  // keep them ahead of the weight loads
     if constexpr (IDS) {
-        if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its only barrier
+        if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its barriers
 #pragma unroll
             for (int r = 0; r < R; ++r)
                 if (kh == 0 && sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
@@ -1037,16 +1037,21 @@ void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, in
                            lds, s, w, wg, (int)K, nrows, row_stride, x, bias, gbias, op, alpha, limit, dst, FxIds{});
 }
 
-// The K-share form (plain, one column, no ids): FW / KS row groups of R rows
-// per workgroup.
+// The K-share form (no gate): FW / KS row groups of R rows per workgroup.
 template <int TYPE, int FW, int R, int KS>
 void launch_fx_ks(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, const float *bias,
-                  float *dst, hipStream_t s) {
+                  float *dst, const FxIds *fi, hipStream_t s) {
     constexpr int64_t ROWS = (int64_t)(FW / KS) * R;
     const int64_t nblocks = (nrows + ROWS - 1) / ROWS;
     const size_t lds = (size_t)fx_part_offset((int)K) + (size_t)(KS - 1) * (FW / KS) * R * 4;
-    hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, false, false, 64, KS>), dim3((unsigned)nblocks), dim3(64 * FW),
-                       lds, s, w, nullptr, (int)K, nrows, row_stride, x, bias, nullptr, 0, 0.0f, 0.0f, dst, FxIds{});
+    if (fi)
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, false, true, 64, KS>),
+                           dim3((unsigned)nblocks, (unsigned)fi->n_pairs), dim3(64 * FW), lds, s, w, nullptr, (int)K,
+                           nrows, row_stride, x, bias, nullptr, 0, 0.0f, 0.0f, dst, *fi);
+    else
+        hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, false, false, 64, KS>), dim3((unsigned)nblocks),
+                           dim3(64 * FW), lds, s, w, nullptr, (int)K, nrows, row_stride, x, bias, nullptr, 0, 0.0f,
+                           0.0f, dst, FxIds{});
 }
 
 // CUs of the current device (the host's cached attribute; 256 on MI355X).
@@ -1107,19 +1112,22 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
     // vs 18.8 (R = 1: Q6_K and Q5_K take 76-84 registers at R = 2, and came
     // out slower there), 6144 rows 21.3 vs 30.3; Q6_K 1024x8192 4.35 vs 9.1.
     // Not for K <= 4096 above 2048 rows (Q8_0 / Q4_0, two steps of 2048):
-    // 4096x4096 took 5.80 / 4.94 us against 5.57 / 4.22 with one share.
+    // 4096x4096 took 5.80 / 4.94 us against 5.57 / 4.22 with one share.  The
+    // ids form takes the layout of the same rows without ids, so each of its
+    // rows equals the one-column op on that expert bit for bit (Mixtral's
+    // ffn_down experts, 4096x14336, run here).
     const int64_t nsteps = (K + 64 * Fmt<TYPE>::W - 1) / (64 * Fmt<TYPE>::W);
-    if (!wg && !fi && !big && nsteps >= 2 && (K > 4096 || nrows <= 2048)) {
+    if (!wg && !big && nsteps >= 2 && (K > 4096 || nrows <= 2048)) {
         constexpr bool heavy = TYPE == TYPE_Q6_K || TYPE == TYPE_Q5_K;
         if (nrows <= 1024) {
-            if (nsteps >= 4) launch_fx_ks<TYPE, 16, 1, 4>(w, K, nrows, row_stride, x, bias, dst, s);
-            else launch_fx_ks<TYPE, 8, 1, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+            if (nsteps >= 4) launch_fx_ks<TYPE, 16, 1, 4>(w, K, nrows, row_stride, x, bias, dst, fi, s);
+            else launch_fx_ks<TYPE, 8, 1, 2>(w, K, nrows, row_stride, x, bias, dst, fi, s);
         } else if (nrows <= 2048 || heavy) {
-            launch_fx_ks<TYPE, 16, 1, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+            launch_fx_ks<TYPE, 16, 1, 2>(w, K, nrows, row_stride, x, bias, dst, fi, s);
         } else if (nrows <= 4096 || nsteps < 4) {
-            launch_fx_ks<TYPE, 16, 2, 2>(w, K, nrows, row_stride, x, bias, dst, s);
+            launch_fx_ks<TYPE, 16, 2, 2>(w, K, nrows, row_stride, x, bias, dst, fi, s);
         } else {
-            launch_fx_ks<TYPE, 16, 2, 4>(w, K, nrows, row_stride, x, bias, dst, s);
+            launch_fx_ks<TYPE, 16, 2, 4>(w, K, nrows, row_stride, x, bias, dst, fi, s);
         }
         return;
     }

@@ -135,6 +135,30 @@ def test_mul_mat_id_few_tokens(tname, n_tokens, ne11):
     assert max_err_scaled(got, ideal) < F64_TOL
 
 
+# Long expert rows (Mixtral's ffn_down is 4096x14336 per expert): the ids form
+# splits K into shares with the one-column op's layout for the same rows, one
+# case per layout, with a dropped slot (-1) in every case.
+@pytest.mark.parametrize("tname,n_as,nrows,K,n_tokens", [("Q4_K", 3, 1000, 14336, 2), ("Q6_K", 3, 2100, 8192, 1),
+                                                         ("Q8_0", 3, 3000, 8192, 2), ("IQ4_XS", 2, 4100, 14336, 1),
+                                                         ("Q4_0", 3, 700, 4096, 2)])
+def test_mul_mat_id_few_tokens_long_rows(tname, n_as, nrows, K, n_tokens):
+    import ggml_hip as G
+    n_ids = 2
+    rng = np.random.default_rng(nrows + K)
+    ids = np.stack([rng.choice(n_as, n_ids, replace=False) for _ in range(n_tokens)]).astype(np.int32)
+    ids[0, 1] = -1
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    got = _check(tname, n_as, nrows, K, x, ids)
+    wq = _experts(TYPES[tname], n_as, nrows, K)
+    w_d, x_d = torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda()
+    for tt in range(n_tokens):
+        for s in range(n_ids):
+            if ids[tt, s] < 0:
+                continue
+            one = G.mul_mat_vec_f32(tname, w_d[ids[tt, s]], K, x_d[tt, 0]).cpu().numpy().reshape(-1)
+            np.testing.assert_array_equal(got[tt, s], one)
+
+
 def test_mul_mat_id_nine_tokens_take_the_grouped_path():
     """The boundary: 9 tokens go through grouping + grouped MMQ, with the same gates."""
     n_as, nrows, K, n_tokens, n_ids = 8, 256, 512, 9, 2
