@@ -13,6 +13,11 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
                            int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
+// gemv.hip: 2-4 f32 columns through the quantize-in-GEMV kernel, or
+// hipErrorNotSupported for shapes it does not take.
+int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
+                        int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream);
+
 namespace {
 size_t q8_1_bytes(int64_t K, int64_t ncols) {
     const int64_t Kp = pad_k(K);
@@ -66,6 +71,11 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     // K shares 14.9 vs 15.6 us).
     if (ncols == 1 && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
         return hip_qmm_mul_mat_vec_f32(type, w, K, nrows, row_stride, x, dst, stream);
+    if (ncols >= 2 && ncols <= 4 && !use_mmq(type, K, nrows, ncols)) {
+        const int e = qmm_mul_mat_fx_cols(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride,
+                                          stream);
+        if (e != (int)hipErrorNotSupported) return e;
+    }
     const int64_t Kp = pad_k(K);
     int8_t *qs = (int8_t *)workspace;
     void *ds = (uint8_t *)workspace + ncols * Kp;

@@ -835,6 +835,102 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     }
 }
 
+// 2-4 f32 columns with the quantization fused in (no gate, bias or ids): the
+// one-column kernel's prologue once per column -- all columns' first-pass
+// loads first, then the weights -- into NC LDS copies of K + K/8 bytes, then
+// each K-step's weights contract against every column in turn.  Column c of
+// x starts at x + c * x_col_stride, of dst at dst + c * dst_col_stride.  The
+// per-column arithmetic is the one-column kernel's with one K share, so a
+// column equals hip_qmm_mul_mat_vec_f32 on it bit for bit wherever that runs
+// one share.
+template <int TYPE, int FW, int R, int NC>
+__global__ __launch_bounds__(64 * FW) void gemv_fxn_kernel(const uint8_t *__restrict__ w, int K32, int64_t nrows,
+                                                             int64_t row_stride, const float *x,
+                                                             int64_t x_col_stride, float *__restrict__ dst,
+                                                             int64_t dst_col_stride) {
+    using F = Fmt<TYPE>;
+    constexpr int CH = 8 * 64 * FW;
+    constexpr int STEP = 64 * F::W;
+    extern __shared__ __align__(16) uint8_t fx_lds[];
+    const int cb = fx_part_offset(K32);  // bytes per column copy
+    const int kq = 8 * (int)threadIdx.x;
+    const int kqc = kq < K32 ? kq : 0;
+    float4 xa[NC], xb[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        xa[c] = *reinterpret_cast<const float4 *>(x + c * x_col_stride + kqc);
+        xb[c] = *reinterpret_cast<const float4 *>(x + c * x_col_stride + kqc + 4);
+    }
+    asm volatile("" ::: "memory");  // keep them ahead of the weight loads
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * FW + wave) * R;
+    const uint8_t *rows[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) rows[r] = w + (row0 + r < nrows ? row0 + r : nrows - 1) * row_stride;
+    int kl = lane * F::W;
+    bool live = kl < K32;
+    int klc = live ? kl : 0;
+    Wt<TYPE> wt[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) wt[r].load(rows[r], klc);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        int8_t *aq = reinterpret_cast<int8_t *>(fx_lds + c * cb);
+        uint32_t *ad = reinterpret_cast<uint32_t *>(fx_lds + c * cb + K32);
+        if (kq < K32) {
+            const float v[8] = {xa[c].x, xa[c].y, xa[c].z, xa[c].w, xb[c].x, xb[c].y, xb[c].z, xb[c].w};
+            const Q8Quad q = q8_1_quantize_quad(v);
+            *reinterpret_cast<uint2 *>(aq + kq) = make_uint2(q.lo, q.hi);
+            if ((threadIdx.x & 3) == 0) ad[kq / QK8] = q.ds;
+        }
+        for (int k = kq + CH; k < K32; k += CH) {
+            const float4 ya = *reinterpret_cast<const float4 *>(x + c * x_col_stride + k);
+            const float4 yb = *reinterpret_cast<const float4 *>(x + c * x_col_stride + k + 4);
+            const float v[8] = {ya.x, ya.y, ya.z, ya.w, yb.x, yb.y, yb.z, yb.w};
+            const Q8Quad q = q8_1_quantize_quad(v);
+            *reinterpret_cast<uint2 *>(aq + k) = make_uint2(q.lo, q.hi);
+            if ((threadIdx.x & 3) == 0) ad[k / QK8] = q.ds;
+        }
+    }
+    __syncthreads();
+    if (row0 >= nrows) return;  // uniform per wave, after the workgroup's only barrier
+    float acc[NC][R];
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[c][r] = 0.0f;
+    for (int k0 = 0;;) {
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            Act<TYPE> a;
+            a.load(reinterpret_cast<const int8_t *>(fx_lds + c * cb),
+                   reinterpret_cast<const uint32_t *>(fx_lds + c * cb + K32), klc);
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                int S[F::NSUB];
+                wt[r].dots(a, S, klc);
+                const float v = wt[r].combine(a, S, klc);
+                acc[c][r] += live ? v : 0.0f;
+            }
+        }
+        k0 += STEP;
+        if (k0 >= K32) break;
+        kl = k0 + lane * F::W;
+        live = kl < K32;
+        klc = live ? kl : 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) wt[r].load(rows[r], klc);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            const float u = seg_sum<64>(acc[c][r]);
+            if (lane == 63 && row0 + r < nrows) dst[c * dst_col_stride + row0 + r] = u;
+        }
+}
+
 template <int TYPE, int NC, int R, int D>
 int launch_rows(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                 const uint32_t *yds, float *dst, int64_t dst_col_stride, hipStream_t s) {
@@ -1148,6 +1244,38 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
     }
 }
 
+template <int TYPE, int FW, int R, int NC>
+void launch_fxn(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t xs,
+                float *dst, int64_t ds, hipStream_t s) {
+    const int64_t nblocks = (nrows + FW * R - 1) / (FW * R);
+    const size_t lds = (size_t)NC * fx_part_offset((int)K);
+    hipLaunchKernelGGL((gemv_fxn_kernel<TYPE, FW, R, NC>), dim3((unsigned)nblocks), dim3(64 * FW), lds, s, w, (int)K,
+                       nrows, row_stride, x, xs, dst, ds);
+}
+
+template <int TYPE, int NC>
+void launch_fxn_shape(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t xs,
+                      float *dst, int64_t ds, hipStream_t s) {
+    // the one-column kernel's workgroup shape below 8192 rows (8 waves of 2 rows)
+    launch_fxn<TYPE, 8, 2, NC>(w, K, nrows, row_stride, x, xs, dst, ds, s);
+}
+
+// Most columns per launch: 2 for the K-quants, 3 for IQ4_XS, 4 for Q8_0 /
+// Q4_0 (more spill registers or take over 128 of them).
+constexpr int fxn_max_cols(int type) {
+    return type == TYPE_Q8_0 || type == TYPE_Q4_0 ? 4 : type == TYPE_IQ4_XS ? 3 : 2;
+}
+
+template <int TYPE>
+void launch_fxn_type(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t ncols,
+                     int64_t xs, float *dst, int64_t ds, hipStream_t s) {
+    if constexpr (fxn_max_cols(TYPE) >= 4)
+        if (ncols == 4) return launch_fxn_shape<TYPE, 4>(w, K, nrows, row_stride, x, xs, dst, ds, s);
+    if constexpr (fxn_max_cols(TYPE) >= 3)
+        if (ncols == 3) return launch_fxn_shape<TYPE, 3>(w, K, nrows, row_stride, x, xs, dst, ds, s);
+    launch_fxn_shape<TYPE, 2>(w, K, nrows, row_stride, x, xs, dst, ds, s);
+}
+
 }  // namespace
 
 namespace {
@@ -1223,4 +1351,33 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void 
                    (int)n_ids, (int)ne11, (int)n_as, (int)(n_tokens * n_ids)};
     return fused_launch(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op, glu_alpha, glu_limit, dst,
                         &fi, stream);
+}
+
+// 2-4 f32 columns through the quantize-in-GEMV kernel (hip_qmm_mul_mat's
+// path for few columns; no workspace).  Returns hipErrorNotSupported when the
+// shape is outside what the kernel takes or where quantizer + GEMV measured
+// faster, so the caller quantizes first.  Measured (op us, quantizer + GEMV
+// against this): 4096x4096 Q4_K 2 columns 6.90 vs 5.09, Q8_0 4 columns 10.40
+// vs 8.24, IQ4_XS 3 columns 7.48 vs 6.42, 1024x4096 Q4_K 2 columns 5.47 vs
+// 4.42; slower from 8192 rows (14336x4096 Q4_K 2 columns 11.19 vs 12.08: the
+// doubled registers halve the workgroups per CU) and on rows of K > 4096
+// (4096x14336 Q4_K 13.08 vs 14.63: no K shares here).
+int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
+                        int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream) {
+    if (ncols < 2 || ncols > fxn_max_cols(type) || K % QK8 != 0 || K > 4096 || nrows >= 8192 ||
+        (uintptr_t)x % 16 || x_col_stride % 4)
+        return (int)hipErrorNotSupported;
+    if (int e = check_shape(type, K, nrows, row_stride)) return e;
+    if ((uintptr_t)w % (uintptr_t)block_align(type) || !dst || nrows <= 0) return (int)hipErrorInvalidValue;
+    hipStream_t s = (hipStream_t)stream;
+    const uint8_t *wb = (const uint8_t *)w;
+    switch (type) {
+    case TYPE_Q4_K: launch_fxn_type<TYPE_Q4_K>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    case TYPE_Q5_K: launch_fxn_type<TYPE_Q5_K>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    case TYPE_Q6_K: launch_fxn_type<TYPE_Q6_K>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    case TYPE_Q4_0: launch_fxn_type<TYPE_Q4_0>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    case TYPE_IQ4_XS: launch_fxn_type<TYPE_IQ4_XS>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    default: launch_fxn_type<TYPE_Q8_0>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
+    }
+    return (int)hipGetLastError();
 }

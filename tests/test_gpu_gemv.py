@@ -138,6 +138,29 @@ def test_gemv_fused_k_shares(tname, nrows, K):
     np.testing.assert_array_equal(with_b.reshape(-1), fused.reshape(-1) + b)
 
 
+# 2-4 f32 columns on at most 4096-long rows below 8192 rows: the op runs the
+# quantize-in-GEMV kernel over all columns in one launch (2 columns for the
+# K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0); each column equals the
+# one-column op on it bit for bit.
+@pytest.mark.parametrize("tname,nrows,K,ncols", [("Q4_K", 4096, 4096, 2), ("Q5_K", 1000, 4096, 2),
+                                                 ("Q6_K", 1024, 4096, 2), ("IQ4_XS", 777, 2048, 3),
+                                                 ("Q8_0", 4100, 4096, 4), ("Q4_0", 333, 96, 3),
+                                                 ("Q8_0", 5000, 1024, 3), ("Q4_0", 4097, 4096, 2),
+                                                 ("IQ4_XS", 6000, 4096, 2)])
+def test_op_few_columns_one_launch(tname, nrows, K, ncols):
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, _ = _run(tname, nrows, K, ncols)
+    got = G.mul_mat(tname, w_d, x_d).cpu().numpy()
+    for c in range(ncols):
+        one = G.mul_mat_vec_f32(tname, w_d, K, x_d[c]).cpu().numpy().reshape(-1)
+        np.testing.assert_array_equal(got[c], one)
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+
+
 def test_gemv_config0_op_level():
     """Config 0: 4096x4096 Q4_K (seed 42) times a 4096x1 activation through the
     op-level entry point, against the CPU ggml path."""
