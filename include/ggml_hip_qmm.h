@@ -176,8 +176,9 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
 /*
  * Op-level MUL_MAT: quantizes x to Q8_1 into `workspace` and runs the GEMV
  * (ncols <= 8) or the int8-MFMA MMQ (ncols > 8).  One column, and 2-4 columns
- * of rows with K <= 4096 below 8192 rows, skip the separate quantizer: the
- * GEMV quantizes the columns in its prologue.  Mirrors the dispatch in
+ * of rows with K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
+ * columns), skip the separate quantizer: the GEMV quantizes the columns in
+ * its prologue.  Mirrors the dispatch in
  * ggml_cuda_mul_mat (src/ggml/cuda/mulmat.zig:576-639).
  * x[c*x_col_stride + k] f32, dst[c*dst_col_stride + r] f32.
  */

@@ -138,7 +138,8 @@ def test_gemv_fused_k_shares(tname, nrows, K):
     np.testing.assert_array_equal(with_b.reshape(-1), fused.reshape(-1) + b)
 
 
-# 2-4 f32 columns on at most 4096-long rows below 8192 rows: the op runs the
+# 2-4 f32 columns on at most 4096-long rows below 8192 rows (and above, for
+# Q8_0 at 3-4 columns and rows of K <= 2048): the op runs the
 # quantize-in-GEMV kernel over all columns in one launch (2 columns for the
 # K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0); each column equals the
 # one-column op on it bit for bit.
@@ -146,7 +147,8 @@ def test_gemv_fused_k_shares(tname, nrows, K):
                                                  ("Q6_K", 1024, 4096, 2), ("IQ4_XS", 777, 2048, 3),
                                                  ("Q8_0", 4100, 4096, 4), ("Q4_0", 333, 96, 3),
                                                  ("Q8_0", 5000, 1024, 3), ("Q4_0", 4097, 4096, 2),
-                                                 ("IQ4_XS", 6000, 4096, 2)])
+                                                 ("IQ4_XS", 6000, 4096, 2), ("Q8_0", 9000, 4096, 4),
+                                                 ("Q4_K", 8200, 2048, 2), ("Q4_0", 8195, 1024, 4)])
 def test_op_few_columns_one_launch(tname, nrows, K, ncols):
     import ggml_hip as G
     t, wq, x, w_d, x_d, qs, _ = _run(tname, nrows, K, ncols)
