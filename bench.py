@@ -3,42 +3,55 @@
 
 Metric: "Q4_K GEMV GB/s (% HBM peak) @14336x4096 b=1; MMQ
 int8 TOPS @b=512".  A step is one ggml_mul_mat of the headline decode shape:
-Q4_K weight 14336x4096 times one f32 activation column; for one column the
-op runs a single kernel, the GEMV with the Q8_1 quantization fused in.  Inputs are resident in HBM; the
-weight is rotated over enough distinct copies (> 2x the 256 MB Infinity
-Cache) that every step streams it from HBM.  Steps are replayed from a HIP
-graph (one node per kernel) so the measurement is of the GPU, not of Python
-launch overhead.
+the Q4_K weight 14336x4096 times one f32 activation column; for one column
+the op runs a single kernel, the GEMV with the Q8_1 quantization fused in.
+Inputs are resident in HBM; the weight is rotated over enough distinct copies
+(> 2x the 256 MB Infinity Cache) that every step streams it from HBM.  The
+timed steps are replayed from one HIP graph of exactly --steps launches, so
+the measurement is of the GPU, not of Python launch overhead.
+
+Inputs: weights f32 N(0, 0.02) from seed 42 quantized with the reference's
+quantize_row_q4_K_ref, activations f32 N(0, 1) from seed 43.  Generating them
+takes the reference quantizer, which lives in the CPU checker (oracle/), so
+they are made in the CPU-baseline leg, which also times the reference's CPU
+path on the same bytes and checks the GPU results against it.  With --no-cpu
+the weights are random valid blocks instead (same work per step).
 
 Printed JSON (one line): value = whole-step GB/s (algorithmic bytes /
 wall-clock per step); roofline = the step's kernel alone (algorithmic bytes /
-its average duration from HIP events); mmq = the T=512 MMQ figure (TOPS and
-fraction of the int8 dense peak); cpu_baseline = the reference CPU path
-(restated AVX2 vec_dot_q4_K_q8_K in ggml's mul_mat chunking) on a bounded
-sample, timed on this host.
+its average duration from HIP events), with HBM traffic per launch measured
+by a rocprofv3 counter pass of this script run as a child process; mmq = the
+T=512 MMQ half of the metric with its own roofline, CPU baseline and parity;
+cpu_baseline = the reference CPU path (restated AVX2 vec_dot_q4_K_q8_K in
+ggml's mul_mat chunking) on a bounded sample, timed on this host; parity =
+NMSE and maximum relative error of the GPU op against that CPU path.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import pathlib
+import shutil
+import statistics
+import subprocess
 import sys
+import tempfile
 import time
 
 ROOT = pathlib.Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT / "llama.zig_amd"))
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
-# HBM bytes per launch of the op's kernel (the fused GEMV) measured with
-# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by a 64 MiB copy's readings
-# (x1.9993 / x1.0): profiles/gemv_q4_K_14336x4096_b1.md
-GEMV_TRAFFIC_BYTES = 33_296_005
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA
 INFINITY_CACHE = 256 << 20
+NMSE_GATE = 5e-4
 
 M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
 T_MMQ = 512
+CPU_SAMPLE_S = 10.0            # CPU work per baseline leg
 
 
 BLOCKS = {"Q4_K": (256, 144), "Q5_K": (256, 176), "Q6_K": (256, 210), "Q8_0": (32, 34), "Q4_0": (32, 18),
@@ -96,10 +109,8 @@ def event_time_kernel(torch, launch, n):
     return sum(ts) / len(ts), ts[len(ts) // 2]
 
 
-def event_time_batch(torch, launch, n):
-    """Average device time per launch of n back-to-back launches: the launches
-    are captured into one HIP graph, and a replay is bracketed by two HIP events
-    on the replaying stream, so host launch cost cannot starve the GPU."""
+def capture(torch, launch, n):
+    """n launches captured into one HIP graph on a side stream."""
     cs = torch.cuda.Stream()
     cs.wait_stream(torch.cuda.current_stream())
     g = torch.cuda.CUDAGraph()
@@ -109,6 +120,14 @@ def event_time_batch(torch, launch, n):
                 launch(i)
     torch.cuda.current_stream().wait_stream(cs)
     torch.cuda.synchronize()
+    return g
+
+
+def event_time_batch(torch, launch, n):
+    """Average device time per launch of n back-to-back launches: the launches
+    are captured into one HIP graph, and a replay is bracketed by two HIP events
+    on the replaying stream, so host launch cost cannot starve the GPU."""
+    g = capture(torch, launch, n)
     g.replay()  # warm
     torch.cuda.synchronize()
     s = torch.cuda.current_stream()
@@ -120,31 +139,184 @@ def event_time_batch(torch, launch, n):
     return a.elapsed_time(b) / n
 
 
-def cpu_baseline(w_host, x_host):
-    """Reference CPU path on a bounded sample: the restated x86 AVX2
-    vec_dot_q4_K_q8_K with quantize_row_q8_K_ref staging, in ggml's mul_mat
-    chunking, on up to 16 host threads."""
+# ---------------------------------------------------------------- the CPU-baseline leg
+
+def _oracle():
     sys.path.insert(0, str(ROOT / "tests"))
-    import oracle_lib as O  # noqa: E402  (test infrastructure: the checker / baseline only)
-    nth = max(1, min(16, os.cpu_count() or 1))
-    impl = O.IMPL_AVX2 if O.has_avx2() else O.IMPL_GENERIC
-    O.mul_mat(O.TYPE_Q4_K, w_host, M, K, x_host, nth=nth, impl=impl)  # warm-up
-    runs, t_total, t0 = 0, 0.0, time.perf_counter()
-    times = []
-    while (time.perf_counter() - t0 < 10.0 and runs < 2000) or runs < 20:
+    import oracle_lib as O  # noqa: E402  (test infrastructure: input generator, baseline and checker only)
+    return O
+
+
+def host_info(threads):
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
+    return {"cpu_model": model, "host_logical_cpus": os.cpu_count(), "cpus_allowed": allowed, "threads": threads,
+            "thread_cap": "16: the GPU box's CPU share for one GPU"}
+
+
+def reference_inputs(T):
+    """Seeded inputs quantized by the reference's own quantizer: weights f32
+    N(0, 0.02) seed 42 -> quantize_row_q4_K_ref, activations f32 N(0, 1) seed
+    43 (one column), and T columns for the MMQ leg (seed 43, index 1)."""
+    O = _oracle()
+    w = O.fill_normal(42, M * K, 0.0, 0.02).reshape(M, K)
+    wq = O.quantize_rows(O.TYPE_Q4_K, w)
+    x = O.fill_normal(43, K).reshape(1, K)
+    xt = O.fill_normal(43 + 1000, T * K).reshape(T, K)
+    return wq, x, xt
+
+
+def time_cpu(fn, budget_s, min_runs=5):
+    fn()  # warm-up
+    times, t0 = [], time.perf_counter()
+    while (time.perf_counter() - t0 < budget_s and len(times) < 2000) or len(times) < min_runs:
         t1 = time.perf_counter()
-        O.mul_mat(O.TYPE_Q4_K, w_host, M, K, x_host, nth=nth, impl=impl)
+        fn()
         times.append(time.perf_counter() - t1)
-        runs += 1
-    times.sort()
-    med = times[len(times) // 2]
+    return statistics.median(times), len(times)
+
+
+def parity(got, want):
+    import numpy as np
+    got = np.asarray(got, dtype=np.float64).reshape(-1)
+    want = np.asarray(want, dtype=np.float64).reshape(-1)
+    nmse = float(np.sum((got - want) ** 2) / max(float(np.sum(want * want)), 1e-300))
+    scale = np.maximum(np.abs(want), 1e-3 * float(np.max(np.abs(want))))
+    return {"nmse_vs_cpu": nmse, "max_rel_vs_cpu": float(np.max(np.abs(got - want) / scale)),
+            "max_rel_floor": "1e-3 x max|cpu|",
+            "max_err_over_max_vs_cpu": float(np.max(np.abs(got - want)) / max(float(np.max(np.abs(want))), 1e-300)),
+            "nmse_gate": NMSE_GATE, "pass": bool(nmse < NMSE_GATE)}
+
+
+def cpu_gemv_leg(wq, x, gpu_out):
+    """Reference CPU path at b=1 on a bounded sample: quantize_row_q8_K_ref
+    staging, the restated AVX2 vec_dot_q4_K_q8_K, ggml's mul_mat chunking, on
+    the host threads this process may use (at most 16); and the GPU op's
+    result checked against that CPU result."""
+    O = _oracle()
+    nth = O.gen_threads()
+    impl = O.IMPL_AVX2 if O.has_avx2() else O.IMPL_GENERIC
+    out = {}
+    med, runs = time_cpu(lambda: out.__setitem__("y", O.mul_mat(O.TYPE_Q4_K, wq, M, K, x, nth=nth, impl=impl)),
+                         CPU_SAMPLE_S, 20)
     bytes_alg = M * q4k_row_bytes(K) + K * 4 + M * 4
-    return {
-        "value": round(bytes_alg / med / 1e9, 3), "unit": "GB/s", "cores": nth,
-        "kind": "port",
-        "sample": f"Q4_K {M}x{K} b=1 mul_mat, {'AVX2' if impl == O.IMPL_AVX2 else 'generic'} vec_dot path, "
-                  f"median of {runs} runs ({med * 1e3:.3f} ms each)",
-    }
+    base = {"value": round(bytes_alg / med / 1e9, 3), "unit": "GB/s", "cores": nth, "kind": "port",
+            "sample": f"Q4_K {M}x{K} b=1 mul_mat (seed-42 weights), {'AVX2' if impl == O.IMPL_AVX2 else 'generic'} "
+                      f"vec_dot path, median of {runs} runs ({med * 1e3:.3f} ms each)",
+            **host_info(nth)}
+    return base, parity(gpu_out, out["y"])
+
+
+def cpu_mmq_leg(wq, xt, gpu_out):
+    """Reference CPU path at T=512: what ggml's CPU mul_mat runs on x86 for 8
+    or more columns, the tiled integer GEMM (restated AVX2 arm, Q8_K
+    activations); the vec_dot path where the host lacks AVX2."""
+    O = _oracle()
+    nth = O.gen_threads()
+    out = {}
+
+    def run():
+        y = O.mul_mat_tiled(O.TYPE_Q4_K, wq, M, K, xt, nth=nth)
+        out["y"] = y if y is not None else O.mul_mat(O.TYPE_Q4_K, wq, M, K, xt, nth=nth)
+
+    med, runs = time_cpu(run, CPU_SAMPLE_S, 3)
+    tiled = O.has_avx2()
+    ops = 2.0 * M * K * T_MMQ
+    base = {"value": round(ops / med / 1e12, 4), "unit": "TOP/s", "cores": nth, "kind": "port",
+            "sample": f"Q4_K {M}x{K} x T={T_MMQ} mul_mat (seed-42 weights), "
+                      f"{'x86 tiled GEMM (AVX2 arm)' if tiled else 'generic vec_dot path'}, "
+                      f"median of {runs} runs ({med * 1e3:.1f} ms each)",
+            **host_info(nth)}
+    return base, parity(gpu_out, out["y"])
+
+
+# ---------------------------------------------------------------- HBM traffic, measured live
+
+PROBE_KERNELS = {"gemv": "gemv_fx_kernel", "mmq": "mmq_q4k_dma_kernel", "copy": "copyBuffer"}
+COPY_BYTES = 64 << 20
+
+
+def traffic_probe():
+    """Child mode (run under rocprofv3 --pmc): a 64 MiB device copy for the
+    counter calibration, then the headline GEMV and the T=512 MMQ kernels on
+    rotated random weights."""
+    import torch
+    import ggml_hip as G
+    dev = torch.device("cuda:0")
+    gen = torch.Generator().manual_seed(7)
+    a = torch.randint(0, 255, (COPY_BYTES,), dtype=torch.uint8, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(8):
+        b.copy_(a)
+    ncopy = max(4, -(-2 * INFINITY_CACHE // (M * q4k_row_bytes(K))))
+    ws = [random_q4k(torch, M, K, gen, dev) for _ in range(ncopy)]
+    x = torch.randn((1, K), generator=gen).to(dev)
+    out = torch.empty((1, M), device=dev)
+    for i in range(4 * ncopy):
+        G.mul_mat_vec_f32("Q4_K", ws[i % ncopy], K, x, out=out)
+    xt = torch.randn((T_MMQ, K), generator=gen).to(dev)
+    qs, ds = G.quantize_q8_1_planar(xt)
+    outt = torch.empty((T_MMQ, M), device=dev)
+    for i in range(2 * ncopy):
+        G.mmq("Q4_K", ws[i % ncopy], K, qs, ds, out=outt)
+    torch.cuda.synchronize()
+
+
+def _counter_medians(csv_path):
+    vals = {k: [] for k in PROBE_KERNELS}
+    with open(csv_path) as f:
+        for r in csv.DictReader(f):
+            for key, pat in PROBE_KERNELS.items():
+                if pat in r["Kernel_Name"]:
+                    vals[key].append(float(r["Counter_Value"]))
+    return {k: statistics.median(v) for k, v in vals.items() if v}
+
+
+def measure_traffic():
+    """HBM bytes per launch of the headline GEMV and the MMQ: two rocprofv3
+    counter passes (FETCH_SIZE, then WRITE_SIZE, KiB per dispatch) over this
+    script's probe mode, each scaled by what the same counter reads for a
+    64 MiB copy.  Returns ({kernel: bytes}, calibration) or (None, reason)."""
+    prof = shutil.which("rocprofv3")
+    if not prof:
+        return None, "rocprofv3 not found"
+    med = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix="qmm_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "probe", "--",
+               sys.executable, str(ROOT / "bench.py"), "--traffic-probe"]
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=dict(os.environ, TMPDIR="/tmp"), capture_output=True, text=True,
+                               timeout=180)
+        except subprocess.TimeoutExpired:
+            shutil.rmtree(d, ignore_errors=True)
+            return None, f"rocprofv3 --pmc {counter} timed out"
+        files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+        if not files:
+            shutil.rmtree(d, ignore_errors=True)
+            return None, f"rocprofv3 --pmc {counter}: no counter file (rc {r.returncode}): {r.stderr[-300:]}"
+        med[counter] = _counter_medians(files[0])
+        shutil.rmtree(d, ignore_errors=True)
+    try:
+        f_scale = (COPY_BYTES / 1024) / med["FETCH_SIZE"]["copy"]
+        w_scale = (COPY_BYTES / 1024) / med["WRITE_SIZE"]["copy"]
+        out = {k: int(round((med["FETCH_SIZE"][k] * f_scale + med["WRITE_SIZE"][k] * w_scale) * 1024))
+               for k in ("gemv", "mmq")}
+    except (KeyError, ZeroDivisionError) as e:
+        return None, f"counter pass incomplete: {e!r}"
+    return out, {"fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4),
+                 "calibration": "64 MiB device copy, same counters, same pass"}
 
 
 def run_suite(name, torch, G, dev, reps):
@@ -323,16 +495,24 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg (random weights, no parity)")
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
+    ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
+    ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
     ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "few"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()
+    if args.traffic_probe:
+        traffic_probe()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        raise SystemExit("--steps must be >= 1 and --warmup >= 0")
 
+    import numpy as np
     import torch
     import ggml_hip as G
     dev = torch.device("cuda:0")
@@ -342,12 +522,22 @@ def main():
         run_suite(args.suite, torch, G, dev, args.reps)
         return
 
-    gen = torch.Generator().manual_seed(42)
     w_bytes = M * q4k_row_bytes(K)
     ncopy = max(4, -(-2 * INFINITY_CACHE // w_bytes))
-    weights = [random_q4k(torch, M, K, gen, dev) for _ in range(ncopy)]
+    gen = torch.Generator().manual_seed(42)
     xg = torch.Generator(device="cpu").manual_seed(43)
-    x = torch.randn((1, K), generator=xg, dtype=torch.float32).to(dev)
+    if not args.no_cpu:
+        wq_np, x_np, xt_np = reference_inputs(T_MMQ)
+        w_host = torch.from_numpy(wq_np)
+        weights = [w_host.to(dev) for _ in range(ncopy)]
+        x = torch.from_numpy(x_np).to(dev)
+        data = (f"synthetic: f32 N(0,0.02) weights from seed 42 quantized with quantize_row_q4_K_ref ({ncopy} "
+                "HBM copies of the same bytes), f32 N(0,1) activations from seed 43")
+    else:
+        weights = [random_q4k(torch, M, K, gen, dev) for _ in range(ncopy)]
+        x = torch.randn((1, K), generator=xg, dtype=torch.float32).to(dev)
+        xt_np = None
+        data = "synthetic: random valid Q4_K blocks (f16 d/dmin at N(0,0.02) scale), N(0,1) f32 activations"
     out = torch.empty((1, M), dtype=torch.float32, device=dev)
     ws = torch.empty(G.workspace_size("Q4_K", K, 1), dtype=torch.uint8, device=dev)
     qs = ws[: G.padded_k(K)].view(torch.int8).view(1, -1)
@@ -356,39 +546,28 @@ def main():
     def step(i):
         G.mul_mat("Q4_K", weights[i % ncopy], x, out=out, workspace=ws)
 
-    for i in range(max(args.warmup, ncopy)):
+    # W untimed warm-up steps, then exactly --steps steps in one HIP graph;
+    # the graph is replayed once untimed first (its upload), then timed.
+    for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
-
-    # one graph replay = ncopy steps (each step: quantize + GEMV)
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(graph, stream=s):
-            for i in range(ncopy):
-                step(i)
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    reps = max(1, -(-args.steps // ncopy))
-    steps = reps * ncopy
-    for _ in range(max(1, args.warmup // ncopy)):
-        graph.replay()
+    graph = capture(torch, step, args.steps)
+    graph.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(reps):
-        graph.replay()
+    graph.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    ms_per_step = wall * 1e3 / steps
+    ms_per_step = wall * 1e3 / args.steps
+    del graph
 
     bytes_alg = w_bytes + K * 4 + M * 4
     value = bytes_alg / (ms_per_step * 1e-3) / 1e9
 
-    # dominant kernel alone: the step is one kernel here (the GEMV with the
-    # Q8_1 quantization fused in); n back-to-back launches between two events
+    # The step's kernel alone (the GEMV with the Q8_1 quantization fused in):
+    # n back-to-back launches between two HIP events on the replaying stream
     # (agrees with rocprofv3's per-dispatch average); per-launch event pairs
-    # are reported beside it but carry ~2 us of event overhead.  The unfused
+    # carry ~2 us of event overhead and are reported beside it.  The unfused
     # pair (quantizer + GEMV on the quantized column) is timed for reference.
     n_ev = 8 * ncopy
     fused = lambda i: G.mul_mat_vec_f32("Q4_K", weights[i % ncopy], K, x, out=out)  # noqa: E731
@@ -400,8 +579,9 @@ def main():
         torch, lambda i: G.lib().hip_qmm_quantize_q8_1_planar(
             G._ptr(x), K, 1, K, G._ptr(qs), G._ptr(ds), G._stream()), n_ev)
     achieved = bytes_alg / (fused_batch_ms * 1e-3) / 1e9
+    gpu_out = G.mul_mat("Q4_K", weights[0], x).cpu().numpy()
 
-    # The same shape as the FFN's gate and up projections fused with SWIGLU
+    # The FFN's gate and up projections of the same shape fused with SWIGLU
     # into one kernel (the GEMV fusion epilogue), beside the three launches it
     # replaces: reported, not the headline metric.
     gates = [random_q4k(torch, M, K, gen, dev) for _ in range(ncopy)]
@@ -426,20 +606,21 @@ def main():
         "value": round(value, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": steps,
+        "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8 dot products, fp32 epilogue (Q4_K weights x Q8_1 activations)",
-        "data": "synthetic: random valid Q4_K blocks (f16 d/dmin at N(0,0.02) scale), N(0,1) f32 activations",
+        "data": data,
         "config": {"workload": "Llama-3-8B ffn_gate/up Q4_K decode GEMV (config 1)", "rows": M, "K": K,
                    "batch": 1, "weight_copies": ncopy,
-                   "step": "mul_mat: GEMV with the Q8_1 quantization fused (one kernel), HIP-graph replay"},
+                   "step": "mul_mat: GEMV with the Q8_1 quantization fused (one kernel)",
+                   "timed": f"one HIP-graph replay of exactly {args.steps} steps between synchronizes; untimed "
+                            f"before it: {args.warmup} warm-up steps and one replay of the same graph (upload)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": GEMV_TRAFFIC_BYTES,
-                     "traffic_source": "rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated (profiles/)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": bytes_alg,
                      "kernel": "gemv_fx_kernel<Q4_K, 14 waves (2 workgroups per CU), 2 rows per wave> (quantize-in-GEMV)",
                      "avg_us": round(fused_batch_ms * 1e3, 3),
@@ -454,24 +635,60 @@ def main():
                                "unfused_3_launches_us": round(ffn_unfused_ms * 1e3, 3)},
     }
 
+    gpu_mmq_out = None
     if not args.no_mmq:
-        xt = torch.randn((T_MMQ, K), generator=xg, dtype=torch.float32).to(dev)
+        if xt_np is not None:
+            xt = torch.from_numpy(xt_np).to(dev)
+        else:
+            xt = torch.randn((T_MMQ, K), generator=xg, dtype=torch.float32).to(dev)
         qst, dst_ = G.quantize_q8_1_planar(xt)
         outt = torch.empty((T_MMQ, M), dtype=torch.float32, device=dev)
         n_m = 2 * ncopy
         mmq = lambda i: G.mmq("Q4_K", weights[i % ncopy], K, qst, dst_, out=outt)  # noqa: E731
         mmq_avg_ms = event_time_batch(torch, mmq, n_m)
         _, mmq_med_ms = event_time_kernel(torch, mmq, n_m)
+        wst = torch.empty(G.workspace_size("Q4_K", K, T_MMQ, M), dtype=torch.uint8, device=dev)
+        op = lambda i: G.mul_mat("Q4_K", weights[i % ncopy], xt, out=outt, workspace=wst)  # noqa: E731
+        op_avg_ms = event_time_batch(torch, op, n_m)
+        gpu_mmq_out = G.mul_mat("Q4_K", weights[0], xt).cpu().numpy()
         ops = 2.0 * M * K * T_MMQ
         tops = ops / (mmq_avg_ms * 1e-3) / 1e12
-        result["mmq"] = {"workload": "Q4_K 14336x4096 x T=512 (config 2)", "tops": round(tops, 2),
-                         "peak_tops": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
-                         "avg_us": round(mmq_avg_ms * 1e3, 2), "event_pair_median_us": round(mmq_med_ms * 1e3, 2)}
+        result["mmq"] = {
+            "workload": f"Q4_K {M}x{K} x T={T_MMQ} (config 2)", "tops": round(tops, 2), "peak_tops": INT8_PEAK_TOPS,
+            "frac": round(tops / INT8_PEAK_TOPS, 4), "avg_us": round(mmq_avg_ms * 1e3, 2),
+            "event_pair_median_us": round(mmq_med_ms * 1e3, 2),
+            "op_avg_us": round(op_avg_ms * 1e3, 2),
+            "op": "mul_mat on f32 columns: Q8_1 quantizer + the MMQ",
+            "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
+                         "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                         "algorithmic_ops": ops, "algorithmic_bytes_read": w_bytes + T_MMQ * (G.padded_k(K) * 9 // 8),
+                         "kernel": "mmq_q4k_dma_kernel (int8 MFMA, direct-to-LDS staging)",
+                         "timing": f"HIP graph of {n_m} launches between HIP events, weights rotated over {ncopy} copies"},
+        }
+
+    if not args.no_traffic:
+        traffic, cal = measure_traffic()
+        if traffic:
+            result["roofline"]["traffic"] = traffic["gemv"]
+            result["roofline"]["traffic_ratio"] = round(traffic["gemv"] / bytes_alg, 4)
+            result["roofline"]["traffic_source"] = {"method": "rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE, over "
+                                                              "bench.py --traffic-probe, in this run", **cal}
+            if "mmq" in result:
+                rf = result["mmq"]["roofline"]
+                rf["traffic"] = traffic["mmq"]
+                rf["traffic_ratio_to_reads"] = round(traffic["mmq"] / (rf["algorithmic_bytes_read"] + T_MMQ * M * 4), 4)
+        else:
+            result["roofline"]["traffic_source"] = f"not measured: {cal}"
 
     if not args.no_cpu:
-        w_host = weights[0].cpu().numpy()
-        x_host = x.cpu().numpy()
-        result["cpu_baseline"] = cpu_baseline(w_host, x_host)
+        base, par = cpu_gemv_leg(wq_np, x_np, gpu_out)
+        result["cpu_baseline"] = base
+        result["parity"] = {"op": f"mul_mat Q4_K {M}x{K} b=1, GPU against the CPU baseline's own result", **par}
+        if gpu_mmq_out is not None:
+            mbase, mpar = cpu_mmq_leg(wq_np, xt_np, gpu_mmq_out)
+            result["mmq"]["cpu_baseline"] = mbase
+            result["mmq"]["parity"] = {"op": f"mul_mat Q4_K {M}x{K} x T={T_MMQ}, GPU against the CPU baseline's "
+                                             "own result", **mpar}
 
     print(json.dumps(result))
 

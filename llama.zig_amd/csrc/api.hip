@@ -63,6 +63,8 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
                                const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
                                int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream) {
     if (ncols <= 0 || !workspace || !x || !dst) return (int)hipErrorInvalidValue;
+    // columns must not overlap, whichever kernel the shape picks
+    if (ncols > 1 && (dst_col_stride < nrows || x_col_stride < K)) return (int)hipErrorInvalidValue;
     if (workspace_size < hip_qmm_mul_mat_workspace_size(type, K, nrows, ncols)) return (int)hipErrorInvalidValue;
     if ((uintptr_t)workspace % 16) return (int)hipErrorInvalidValue;
     // One column: the quantization runs inside the GEMV (one launch), which

@@ -674,6 +674,15 @@ const ggml_tensor *bias_of(const ggml_tensor *add, const ggml_tensor *mm) {
     return nullptr;
 }
 
+// Whether t is one of the nodes g->nodes[i0 .. i0+n): a fused launch
+// computes none of them before it reads its operands, so such a tensor
+// cannot serve as a bias (ADD(mm, mm), or one lane's ADD as the other's bias).
+bool in_run(const ggml_cgraph *g, int i0, int n, const ggml_tensor *t) {
+    for (int j = i0; j < i0 + n && j < g->n_nodes; ++j)
+        if (g->nodes[j] == t) return true;
+    return false;
+}
+
 // ggml_cuda_should_fuse_mul_mat (src/ggml/cuda/mulmat.zig:355-410) for the
 // one-column kernel: same weight type, shape and strides, the same
 // activation tensor, a split non-swapped GLU of a fused op.
@@ -773,7 +782,8 @@ int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
         // which lane gates follows from the GLU's sources (fusion.zig:1313-1325)
         const bool a_gates = glu->src[0] == aa && glu->src[1] == ab;
         const bool b_gates = glu->src[0] == ab && glu->src[1] == aa;
-        if (bias_ok(ba, ma) && bias_ok(bb, mb) && (a_gates || b_gates)) {
+        if (bias_ok(ba, ma) && bias_ok(bb, mb) && !in_run(g, i, 5, ba) && !in_run(g, i, 5, bb) &&
+            (a_gates || b_gates)) {
             const ggml_tensor *gate = a_gates ? ma : mb, *up = a_gates ? mb : ma;
             const ggml_tensor *gb = a_gates ? ba : bb, *ub = a_gates ? bb : ba;
             if (gate_up_fusable(up, gate, glu) && run_is_closed(g, i, 5, glu) &&
@@ -792,7 +802,8 @@ int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
     if (is(i + 1, GGML_OP_ADD)) {
         const ggml_tensor *mm = node(i), *add = node(i + 1);
         const ggml_tensor *b = bias_of(add, mm);
-        if (bias_ok(b, mm) && vec_fusable(mm) && same_shape(add, mm) && run_is_closed(g, i, 2, add) &&
+        if (bias_ok(b, mm) && !in_run(g, i, 2, b) && vec_fusable(mm) && same_shape(add, mm) &&
+            run_is_closed(g, i, 2, add) &&
             launch_fused(ctx, mm, nullptr, b, nullptr, add, ok))
             return 2;
     }
@@ -979,6 +990,10 @@ extern "C" {
 bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
     if (!op) return false;
     if (is_noop(op->op)) return true;
+    // With fusion off (GGML_HIP_DISABLE_FUSION) the GLU and bias-add nodes
+    // have no reason to stay on the device: the answer narrows to MUL_MAT /
+    // MUL_MAT_ID and the no-op views, and everything else stays on the CPU.
+    if ((op->op == GGML_OP_GLU || op->op == GGML_OP_ADD) && fusion_disabled()) return false;
     if (op->op == GGML_OP_GLU) {
         // f32 GLU of a device op (glu_op_supported), split or one-tensor form
         const ggml_tensor *a = op->src[0], *b = op->src[1];

@@ -1362,14 +1362,16 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void 
 // 4.42; slower from 8192 rows (14336x4096 Q4_K 2 columns 11.19 vs 12.08,
 // IQ4_XS 12.44 vs 14.10: the doubled registers halve the workgroups per CU)
 // but for Q8_0 at 3-4 columns (14336x4096, 4 columns: 24.56 vs 20.77) and
-// rows of K <= 2048 (8192x2048 Q4_K 2 columns 7.71 vs 5.86); slower on rows
+// Q4_K / Q4_0 rows of K <= 2048 (8192x2048 Q4_K 2 columns 7.71 vs 5.86; the
+// other types were not measured there and keep quantizer + GEMV); slower on rows
 // of K > 4096 (4096x14336 Q4_K 13.08 vs 14.63: no K shares here).
 int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
                         int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream) {
-    const bool big_wins = K <= 2048 || (type == TYPE_Q8_0 && ncols >= 3);
+    const bool big_wins = (K <= 2048 && (type == TYPE_Q4_K || type == TYPE_Q4_0)) || (type == TYPE_Q8_0 && ncols >= 3);
     if (ncols < 2 || ncols > fxn_max_cols(type) || K % QK8 != 0 || K > 4096 || (nrows >= 8192 && !big_wins) ||
         (uintptr_t)x % 16 || x_col_stride % 4)
         return (int)hipErrorNotSupported;
+    if (dst_col_stride < nrows || x_col_stride < K) return (int)hipErrorInvalidValue;
     if (int e = check_shape(type, K, nrows, row_stride)) return e;
     if ((uintptr_t)w % (uintptr_t)block_align(type) || !dst || nrows <= 0) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;

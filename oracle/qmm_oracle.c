@@ -1916,14 +1916,476 @@ static uint64_t splitmix64(uint64_t *s) {
     return z ^ (z >> 31);
 }
 
-void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out) {
-    uint64_t s = seed;
+/* The values from element i0 (even) on: SplitMix64 advances its state by one
+ * constant per draw and each pair of outputs takes two draws, so the state
+ * before pair i0/2 is seed + i0 * 0x9E3779B97F4A7C15. */
+static void fill_normal_from(uint64_t seed, int64_t i0, int64_t n, float mean, float stddev, float *out) {
+    uint64_t s = seed + (uint64_t)i0 * 0x9E3779B97F4A7C15ull;
     const double two_pi = 6.283185307179586476925286766559;
-    for (int64_t i = 0; i < n; i += 2) {
+    for (int64_t i = i0; i < n; i += 2) {
         const double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740992.0); /* (0,1] */
         const double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);       /* [0,1) */
         const double r = sqrt(-2.0 * log(u1));
         out[i] = (float)(mean + stddev * r * cos(two_pi * u2));
         if (i + 1 < n) out[i + 1] = (float)(mean + stddev * r * sin(two_pi * u2));
     }
+}
+
+void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out) {
+    fill_normal_from(seed, 0, n, mean, stddev, out);
+}
+
+/* Threaded forms of the input generators, equal to the serial ones element
+ * for element: the normal fill split at even indices (each part starts from
+ * the SplitMix64 state of its first pair) and the row quantizer split by rows
+ * (quantize_row_*_ref treats rows independently). */
+typedef struct {
+    int kind; /* 0: fill, 1: quantize rows */
+    uint64_t seed; int64_t i0, i1; float mean, stddev; float *out;
+    int type; const float *src; uint8_t *dst; int64_t n_per_row;
+} gen_job;
+
+static void *gen_worker(void *arg) {
+    gen_job *j = (gen_job *)arg;
+    if (j->kind == 0) {
+        fill_normal_from(j->seed, j->i0, j->i1, j->mean, j->stddev, j->out);
+    } else {
+        const size_t rs = orc_row_size(j->type, j->n_per_row);
+        if (j->i1 > j->i0)
+            orc_quantize_chunk(j->type, j->src + j->i0 * j->n_per_row, j->dst + (size_t)j->i0 * rs, 0, j->i1 - j->i0,
+                               j->n_per_row, NULL);
+    }
+    return NULL;
+}
+
+void orc_fill_normal_mt(uint64_t seed, int64_t n, float mean, float stddev, float *out, int nth) {
+    if (nth < 1) nth = 1;
+    gen_job *js = (gen_job *)calloc((size_t)nth, sizeof(gen_job));
+    const int64_t pairs = (n + 1) / 2, per = (pairs + nth - 1) / nth;
+    for (int i = 0; i < nth; ++i) {
+        const int64_t p0 = per * i < pairs ? per * i : pairs, p1 = per * (i + 1) < pairs ? per * (i + 1) : pairs;
+        js[i].kind = 0; js[i].seed = seed; js[i].i0 = 2 * p0; js[i].i1 = 2 * p1 < n ? 2 * p1 : n;
+        js[i].mean = mean; js[i].stddev = stddev; js[i].out = out;
+    }
+    run_threads(nth, js, sizeof(gen_job), gen_worker);
+    free(js);
+}
+
+void orc_quantize_rows_mt(int type, const float *src, void *dst, int64_t nrows, int64_t n_per_row, int nth) {
+    if (nth < 1) nth = 1;
+    gen_job *js = (gen_job *)calloc((size_t)nth, sizeof(gen_job));
+    const int64_t per = (nrows + nth - 1) / nth;
+    for (int i = 0; i < nth; ++i) {
+        js[i].kind = 1; js[i].type = type; js[i].src = src; js[i].dst = (uint8_t *)dst; js[i].n_per_row = n_per_row;
+        js[i].i0 = per * i < nrows ? per * i : nrows; js[i].i1 = per * (i + 1) < nrows ? per * (i + 1) : nrows;
+    }
+    run_threads(nth, js, sizeof(gen_job), gen_worker);
+    free(js);
+}
+
+/* ------------------------------------------------------------------------ */
+/* The x86 tiled K-quant GEMM: what the reference's CPU mul_mat runs first on
+ * x86 when src1 has at least 8 columns (src/ggml/cpu/mulmat.zig:218-220,
+ * ggml_compute_forward_mul_mat_tiled at src/ggml/cpu/tiled.zig:1262-1268).
+ * Restated from src/ggml/cpu/tiled.zig (unpackers :102-330, src1 staging
+ * :565-594, narrow K extent :697-710, window store :714-737, one chunk
+ * :982-1112, driver :1114-1223) and src/ggml/cpu/tiled_kernel.zig (tiles
+ * :80-117, the AVX2 microtile :505-690 with its column reduction :226-240,
+ * the repacks :721-797), the __AVX2__ arm, for the tiled types this path
+ * serves: Q4_K, Q5_K, Q6_K and IQ4_XS.  Activations are staged to Q8_K with
+ * quantize_row_q8_K_ref, per thread slices, as the reference's driver does. */
+#if ORC_X86
+
+#define TL_K 256      /* TILED_TILE_K */
+#define TL_ROWS 256   /* TILED_TILE_ROWS */
+#define TL_MICRO 16   /* TILED_MICRO */
+#define TL_NBMAX 16   /* NB_MAX */
+
+typedef struct {
+    uint8_t q[TL_ROWS * TL_K];
+    float d[TL_ROWS], dmin[TL_ROWS];
+    int32_t scales[TL_ROWS * TL_NBMAX], mins[TL_ROWS * TL_NBMAX];
+} tl_src0;
+
+typedef struct {
+    int8_t q[TL_ROWS * TL_K];
+    int32_t bsums[(TL_K / 16) * TL_ROWS];
+    float d[TL_ROWS];
+} tl_src1;
+
+typedef struct {
+    tl_src0 src0;
+    tl_src1 src1;
+    float acc[TL_ROWS * TL_ROWS];
+} tl_ws;
+
+/* The per-format constants of ggml_tiled_matmul_type_dispatch
+ * (tiled.zig:786-803): sub-block width, min term, weight bias, act bias. */
+typedef struct { int subblk, has_min, bias, actbias; } tl_fmt;
+
+static int tl_fmt_of(int type, tl_fmt *f) {
+    switch (type) {
+    case ORC_TYPE_Q6_K: *f = (tl_fmt){16, 0, 32, 1}; return 1;
+    case ORC_TYPE_Q5_K: *f = (tl_fmt){32, 1, 0, 0}; return 1;
+    case ORC_TYPE_Q4_K: *f = (tl_fmt){32, 1, 0, 0}; return 1;
+    case ORC_TYPE_IQ4_XS: *f = (tl_fmt){32, 0, 128, 0}; return 1;
+    }
+    return 0;
+}
+
+/* 32 packed bytes to their low and high nibbles (unpkNib4). */
+static void tl_nib4(const uint8_t *src, uint8_t *lo, uint8_t *hi) {
+    for (int l = 0; l < 32; ++l) { lo[l] = src[l] & 0x0F; hi[l] = src[l] >> 4; }
+}
+
+/* ORs the m-bit field at bit s of src[l] into bit d of dst[l] (unpkOr). */
+static void tl_or(int s, int d, int m, uint8_t *dst, const uint8_t *src) {
+    for (int l = 0; l < 32; ++l) dst[l] |= (uint8_t)(((src[l] >> s) & m) << d);
+}
+
+/* One unpacker per format (tiled.zig:102-330): num_k consecutive blocks of
+ * n_rows rows, rows rs blocks apart, into the weight tile. */
+static void tl_unpack_src0(int type, const uint8_t *base, size_t bsize, int64_t rs, int n_rows, tl_src0 *t, int num_k) {
+    const int nb = type == ORC_TYPE_Q6_K ? 16 : 8;
+    const size_t qk_stride = (size_t)num_k * TL_K, nb_stride = (size_t)nb * num_k;
+    for (int slab = 0; slab < num_k; ++slab)
+        for (int r = 0; r < n_rows; ++r) {
+            const size_t d_off = (size_t)slab * TL_MICRO + r;
+            uint8_t *q = t->q + r * qk_stride + (size_t)slab * TL_K;
+            const size_t s_off = r * nb_stride + (size_t)slab * nb;
+            const uint8_t *blk = base + ((size_t)r * rs + slab) * bsize;
+            if (type == ORC_TYPE_Q4_K || type == ORC_TYPE_Q5_K) {
+                const uint16_t d = type == ORC_TYPE_Q4_K ? ((const blk_q4_K *)blk)->d : ((const blk_q5_K *)blk)->d;
+                const uint16_t dm = type == ORC_TYPE_Q4_K ? ((const blk_q4_K *)blk)->dmin : ((const blk_q5_K *)blk)->dmin;
+                const uint8_t *sc = type == ORC_TYPE_Q4_K ? ((const blk_q4_K *)blk)->scales : ((const blk_q5_K *)blk)->scales;
+                const uint8_t *qs = type == ORC_TYPE_Q4_K ? ((const blk_q4_K *)blk)->qs : ((const blk_q5_K *)blk)->qs;
+                t->d[d_off] = F32(d);
+                t->dmin[d_off] = F32(dm);
+                uint32_t utmp[4];
+                unpack_scales_k4(sc, utmp); /* kScaleMins: eight scales then eight mins */
+                const uint8_t *sm = (const uint8_t *)utmp;
+                for (int s = 0; s < 8; ++s) { t->scales[s_off + s] = sm[s]; t->mins[s_off + s] = sm[8 + s]; }
+                for (int c = 0; c < 4; ++c) tl_nib4(qs + 32 * c, q + 64 * c, q + 64 * c + 32);
+                if (type == ORC_TYPE_Q5_K) /* 64-element chunk j takes qh bits 2j and 2j+1 */
+                    for (int b = 0; b < 8; ++b) tl_or(b, 4, 1, q + 32 * b, ((const blk_q5_K *)blk)->qh);
+            } else if (type == ORC_TYPE_Q6_K) {
+                const blk_q6_K *x = (const blk_q6_K *)blk;
+                t->d[d_off] = F32(x->d);
+                for (int h = 0; h < 2; ++h) {
+                    uint8_t *out = q + 128 * h;
+                    const uint8_t *ql = x->ql + 64 * h, *qh = x->qh + 32 * h;
+                    tl_nib4(ql, out, out + 64);
+                    tl_nib4(ql + 32, out + 32, out + 96);
+                    for (int b = 0; b < 4; ++b) tl_or(2 * b, 4, 3, out + 32 * b, qh);
+                }
+                for (int s = 0; s < 16; ++s) t->scales[s_off + s] = x->scales[s];
+            } else { /* IQ4_XS: codes through kvalues_iq4nl + 128, scales ls - 32 */
+                const blk_iq4_xs *x = (const blk_iq4_xs *)blk;
+                t->d[d_off] = F32(x->d);
+                for (int s = 0; s < 8; ++s) {
+                    const int lo = (x->scales_l[s / 2] >> (4 * (s % 2))) & 0xf, hi = (x->scales_h >> (2 * s)) & 3;
+                    t->scales[s_off + s] = (lo | (hi << 4)) - 32;
+                }
+                for (int w = 0; w < 4; ++w) {
+                    uint8_t lo[32], hi[32];
+                    tl_nib4(x->qs + 32 * w, lo, hi);
+                    for (int j = 0; j < 16; ++j) {
+                        q[64 * w + j] = (uint8_t)(KV_IQ4NL[lo[j]] + 128);
+                        q[64 * w + 16 + j] = (uint8_t)(KV_IQ4NL[hi[j]] + 128);
+                        q[64 * w + 32 + j] = (uint8_t)(KV_IQ4NL[lo[16 + j]] + 128);
+                        q[64 * w + 48 + j] = (uint8_t)(KV_IQ4NL[hi[16 + j]] + 128);
+                    }
+                }
+            }
+        }
+}
+
+/* tiled_unpack_src1_q8_K (tiled.zig:565-594): num_k Q8_K blocks of each of
+ * n_rows activation rows from block kblk on; the 16-row band's ragged tail
+ * zeroed. */
+static void tl_unpack_src1(const blk_q8_K *const *rows, int n_rows, tl_src1 *t, int kblk, int num_k) {
+    const int n_padded = (n_rows + TL_MICRO - 1) & ~(TL_MICRO - 1);
+    const int bs_stride = num_k == 1 ? TL_ROWS : TL_MICRO;
+    const int n16 = TL_K / TL_MICRO;
+    for (int slab = 0; slab < num_k; ++slab) {
+        for (int r = 0; r < n_padded; ++r) {
+            int8_t *dst = t->q + (size_t)r * num_k * TL_K + (size_t)slab * TL_K;
+            if (r < n_rows) memcpy(dst, rows[r][kblk + slab].qs, TL_K);
+            else memset(dst, 0, TL_K);
+        }
+        for (int r = 0; r < n_padded; ++r) {
+            const blk_q8_K *x = r < n_rows ? &rows[r][kblk + slab] : NULL;
+            for (int s = 0; s < n16; ++s) t->bsums[(slab * n16 + s) * bs_stride + r] = x ? x->bsums[s] : 0;
+            t->d[slab * TL_MICRO + r] = x ? x->d : 0.0f;
+        }
+    }
+}
+
+/* tiled_repack_src1, __AVX2__ arm (tiled_kernel.zig:738-751): with the act
+ * bias, each code of the 16-row band as q + 128 (sign bit flipped). */
+static void tl_repack_src1(tl_src1 *t, int row0, int num_k, int bias) {
+    if (!bias) return;
+    const size_t row_stride = (size_t)num_k * TL_K;
+    uint8_t *base = (uint8_t *)t->q + (size_t)row0 * row_stride;
+    for (int r = 0; r < TL_MICRO; ++r)
+        for (size_t o = 0; o < row_stride; ++o) base[r * row_stride + o] ^= 0x80;
+}
+
+/* tiled_repack_src0 (tiled_kernel.zig:773-797): for the act-bias formats,
+ * each row's correction 128 * sum_s scales[s] * (sum of the sub-block's
+ * debiased weights), kept in mins[r][0] (wrapping i32 arithmetic). */
+static void tl_repack_src0(const tl_fmt *f, tl_src0 *t, int n_rows, int num_k) {
+    if (!f->actbias) return;
+    const int nb = TL_K / f->subblk;
+    const size_t nb_stride = (size_t)nb * num_k;
+    for (int slab = 0; slab < num_k; ++slab)
+        for (int r = 0; r < n_rows; ++r) {
+            const uint8_t *q = t->q + (size_t)r * num_k * TL_K + (size_t)slab * TL_K;
+            const int32_t *sc = t->scales + r * nb_stride + (size_t)slab * nb;
+            uint32_t corr = 0;
+            for (int s = 0; s < nb; ++s) {
+                int32_t qsum = 0;
+                for (int k = 0; k < f->subblk; ++k) qsum += q[s * f->subblk + k];
+                corr += 128u * (uint32_t)sc[s] * (uint32_t)(qsum - f->subblk * f->bias);
+            }
+            t->mins[r * nb_stride + (size_t)slab * nb] = (int32_t)corr;
+        }
+}
+
+/* The column reduction the AVX2 microtile ends each group on
+ * (tiled_kernel.zig:226-240): lane t = wrapping sum of acc[t]'s lanes. */
+AVX2_FN static inline __m256i tl_column_sums(const __m256i acc[8]) {
+    const __m256i ab = _mm256_hadd_epi32(acc[0], acc[1]), cd = _mm256_hadd_epi32(acc[2], acc[3]);
+    const __m256i ef = _mm256_hadd_epi32(acc[4], acc[5]), gh = _mm256_hadd_epi32(acc[6], acc[7]);
+    const __m256i abcd = _mm256_hadd_epi32(ab, cd), efgh = _mm256_hadd_epi32(ef, gh);
+    const __m256i lo = _mm256_permute2x128_si256(abcd, efgh, 0x20), hi = _mm256_permute2x128_si256(abcd, efgh, 0x31);
+    return _mm256_add_epi32(lo, hi);
+}
+
+/* tiled_run_microtile_avx2 (tiled_kernel.zig:505-690): the 16 x 16
+ * microtile at (ri0, j0) over slab `slab` of a num_k-slab tile, added into
+ * buf (row-major, buf_stride floats per row).  Per row, 8-column groups:
+ * maddubs + madd against the broadcast sub-block scale; the min term from the
+ * Q8_K bsums; then d * s1 (- dmin * s2 fused) and buf += res * d8 fused. */
+AVX2_FN static void tl_microtile(const tl_fmt *f, const tl_src0 *s0, const tl_src1 *s1, int ri0, int j0, int num_k,
+                                 int slab, float *buf, int buf_stride) {
+    const int NB = TL_K / f->subblk;
+    const size_t qk_stride = (size_t)num_k * TL_K, qk_off = (size_t)slab * TL_K;
+    const size_t nb_stride = (size_t)NB * num_k, nb_off = (size_t)slab * NB;
+    const size_t bs_stride = num_k == 1 ? TL_ROWS : TL_MICRO, bs_off = (size_t)slab * TL_MICRO;
+    const __m256i bias8 = _mm256_set1_epi8((char)(uint8_t)f->bias);
+    for (int i = 0; i < TL_MICRO; ++i) {
+        const int ar = ri0 + i;
+        const size_t d_off = (size_t)slab * TL_MICRO + ar;
+        const float d0 = s0->d[d_off], dmin0 = s0->dmin[d_off];
+        const uint8_t *q0 = s0->q + ar * qk_stride + qk_off;
+        const int32_t *scales_row = s0->scales + ar * nb_stride + nb_off;
+        const int32_t *mins_row = s0->mins + ar * nb_stride + nb_off;
+        for (int g = 0; g < TL_MICRO; g += 8) {
+            const int8_t *q1p[8];
+            for (int t = 0; t < 8; ++t) q1p[t] = s1->q + (size_t)(j0 + g + t) * qk_stride + qk_off;
+            __m256i s2 = _mm256_setzero_si256();
+            __m256i acc[8];
+            for (int t = 0; t < 8; ++t) acc[t] = _mm256_setzero_si256();
+            if (f->subblk == 32) {
+                for (int s = 0; s < NB; ++s) {
+                    const __m256i q0v = _mm256_loadu_si256((const __m256i *)(q0 + s * 32));
+                    const __m256i sc16 = _mm256_set1_epi16((short)scales_row[s]);
+                    if (f->bias) { /* IQ4_XS: the sign trick on the debiased levels */
+                        const __m256i w = _mm256_sub_epi8(q0v, bias8);
+                        const __m256i ax = _mm256_sign_epi8(w, w);
+                        for (int t = 0; t < 8; ++t) {
+                            const __m256i q1 = _mm256_loadu_si256((const __m256i *)(q1p[t] + s * 32));
+                            acc[t] = _mm256_add_epi32(acc[t],
+                                                      _mm256_madd_epi16(sc16, _mm256_maddubs_epi16(ax, _mm256_sign_epi8(q1, w))));
+                        }
+                    } else {
+                        for (int t = 0; t < 8; ++t) {
+                            const __m256i q1 = _mm256_loadu_si256((const __m256i *)(q1p[t] + s * 32));
+                            acc[t] = _mm256_add_epi32(acc[t], _mm256_madd_epi16(sc16, _mm256_maddubs_epi16(q0v, q1)));
+                        }
+                    }
+                    if (f->has_min) {
+                        const __m256i b0 = _mm256_loadu_si256((const __m256i *)(s1->bsums + (bs_off + 2 * s) * bs_stride + j0 + g));
+                        const __m256i b1 = _mm256_loadu_si256((const __m256i *)(s1->bsums + (bs_off + 2 * s + 1) * bs_stride + j0 + g));
+                        s2 = _mm256_add_epi32(s2, _mm256_mullo_epi32(_mm256_add_epi32(b0, b1), _mm256_set1_epi32(mins_row[s])));
+                    }
+                }
+            } else { /* 16-wide sub-blocks (Q6_K): two per 32-byte load, scale per 128-bit half */
+                for (int sp = 0; sp < NB; sp += 2) {
+                    const __m256i q0v = _mm256_loadu_si256((const __m256i *)(q0 + sp * 16));
+                    const __m256i scv = _mm256_set_m128i(_mm_set1_epi16((short)scales_row[sp + 1]),
+                                                         _mm_set1_epi16((short)scales_row[sp]));
+                    const __m256i w = _mm256_sub_epi8(q0v, bias8); /* debiased weight; act pre-biased by 128 */
+                    for (int t = 0; t < 8; ++t) {
+                        const __m256i q1b = _mm256_loadu_si256((const __m256i *)(q1p[t] + sp * 16));
+                        acc[t] = _mm256_add_epi32(acc[t], _mm256_madd_epi16(scv, _mm256_maddubs_epi16(q1b, w)));
+                    }
+                }
+            }
+            __m256i s1v = tl_column_sums(acc);
+            if (f->bias && f->actbias) s1v = _mm256_sub_epi32(s1v, _mm256_set1_epi32(mins_row[0]));
+            const __m256 d1 = _mm256_loadu_ps(s1->d + (size_t)slab * TL_MICRO + j0 + g);
+            __m256 res = _mm256_mul_ps(_mm256_set1_ps(d0), _mm256_cvtepi32_ps(s1v));
+            if (f->has_min) res = _mm256_fnmadd_ps(_mm256_set1_ps(dmin0), _mm256_cvtepi32_ps(s2), res);
+            float *bp = buf + (size_t)ar * buf_stride + j0 + g;
+            _mm256_storeu_ps(bp, _mm256_fmadd_ps(res, d1, _mm256_loadu_ps(bp)));
+        }
+    }
+}
+
+/* ggml_tiled_narrow_k_extent (tiled.zig:697-710). */
+static int tl_narrow_k_extent(int64_t n_rows, int64_t ne00) {
+    const int l1 = 31 * 1024;
+    int rows = (int)n_rows < TL_MICRO ? TL_MICRO : (int)n_rows;
+    int ke = l1 / (TL_MICRO + rows);
+    ke &= ~(TL_K - 1);
+    const int ke_max = TL_ROWS * TL_K / TL_MICRO;
+    if (ke > ke_max) ke = ke_max;
+    while (ke >= TL_K && ne00 % ke != 0) ke -= TL_K;
+    return ke < TL_K ? 0 : ke;
+}
+
+/* tiled_store_window (tiled.zig:714-737): the window back out, column-major. */
+static void tl_store_window(const float *buf, int n0, int n1, int bs, float *dst, size_t dst_stride) {
+    for (int ri = 0; ri < n0; ++ri)
+        for (int j = 0; j < n1; ++j) dst[ri + j * dst_stride] = buf[(size_t)ri * bs + j];
+}
+
+typedef struct {
+    int type, nth;
+    tl_fmt f;
+    const uint8_t *w;
+    int64_t nrows, K, ncols;
+    const float *x;
+    float *dst;
+    uint8_t *wdata; /* Q8_K rows of x */
+    size_t wrow;
+    tl_ws *ws;      /* one per thread */
+    atomic_long current_chunk;
+    int64_t nchunk0, nchunk1, dr0, dr1;
+} tl_ctx;
+
+typedef struct { tl_ctx *ctx; int ith; } tl_thread;
+
+/* ggml_compute_forward_mul_mat_tiled_one_chunk (tiled.zig:982-1112), one
+ * batch: 256 x 256 windows, the narrow path for windows of at most 16
+ * columns, the standard per-slab path otherwise. */
+AVX2_FN static void tl_one_chunk(tl_ctx *c, tl_ws *ws, int64_t ir0_start, int64_t ir0_end, int64_t ir1_start,
+                                 int64_t ir1_end) {
+    if (ir0_start >= ir0_end || ir1_start >= ir1_end) return;
+    const size_t bsize = orc_type_size(c->type), rs_bytes = orc_row_size(c->type, c->K);
+    const int64_t src0_stride = (int64_t)(rs_bytes / bsize);
+    const blk_q8_K *rows[TL_ROWS];
+    for (int64_t iir1 = ir1_start; iir1 < ir1_end;) {
+        const int64_t iir1_end = iir1 + TL_ROWS < ir1_end ? iir1 + TL_ROWS : ir1_end;
+        const int n_src1 = (int)(iir1_end - iir1);
+        for (int r = 0; r < n_src1; ++r) rows[r] = (const blk_q8_K *)(c->wdata + (size_t)(iir1 + r) * c->wrow);
+        for (int64_t iir0 = ir0_start; iir0 < ir0_end; iir0 += TL_ROWS) {
+            const int64_t iir0_end = iir0 + TL_ROWS < ir0_end ? iir0 + TL_ROWS : ir0_end;
+            const int n_src0 = (int)(iir0_end - iir0);
+            memset(ws->acc, 0, sizeof ws->acc);
+            if (n_src1 <= TL_MICRO) {
+                const int k_extent = tl_narrow_k_extent(n_src1, c->K);
+                const int num_k = k_extent / TL_K;
+                for (int64_t k0 = 0; k0 < c->K; k0 += k_extent) {
+                    const int kstart = (int)(k0 / TL_K);
+                    tl_unpack_src1(rows, n_src1, &ws->src1, kstart, num_k);
+                    tl_repack_src1(&ws->src1, 0, num_k, c->f.actbias);
+                    for (int64_t ir0 = iir0; ir0 < iir0_end; ir0 += TL_MICRO) {
+                        const int n0 = (int)(iir0_end - ir0 < TL_MICRO ? iir0_end - ir0 : TL_MICRO);
+                        tl_unpack_src0(c->type, c->w + (size_t)ir0 * rs_bytes + (size_t)kstart * bsize, bsize,
+                                       src0_stride, n0, &ws->src0, num_k);
+                        tl_repack_src0(&c->f, &ws->src0, n0, num_k);
+                        float *buf = ws->acc + (size_t)(ir0 - iir0) * TL_ROWS;
+                        for (int slab = 0; slab < num_k; ++slab)
+                            tl_microtile(&c->f, &ws->src0, &ws->src1, 0, 0, num_k, slab, buf, TL_ROWS);
+                    }
+                }
+            } else {
+                for (int64_t ib = 0; ib < c->K; ib += TL_K) {
+                    const int kblk = (int)(ib / TL_K);
+                    tl_unpack_src0(c->type, c->w + (size_t)iir0 * rs_bytes + (size_t)kblk * bsize, bsize, src0_stride,
+                                   n_src0, &ws->src0, 1);
+                    tl_repack_src0(&c->f, &ws->src0, n_src0, 1);
+                    tl_unpack_src1(rows, n_src1, &ws->src1, kblk, 1);
+                    for (int64_t ir1 = iir1; ir1 < iir1_end; ir1 += TL_MICRO) {
+                        tl_repack_src1(&ws->src1, (int)(ir1 - iir1), 1, c->f.actbias);
+                        for (int64_t ir0 = iir0; ir0 < iir0_end; ir0 += TL_MICRO)
+                            tl_microtile(&c->f, &ws->src0, &ws->src1, (int)(ir0 - iir0), (int)(ir1 - iir1), 1, 0,
+                                         ws->acc, TL_ROWS);
+                    }
+                }
+            }
+            tl_store_window(ws->acc, n_src0, n_src1, TL_ROWS, c->dst + iir0 + iir1 * c->nrows, (size_t)c->nrows);
+        }
+        iir1 = iir1_end;
+    }
+}
+
+static void *tl_stage_worker(void *arg) {
+    tl_thread *t = (tl_thread *)arg;
+    tl_ctx *c = t->ctx;
+    const int64_t nbk = c->K / QK_K;
+    const int64_t b0 = (int64_t)t->ith * nbk / c->nth, b1 = ((int64_t)t->ith + 1) * nbk / c->nth;
+    for (int64_t j = 0; j < c->ncols; ++j)
+        orc_quantize_row_q8_K_ref(c->x + j * c->K + b0 * QK_K, c->wdata + (size_t)j * c->wrow + (size_t)b0 * sizeof(blk_q8_K),
+                                  (b1 - b0) * QK_K);
+    return NULL;
+}
+
+static void *tl_compute_worker(void *arg) {
+    tl_thread *t = (tl_thread *)arg;
+    tl_ctx *c = t->ctx;
+    long chunk = t->ith;
+    while (chunk < c->nchunk0 * c->nchunk1) {
+        const int64_t i0 = chunk % c->nchunk0, i1 = chunk / c->nchunk0;
+        const int64_t r0 = c->dr0 * i0, r1 = c->dr1 * i1;
+        tl_one_chunk(c, &c->ws[t->ith], r0, r0 + c->dr0 < c->nrows ? r0 + c->dr0 : c->nrows, r1,
+                     r1 + c->dr1 < c->ncols ? r1 + c->dr1 : c->ncols);
+        if (c->nth >= c->nchunk0 * c->nchunk1) break;
+        chunk = atomic_fetch_add(&c->current_chunk, 1);
+    }
+    return NULL;
+}
+#endif /* ORC_X86 */
+
+int orc_mul_mat_tiled(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols, float *dst,
+                      int nth) {
+#if ORC_X86
+    tl_fmt f;
+    if (!orc_has_avx2() || !tl_fmt_of(type, &f) || K % QK_K != 0 || nrows <= 0 || ncols <= 0) return 0;
+    if (nth < 1) nth = 1;
+    tl_ctx c;
+    memset(&c, 0, sizeof c);
+    c.type = type; c.nth = nth; c.f = f; c.w = (const uint8_t *)w;
+    c.nrows = nrows; c.K = K; c.ncols = ncols; c.x = x; c.dst = dst;
+    c.wrow = (size_t)(K / QK_K) * sizeof(blk_q8_K);
+    c.wdata = (uint8_t *)malloc(c.wrow * (size_t)ncols);
+    c.ws = (tl_ws *)aligned_alloc(64, sizeof(tl_ws) * (size_t)nth);
+    memset(c.ws, 0, sizeof(tl_ws) * (size_t)nth);
+    tl_thread *ts = (tl_thread *)malloc(sizeof(tl_thread) * (size_t)nth);
+    for (int i = 0; i < nth; ++i) { ts[i].ctx = &c; ts[i].ith = i; }
+    run_threads(nth, ts, sizeof(tl_thread), tl_stage_worker);
+    /* chunking of mulMatDriver (tiled.zig:1175-1195): 256 halved until four
+     * chunks per thread, not below the 16-row microtile */
+    int64_t chunk = 256;
+    int64_t n0 = (nrows + chunk - 1) / chunk, n1 = (ncols + chunk - 1) / chunk;
+    while (n0 * n1 < (int64_t)nth * 4 && chunk > 16) {
+        chunk /= 2;
+        n0 = (nrows + chunk - 1) / chunk;
+        n1 = (ncols + chunk - 1) / chunk;
+    }
+    c.nchunk0 = n0; c.nchunk1 = n1;
+    c.dr0 = (nrows + n0 - 1) / n0; c.dr1 = (ncols + n1 - 1) / n1;
+    atomic_store(&c.current_chunk, nth);
+    run_threads(nth, ts, sizeof(tl_thread), tl_compute_worker);
+    free(ts);
+    free(c.ws);
+    free(c.wdata);
+    return 1;
+#else
+    (void)type; (void)w; (void)nrows; (void)K; (void)x; (void)ncols; (void)dst; (void)nth;
+    return 0;
+#endif
 }

@@ -98,6 +98,13 @@ void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nro
                     int64_t K, const float *x, int64_t ne11, int64_t n_tokens,
                     const int32_t *ids, int64_t n_ids, float *dst, int nth);
 
+/* The reference's x86 tiled K-quant GEMM (the CPU mul_mat for src1 with 8 or
+ * more columns on AVX2 hosts, src/ggml/cpu/tiled.zig:1262-1268), for Q4_K,
+ * Q5_K, Q6_K and IQ4_XS; same layouts as orc_mul_mat.  Returns 0 (and writes
+ * nothing) when the type is not tiled or the host lacks AVX2. */
+int orc_mul_mat_tiled(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols, float *dst,
+                      int nth);
+
 /* GLU ops (ggml_glu_op: positions in GGML_GLU_OP_NAME, src/ggml/types.zig:103-106) */
 #define ORC_GLU_REGLU 0
 #define ORC_GLU_GEGLU 1
@@ -115,6 +122,10 @@ void orc_glu_f32(int op, int64_t n, const float *gate, const float *up, float al
 
 /* synthetic inputs: SplitMix64 -> Box-Muller (double) -> f32 */
 void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out);
+/* the same values from nth threads */
+void orc_fill_normal_mt(uint64_t seed, int64_t n, float mean, float stddev, float *out, int nth);
+/* nrows rows of quantize_row_<type>_ref (orc_quantize_chunk, no imatrix) from nth threads */
+void orc_quantize_rows_mt(int type, const float *src, void *dst, int64_t nrows, int64_t n_per_row, int nth);
 
 int orc_has_avx2(void);
 

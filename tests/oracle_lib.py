@@ -4,6 +4,7 @@ Test infrastructure: imported by tests/, __graft_entry__.smoke() and bench.py's
 cpu_baseline leg only.
 """
 import ctypes
+import os
 import pathlib
 import subprocess
 
@@ -62,11 +63,17 @@ def lib():
         L.orc_mul_mat_q8_1_f64.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, vp]
         L.orc_mul_mat.restype = None
         L.orc_mul_mat.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
+        L.orc_mul_mat_tiled.restype = ctypes.c_int
+        L.orc_mul_mat_tiled.argtypes = [ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
         L.orc_mul_mat_id.restype = None
         L.orc_mul_mat_id.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, i64, f32p, i64, i64, vp, i64,
                                      f32p, ctypes.c_int]
         L.orc_fill_normal.restype = None
         L.orc_fill_normal.argtypes = [ctypes.c_uint64, i64, ctypes.c_float, ctypes.c_float, f32p]
+        L.orc_fill_normal_mt.restype = None
+        L.orc_fill_normal_mt.argtypes = [ctypes.c_uint64, i64, ctypes.c_float, ctypes.c_float, f32p, ctypes.c_int]
+        L.orc_quantize_rows_mt.restype = None
+        L.orc_quantize_rows_mt.argtypes = [ctypes.c_int, vp, vp, i64, i64, ctypes.c_int]
         L.orc_fnv1a.restype = ctypes.c_uint64
         L.orc_fnv1a.argtypes = [vp, ctypes.c_size_t]
         L.orc_has_avx2.restype = ctypes.c_int
@@ -100,10 +107,26 @@ def quantize_ref(t, x):
     return out
 
 
-def quantize_rows(t, w):
-    """Quantize a [nrows, K] f32 matrix row by row (quantize_row_*_ref)."""
+def gen_threads():
+    """Threads for the input generators: the CPUs this process may use, at
+    most 16 (a GPU box's CPU share)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
+
+
+def quantize_rows(t, w, nth=None):
+    """Quantize a [nrows, K] f32 matrix row by row (quantize_row_*_ref); rows
+    are independent, so threads split them (same bytes as one thread)."""
     w = np.ascontiguousarray(w, dtype=np.float32)
-    return quantize_ref(t, w.reshape(-1)).reshape(w.shape[0], -1)
+    nrows, k = w.shape
+    if t in (TYPE_Q8_1, TYPE_Q8_K):
+        return quantize_ref(t, w.reshape(-1)).reshape(nrows, -1)
+    out = np.zeros((nrows, row_bytes(t, k)), dtype=np.uint8)
+    lib().orc_quantize_rows_mt(t, _p(w), _p(out), nrows, k, gen_threads() if nth is None else nth)
+    return out
 
 
 def dequantize(t, q, k):
@@ -148,6 +171,17 @@ def mul_mat(t, wq, nrows, K, x, nth=4, impl=IMPL_GENERIC):
     return out
 
 
+def mul_mat_tiled(t, wq, nrows, K, x, nth=4):
+    """The reference's x86 tiled GEMM (AVX2 arm) for Q4_K / Q5_K / Q6_K /
+    IQ4_XS: x [ncols, K] f32 -> [ncols, nrows] f32, or None where the host
+    lacks AVX2 or the type is not tiled."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ncols = x.shape[0]
+    out = np.full((ncols, nrows), np.nan, dtype=np.float32)
+    ok = lib().orc_mul_mat_tiled(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(x), ncols, _p(out), nth)
+    return out if ok else None
+
+
 def mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=4, impl=IMPL_GENERIC):
     """x: [n_tokens, ne11, K]; ids: [n_tokens, n_ids] int32 -> [n_tokens, n_ids, nrows]."""
     x = np.ascontiguousarray(x, dtype=np.float32)
@@ -177,9 +211,15 @@ def glu(op, gate, up, alpha=0.0, limit=0.0):
     return out
 
 
-def fill_normal(seed, n, mean=0.0, std=1.0):
+def fill_normal(seed, n, mean=0.0, std=1.0, nth=None):
+    """SplitMix64 -> Box-Muller normals; threads split the array at even
+    indices (same values as one thread)."""
     out = np.zeros(n, dtype=np.float32)
-    lib().orc_fill_normal(seed, n, mean, std, _p(out))
+    nth = (gen_threads() if n >= (1 << 20) else 1) if nth is None else nth
+    if nth == 1:
+        lib().orc_fill_normal(seed, n, mean, std, _p(out))
+    else:
+        lib().orc_fill_normal_mt(seed, n, mean, std, _p(out), nth)
     return out
 
 

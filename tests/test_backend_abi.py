@@ -218,3 +218,46 @@ def test_fused_and_elementwise_entry_points_reject_bad_arguments(L):
     assert L.hip_qmm_glu_f32(2, 0.0, 0.0, 0, 2, x, 8, x, 8, d, 8, None) == 0   # nothing to do
     assert L.hip_qmm_add_f32(8, 2, x, 8, x, 8, None, 8, None) == 1
     assert L.hip_qmm_add_f32(8, 0, x, 8, x, 8, d, 8, None) == 0
+
+
+def test_fusion_off_narrows_supports_op_to_mul_mat():
+    """With GGML_HIP_DISABLE_FUSION=1 the device keeps only MUL_MAT /
+    MUL_MAT_ID and the no-op views: GLU and ADD go back to the CPU, which is
+    the strict boundary of the quantized-matmul path.  Runs in a fresh
+    process, since the library reads the variable once."""
+    import os
+    import subprocess
+    import sys
+    code = r'''
+import ctypes as C, sys
+sys.path.insert(0, sys.argv[1]); sys.path.insert(0, sys.argv[2])
+import ggml_hip.backend as B
+from ggml_hip import abi
+import test_backend_abi as T
+L = B.lib()
+ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))
+g = abi.make_tensor(abi.GGML_TYPE_F32, [64, 1]); u = abi.make_tensor(abi.GGML_TYPE_F32, [64, 1])
+assert not ok(abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g, u, [64, 1]))
+assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [64, 1], op=abi.GGML_OP_ADD, srcs=(g, u)))
+assert ok(T.mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 1)[2])
+assert ok(T.mmid(abi.GGML_TYPE_Q6_K, 2048, 768, 128, 8, 512)[3])
+assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=abi.GGML_OP_VIEW))
+print("strict ok")
+'''
+    env = dict(os.environ, GGML_HIP_DISABLE_FUSION="1")
+    r = subprocess.run([sys.executable, "-c", code, str(ROOT / "llama.zig_amd"), str(ROOT / "tests")], env=env,
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and "strict ok" in r.stdout, r.stderr[-2000:]
+
+
+def test_mul_mat_rejects_overlapping_columns_before_any_launch(L):
+    """hip_qmm_mul_mat refuses column strides below the column length with
+    hipErrorInvalidValue before it touches memory (placeholder pointers)."""
+    import ctypes as C
+    vp, i64 = C.c_void_p, C.c_int64
+    L.hip_qmm_mul_mat.restype = C.c_int
+    L.hip_qmm_mul_mat.argtypes = [C.c_int, vp, i64, i64, i64, vp, i64, i64, vp, i64, vp, C.c_size_t, vp]
+    w, x, d, ws = 0x100000, 0x200000, 0x300000, 0x400000  # aligned placeholders, never dereferenced
+    for ncols in (2, 3, 8, 64):
+        assert L.hip_qmm_mul_mat(12, w, 4096, 1024, 16 * 144, x, ncols, 4096, d, 1023, ws, 1 << 30, None) == 1
+        assert L.hip_qmm_mul_mat(12, w, 4096, 1024, 16 * 144, x, ncols, 4064, d, 1024, ws, 1 << 30, None) == 1

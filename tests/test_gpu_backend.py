@@ -141,3 +141,16 @@ def test_graph_rejects_unsupported_node(hb):
     glu = abi.make_glu(abi.GGML_GLU_OP_GEGLU_ERF, a, a, [64, 4])
     hb.alloc([glu])
     assert hb.compute([glu]) == abi.GGML_STATUS_FAILED
+
+
+def test_alloc_buffer_out_of_memory_returns_null(hb):
+    """alloc_buffer answers NULL when hipMalloc fails (cuda/backend.zig:294-303),
+    forced from the host with a size no device holds, and clears the error:
+    the next allocation and a MUL_MAT on it succeed."""
+    from ggml_hip import abi
+    assert not hb.buft.iface.alloc_buffer(hb.buft_ptr, 1 << 52)  # 4 PiB
+    K, M = 1024, 256
+    wq = weights_q(O.TYPE_Q4_K, M, K)
+    x = np.array(acts(2, K))
+    got = _mul_mat_graph(hb, abi.GGML_TYPE_Q4_K, wq, K, M, x)
+    assert nmse(got[0], O.mul_mat(O.TYPE_Q4_K, wq, M, K, x, nth=8)) < NMSE_GATE

@@ -1,0 +1,170 @@
+"""Parity at every cell of the benchmark configurations, through the op-level
+entry points (hip_qmm_mul_mat / hip_qmm_mul_mat_id), so that each cell runs
+the kernel the shape-based dispatch picks for it.
+
+Configurations (weights f32 N(0, 0.02) from seed 42 quantized with
+quantize_row_*_ref, activations f32 N(0, 1) from seed 43, router logits from
+seed 44):
+  0  Q4_K 4096x4096, one column (the CPU-runnable case);
+  1  Llama-3-8B decode GEMVs at 1, 2, 4 and 8 columns: Q4_K attn_q/o
+     4096x4096, Q4_K attn_k 1024x4096, Q6_K attn_v 1024x4096, Q4_K
+     ffn_gate/up 14336x4096, Q6_K ffn_down 4096x14336;
+  2  Q4_K 14336x4096 at T = 128, 512, 2048 (MMQ);
+  3  Q8_0 / Q6_K / Q4_K at 4096x4096 and 4096x14336, T = 1, 32, 512;
+  4  Qwen3-30B-A3B MoE: 128 experts, Q4_K gate/up 768x2048 (one activation
+     row per token) and down 2048x768 (one row per slot), 512 tokens top-8.
+
+Gates, per cell:
+  - NMSE < 5e-4 against the CPU ggml path (the restated
+    ggml_compute_forward_mul_mat / _mul_mat_id with Q8_K / Q8_0 activations,
+    src/ggml/cpu/mulmat.zig:205-423, 555-777; the measure of
+    harness/blas_diff.c:341-350);
+  - within 2e-6 (error / max |out|) of the f64 evaluation of the Q8_1 formula
+    on activations quantized by the oracle's quantize_row_q8_1_ref, which
+    catches scale, index and min-term slips that NMSE would hide;
+  - every output finite.
+Large cells are checked on row (or token) subsets: three contiguous segments
+(first, middle, last rows, which cross tile and workgroup edges) plus seeded
+random rows, sized so each CPU check takes about a second.
+
+The maximum relative error against the CPU path (|err| / max(|want|, 1e-3 x
+max |want|)) and the largest error over the output scale are computed per
+cell and, with NMSE and the f64 agreement, written as JSON to the file named
+by the QMM_PARITY_RECORD environment variable when it is set.  For the
+K-quants the CPU path quantizes activations to Q8_K (one scale per 256) where
+the GPU path uses Q8_1 (one per 32), so outputs that cancel to near zero
+differ by several times their own size there while NMSE stays near 6e-5.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+from cases import acts, max_err_scaled, max_rel, nmse, route_top_k, weights_f32, weights_q
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+NMSE_GATE = 5e-4   # test-backend-ops' gate for mul_mat
+F64_TOL = 2e-6     # fp32 epilogue vs exact f64 of the same Q8_1 formula, / max|out|
+CHECK_MACS = 6e8   # CPU budget per cell: rows * K * T of the f64 check
+
+TYPES = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0}
+
+
+def _dense_cells():
+    cells = {}
+
+    def add(cfg, label, tname, nrows, K, T):
+        cells.setdefault((tname, nrows, K, T), []).append(f"config {cfg} {label}")
+
+    add(0, "single mul_mat", "Q4_K", 4096, 4096, 1)
+    for T in (1, 2, 4, 8):
+        add(1, "attn_q/attn_output", "Q4_K", 4096, 4096, T)
+        add(1, "attn_k", "Q4_K", 1024, 4096, T)
+        add(1, "attn_v", "Q6_K", 1024, 4096, T)
+        add(1, "ffn_gate/ffn_up", "Q4_K", 14336, 4096, T)
+        add(1, "ffn_down", "Q6_K", 4096, 14336, T)
+    for T in (128, 512, 2048):
+        add(2, "MMQ", "Q4_K", 14336, 4096, T)
+    for tname in ("Q8_0", "Q6_K", "Q4_K"):
+        for K in (4096, 14336):
+            for T in (1, 32, 512):
+                add(3, "cross-quant", tname, 4096, K, T)
+    # grouped by weight so each matrix is quantized and uploaded once
+    return sorted(cells.items(), key=lambda kv: (kv[0][0], kv[0][1], kv[0][2], kv[0][3]))
+
+
+DENSE = _dense_cells()
+_RECORD = []
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _parity_record():
+    yield
+    path = os.environ.get("QMM_PARITY_RECORD")
+    if path and _RECORD:
+        os.makedirs(os.path.dirname(os.path.abspath(path)), exist_ok=True)
+        with open(path, "w") as f:
+            json.dump({"gates": {"nmse_vs_cpu": NMSE_GATE, "f64_max_err_scaled": F64_TOL}, "cells": _RECORD}, f,
+                      indent=1)
+
+
+def _check_rows(nrows, K, T):
+    """Rows the CPU checks: all of them when small, else segments + random."""
+    n = int(max(48, min(nrows, CHECK_MACS // (K * T))))
+    if n >= nrows:
+        return np.arange(nrows)
+    seg = max(16, n // 4)
+    mid = nrows // 2 - seg // 2
+    fixed = np.r_[0:seg, mid:mid + seg, nrows - seg:nrows]
+    rest = np.setdiff1d(np.arange(nrows), fixed)
+    rnd = np.random.default_rng(nrows * 7 + K + T).choice(rest, size=max(0, n - fixed.size), replace=False)
+    return np.sort(np.r_[fixed, rnd])
+
+
+def _q8_1_cols(x, K):
+    """quantize_row_q8_1_ref of each column: K / 32 blocks per column, the
+    layout the f64 evaluation reads."""
+    return O.quantize_rows(O.TYPE_Q8_1, np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K))
+
+
+@pytest.mark.parametrize("cell", DENSE, ids=[f"{c[0][0]}-{c[0][1]}x{c[0][2]}-T{c[0][3]}" for c in DENSE])
+def test_config_cell(cell):
+    import ggml_hip as G
+    (tname, nrows, K, T), labels = cell
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(T, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    out = torch.full((T, nrows), float("nan"), device="cuda")
+    got = G.mul_mat(tname, w_d, x_d, out=out).cpu().numpy()
+    assert np.all(np.isfinite(got)), "non-finite or unwritten outputs"
+    rows = _check_rows(nrows, K, T)
+    sub = got[:, rows]
+    ideal = O.mul_mat_q8_1_f64(t, wq[rows], len(rows), K, _q8_1_cols(x, K), T)
+    f64_err = max_err_scaled(sub, ideal)
+    cpu = O.mul_mat(t, wq[rows], len(rows), K, x, nth=O.gen_threads())
+    e, mr = nmse(sub, cpu), max_rel(sub, cpu)
+    _RECORD.append({"cell": f"{tname} {nrows}x{K} T={T}", "configs": labels, "entry": "hip_qmm_mul_mat",
+                    "rows_checked": int(len(rows)), "nmse_vs_cpu": e, "max_rel_vs_cpu": mr,
+                    "max_err_over_max_vs_cpu": max_err_scaled(sub, cpu), "f64_max_err_scaled": f64_err})
+    assert f64_err < F64_TOL, f"f64 agreement {f64_err:.3g}"
+    assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {mr:.3g}"
+
+
+@pytest.mark.parametrize("proj", ["gate_up", "down"])
+def test_config4_moe_cell(proj):
+    """Config 4 through hip_qmm_mul_mat_id at full size (512 tokens, top-8 of
+    128 experts); gate/up reads one activation row per token, down one row
+    per (token, slot).  Checked on every 8th token."""
+    import ggml_hip as G
+    n_as, n_tokens, k = 128, 512, 8
+    nrows, K, ne11 = (768, 2048, 1) if proj == "gate_up" else (2048, 768, k)
+    ids, _ = route_top_k(n_tokens, n_as, k)
+    t = O.TYPE_Q4_K
+    wq = O.quantize_rows(t, weights_f32(n_as * nrows, K, 1 if proj == "down" else 0)).reshape(n_as, nrows, -1)
+    x = np.array(acts(n_tokens * ne11, K, 1 if proj == "down" else 0)).reshape(n_tokens, ne11, K)
+    out = torch.full((n_tokens, k, nrows), float("nan"), device="cuda")
+    got = G.mul_mat_id("Q4_K", torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda(),
+                       out=out).cpu().numpy()
+    assert np.all(np.isfinite(got)), "non-finite or unwritten outputs"
+    sub = np.arange(0, n_tokens, 8)
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x[sub], ids[sub], nth=O.gen_threads())
+    ys = _q8_1_cols(x[sub].reshape(-1, K), K)
+    ideal = np.zeros((len(sub), k, nrows))
+    for e_ in np.unique(ids[sub]):
+        ts, ss = np.nonzero(ids[sub] == e_)
+        cols = ys[ts * ne11 + ss % ne11]
+        ideal[ts, ss] = O.mul_mat_q8_1_f64(t, wq[e_], nrows, K, cols, len(ts))
+    f64_err = max_err_scaled(got[sub], ideal)
+    e, mr = nmse(got[sub], cpu), max_rel(got[sub], cpu)
+    _RECORD.append({"cell": f"MoE Q4_K 128 x {nrows}x{K}, 512 tokens top-8, ne11={ne11}", "configs":
+                    [f"config 4 {proj.replace('_', '/')}"], "entry": "hip_qmm_mul_mat_id",
+                    "rows_checked": int(len(sub) * k), "nmse_vs_cpu": e, "max_rel_vs_cpu": mr,
+                    "max_err_over_max_vs_cpu": max_err_scaled(got[sub], cpu), "f64_max_err_scaled": f64_err})
+    assert f64_err < F64_TOL, f"f64 agreement {f64_err:.3g}"
+    assert e < NMSE_GATE, f"NMSE {e:.3g}, max rel {mr:.3g}"

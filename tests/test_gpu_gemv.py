@@ -138,24 +138,41 @@ def test_gemv_fused_k_shares(tname, nrows, K):
     np.testing.assert_array_equal(with_b.reshape(-1), fused.reshape(-1) + b)
 
 
+def _one_column_op_splits_k(tname, nrows, K):
+    """Whether the one-column op splits this row into K shares: rows of two or
+    more 64-lane steps (2048 elements for Q8_0 / Q4_0, 4096 for the others)
+    below 8192 rows, when K > 4096 or there are at most 2048 rows."""
+    step = 64 * (32 if tname in ("Q8_0", "Q4_0") else 64)
+    return nrows < 8192 and K > step and (K > 4096 or nrows <= 2048)
+
+
 # 2-4 f32 columns on at most 4096-long rows below 8192 rows (and above, for
 # Q8_0 at 3-4 columns and rows of K <= 2048): the op runs the
 # quantize-in-GEMV kernel over all columns in one launch (2 columns for the
-# K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0); each column equals the
-# one-column op on it bit for bit.
+# K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0).  Where the one-column op runs
+# one K share, each column equals it bit for bit; where the one-column op
+# splits the row into K shares (Q8_0 / Q4_0 rows of two 2048-steps on at most
+# 2048 rows: attn_k / attn_v shapes) the one-launch kernel adds both steps in
+# each lane before the wave sum, another rounding order, so only the f64 and
+# CPU gates apply.
 @pytest.mark.parametrize("tname,nrows,K,ncols", [("Q4_K", 4096, 4096, 2), ("Q5_K", 1000, 4096, 2),
                                                  ("Q6_K", 1024, 4096, 2), ("IQ4_XS", 777, 2048, 3),
                                                  ("Q8_0", 4100, 4096, 4), ("Q4_0", 333, 96, 3),
                                                  ("Q8_0", 5000, 1024, 3), ("Q4_0", 4097, 4096, 2),
                                                  ("IQ4_XS", 6000, 4096, 2), ("Q8_0", 9000, 4096, 4),
-                                                 ("Q4_K", 8200, 2048, 2), ("Q4_0", 8195, 1024, 4)])
+                                                 ("Q4_K", 8200, 2048, 2), ("Q4_0", 8195, 1024, 4),
+                                                 ("Q8_0", 1024, 4096, 2), ("Q4_0", 500, 4096, 3),
+                                                 ("Q8_0", 2048, 4096, 4)])
 def test_op_few_columns_one_launch(tname, nrows, K, ncols):
     import ggml_hip as G
     t, wq, x, w_d, x_d, qs, _ = _run(tname, nrows, K, ncols)
     got = G.mul_mat(tname, w_d, x_d).cpu().numpy()
     for c in range(ncols):
         one = G.mul_mat_vec_f32(tname, w_d, K, x_d[c]).cpu().numpy().reshape(-1)
-        np.testing.assert_array_equal(got[c], one)
+        if _one_column_op_splits_k(tname, nrows, K):
+            assert max_err_scaled(got[c], one) < 1e-6
+        else:
+            np.testing.assert_array_equal(got[c], one)
     y = G.quantize_q8_1(x_d, K).cpu().numpy()
     ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
     assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
@@ -175,3 +192,24 @@ def test_gemv_config0_op_level():
     cpu = O.mul_mat(O.TYPE_Q4_K, wq, nrows, K, x, nth=8)
     assert nmse(got, cpu) < NMSE_GATE
     assert np.all(np.isfinite(got))
+
+
+def test_op_rejects_overlapping_columns():
+    """hip_qmm_mul_mat refuses column strides below the column length (outputs
+    or inputs that would overlap) for every column count, with
+    hipErrorInvalidValue, before any launch."""
+    import ctypes
+    import ggml_hip as G
+    nrows, K = 1024, 4096
+    wq = weights_q(O.TYPE_Q4_K, nrows, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    for ncols in (2, 4, 8, 16):
+        x_d = torch.from_numpy(np.array(acts(ncols, K))).cuda()
+        out = torch.zeros((ncols, nrows), device="cuda")
+        ws = torch.empty(G.workspace_size("Q4_K", K, ncols, nrows), dtype=torch.uint8, device="cuda")
+        for xs, ds in ((K, nrows - 1), (K - 32, nrows)):
+            e = G.lib().hip_qmm_mul_mat(O.TYPE_Q4_K, G._ptr(w_d), K, nrows, w_d.stride(0), G._ptr(x_d), ncols, xs,
+                                        G._ptr(out), ds, G._ptr(ws), ctypes.c_size_t(ws.numel()), G._stream())
+            assert e == 1, (ncols, xs, ds, e)
+    torch.cuda.synchronize()
+    assert float(out.abs().sum()) == 0.0

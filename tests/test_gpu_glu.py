@@ -329,6 +329,30 @@ def test_plugin_fuses_mul_mat_bias_and_runs_glu_alone(hb):
     glu_matches(O.GLU_GEGLU, hv[:, 32:], hv[:, :32], hb.get(gl, np.float32, (3, 32)), want)
 
 
+def test_plugin_does_not_take_a_run_node_as_bias(hb):
+    """ADD(mm, mm): the bias would be mm itself, which a fused launch never
+    computes, so the pair runs node by node and the sum is 2 * mm."""
+    import ggml_hip as G
+    from ggml_hip import abi
+    M, K = 4096, 4096
+    wq = weights_q(O.TYPE_Q4_K, M, K)
+    x = acts(1, K)
+    tw = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M], name=b"w")
+    tx = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1], name=b"x")
+    mm = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(tw, tx), name=b"mm")
+    add = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_ADD, srcs=(mm, mm), name=b"mm_mm")
+    hb.alloc([tw], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([tx, mm, add], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(tw, wq)
+    hb.set(tx, x)
+    hb.set(mm, np.full(M, np.nan, dtype=np.float32))
+    hb.set(add, np.full(M, np.nan, dtype=np.float32))
+    assert hb.compute([mm, add]) == abi.GGML_STATUS_SUCCESS
+    plain = G.mul_mat_vec_f32("Q4_K", _dev(wq), K, _dev(x)[0]).cpu().numpy().reshape(-1)
+    np.testing.assert_array_equal(hb.get(mm, np.float32, (M,)), plain)
+    np.testing.assert_array_equal(hb.get(add, np.float32, (M,)), plain + plain)
+
+
 # ---------------------------------------------------------------- MUL_MAT_ID (MoE decode)
 
 def _moe(tname, n_as, M, K, n_tokens, n_ids, seed):

@@ -255,3 +255,87 @@ def test_fill_normal_moments_and_fingerprint():
 
 
 FINGERPRINTS = {42: 3664293373807877317, 43: 7632513219039429954, 44: 984130064333561219}
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 4096, (1 << 20) + 3])
+def test_threaded_generators_equal_serial(n):
+    """The threaded normal fill (split at even indices, each part seeded from
+    its first pair's SplitMix64 state) and the threaded row quantizer give the
+    serial generators' values exactly, for odd lengths and ragged splits."""
+    serial = O.fill_normal(42, n, 0.0, 0.02, nth=1)
+    for nth in (2, 3, 8):
+        assert np.array_equal(O.fill_normal(42, n, 0.0, 0.02, nth=nth), serial)
+    rows = RNG.standard_normal((13, 512)).astype(np.float32) * 0.02
+    for t in (O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0):
+        one = O.quantize_ref(t, rows.reshape(-1)).reshape(13, -1)
+        for nth in (1, 4, 16):
+            assert np.array_equal(O.quantize_rows(t, rows, nth=nth), one)
+
+
+TILED = [O.TYPE_Q4_K, O.TYPE_Q5_K, O.TYPE_Q6_K, O.TYPE_IQ4_XS]
+
+
+def _random_blocks(t, nrows, K, rng):
+    """Random bytes as blocks with a modest finite fp16 scale, as the
+    reference's tiled test builds them (tiled.zig:1323-1343)."""
+    bs, bb = O.BLOCK[t]
+    nb = nrows * K // bs
+    blk = rng.integers(0, 256, size=(nb, bb), dtype=np.uint8)
+    scale = (0x3000 | (rng.integers(0, 1 << 16, size=nb) & 0x03FF)).astype(np.uint16)
+    if t == O.TYPE_Q6_K:
+        blk[:, bb - 2:bb] = scale.view(np.uint8).reshape(nb, 2)
+    else:
+        blk[:, 0:2] = scale.view(np.uint8).reshape(nb, 2)
+        if t in (O.TYPE_Q4_K, O.TYPE_Q5_K):
+            blk[:, 2:4] = (scale ^ 0x0100).view(np.uint8).reshape(nb, 2)
+    return blk.reshape(nrows, -1)
+
+
+@pytest.mark.skipif(not O.has_avx2(), reason="the tiled path is the AVX2 arm")
+@pytest.mark.parametrize("t", TILED)
+@pytest.mark.parametrize("K,nrows,ncols", [(512, 40, 33), (768, 24, 5)])
+def test_tiled_gemm_agrees_with_vec_dot(t, K, nrows, ncols):
+    """The reference's own check (checkMulMat, tiled.zig:1367-1438): every
+    element within 2e-4 x max|out| of vec_dot on the same Q8_K rows, on the
+    standard path (33 columns: a ragged 16-row and 16-column tail) and the
+    narrow one (5 columns, K in two- and one-slab extents), for random blocks
+    and for quantized N(0, 0.02) weights."""
+    rng = np.random.default_rng(0x711ED + t + K)
+    x = (rng.random((ncols, K), dtype=np.float32) * 2 - 1).astype(np.float32)
+    for wq in (_random_blocks(t, nrows, K, rng),
+               O.quantize_rows(t, rng.standard_normal((nrows, K)).astype(np.float32) * 0.02)):
+        got = O.mul_mat_tiled(t, wq, nrows, K, x, nth=1)
+        want = np.zeros_like(got)
+        for j in range(ncols):
+            y = O.quantize_ref(O.TYPE_Q8_K, x[j])
+            for i in range(nrows):
+                want[j, i] = O.vec_dot(t, O.IMPL_GENERIC, K, wq[i], y)
+        scale = float(np.max(np.abs(got)))
+        assert scale > 0 and np.all(np.isfinite(got))
+        assert np.max(np.abs(got - want)) <= 2e-4 * scale
+
+
+@pytest.mark.skipif(not O.has_avx2(), reason="the tiled path is the AVX2 arm")
+@pytest.mark.parametrize("t", TILED)
+def test_tiled_gemm_is_independent_of_threads_and_windows(t):
+    """Each output adds its slabs' terms in K order whatever the chunking, the
+    window or the path: the same bits on 1, 3 and 8 threads (other chunk
+    sizes, 256-row windows on 300 rows), and a column alone (the narrow
+    path) equals that column inside a wide run (the standard path)."""
+    rng = np.random.default_rng(77 + t)
+    nrows, K, ncols = 300, 1024, 40
+    wq = O.quantize_rows(t, rng.standard_normal((nrows, K)).astype(np.float32) * 0.02)
+    x = rng.standard_normal((ncols, K)).astype(np.float32)
+    one = O.mul_mat_tiled(t, wq, nrows, K, x, nth=1)
+    for nth in (3, 8):
+        assert np.array_equal(O.mul_mat_tiled(t, wq, nrows, K, x, nth=nth), one)
+    narrow = O.mul_mat_tiled(t, wq, nrows, K, x[17:20], nth=2)
+    assert np.array_equal(narrow, one[17:20])
+    # and the whole result is the CPU mul_mat's within the NMSE gate
+    cpu = O.mul_mat(t, wq, nrows, K, x, nth=4)
+    assert float(np.sum((one.astype(np.float64) - cpu) ** 2) / np.sum(cpu.astype(np.float64) ** 2)) < 1e-10
+
+
+def test_tiled_gemm_declines_untiled_types():
+    wq = O.quantize_rows(O.TYPE_Q8_0, np.zeros((16, 256), np.float32))
+    assert O.mul_mat_tiled(O.TYPE_Q8_0, wq, 16, 256, np.zeros((8, 256), np.float32)) is None
