@@ -186,6 +186,30 @@ int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t r
                     const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
                     int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
 
+/* Scratch bytes behind hip_qmm_mul_mat_noalloc, per device (32 MiB). */
+#define HIP_QMM_NOALLOC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * hip_qmm_mul_mat without the workspace arguments: the same dispatch, the
+ * same kernels and the same results, with its scratch (the Q8_1 copy of x and
+ * any split-K partials) in a fixed device array of
+ * HIP_QMM_NOALLOC_SCRATCH_BYTES that each device holds for the life of the
+ * process.  It calls no hipMalloc / hipFree or anything that allocates; the
+ * array's address is looked up once per device on the first call with that
+ * device current.  Uses the current device's array: `stream` must belong to
+ * the current device.  Shapes whose workspace
+ * (hip_qmm_mul_mat_workspace_size) exceeds the array are rejected with
+ * hipErrorInvalidValue before any launch.  All calls on one device share the
+ * array, so calls that may overlap on one GPU (different streams, threads)
+ * race; calls in one stream's order do not.
+ * No counterpart in the reference: an entry point for callers that cannot
+ * allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid allocation).
+ */
+int hip_qmm_mul_mat_noalloc(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                            const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
+                            int64_t dst_col_stride, void *stream);
+
 /*
  * int8-MFMA GEMM against planar Q8_1 activations for any column count
  * (K a multiple of 256).  Replaces launch_mul_mat_q (src/ggml/cuda/mmq.zig:282-408).

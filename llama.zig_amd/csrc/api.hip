@@ -6,6 +6,9 @@
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
+#include <atomic>
+#include <mutex>
+
 using namespace qmm;
 
 extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
@@ -99,4 +102,54 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
             return e;
     }
     return 0;
+}
+
+// ---------------------------------------------------------------- allocation-free MUL_MAT
+//
+// For callers that cannot allocate (code under HIP graph capture, serving
+// loops, harnesses that forbid hipMalloc): hip_qmm_mul_mat with its workspace
+// taken from a fixed device array instead of an argument.  Each device holds
+// its own copy of the array for the life of the process.  Its device address
+// is looked up once per device, with that device current, and kept; host
+// code never passes the array's name (a host-side stand-in) to a kernel.
+// Every call on one device shares its array: calls that overlap on one GPU
+// race, and a call leaves its scratch contents behind (nothing in the op
+// reads scratch before writing it, so no clearing is needed).
+
+static __device__ __align__(256) uint8_t scratch[HIP_QMM_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int MAX_DEVICES = 64;
+std::atomic<void *> scratch_addr[MAX_DEVICES];
+std::mutex scratch_mu;
+
+int current_device_scratch(void **out) {
+    int dev = -1;
+    if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+    if (dev < 0 || dev >= MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    void *p = scratch_addr[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(scratch_mu);
+        p = scratch_addr[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            if (hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) return (int)e;
+            if (!p) return (int)hipErrorInvalidSymbol;
+            scratch_addr[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return 0;
+}
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_noalloc(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                       const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
+                                       int64_t dst_col_stride, void *stream) {
+    if (ncols <= 0 || K <= 0) return (int)hipErrorInvalidValue;
+    if (hip_qmm_mul_mat_workspace_size(type, K, nrows, ncols) > (size_t)HIP_QMM_NOALLOC_SCRATCH_BYTES)
+        return (int)hipErrorInvalidValue;
+    void *ws = nullptr;
+    if (int e = current_device_scratch(&ws)) return e;
+    return hip_qmm_mul_mat(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, ws,
+                           (size_t)HIP_QMM_NOALLOC_SCRATCH_BYTES, stream);
 }
