@@ -86,6 +86,38 @@ int hip_qmm_mul_mat_vec(int type, const void *w, int64_t K, int64_t nrows, int64
                         int64_t dst_col_stride, void *stream);
 
 /*
+ * The reference's mul_mat_vec_q launch, argument for argument: the parameter
+ * list of mul_mat_vec_q_switch_type (src/ggml/cuda/mmvq.zig:496), which fills
+ * the kernel's Common struct (:260-280) at :349-420 from the strides
+ * mulMatVecQ computes (:531-696).  vy is AoS block_q8_1 as
+ * hip_qmm_quantize_q8_1 writes it; units as there: stride_*_x in weight
+ * blocks, stride_*_y in Q8_1 blocks, stride_*_dst in floats; ncols_x = K,
+ * nrows_x = M, ncols_dst 1..8.
+ *  - ids == NULL (MUL_MAT): for channel ch < nchannels_dst, sample s <
+ *    nsamples_dst and column c < ncols_dst, the rows
+ *    dst[c*stride_col_dst + ch*stride_channel_dst + s*stride_sample_dst + r]
+ *    = W[ch / (nchannels_dst/nchannels_x), s / (nsamples_dst/nsamples_x)]
+ *      . y[c*stride_col_y + ch*stride_channel_y + s*stride_sample_y];
+ *    nchannels_y == nchannels_dst, the ratios whole numbers.
+ *  - ids != NULL (MUL_MAT_ID): ncols_dst tokens, nchannels_dst slots; slot
+ *    ch of token c reads expert e = ids[c*ids_stride + ch] (weights at
+ *    e*stride_channel_x) and the activation row
+ *    y[c*stride_col_y + (ch % nchannels_y)*stride_channel_y], and writes the
+ *    row at dst[c*stride_col_dst + ch*stride_channel_dst]; an id outside
+ *    [0, nchannels_x) writes a zero row.  nsamples_x = nsamples_dst = 1.
+ * One launch (grid: rows x channels x samples or tokens), no workspace.
+ * Weight rows and strides at the blocks' natural alignment (16 B for Q4_K /
+ * Q5_K, 8 for IQ4_XS, 2 otherwise), vy 4-byte aligned.
+ */
+int hip_qmm_mul_mat_vec_q(int type, const void *vx, const void *vy, const int32_t *ids, float *dst,
+                          int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
+                          int64_t stride_col_y, int64_t stride_col_dst, int64_t nchannels_x, int64_t nchannels_y,
+                          int64_t nchannels_dst, int64_t stride_channel_x, int64_t stride_channel_y,
+                          int64_t stride_channel_dst, int64_t nsamples_x, int64_t nsamples_dst,
+                          int64_t stride_sample_x, int64_t stride_sample_y, int64_t stride_sample_dst,
+                          int64_t ids_stride, void *stream);
+
+/*
  * Decode GEMV of one f32 activation column with the Q8_1 quantization fused
  * in: dst[r] = sum_k W[r,k] * q8_1(x)[k], bit-identical to
  * hip_qmm_quantize_q8_1_planar followed by hip_qmm_mul_mat_vec on one column

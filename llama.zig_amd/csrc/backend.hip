@@ -494,6 +494,29 @@ bool run_mul_mat(BackendCtx *ctx, const ggml_tensor *node) {
     const ggml_tensor *a = node->src[0], *b = node->src[1];
     const int64_t K = a->ne[0], M = a->ne[1], N = b->ne[1];
     const int64_t r2 = b->ne[2] / a->ne[2], r3 = b->ne[3] / a->ne[3];
+    const TypeInfo ta = type_info(a->type);
+    const int64_t nbatch = b->ne[2] * b->ne[3];
+    if (nbatch > 1 && N <= 8 && b->ne[2] <= 65535 && b->ne[3] <= 65535 && a->nb[1] % ta.size == 0 &&
+        a->nb[2] % ta.size == 0 && a->nb[3] % ta.size == 0 && b->nb[1] % 4 == 0 && b->nb[2] % 4 == 0 &&
+        b->nb[3] % 4 == 0 && node->nb[2] % 4 == 0 && node->nb[3] % 4 == 0) {
+        // Batched decode, as the reference's mulMatVecQ runs it
+        // (src/ggml/cuda/mmvq.zig:531-696): every column of every batch to AoS
+        // Q8_1 in one launch, then one GEMV launch over channels and samples.
+        const int64_t Kp = (K + ROW_PADDING - 1) / ROW_PADDING * ROW_PADDING, cb = Kp / 32;
+        void *ws = workspace(ctx, (size_t)(N * nbatch * cb) * 36);
+        int rc = hip_qmm_quantize_q8_1(static_cast<const float *>(b->data), ws, K, (int64_t)(b->nb[1] / 4),
+                                       (int64_t)(b->nb[2] / 4), (int64_t)(b->nb[3] / 4), Kp, N, b->ne[2], b->ne[3],
+                                       ctx->stream);
+        if (!report(rc, "hip_qmm_quantize_q8_1", node)) return false;
+        rc = hip_qmm_mul_mat_vec_q(a->type, a->data, ws, nullptr, static_cast<float *>(node->data), K, M, N,
+                                   (int64_t)(a->nb[1] / ta.size), cb, (int64_t)(node->nb[1] / 4), a->ne[2], b->ne[2],
+                                   node->ne[2], (int64_t)(a->nb[2] / ta.size), N * cb, (int64_t)(node->nb[2] / 4),
+                                   a->ne[3], node->ne[3], (int64_t)(a->nb[3] / ta.size), N * b->ne[2] * cb,
+                                   (int64_t)(node->nb[3] / 4), 0, ctx->stream);
+        return report(rc, "hip_qmm_mul_mat_vec_q", node);
+    }
+    // One batch, or more than 8 columns: the op per (i2, i3) slice (its
+    // MMQ takes one weight matrix per launch).
     const size_t need = hip_qmm_mul_mat_workspace_size(a->type, K, M, N);
     void *ws = workspace(ctx, need);
     for (int64_t i3 = 0; i3 < b->ne[3]; ++i3)

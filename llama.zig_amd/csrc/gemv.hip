@@ -79,6 +79,16 @@ struct Act<TYPE_Q4_K> {
         ds[0] = t.x;
         ds[1] = t.y;
     }
+    // The same slice from AoS block_q8_1 (36 B: d, s, qs[32]) of one column.
+    __device__ __forceinline__ void load_aos(const uint8_t *col, int kl) {
+        const uint8_t *b0 = col + (kl / QK8) * Q81_BYTES, *b1 = b0 + Q81_BYTES;
+        ds[0] = ld_u32(b0);
+        ds[1] = ld_u32(b1);
+        q[0] = ld16_u(b0 + 4);
+        q[1] = ld16_u(b0 + 20);
+        q[2] = ld16_u(b1 + 4);
+        q[3] = ld16_u(b1 + 20);
+    }
 };
 
 // Q5_K and IQ4_XS take the activation slice as Q4_K does (64 values, two
@@ -107,6 +117,22 @@ struct Act<TYPE_Q6_K> {
         ds[1] = t.y;
         ds[2] = t.z;
         ds[3] = t.w;
+        sums();
+    }
+    // The same slice from AoS block_q8_1: group g is half h of block 8sb + 4n + g.
+    __device__ __forceinline__ void load_aos(const uint8_t *col, int kl) {
+        const int sb = kl / QK_K;
+        const int qq = (kl % QK_K) / 64;
+        const int n = qq >> 1, h = qq & 1;
+        const uint8_t *b = col + (int64_t)(sb * 8 + 4 * n) * Q81_BYTES;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            ds[g] = ld_u32(b + g * Q81_BYTES);
+            q[g] = ld16_u(b + g * Q81_BYTES + 4 + 16 * h);
+        }
+        sums();
+    }
+    __device__ __forceinline__ void sums() {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             int s = dot4(q[g].x, 0x01010101u, 0);
@@ -128,6 +154,12 @@ struct Act<TYPE_Q8_0> {
         q[1] = ld_u128(p + 16);
         ds = dsp[kl / QK8];
     }
+    __device__ __forceinline__ void load_aos(const uint8_t *col, int kl) {
+        const uint8_t *b = col + (kl / QK8) * Q81_BYTES;
+        ds = ld_u32(b);
+        q[0] = ld16_u(b + 4);
+        q[1] = ld16_u(b + 20);
+    }
 };
 
 // Q4_0: the Q8_0 slice plus its integer sum, which turns the dot of the raw
@@ -135,8 +167,15 @@ struct Act<TYPE_Q8_0> {
 template <>
 struct Act<TYPE_Q4_0> : Act<TYPE_Q8_0> {
     int asum;
+    __device__ __forceinline__ void load_aos(const uint8_t *col, int kl) {
+        Act<TYPE_Q8_0>::load_aos(col, kl);
+        sum();
+    }
     __device__ __forceinline__ void load(const int8_t *qs, const uint32_t *dsp, int kl) {
         Act<TYPE_Q8_0>::load(qs, dsp, kl);
+        sum();
+    }
+    __device__ __forceinline__ void sum() {
         int s = dot4(q[0].x, 0x01010101u, 0);
         s = dot4(q[0].y, 0x01010101u, s);
         s = dot4(q[0].z, 0x01010101u, s);
@@ -1385,4 +1424,198 @@ int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64
     default: launch_fxn_type<TYPE_Q8_0>(wb, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride, s); break;
     }
     return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------- the reference's MMVQ launch
+//
+// hip_qmm_mul_mat_vec_q: one launch over the channels and samples (or the
+// MUL_MAT_ID slots and tokens) of a batched GEMV, on AoS block_q8_1
+// activations as hip_qmm_quantize_q8_1 writes them, with the launch arguments
+// of the reference's mul_mat_vec_q (the Common struct, src/ggml/cuda/mmvq.zig
+// :260-280, filled at :349-420 from mulMatVecQ's strides, :531-696).  The
+// arithmetic is the two-rows-per-wave kernel's (Act::load_aos reads the same
+// slices from the AoS blocks).  Grid: x = row pairs of 4-wave workgroups,
+// y = destination channel (the slot with ids), z = sample (the token column
+// with ids).
+
+namespace {
+
+struct VecQArgs {
+    const uint8_t *vx, *vy;
+    const int32_t *ids;
+    float *dst;
+    int64_t ncols_x, nrows_x;
+    int64_t row_x;                           // bytes between weight rows
+    int64_t col_y, col_dst;                  // bytes of Q8_1 / floats between columns
+    int64_t nchannels_x, nchannels_y;
+    int64_t channel_x, channel_y, channel_dst;  // bytes, bytes, floats
+    int64_t channel_ratio, sample_ratio;
+    int64_t sample_x, sample_y, sample_dst;     // bytes, bytes, floats
+    int64_t ids_stride;
+};
+
+template <int TYPE, int NC, bool IDS>
+__global__ __launch_bounds__(64 * WAVES_PER_BLOCK) void gemv_vecq_kernel(const VecQArgs a) {
+    using F = Fmt<TYPE>;
+    constexpr int RPW = 2;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t row0 = ((int64_t)blockIdx.x * WAVES_PER_BLOCK + wave) * RPW;
+    if (row0 >= a.nrows_x) return;
+    const int64_t ch = blockIdx.y, z = blockIdx.z;
+    const uint8_t *x, *y;
+    float *d;
+    if constexpr (IDS) {
+        // one token column per grid z; its slot's expert from ids
+        const int64_t e = a.ids[z * a.ids_stride + ch];
+        d = a.dst + z * a.col_dst + ch * a.channel_dst;
+        if (e < 0 || e >= a.nchannels_x) {  // a dropped slot: a zero row
+            if (lane < RPW && row0 + lane < a.nrows_x) d[row0 + lane] = 0.0f;
+            return;
+        }
+        x = a.vx + e * a.channel_x;
+        y = a.vy + z * a.col_y + (ch % a.nchannels_y) * a.channel_y;
+    } else {
+        x = a.vx + (ch / a.channel_ratio) * a.channel_x + (z / a.sample_ratio) * a.sample_x;
+        y = a.vy + ch * a.channel_y + z * a.sample_y;
+        d = a.dst + ch * a.channel_dst + z * a.sample_dst;
+    }
+    const uint8_t *rowp[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) rowp[r] = x + (row0 + r < a.nrows_x ? row0 + r : a.nrows_x - 1) * a.row_x;
+    float acc[RPW][NC];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) acc[r][c] = 0.0f;
+    constexpr int STEP = 64 * F::W;
+    const int K32 = (int)a.ncols_x;
+    for (int k0 = 0; k0 < K32; k0 += STEP) {
+        const int kl = k0 + lane * F::W;
+        if (kl < K32) {
+            Wt<TYPE> wt[RPW];
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) wt[r].load(rowp[r], kl);
+            Act<TYPE> av[NC];
+#pragma unroll
+            for (int c = 0; c < NC; ++c) av[c].load_aos(y + c * a.col_y, kl);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r)
+#pragma unroll
+                for (int c = 0; c < NC; ++c) {
+                    int S[F::NSUB];
+                    wt[r].dots(av[c], S, kl);
+                    acc[r][c] += wt[r].combine(av[c], S, kl);
+                }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const float v = wave_sum(acc[r][c]);
+            if (lane == r * NC + c && row0 + r < a.nrows_x) d[c * a.col_dst + row0 + r] = v;
+        }
+}
+
+template <int TYPE, bool IDS>
+int launch_vecq(const VecQArgs &a, int64_t ncols, dim3 grid, hipStream_t s) {
+    const dim3 block(64 * WAVES_PER_BLOCK);
+    if constexpr (IDS) {
+        hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 1, true>), grid, block, 0, s, a);
+    } else {
+        switch (ncols) {
+        case 1: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 1, false>), grid, block, 0, s, a); break;
+        case 2: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 2, false>), grid, block, 0, s, a); break;
+        case 3: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 3, false>), grid, block, 0, s, a); break;
+        case 4: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 4, false>), grid, block, 0, s, a); break;
+        case 5: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 5, false>), grid, block, 0, s, a); break;
+        case 6: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 6, false>), grid, block, 0, s, a); break;
+        case 7: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 7, false>), grid, block, 0, s, a); break;
+        default: hipLaunchKernelGGL((gemv_vecq_kernel<TYPE, 8, false>), grid, block, 0, s, a); break;
+        }
+    }
+    return (int)hipGetLastError();
+}
+
+template <bool IDS>
+int launch_vecq_type(int type, const VecQArgs &a, int64_t ncols, dim3 grid, hipStream_t s) {
+    switch (type) {
+    case TYPE_Q4_K: return launch_vecq<TYPE_Q4_K, IDS>(a, ncols, grid, s);
+    case TYPE_Q5_K: return launch_vecq<TYPE_Q5_K, IDS>(a, ncols, grid, s);
+    case TYPE_Q6_K: return launch_vecq<TYPE_Q6_K, IDS>(a, ncols, grid, s);
+    case TYPE_Q4_0: return launch_vecq<TYPE_Q4_0, IDS>(a, ncols, grid, s);
+    case TYPE_IQ4_XS: return launch_vecq<TYPE_IQ4_XS, IDS>(a, ncols, grid, s);
+    default: return launch_vecq<TYPE_Q8_0, IDS>(a, ncols, grid, s);
+    }
+}
+
+int64_t block_bytes(int type) {
+    switch (type) {
+    case TYPE_Q4_K: return Q4K_BYTES;
+    case TYPE_Q5_K: return Q5K_BYTES;
+    case TYPE_Q6_K: return Q6K_BYTES;
+    case TYPE_Q4_0: return Q40_BYTES;
+    case TYPE_IQ4_XS: return IQ4XS_BYTES;
+    case TYPE_Q8_0: return Q80_BYTES;
+    default: return 0;
+    }
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_vec_q(int type, const void *vx, const void *vy, const int32_t *ids, float *dst,
+                                     int64_t ncols_x, int64_t nrows_x, int64_t ncols_dst, int64_t stride_row_x,
+                                     int64_t stride_col_y, int64_t stride_col_dst, int64_t nchannels_x,
+                                     int64_t nchannels_y, int64_t nchannels_dst, int64_t stride_channel_x,
+                                     int64_t stride_channel_y, int64_t stride_channel_dst, int64_t nsamples_x,
+                                     int64_t nsamples_dst, int64_t stride_sample_x, int64_t stride_sample_y,
+                                     int64_t stride_sample_dst, int64_t ids_stride, void *stream) {
+    const int64_t bb = block_bytes(type);
+    if (!bb || !vx || !vy || !dst || ncols_dst < 1 || ncols_dst > 8) return (int)hipErrorInvalidValue;
+    if (nchannels_x < 1 || nchannels_y < 1 || nchannels_dst < 1 || nsamples_x < 1 || nsamples_dst < 1)
+        return (int)hipErrorInvalidValue;
+    if (int e = check_shape(type, ncols_x, nrows_x, stride_row_x * bb)) return e;
+    const int64_t walign = block_align(type);
+    if ((uintptr_t)vx % walign || (stride_channel_x * bb) % walign || (stride_sample_x * bb) % walign ||
+        (uintptr_t)vy % 4 || stride_channel_x < 0 || stride_sample_x < 0)
+        return (int)hipErrorInvalidValue;
+    // each activation column holds the row's Q8_1 blocks
+    if (stride_col_y < ncols_x / QK8 || stride_channel_y < 0 || stride_sample_y < 0 || stride_col_dst < 0 ||
+        stride_channel_dst < 0 || stride_sample_dst < 0)
+        return (int)hipErrorInvalidValue;
+    const bool has_ids = ids != nullptr;
+    if (has_ids && (nsamples_x != 1 || nsamples_dst != 1 || ids_stride < nchannels_dst)) return (int)hipErrorInvalidValue;
+    if (!has_ids && (nchannels_dst % nchannels_x || nsamples_dst % nsamples_x || nchannels_y != nchannels_dst))
+        return (int)hipErrorInvalidValue;
+    if (!has_ids && ncols_dst > 1 && stride_col_dst < nrows_x) return (int)hipErrorInvalidValue;
+    const int64_t gz = has_ids ? ncols_dst : nsamples_dst;
+    const int64_t gx = (nrows_x + 2 * WAVES_PER_BLOCK - 1) / (2 * WAVES_PER_BLOCK);
+    if (gx > 0x7FFFFFFF || nchannels_dst > 65535 || gz > 65535) return (int)hipErrorInvalidValue;
+    VecQArgs a{};
+    a.vx = (const uint8_t *)vx;
+    a.vy = (const uint8_t *)vy;
+    a.ids = ids;
+    a.dst = dst;
+    a.ncols_x = ncols_x;
+    a.nrows_x = nrows_x;
+    a.row_x = stride_row_x * bb;
+    a.col_y = stride_col_y * Q81_BYTES;
+    a.col_dst = stride_col_dst;
+    a.nchannels_x = nchannels_x;
+    a.nchannels_y = nchannels_y;
+    a.channel_x = stride_channel_x * bb;
+    a.channel_y = stride_channel_y * Q81_BYTES;
+    a.channel_dst = stride_channel_dst;
+    a.channel_ratio = has_ids ? 1 : nchannels_dst / nchannels_x;
+    a.sample_ratio = nsamples_dst / nsamples_x;
+    a.sample_x = stride_sample_x * bb;
+    a.sample_y = stride_sample_y * Q81_BYTES;
+    a.sample_dst = stride_sample_dst;
+    a.ids_stride = ids_stride;
+    const dim3 grid((unsigned)gx, (unsigned)nchannels_dst, (unsigned)gz);
+    hipStream_t s = (hipStream_t)stream;
+    return has_ids ? launch_vecq_type<true>(type, a, ncols_dst, grid, s)
+                   : launch_vecq_type<false>(type, a, ncols_dst, grid, s);
 }

@@ -2,7 +2,7 @@
 //
 // The reference sends 2-24 src1 columns to a separate "few-row" MMQ kernel
 // (src/ggml/cuda/mmq_few.zig:1-20, mulMatQFew :204-255, shouldUseMmqFew
-// :847-860): at that width the weights are streamed once and the 128 x 32
+// :270-281): at that width the weights are streamed once and the 128 x 32
 // MMQ tile is mostly empty.  This is the CDNA4 kernel for that regime.
 //
 // Arithmetic (as mmq.hip / mmq_q4k_dma.hip, on the 16x16 MFMA shapes):

@@ -22,6 +22,7 @@ constexpr int Q4K_BYTES = 144;
 constexpr int Q5K_BYTES = 176;
 constexpr int Q6K_BYTES = 210;
 constexpr int Q80_BYTES = 34;
+constexpr int Q81_BYTES = 36;  // block_q8_1: d, s (f16), qs[32]
 constexpr int Q40_BYTES = 18;
 constexpr int IQ4XS_BYTES = 136;
 constexpr int64_t ROW_PAD = 512;  // activation row padding (MATRIX_ROW_PADDING)

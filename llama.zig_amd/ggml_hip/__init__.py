@@ -76,6 +76,8 @@ def lib():
         L.hip_qmm_mul_mat_id.restype = i32
         L.hip_qmm_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, i64,
                                          vp, ctypes.c_size_t, vp]
+        L.hip_qmm_mul_mat_vec_q.restype = i32
+        L.hip_qmm_mul_mat_vec_q.argtypes = [i32, vp, vp, vp, vp] + [i64] * 18 + [vp]
         L.hip_qmm_block_dots.restype = i32
         L.hip_qmm_block_dots.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, vp]
         _lib = L
@@ -277,6 +279,29 @@ def mmq(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=
     _check(lib().hip_qmm_mmq(t, _ptr(w), K, nrows, rs, _ptr(qs), _ptr(ds), n, _ptr(out), out.stride(0), wp, wn,
                              _stream()), "hip_qmm_mmq")
     return out
+
+
+def mul_mat_vec_q(qtype, w: torch.Tensor, y_q8_1: torch.Tensor, K: int, ncols_dst: int, dst: torch.Tensor, *,
+                  nchannels_x=1, nchannels_y=1, nchannels_dst=1, nsamples_x=1, nsamples_dst=1,
+                  stride_col_y, stride_col_dst, stride_channel_x=0, stride_channel_y=0, stride_channel_dst=0,
+                  stride_sample_x=0, stride_sample_y=0, stride_sample_dst=0, ids=None, ids_stride=0, nrows=None):
+    """hip_qmm_mul_mat_vec_q: the reference's mul_mat_vec_q launch on AoS
+    block_q8_1 activations (strides of x in weight blocks, of y in Q8_1
+    blocks, of dst in floats; w's first matrix gives the row stride)."""
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    _require_cuda(w, y_q8_1, dst)
+    bs, bb = BLOCK[t]
+    nrows = w.shape[-2] if nrows is None else nrows
+    row_stride = w.stride(-2)
+    if row_stride % bb:
+        raise HipQmmError("weight rows must be whole blocks apart")
+    _check(lib().hip_qmm_mul_mat_vec_q(t, _ptr(w), _ptr(y_q8_1), _ptr(ids) if ids is not None else None, _ptr(dst),
+                                       K, nrows, ncols_dst, row_stride // bb, stride_col_y, stride_col_dst,
+                                       nchannels_x, nchannels_y, nchannels_dst, stride_channel_x, stride_channel_y,
+                                       stride_channel_dst, nsamples_x, nsamples_dst, stride_sample_x,
+                                       stride_sample_y, stride_sample_dst, ids_stride, _stream()),
+           "hip_qmm_mul_mat_vec_q")
+    return dst
 
 
 def block_dots(qtype, w: torch.Tensor, K: int, qs: torch.Tensor):

@@ -154,3 +154,35 @@ def test_alloc_buffer_out_of_memory_returns_null(hb):
     x = np.array(acts(2, K))
     got = _mul_mat_graph(hb, abi.GGML_TYPE_Q4_K, wq, K, M, x)
     assert nmse(got[0], O.mul_mat(O.TYPE_Q4_K, wq, M, K, x, nth=8)) < NMSE_GATE
+
+
+@pytest.mark.parametrize("tname,N,bw,bx", [("Q4_K", 8, (2, 1), (4, 3)), ("Q6_K", 2, (1, 2), (2, 4)),
+                                           ("IQ4_XS", 1, (3, 1), (3, 2)), ("Q8_0", 12, (2, 1), (4, 1))])
+def test_graph_mul_mat_batched_dims_2_and_3(hb, tname, N, bw, bx):
+    """A MUL_MAT batched over dims 2 and 3 with src0 broadcast over both: up to
+    8 columns run as one AoS quantize + one hip_qmm_mul_mat_vec_q launch over
+    channels and samples (the reference's mulMatVecQ); more columns run the op
+    per slice.  Every slice against the CPU path on its weight matrix."""
+    from ggml_hip import abi
+    t = TYPES[tname]
+    M, K = 320, 1024
+    nw, nx = bw[0] * bw[1], bx[0] * bx[1]
+    w = np.stack([O.quantize_rows(t, weights_f32(M, K, idx=i)) for i in range(nw)])
+    x = np.array(acts(nx * N, K)).reshape(nx, N, K)
+    a = abi.make_tensor(t, [K, M, bw[0], bw[1]], name=b"w")
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [K, N, bx[0], bx[1]], name=b"x")
+    d = abi.make_tensor(abi.GGML_TYPE_F32, [M, N, bx[0], bx[1]], op=abi.GGML_OP_MUL_MAT, srcs=(a, b), name=b"out")
+    hb.alloc([a], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([b, d], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(a, w)
+    hb.set(b, x)
+    hb.set(d, np.full((nx, N, M), np.nan, dtype=np.float32))
+    assert hb.compute([d]) == abi.GGML_STATUS_SUCCESS
+    got = hb.get(d, np.float32, (nx, N, M))
+    r2, r3 = bx[0] // bw[0], bx[1] // bw[1]
+    for i3 in range(bx[1]):
+        for i2 in range(bx[0]):
+            wi = (i3 // r3) * bw[0] + i2 // r2
+            xi = i3 * bx[0] + i2
+            cpu = O.mul_mat(t, w[wi], M, K, x[xi], nth=8)
+            assert nmse(got[xi], cpu) < NMSE_GATE, (i2, i3)

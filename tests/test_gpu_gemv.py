@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 
 import oracle_lib as O
-from cases import acts, max_err_scaled, max_rel, nmse, weights_q
+from cases import acts, max_err_scaled, max_rel, nmse, weights_f32, weights_q
 
 torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
@@ -213,3 +213,113 @@ def test_op_rejects_overlapping_columns():
             assert e == 1, (ncols, xs, ds, e)
     torch.cuda.synchronize()
     assert float(out.abs().sum()) == 0.0
+
+
+# ---------------------------------------------------------------- the reference's MMVQ launch
+
+def _aos(G, x2d, K, padded=True):
+    xd = torch.from_numpy(np.ascontiguousarray(x2d, dtype=np.float32)).cuda()
+    return G.quantize_q8_1(xd) if padded else G.quantize_q8_1(xd, K)
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K", "Q8_0", "Q4_0", "IQ4_XS"])
+def test_mul_mat_vec_q_broadcast_channels_and_samples(tname):
+    """hip_qmm_mul_mat_vec_q without ids: 3 columns x 4 destination channels x
+    2 samples in one launch, weights broadcast over channels (ratio 2) and
+    samples (ratio 2), AoS Q8_1 activations padded to 512 as the reference's
+    quantizer leaves them; every (channel, sample) slice against the f64
+    formula and the CPU path on its own weight matrix."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    K, M, N = 2048, 300, 3
+    ncx, nsx, ncd, nsd = 2, 1, 4, 2
+    bs, bb = O.BLOCK[t]
+    wq = np.stack([np.array(weights_q(t, M, K, idx)) for idx in range(ncx * nsx)])
+    rb_blocks = wq.shape[2] // bb
+    x = np.array(acts(nsd * ncd * N, K)).reshape(nsd, ncd, N, K)
+    y = _aos(G, x.reshape(-1, K), K)
+    cb = G.padded_k(K) // 32
+    dst = torch.full((nsd, ncd, N, M), float("nan"), device="cuda")
+    G.mul_mat_vec_q(tname, torch.from_numpy(wq).cuda(), y, K, N, dst, nchannels_x=ncx, nchannels_y=ncd,
+                    nchannels_dst=ncd, nsamples_x=nsx, nsamples_dst=nsd, stride_col_y=cb, stride_col_dst=M,
+                    stride_channel_x=M * rb_blocks, stride_channel_y=N * cb, stride_channel_dst=N * M,
+                    stride_sample_x=ncx * M * rb_blocks, stride_sample_y=ncd * N * cb, stride_sample_dst=ncd * N * M)
+    got = dst.cpu().numpy()
+    yk = _aos(G, x.reshape(-1, K), K, padded=False).cpu().numpy().reshape(nsd, ncd, N, -1)
+    for s in range(nsd):
+        for ch in range(ncd):
+            wsl = wq[(s // (nsd // nsx)) * ncx + ch // (ncd // ncx)]
+            ideal = O.mul_mat_q8_1_f64(t, wsl, M, K, yk[s, ch], N)
+            assert max_err_scaled(got[s, ch], ideal) < F64_TOL, (s, ch, max_err_scaled(got[s, ch], ideal))
+            assert nmse(got[s, ch], O.mul_mat(t, wsl, M, K, x[s, ch], nth=8)) < NMSE_GATE
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q6_K", "Q8_0", "IQ4_XS"])
+@pytest.mark.parametrize("ne11", [1, 4])
+def test_mul_mat_vec_q_ids(tname, ne11):
+    """hip_qmm_mul_mat_vec_q with ids (MUL_MAT_ID): 3 tokens x 4 slots, one
+    activation row per token (ne11 = 1) or per slot, ids of -1 and past the
+    expert count writing zero rows; against mul_mat_id on the CPU and the f64
+    formula per expert."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    n_as, M, K, n_tokens, n_ids = 5, 200, 1024, 3, 4
+    bs, bb = O.BLOCK[t]
+    wq = O.quantize_rows(t, np.array(weights_f32(n_as * M, K, 3))).reshape(n_as, M, -1)
+    rb_blocks = wq.shape[2] // bb
+    ids = np.random.default_rng(ne11).integers(0, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    ids[0, 1] = -1
+    ids[2, 3] = n_as + 2
+    x = np.array(acts(n_tokens * ne11, K, 2)).reshape(n_tokens, ne11, K)
+    y = _aos(G, x.reshape(-1, K), K)
+    cb = G.padded_k(K) // 32
+    dst = torch.full((n_tokens, n_ids, M), float("nan"), device="cuda")
+    G.mul_mat_vec_q(tname, torch.from_numpy(wq).cuda(), y, K, n_tokens, dst, nchannels_x=n_as, nchannels_y=ne11,
+                    nchannels_dst=n_ids, stride_col_y=ne11 * cb, stride_col_dst=n_ids * M,
+                    stride_channel_x=M * rb_blocks, stride_channel_y=cb, stride_channel_dst=M,
+                    ids=torch.from_numpy(ids).cuda(), ids_stride=n_ids)
+    got = dst.cpu().numpy()
+    bad = (ids < 0) | (ids >= n_as)
+    assert np.all(got[bad] == 0.0)
+    ok_ids = np.where(bad, -1, ids).astype(np.int32)
+    assert nmse(got, O.mul_mat_id(t, wq, n_as, M, K, x, ok_ids, nth=8)) < NMSE_GATE
+    yk = _aos(G, x.reshape(-1, K), K, padded=False).cpu().numpy()
+    from cases import mul_mat_id_f64
+    ideal = mul_mat_id_f64(t, wq, M, K, yk, ne11, ok_ids)
+    assert max_err_scaled(got, ideal) < F64_TOL
+
+
+@pytest.mark.parametrize("tname,nrows,K,ncols", [("Q8_0", 4100, 2048, 1), ("Q4_0", 4100, 2048, 2),
+                                                 ("Q6_K", 4100, 4096, 3), ("Q4_K", 4100, 4096, 1),
+                                                 ("IQ4_XS", 4100, 4096, 1), ("Q5_K", 4100, 4096, 1)])
+def test_mul_mat_vec_q_equals_the_planar_gemv(tname, nrows, K, ncols):
+    """On shapes where hip_qmm_mul_mat_vec runs the two-rows-per-wave kernel,
+    the AoS launch gives the same bits: the same slices, dots and order."""
+    import ggml_hip as G
+    t, wq, x, w_d, x_d, qs, planar = _run(tname, nrows, K, ncols)
+    y = G.quantize_q8_1(x_d)
+    cb = G.padded_k(K) // 32
+    dst = torch.full((ncols, nrows), float("nan"), device="cuda")
+    G.mul_mat_vec_q(tname, w_d, y, K, ncols, dst, stride_col_y=cb, stride_col_dst=nrows)
+    np.testing.assert_array_equal(dst.cpu().numpy(), planar)
+
+
+def test_mul_mat_vec_q_rejects_bad_launches():
+    import ggml_hip as G
+    t = O.TYPE_Q4_K
+    K, M = 1024, 64
+    w_d = torch.from_numpy(np.array(weights_q(t, M, K))).cuda()
+    y = G.quantize_q8_1(torch.zeros((2, K), device="cuda"))
+    dst = torch.zeros((2, M), device="cuda")
+    cb = G.padded_k(K) // 32
+    ok = dict(stride_col_y=cb, stride_col_dst=M)
+    with pytest.raises(G.HipQmmError):  # channel ratio not whole
+        G.mul_mat_vec_q("Q4_K", w_d, y, K, 1, dst, nchannels_x=2, nchannels_y=3, nchannels_dst=3, **ok)
+    with pytest.raises(G.HipQmmError):  # columns shorter than the row
+        G.mul_mat_vec_q("Q4_K", w_d, y, K, 2, dst, stride_col_y=K // 32 - 1, stride_col_dst=M)
+    with pytest.raises(G.HipQmmError):  # more than 8 columns
+        G.mul_mat_vec_q("Q4_K", w_d, y, K, 9, dst, **ok)
+    with pytest.raises(G.HipQmmError):  # overlapping output columns
+        G.mul_mat_vec_q("Q4_K", w_d, y, K, 2, dst, stride_col_y=cb, stride_col_dst=M - 1)
+    torch.cuda.synchronize()
+    assert float(dst.abs().sum()) == 0.0
