@@ -264,16 +264,17 @@ int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols);
 
 /*
  * Expert-grouped MMQ over device-side tile tables (see hip_qmm_mul_mat_id):
- * tiles[2*i] = expert, tiles[2*i+1] = first routed column of the tile;
- * *n_tiles live entries; expert_off[e]..expert_off[e+1] are expert e's
- * columns; col_src / col_dst map a routed column to its activation row and
- * its dst row.  Mirrors mul_mat_q's ids path (src/ggml/cuda/mmq.zig:750-855).
+ * tiles[4*i .. 4*i+3] = {expert, col_low, col_high, unused}, the layout of
+ * the reference's ggml_cuda_mm_id_tile_spec (src/ggml/cuda/mmid.zig:18-27):
+ * routed columns col_low .. col_high-1 (at most bn of them) of that expert;
+ * *n_tiles live entries, at most max_tiles; col_src / col_dst map a routed
+ * column to its activation row and its dst row.  Mirrors mul_mat_q's ids
+ * path (src/ggml/cuda/mmq.zig:750-855).  tiles 16-byte aligned.
  */
 int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                         int64_t expert_stride, const int8_t *y_qs, const void *y_ds, float *dst,
                         int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
-                        const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
-                        const int32_t *col_dst, void *stream);
+                        const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst, void *stream);
 
 /* Bytes of workspace hip_qmm_mul_mat_id needs. */
 size_t hip_qmm_mul_mat_id_workspace_size(int type, int64_t K, int64_t n_as, int64_t ne11, int64_t n_tokens,

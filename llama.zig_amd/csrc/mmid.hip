@@ -19,132 +19,190 @@ using namespace qmm;
 extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                    int64_t expert_stride, const int8_t *y_qs, const void *y_ds, float *dst,
                                    int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
-                                   const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
-                                   const int32_t *col_dst, void *stream);
+                                   const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst,
+                                   void *stream);
 
 namespace {
 
-constexpr int GROUP_THREADS = 1024;
 constexpr int MAX_EXPERTS = 1024;
+constexpr int PREP_THREADS = 256;
+constexpr int IDS_PER_THREAD = 16;                          // consecutive pairs per thread and chunk
+constexpr int CHUNK = PREP_THREADS * IDS_PER_THREAD;        // pairs per chunk
+constexpr int QUANT_VALS = PREP_THREADS * 8;                // K values one quantizing workgroup covers
 
-constexpr int IDS_PER_THREAD = 16;  // ids held in registers between the passes
-
-// Exclusive prefix sums of two per-thread values over the workgroup (thread i
-// holds the values of expert i), with the totals.
-__device__ __forceinline__ void block_excl_scan2(int &a, int &b, int &tot_a, int &tot_b) {
-    __shared__ int wa[GROUP_THREADS / 64], wb[GROUP_THREADS / 64];
+// Exclusive prefix sum of one value per thread over the workgroup, with the
+// total.  `buf` is PREP_THREADS / 64 ints of LDS; ends with a barrier.
+__device__ __forceinline__ int block_excl_scan(int a, int &total, int *buf) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    int ia = a, ib = b;  // inclusive scans inside the wave
+    int ia = a;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
-        const int ua = __shfl_up(ia, off), ub = __shfl_up(ib, off);
-        if (lane >= off) {
-            ia += ua;
-            ib += ub;
-        }
+        const int u = __shfl_up(ia, off);
+        if (lane >= off) ia += u;
     }
-    if (lane == 63) {
-        wa[wave] = ia;
-        wb[wave] = ib;
-    }
+    if (lane == 63) buf[wave] = ia;
     __syncthreads();
-    int pa = 0, pb = 0;
-    tot_a = 0;
-    tot_b = 0;
-    for (int w = 0; w < GROUP_THREADS / 64; ++w) {
-        if (w < wave) {
-            pa += wa[w];
-            pb += wb[w];
-        }
-        tot_a += wa[w];
-        tot_b += wb[w];
+    int pre = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < PREP_THREADS / 64; ++w) {
+        const int v = buf[w];
+        if (w < wave) pre += v;
+        total += v;
     }
-    a = pa + ia - a;
-    b = pb + ib - b;
+    __syncthreads();  // buf may be reused by the caller's next scan
+    return pre + ia - a;
 }
 
-// One workgroup.  Every thread first loads its ids into registers (all loads
-// in flight at once); pass 1 counts the pairs routed to each expert (LDS
-// atomics); parallel exclusive scans give each expert its column range and
-// its tile range, and thread e writes expert e's tiles; pass 2 places every
-// pair at its expert's cursor.  The order of pairs inside an expert's range is
-// whatever the atomics give: each pair writes its own output row, so the
-// order does not change any result.
-__global__ __launch_bounds__(GROUP_THREADS) void mmid_group(
+// One launch that prepares a MUL_MAT_ID: workgroups [0, n_group) build the
+// expert grouping, the rest quantize the activation rows to planar Q8_1 (the
+// 8-values-per-lane form of quantize_q8_1.hip); the two parts are independent.
+//
+// Grouping, in the shape of the reference's mm_ids_helper (one block per
+// expert, src/ggml/cuda/mmid.zig:30-70): every grouping workgroup counts the
+// pairs of all experts (the ids are a few KB, read from L2 by all of them),
+// scans the counts into column and tile offsets, and then writes, for its own
+// experts e = g, g + n_group, ..., the pairs routed to e in pair order
+// (col_src: activation row, col_dst: output row) and e's column tiles
+// {expert, col_low, col_high, 0}.  Workgroup 0 also writes the tile count.
+// Pairs whose id is -1 or out of
+// [0, n_as) get a zero output row (mulmat.zig:670-676), written by one thread
+// of the grouping workgroups.  The result does not depend on scheduling:
+// every position is a function of the ids alone.
+__global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
     const int32_t *__restrict__ ids, int64_t ids_stride, int64_t n_tokens, int64_t n_ids, int n_as, int64_t ne11,
-    int bn, int32_t *__restrict__ col_src, int32_t *__restrict__ col_dst, int32_t *__restrict__ expert_off,
-    int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles, float *__restrict__ dst, int64_t dst_row_stride,
-    int64_t nrows) {
-    __shared__ int count[MAX_EXPERTS];
-    __shared__ int cursor[MAX_EXPERTS];
-    // pair indices fit in 32 bits (checked by the host): 32-bit division
-    // instead of the much longer 64-bit sequence
-    const uint32_t npairs = (uint32_t)(n_tokens * n_ids), nid = (uint32_t)n_ids;
+    int bn, int n_group, int32_t *__restrict__ col_src, int32_t *__restrict__ col_dst,
+    int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
+    float *__restrict__ dst, int64_t dst_row_stride, int64_t nrows, const float *__restrict__ x, int64_t K,
+    int64_t x_row_stride, int64_t Kp, int nq_per_row, int8_t *__restrict__ qs, uint32_t *__restrict__ ds) {
     const int tid = threadIdx.x;
+    if ((int)blockIdx.x >= n_group) {
+        // quantize: workgroup (row, K slice of QUANT_VALS values); Kp is a
+        // multiple of 512, so a quad (one 32-block) is wholly inside or past Kp
+        const int b = (int)blockIdx.x - n_group;
+        const int64_t c = b / nq_per_row;
+        const int64_t k = (int64_t)(b - c * nq_per_row) * QUANT_VALS + tid * 8;
+        if (k >= Kp) return;
+        float v[8];
+        if (k < K) {  // K % 32 == 0
+            const float4 a0 = *reinterpret_cast<const float4 *>(x + c * x_row_stride + k);
+            const float4 a1 = *reinterpret_cast<const float4 *>(x + c * x_row_stride + k + 4);
+            v[0] = a0.x; v[1] = a0.y; v[2] = a0.z; v[3] = a0.w;
+            v[4] = a1.x; v[5] = a1.y; v[6] = a1.z; v[7] = a1.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+        }
+        const Q8Quad r = q8_1_quantize_quad(v);
+        *reinterpret_cast<uint2 *>(qs + c * Kp + k) = make_uint2(r.lo, r.hi);
+        if ((tid & 3) == 0) ds[c * (Kp / QK8) + k / QK8] = r.ds;
+        return;
+    }
+
+    __shared__ int count[MAX_EXPERTS];
+    __shared__ int coff[MAX_EXPERTS], toff[MAX_EXPERTS];
+    __shared__ int sbuf[PREP_THREADS / 64];
+    const int g = (int)blockIdx.x;
+    // pair indices fit in 32 bits (checked by the host): 32-bit division
+    const uint32_t npairs = (uint32_t)(n_tokens * n_ids), nid = (uint32_t)n_ids;
+    const bool dense_ids = ids_stride == n_ids;  // uniform; the usual layout, no division per id
     auto id_of = [&](uint32_t p) -> int {
-        const uint32_t t = p / nid;
-        const int e = ids[(int64_t)t * ids_stride + (p - t * nid)];
+        int e;
+        if (dense_ids) {
+            e = ids[p];
+        } else {
+            const uint32_t t = p / nid;
+            e = ids[(int64_t)t * ids_stride + (p - t * nid)];
+        }
         return e >= 0 && e < n_as ? e : -1;
     };
-    int eid[IDS_PER_THREAD];
-#pragma unroll
-    for (int k = 0; k < IDS_PER_THREAD; ++k) {
-        const uint32_t p = tid + (uint32_t)k * GROUP_THREADS;
-        eid[k] = p < npairs ? id_of(p) : -1;
-    }
-    for (int e = tid; e < n_as; e += GROUP_THREADS) count[e] = 0;
+    for (int e = tid; e < n_as; e += PREP_THREADS) count[e] = 0;
     __syncthreads();
-#pragma unroll
-    for (int k = 0; k < IDS_PER_THREAD; ++k)
-        if (eid[k] >= 0) atomicAdd(&count[eid[k]], 1);
-    for (uint32_t p = tid + (uint32_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) {
-        const int e = id_of(p);
-        if (e >= 0) atomicAdd(&count[e], 1);
-    }
-    __syncthreads();
-    {
-        int c = tid < n_as ? count[tid] : 0;
-        int nt = (c + bn - 1) / bn;
-        const int nt_own = nt;
-        int total_c, total_t;
-        block_excl_scan2(c, nt, total_c, total_t);
-        if (tid < n_as) {
-            cursor[tid] = c;
-            expert_off[tid] = c;
-            for (int i = 0; i < nt_own; ++i) {
-                tiles[2 * (nt + i)] = tid;
-                tiles[2 * (nt + i) + 1] = c + i * bn;
-            }
-        }
-        if (tid == 0) {
-            expert_off[n_as] = total_c;
-            *n_tiles = total_t;
-        }
-    }
-    __syncthreads();
-    const uint32_t n11 = (uint32_t)ne11;  // 1 or n_ids
-    auto place = [&](uint32_t p, int e) {
-        if (e >= 0) {
-            const int pos = atomicAdd(&cursor[e], 1);
-            const uint32_t t = p / nid, sl = p - t * nid;
-            col_src[pos] = (int32_t)(t * n11 + (n11 == 1 ? 0u : sl));
-            col_dst[pos] = (int32_t)p;
-        } else {
-            float *row = dst + (int64_t)p * dst_row_stride;
-            for (int64_t r = 0; r < nrows; ++r) row[r] = 0.0f;
-        }
+    // ids of pair p, or -1 past the end; the loads are unconditional (index
+    // clamped) so that a thread's loads are all in flight before the first use
+    auto id_or_none = [&](uint32_t p) -> int {
+        const int e = id_of(p < npairs ? p : npairs - 1);
+        return p < npairs ? e : -1;
     };
+    for (uint32_t base = 0; base < npairs; base += CHUNK) {
+        int ev[IDS_PER_THREAD];
 #pragma unroll
-    for (int k = 0; k < IDS_PER_THREAD; ++k) {
-        const uint32_t p = tid + (uint32_t)k * GROUP_THREADS;
-        if (p < npairs) place(p, eid[k]);
+        for (int k = 0; k < IDS_PER_THREAD; ++k) ev[k] = id_or_none(base + (uint32_t)k * PREP_THREADS + tid);
+#pragma unroll
+        for (int k = 0; k < IDS_PER_THREAD; ++k)
+            if (ev[k] >= 0) atomicAdd(&count[ev[k]], 1);
     }
-    for (uint32_t p = tid + (uint32_t)IDS_PER_THREAD * GROUP_THREADS; p < npairs; p += GROUP_THREADS) place(p, id_of(p));
+    __syncthreads();
+    // column and tile offsets of every expert: each thread scans a run of
+    // consecutive experts, then the runs are scanned across the workgroup
+    constexpr int EPT = MAX_EXPERTS / PREP_THREADS;
+    int c_run = 0, t_run = 0;
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid * EPT + i;
+        if (e < n_as) {
+            c_run += count[e];
+            t_run += (count[e] + bn - 1) / bn;
+        }
+    }
+    int c_tot, t_tot;
+    int c_pre = block_excl_scan(c_run, c_tot, sbuf);
+    int t_pre = block_excl_scan(t_run, t_tot, sbuf);
+#pragma unroll
+    for (int i = 0; i < EPT; ++i) {
+        const int e = tid * EPT + i;
+        if (e < n_as) {
+            coff[e] = c_pre;
+            toff[e] = t_pre;
+            c_pre += count[e];
+            t_pre += (count[e] + bn - 1) / bn;
+        }
+    }
+    __syncthreads();
+    if (g == 0 && tid == 0) *n_tiles = t_tot;
+    for (int e = g; e < n_as; e += n_group) {
+        const int ce = count[e], c0 = coff[e], t0 = toff[e];
+        for (int i = tid; i * bn < ce; i += PREP_THREADS) {
+            const int lo = c0 + i * bn, hi = lo + bn < c0 + ce ? lo + bn : c0 + ce;
+            *reinterpret_cast<int4 *>(tiles + 4 * (t0 + i)) = make_int4(e, lo, hi, 0);
+        }
+        // e's pairs in pair order: thread tid takes IDS_PER_THREAD consecutive
+        // pairs of each chunk, counts its matches and scans for its position
+        int pos = c0;
+        for (uint32_t base = 0; base < npairs; base += CHUNK) {
+            const uint32_t p0 = base + (uint32_t)tid * IDS_PER_THREAD;
+            int ev[IDS_PER_THREAD];
+#pragma unroll
+            for (int k = 0; k < IDS_PER_THREAD; ++k) ev[k] = id_or_none(p0 + k);
+            uint32_t mask = 0;
+#pragma unroll
+            for (int k = 0; k < IDS_PER_THREAD; ++k) mask |= (ev[k] == e ? 1u : 0u) << k;
+            int tot;
+            int at = pos + block_excl_scan(__builtin_popcount(mask), tot, sbuf);
+            const uint32_t n11 = (uint32_t)ne11;  // 1 or n_ids
+            while (mask) {
+                const int k = __builtin_ctz(mask);
+                mask &= mask - 1;
+                const uint32_t p = p0 + k, t = p / nid, sl = p - t * nid;
+                col_src[at] = (int32_t)(t * n11 + (n11 == 1 ? 0u : sl));
+                col_dst[at] = (int32_t)p;
+                ++at;
+            }
+            pos += tot;
+        }
+    }
+    // zero rows for invalid ids: one pair per thread, the pairs spread over
+    // the grouping workgroups (independent loads, no chain of round trips)
+    for (uint32_t p = (uint32_t)g * PREP_THREADS + tid; p < npairs; p += (uint32_t)n_group * PREP_THREADS) {
+        if (id_of(p) >= 0) continue;
+        float *row = dst + (int64_t)p * dst_row_stride;
+        for (int64_t r = 0; r < nrows; ++r) row[r] = 0.0f;
+    }
 }
 
 struct MmidLayout {
     int64_t Kp, nrows_x, npairs, max_tiles;
-    size_t off_qs, off_ds, off_src, off_dst, off_eoff, off_tiles, off_ntiles, total;
+    size_t off_qs, off_ds, off_src, off_dst, off_tiles, off_ntiles, total;
 };
 
 MmidLayout layout(int64_t K, int64_t n_as, int64_t ne11, int64_t n_tokens, int64_t n_ids, int bn) {
@@ -159,8 +217,7 @@ MmidLayout layout(int64_t K, int64_t n_as, int64_t ne11, int64_t n_tokens, int64
     L.off_ds = o;     o = a256(o + (size_t)(L.nrows_x * (L.Kp / QK8)) * 4);
     L.off_src = o;    o = a256(o + (size_t)L.npairs * 4);
     L.off_dst = o;    o = a256(o + (size_t)L.npairs * 4);
-    L.off_eoff = o;   o = a256(o + (size_t)(n_as + 1) * 4);
-    L.off_tiles = o;  o = a256(o + (size_t)L.max_tiles * 8);
+    L.off_tiles = o;  o = a256(o + (size_t)L.max_tiles * 16);
     L.off_ntiles = o; o = a256(o + 4);
     L.total = o;
     return L;
@@ -210,14 +267,26 @@ extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nr
     int8_t *qs = (int8_t *)(ws + L.off_qs);
     void *ds = ws + L.off_ds;
     int32_t *col_src = (int32_t *)(ws + L.off_src), *col_dst = (int32_t *)(ws + L.off_dst);
-    int32_t *eoff = (int32_t *)(ws + L.off_eoff), *tiles = (int32_t *)(ws + L.off_tiles);
+    int32_t *tiles = (int32_t *)(ws + L.off_tiles);
     int32_t *ntiles = (int32_t *)(ws + L.off_ntiles);
     hipStream_t s = (hipStream_t)stream;
 
-    if (int e = hip_qmm_quantize_q8_1_planar(x, K, L.nrows_x, x_row_stride, qs, ds, stream)) return e;
-    hipLaunchKernelGGL(mmid_group, dim3(1), dim3(GROUP_THREADS), 0, s, ids, ids_stride, n_tokens, n_ids, (int)n_as,
-                       ne11, bn, col_src, col_dst, eoff, tiles, ntiles, dst, dst_row_stride, nrows);
+    const int n_group = n_as < 256 ? (int)n_as : 256;
+    if ((uintptr_t)x % 16 == 0 && x_row_stride % 4 == 0 && K % QK8 == 0) {
+        // one launch: grouping and quantization
+        const int nq_per_row = (int)((L.Kp + QUANT_VALS - 1) / QUANT_VALS);
+        const int64_t nwg = n_group + L.nrows_x * nq_per_row;
+        if (nwg > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+        hipLaunchKernelGGL(mmid_prepare, dim3((unsigned)nwg), dim3(PREP_THREADS), 0, s, ids, ids_stride, n_tokens,
+                           n_ids, (int)n_as, ne11, bn, n_group, col_src, col_dst, tiles, ntiles, dst,
+                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, nq_per_row, qs, (uint32_t *)ds);
+    } else {
+        if (int e = hip_qmm_quantize_q8_1_planar(x, K, L.nrows_x, x_row_stride, qs, ds, stream)) return e;
+        hipLaunchKernelGGL(mmid_prepare, dim3((unsigned)n_group), dim3(PREP_THREADS), 0, s, ids, ids_stride, n_tokens,
+                           n_ids, (int)n_as, ne11, bn, n_group, col_src, col_dst, tiles, ntiles, dst,
+                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, 1, qs, (uint32_t *)ds);
+    }
     if (int e = (int)hipGetLastError()) return e;
     return hip_qmm_mmq_grouped(type, w, K, nrows, row_stride, expert_stride, qs, ds, dst, dst_row_stride, bn,
-                               L.max_tiles, tiles, ntiles, eoff, col_src, col_dst, stream);
+                               L.max_tiles, tiles, ntiles, col_src, col_dst, stream);
 }

@@ -41,8 +41,8 @@ using namespace qmm;
 // mmq_q4k_dma.hip: the Q4_K kernel fed by direct global->LDS loads
 int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
-                       const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s);
+                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
+                       const int32_t *col_dst, float *partial, hipStream_t s);
 // mmq_few.hip: the Q4_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
@@ -365,8 +365,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
     int64_t dst_col_stride,
     // expert-grouped mode (tiles != nullptr): column tile table and gather/scatter maps
-    const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles, const int32_t *__restrict__ expert_off,
-    const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst,
+    const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles, const int32_t *__restrict__ col_src,
+    const int32_t *__restrict__ col_dst,
     // split-K (gridDim.z > 1): this workgroup's share of the K-steps goes to
     // partial[z][col][row] instead of dst
     float *__restrict__ partial) {
@@ -385,11 +385,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     const uint8_t *wexp = w;
     if (tiles) {
         if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup
-        const int e = tiles[2 * blockIdx.y], cs = tiles[2 * blockIdx.y + 1];
-        wexp = w + (int64_t)e * expert_stride;
-        col0 = cs;
-        const int64_t ce = expert_off[e + 1];
-        col_end = ce < col0 + BN ? ce : col0 + BN;
+        const int4 t = *reinterpret_cast<const int4 *>(tiles + 4 * blockIdx.y);  // {expert, col_low, col_high, -}
+        wexp = w + (int64_t)t.x * expert_stride;
+        col0 = t.y;
+        col_end = t.z;
     }
 
     // wave -> sub-tile: TI x TJ MFMA tiles of 32x32 at (wr, wc)
@@ -663,8 +662,8 @@ int launch_reduce(const float *partial, int split, int64_t nrows, int64_t ncols,
 template <int TYPE, int BN>
 int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride, const int8_t *yqs,
            const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy, const int32_t *tiles,
-           const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src, const int32_t *col_dst,
-           int split, float *partial, hipStream_t s) {
+           const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst, int split, float *partial,
+           hipStream_t s) {
     const int64_t gx = (nrows + BM - 1) / BM;
     if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64) return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)split);
@@ -672,13 +671,13 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
     // global->LDS loads; the weight rows are checked by check_weights)
     if (TYPE == TYPE_Q4_K && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
         if (int e = mmq_q4k_dma_launch(BN, w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst,
-                                       dst_col_stride, grid, tiles, n_tiles, expert_off, col_src, col_dst,
+                                       dst_col_stride, grid, tiles, n_tiles, col_src, col_dst,
                                        split > 1 ? partial : nullptr, s))
             return e;
     } else {
         hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,
                            row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols, dst, dst_col_stride, tiles,
-                           n_tiles, expert_off, col_src, col_dst, split > 1 ? partial : nullptr);
+                           n_tiles, col_src, col_dst, split > 1 ? partial : nullptr);
         if (int e = (int)hipGetLastError()) return e;
     }
     return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
@@ -687,14 +686,14 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
 template <int TYPE>
 int launch_bn(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
               const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy,
-              const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
-              const int32_t *col_dst, int split, float *partial, hipStream_t s) {
+              const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst,
+              int split, float *partial, hipStream_t s) {
     // A 128-column tile needs more than the 256 registers per lane that two
     // workgroups per CU leave (its two accumulator sets alone take 128), so
     // tiles stop at 64 columns.
     if (bn == 32)
-        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, split, partial, s);
-    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, expert_off, col_src, col_dst, split, partial, s);
+        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, s);
+    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, s);
 }
 
 int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
@@ -785,12 +784,12 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
         return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
     }
     switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
     }
 }
 
@@ -800,20 +799,20 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
 extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                    int64_t expert_stride, const int8_t *y_qs, const void *y_ds, float *dst,
                                    int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
-                                   const int32_t *n_tiles, const int32_t *expert_off, const int32_t *col_src,
-                                   const int32_t *col_dst, void *stream) {
-    if (!w || !y_qs || !y_ds || !dst || !tiles || !n_tiles || !expert_off || !col_src || !col_dst || K <= 0 ||
-        nrows <= 0 || dst_row_stride < nrows || max_tiles < 1)
+                                   const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst,
+                                   void *stream) {
+    if (!w || !y_qs || !y_ds || !dst || !tiles || !n_tiles || !col_src || !col_dst || K <= 0 ||
+        nrows <= 0 || dst_row_stride < nrows || max_tiles < 1 || (uintptr_t)tiles % 16 != 0)
         return (int)hipErrorInvalidValue;
     if (K % BK != 0 || K > (1 << 30) || (bn != 32 && bn != 64)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
     hipStream_t s = (hipStream_t)stream;
     switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
-    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, expert_off, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
+    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
+    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
+    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
     }
 }

@@ -54,13 +54,31 @@ __device__ __forceinline__ void wait_vmem() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
 }
 
+// One lane's 16 outputs of a 32x32 MFMA tile (column fixed, rows r0 + 8q +
+// 0..3 for q = 0..3, r0 a multiple of 4) into the column at o: four 16-byte
+// stores when the column is 16-byte aligned and all rows are below nrows,
+// else one store per row below nrows.
+__device__ __forceinline__ void store_tile_column(float *o, int64_t r0, int64_t nrows, const v16f &a) {
+    if (((uintptr_t)(o + r0) & 15) == 0 && r0 + 27 < nrows) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4 *>(o + r0 + 8 * q) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+            if (r < nrows) o[r] = a[v];
+        }
+    }
+}
+
 template <int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
     const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
     int64_t dst_col_stride, const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles,
-    const int32_t *__restrict__ expert_off, const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst,
-    float *__restrict__ partial, int gx, int gy, int gz) {
+    const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst, float *__restrict__ partial, int gx,
+    int gy, int gz) {
     constexpr int TJ = BN / 32;
     constexpr int NQB = BN / 4;    // 1 KiB transfers of B int8 per step
     constexpr int NQD = BN / 32;   // 1 KiB transfers of B headers per step
@@ -97,26 +115,26 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
         I.col_end = (int)ncols;
         I.wexp = w;
         if constexpr (GROUPED) {
-            const int e = tiles[2 * by], cs = tiles[2 * by + 1];
-            I.wexp = w + (int64_t)e * expert_stride;
-            I.col0 = cs;
-            const int ce = expert_off[e + 1];
-            I.col_end = ce < I.col0 + BN ? ce : I.col0 + BN;
+            const int4 t = *reinterpret_cast<const int4 *>(tiles + 4 * by);  // {expert, col_low, col_high, -}
+            I.wexp = w + (int64_t)t.x * expert_stride;
+            I.col0 = t.y;
+            I.col_end = t.z;
         }
         return I;
     };
-    auto item = [&](int it) { return item_xyz(it % gx, (it / gx) % gy_live, it / (gx * gy_live)); };
 
     // per-lane sources of this wave's transfers for one item (fixed over its K-steps)
     const uint8_t *a_src[(18 + 3) / 4];
     const int8_t *b_src[(NQB + 3) / 4];
     const uint32_t *d_src = yds;
-    auto set_sources = [&](const Item &I) {
-        auto src_col = [&](int n) -> int64_t {  // activation row of tile column n
-            int64_t cc = (int64_t)I.col0 + n;
-            if (cc >= I.col_end) cc = I.col0;
-            return GROUPED ? (int64_t)col_src[cc] : cc;
-        };
+    // tile column whose activations lane `lane` moves in B transfer i, and in
+    // the header transfer (waves < NQD)
+    auto b_col = [&](int i) {
+        const int q = wave + 4 * i;
+        return ((q < NQB ? q : 0) * 1024 + lane * 16) >> 8;
+    };
+    const int d_col = (wave * 1024 + lane * 16) >> 5;
+    auto set_a = [&](const Item &I) {
 #pragma unroll
         for (int i = 0; i < (18 + 3) / 4; ++i) {
             const int q = wave + 4 * i;
@@ -125,17 +143,38 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             const int64_t grow = (int64_t)I.row0 + r < nrows ? (int64_t)I.row0 + r : nrows - 1;
             a_src[i] = I.wexp + grow * row_stride + ch * 16;
         }
+    };
+    // activation rows (planar Q8_1 columns) of the lane's B and header transfers
+    struct Rows {
+        int b[(NQB + 3) / 4];
+        int d;
+    };
+    auto set_b = [&](const Rows &R) {
 #pragma unroll
         for (int i = 0; i < (NQB + 3) / 4; ++i) {
             const int q = wave + 4 * i;
             const int pos = (q < NQB ? q : 0) * 1024 + lane * 16;
             const int n = pos >> 8, p = (pos >> 4) & 15;
-            b_src[i] = yqs + src_col(n) * Kp + 16 * (p ^ (n & 15));
+            b_src[i] = yqs + (int64_t)R.b[i] * Kp + 16 * (p ^ (n & 15));
         }
-        if (wave < NQD) {
-            const int pos = wave * 1024 + lane * 16;
-            d_src = yds + src_col(pos >> 5) * (Kp / QK8) + 4 * ((pos >> 4) & 1);
-        }
+        if (wave < NQD) d_src = yds + (int64_t)R.d * (Kp / QK8) + 4 * ((wave * 1024 + lane * 16) >> 4 & 1);
+    };
+    // the rows of an item's columns; past col_end a tile column repeats its
+    // first column (loaded, never stored)
+    auto rows_of = [&](int col0, int col_end) {
+        auto src = [&](int n) -> int {
+            const int cc = col0 + n < col_end ? col0 + n : col0;
+            return GROUPED ? col_src[cc] : cc;
+        };
+        Rows R;
+#pragma unroll
+        for (int i = 0; i < (NQB + 3) / 4; ++i) R.b[i] = src(b_col(i));
+        R.d = wave < NQD ? src(d_col) : 0;
+        return R;
+    };
+    auto set_sources = [&](const Item &I) {
+        set_a(I);
+        set_b(rows_of(I.col0, I.col_end));
     };
 
     auto dma = [&](int64_t kb, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
@@ -307,31 +346,65 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             float *o;
             if constexpr (GROUPED) o = dst + (int64_t)col_dst[c] * dst_col_stride;
             else o = partial ? partial + ((int64_t)C.z * ncols + c) * nrows : dst + c * dst_col_stride;
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int64_t r = (int64_t)C.row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
-                if (r < nrows) o[r] = acc[j][v];
-            }
+            store_tile_column(o, (int64_t)C.row0 + wr + 4 * lh, nrows, acc[j]);
         }
     } else {
-    int it_c = (int)blockIdx.x;
+        // Persistent workgroups walk items blockIdx.x, +G, +2G, ... (G =
+        // gridDim.x; one K part).  The transfer cursor (item it_n, step kb_n)
+        // runs one step ahead of the contraction (item it_c, step kb_c) and
+        // crosses into the next item while the current one finishes, so a
+        // tile's first transfer is not exposed.  The tables an item needs
+        // are fetched ahead, so no item boundary waits on a dependent load:
+        // the tile entries of the items two ahead of the transfer cursor and
+        // one ahead of the contraction, the gather rows (col_src) of the item
+        // one ahead of the transfer cursor, and the scatter rows (col_dst) of
+        // the contraction's item as it starts.
+        const int G = (int)gridDim.x;
+        int it_c = (int)blockIdx.x;
         if (it_c >= nitems) return;  // uniform per workgroup
-        // The transfer cursor (item it_n, step kb_n) runs one step ahead of the
-        // contraction (item it_c, step kb_c) and crosses into the next item while
-        // the current one finishes, so a tile's first transfer is not exposed.
-        Item C = item(it_c);
+        auto tile_of = [&](int it) { return *reinterpret_cast<const int4 *>(tiles + 4 * ((it / gx) % gy_live)); };
+        auto item_of = [&](int it, const int4 &t) {
+            Item I;
+            I.row0 = (it % gx) * BM;
+            I.z = 0;
+            I.kb0 = 0;
+            I.kb1 = nkb_all;
+            I.wexp = w + (int64_t)t.x * expert_stride;
+            I.col0 = t.y;
+            I.col_end = t.z;
+            return I;
+        };
+        int drow[TJ];  // scatter rows of the contraction item's lane columns
+        auto load_drows = [&](const Item &I) {
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const int c = I.col0 + 32 * j + li;
+                drow[j] = col_dst[c < I.col_end ? c : I.col0];
+            }
+        };
+        const int4 t0 = tile_of(it_c);
+        Item C = item_of(it_c, t0);
+        load_drows(C);
+        set_a(C);
+        set_b(rows_of(t0.y, t0.z));
+        int4 tc1 = it_c + G < nitems ? tile_of(it_c + G) : t0;  // contraction: next item's tile
+        int4 tn1 = tc1, tn2 = t0;                                 // transfer: tiles one and two ahead
+        Rows rn1 = {};                                            // transfer: rows one ahead
+        if (it_c + G < nitems) rn1 = rows_of(tn1.y, tn1.z);
+        if (it_c + 2 * G < nitems) tn2 = tile_of(it_c + 2 * G);
         int it_n = it_c;
-        int kb_n = C.kb0, kb1_n = C.kb1, kb_c = C.kb0;
+        int kb_n = 0, kb_c = 0;
         bool dma_live = true;
-        set_sources(C);
         auto advance = [&]() {
-            if (++kb_n < kb1_n) return;
-            it_n += (int)gridDim.x;
+            if (++kb_n < nkb_all) return;
+            it_n += G;
             if (it_n < nitems) {
-                const Item N = item(it_n);
-                kb_n = N.kb0;
-                kb1_n = N.kb1;
-                set_sources(N);
+                kb_n = 0;
+                set_a(item_of(it_n, tn1));
+                set_b(rn1);
+                tn1 = tn2;
+                if (it_n + G < nitems) rn1 = rows_of(tn1.y, tn1.z);
+                if (it_n + 2 * G < nitems) tn2 = tile_of(it_n + 2 * G);
             } else {
                 dma_live = false;
             }
@@ -341,26 +414,24 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             for (int j = 0; j < TJ; ++j) {
                 const int64_t c = (int64_t)C.col0 + 32 * j + li;
                 if (c >= C.col_end) continue;
-                float *o = dst + (int64_t)col_dst[c] * dst_col_stride;
-#pragma unroll
-                for (int v = 0; v < 16; ++v) {
-                    const int64_t r = (int64_t)C.row0 + wr + 8 * (v >> 2) + 4 * lh + (v & 3);
-                    if (r < nrows) o[r] = acc[j][v];
-                }
+                store_tile_column(dst + (int64_t)drow[j] * dst_col_stride, (int64_t)C.row0 + wr + 4 * lh, nrows,
+                                  acc[j]);
             }
         };
         // after a step's contraction: at an item's last step store it and move on
         auto finish_step = [&]() -> bool {
-            if (++kb_c < C.kb1) return true;
+            if (++kb_c < nkb_all) return true;
             store();
 #pragma unroll
             for (int j = 0; j < TJ; ++j)
 #pragma unroll
                 for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
-            it_c += (int)gridDim.x;
+            it_c += G;
             if (it_c >= nitems) return false;
-            C = item(it_c);
-            kb_c = C.kb0;
+            C = item_of(it_c, tc1);
+            kb_c = 0;
+            load_drows(C);
+            if (it_c + G < nitems) tc1 = tile_of(it_c + G);
             return true;
         };
 
@@ -398,8 +469,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
 // budget); otherwise each workgroup takes one tile.
 int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *expert_off,
-                       const int32_t *col_src, const int32_t *col_dst, float *partial, hipStream_t s) {
+                       dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
+                       const int32_t *col_dst, float *partial, hipStream_t s) {
     // workgroups resident at once: 2 per CU of the current device (queried per
     // call: a process may drive GPUs of different sizes; the query is a host
     // attribute read)
@@ -420,8 +491,8 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
     hipLaunchKernelGGL((mmq_q4k_dma_kernel<BNV, GR>), GR && BNV == 32 ? pgrid : grid, dim3(NTHREADS), 0, s, wb, K,   \
                        nrows,                                                                                          \
                        row_stride,                                                                                     \
-                       expert_stride, yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, expert_off, col_src,       \
-                       col_dst, partial, gx, gy, gz)
+                       expert_stride, yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, col_src, col_dst,         \
+                       partial, gx, gy, gz)
     if (tiles) {
         if (bn == 32) MMQ_DMA_LAUNCH(32, true);
         else MMQ_DMA_LAUNCH(64, true);

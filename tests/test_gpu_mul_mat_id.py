@@ -165,3 +165,40 @@ def test_mul_mat_id_nine_tokens_take_the_grouped_path():
     ids = np.random.default_rng(3).integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
     x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
     _check("Q4_K", n_as, nrows, K, x, ids)
+
+
+def test_mul_mat_id_grouping_chunks_expert_loops_and_unaligned_activations():
+    """Grouping past one chunk of pairs (5600 pairs) and past one expert per
+    grouping workgroup (300 experts), with out-of-range ids; the one-launch
+    form (aligned activations) and the two-launch form (a row stride that is
+    not a multiple of 4 floats) give identical outputs, and both pass the
+    CPU and f64 gates."""
+    import ctypes
+    import ggml_hip as G
+    n_as, nrows, K, n_tokens, n_ids = 300, 64, 256, 700, 8
+    rng = np.random.default_rng(11)
+    ids = rng.integers(-1, n_as + 2, size=(n_tokens, n_ids)).astype(np.int32)
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    t, wq, got = _run("Q4_K", n_as, nrows, K, x, ids)
+    bad = (ids < 0) | (ids >= n_as)
+    assert np.all(got[bad] == 0.0)
+    ok_ids = np.where(bad, -1, ids).astype(np.int32)
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x, ok_ids, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    y = G.quantize_q8_1(torch.from_numpy(x.reshape(-1, K)).cuda(), K).cpu().numpy()
+    ideal = mul_mat_id_f64(t, wq, nrows, K, y, 1, ok_ids)
+    assert max_err_scaled(got, ideal) < F64_TOL
+
+    stride = K + 1
+    xs = torch.zeros((n_tokens, stride), dtype=torch.float32, device="cuda")
+    xs[:, :K] = torch.from_numpy(x.reshape(n_tokens, K)).cuda()
+    w_d, ids_d = torch.from_numpy(wq).cuda(), torch.from_numpy(ids).cuda()
+    out = torch.full((n_tokens, n_ids, nrows), float("nan"), device="cuda")
+    need = int(G.lib().hip_qmm_mul_mat_id_workspace_size(t, K, n_as, 1, n_tokens, n_ids))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    p = lambda a: ctypes.c_void_p(a.data_ptr())  # noqa: E731
+    rc = G.lib().hip_qmm_mul_mat_id(t, p(w_d), K, nrows, w_d.stride(1), w_d.stride(0), n_as, p(xs), 1, n_tokens,
+                                    stride, p(ids_d), n_ids, n_ids, p(out), nrows, p(ws), need,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    np.testing.assert_array_equal(out.cpu().numpy(), got)
