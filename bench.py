@@ -50,6 +50,7 @@ INFINITY_CACHE = 256 << 20
 NMSE_GATE = 5e-4
 
 M, K = 14336, 4096             # headline weight: Llama-3-8B ffn_gate/up
+HEADLINE = (M, K)
 T_MMQ = 512
 CPU_SAMPLE_S = 10.0            # CPU work per baseline leg
 
@@ -486,6 +487,29 @@ def run_suite(name, torch, G, dev, reps):
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4)})
             del wu, wg
             torch.cuda.empty_cache()
+    elif name == "floor":
+        # The headline's weight stream against the memory floor: the same
+        # rotated copies of the 14336x4096 Q4_K weight read by (1) the
+        # streaming-read probe (the fastest plain read measured here), (2) the
+        # GEMV on an already quantized column, (3) the headline op (GEMV with
+        # the column's quantization fused in).  Bytes = the weight bytes.
+        hm, hk = HEADLINE
+        ws, wb = copies("Q4_K", hm, hk)
+        x = torch.randn((1, hk), generator=xg, dtype=torch.float32).to(dev)
+        qs, ds = G.quantize_q8_1_planar(x)
+        out = torch.empty((1, hm), dtype=torch.float32, device=dev)
+        sink = torch.empty(int(G.lib().hip_qmm_probe_sink_words(wb)), dtype=torch.int32, device=dev)
+        n = len(ws) * reps
+        cases = (("stream read probe", lambda i: G.probe_stream_read(ws[i % len(ws)], sink=sink)),
+                 ("gemv on a quantized column", lambda i: G.mul_mat_vec("Q4_K", ws[i % len(ws)], hk, qs, ds, out=out)),
+                 ("op: gemv with fused quantization", lambda i: G.mul_mat("Q4_K", ws[i % len(ws)], x, out=out)))
+        for kern, fn in cases:
+            ms = event_time_batch(torch, fn, n)
+            emit({"suite": name, "kernel": kern, "type": "Q4_K", "shape": f"{hm}x{hk}", "T": 1, "bytes": wb,
+                  "weight_copies": len(ws), "us": round(ms * 1e3, 3), "GB/s": round(wb / ms / 1e6, 1),
+                  "hbm_frac": round(wb / ms / 1e6 / HBM_PEAK_GBS, 4)})
+        del ws
+        torch.cuda.empty_cache()
     else:
         raise SystemExit(f"unknown suite {name}")
 
@@ -499,7 +523,7 @@ def main():
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "few"],
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "few", "floor"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()

@@ -310,6 +310,16 @@ int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_
 int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                        const int8_t *y_qs, int64_t ncols, int32_t *out, void *stream);
 
+/*
+ * Measurement aid, no counterpart in the reference: a plain streaming read of
+ * `bytes` (a multiple of 16, src 16-byte aligned) with the access shape that
+ * reads HBM fastest here, the floor the decode GEMV's weight stream is
+ * compared against.  The loaded words are XOR-folded into
+ * hip_qmm_probe_sink_words(bytes) words of `sink` so the loads stay.
+ */
+size_t hip_qmm_probe_sink_words(size_t bytes);
+int hip_qmm_probe_stream_read(const void *src, size_t bytes, uint32_t *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif
