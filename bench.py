@@ -441,6 +441,28 @@ def run_suite(name, torch, G, dev, reps):
                       "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": 1, "top_k": k,
                       "us": round(msf * 1e3, 3), "GB/s": round(algf / msf / 1e6, 1),
                       "unfused_3_launches_us": round(msu * 1e3, 3)})
+                # with a shared expert of the same shape in the same launch,
+                # against the routed launch plus the shared expert's own one
+                sus = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+                sgs = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+                sh_out = torch.empty((1, M), dtype=torch.float32, device=dev)
+                fs = lambda i: G.mul_mat_id_vec_fused_shared("Q4_K", ws[i % n], gs[i % n], x1, ids1,  # noqa: E731
+                                                             sus[i % n], sgs[i % n], glu="SWIGLU", out=out1,
+                                                             shared_out=sh_out)
+
+                def two(i):
+                    fz(i)
+                    G.mul_mat_vec_fused("Q4_K", sus[i % n], Kx, x1.view(1, Kx), w_gate=sgs[i % n], glu="SWIGLU",
+                                        out=sh_out)
+
+                mss = event_time_batch(torch, fs, n * reps * 4)
+                ms2 = event_time_batch(torch, two, n * reps * 4)
+                algs = algf + 2 * M * row_bytes("Q4_K", Kx) + M * 4
+                emit({"suite": name, "kernel": "mul_mat_id decode gate+up+swiglu fused with a shared expert",
+                      "type": "Q4_K", "shape": f"{n_as}x{M}x{Kx} + shared {M}x{Kx}", "label": label, "tokens": 1,
+                      "top_k": k, "us": round(mss * 1e3, 3), "GB/s": round(algs / mss / 1e6, 1),
+                      "routed_then_shared_2_launches_us": round(ms2 * 1e3, 3)})
+                del sus, sgs
                 del gs
             del ws
             torch.cuda.empty_cache()

@@ -208,6 +208,14 @@ struct ggml_backend_buffer {
     enum ggml_backend_buffer_usage usage;
 };
 
+/* What the scheduler hands graph_optimize (src/ggml/backend_sched.zig:997-1000,
+ * backend.zig:1236): add_alloc_dep(user_data, tensor, until) keeps `tensor`
+ * allocated until `until` has run. */
+struct ggml_backend_graph_optimize_params {
+    void (*add_alloc_dep)(void *user_data, struct ggml_tensor *tensor, struct ggml_tensor *until);
+    void *user_data;
+};
+
 struct ggml_backend_i {
     const char *(*get_name)(ggml_backend_t backend);
     void (*free)(ggml_backend_t backend);
@@ -229,7 +237,8 @@ struct ggml_backend_i {
     enum ggml_status (*graph_compute)(ggml_backend_t backend, struct ggml_cgraph *cgraph);
     void (*event_record)(ggml_backend_t backend, ggml_backend_event_t event);
     void (*event_wait)(ggml_backend_t backend, ggml_backend_event_t event);
-    void (*graph_optimize)(ggml_backend_t backend, struct ggml_cgraph *cgraph);
+    void (*graph_optimize)(ggml_backend_t backend, struct ggml_cgraph *cgraph,
+                           struct ggml_backend_graph_optimize_params *params);
 };
 
 struct ggml_backend {

@@ -178,6 +178,24 @@ int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void *w_gate, in
                                  float *dst, int64_t dst_row_stride, void *stream);
 
 /*
+ * hip_qmm_mul_mat_id_vec_fused (gated, one activation row per token, ne11 = 1)
+ * with a shared expert in the same launch: the reference's shared_up /
+ * shared_gate / shared_dst fusion arguments (src/ggml/cuda/common.zig:1448-1459,
+ * mmvq.zig:300-320, 574-590; the graph pattern of fusion.zig:930-955).
+ * Besides the routed rows, token t's column x + t*x_row_stride goes through
+ * the shared expert: shared_dst + t*shared_dst_row_stride =
+ * glu(glu_op, shared_gate . q8_1(x_t), shared_up . q8_1(x_t)).  The shared
+ * weights have the experts' type, row count, K and row_stride (block-aligned);
+ * n_tokens*(n_ids + 1) at most 65535.
+ */
+int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                        int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
+                                        int64_t n_tokens, int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
+                                        int64_t ids_stride, int glu_op, float glu_alpha, float glu_limit, float *dst,
+                                        int64_t dst_row_stride, const void *shared_up, const void *shared_gate,
+                                        float *shared_dst, int64_t shared_dst_row_stride, void *stream);
+
+/*
  * Standalone GLU over rows of f32 (ggml_compute_forward_glu,
  * src/ggml/cpu/ops/activation.zig:594-608, per element as above):
  * dst[r*dst_stride + i] = glu(op, gate[r*gate_stride + i], up[r*up_stride + i])

@@ -15,6 +15,7 @@
 #include <cctype>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <new>
@@ -759,6 +760,7 @@ bool gate_up_id_fusable(const ggml_tensor *up, const ggml_tensor *gate, const gg
         if (wu->nb[i] != wg->nb[i]) return false;
     if (up->src[1] != gate->src[1] || up->src[2] != gate->src[2] || !same_shape(glu, up)) return false;
     if (glu->nb[2] != (size_t)glu->ne[1] * glu->nb[1] || glu->nb[1] % 4) return false;
+    if (x->nb[2] != (size_t)x->ne[1] * x->nb[1]) return false;  // row (t, i11) at (t * ne11 + i11) * nb1
     const int64_t K = wu->ne[0], n_tokens = x->ne[2];
     const size_t walign = weight_align(wu->type);
     return n_tokens <= 8 && n_tokens * glu->ne[1] <= 65535 && K % 32 == 0 && K <= 32768 &&
@@ -782,12 +784,116 @@ bool launch_fused_id(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *
     return true;
 }
 
+// ---- shared expert: a routed {MUL_MAT_ID, MUL_MAT_ID, GLU} and a shared
+// expert's {MUL_MAT, MUL_MAT, GLU} on the same tokens in one launch (the
+// reference's shared_up / shared_gate / shared_dst fusion,
+// src/ggml/cuda/fusion.zig:930-955, mmvq.zig:300-320, 574-590).
+
+// Nodes idx[0..n) but the outputs are read only inside the set, are not graph
+// outputs and are not views (ggml_can_fuse_subgraph_ext, src/ggml/graph.zig:1207-1250).
+bool set_is_closed(const ggml_cgraph *g, const int *idx, int n, const ggml_tensor *out_a, const ggml_tensor *out_b) {
+    for (int a = 0; a < n; ++a) {
+        const ggml_tensor *t = g->nodes[idx[a]];
+        if (t == out_a || t == out_b) continue;
+        if ((t->flags & GGML_TENSOR_FLAG_OUTPUT) || t->view_src) return false;
+        int uses = 0;
+        for (int b = 0; b < n; ++b)
+            for (int k = 0; k < GGML_MAX_SRC; ++k) uses += g->nodes[idx[b]]->src[k] == t;
+        if (use_count(g, t) != uses) return false;
+    }
+    return true;
+}
+
+// Whether {a, b} are the nodes k and k + 1 in either order.
+bool node_pair(const ggml_cgraph *g, int k, const ggml_tensor *a, const ggml_tensor *b) {
+    return (a == g->nodes[k] && b == g->nodes[k + 1]) || (b == g->nodes[k] && a == g->nodes[k + 1]);
+}
+
+// A split, non-swapped f32 GLU of an op the fused kernels apply.
+bool fusable_glu(const ggml_tensor *glu) {
+    const int op = glu->op_params[0];
+    return (op == HIP_QMM_GLU_GEGLU || op == HIP_QMM_GLU_SWIGLU || op == HIP_QMM_GLU_SWIGLU_OAI ||
+            op == HIP_QMM_GLU_SWIGLU_CLAMP) &&
+           glu->op_params[1] == 0 && glu->src[1] && glu->type == GGML_TYPE_F32 && glu->nb[0] == 4;
+}
+
+bool same_weights(const ggml_tensor *a, const ggml_tensor *b) {
+    if (a->type != b->type || !same_shape(a, b)) return false;
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (a->nb[i] != b->nb[i]) return false;
+    return true;
+}
+
+// ggml_cuda_match_shared_expert (src/ggml/cuda/fusion.zig:853-905): the
+// routed experts' gate / up / GLU at r and a shared expert's at s, checks
+// that do not depend on the batch size (graph_optimize gives every batch the
+// same order; try_fuse checks the batch).
+bool match_shared_expert(const ggml_cgraph *g, int r, int s) {
+    if (r + 2 >= g->n_nodes || s + 2 >= g->n_nodes || s < r + 3) return false;
+    const int idx[6] = {r, r + 1, r + 2, s, s + 1, s + 2};
+    const int ops[6] = {GGML_OP_MUL_MAT_ID, GGML_OP_MUL_MAT_ID, GGML_OP_GLU, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT, GGML_OP_GLU};
+    for (int k = 0; k < 6; ++k)
+        if (g->nodes[idx[k]]->op != ops[k] || !ggml_backend_hip_op_supported(g->nodes[idx[k]])) return false;
+    const ggml_tensor *routed = g->nodes[r + 2], *shared = g->nodes[s + 2];
+    if (!set_is_closed(g, idx, 6, routed, shared)) return false;
+    const ggml_tensor *gate = routed->src[0], *up = routed->src[1];
+    const ggml_tensor *sgate = shared->src[0], *sup = shared->src[1];
+    if (!node_pair(g, r, gate, up) || !node_pair(g, s, sgate, sup) || !fusable_glu(routed) || !fusable_glu(shared))
+        return false;
+    if (routed->op_params[0] != shared->op_params[0] || routed->op_params[2] != shared->op_params[2] ||
+        routed->op_params[3] != shared->op_params[3])
+        return false;
+    if (!same_weights(up->src[0], gate->src[0]) || up->src[1] != gate->src[1] || up->src[2] != gate->src[2] ||
+        !same_weights(sup->src[0], sgate->src[0]) || sup->src[1] != sgate->src[1])
+        return false;
+    const ggml_tensor *input = up->src[1], *w = up->src[0], *sw = sup->src[0], *sx = sup->src[1];
+    if (input->op != GGML_OP_RESHAPE || input->src[0] != sx || input->ne[1] != 1 || input->ne[3] != 1 ||
+        !contiguous(input) || !contiguous(sx) || sx->ne[2] != 1 || sx->ne[3] != 1)
+        return false;
+    if (w->type != sw->type || w->ne[0] != sw->ne[0] || w->ne[1] != sw->ne[1] || w->nb[1] != sw->nb[1] ||
+        w->ne[3] != 1 || sw->ne[2] != 1 || sw->ne[3] != 1 || !contiguous(sw) || !contiguous(sgate->src[0]))
+        return false;
+    if (!contiguous(routed) || !contiguous(shared) || sw->op != GGML_OP_NONE || sgate->src[0]->op != GGML_OP_NONE)
+        return false;
+    return true;
+}
+
+// The routed and shared lanes at i .. i+5 in one launch, when the batch fits
+// the fused ids kernel; false leaves them to run unfused.
+bool launch_shared_expert(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
+    const ggml_tensor *routed = g->nodes[i + 2], *shared = g->nodes[i + 5];
+    const ggml_tensor *gate = routed->src[0], *up = routed->src[1], *sgate = shared->src[0], *sup = shared->src[1];
+    if (!gate_up_id_fusable(up, gate, routed)) return false;
+    const ggml_tensor *w = up->src[0], *x = up->src[1], *ids = up->src[2];
+    const size_t walign = weight_align(w->type);
+    const int64_t K = w->ne[0], M = w->ne[1], n_tokens = x->ne[2];
+    if ((uintptr_t)sup->src[0]->data % walign || (uintptr_t)sgate->src[0]->data % walign) return false;
+    if (shared->ne[0] != M || shared->ne[1] != n_tokens || shared->nb[1] % 4 ||
+        n_tokens * (ids->ne[0] + 1) > 65535)
+        return false;
+    const size_t ob = nbytes(routed), sb = nbytes(shared);
+    if (overlaps(routed->data, ob, x->data, nbytes(x)) || overlaps(routed->data, ob, ids->data, nbytes(ids)) ||
+        overlaps(shared->data, sb, x->data, nbytes(x)) || overlaps(shared->data, sb, ids->data, nbytes(ids)) ||
+        overlaps(routed->data, ob, shared->data, sb))
+        return false;
+    const int rc = hip_qmm_mul_mat_id_vec_fused_shared(
+        w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
+        static_cast<const float *>(x->data), n_tokens, (int64_t)(x->nb[2] / 4), static_cast<const int32_t *>(ids->data),
+        ids->ne[0], (int64_t)(ids->nb[1] / 4), routed->op_params[0], op_param_f32(routed, 2),
+        op_param_f32(routed, 3), static_cast<float *>(routed->data), (int64_t)(routed->nb[1] / 4),
+        sup->src[0]->data, sgate->src[0]->data, static_cast<float *>(shared->data), (int64_t)(shared->nb[1] / 4),
+        ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_id_vec_fused_shared", routed);
+    return true;
+}
+
 // Nodes consumed by a fused launch at node i (0: none); *ok false on a failed launch.
 int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
     if (fusion_disabled()) return 0;
     auto node = [&](int k) { return k < g->n_nodes ? g->nodes[k] : nullptr; };
     auto is = [&](int k, int op) { return node(k) && node(k)->op == op && ggml_backend_hip_op_supported(node(k)); };
     if (g->nodes[i]->op == GGML_OP_MUL_MAT_ID) {
+        if (match_shared_expert(g, i, i + 3) && launch_shared_expert(ctx, g, i, ok)) return 6;
         if (!is(i + 1, GGML_OP_MUL_MAT_ID) || !is(i + 2, GGML_OP_GLU)) return 0;
         const ggml_tensor *glu = node(i + 2);
         const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
@@ -861,6 +967,32 @@ ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
     return GGML_STATUS_SUCCESS;
 }
 
+// The reference's graph_optimize grouping for the shared expert
+// (src/ggml/cuda/graph.zig:826-848): after each routed gate / up / GLU, the
+// first matching shared-expert triple before the next routed pair is moved
+// up to follow it (it reads only the layer input and its weights, so the
+// order stays topological), and the routed input and ids are kept allocated
+// until the shared GLU has run, so the fused launch's operands cannot alias
+// its second output.  Nothing moves with fusion disabled.
+void be_graph_optimize(ggml_backend_t, ggml_cgraph *g, ggml_backend_graph_optimize_params *params) {
+    if (fusion_disabled() || !g) return;
+    for (int r = 0; r + 5 < g->n_nodes; ++r) {
+        if (g->nodes[r]->op != GGML_OP_MUL_MAT_ID) continue;
+        for (int j = r + 3; j + 2 < g->n_nodes; ++j) {
+            if (g->nodes[j]->op == GGML_OP_MUL_MAT_ID && g->nodes[j + 1]->op == GGML_OP_MUL_MAT_ID) break;
+            if (g->nodes[j]->op != GGML_OP_MUL_MAT || !match_shared_expert(g, r, j)) continue;
+            std::rotate(g->nodes + r + 3, g->nodes + j, g->nodes + j + 3);
+            const ggml_tensor *up = g->nodes[r + 2]->src[1];
+            if (params && params->add_alloc_dep) {
+                params->add_alloc_dep(params->user_data, up->src[1], g->nodes[r + 5]);
+                params->add_alloc_dep(params->user_data, up->src[2], g->nodes[r + 5]);
+            }
+            r += 5;
+            break;
+        }
+    }
+}
+
 void be_event_record(ggml_backend_t be, ggml_backend_event_t ev) {
     HIP_CHECK(hipEventRecord(static_cast<hipEvent_t>(ev->context), be_ctx(be)->stream));
 }
@@ -889,7 +1021,7 @@ const ggml_backend_i backend_iface = {
     be_graph_compute,
     be_event_record,
     be_event_wait,
-    nullptr,
+    be_graph_optimize,
 };
 
 // ---------------------------------------------------------------- device vtable

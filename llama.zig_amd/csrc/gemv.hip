@@ -680,7 +680,10 @@ __global__ __launch_bounds__(256) void gemv_ks_kernel(
 // the pair's expert e = ids[t, s] selects the weights (w + e * expert_stride),
 // its column is x row t * ne11 + s % ne11, its result dst row t * n_ids + s.
 // An id outside [0, n_as) yields a zero row, as the CPU path's -1 does
-// (src/ggml/cpu/mulmat.zig:555-777).
+// (src/ggml/cpu/mulmat.zig:555-777).  A shared expert (the reference's
+// shared_up / shared_gate / shared_dst fusion arguments, mmvq.zig:300-320,
+// 574-590) is one more row of workgroups after the pairs: grid y = n_pairs +
+// t runs token t's column through the shared weights into shared_dst.
 constexpr int FX_MAXK = 32768;
 
 // Byte offset of the K-share partial sums in the fused GEMV's dynamic LDS:
@@ -691,6 +694,13 @@ struct FxIds {
     const int32_t *ids;
     int64_t ids_stride, x_row_stride, expert_stride, dst_row_stride;
     int n_ids, ne11, n_as, n_pairs;
+    // shared expert (gated): grid y rows n_pairs .. n_pairs + n_shared - 1
+    // are token t = y - n_pairs through shared_up / shared_gate, into
+    // shared_dst + t * shared_dst_row_stride
+    const uint8_t *shared_up, *shared_gate;
+    float *shared_dst;
+    int64_t shared_dst_row_stride;
+    int n_shared;
 };
 
 template <int TYPE, int FW, int R, bool GATE, bool IDS, int SEG, int KS>
@@ -702,12 +712,20 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
                                                              FxIds fi) {
     using F = Fmt<TYPE>;
     int expert = 0;
+    bool shared = false;  // uniform per workgroup
     if constexpr (IDS) {
         const int p = blockIdx.y;
-        const int t = p / fi.n_ids, slot = p - t * fi.n_ids;
-        x += (int64_t)(t * fi.ne11 + slot % fi.ne11) * fi.x_row_stride;
-        dst += (int64_t)p * fi.dst_row_stride;
-        expert = __builtin_amdgcn_readfirstlane(fi.ids[(int64_t)t * fi.ids_stride + slot]);
+        if (p < fi.n_pairs) {
+            const int t = p / fi.n_ids, slot = p - t * fi.n_ids;
+            x += (int64_t)(t * fi.ne11 + slot % fi.ne11) * fi.x_row_stride;
+            dst += (int64_t)p * fi.dst_row_stride;
+            expert = __builtin_amdgcn_readfirstlane(fi.ids[(int64_t)t * fi.ids_stride + slot]);
+        } else {
+            const int t = p - fi.n_pairs;
+            x += (int64_t)t * fi.ne11 * fi.x_row_stride;
+            dst = fi.shared_dst + (int64_t)t * fi.shared_dst_row_stride;
+            shared = true;
+        }
     }
     constexpr int NM = GATE ? 2 : 1;
     constexpr int NSEG = 64 / SEG;            // weight rows side by side in a wave
@@ -753,14 +771,19 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     }
     asm volatile("" ::: "memory");  // keep them ahead of the weight loads
     if constexpr (IDS) {
-        if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its barriers
+        if (shared) {
+            w = fi.shared_up;
+            if constexpr (GATE) wg = fi.shared_gate;
+        } else {
+            if (expert < 0 || expert >= fi.n_as) {  // uniform per workgroup, before its barriers
 #pragma unroll
-            for (int r = 0; r < R; ++r)
-                if (kh == 0 && sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
-            return;
+                for (int r = 0; r < R; ++r)
+                    if (kh == 0 && sl == SEG - 1 && row0 + r * NSEG + seg < nrows) dst[row0 + r * NSEG + seg] = 0.0f;
+                return;
+            }
+            w += (int64_t)expert * fi.expert_stride;
+            if constexpr (GATE) wg += (int64_t)expert * fi.expert_stride;
         }
-        w += (int64_t)expert * fi.expert_stride;
-        if constexpr (GATE) wg += (int64_t)expert * fi.expert_stride;
     }
     const uint8_t *rows[NM][R];
 #pragma unroll
@@ -1165,7 +1188,8 @@ void launch_fx(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrows, in
     const size_t lds = (size_t)K + (size_t)(K / QK8) * 4;
     if (fi)
         hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, true, SEG, 1>),
-                           dim3((unsigned)nblocks, (unsigned)fi->n_pairs), dim3(64 * FW), lds, s, w, wg, (int)K, nrows,
+                           dim3((unsigned)nblocks, (unsigned)(fi->n_pairs + fi->n_shared)), dim3(64 * FW), lds, s, w, wg,
+                           (int)K, nrows,
                            row_stride, x, bias, gbias, op, alpha, limit, dst, *fi);
     else
         hipLaunchKernelGGL((gemv_fx_kernel<TYPE, FW, R, GATE, false, SEG, 1>), dim3((unsigned)nblocks), dim3(64 * FW),
@@ -1374,22 +1398,65 @@ extern "C" int hip_qmm_mul_mat_vec_fused(int type, const void *w, const void *w_
                         nullptr, stream);
 }
 
+namespace {
+
+struct FxShared {
+    const void *up, *gate;
+    float *dst;
+    int64_t dst_row_stride;
+};
+
+int id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows, int64_t row_stride,
+                 int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
+                 int64_t x_row_stride, const int32_t *ids, int64_t n_ids, int64_t ids_stride, int glu_op,
+                 float glu_alpha, float glu_limit, float *dst, int64_t dst_row_stride, const FxShared *sh,
+                 void *stream) {
+    if (!ids || n_as <= 0 || n_as > 0x7FFFFFFF || n_tokens <= 0 || n_ids <= 0 || ids_stride < n_ids ||
+        (ne11 != 1 && ne11 != n_ids) || x_row_stride < K || x_row_stride % 4 || dst_row_stride < nrows)
+        return (int)hipErrorInvalidValue;
+    const int64_t n_shared = sh ? n_tokens : 0;
+    if (n_tokens * n_ids + n_shared > 65535 || n_tokens * ne11 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    const int64_t walign = block_align(type);
+    if (expert_stride < nrows * row_stride || expert_stride % walign || expert_stride > ((int64_t)1 << 40))
+        return (int)hipErrorInvalidValue;
+    if (sh && (!w_gate || !sh->up || !sh->gate || !sh->dst || ne11 != 1 || sh->dst_row_stride < nrows ||
+               (uintptr_t)sh->up % (uintptr_t)walign || (uintptr_t)sh->gate % (uintptr_t)walign))
+        return (int)hipErrorInvalidValue;
+    FxIds fi{ids, ids_stride, x_row_stride, expert_stride, dst_row_stride,
+             (int)n_ids, (int)ne11, (int)n_as, (int)(n_tokens * n_ids),
+             nullptr, nullptr, nullptr, 0, (int)n_shared};
+    if (sh) {
+        fi.shared_up = (const uint8_t *)sh->up;
+        fi.shared_gate = (const uint8_t *)sh->gate;
+        fi.shared_dst = sh->dst;
+        fi.shared_dst_row_stride = sh->dst_row_stride;
+    }
+    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op, glu_alpha, glu_limit, dst,
+                        &fi, stream);
+}
+
+}  // namespace
+
 extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
                                             int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
                                             int64_t ne11, int64_t n_tokens, int64_t x_row_stride, const int32_t *ids,
                                             int64_t n_ids, int64_t ids_stride, int glu_op, float glu_alpha,
                                             float glu_limit, float *dst, int64_t dst_row_stride, void *stream) {
-    if (!ids || n_as <= 0 || n_as > 0x7FFFFFFF || n_tokens <= 0 || n_ids <= 0 || ids_stride < n_ids ||
-        (ne11 != 1 && ne11 != n_ids) || x_row_stride < K || x_row_stride % 4 || dst_row_stride < nrows)
-        return (int)hipErrorInvalidValue;
-    if (n_tokens * n_ids > 65535 || n_tokens * ne11 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
-    const int64_t walign = block_align(type);
-    if (expert_stride < nrows * row_stride || expert_stride % walign || expert_stride > ((int64_t)1 << 40))
-        return (int)hipErrorInvalidValue;
-    const FxIds fi{ids, ids_stride, x_row_stride, expert_stride, dst_row_stride,
-                   (int)n_ids, (int)ne11, (int)n_as, (int)(n_tokens * n_ids)};
-    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op, glu_alpha, glu_limit, dst,
-                        &fi, stream);
+    return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, ne11, n_tokens, x_row_stride,
+                        ids, n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, nullptr, stream);
+}
+
+extern "C" int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, const void *w_gate, int64_t K,
+                                                   int64_t nrows, int64_t row_stride, int64_t expert_stride,
+                                                   int64_t n_as, const float *x, int64_t n_tokens,
+                                                   int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
+                                                   int64_t ids_stride, int glu_op, float glu_alpha, float glu_limit,
+                                                   float *dst, int64_t dst_row_stride, const void *shared_up,
+                                                   const void *shared_gate, float *shared_dst,
+                                                   int64_t shared_dst_row_stride, void *stream) {
+    const FxShared sh{shared_up, shared_gate, shared_dst, shared_dst_row_stride};
+    return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, 1, n_tokens, x_row_stride, ids,
+                        n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, &sh, stream);
 }
 
 // 2-4 f32 columns through the quantize-in-GEMV kernel (hip_qmm_mul_mat's

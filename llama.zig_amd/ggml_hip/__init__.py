@@ -57,6 +57,10 @@ def lib():
         L.hip_qmm_mul_mat_id_vec_fused.restype = i32
         L.hip_qmm_mul_mat_id_vec_fused.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64,
                                                    i64, i32, ctypes.c_float, ctypes.c_float, vp, i64, vp]
+        L.hip_qmm_mul_mat_id_vec_fused_shared.restype = i32
+        L.hip_qmm_mul_mat_id_vec_fused_shared.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, vp,
+                                                          i64, i64, i32, ctypes.c_float, ctypes.c_float, vp, i64, vp,
+                                                          vp, vp, i64, vp]
         L.hip_qmm_glu_f32.restype = i32
         L.hip_qmm_glu_f32.argtypes = [i32, ctypes.c_float, ctypes.c_float, i64, i64, vp, i64, vp, i64, vp, i64, vp]
         L.hip_qmm_add_f32.restype = i32
@@ -233,6 +237,34 @@ def mul_mat_id_vec_fused(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Ten
                                               n_ids, n_ids, op, alpha, limit, _ptr(out), nrows, _stream()),
            "hip_qmm_mul_mat_id_vec_fused")
     return out
+
+
+def mul_mat_id_vec_fused_shared(qtype, w: torch.Tensor, w_gate: torch.Tensor, x: torch.Tensor, ids: torch.Tensor,
+                                shared_up: torch.Tensor, shared_gate: torch.Tensor, glu="SWIGLU", alpha=1.702,
+                                limit=7.0, out=None, shared_out=None):
+    """The routed experts' gate / up / GLU over the (token, slot) pairs and a
+    shared expert's gate / up / GLU on every token, one launch.  w / w_gate:
+    uint8 [n_as, nrows, row_bytes]; shared_up / shared_gate: uint8 [nrows,
+    row_bytes]; x: f32 [n_tokens, 1, K]; ids: int32 [n_tokens, n_ids].
+    Returns (routed [n_tokens, n_ids, nrows], shared [n_tokens, nrows])."""
+    _require_cuda(w, w_gate, x, ids, shared_up, shared_gate)
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    n_as, nrows, rb = w.shape
+    n_tokens, ne11, K = x.shape
+    n_ids = ids.shape[1]
+    if (rb < row_size(t, K) or ne11 != 1 or ids.shape[0] != n_tokens or ids.dtype != torch.int32 or
+            w_gate.shape != w.shape or tuple(shared_up.shape) != (nrows, rb) or shared_gate.shape != shared_up.shape):
+        raise HipQmmError("bad shared-expert shapes")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty((n_tokens, n_ids, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    shared_out = (torch.empty((n_tokens, nrows), dtype=torch.float32, device=x.device) if shared_out is None
+                  else shared_out)
+    _check(lib().hip_qmm_mul_mat_id_vec_fused_shared(t, _ptr(w), _ptr(w_gate), K, nrows, w.stride(1), w.stride(0),
+                                                     n_as, _ptr(x), n_tokens, K, _ptr(ids), n_ids, n_ids, op, alpha,
+                                                     limit, _ptr(out), nrows, _ptr(shared_up), _ptr(shared_gate),
+                                                     _ptr(shared_out), nrows, _stream()),
+           "hip_qmm_mul_mat_id_vec_fused_shared")
+    return out, shared_out
 
 
 def glu_f32(gate: torch.Tensor, up: torch.Tensor, glu="SWIGLU", alpha=1.702, limit=7.0, out=None):

@@ -125,6 +125,14 @@ class buffer(C.Structure):
     _fields_ = [("iface", buffer_i), ("buft", VP), ("context", VP), ("size", SZ), ("usage", C.c_int)]
 
 
+ADD_ALLOC_DEP = FN(None, VP, VP, VP)
+
+
+class graph_optimize_params(C.Structure):
+    """struct ggml_backend_graph_optimize_params (src/ggml/backend_sched.zig:997-1000)."""
+    _fields_ = [("add_alloc_dep", ADD_ALLOC_DEP), ("user_data", VP)]
+
+
 class backend_i(C.Structure):
     _fields_ = [
         ("get_name", FN(C.c_char_p, VP)),
@@ -142,7 +150,7 @@ class backend_i(C.Structure):
         ("graph_compute", FN(C.c_int, VP, C.POINTER(ggml_cgraph))),
         ("event_record", FN(None, VP, VP)),
         ("event_wait", FN(None, VP, VP)),
-        ("graph_optimize", VP),
+        ("graph_optimize", FN(None, VP, C.POINTER(ggml_cgraph), VP)),
     ]
 
 

@@ -114,20 +114,21 @@ class HipBackend:
         buf.iface.get_tensor(t.buffer, C.pointer(t), out.ctypes.data, 0, out.nbytes)
         return out
 
-    def compute(self, nodes, use_counts=True):
-        """Run `nodes` as one graph.  With use_counts, the graph carries the
-        visited hash set and per-tensor use counts ggml_build_forward fills
-        (every node and source keyed at (addr >> 4) % size with linear
-        probing, src/ggml/impl.zig:509-557; the count of a tensor is the
-        number of node source slots naming it, src/ggml/graph.zig:472-520),
-        which the backend's fusion reads."""
+    @staticmethod
+    def _graph(nodes, use_counts=True):
+        """A ggml_cgraph over `nodes`, and the arrays it points at.  With
+        use_counts, the graph carries the visited hash set and per-tensor use
+        counts ggml_build_forward fills (every node and source keyed at
+        (addr >> 4) % size with linear probing, src/ggml/impl.zig:509-557; the
+        count of a tensor is the number of node source slots naming it,
+        src/ggml/graph.zig:472-520), which the backend's fusion reads."""
         arr = (abi.PT * len(nodes))(*[C.pointer(n) for n in nodes])
         g = abi.ggml_cgraph()
         g.size = len(nodes)
         g.n_nodes = len(nodes)
         g.n_leafs = 0
         g.nodes = arr
-        keep = []
+        keep = [arr]
         if use_counts:
             tensors = []
             for n in nodes:
@@ -158,11 +159,30 @@ class HipBackend:
             g.hash_size = size
             g.hash_used = C.cast(used, C.c_void_p)
             g.hash_keys = C.cast(keys, C.c_void_p)
-            keep = [used, keys, counts]
+            keep += [used, keys, counts]
+        return g, keep
+
+    def compute(self, nodes, use_counts=True):
+        """Run `nodes` as one graph (see _graph for the use counts)."""
+        g, keep = self._graph(nodes, use_counts)
         st = self.be.iface.graph_compute(self.be_ptr, C.pointer(g))
         self.be.iface.synchronize(self.be_ptr)
         del keep
         return st
+
+    def optimized(self, nodes, use_counts=True):
+        """The backend's graph_optimize on a graph of `nodes`: the node order
+        it leaves and the (tensor, until) allocation dependencies it adds,
+        as addresses."""
+        g, keep = self._graph(nodes, use_counts)
+        deps = []
+        cb = abi.ADD_ALLOC_DEP(lambda ud, tensor, until: deps.append((tensor, until)))
+        params = abi.graph_optimize_params(cb, None)
+        self.be.iface.graph_optimize(self.be_ptr, C.pointer(g), C.cast(C.pointer(params), C.c_void_p))
+        by_addr = {C.addressof(n): n for n in nodes}
+        order = [by_addr[C.addressof(keep[0][k].contents)] for k in range(len(nodes))]
+        del keep
+        return order, deps
 
     def close(self):
         for b in self.buffers:

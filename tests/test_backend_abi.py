@@ -261,3 +261,20 @@ def test_mul_mat_rejects_overlapping_columns_before_any_launch(L):
     for ncols in (2, 3, 8, 64):
         assert L.hip_qmm_mul_mat(12, w, 4096, 1024, 16 * 144, x, ncols, 4096, d, 1023, ws, 1 << 30, None) == 1
         assert L.hip_qmm_mul_mat(12, w, 4096, 1024, 16 * 144, x, ncols, 4064, d, 1024, ws, 1 << 30, None) == 1
+
+
+def test_scaled_gate_up_lane_is_not_taken(L):
+    """The reference's x_scale / gate_scale lane ({MUL_MAT, MUL(scale), MUL_MAT,
+    MUL(scale), GLU}) fuses only for NVFP4 and F8_E4M3 weights
+    (getMulMatScale, src/ggml/cuda/mulmat.zig:474-486); for the quantized
+    types this backend takes the scale MUL is an ordinary node, which stays
+    on the CPU backend, so the MUL_MATs and the GLU run as they do unscaled."""
+    from ggml_hip import abi
+    ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))  # noqa: E731
+    GGML_OP_MUL = 6  # src/ggml/types.zig:24-48
+    for t in (abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_Q6_K, abi.GGML_TYPE_Q8_0):
+        a, b, d = mm(t, 4096, 4096, 1)
+        assert ok(d)
+        s = abi.make_tensor(abi.GGML_TYPE_F32, [1], name=b"scale")
+        scaled = abi.make_tensor(abi.GGML_TYPE_F32, [4096, 1], op=GGML_OP_MUL, srcs=(d, s))
+        assert not ok(scaled)

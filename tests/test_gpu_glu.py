@@ -423,3 +423,133 @@ def test_plugin_fuses_moe_gate_up_glu(hb):
     assert hb.compute([gate, up, glu], use_counts=False) == abi.GGML_STATUS_SUCCESS
     assert not np.isnan(hb.get(up, np.float32, shape)).any()
     np.testing.assert_array_equal(hb.get(glu, np.float32, shape), out)
+
+
+# ---------------------------------------------------------------- shared expert (MoE decode)
+
+def _shared(tname, M, K, seed):
+    t = TYPES[tname]
+    su = O.quantize_rows(t, O.fill_normal(400 + seed, M * K, 0.0, 0.02).reshape(M, K))
+    sg = O.quantize_rows(t, O.fill_normal(500 + seed, M * K, 0.0, 0.02).reshape(M, K))
+    return su, sg
+
+
+@pytest.mark.parametrize("tname,n_tokens,opname", [("Q4_K", 1, "SWIGLU"), ("Q4_K", 3, "GEGLU"),
+                                                    ("Q6_K", 2, "SWIGLU_OAI"), ("Q8_0", 8, "SWIGLU_CLAMP")])
+def test_fused_gate_up_glu_with_ids_and_shared_expert(tname, n_tokens, opname):
+    """Routed experts and a shared expert in one launch: the routed rows equal
+    the launch without the shared expert, and each token's shared row equals
+    the one-column fused gate / up / GLU on the shared weights, bit for bit;
+    both pass the CPU gate."""
+    import ggml_hip as G
+    n_as, M, K, n_ids = 16, 768, 1024, 4
+    t, wu, wg, ids, x = _moe(tname, n_as, M, K, n_tokens, n_ids, 20 + n_tokens)
+    su, sg = _shared(tname, M, K, n_tokens)
+    wu_d, wg_d, x_d, ids_d, su_d, sg_d = _dev(wu), _dev(wg), _dev(x), _dev(ids), _dev(su), _dev(sg)
+    routed, shared = G.mul_mat_id_vec_fused_shared(tname, wu_d, wg_d, x_d, ids_d, su_d, sg_d, glu=opname,
+                                                   alpha=ALPHA, limit=LIMIT)
+    routed, shared = routed.cpu().numpy(), shared.cpu().numpy()
+    alone = G.mul_mat_id_vec_fused(tname, wu_d, x_d, ids_d, w_gate=wg_d, glu=opname, alpha=ALPHA,
+                                   limit=LIMIT).cpu().numpy()
+    np.testing.assert_array_equal(routed, alone)
+    for tt in range(n_tokens):
+        one = G.mul_mat_vec_fused(tname, su_d, K, x_d[tt, 0], w_gate=sg_d, glu=opname, alpha=ALPHA,
+                                  limit=LIMIT).cpu().numpy().reshape(-1)
+        np.testing.assert_array_equal(shared[tt], one)
+    xs = x.reshape(n_tokens, K)
+    cu = O.mul_mat(t, su, M, K, xs, nth=8)
+    cg = O.mul_mat(t, sg, M, K, xs, nth=8)
+    assert nmse(shared, O.glu(OPS[opname], cg, cu, ALPHA, LIMIT)) < NMSE_GATE
+
+
+def test_fused_shared_expert_rejects_bad_arguments():
+    import ctypes
+    import ggml_hip as G
+    n_as, M, K, n_tokens, n_ids = 4, 256, 256, 2, 2
+    t, wu, wg, ids, x = _moe("Q4_K", n_as, M, K, n_tokens, n_ids, 3)
+    su, sg = _shared("Q4_K", M, K, 3)
+    d = [_dev(a) for a in (wu, wg, x, ids, su, sg)]
+    out = torch.empty((n_tokens, n_ids, M), device="cuda")
+    sout = torch.empty((n_tokens, M), device="cuda")
+    p = lambda a: ctypes.c_void_p(a.data_ptr()) if a is not None else None  # noqa: E731
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def call(w_gate=d[1], shared_up=d[4], shared_gate=d[5], shared_dst=sout, sstride=M):
+        return G.lib().hip_qmm_mul_mat_id_vec_fused_shared(
+            t, p(d[0]), p(w_gate), K, M, d[0].stride(1), d[0].stride(0), n_as, p(d[2]), n_tokens, K, p(d[3]),
+            n_ids, n_ids, G.GLU_OPS["SWIGLU"], 1.702, 7.0, p(out), M, p(shared_up), p(shared_gate), p(shared_dst),
+            sstride, s)
+
+    assert call() == 0
+    assert call(w_gate=None) != 0       # the shared lane is gated
+    assert call(shared_up=None) != 0
+    assert call(shared_dst=None) != 0
+    assert call(sstride=M - 1) != 0     # overlapping shared rows
+    torch.cuda.synchronize()
+
+
+def test_plugin_groups_and_fuses_shared_expert(hb):
+    """graph_optimize moves the shared expert's {MUL_MAT, MUL_MAT, GLU} up
+    behind the routed {MUL_MAT_ID, MUL_MAT_ID, GLU} (an unrelated node between
+    them moves after) and keeps the routed input and ids alive until the
+    shared GLU; the six nodes then run as one launch (intermediates stay NaN)
+    equal to the kernel-level call, and unfused graphs give the same values."""
+    import ctypes as C
+    import ggml_hip as G
+    from ggml_hip import abi
+    n_as, M, K, n_tokens, n_ids = 16, 768, 1024, 3, 4
+    t, wu, wg, ids, x = _moe("Q4_K", n_as, M, K, n_tokens, n_ids, 9)
+    su, sg = _shared("Q4_K", M, K, 9)
+    wo = weights_q(O.TYPE_Q4_K, 512, K, 5)
+    q4 = abi.GGML_TYPE_Q4_K
+    tw_u = abi.make_tensor(q4, [K, M, n_as], name=b"ffn_up_exps")
+    tw_g = abi.make_tensor(q4, [K, M, n_as], name=b"ffn_gate_exps")
+    tw_su = abi.make_tensor(q4, [K, M], name=b"ffn_up_shexp")
+    tw_sg = abi.make_tensor(q4, [K, M], name=b"ffn_gate_shexp")
+    tw_o = abi.make_tensor(q4, [K, 512], name=b"other")
+    tx = abi.make_tensor(abi.GGML_TYPE_F32, [K, n_tokens], name=b"x")
+    tids = abi.make_tensor(abi.GGML_TYPE_I32, [n_ids, n_tokens], name=b"ids")
+    xr = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1, n_tokens], op=abi.GGML_OP_RESHAPE, srcs=(tx,), name=b"x_r")
+    xr.view_src = C.pointer(tx)
+    rs = [M, n_ids, n_tokens]
+    up = abi.make_tensor(abi.GGML_TYPE_F32, rs, op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_u, xr, tids), name=b"up")
+    gate = abi.make_tensor(abi.GGML_TYPE_F32, rs, op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_g, xr, tids), name=b"gate")
+    glu_r = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, gate, up, rs, name=b"routed")
+    other = abi.make_tensor(abi.GGML_TYPE_F32, [512, n_tokens], op=abi.GGML_OP_MUL_MAT, srcs=(tw_o, tx), name=b"o")
+    sup = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_tokens], op=abi.GGML_OP_MUL_MAT, srcs=(tw_su, tx), name=b"sup")
+    sgate = abi.make_tensor(abi.GGML_TYPE_F32, [M, n_tokens], op=abi.GGML_OP_MUL_MAT, srcs=(tw_sg, tx), name=b"sgt")
+    glu_s = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, sgate, sup, [M, n_tokens], name=b"shared")
+    hb.alloc([tw_u, tw_g, tw_su, tw_sg, tw_o], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([tx, tids, up, gate, glu_r, other, sup, sgate, glu_s], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    xr.data, xr.buffer = tx.data, tx.buffer
+    for tns, arr in ((tw_u, wu), (tw_g, wg), (tw_su, su), (tw_sg, sg), (tw_o, wo), (tx, x), (tids, ids)):
+        hb.set(tns, arr)
+    order = [xr, gate, up, glu_r, other, sgate, sup, glu_s]
+
+    # graph_optimize through the backend's vtable; without use counts the
+    # nodes cannot be shown closed, so nothing moves
+    same, deps0 = hb.optimized(order, use_counts=False)
+    assert [C.addressof(n) for n in same] == [C.addressof(n) for n in order] and deps0 == []
+    ordered = hb.optimized(order)
+    want_order = [C.addressof(n) for n in [xr, gate, up, glu_r, sgate, sup, glu_s, other]]
+    assert [C.addressof(n) for n in ordered[0]] == want_order
+    assert sorted(ordered[1]) == sorted([(C.addressof(xr), C.addressof(glu_s)), (C.addressof(tids), C.addressof(glu_s))])
+
+    rsh, ssh = (n_tokens, n_ids, M), (n_tokens, M)
+    for tns, sh in ((up, rsh), (gate, rsh), (glu_r, rsh), (sup, ssh), (sgate, ssh), (glu_s, ssh)):
+        hb.set(tns, np.full(sh, np.nan, dtype=np.float32))
+    assert hb.compute(ordered[0]) == abi.GGML_STATUS_SUCCESS
+    for tns, sh in ((up, rsh), (gate, rsh), (sup, ssh), (sgate, ssh)):
+        assert np.isnan(hb.get(tns, np.float32, sh)).all()
+    r_out, s_out = hb.get(glu_r, np.float32, rsh), hb.get(glu_s, np.float32, ssh)
+    want_r, want_s = G.mul_mat_id_vec_fused_shared("Q4_K", _dev(wu), _dev(wg), _dev(x.reshape(n_tokens, 1, K)),
+                                                   _dev(ids), _dev(su), _dev(sg), glu="SWIGLU")
+    np.testing.assert_array_equal(r_out, want_r.cpu().numpy())
+    np.testing.assert_array_equal(s_out, want_s.cpu().numpy())
+    # unfused (no use counts): every node on its own
+    assert hb.compute(ordered[0], use_counts=False) == abi.GGML_STATUS_SUCCESS
+    assert not np.isnan(hb.get(sup, np.float32, ssh)).any()
+    np.testing.assert_array_equal(hb.get(glu_r, np.float32, rsh), r_out)
+    u2, g2 = hb.get(sup, np.float32, ssh), hb.get(sgate, np.float32, ssh)
+    assert nmse(hb.get(glu_s, np.float32, ssh), s_out) < 1e-10
+    assert nmse(O.glu(O.GLU_SWIGLU, g2, u2), s_out) < 1e-10
