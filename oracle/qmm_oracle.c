@@ -2389,3 +2389,110 @@ int orc_mul_mat_tiled(int type, const void *w, int64_t nrows, int64_t K, const f
     return 0;
 #endif
 }
+
+/* ------------------------------------------------------------------------ */
+/* The reference's x86 Q8_0 / Q4_0 GEMM: llamafile_sgemm's tinyBLAS_Q0_AVX
+ * (src/ggml/cpu/ops/sgemm.zig:578-880, dispatched at :1067-1070 and reached
+ * from mul_mat's second llamafile attempt, src/ggml/cpu/mulmat.zig:336-367,
+ * for src1 of 2 or more columns once it is staged as Q8_0).  Every tile
+ * kernel (gemm4xN, gemmMx4, gemm; sgemm.zig:771-880) gives an output the same
+ * value, so only the per-output arithmetic is restated:
+ *   for each block l: s = f32(d_a) * f32(d_b); lane i (0..7) of the block's
+ *   dot is the exact int32 sum of elements 4i..4i+3 (dot via maddubs / madd,
+ *   sgemm.zig:634-645; no saturation for these operands), converted to f32;
+ *   acc[i] = fma(s, lane_i, acc[i]);
+ *   out = hsumAvx(acc) = (h0 + h2) + (h1 + h3) with h = acc[4..7] + acc[0..3]
+ *   (sgemm.zig:119-124).
+ * Q4_0 weights are their nibbles minus 8, low nibbles first (denibble,
+ * sgemm.zig:594-600, 618-620). */
+
+static int tb_lane_dots(int type, const uint8_t *a, const blk_q8_0 *b, int32_t lanes[8], float *da) {
+    int8_t av[32];
+    if (type == ORC_TYPE_Q8_0) {
+        const blk_q8_0 *q = (const blk_q8_0 *)a;
+        memcpy(av, q->qs, 32);
+        *da = orc_fp16_to_fp32(q->d);
+    } else {
+        const blk_q4_0 *q = (const blk_q4_0 *)a;
+        for (int j = 0; j < 16; ++j) {
+            av[j] = (int8_t)((q->qs[j] & 0x0F) - 8);
+            av[j + 16] = (int8_t)((q->qs[j] >> 4) - 8);
+        }
+        *da = orc_fp16_to_fp32(q->d);
+    }
+    for (int i = 0; i < 8; ++i) {
+        int32_t s = 0;
+        for (int m = 0; m < 4; ++m) s += (int32_t)av[4 * i + m] * (int32_t)b->qs[4 * i + m];
+        lanes[i] = s;
+    }
+    return 0;
+}
+
+typedef struct {
+    int type;
+    const uint8_t *w;
+    const blk_q8_0 *y;
+    int64_t nrows, nb, ncols, nth;
+    size_t wrow;
+    float *dst;
+} tb_ctx;
+
+typedef struct { tb_ctx *c; int ith; } tb_thread;
+
+static void *tb_worker(void *arg) {
+    tb_thread *t = (tb_thread *)arg;
+    const tb_ctx *c = t->c;
+    const size_t ab = c->type == ORC_TYPE_Q8_0 ? sizeof(blk_q8_0) : sizeof(blk_q4_0);
+    /* rows split statically (the tile kernels' duty split does not change values) */
+    const int64_t r0 = c->nrows * t->ith / c->nth, r1 = c->nrows * (t->ith + 1) / c->nth;
+    for (int64_t col = 0; col < c->ncols; ++col)
+        for (int64_t r = r0; r < r1; ++r) {
+            float acc[8] = {0};
+            for (int64_t l = 0; l < c->nb; ++l) {
+                int32_t lanes[8];
+                float da;
+                const blk_q8_0 *b = c->y + col * c->nb + l;
+                tb_lane_dots(c->type, c->w + (size_t)r * c->wrow + (size_t)l * ab, b, lanes, &da);
+                const float s = da * orc_fp16_to_fp32(b->d);
+                for (int i = 0; i < 8; ++i) acc[i] = fmaf(s, (float)lanes[i], acc[i]);
+            }
+            float h[4];
+            for (int i = 0; i < 4; ++i) h[i] = acc[4 + i] + acc[i];
+            c->dst[col * c->nrows + r] = (h[0] + h[2]) + (h[1] + h[3]);
+        }
+    return NULL;
+}
+
+int orc_tinyblas_q0(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
+                    float *dst, int nth) {
+    if ((type != ORC_TYPE_Q8_0 && type != ORC_TYPE_Q4_0) || K % QK8_0 != 0 || nrows <= 0 || ncols <= 0) return 0;
+    if (nth < 1) nth = 1;
+    tb_ctx c;
+    c.type = type;
+    c.w = (const uint8_t *)w;
+    c.y = (const blk_q8_0 *)y_q8_0;
+    c.nrows = nrows;
+    c.nb = K / QK8_0;
+    c.ncols = ncols;
+    c.nth = nth;
+    c.wrow = orc_row_size(type, K);
+    c.dst = dst;
+    tb_thread *ts = (tb_thread *)malloc(sizeof(tb_thread) * (size_t)nth);
+    for (int i = 0; i < nth; ++i) { ts[i].c = &c; ts[i].ith = i; }
+    run_threads(nth, ts, sizeof *ts, tb_worker);
+    free(ts);
+    return 1;
+}
+
+int orc_mul_mat_tinyblas(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols,
+                         float *dst, int nth) {
+    /* llamafile_sgemm returns false below 2 columns (sgemm.zig:898) */
+    if ((type != ORC_TYPE_Q8_0 && type != ORC_TYPE_Q4_0) || ncols < 2 || K % QK8_0 != 0 || !orc_has_avx2())
+        return 0;
+    const size_t yrow = orc_row_size(ORC_TYPE_Q8_0, K);
+    uint8_t *y = (uint8_t *)malloc(yrow * (size_t)ncols);
+    for (int64_t col = 0; col < ncols; ++col) orc_quantize_row_q8_0_avx2(x + col * K, y + (size_t)col * yrow, K);
+    const int ok = orc_tinyblas_q0(type, w, nrows, K, y, ncols, dst, nth);
+    free(y);
+    return ok;
+}

@@ -105,6 +105,18 @@ void orc_mul_mat_id(int type, int impl, const void *w, int64_t n_as, int64_t nro
 int orc_mul_mat_tiled(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols, float *dst,
                       int nth);
 
+/* The reference's x86 Q8_0 / Q4_0 GEMM (llamafile_sgemm's tinyBLAS_Q0_AVX,
+ * src/ggml/cpu/ops/sgemm.zig:578-880, reached from mul_mat for 2 or more
+ * columns, src/ggml/cpu/mulmat.zig:336-367).  orc_tinyblas_q0 takes the
+ * columns already as Q8_0 (ncols x K/32 blocks); orc_mul_mat_tinyblas
+ * quantizes f32 columns with the x86 quantize_row_q8_0 first.  Layouts as
+ * orc_mul_mat.  Return 0 (writing nothing) for other types, and
+ * orc_mul_mat_tinyblas also below 2 columns or without AVX2. */
+int orc_tinyblas_q0(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
+                    float *dst, int nth);
+int orc_mul_mat_tinyblas(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols,
+                         float *dst, int nth);
+
 /* GLU ops (ggml_glu_op: positions in GGML_GLU_OP_NAME, src/ggml/types.zig:103-106) */
 #define ORC_GLU_REGLU 0
 #define ORC_GLU_GEGLU 1

@@ -65,6 +65,10 @@ def lib():
         L.orc_mul_mat.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
         L.orc_mul_mat_tiled.restype = ctypes.c_int
         L.orc_mul_mat_tiled.argtypes = [ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
+        L.orc_tinyblas_q0.restype = ctypes.c_int
+        L.orc_tinyblas_q0.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, f32p, ctypes.c_int]
+        L.orc_mul_mat_tinyblas.restype = ctypes.c_int
+        L.orc_mul_mat_tinyblas.argtypes = [ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
         L.orc_mul_mat_id.restype = None
         L.orc_mul_mat_id.argtypes = [ctypes.c_int, ctypes.c_int, vp, i64, i64, i64, f32p, i64, i64, vp, i64,
                                      f32p, ctypes.c_int]
@@ -180,6 +184,43 @@ def mul_mat_tiled(t, wq, nrows, K, x, nth=4):
     out = np.full((ncols, nrows), np.nan, dtype=np.float32)
     ok = lib().orc_mul_mat_tiled(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(x), ncols, _p(out), nth)
     return out if ok else None
+
+
+def tinyblas_q0(t, wq, nrows, K, y_q8_0, ncols, nth=4):
+    """tinyBLAS_Q0_AVX's outputs for Q8_0 / Q4_0 weights against columns
+    already quantized to Q8_0 (ncols x K/32 blocks) -> [ncols, nrows], or None
+    for other types."""
+    out = np.full((ncols, nrows), np.nan, dtype=np.float32)
+    ok = lib().orc_tinyblas_q0(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(np.ascontiguousarray(y_q8_0)), ncols,
+                               _p(out), nth)
+    return out if ok else None
+
+
+def mul_mat_tinyblas(t, wq, nrows, K, x, nth=4):
+    """The reference's x86 Q8_0 / Q4_0 mul_mat for 2+ columns (x86
+    quantize_row_q8_0, then tinyBLAS_Q0_AVX): x [ncols, K] -> [ncols, nrows],
+    or None where it does not apply."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    ncols = x.shape[0]
+    out = np.full((ncols, nrows), np.nan, dtype=np.float32)
+    ok = lib().orc_mul_mat_tinyblas(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(x), ncols, _p(out), nth)
+    return out if ok else None
+
+
+def mul_mat_x86(t, wq, nrows, K, x, nth=4):
+    """ggml_compute_forward_mul_mat as an x86 AVX2 host runs it
+    (src/ggml/cpu/mulmat.zig:218-220, 336-367): the tiled GEMM for the tiled
+    K-quants from 8 columns, tinyBLAS for Q8_0 / Q4_0 from 2 columns, else
+    the AVX2 vec_dot route."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, K)
+    if x.shape[0] >= 8:
+        out = mul_mat_tiled(t, wq, nrows, K, x, nth=nth)
+        if out is not None:
+            return out
+    out = mul_mat_tinyblas(t, wq, nrows, K, x, nth=nth)
+    if out is not None:
+        return out
+    return mul_mat(t, wq, nrows, K, x, nth=nth, impl=IMPL_AVX2)
 
 
 def mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=4, impl=IMPL_GENERIC):

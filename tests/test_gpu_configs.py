@@ -15,9 +15,11 @@ seed 44):
      row per token) and down 2048x768 (one row per slot), 512 tokens top-8.
 
 Gates, per cell:
-  - NMSE < 5e-4 against the CPU ggml path (the restated
-    ggml_compute_forward_mul_mat / _mul_mat_id with Q8_K / Q8_0 activations,
-    src/ggml/cpu/mulmat.zig:205-423, 555-777; the measure of
+  - NMSE < 5e-4 against the CPU ggml path as an x86 AVX2 host runs it (the
+    restated ggml_compute_forward_mul_mat, src/ggml/cpu/mulmat.zig:205-423:
+    the tiled K-quant GEMM from 8 columns, tinyBLAS for Q8_0 from 2 columns,
+    else the AVX2 vec_dot route with Q8_K / Q8_0 activations;
+    _mul_mat_id, mulmat.zig:555-777, through vec_dot; the measure of
     harness/blas_diff.c:341-350);
   - within 2e-6 (error / max |out|) of the f64 evaluation of the Q8_1 formula
     on activations quantized by the oracle's quantize_row_q8_1_ref, which
@@ -127,9 +129,12 @@ def test_config_cell(cell):
     sub = got[:, rows]
     ideal = O.mul_mat_q8_1_f64(t, wq[rows], len(rows), K, _q8_1_cols(x, K), T)
     f64_err = max_err_scaled(sub, ideal)
-    cpu = O.mul_mat(t, wq[rows], len(rows), K, x, nth=O.gen_threads())
+    cpu = O.mul_mat_x86(t, wq[rows], len(rows), K, x, nth=O.gen_threads())
+    route = ("tiled" if T >= 8 and tname in ("Q4_K", "Q6_K") and O.has_avx2() else
+             "tinyBLAS" if T >= 2 and tname == "Q8_0" and O.has_avx2() else "vec_dot")
     e, mr = nmse(sub, cpu), max_rel(sub, cpu)
     _RECORD.append({"cell": f"{tname} {nrows}x{K} T={T}", "configs": labels, "entry": "hip_qmm_mul_mat",
+                    "cpu_route": route,
                     "rows_checked": int(len(rows)), "nmse_vs_cpu": e, "max_rel_vs_cpu": mr,
                     "max_err_over_max_vs_cpu": max_err_scaled(sub, cpu), "f64_max_err_scaled": f64_err})
     assert f64_err < F64_TOL, f"f64 agreement {f64_err:.3g}"

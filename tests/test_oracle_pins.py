@@ -18,7 +18,14 @@ term fails here:
 - the AVX2 restatements (no x86 goldens exist in the reference): checked
   against the generic ones, integers exact and floats within rounding;
 - orc_fill_normal: moments of the distribution and a committed fingerprint of
-  the seeded stream (determinism across machines).
+  the seeded stream (determinism across machines);
+- orc_tinyblas_q0 (x86 Q8_0 / Q4_0 GEMM): with unit scales every output is the
+  exact integer dot (numpy), which pins the lane grouping, the Q4_0 nibble
+  order and offset and the block / column indexing; one case whose lanes hold
+  2^24, -2^24 and 1 sums to exactly 1 only in the reference's horizontal order
+  ((h0 + h2) + (h1 + h3), h = upper + lower half), where a sequential or
+  adjacent-pair order loses the 1; on quantized normal data it agrees with the
+  golden-pinned vec_dot route within rounding and does not depend on threads.
 """
 import numpy as np
 import pytest
@@ -339,3 +346,68 @@ def test_tiled_gemm_is_independent_of_threads_and_windows(t):
 def test_tiled_gemm_declines_untiled_types():
     wq = O.quantize_rows(O.TYPE_Q8_0, np.zeros((16, 256), np.float32))
     assert O.mul_mat_tiled(O.TYPE_Q8_0, wq, 16, 256, np.zeros((8, 256), np.float32)) is None
+
+
+# ---------------------------------------------------------------- tinyBLAS (x86 Q8_0 / Q4_0 GEMM)
+
+Q80 = np.dtype([("d", "<u2"), ("qs", "i1", 32)])
+Q40 = np.dtype([("d", "<u2"), ("qs", "u1", 16)])
+
+
+def _q8_0_blocks(vals, d=F16_ONE):
+    """int8 values [rows, K] -> Q8_0 blocks with scale d."""
+    rows, K = vals.shape
+    b = np.zeros((rows, K // 32), dtype=Q80)
+    b["d"] = d
+    b["qs"] = vals.reshape(rows, K // 32, 32)
+    return b
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_0])
+def test_tinyblas_exact_on_unit_scales(t):
+    rng = np.random.default_rng(77 + t)
+    nrows, K, ncols = 13, 256, 5
+    if t == O.TYPE_Q8_0:
+        wv = rng.integers(-127, 128, size=(nrows, K)).astype(np.int8)
+        w = _q8_0_blocks(wv)
+    else:
+        wv = rng.integers(-8, 8, size=(nrows, K)).astype(np.int8)
+        nib = (wv + 8).astype(np.uint8).reshape(nrows, K // 32, 32)
+        w = np.zeros((nrows, K // 32), dtype=Q40)
+        w["d"] = F16_ONE
+        w["qs"] = nib[:, :, :16] | (nib[:, :, 16:] << 4)
+    yv = rng.integers(-127, 128, size=(ncols, K)).astype(np.int8)
+    y = _q8_0_blocks(yv)
+    got = O.tinyblas_q0(t, w.view(np.uint8), nrows, K, y.view(np.uint8), ncols, nth=3)
+    want = (yv.astype(np.int64) @ wv.astype(np.int64).T).astype(np.float64)
+    np.testing.assert_array_equal(got.astype(np.float64), want)
+
+
+def test_tinyblas_horizontal_sum_order():
+    K = 64
+    w = np.zeros((1, 2), dtype=Q80)
+    y = np.zeros((1, 2), dtype=Q80)
+    big = np.float16(2048.0).view(np.uint16)  # 2048 * 2048 = 2^22
+    w[0, 0]["d"], y[0, 0]["d"] = big, big
+    w[0, 0]["qs"][0], y[0, 0]["qs"][0] = 4, 1     # lane 0: 4 * 2^22 = 2^24
+    w[0, 0]["qs"][16], y[0, 0]["qs"][16] = -4, 1  # lane 4: -2^24
+    w[0, 1]["d"], y[0, 1]["d"] = F16_ONE, F16_ONE
+    w[0, 1]["qs"][4], y[0, 1]["qs"][4] = 1, 1     # lane 1: 1
+    got = O.tinyblas_q0(O.TYPE_Q8_0, w.view(np.uint8), 1, K, y.view(np.uint8), 1)
+    assert got[0, 0] == 1.0  # exact; ((L0 + L1) + ...) or ((L0 + L1) + (L2 + L3)) + ... give 0
+
+
+@pytest.mark.skipif(not O.has_avx2(), reason="the tinyBLAS path is the x86 AVX2 arm")
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_0])
+def test_tinyblas_agrees_with_vec_dot_route(t):
+    nrows, K, ncols = 48, 1024, 7
+    wq = O.quantize_rows(t, O.fill_normal(31 + t, nrows * K, 0.0, 0.02).reshape(nrows, K))
+    x = O.fill_normal(41 + t, ncols * K).reshape(ncols, K)
+    tb = O.mul_mat_tinyblas(t, wq, nrows, K, x, nth=1)
+    vd = O.mul_mat(t, wq, nrows, K, x, nth=2, impl=O.IMPL_AVX2)
+    scale = np.abs(vd).max()
+    assert np.abs(tb - vd).max() <= 2e-6 * scale
+    np.testing.assert_array_equal(O.mul_mat_tinyblas(t, wq, nrows, K, x, nth=5), tb)
+    assert O.mul_mat_tinyblas(t, wq, nrows, K, x[:1]) is None  # llamafile_sgemm declines one column
+    assert O.mul_mat_tinyblas(O.TYPE_Q4_K, O.quantize_rows(O.TYPE_Q4_K, O.fill_normal(1, 256 * 8).reshape(8, 256)),
+                              8, 256, x[:, :256]) is None
