@@ -43,11 +43,12 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
                        const int32_t *col_dst, float *partial, hipStream_t s);
-// mmq_few.hip: the Q4_K kernel for at most 32 columns
+// mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
-int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
-                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
-                       hipStream_t s);
+bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
+int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                   const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
+                   hipStream_t s);
 
 namespace {
 
@@ -744,19 +745,29 @@ int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return (int)split;
 }
 
-// Q4_K with at most 32 columns runs the few-column kernel (mmq_few.hip) when
-// the activation planes are 16-byte aligned.
-bool few_cols(int type, int64_t ncols) { return type == TYPE_Q4_K && ncols <= 32; }
+// The few-column kernel (mmq_few.hip) takes Q4_K and Q8_0 up to 32 columns
+// and Q6_K up to 16 (K % 2048 == 0; Q8_0 / Q6_K on 16-byte-aligned rows),
+// when the activation planes are 16-byte aligned.  Measured against the
+// 128-row tile (us, 4096x14336, same weights): Q8_0 9 / 32 columns 18.6 / 23.2
+// against 33.2 / 39.1; Q6_K 9 / 16 columns 22.6 / 23.2 against 28.3 / 29.3,
+// but 48.3 / 48.8 against 31.3 / 33.4 at 24 / 32 (two column tiles), so those
+// keep the tile.  few_cols_type is the part that depends on the shape alone
+// (the split and workspace queries); the dispatch also checks the rows
+// (mmq_few_takes).
+bool few_cols_type(int type, int64_t K, int64_t ncols) {
+    return (ncols <= 32 && (type == TYPE_Q4_K || type == TYPE_Q8_0)) ||
+           (ncols <= 16 && type == TYPE_Q6_K && K % 2048 == 0);
+}
 
 extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
-    return few_cols(type, ncols) ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
+    return few_cols_type(type, K, ncols) ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
 }
 
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 0;
     int split = split_std(type, K, nrows, ncols);
-    if (few_cols(type, ncols) && mmq_few_split_k(K, nrows) > split) split = mmq_few_split_k(K, nrows);
+    if (few_cols_type(type, K, ncols) && mmq_few_split_k(K, nrows) > split) split = mmq_few_split_k(K, nrows);
     return split > 1 ? (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) : 0;
 }
 
@@ -769,7 +780,8 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     if (int e = check_weights(type, w, K, row_stride)) return e;
     const int bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
-    const bool few = few_cols(type, ncols) && (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;
+    const bool few = few_cols_type(type, K, ncols) && mmq_few_takes(type, K, w, row_stride) &&
+                     (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;
     // split K only when the caller's workspace holds the partials
     int split = few ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
     if (split > 1 && (!workspace || workspace_size < (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) ||
@@ -778,8 +790,8 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     float *partial = (float *)workspace;
     hipStream_t s = (hipStream_t)stream;
     if (few) {
-        if (int e = mmq_few_q4k_launch(w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, split, partial,
-                                       s))
+        if (int e = mmq_few_launch(type, w, K, nrows, row_stride, y_qs, y_ds, ncols, dst, dst_col_stride, split,
+                                   partial, s))
             return e;
         return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
     }

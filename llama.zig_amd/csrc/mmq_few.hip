@@ -1,4 +1,5 @@
-// mmq_few.hip -- Q4_K GEMM for few activation columns (up to 32), on 16x16 int8 MFMA.
+// mmq_few.hip -- Q4_K / Q6_K / Q8_0 GEMM for few activation columns (up to 32),
+// on 16x16 int8 MFMA.
 //
 // The reference sends 2-24 src1 columns to a separate "few-row" MMQ kernel
 // (src/ggml/cuda/mmq_few.zig:1-20, mulMatQFew :204-255, shouldUseMmqFew
@@ -28,6 +29,21 @@
 // (vmcnt = its transfer count of one step) before the step's barrier.  The
 // weight decode (nibbles, scales) is shared by the column tiles.
 //
+// The 2-byte-aligned types (the reference routes them here too,
+// mmq_few.zig:246-266): a K-step is still 256 weights of a row.
+//   - Q8_0: 8 blocks of 34 bytes, 272 bytes, 16-byte aligned when the rows
+//     are; per block S_b from one int8 MFMA and the scale d_w * d8 from the
+//     f16 scale MFMA; no super-block terms.
+//   - Q6_K: one 210-byte block, which sits at 2-byte alignment.  The step
+//     moves the 224 aligned bytes around it (14 x 16, from (210 * k) & ~15:
+//     the block starts (2 * k) % 16 bytes in), which stay inside the row when
+//     its block count is a multiple of 8 (K % 2048 == 0).  Each 32 weights hold
+//     two 16-weight sub-blocks with their own int8 scale: two int8 MFMAs, each
+//     with the other sub-block's lanes zeroed, against the same Q8_1 block;
+//     the weights go in as q - 32 (bytewise, no carries); d once per step.
+// Operand reads at 2-byte alignment in LDS take two byte funnel shifts of
+// three aligned dwords.
+//
 // 16x16 MFMA operand convention: lane l supplies row (l % 16) of A and column
 // (l % 16) of B over the K-slice [(l / 16) * K/4, +K/4); the result value i of
 // lane l is row 4*(l/16) + i, column l % 16.
@@ -45,14 +61,35 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 
 constexpr int FBN = 32;  // most columns (two 16-column MFMA tiles)
 
+// Bytes of one row's K-step as moved to LDS, and where step k starts in the row.
+template <int TYPE>
+struct FewFmt;
+template <>
+struct FewFmt<TYPE_Q4_K> {
+    static constexpr int WROW = Q4K_BYTES;
+    __device__ static int64_t aoff(int kb) { return (int64_t)kb * Q4K_BYTES; }
+};
+template <>
+struct FewFmt<TYPE_Q8_0> {
+    static constexpr int WROW = 8 * Q80_BYTES;  // 272
+    __device__ static int64_t aoff(int kb) { return (int64_t)kb * (8 * Q80_BYTES); }
+};
+template <>
+struct FewFmt<TYPE_Q6_K> {
+    static constexpr int WROW = 224;  // the aligned window around one 210-byte block
+    __device__ static int64_t aoff(int kb) { return ((int64_t)kb * Q6K_BYTES) & ~(int64_t)15; }
+};
+
 // Workgroup geometry for NW waves of 16 rows each and NCT tiles of 16
 // columns: the step's LDS stage and its 1 KiB transfers (transfer q goes to
 // wave q % NW).
-template <int NW, int NCT>
+template <int TYPE, int NW, int NCT>
 struct FewGeo {
+    static constexpr int WROW = FewFmt<TYPE>::WROW;
     static constexpr int BM = 16 * NW;                 // rows per workgroup
     static constexpr int NT = 64 * NW;                 // threads
-    static constexpr int A = BM * Q4K_BYTES;           // weights per step
+    static constexpr int A = BM * WROW;                // weights per step
+    static_assert(A % 1024 == 0, "whole weight transfers");
     static constexpr int B = 16 * NCT * QK_K;          // codes per step
     static constexpr int D = 16 * NCT * 8 * 4;         // headers per step
     static constexpr int NQ = (A + B + D + 1023) / 1024;
@@ -71,6 +108,22 @@ __device__ __forceinline__ uint32_t byte_f16(uint32_t v, int b) {
 }
 
 __device__ __forceinline__ long as_long(uint2 v) { return (long)(((uint64_t)v.y << 32) | v.x); }
+
+// 8 bytes at a 2-byte-aligned LDS address: three aligned dwords, funnel-shifted
+// (may read up to 4 bytes past p + 8, inside the stage).
+__device__ __forceinline__ uint2 lds8_a2(const uint8_t *p) {
+    const uint32_t sh = (uint32_t)((uintptr_t)p & 2u);
+    const uint32_t *b = reinterpret_cast<const uint32_t *>(p - sh);
+    const uint32_t a0 = b[0], a1 = b[1], a2 = b[2];
+    return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(a2, a1, sh));
+}
+
+// Q6_K weights q (0..63 per byte) to q - 32 as signed bytes: q ^ 32 is
+// (q - 32) mod 64; its bit 5 copied into bits 6 and 7 sign-extends it.
+__device__ __forceinline__ uint32_t q6_signed(uint32_t q) {
+    const uint32_t x = q ^ 0x20202020u, t = x & 0x20202020u;
+    return x | (t << 1) | (t << 2);
+}
 
 // 16 bytes per lane from global memory to LDS at base + 16 * lane (base is
 // wave-uniform).  Issued as inline assembly on purpose: the compiler does not
@@ -124,18 +177,19 @@ __device__ __forceinline__ void wait_step(bool big, int ahead) {
 }
 
 // workgroups per CU that the LDS (160 KiB) holds with an NST-stage ring
-template <int NW, int NCT>
-constexpr int few_occupancy(int nst) { return 163840 / (nst * FewGeo<NW, NCT>::STAGE); }
+template <int TYPE, int NW, int NCT>
+constexpr int few_occupancy(int nst) { return 163840 / (nst * FewGeo<TYPE, NW, NCT>::STAGE); }
 
-template <int NST, int NW, int NCT>
-__global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST))) void mmq_few_q4k_kernel(const uint8_t *__restrict__ w, int64_t K, int64_t nrows,
-                                                            int64_t row_stride, const int8_t *__restrict__ yqs,
-                                                            const uint32_t *__restrict__ yds, int ncols,
-                                                            float *__restrict__ dst, int64_t dst_col_stride,
-                                                            float *__restrict__ partial) {
-    using G = FewGeo<NW, NCT>;
-    constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER;
-    static_assert(NST >= 2 && few_occupancy<NW, NCT>(NST) >= 1, "ring depth");
+template <int TYPE, int NST, int NW, int NCT>
+__global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, NW, NCT>(NST))) void mmq_few_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
+    const uint32_t *__restrict__ yds, int ncols, float *__restrict__ dst, int64_t dst_col_stride,
+    float *__restrict__ partial) {
+    using G = FewGeo<TYPE, NW, NCT>;
+    using FF = FewFmt<TYPE>;
+    constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER, WROW = G::WROW;
+    constexpr int NQA = FA / 1024;  // transfers 0 .. NQA-1 move weights
+    static_assert(NST >= 2 && few_occupancy<TYPE, NW, NCT>(NST) >= 1, "ring depth");
     static_assert((NST - 2) * G::transfers_of(0) <= 63, "vmcnt field");
     __shared__ alignas(16) uint8_t st[NST][G::STAGE];
 
@@ -157,10 +211,10 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
         const int q = wave + NW * i;
         const int pos = (q < FNQ ? q : 0) * 1024 + lane * 16;
         if (pos < FA) {
-            const int r = pos / Q4K_BYTES, off = pos - r * Q4K_BYTES;
+            const int r = pos / WROW, off = pos - r * WROW;
             const int64_t grow = row0 + r < nrows ? row0 + r : nrows - 1;  // rows past the end: duplicates
             src[i] = w + grow * row_stride + off;
-            kstep[i] = Q4K_BYTES;
+            kstep[i] = 0;  // the weights' step offset is FF::aoff
         } else if (pos < FA + FB) {
             const int p = pos - FA, n = p >> 8, c = ((p >> 4) & 15) ^ (n & 15);
             const int col = n < ncols ? n : ncols - 1;  // columns past the end: duplicates
@@ -176,9 +230,12 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
         }
     }
     auto dma = [&](int kb, uint8_t *st) {
+        const int64_t ao = FF::aoff(kb);
 #pragma unroll
-        for (int i = 0; i < PER; ++i)
-            if (wave + NW * i < FNQ) dma16(src[i] + (int64_t)kb * kstep[i], st + (wave + NW * i) * 1024);
+        for (int i = 0; i < PER; ++i) {
+            const int q = wave + NW * i;  // uniform
+            if (q < FNQ) dma16(src[i] + (q < NQA ? ao : (int64_t)kb * kstep[i]), st + q * 1024);
+        }
     };
 
     v4f acc[NCT];
@@ -189,6 +246,103 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
     // zero, so their (finite) B values add nothing.
     const uint32_t m_sc = kq == 0 ? 0xFFFFFFFFu : 0u;
     const uint32_t m_mn = kq < 2 ? 0xFFFFFFFFu : 0u;
+
+    // per column tile j: the lane's column 16j + li, its codes and its
+    // (d8 | s8 << 16) headers of the step's 8 blocks
+    auto col_headers = [&](const uint8_t *st, int j, const uint8_t *&bcol, uint4 &dh0, uint4 &dh1) {
+        bcol = st + FA + (16 * j + li) * QK_K;
+        const uint32_t *dcol = reinterpret_cast<const uint32_t *>(st + FA + FB) + (16 * j + li) * 8;
+        dh0 = *reinterpret_cast<const uint4 *>(dcol);
+        dh1 = *reinterpret_cast<const uint4 *>(dcol + 4);
+    };
+    // the scale MFMA's B operand for block g: the headers of blocks 2h, 2h+1
+    // (h = g/2) as stored, d8 of block g in K slot 0 (g even) or 2 (g odd)
+    auto scale_b = [&](int g, const uint4 &dh0, const uint4 &dh1) {
+        const uint4 &dh = g < 4 ? dh0 : dh1;
+        return __builtin_bit_cast(v4h, (g & 2) ? make_uint2(dh.z, dh.w) : make_uint2(dh.x, dh.y));
+    };
+    // ... and its A operand: the row's f16 scale bits in the slot of block g
+    auto scale_a = [&](int g, uint32_t f16bits) {
+        return __builtin_bit_cast(v4h, (g & 1) ? make_uint2(0u, f16bits) : make_uint2(f16bits, 0u));
+    };
+
+    auto compute_q8_0 = [&](const uint8_t *st) {
+        const uint8_t *arow = st + (wave * 16 + li) * WROW;
+        const uint8_t *bcol[NCT];
+        uint4 dh0[NCT], dh1[NCT];
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) col_headers(st, j, bcol[j], dh0[j], dh1[j]);
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const uint8_t *blk = arow + g * Q80_BYTES;
+            const uint2 a = lds8_a2(blk + 2 + 8 * kq);
+            const uint32_t dw = (uint32_t)*reinterpret_cast<const uint16_t *>(blk) & m_sc;
+            const v4h sa = scale_a(g, dw);
+            const int c = 2 * g + (kq >> 1);
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) {
+                const uint2 b = *reinterpret_cast<const uint2 *>(bcol[j] + 16 * (c ^ li) + 8 * (kq & 1));
+                const v4i zi = {0, 0, 0, 0};
+                const v4i S = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a), as_long(b), zi, 0, 0, 0);
+                const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+                const v4f SC = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, scale_b(g, dh0[j], dh1[j]), zf, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[j][v] = fmaf((float)S[v], SC[v], acc[j][v]);
+            }
+        }
+    };
+
+    auto compute_q6_k = [&](const uint8_t *st, int kb) {
+        const int delta = (int)(((int64_t)kb * Q6K_BYTES) & 15);  // the block's start in the window
+        const uint8_t *blk = st + (wave * 16 + li) * WROW + delta;
+        const uint8_t *bcol[NCT];
+        uint4 dh0[NCT], dh1[NCT];
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) col_headers(st, j, bcol[j], dh0[j], dh1[j]);
+        v4f accb[NCT];
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) accb[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        // two 32-weight chunks per pass keep the registers below the spill line
+#pragma unroll 2
+        for (int g = 0; g < 8; ++g) {
+            const int n = g >> 2, m = g & 3;
+            const uint2 ql = lds8_a2(blk + 64 * n + 32 * (m & 1) + 8 * kq);
+            const uint2 qh = lds8_a2(blk + 128 + 32 * n + 8 * kq);
+            const int sl = 4 * (m >> 1), shh = 2 * m;
+            const uint32_t v0 = q6_signed(((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> shh) & 0x03030303u) << 4));
+            const uint32_t v1 = q6_signed(((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> shh) & 0x03030303u) << 4));
+            // sub-block 2g is the lanes' K-slices 0, 1 (kq < 2), sub-block 2g+1 slices 2, 3
+            const uint2 a_lo = kq < 2 ? make_uint2(v0, v1) : make_uint2(0u, 0u);
+            const uint2 a_hi = kq < 2 ? make_uint2(0u, 0u) : make_uint2(v0, v1);
+            // the row's int8 scales of sub-blocks 2g and 2g+1
+            const uint32_t w2 = *reinterpret_cast<const uint16_t *>(blk + 192 + 2 * g);
+            const uint32_t sc0 = f16_bits((float)(int8_t)w2) & m_sc;
+            const uint32_t sc1 = f16_bits((float)(int8_t)(w2 >> 8)) & m_sc;
+            const v4h sa0 = scale_a(g, sc0), sa1 = scale_a(g, sc1);
+            const int c = 2 * g + (kq >> 1);
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) {
+                const uint2 b = *reinterpret_cast<const uint2 *>(bcol[j] + 16 * (c ^ li) + 8 * (kq & 1));
+                const v4i zi = {0, 0, 0, 0};
+                const v4i S0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a_lo), as_long(b), zi, 0, 0, 0);
+                const v4i S1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a_hi), as_long(b), zi, 0, 0, 0);
+                const v4h sb = scale_b(g, dh0[j], dh1[j]);
+                const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+                const v4f SC0 = __builtin_amdgcn_mfma_f32_16x16x16f16(sa0, sb, zf, 0, 0, 0);
+                const v4f SC1 = __builtin_amdgcn_mfma_f32_16x16x16f16(sa1, sb, zf, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) accb[j][v] = fmaf((float)S1[v], SC1[v], fmaf((float)S0[v], SC0[v], accb[j][v]));
+            }
+        }
+        // d of the output rows (4*kq + v of this wave's 16)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint8_t *ob = st + (wave * 16 + 4 * kq + v) * WROW + delta;
+            const float d = h2f((uint32_t)*reinterpret_cast<const uint16_t *>(ob + 208));
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) acc[j][v] = fmaf(d, accb[j][v], acc[j][v]);
+        }
+    };
 
     auto compute = [&](const uint8_t *st) {
         const uint8_t *arow = st + (wave * 16 + li) * Q4K_BYTES;
@@ -271,7 +425,9 @@ __global__ __launch_bounds__((FewGeo<NW, NCT>::NT), (few_occupancy<NW, NCT>(NST)
             wait_step<NST - 2, G::transfers_of(0), G::transfers_of(NW - 1)>(big, left < NST - 2 ? left : NST - 2);
             lds_barrier();
             if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
-            compute(st[i]);
+            if constexpr (TYPE == TYPE_Q4_K) compute(st[i]);
+            else if constexpr (TYPE == TYPE_Q8_0) compute_q8_0(st[i]);
+            else compute_q6_k(st[i], kb);
             if (++kb >= kb1) break;
         }
     }
@@ -317,25 +473,48 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
     return (int)split;
 }
 
-// Launch for mmq.hip's dispatch: Q4_K rows 16-byte aligned (row_stride % 16 ==
-// 0), the activation planes 16-byte aligned, 1 <= ncols <= 32, K % 256 == 0,
-// which the caller checks.  `partial` (split * nrows * ncols floats) takes the
+// Whether the few-column kernel takes this weight layout: Q4_K; Q8_0 and
+// Q6_K with 16-byte-aligned rows (and, Q6_K, K % 2048 == 0, so that its
+// aligned windows stay inside the row).
+bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride) {
+    if (type == TYPE_Q4_K) return true;
+    if (type != TYPE_Q8_0 && type != TYPE_Q6_K) return false;
+    if ((uintptr_t)w % 16 || row_stride % 16 || K % QK_K) return false;
+    return type == TYPE_Q8_0 || K % 2048 == 0;
+}
+
+// Launch for mmq.hip's dispatch: the rows as mmq_few_takes says, the
+// activation planes 16-byte aligned, 1 <= ncols <= 32 (Q6_K: 16), K % 256 ==
+// 0, which the caller checks.  `partial` (split * nrows * ncols floats) takes the
 // split-K partials when split > 1.
-int mmq_few_q4k_launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
-                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
-                       hipStream_t s) {
+int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                   const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int split, float *partial,
+                   hipStream_t s) {
     const int64_t gx = (nrows + 16 * FEW_NW - 1) / (16 * FEW_NW);
-    if (ncols < 1 || ncols > FBN || gx > 0x7FFFFFFF || split < 1 || split > 16 || K / QK_K > 0x7FFFFFFF)
+    if (ncols < 1 || ncols > FBN || gx > 0x7FFFFFFF || split < 1 || split > 16 || K / QK_K > 0x7FFFFFFF ||
+        !mmq_few_takes(type, K, w, row_stride))
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, 1, (unsigned)split);
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     float *pp = split > 1 ? partial : nullptr;
-#define FEW_LAUNCH(NST, NW, NCT)                                                                                       \
-    hipLaunchKernelGGL((mmq_few_q4k_kernel<NST, NW, NCT>), grid, dim3(64 * NW), 0, s, wb, K, nrows, row_stride, yqs,   \
-                       ds, (int)ncols, dst, dst_col_stride, pp)
-    if (ncols > 16) FEW_LAUNCH(FEW_NST, FEW_NW, 2);
-    else FEW_LAUNCH(FEW_NST, FEW_NW, 1);
+#define FEW_LAUNCH(TYPE, NCT)                                                                                          \
+    hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT>), grid, dim3(64 * FEW_NW), 0, s, wb, K, nrows,      \
+                       row_stride, yqs, ds, (int)ncols, dst, dst_col_stride, pp)
+    switch (type) {
+    case TYPE_Q8_0:
+        if (ncols > 16) FEW_LAUNCH(TYPE_Q8_0, 2);
+        else FEW_LAUNCH(TYPE_Q8_0, 1);
+        break;
+    case TYPE_Q6_K:  // one column tile: two measured slower than the 128-row MMQ tile
+        if (ncols > 16) return (int)hipErrorInvalidValue;
+        FEW_LAUNCH(TYPE_Q6_K, 1);
+        break;
+    default:
+        if (ncols > 16) FEW_LAUNCH(TYPE_Q4_K, 2);
+        else FEW_LAUNCH(TYPE_Q4_K, 1);
+        break;
+    }
 #undef FEW_LAUNCH
     return (int)hipGetLastError();
 }

@@ -100,3 +100,41 @@ def test_op_few_columns(nrows, K, ncols):
     assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
     cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
     assert nmse(got, cpu) < NMSE_GATE
+
+
+def _offset_copy(w_d, off=2):
+    """The same weight rows at a base `off` bytes past 16-byte alignment (a
+    contiguous view into a larger buffer)."""
+    buf = torch.zeros(w_d.numel() + 16, dtype=torch.uint8, device="cuda")
+    v = buf[off:off + w_d.numel()].view(w_d.shape)
+    v.copy_(w_d)
+    return v
+
+
+@pytest.mark.parametrize("tname", ["Q6_K", "Q8_0"])
+@pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 3), (4096, 2048, 9), (700, 14336, 17), (4100, 4096, 32),
+                                           (64, 2048, 16)])
+def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
+    """Q8_0 with at most 32 columns and Q6_K with at most 16 take the
+    few-column kernel on 16-byte-aligned rows (Q6_K from K % 2048 == 0):
+    within the f64 and CPU gates, and within rounding of the 128-row MMQ tile
+    that the same rows take at a 2-byte-aligned base (and Q6_K at 17-32
+    columns)."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    got = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    tile = G.mmq(tname, _offset_copy(w_d), K, qs, ds).cpu().numpy()
+    assert max_err_scaled(got, tile) < 1e-6
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
+    cpu = O.mul_mat_x86(t, wq, nrows, K, x, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE
+    # the op at > 8 columns goes through the same dispatch
+    if ncols > 8:
+        np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
