@@ -170,6 +170,20 @@ class HipBackend:
         del keep
         return st
 
+    def compute_view(self, nodes, i0, i1):
+        """Run nodes[i0:i1] as the scheduler runs a split: a view of the whole
+        graph's node array (ggml_graph_view, src/ggml/graph.zig) that shares
+        its hash set and use counts, so uses by nodes outside the split count."""
+        g, keep = self._graph(nodes, True)
+        view = abi.ggml_cgraph()
+        C.memmove(C.addressof(view), C.addressof(g), C.sizeof(g))
+        view.size = view.n_nodes = i1 - i0
+        view.nodes = C.cast(C.addressof(keep[0]) + i0 * C.sizeof(abi.PT), C.POINTER(abi.PT))
+        st = self.be.iface.graph_compute(self.be_ptr, C.pointer(view))
+        self.be.iface.synchronize(self.be_ptr)
+        del keep
+        return st
+
     def optimized(self, nodes, use_counts=True):
         """The backend's graph_optimize on a graph of `nodes`: the node order
         it leaves and the (tensor, until) allocation dependencies it adds,
