@@ -66,6 +66,7 @@ enum ggml_type {
 enum ggml_op {
     GGML_OP_NONE = 0,
     GGML_OP_ADD = 2,
+    GGML_OP_ADD_ID = 3,
     GGML_OP_MUL_MAT = 28,
     GGML_OP_MUL_MAT_ID = 29,
     GGML_OP_RESHAPE = 35,

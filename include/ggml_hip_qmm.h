@@ -178,6 +178,21 @@ int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void *w_gate, in
                                  float *dst, int64_t dst_row_stride, void *stream);
 
 /*
+ * hip_qmm_mul_mat_id_vec_fused with per-expert biases (the MUL_MAT_ID bias
+ * lanes, ADD_ID nodes, of src/ggml/cuda/fusion.zig:1308-1360, 1482-1520;
+ * the x_bias / gate_bias fusion arguments of mmvq.zig:591-610): the row of
+ * pair (t, s) with expert e adds bias + e*bias_expert_stride (u, before the
+ * GLU) and gate_bias + e*bias_expert_stride (g); either may be NULL, gate_bias
+ * only with w_gate.  bias_expert_stride >= nrows (floats).
+ */
+int hip_qmm_mul_mat_id_vec_fused_bias(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                      int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
+                                      int64_t ne11, int64_t n_tokens, int64_t x_row_stride, const int32_t *ids,
+                                      int64_t n_ids, int64_t ids_stride, const float *bias, const float *gate_bias,
+                                      int64_t bias_expert_stride, int glu_op, float glu_alpha, float glu_limit,
+                                      float *dst, int64_t dst_row_stride, void *stream);
+
+/*
  * hip_qmm_mul_mat_id_vec_fused (gated, one activation row per token, ne11 = 1)
  * with a shared expert in the same launch: the reference's shared_up /
  * shared_gate / shared_dst fusion arguments (src/ggml/cuda/common.zig:1448-1459,
@@ -194,6 +209,18 @@ int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, const void *w_g
                                         int64_t ids_stride, int glu_op, float glu_alpha, float glu_limit, float *dst,
                                         int64_t dst_row_stride, const void *shared_up, const void *shared_gate,
                                         float *shared_dst, int64_t shared_dst_row_stride, void *stream);
+
+/*
+ * Standalone ADD_ID (ggml_compute_forward_add_id_f32,
+ * src/ggml/cpu/ops/arith.zig:155-213) over n_tokens x n_slots rows of nc floats:
+ * dst[t*dst_token_stride + s*dst_slot_stride + i] = a[...] + b[ids[t*ids_stride + s]*b_row_stride + i],
+ * or a[...] alone where the id is -1 (or outside [0, n_b), which the reference
+ * asserts against).  Strides in floats (ids: int32 elements).
+ */
+int hip_qmm_add_id_f32(int64_t nc, int64_t n_slots, int64_t n_tokens, const float *a, int64_t a_slot_stride,
+                       int64_t a_token_stride, const float *b, int64_t b_row_stride, int64_t n_b, const int32_t *ids,
+                       int64_t ids_stride, float *dst, int64_t dst_slot_stride, int64_t dst_token_stride,
+                       void *stream);
 
 /*
  * Standalone GLU over rows of f32 (ggml_compute_forward_glu,

@@ -616,6 +616,18 @@ bool run_add(BackendCtx *ctx, const ggml_tensor *node) {
     return true;
 }
 
+// dst row (s, t) = src0 row + src1 row ids[t][s] (ggml_add_id; -1: src0 alone).
+bool run_add_id(BackendCtx *ctx, const ggml_tensor *node) {
+    const ggml_tensor *a = node->src[0], *b = node->src[1], *ids = node->src[2];
+    const int rc = hip_qmm_add_id_f32(node->ne[0], node->ne[1], node->ne[2], static_cast<const float *>(a->data),
+                                      (int64_t)(a->nb[1] / 4), (int64_t)(a->nb[2] / 4),
+                                      static_cast<const float *>(b->data), (int64_t)(b->nb[1] / 4), b->ne[1],
+                                      static_cast<const int32_t *>(ids->data), (int64_t)(ids->nb[1] / 4),
+                                      static_cast<float *>(node->data), (int64_t)(node->nb[1] / 4),
+                                      (int64_t)(node->nb[2] / 4), ctx->stream);
+    return report(rc, "hip_qmm_add_id_f32", node);
+}
+
 // ---------------------------------------------------------------- fusion
 //
 // The mul_mat_vec fusions of the reference's CUDA backend
@@ -887,6 +899,51 @@ bool launch_shared_expert(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok
     return true;
 }
 
+// ---- MUL_MAT_ID bias lanes (ADD_ID; fusion.zig:1308-1360 gated,
+// :1482-1520 one lane): the ADD_ID reads the MUL_MAT_ID as src0, with the same
+// ids, and its src1 is the per-expert bias [nrows, n_as].
+const ggml_tensor *id_bias_of(const ggml_tensor *add_id, const ggml_tensor *mm) {
+    if (add_id->op != GGML_OP_ADD_ID || add_id->src[0] != mm || add_id->src[2] != mm->src[2]) return nullptr;
+    const ggml_tensor *b = add_id->src[1], *w = mm->src[0];
+    if (!b || b->type != GGML_TYPE_F32 || b->nb[0] != 4 || b->nb[1] % 4 || b->ne[0] != w->ne[1] ||
+        b->ne[1] != w->ne[2] || !same_shape(add_id, mm))
+        return nullptr;
+    return b;
+}
+
+// A lone MUL_MAT_ID the fused ids kernel takes (the gated check without a gate).
+bool id_lane_fusable(const ggml_tensor *mm, const ggml_tensor *out) {
+    const ggml_tensor *w = mm->src[0], *x = mm->src[1];
+    if (out->type != GGML_TYPE_F32 || out->nb[0] != 4 || out->nb[1] % 4 ||
+        out->nb[2] != (size_t)out->ne[1] * out->nb[1])
+        return false;
+    const int64_t K = w->ne[0], n_tokens = x->ne[2];
+    const size_t walign = weight_align(w->type);
+    return n_tokens <= 8 && n_tokens * out->ne[1] <= 65535 && K % 32 == 0 && K <= 32768 &&
+           (uintptr_t)x->data % 16 == 0 && x->nb[1] % 16 == 0 && x->nb[2] == (size_t)x->ne[1] * x->nb[1] &&
+           (uintptr_t)w->data % walign == 0 && w->nb[1] % walign == 0 && w->nb[2] % walign == 0;
+}
+
+bool launch_fused_id_bias(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *ub,
+                          const ggml_tensor *gb, const ggml_tensor *out, bool *ok) {
+    const ggml_tensor *w = up->src[0], *x = up->src[1], *ids = up->src[2];
+    const int64_t K = w->ne[0], M = w->ne[1];
+    if (gb && gb->nb[1] != ub->nb[1]) return false;  // one expert stride for both biases
+    const size_t ob = nbytes(out);
+    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids)) ||
+        overlaps(out->data, ob, ub->data, nbytes(ub)) || (gb && overlaps(out->data, ob, gb->data, nbytes(gb))))
+        return false;
+    const int rc = hip_qmm_mul_mat_id_vec_fused_bias(
+        w->type, w->data, gate ? gate->src[0]->data : nullptr, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
+        static_cast<const float *>(x->data), x->ne[1], x->ne[2], (int64_t)(x->nb[1] / 4),
+        static_cast<const int32_t *>(ids->data), ids->ne[0], (int64_t)(ids->nb[1] / 4),
+        static_cast<const float *>(ub->data), gb ? static_cast<const float *>(gb->data) : nullptr,
+        (int64_t)(ub->nb[1] / 4), gate ? out->op_params[0] : 0, gate ? op_param_f32(out, 2) : 0.0f,
+        gate ? op_param_f32(out, 3) : 0.0f, static_cast<float *>(out->data), (int64_t)(out->nb[1] / 4), ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_id_vec_fused_bias", out);
+    return true;
+}
+
 // Nodes consumed by a fused launch at node i (0: none); *ok false on a failed launch.
 int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
     if (fusion_disabled()) return 0;
@@ -894,13 +951,36 @@ int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
     auto is = [&](int k, int op) { return node(k) && node(k)->op == op && ggml_backend_hip_op_supported(node(k)); };
     if (g->nodes[i]->op == GGML_OP_MUL_MAT_ID) {
         if (match_shared_expert(g, i, i + 3) && launch_shared_expert(ctx, g, i, ok)) return 6;
-        if (!is(i + 1, GGML_OP_MUL_MAT_ID) || !is(i + 2, GGML_OP_GLU)) return 0;
-        const ggml_tensor *glu = node(i + 2);
-        const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
-        const bool pair = (gate == node(i) && up == node(i + 1)) || (gate == node(i + 1) && up == node(i));
-        if (pair && gate_up_id_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
-            launch_fused_id(ctx, up, gate, glu, ok))
-            return 3;
+        if (is(i + 1, GGML_OP_ADD_ID) && is(i + 2, GGML_OP_MUL_MAT_ID) && is(i + 3, GGML_OP_ADD_ID) &&
+            is(i + 4, GGML_OP_GLU)) {
+            // which lane gates follows from the GLU's sources (fusion.zig:1313-1325)
+            const ggml_tensor *glu = node(i + 4), *ma = node(i), *mb = node(i + 2);
+            const ggml_tensor *gbn = glu->src[0], *ubn = glu->src[1];
+            const bool a_gates = gbn == node(i + 1) && ubn == node(i + 3);
+            const bool b_gates = gbn == node(i + 3) && ubn == node(i + 1);
+            if (a_gates || b_gates) {
+                const ggml_tensor *gate = a_gates ? ma : mb, *up = a_gates ? mb : ma;
+                const ggml_tensor *gb = id_bias_of(gbn, gate), *ub = id_bias_of(ubn, up);
+                if (gb && ub && !in_run(g, i, 5, gb) && !in_run(g, i, 5, ub) && gate_up_id_fusable(up, gate, glu) &&
+                    run_is_closed(g, i, 5, glu) && launch_fused_id_bias(ctx, up, gate, ub, gb, glu, ok))
+                    return 5;
+            }
+        }
+        if (is(i + 1, GGML_OP_MUL_MAT_ID) && is(i + 2, GGML_OP_GLU)) {
+            const ggml_tensor *glu = node(i + 2);
+            const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
+            const bool pair = (gate == node(i) && up == node(i + 1)) || (gate == node(i + 1) && up == node(i));
+            if (pair && gate_up_id_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
+                launch_fused_id(ctx, up, gate, glu, ok))
+                return 3;
+        }
+        if (is(i + 1, GGML_OP_ADD_ID)) {
+            const ggml_tensor *mm = node(i), *add = node(i + 1);
+            const ggml_tensor *b = id_bias_of(add, mm);
+            if (b && !in_run(g, i, 2, b) && id_lane_fusable(mm, add) && run_is_closed(g, i, 2, add) &&
+                launch_fused_id_bias(ctx, mm, nullptr, b, nullptr, add, ok))
+                return 2;
+        }
         return 0;
     }
     if (g->nodes[i]->op != GGML_OP_MUL_MAT) return 0;
@@ -960,6 +1040,7 @@ ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
         case GGML_OP_MUL_MAT: ok = run_mul_mat(ctx, node); break;
         case GGML_OP_MUL_MAT_ID: ok = run_mul_mat_id(ctx, node); break;
         case GGML_OP_GLU: ok = run_glu(ctx, node); break;
+        case GGML_OP_ADD_ID: ok = run_add_id(ctx, node); break;
         default: ok = run_add(ctx, node); break;
         }
         if (!ok) return GGML_STATUS_FAILED;
@@ -1148,7 +1229,8 @@ bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
     // With fusion off (GGML_HIP_DISABLE_FUSION) the GLU and bias-add nodes
     // have no reason to stay on the device: the answer narrows to MUL_MAT /
     // MUL_MAT_ID and the no-op views, and everything else stays on the CPU.
-    if ((op->op == GGML_OP_GLU || op->op == GGML_OP_ADD) && fusion_disabled()) return false;
+    if ((op->op == GGML_OP_GLU || op->op == GGML_OP_ADD || op->op == GGML_OP_ADD_ID) && fusion_disabled())
+        return false;
     if (op->op == GGML_OP_GLU) {
         // f32 GLU of a device op (glu_op_supported), split or one-tensor form
         const ggml_tensor *a = op->src[0], *b = op->src[1];
@@ -1163,6 +1245,15 @@ bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
         // same-shape f32 add (the bias add of the GEMV fusion); no broadcasting
         const ggml_tensor *a = op->src[0], *b = op->src[1];
         return a && b && f32_rows(a) && f32_rows(b) && f32_rows(op) && same_shape(a, b) && same_shape(a, op);
+    }
+    if (op->op == GGML_OP_ADD_ID) {
+        // f32 rows plus a row of b chosen per (slot, token) by int32 ids (the
+        // per-expert bias of an MoE projection, ggml_add_id, ops.zig:113-130)
+        const ggml_tensor *a = op->src[0], *b = op->src[1], *ids = op->src[2];
+        if (!a || !b || !ids || !f32_rows(a) || !f32_rows(b) || !f32_rows(op) || !same_shape(a, op)) return false;
+        if (ids->type != GGML_TYPE_I32 || ids->nb[0] != 4 || ids->nb[1] % 4 != 0) return false;
+        return b->ne[0] == a->ne[0] && ids->ne[0] == a->ne[1] && ids->ne[1] == a->ne[2] && a->ne[3] == 1 &&
+               b->ne[2] == 1 && b->ne[3] == 1;
     }
     if (op->op != GGML_OP_MUL_MAT && op->op != GGML_OP_MUL_MAT_ID) return false;
     const ggml_tensor *a = op->src[0], *b = op->src[1];

@@ -701,6 +701,9 @@ struct FxIds {
     float *shared_dst;
     int64_t shared_dst_row_stride;
     int n_shared;
+    // per-expert biases (ADD_ID): the routed rows of expert e add bias +
+    // e * bias_expert_stride (and gate_bias likewise)
+    int64_t bias_expert_stride;
 };
 
 template <int TYPE, int FW, int R, bool GATE, bool IDS, int SEG, int KS>
@@ -759,6 +762,15 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
     // the share's K-steps [s0, s1) (KS = 1: all of them)
     const int nsteps = (K32 + STEP - 1) / STEP;
     const int s0 = kh * nsteps / KS, s1 = (kh + 1) * nsteps / KS;
+    // IDS: the routed expert's bias rows (the id clamped to a valid expert
+    // for the address; an invalid id's row is zero and the value unused)
+    if constexpr (IDS) {
+        if (!shared) {
+            const int64_t eb = (int64_t)(expert >= 0 && expert < fi.n_as ? expert : 0) * fi.bias_expert_stride;
+            if (bias) bias += eb;
+            if (gbias) gbias += eb;
+        }
+    }
     // lane rows: row0 + r * NSEG + seg, clamped for loading
     int64_t rowc[R];
     float bu[R], bg[R];
@@ -1410,7 +1422,8 @@ int id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t
                  int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
                  int64_t x_row_stride, const int32_t *ids, int64_t n_ids, int64_t ids_stride, int glu_op,
                  float glu_alpha, float glu_limit, float *dst, int64_t dst_row_stride, const FxShared *sh,
-                 void *stream) {
+                 const float *bias, const float *gate_bias, int64_t bias_expert_stride, void *stream) {
+    if ((bias || gate_bias) && (sh || bias_expert_stride < nrows)) return (int)hipErrorInvalidValue;
     if (!ids || n_as <= 0 || n_as > 0x7FFFFFFF || n_tokens <= 0 || n_ids <= 0 || ids_stride < n_ids ||
         (ne11 != 1 && ne11 != n_ids) || x_row_stride < K || x_row_stride % 4 || dst_row_stride < nrows)
         return (int)hipErrorInvalidValue;
@@ -1424,14 +1437,14 @@ int id_vec_fused(int type, const void *w, const void *w_gate, int64_t K, int64_t
         return (int)hipErrorInvalidValue;
     FxIds fi{ids, ids_stride, x_row_stride, expert_stride, dst_row_stride,
              (int)n_ids, (int)ne11, (int)n_as, (int)(n_tokens * n_ids),
-             nullptr, nullptr, nullptr, 0, (int)n_shared};
+             nullptr, nullptr, nullptr, 0, (int)n_shared, bias_expert_stride};
     if (sh) {
         fi.shared_up = (const uint8_t *)sh->up;
         fi.shared_gate = (const uint8_t *)sh->gate;
         fi.shared_dst = sh->dst;
         fi.shared_dst_row_stride = sh->dst_row_stride;
     }
-    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op, glu_alpha, glu_limit, dst,
+    return fused_launch(type, w, w_gate, K, nrows, row_stride, x, bias, gate_bias, glu_op, glu_alpha, glu_limit, dst,
                         &fi, stream);
 }
 
@@ -1443,7 +1456,20 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused(int type, const void *w, const void 
                                             int64_t n_ids, int64_t ids_stride, int glu_op, float glu_alpha,
                                             float glu_limit, float *dst, int64_t dst_row_stride, void *stream) {
     return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, ne11, n_tokens, x_row_stride,
-                        ids, n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, nullptr, stream);
+                        ids, n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, nullptr, nullptr,
+                        nullptr, 0, stream);
+}
+
+extern "C" int hip_qmm_mul_mat_id_vec_fused_bias(int type, const void *w, const void *w_gate, int64_t K,
+                                                 int64_t nrows, int64_t row_stride, int64_t expert_stride,
+                                                 int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
+                                                 int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
+                                                 int64_t ids_stride, const float *bias, const float *gate_bias,
+                                                 int64_t bias_expert_stride, int glu_op, float glu_alpha,
+                                                 float glu_limit, float *dst, int64_t dst_row_stride, void *stream) {
+    return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, ne11, n_tokens, x_row_stride,
+                        ids, n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, nullptr, bias,
+                        gate_bias, bias_expert_stride, stream);
 }
 
 extern "C" int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, const void *w_gate, int64_t K,
@@ -1456,7 +1482,8 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, cons
                                                    int64_t shared_dst_row_stride, void *stream) {
     const FxShared sh{shared_up, shared_gate, shared_dst, shared_dst_row_stride};
     return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, 1, n_tokens, x_row_stride, ids,
-                        n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, &sh, stream);
+                        n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, &sh, nullptr, nullptr, 0,
+                        stream);
 }
 
 // 2-4 f32 columns through the quantize-in-GEMV kernel (hip_qmm_mul_mat's

@@ -61,6 +61,12 @@ def lib():
         L.hip_qmm_mul_mat_id_vec_fused_shared.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, vp,
                                                           i64, i64, i32, ctypes.c_float, ctypes.c_float, vp, i64, vp,
                                                           vp, vp, i64, vp]
+        L.hip_qmm_mul_mat_id_vec_fused_bias.restype = i32
+        L.hip_qmm_mul_mat_id_vec_fused_bias.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp,
+                                                        i64, i64, vp, vp, i64, i32, ctypes.c_float, ctypes.c_float, vp,
+                                                        i64, vp]
+        L.hip_qmm_add_id_f32.restype = i32
+        L.hip_qmm_add_id_f32.argtypes = [i64, i64, i64, vp, i64, i64, vp, i64, i64, vp, i64, vp, i64, i64, vp]
         L.hip_qmm_glu_f32.restype = i32
         L.hip_qmm_glu_f32.argtypes = [i32, ctypes.c_float, ctypes.c_float, i64, i64, vp, i64, vp, i64, vp, i64, vp]
         L.hip_qmm_add_f32.restype = i32
@@ -236,6 +242,38 @@ def mul_mat_id_vec_fused(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Ten
                                               w.stride(1), w.stride(0), n_as, _ptr(x), ne11, n_tokens, K, _ptr(ids),
                                               n_ids, n_ids, op, alpha, limit, _ptr(out), nrows, _stream()),
            "hip_qmm_mul_mat_id_vec_fused")
+    return out
+
+
+def mul_mat_id_vec_fused_bias(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, bias: torch.Tensor,
+                              w_gate=None, gate_bias=None, glu="SWIGLU", alpha=1.702, limit=7.0, out=None):
+    """mul_mat_id_vec_fused with per-expert biases: bias / gate_bias f32
+    [n_as, nrows] (row e for expert e), added to u / g before the GLU."""
+    _require_cuda(w, x, ids, bias)
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    n_as, nrows, rb = w.shape
+    n_tokens, ne11, K = x.shape
+    n_ids = ids.shape[1]
+    if (rb < row_size(t, K) or ids.shape[0] != n_tokens or tuple(bias.shape) != (n_as, nrows) or
+            (gate_bias is not None and (w_gate is None or gate_bias.shape != bias.shape))):
+        raise HipQmmError("bad mul_mat_id bias shapes")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty((n_tokens, n_ids, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_id_vec_fused_bias(
+        t, _ptr(w), _ptr(w_gate) if w_gate is not None else None, K, nrows, w.stride(1), w.stride(0), n_as, _ptr(x),
+        ne11, n_tokens, K, _ptr(ids), n_ids, n_ids, _ptr(bias), _ptr(gate_bias) if gate_bias is not None else None,
+        bias.stride(0), op, alpha, limit, _ptr(out), nrows, _stream()), "hip_qmm_mul_mat_id_vec_fused_bias")
+    return out
+
+
+def add_id_f32(a: torch.Tensor, b: torch.Tensor, ids: torch.Tensor, out=None):
+    """ggml_add_id: a [n_tokens, n_slots, nc] + b[ids[t, s]] (b [n_b, nc]); -1 ids copy a."""
+    _require_cuda(a, b, ids)
+    n_tokens, n_slots, nc = a.shape
+    out = torch.empty_like(a) if out is None else out
+    _check(lib().hip_qmm_add_id_f32(nc, n_slots, n_tokens, _ptr(a), a.stride(1), a.stride(0), _ptr(b), b.stride(0),
+                                    b.shape[0], _ptr(ids), ids.stride(0), _ptr(out), out.stride(1), out.stride(0),
+                                    _stream()), "hip_qmm_add_id_f32")
     return out
 
 

@@ -22,7 +22,7 @@ GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q4_0, GGML_TYPE_Q8_0, GGML_TYPE_Q8_1 = 0
 GGML_TYPE_Q4_K, GGML_TYPE_Q5_K, GGML_TYPE_Q6_K, GGML_TYPE_Q8_K, GGML_TYPE_I32 = 12, 13, 14, 15, 26
 GGML_TYPE_IQ4_XS = 23
 # ggml_op ids (position in op_name)
-GGML_OP_NONE, GGML_OP_ADD, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT_ID = 0, 2, 28, 29
+GGML_OP_NONE, GGML_OP_ADD, GGML_OP_ADD_ID, GGML_OP_MUL_MAT, GGML_OP_MUL_MAT_ID = 0, 2, 3, 28, 29
 GGML_OP_RESHAPE, GGML_OP_VIEW, GGML_OP_PERMUTE, GGML_OP_TRANSPOSE = 35, 36, 37, 38
 GGML_OP_GLU = 98
 # ggml_glu_op ids

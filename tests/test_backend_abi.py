@@ -222,7 +222,7 @@ def test_fused_and_elementwise_entry_points_reject_bad_arguments(L):
 
 def test_fusion_off_narrows_supports_op_to_mul_mat():
     """With GGML_HIP_DISABLE_FUSION=1 the device keeps only MUL_MAT /
-    MUL_MAT_ID and the no-op views: GLU and ADD go back to the CPU, which is
+    MUL_MAT_ID and the no-op views: GLU, ADD and ADD_ID go back to the CPU, which is
     the strict boundary of the quantized-matmul path.  Runs in a fresh
     process, since the library reads the variable once."""
     import os
@@ -239,6 +239,9 @@ ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))
 g = abi.make_tensor(abi.GGML_TYPE_F32, [64, 1]); u = abi.make_tensor(abi.GGML_TYPE_F32, [64, 1])
 assert not ok(abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g, u, [64, 1]))
 assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [64, 1], op=abi.GGML_OP_ADD, srcs=(g, u)))
+mm3 = abi.make_tensor(abi.GGML_TYPE_F32, [64, 2, 3]); b = abi.make_tensor(abi.GGML_TYPE_F32, [64, 4])
+ids = abi.make_tensor(abi.GGML_TYPE_I32, [2, 3])
+assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [64, 2, 3], op=abi.GGML_OP_ADD_ID, srcs=(mm3, b, ids)))
 assert ok(T.mm(abi.GGML_TYPE_Q4_K, 4096, 4096, 1)[2])
 assert ok(T.mmid(abi.GGML_TYPE_Q6_K, 2048, 768, 128, 8, 512)[3])
 assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=abi.GGML_OP_VIEW))
@@ -278,3 +281,21 @@ def test_scaled_gate_up_lane_is_not_taken(L):
         s = abi.make_tensor(abi.GGML_TYPE_F32, [1], name=b"scale")
         scaled = abi.make_tensor(abi.GGML_TYPE_F32, [4096, 1], op=GGML_OP_MUL, srcs=(d, s))
         assert not ok(scaled)
+
+
+def test_supports_add_id(L):
+    """ADD_ID (ggml_add_id, src/ggml/ops.zig:113-130): f32 rows plus the row
+    of b the int32 ids pick, the per-expert bias of an MoE projection."""
+    from ggml_hip import abi
+    ok = lambda t: L.ggml_backend_hip_op_supported(C.pointer(t))  # noqa: E731
+    a = abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], name=b"mm")
+    b = abi.make_tensor(abi.GGML_TYPE_F32, [768, 128], name=b"bias")
+    ids = abi.make_tensor(abi.GGML_TYPE_I32, [8, 5], name=b"ids")
+    add = abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, b, ids))
+    assert ok(add)
+    bad_b = abi.make_tensor(abi.GGML_TYPE_F32, [512, 128], name=b"bias")
+    assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, bad_b, ids)))
+    bad_ids = abi.make_tensor(abi.GGML_TYPE_I32, [4, 5], name=b"ids")
+    assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, b, bad_ids)))
+    f16_ids = abi.make_tensor(abi.GGML_TYPE_F16, [8, 5], name=b"ids")
+    assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, b, f16_ids)))

@@ -553,3 +553,101 @@ def test_plugin_groups_and_fuses_shared_expert(hb):
     u2, g2 = hb.get(sup, np.float32, ssh), hb.get(sgate, np.float32, ssh)
     assert nmse(hb.get(glu_s, np.float32, ssh), s_out) < 1e-10
     assert nmse(O.glu(O.GLU_SWIGLU, g2, u2), s_out) < 1e-10
+
+
+# ---------------------------------------------------------------- MUL_MAT_ID bias lanes (ADD_ID)
+
+def test_add_id_kernel_exact():
+    """ADD_ID rows equal a + b[id] in f32 exactly; -1 ids copy the row."""
+    import ggml_hip as G
+    rng = np.random.default_rng(12)
+    T_, S, nc, n_b = 5, 8, 777, 16
+    a = rng.standard_normal((T_, S, nc)).astype(np.float32)
+    b = rng.standard_normal((n_b, nc)).astype(np.float32)
+    ids = rng.integers(-1, n_b, size=(T_, S)).astype(np.int32)
+    got = G.add_id_f32(_dev(a), _dev(b), _dev(ids)).cpu().numpy()
+    want = np.where((ids >= 0)[:, :, None], a + b[np.maximum(ids, 0)], a)
+    np.testing.assert_array_equal(got, want)
+
+
+def _moe_bias(n_as, M, seed):
+    rng = np.random.default_rng(900 + seed)
+    return ((rng.standard_normal((n_as, M)) * 0.5).astype(np.float32),
+            (rng.standard_normal((n_as, M)) * 0.5).astype(np.float32))
+
+
+@pytest.mark.parametrize("tname,n_tokens,opname", [("Q4_K", 1, "SWIGLU_OAI"), ("Q8_0", 3, "SWIGLU"),
+                                                    ("Q6_K", 8, "GEGLU")])
+def test_fused_gate_up_glu_with_ids_and_biases(tname, n_tokens, opname):
+    """gpt-oss style MoE FFN with per-expert biases in one launch: equal bit
+    for bit to the unfused GPU sequence (ids GEMV, ADD_ID, GLU) and within the
+    CPU gate; the one-lane form equals ids GEMV + ADD_ID."""
+    import ggml_hip as G
+    n_as, M, K, n_ids = 16, 768, 1024, 4
+    t, wu, wg, ids, x = _moe(tname, n_as, M, K, n_tokens, n_ids, 30 + n_tokens)
+    ids[0, 0] = -1
+    bu, bg = _moe_bias(n_as, M, n_tokens)
+    wu_d, wg_d, x_d, ids_d, bu_d, bg_d = _dev(wu), _dev(wg), _dev(x), _dev(ids), _dev(bu), _dev(bg)
+    got = G.mul_mat_id_vec_fused_bias(tname, wu_d, x_d, ids_d, bu_d, w_gate=wg_d, gate_bias=bg_d, glu=opname,
+                                      alpha=ALPHA, limit=LIMIT).cpu().numpy()
+    u = G.add_id_f32(G.mul_mat_id_vec_fused(tname, wu_d, x_d, ids_d), bu_d, ids_d)
+    g = G.add_id_f32(G.mul_mat_id_vec_fused(tname, wg_d, x_d, ids_d), bg_d, ids_d)
+    want = G.glu_f32(g.view(-1, M), u.view(-1, M), opname, alpha=ALPHA, limit=LIMIT).view(n_tokens, n_ids, M)
+    np.testing.assert_array_equal(got, want.cpu().numpy())
+    assert np.all(got[0, 0] == 0.0)  # an id of -1: zero row, no bias
+    one = G.mul_mat_id_vec_fused_bias(tname, wu_d, x_d, ids_d, bu_d).cpu().numpy()
+    one[0, 0] = 0.0  # the fused lone lane leaves the -1 row zero; ADD_ID alone would copy its input (zero) too
+    np.testing.assert_array_equal(one, u.cpu().numpy())
+    ok = ids >= 0
+    cu = O.mul_mat_id(t, wu, n_as, M, K, x, np.where(ok, ids, -1), nth=8) + np.where(ok[:, :, None], bu[np.maximum(ids, 0)], 0)
+    cg = O.mul_mat_id(t, wg, n_as, M, K, x, np.where(ok, ids, -1), nth=8) + np.where(ok[:, :, None], bg[np.maximum(ids, 0)], 0)
+    assert nmse(got[ok], O.glu(OPS[opname], cg, cu, ALPHA, LIMIT)[ok]) < NMSE_GATE
+
+
+def test_plugin_fuses_moe_bias_lanes(hb):
+    """{MUL_MAT_ID, ADD_ID, MUL_MAT_ID, ADD_ID, GLU} and {MUL_MAT_ID, ADD_ID}
+    fuse (intermediates stay NaN) and equal the kernel-level calls; without
+    use counts every node runs alone, with the same values."""
+    import ggml_hip as G
+    from ggml_hip import abi
+    n_as, M, K, n_tokens, n_ids = 16, 768, 1024, 2, 4
+    t, wu, wg, ids, x = _moe("Q4_K", n_as, M, K, n_tokens, n_ids, 17)
+    bu, bg = _moe_bias(n_as, M, 17)
+    q4, f32 = abi.GGML_TYPE_Q4_K, abi.GGML_TYPE_F32
+    tw_u = abi.make_tensor(q4, [K, M, n_as], name=b"ffn_up_exps")
+    tw_g = abi.make_tensor(q4, [K, M, n_as], name=b"ffn_gate_exps")
+    tb_u = abi.make_tensor(f32, [M, n_as], name=b"ffn_up_exps_b")
+    tb_g = abi.make_tensor(f32, [M, n_as], name=b"ffn_gate_exps_b")
+    tx = abi.make_tensor(f32, [K, 1, n_tokens], name=b"x")
+    tids = abi.make_tensor(abi.GGML_TYPE_I32, [n_ids, n_tokens], name=b"ids")
+    rs = [M, n_ids, n_tokens]
+    up = abi.make_tensor(f32, rs, op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_u, tx, tids), name=b"up")
+    upb = abi.make_tensor(f32, rs, op=abi.GGML_OP_ADD_ID, srcs=(up, tb_u, tids), name=b"up_b")
+    gate = abi.make_tensor(f32, rs, op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_g, tx, tids), name=b"gate")
+    gateb = abi.make_tensor(f32, rs, op=abi.GGML_OP_ADD_ID, srcs=(gate, tb_g, tids), name=b"gate_b")
+    glu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU_OAI, gateb, upb, rs, ALPHA, LIMIT)
+    # a lone biased projection (the down projection's shape of use)
+    lone = abi.make_tensor(f32, rs, op=abi.GGML_OP_MUL_MAT_ID, srcs=(tw_u, tx, tids), name=b"lone")
+    loneb = abi.make_tensor(f32, rs, op=abi.GGML_OP_ADD_ID, srcs=(lone, tb_u, tids), name=b"lone_b")
+    hb.alloc([tw_u, tw_g], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    inter = [up, upb, gate, gateb, lone]
+    hb.alloc([tb_u, tb_g, tx, tids, glu, loneb] + inter, usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    for tns, arr in ((tw_u, wu), (tw_g, wg), (tb_u, bu), (tb_g, bg), (tx, x), (tids, ids)):
+        hb.set(tns, arr)
+    shape = (n_tokens, n_ids, M)
+    nodes = [gate, gateb, up, upb, glu, lone, loneb]
+    for tns in inter + [glu, loneb]:
+        hb.set(tns, np.full(shape, np.nan, dtype=np.float32))
+    assert hb.compute(nodes) == abi.GGML_STATUS_SUCCESS
+    for tns in inter:
+        assert np.isnan(hb.get(tns, np.float32, shape)).all()
+    out, lout = hb.get(glu, np.float32, shape), hb.get(loneb, np.float32, shape)
+    wu_d, wg_d, x_d, ids_d = _dev(wu), _dev(wg), _dev(x), _dev(ids)
+    want = G.mul_mat_id_vec_fused_bias("Q4_K", wu_d, x_d, ids_d, _dev(bu), w_gate=wg_d, gate_bias=_dev(bg),
+                                       glu="SWIGLU_OAI", alpha=ALPHA, limit=LIMIT).cpu().numpy()
+    np.testing.assert_array_equal(out, want)
+    np.testing.assert_array_equal(lout, G.mul_mat_id_vec_fused_bias("Q4_K", wu_d, x_d, ids_d, _dev(bu)).cpu().numpy())
+    assert hb.compute(nodes, use_counts=False) == abi.GGML_STATUS_SUCCESS
+    assert not np.isnan(hb.get(upb, np.float32, shape)).any()
+    np.testing.assert_array_equal(hb.get(glu, np.float32, shape), out)
+    np.testing.assert_array_equal(hb.get(loneb, np.float32, shape), lout)
