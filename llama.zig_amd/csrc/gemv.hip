@@ -285,10 +285,10 @@ struct Wt<TYPE_Q6_K> {
         const uint8_t *blk = row + (kl / QK_K) * Q6K_BYTES;
         const int qq = (kl % QK_K) / 64;
         const int n = qq >> 1, h = qq & 1;
-        ql0 = ld16_a2(blk + 64 * n + 16 * h);
-        ql1 = ld16_a2(blk + 64 * n + 32 + 16 * h);
-        qh = ld16_a2(blk + 128 + 32 * n + 16 * h);
-        sc = ld16_a2(blk + 192);
+        ql0 = ld16_u(blk + 64 * n + 16 * h);
+        ql1 = ld16_u(blk + 64 * n + 32 + 16 * h);
+        qh = ld16_u(blk + 128 + 32 * n + 16 * h);
+        sc = ld16_u(blk + 192);
         d = ld_u16(blk + 208);
     }
     __device__ __forceinline__ void dots(const Act<TYPE_Q6_K> &a, int T[4], int = 0) const {
@@ -1126,7 +1126,7 @@ int check_shape(int type, int64_t K, int64_t nrows, int64_t row_stride) {
     }
     if (K % bs != 0 || K > (1 << 30) || row_stride < K / bs * bb) return (int)hipErrorInvalidValue;
     // row bases keep the blocks' natural alignment: 16 bytes for Q4_K (144-byte
-    // blocks, read as dwordx4), 2 bytes for Q6_K / Q8_0 (read by ld16_a2)
+    // blocks, read as dwordx4), 2 bytes for Q6_K / Q8_0 (read by ld16_u / ld16_a2)
     if (row_stride % block_align(type)) return (int)hipErrorInvalidValue;
     return 0;
 }

@@ -4,10 +4,11 @@
 // (src/ggml/quants/blocks.zig:67-222): block_q4_K {d, dmin, scales[12],
 // qs[128]} 144 B; block_q6_K {ql[128], qh[64], scales[16], d} 210 B;
 // block_q8_0 {d, qs[32]} 34 B.  Q6_K and Q8_0 blocks sit at 2-byte alignment
-// inside a row.  The GEMV kernels read them with dword-aligned loads plus a
-// byte funnel shift (v_alignbyte_b32, ld16_a2); the MMQ staging loads use one
-// unaligned vector load (ld16_u), which measured faster there.  Neither reads
-// outside the block.
+// inside a row.  Two ways read 16 of their bytes: dword-aligned loads plus a
+// byte funnel shift (v_alignbyte_b32, ld16_a2), or one unaligned vector load
+// (ld16_u).  Each kernel uses the one that measured faster for it: ld16_u for
+// the MMQ staging loads and the Q6_K GEMV, ld16_a2 for the Q8_0 and Q4_0
+// GEMVs.  Neither reads outside the block.
 #pragma once
 
 #include <hip/hip_fp16.h>
@@ -86,8 +87,10 @@ __device__ __forceinline__ uint4 ld16_a2(const uint8_t *p) {
 // The same 16 bytes with one instruction: a memcpy from a pointer known to be
 // 2-byte aligned compiles to a single global_load_dwordx4 (global memory
 // accepts unaligned vector loads on gfx950).  It reads exactly [p, p+16).
-// Measured faster for the MMQ's Q6_K staging loads, slower for the GEMV's
-// Q8_0 loads (where the aligned dwords above stay).
+// Measured faster for the MMQ's Q6_K staging loads and the Q6_K GEMV (its
+// op at 4096x14336: 13.0 against 15.1 us), slower for the Q8_0 and Q4_0
+// GEMVs (13.7 against 15.9 us at 4096x14336 Q8_0), where the aligned dwords
+// above stay.
 __device__ __forceinline__ uint4 ld16_u(const uint8_t *p) {
     uint4 r;
     __builtin_memcpy(&r, __builtin_assume_aligned(p, 2), 16);
