@@ -525,6 +525,74 @@ def run_suite(name, torch, G, dev, reps):
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4)})
             del wu, wg
             torch.cuda.empty_cache()
+    elif name == "prefill_ffn":
+        # Prefill FFN gate + up + SWIGLU: the fused MMQ (hip_qmm_mul_mat_glu:
+        # one quantization, one tile kernel over both weights, GLU in its
+        # epilogue) against the unfused sequence (two hip_qmm_mul_mat and the
+        # GLU kernel); then the MoE form at config 4 (hip_qmm_mul_mat_id_glu
+        # against two hip_qmm_mul_mat_id and the GLU kernel).
+        M, Kx = 14336, 4096
+        wb = M * row_bytes("Q4_K", Kx)
+        n = max(3, -(-2 * INFINITY_CACHE // (2 * wb)))
+        wu = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+        wg = [random_blocks(torch, "Q4_K", M, Kx, gen, dev) for _ in range(n)]
+        for T in (64, 128, 512, 2048):
+            x = torch.randn((T, Kx), generator=xg, dtype=torch.float32).to(dev)
+            out = torch.empty((T, M), dtype=torch.float32, device=dev)
+            u = torch.empty_like(out)
+            g = torch.empty_like(out)
+            t = G.TYPE_IDS["Q4_K"]
+            wsf = torch.empty(max(1, int(G.lib().hip_qmm_mul_mat_glu_workspace_size(t, Kx, M, T))),
+                              dtype=torch.uint8, device=dev)
+            wsu = torch.empty(int(G.lib().hip_qmm_mul_mat_workspace_size(t, Kx, M, T)), dtype=torch.uint8, device=dev)
+
+            def fused(i):
+                G.mul_mat_glu("Q4_K", wu[i % n], wg[i % n], x, "SWIGLU", out=out, workspace=wsf)
+
+            def unfused(i):
+                G.mul_mat("Q4_K", wg[i % n], x, out=g, workspace=wsu)
+                G.mul_mat("Q4_K", wu[i % n], x, out=u, workspace=wsu)
+                G.glu_f32(g, u, "SWIGLU", out=out)
+
+            msf = event_time_batch(torch, fused, n * reps)
+            msu = event_time_batch(torch, unfused, n * reps)
+            ops = 2.0 * 2 * M * Kx * T
+            emit({"suite": name, "kernel": "gate+up+swiglu fused MMQ", "type": "Q4_K", "shape": f"2x{M}x{Kx}",
+                  "label": "llama3-8b ffn_gate/up", "T": T, "fused": bool(G.lib().hip_qmm_mul_mat_glu_fused(
+                      t, Kx, M, T)), "us": round(msf * 1e3, 3), "unfused_us": round(msu * 1e3, 3),
+                  "TOPS": round(ops / msf / 1e9, 2), "int8_frac": round(ops / msf / 1e9 / INT8_PEAK_TOPS, 4)})
+        del wu, wg
+        torch.cuda.empty_cache()
+        n_as, n_tokens, k, M, Kx = 128, 512, 8, 768, 2048
+        logits = torch.randn((n_tokens, n_as), generator=torch.Generator().manual_seed(44))
+        ids = torch.topk(torch.softmax(logits, dim=1), k, dim=1).indices.to(torch.int32).to(dev)
+        wb = n_as * M * row_bytes("Q4_K", Kx)
+        n = max(2, -(-2 * INFINITY_CACHE // (2 * wb)))
+        wu = [random_blocks(torch, "Q4_K", n_as * M, Kx, gen, dev).view(n_as, M, -1) for _ in range(n)]
+        wg = [random_blocks(torch, "Q4_K", n_as * M, Kx, gen, dev).view(n_as, M, -1) for _ in range(n)]
+        x = torch.randn((n_tokens, 1, Kx), generator=xg, dtype=torch.float32).to(dev)
+        out = torch.empty((n_tokens, k, M), dtype=torch.float32, device=dev)
+        u = torch.empty_like(out)
+        g = torch.empty_like(out)
+        wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_id_workspace_size(12, Kx, n_as, 1, n_tokens, k)),
+                          dtype=torch.uint8, device=dev)
+
+        def fused_id(i):
+            G.mul_mat_id_glu("Q4_K", wu[i % n], wg[i % n], x, ids, "SWIGLU", out=out, workspace=wsp)
+
+        def unfused_id(i):
+            G.mul_mat_id("Q4_K", wg[i % n], x, ids, out=g, workspace=wsp)
+            G.mul_mat_id("Q4_K", wu[i % n], x, ids, out=u, workspace=wsp)
+            G.glu_f32(g.view(-1, M), u.view(-1, M), "SWIGLU", out=out.view(-1, M))
+
+        msf = event_time_batch(torch, fused_id, n * reps)
+        msu = event_time_batch(torch, unfused_id, n * reps)
+        alg = 2 * wb + n_tokens * Kx * 4 + n_tokens * k * M * 4
+        emit({"suite": name, "kernel": "mul_mat_id gate+up+swiglu fused (grouped MMQ)", "type": "Q4_K",
+              "shape": f"2x{n_as}x{M}x{Kx}", "label": "qwen3-30b-a3b ffn_gate/up_exps", "tokens": n_tokens, "top_k": k,
+              "us": round(msf * 1e3, 3), "unfused_us": round(msu * 1e3, 3), "GB/s": round(alg / msf / 1e6, 1)})
+        del wu, wg
+        torch.cuda.empty_cache()
     elif name == "floor":
         # The headline's weight stream against the memory floor: the same
         # rotated copies of the 14336x4096 Q4_K weight read by (1) the
@@ -561,7 +629,7 @@ def main():
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "few", "floor"],
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "prefill_ffn", "few", "floor"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()

@@ -321,6 +321,52 @@ int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t nrows, int64
                         int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
                         const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst, void *stream);
 
+/*
+ * Gate/up/GLU fused MMQ: dst[c*dst_col_stride + r] = glu(glu_op, (Wg . y_c)[r], (W . y_c)[r]) over
+ * planar Q8_1 columns y, glu as in hip_qmm_mul_mat_vec_fused.  The reference's mul_mat_q with
+ * a gate (src/ggml/cuda/mmq.zig:568-640, called from its gate/up/GLU fusion,
+ * src/ggml/cuda/fusion.zig:1226-1298, 1391).  W and Wg share type, shape and row stride; the
+ * limits of hip_qmm_mmq otherwise.  One tile kernel reads both weights (64 output rows per
+ * 128-row tile), with no K split, so each gate and up sum equals hip_qmm_mmq's without a
+ * workspace bit for bit.  No workspace.
+ */
+int hip_qmm_mmq_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows, int64_t row_stride,
+                    const int8_t *y_qs, const void *y_ds, int64_t ncols, int glu_op, float glu_alpha,
+                    float glu_limit, float *dst, int64_t dst_col_stride, void *stream);
+
+/* hip_qmm_mmq_grouped with a gate: the routed columns of each expert through
+ * W_e and Wg_e = w_gate + e*expert_stride, writing glu(gate, up) rows
+ * (the reference's mul_mat_q with ids and a gate, src/ggml/cuda/mmq.zig:568-640). */
+int hip_qmm_mmq_grouped_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                            int64_t row_stride, int64_t expert_stride, const int8_t *y_qs, const void *y_ds,
+                            float *dst, int64_t dst_row_stride, int bn, int64_t max_tiles, const int32_t *tiles,
+                            const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst, int glu_op,
+                            float glu_alpha, float glu_limit, void *stream);
+
+/* Bytes of workspace hip_qmm_mul_mat_glu needs (none for one column when the fused GEMV takes it). */
+size_t hip_qmm_mul_mat_glu_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
+
+/* 1 if hip_qmm_mul_mat_glu runs the fused MMQ for this shape (the products
+ * would each run the MMQ tile kernel), else 0: the reference's
+ * shouldFuseMulMatQ (src/ggml/cuda/mulmat.zig:548-571) for this backend. */
+int hip_qmm_mul_mat_glu_fused(int type, int64_t K, int64_t nrows, int64_t ncols);
+
+/*
+ * Op-level gate/up/GLU, the {MUL_MAT gate, MUL_MAT up, GLU} subgraph the
+ * reference fuses (src/ggml/cuda/fusion.zig:1391-1440; shouldFuseMulMatQ,
+ * src/ggml/cuda/mulmat.zig:548-571): dst[c][r] = glu(glu_op, (Wg . x_c)[r], (W . x_c)[r])
+ * for ncols f32 columns x[c*x_col_stride + k].  One column:
+ * hip_qmm_mul_mat_vec_fused.  Where the unfused products would run the MMQ
+ * tile kernel: one Q8_1 quantization and hip_qmm_mmq_glu.  Between (the
+ * GEMV's and the few-column kernel's column counts, which the reference does
+ * not fuse either): the two hip_qmm_mul_mat products into the workspace and
+ * hip_qmm_glu_f32, as the unfused graph runs.  Limits of hip_qmm_mul_mat.
+ */
+int hip_qmm_mul_mat_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows, int64_t row_stride,
+                        const float *x, int64_t ncols, int64_t x_col_stride, int glu_op, float glu_alpha,
+                        float glu_limit, float *dst, int64_t dst_col_stride, void *workspace, size_t workspace_size,
+                        void *stream);
+
 /* Bytes of workspace hip_qmm_mul_mat_id needs. */
 size_t hip_qmm_mul_mat_id_workspace_size(int type, int64_t K, int64_t n_as, int64_t ne11, int64_t n_tokens,
                                          int64_t n_ids);
@@ -346,6 +392,21 @@ int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_
                        int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
                        int64_t x_row_stride, const int32_t *ids, int64_t n_ids, int64_t ids_stride, float *dst,
                        int64_t dst_row_stride, void *workspace, size_t workspace_size, void *stream);
+
+/*
+ * hip_qmm_mul_mat_id with a gate: dst row (t, s) = glu(glu_op, Wg_e . x, W_e . x)
+ * for expert e = ids[t*ids_stride + s] (a zero row for an id outside
+ * [0, n_as)), Wg_e = w_gate + e*expert_stride; the reference's MUL_MAT_ID
+ * gate/up/GLU fusion (src/ggml/cuda/fusion.zig:1153-1306, into mmvq or
+ * mul_mat_q with ids).  Up to 8 tokens: hip_qmm_mul_mat_id_vec_fused; above,
+ * one grouping and Q8_1 copy feed hip_qmm_mmq_grouped_glu.  Workspace and
+ * limits of hip_qmm_mul_mat_id.
+ */
+int hip_qmm_mul_mat_id_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                           int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11,
+                           int64_t n_tokens, int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
+                           int64_t ids_stride, int glu_op, float glu_alpha, float glu_limit, float *dst,
+                           int64_t dst_row_stride, void *workspace, size_t workspace_size, void *stream);
 
 /*
  * Test hook: the integer block dot products the GEMV forms, written out

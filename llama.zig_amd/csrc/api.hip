@@ -16,6 +16,9 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
                            int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream);
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
+// mmq.hip: whether the few-column kernel takes this shape (given aligned operands)
+bool few_cols_type(int type, int64_t K, int64_t ncols);
+
 // gemv.hip: 2-4 f32 columns through the quantize-in-GEMV kernel, or
 // hipErrorNotSupported for shapes it does not take.
 int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
@@ -48,6 +51,21 @@ bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
 
 bool use_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return K % 256 == 0 && (ncols > 8 || few_cols_wins(type, K, nrows, ncols));
+}
+
+// Whether gate/up/GLU over ncols columns runs the fused MMQ: where each
+// product alone would run the MMQ tile kernel (not the GEMV and not the
+// few-column kernel; the reference's shouldFuseMulMatQ likewise leaves the
+// matmuls its few-row MMQ and MMVQ take, src/ggml/cuda/mulmat.zig:560-567).
+bool glu_fuses_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return ncols >= 2 && use_mmq(type, K, nrows, ncols) && !few_cols_type(type, K, ncols);
+}
+
+// The unfused gate/up/GLU's workspace: the gate and up products, then
+// hip_qmm_mul_mat's own workspace.
+size_t glu_unfused_bytes(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return align256((size_t)2 * (size_t)nrows * (size_t)ncols * sizeof(float)) +
+           hip_qmm_mul_mat_workspace_size(type, K, nrows, ncols);
 }
 }  // namespace
 
@@ -102,6 +120,50 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
             return e;
     }
     return 0;
+}
+
+extern "C" int hip_qmm_mul_mat_glu_fused(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return K > 0 && nrows > 0 && glu_fuses_mmq(type, K, nrows, ncols) ? 1 : 0;
+}
+
+extern "C" size_t hip_qmm_mul_mat_glu_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    if (K <= 0 || nrows <= 0 || ncols <= 0) return 0;
+    if (glu_fuses_mmq(type, K, nrows, ncols)) return q8_1_bytes(K, ncols);
+    return glu_unfused_bytes(type, K, nrows, ncols);  // one column: only used when the fused GEMV cannot run
+}
+
+extern "C" int hip_qmm_mul_mat_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                   int64_t row_stride, const float *x, int64_t ncols, int64_t x_col_stride,
+                                   int glu_op, float glu_alpha, float glu_limit, float *dst, int64_t dst_col_stride,
+                                   void *workspace, size_t workspace_size, void *stream) {
+    if (ncols <= 0 || nrows <= 0 || K <= 0 || !w || !w_gate || !x || !dst || !glu_op_valid(glu_op))
+        return (int)hipErrorInvalidValue;
+    if (ncols > 1 && (dst_col_stride < nrows || x_col_stride < K)) return (int)hipErrorInvalidValue;
+    if (ncols == 1 && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
+        return hip_qmm_mul_mat_vec_fused(type, w, w_gate, K, nrows, row_stride, x, nullptr, nullptr, glu_op,
+                                         glu_alpha, glu_limit, dst, stream);
+    if (!workspace || (uintptr_t)workspace % 256 ||
+        workspace_size < hip_qmm_mul_mat_glu_workspace_size(type, K, nrows, ncols))
+        return (int)hipErrorInvalidValue;
+    if (glu_fuses_mmq(type, K, nrows, ncols)) {
+        const int64_t Kp = pad_k(K);
+        int8_t *qs = (int8_t *)workspace;
+        void *ds = (uint8_t *)workspace + ncols * Kp;
+        if (int e = hip_qmm_quantize_q8_1_planar(x, K, ncols, x_col_stride, qs, ds, stream)) return e;
+        return hip_qmm_mmq_glu(type, w, w_gate, K, nrows, row_stride, qs, ds, ncols, glu_op, glu_alpha, glu_limit,
+                               dst, dst_col_stride, stream);
+    }
+    float *g = (float *)workspace, *u = g + nrows * ncols;
+    const size_t off = align256((size_t)2 * (size_t)nrows * (size_t)ncols * sizeof(float));
+    void *rest = (uint8_t *)workspace + off;
+    if (int e = hip_qmm_mul_mat(type, w_gate, K, nrows, row_stride, x, ncols, x_col_stride, g, nrows, rest,
+                                workspace_size - off, stream))
+        return e;
+    if (int e = hip_qmm_mul_mat(type, w, K, nrows, row_stride, x, ncols, x_col_stride, u, nrows, rest,
+                                workspace_size - off, stream))
+        return e;
+    return hip_qmm_glu_f32(glu_op, glu_alpha, glu_limit, nrows, ncols, g, nrows, u, nrows, dst, dst_col_stride,
+                           stream);
 }
 
 // ---------------------------------------------------------------- allocation-free MUL_MAT

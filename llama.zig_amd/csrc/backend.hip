@@ -796,6 +796,80 @@ bool launch_fused_id(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *
     return true;
 }
 
+// ---- prefill: {MUL_MAT gate, MUL_MAT up, GLU} and its MUL_MAT_ID form into
+// the fused MMQ (the reference's shouldFuseMulMatQ, src/ggml/cuda/mulmat.zig:
+// 548-571, then mul_mat_q with the gate, fusion.zig:1226-1298, 1391).
+
+// The gate/up weights and GLU checks the fused kernels share: a split
+// non-swapped f32 GLU of an op they apply, weights of one type, shape and
+// strides, the same activations.
+bool gate_up_pair_ok(const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *glu) {
+    const ggml_tensor *wu = up->src[0], *wg = gate->src[0];
+    const int op = glu->op_params[0];
+    if (op != HIP_QMM_GLU_GEGLU && op != HIP_QMM_GLU_SWIGLU && op != HIP_QMM_GLU_SWIGLU_OAI &&
+        op != HIP_QMM_GLU_SWIGLU_CLAMP)
+        return false;
+    if (glu->op_params[1] != 0 || !glu->src[1] || glu->type != GGML_TYPE_F32 || glu->nb[0] != 4) return false;
+    if (wu->type != wg->type || !same_shape(wu, wg)) return false;
+    for (int i = 0; i < GGML_MAX_DIMS; ++i)
+        if (wu->nb[i] != wg->nb[i]) return false;
+    return up->src[1] == gate->src[1] && up->src[2] == gate->src[2] && same_shape(glu, up);
+}
+
+// Dense: one 2-D product of 2+ f32 columns that each product alone would run
+// on the MMQ tile kernel (hip_qmm_mul_mat_glu_fused), dense columns.
+bool gate_up_mmq_fusable(const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *glu) {
+    if (!gate_up_pair_ok(up, gate, glu)) return false;
+    const ggml_tensor *w = up->src[0], *x = up->src[1];
+    for (int i = 2; i < GGML_MAX_DIMS; ++i)
+        if (w->ne[i] != 1 || x->ne[i] != 1) return false;
+    if (x->type != GGML_TYPE_F32 || x->nb[0] != 4 || x->nb[1] % 4 != 0 || glu->nb[1] % 4 != 0) return false;
+    return hip_qmm_mul_mat_glu_fused(w->type, w->ne[0], w->ne[1], x->ne[1]) == 1;
+}
+
+bool launch_fused_mmq(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *out,
+                      bool *ok) {
+    const ggml_tensor *w = up->src[0], *x = up->src[1];
+    const int64_t K = w->ne[0], M = w->ne[1], N = x->ne[1];
+    if (overlaps(out->data, nbytes(out), x->data, nbytes(x))) return false;
+    void *ws = workspace(ctx, hip_qmm_mul_mat_glu_workspace_size(w->type, K, M, N));
+    const int rc = hip_qmm_mul_mat_glu(w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1],
+                                       static_cast<const float *>(x->data), N, (int64_t)(x->nb[1] / 4),
+                                       out->op_params[0], op_param_f32(out, 2), op_param_f32(out, 3),
+                                       static_cast<float *>(out->data), (int64_t)(out->nb[1] / 4), ws, ctx->ws_size,
+                                       ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_glu", out);
+    return true;
+}
+
+// MUL_MAT_ID over more than 8 tokens: the grouped fused MMQ, with the layout
+// hip_qmm_mul_mat_id addresses (rows (t, i11) of x and (t, s) of dst dense).
+bool gate_up_id_mmq_fusable(const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *glu) {
+    if (!gate_up_pair_ok(up, gate, glu)) return false;
+    const ggml_tensor *w = up->src[0], *x = up->src[1];
+    if (glu->nb[2] != (size_t)glu->ne[1] * glu->nb[1] || glu->nb[1] % 4) return false;
+    if (x->nb[2] != (size_t)x->ne[1] * x->nb[1] || x->nb[1] % 4 || x->nb[0] != 4) return false;
+    return x->ne[2] > 8 && w->ne[0] % 256 == 0;
+}
+
+bool launch_fused_id_mmq(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gate, const ggml_tensor *out,
+                         bool *ok) {
+    const ggml_tensor *w = up->src[0], *x = up->src[1], *ids = up->src[2];
+    const int64_t K = w->ne[0], M = w->ne[1], n_as = w->ne[2];
+    const int64_t ne11 = x->ne[1], n_tokens = x->ne[2], n_ids = ids->ne[0];
+    const size_t ob = nbytes(out);
+    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids))) return false;
+    void *ws = workspace(ctx, hip_qmm_mul_mat_id_workspace_size(w->type, K, n_as, ne11, n_tokens, n_ids));
+    const int rc = hip_qmm_mul_mat_id_glu(
+        w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], n_as,
+        static_cast<const float *>(x->data), ne11, n_tokens, (int64_t)(x->nb[1] / 4),
+        static_cast<const int32_t *>(ids->data), n_ids, (int64_t)(ids->nb[1] / 4), out->op_params[0],
+        op_param_f32(out, 2), op_param_f32(out, 3), static_cast<float *>(out->data), (int64_t)(out->nb[1] / 4), ws,
+        ctx->ws_size, ctx->stream);
+    *ok = report(rc, "hip_qmm_mul_mat_id_glu", out);
+    return true;
+}
+
 // ---- shared expert: a routed {MUL_MAT_ID, MUL_MAT_ID, GLU} and a shared
 // expert's {MUL_MAT, MUL_MAT, GLU} on the same tokens in one launch (the
 // reference's shared_up / shared_gate / shared_dst fusion,
@@ -973,6 +1047,9 @@ int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
             if (pair && gate_up_id_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
                 launch_fused_id(ctx, up, gate, glu, ok))
                 return 3;
+            if (pair && gate_up_id_mmq_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
+                launch_fused_id_mmq(ctx, up, gate, glu, ok))
+                return 3;
         }
         if (is(i + 1, GGML_OP_ADD_ID)) {
             const ggml_tensor *mm = node(i), *add = node(i + 1);
@@ -1006,6 +1083,9 @@ int try_fuse(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok) {
         const bool pair = (gate == node(i) && up == node(i + 1)) || (gate == node(i + 1) && up == node(i));
         if (pair && gate_up_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
             launch_fused(ctx, up, gate, nullptr, nullptr, glu, ok))
+            return 3;
+        if (pair && gate_up_mmq_fusable(up, gate, glu) && run_is_closed(g, i, 3, glu) &&
+            launch_fused_mmq(ctx, up, gate, glu, ok))
             return 3;
     }
     if (is(i + 1, GGML_OP_ADD)) {

@@ -1365,9 +1365,7 @@ int fused_launch(int type, const void *w, const void *w_gate, int64_t K, int64_t
     const uintptr_t walign = (uintptr_t)block_align(type);
     if ((uintptr_t)w % walign || (uintptr_t)w_gate % walign) return (int)hipErrorInvalidValue;
     if (!w_gate && gate_bias) return (int)hipErrorInvalidValue;
-    if (w_gate && glu_op != GLU_REGLU && glu_op != GLU_GEGLU && glu_op != GLU_SWIGLU && glu_op != GLU_SWIGLU_OAI &&
-        glu_op != GLU_SWIGLU_CLAMP)
-        return (int)hipErrorInvalidValue;
+    if (w_gate && !glu_op_valid(glu_op)) return (int)hipErrorInvalidValue;
     if ((nrows + 7) / 8 > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
     hipStream_t s = (hipStream_t)stream;
     const uint8_t *wb = (const uint8_t *)w, *gb = (const uint8_t *)w_gate;

@@ -239,11 +239,15 @@ extern "C" size_t hip_qmm_mul_mat_id_workspace_size(int type, int64_t K, int64_t
     return layout(K, n_as, ne11, n_tokens, n_ids, grouped_bn(n_tokens * n_ids, n_as)).total;
 }
 
-extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
-                                  int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11,
-                                  int64_t n_tokens, int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
-                                  int64_t ids_stride, float *dst, int64_t dst_row_stride, void *workspace,
-                                  size_t workspace_size, void *stream) {
+namespace {
+
+// MUL_MAT_ID, and with w_gate its gate/up/GLU fusion (glu_op etc. unused
+// without it).
+int mul_mat_id(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows, int64_t row_stride,
+               int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11, int64_t n_tokens,
+               int64_t x_row_stride, const int32_t *ids, int64_t n_ids, int64_t ids_stride, int glu_op,
+               float glu_alpha, float glu_limit, float *dst, int64_t dst_row_stride, void *workspace,
+               size_t workspace_size, void *stream) {
     if (!w || !x || !ids || !dst || !workspace || K <= 0 || nrows <= 0 || n_as <= 0 || n_as > MAX_EXPERTS ||
         ne11 <= 0 || n_tokens <= 0 || n_ids <= 0 || ids_stride < n_ids || dst_row_stride < nrows ||
         x_row_stride < K || expert_stride < nrows * row_stride)
@@ -256,9 +260,9 @@ extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nr
     const int64_t walign = block_align(type);
     if (n_tokens <= 8 && n_tokens * n_ids <= 65535 && K % 32 == 0 && K <= 32768 && (uintptr_t)x % 16 == 0 &&
         x_row_stride % 4 == 0 && expert_stride % walign == 0)
-        return hip_qmm_mul_mat_id_vec_fused(type, w, nullptr, K, nrows, row_stride, expert_stride, n_as, x, ne11,
-                                            n_tokens, x_row_stride, ids, n_ids, ids_stride, 0, 0.0f, 0.0f, dst,
-                                            dst_row_stride, stream);
+        return hip_qmm_mul_mat_id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, ne11,
+                                            n_tokens, x_row_stride, ids, n_ids, ids_stride, glu_op, glu_alpha,
+                                            glu_limit, dst, dst_row_stride, stream);
     const int bn = grouped_bn(n_tokens * n_ids, n_as);
     const MmidLayout L = layout(K, n_as, ne11, n_tokens, n_ids, bn);
     if (workspace_size < L.total || (uintptr_t)workspace % 256) return (int)hipErrorInvalidValue;
@@ -287,6 +291,37 @@ extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nr
                            dst_row_stride, nrows, x, K, x_row_stride, L.Kp, 1, qs, (uint32_t *)ds);
     }
     if (int e = (int)hipGetLastError()) return e;
+    if (w_gate)
+        return hip_qmm_mmq_grouped_glu(type, w, w_gate, K, nrows, row_stride, expert_stride, qs, ds, dst,
+                                       dst_row_stride, bn, L.max_tiles, tiles, ntiles, col_src, col_dst, glu_op,
+                                       glu_alpha, glu_limit, stream);
     return hip_qmm_mmq_grouped(type, w, K, nrows, row_stride, expert_stride, qs, ds, dst, dst_row_stride, bn,
                                L.max_tiles, tiles, ntiles, col_src, col_dst, stream);
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_mul_mat_id(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                                  int64_t expert_stride, int64_t n_as, const float *x, int64_t ne11,
+                                  int64_t n_tokens, int64_t x_row_stride, const int32_t *ids, int64_t n_ids,
+                                  int64_t ids_stride, float *dst, int64_t dst_row_stride, void *workspace,
+                                  size_t workspace_size, void *stream) {
+    return mul_mat_id(type, w, nullptr, K, nrows, row_stride, expert_stride, n_as, x, ne11, n_tokens, x_row_stride,
+                      ids, n_ids, ids_stride, 0, 0.0f, 0.0f, dst, dst_row_stride, workspace, workspace_size, stream);
+}
+
+// Gate/up/GLU over the routed pairs (the reference's MUL_MAT_ID fusion,
+// src/ggml/cuda/fusion.zig:1153-1306 into mmvq or mmq with ids): the same
+// grouping and one Q8_1 copy feed both weights; dst row (t, s) =
+// glu(Wg_e . x, W_e . x), a zero row for an id outside [0, n_as).
+extern "C" int hip_qmm_mul_mat_id_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                      int64_t row_stride, int64_t expert_stride, int64_t n_as, const float *x,
+                                      int64_t ne11, int64_t n_tokens, int64_t x_row_stride, const int32_t *ids,
+                                      int64_t n_ids, int64_t ids_stride, int glu_op, float glu_alpha,
+                                      float glu_limit, float *dst, int64_t dst_row_stride, void *workspace,
+                                      size_t workspace_size, void *stream) {
+    if (!w_gate || !glu_op_valid(glu_op)) return (int)hipErrorInvalidValue;
+    return mul_mat_id(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, ne11, n_tokens, x_row_stride,
+                      ids, n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, workspace,
+                      workspace_size, stream);
 }

@@ -42,7 +42,7 @@ using namespace qmm;
 int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
-                       const int32_t *col_dst, float *partial, hipStream_t s);
+                       const int32_t *col_dst, float *partial, const MmqGlu &glu, hipStream_t s);
 // mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
@@ -370,24 +370,28 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     const int32_t *__restrict__ col_dst,
     // split-K (gridDim.z > 1): this workgroup's share of the K-steps goes to
     // partial[z][col][row] instead of dst
-    float *__restrict__ partial) {
+    float *__restrict__ partial,
+    // gate/up/GLU fusion (glu.gate != nullptr): 64 output rows per tile, no split-K
+    MmqGlu glu) {
     using F = MmqFmt<TYPE>;
     constexpr bool KMIN = TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K;  // scales with a min term
     constexpr bool LEGACY = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0;  // one scale per 32-block, no super-block
     __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
-    const int64_t row0 = (int64_t)blockIdx.x * BM;
+    const bool fused = glu.gate != nullptr;                        // uniform
+    const int64_t row0 = (int64_t)blockIdx.x * (fused ? BM / 2 : BM);  // first output row
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
 
     // column tile: dense (col0 .. col0+BN of ncols) or one expert's routed columns
     int64_t col0 = (int64_t)blockIdx.y * BN, col_end = ncols;
-    const uint8_t *wexp = w;
+    const uint8_t *wexp = w, *wgexp = glu.gate;
     if (tiles) {
         if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup
         const int4 t = *reinterpret_cast<const int4 *>(tiles + 4 * blockIdx.y);  // {expert, col_low, col_high, -}
         wexp = w + (int64_t)t.x * expert_stride;
+        wgexp = fused ? glu.gate + (int64_t)t.x * expert_stride : nullptr;
         col0 = t.y;
         col_end = t.z;
     }
@@ -408,8 +412,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
 
     // ---- register staging of one K-step ----
     const int ar_row = threadIdx.x >> 1, ar_half = threadIdx.x & 1;
-    const bool a_ok = row0 + ar_row < nrows;
-    const uint8_t *a_row = wexp + (a_ok ? row0 + ar_row : 0) * row_stride;
+    const int64_t a_orow = row0 + (fused ? mmq_glu_tile_row(ar_row) : ar_row);
+    const bool a_ok = a_orow < nrows;
+    const uint8_t *a_row = (fused && (ar_row & 2) == 0 ? wgexp : wexp) + (a_ok ? a_orow : 0) * row_stride;
     AReg<TYPE> areg;
     BReg<BN> breg;
     auto gload = [&](int64_t kb) {
@@ -597,6 +602,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
             if (c >= col_end) continue;
             const int64_t drow = tiles ? (int64_t)col_dst[c] : c;
             float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + drow * dst_col_stride;
+            if (fused) {
+                store_glu_column(o, row0 + wr / 2 + 2 * lh, nrows, acc[i][j], glu);
+                continue;
+            }
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int64_t r = row0 + wr + 32 * i + 8 * (v >> 2) + 4 * lh + (v & 3);
@@ -664,21 +673,23 @@ template <int TYPE, int BN>
 int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride, const int8_t *yqs,
            const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy, const int32_t *tiles,
            const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst, int split, float *partial,
-           hipStream_t s) {
-    const int64_t gx = (nrows + BM - 1) / BM;
-    if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64) return (int)hipErrorInvalidValue;
+           const MmqGlu &glu, hipStream_t s) {
+    const int64_t tile_rows = glu.gate ? BM / 2 : BM;  // output rows per tile
+    const int64_t gx = (nrows + tile_rows - 1) / tile_rows;
+    if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64 || (glu.gate && split != 1))
+        return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)split);
     // Q4_K with 16-byte aligned operands (the transfer unit of the direct
     // global->LDS loads; the weight rows are checked by check_weights)
     if (TYPE == TYPE_Q4_K && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
         if (int e = mmq_q4k_dma_launch(BN, w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst,
                                        dst_col_stride, grid, tiles, n_tiles, col_src, col_dst,
-                                       split > 1 ? partial : nullptr, s))
+                                       split > 1 ? partial : nullptr, glu, s))
             return e;
     } else {
         hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,
                            row_stride, expert_stride, yqs, (const uint32_t *)yds, ncols, dst, dst_col_stride, tiles,
-                           n_tiles, col_src, col_dst, split > 1 ? partial : nullptr);
+                           n_tiles, col_src, col_dst, split > 1 ? partial : nullptr, glu);
         if (int e = (int)hipGetLastError()) return e;
     }
     return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
@@ -688,13 +699,33 @@ template <int TYPE>
 int launch_bn(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
               const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy,
               const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst,
-              int split, float *partial, hipStream_t s) {
+              int split, float *partial, const MmqGlu &glu, hipStream_t s) {
     // A 128-column tile needs more than the 256 registers per lane that two
     // workgroups per CU leave (its two accumulator sets alone take 128), so
     // tiles stop at 64 columns.
     if (bn == 32)
-        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, s);
-    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, s);
+        return launch<TYPE, 32>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, glu, s);
+    return launch<TYPE, 64>(w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy, tiles, n_tiles, col_src, col_dst, split, partial, glu, s);
+}
+
+int launch_type(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
+                const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, int64_t gy,
+                const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src, const int32_t *col_dst,
+                int split, float *partial, const MmqGlu &glu, hipStream_t s) {
+#define MMQ_TYPE_CASE(T)                                                                                              \
+    case T:                                                                                                          \
+        return launch_bn<T>(bn, w, K, nrows, row_stride, expert_stride, yqs, yds, ncols, dst, dst_col_stride, gy,    \
+                            tiles, n_tiles, col_src, col_dst, split, partial, glu, s)
+    switch (type) {
+        MMQ_TYPE_CASE(TYPE_Q4_K);
+        MMQ_TYPE_CASE(TYPE_Q5_K);
+        MMQ_TYPE_CASE(TYPE_Q6_K);
+        MMQ_TYPE_CASE(TYPE_Q4_0);
+        MMQ_TYPE_CASE(TYPE_IQ4_XS);
+        MMQ_TYPE_CASE(TYPE_Q8_0);
+    default: return (int)hipErrorInvalidValue;
+    }
+#undef MMQ_TYPE_CASE
 }
 
 int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
@@ -795,14 +826,8 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
             return e;
         return split > 1 ? launch_reduce(partial, split, nrows, ncols, dst, dst_col_stride, s) : 0;
     }
-    switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr, nullptr, nullptr, split, partial, s);
-    }
+    return launch_type(type, bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr, nullptr,
+                       nullptr, nullptr, split, partial, MmqGlu{}, s);
 }
 
 // Expert-grouped form used by hip_qmm_mul_mat_id: column tiles come from the
@@ -819,12 +844,46 @@ extern "C" int hip_qmm_mmq_grouped(int type, const void *w, int64_t K, int64_t n
     if (K % BK != 0 || K > (1 << 30) || (bn != 32 && bn != 64)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
     hipStream_t s = (hipStream_t)stream;
-    switch (type) {
-    case TYPE_Q4_K: return launch_bn<TYPE_Q4_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q5_K: return launch_bn<TYPE_Q5_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q6_K: return launch_bn<TYPE_Q6_K>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    case TYPE_Q4_0: return launch_bn<TYPE_Q4_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    case TYPE_IQ4_XS: return launch_bn<TYPE_IQ4_XS>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    default: return launch_bn<TYPE_Q8_0>(bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles, tiles, n_tiles, col_src, col_dst, 1, nullptr, s);
-    }
+    return launch_type(type, bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles,
+                       tiles, n_tiles, col_src, col_dst, 1, nullptr, MmqGlu{}, s);
+}
+
+// Gate/up/GLU fused forms (the reference's mul_mat_q with a gate, its
+// gate/up/GLU fusion, src/ggml/cuda/mmq.zig:568-640 and fusion.zig:1391,
+// 1226-1298): both weights' rows go through one tile kernel, 64 output rows
+// per tile, and the tile writes glu(gate, up).  No K split (the reference's
+// fused kernel also runs one block per tile).  Each gate and up sum is the
+// unfused kernel's at the same K order, so the output equals the GLU of two
+// unsplit MMQs bit for bit.
+extern "C" int hip_qmm_mmq_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                               int64_t row_stride, const int8_t *y_qs, const void *y_ds, int64_t ncols, int glu_op,
+                               float glu_alpha, float glu_limit, float *dst, int64_t dst_col_stride, void *stream) {
+    if (!w || !w_gate || !y_qs || !y_ds || !dst || K <= 0 || nrows <= 0 || ncols <= 0 || dst_col_stride < nrows ||
+        !glu_op_valid(glu_op))
+        return (int)hipErrorInvalidValue;
+    if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
+    if (int e = check_weights(type, w, K, row_stride)) return e;
+    if (int e = check_weights(type, w_gate, K, row_stride)) return e;
+    const int bn = hip_qmm_mmq_tile_n(ncols);
+    const int64_t gy = (ncols + bn - 1) / bn;
+    const MmqGlu glu{(const uint8_t *)w_gate, glu_op, glu_alpha, glu_limit};
+    return launch_type(type, bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr,
+                       nullptr, nullptr, nullptr, 1, nullptr, glu, (hipStream_t)stream);
+}
+
+extern "C" int hip_qmm_mmq_grouped_glu(int type, const void *w, const void *w_gate, int64_t K, int64_t nrows,
+                                       int64_t row_stride, int64_t expert_stride, const int8_t *y_qs,
+                                       const void *y_ds, float *dst, int64_t dst_row_stride, int bn,
+                                       int64_t max_tiles, const int32_t *tiles, const int32_t *n_tiles,
+                                       const int32_t *col_src, const int32_t *col_dst, int glu_op, float glu_alpha,
+                                       float glu_limit, void *stream) {
+    if (!w || !w_gate || !y_qs || !y_ds || !dst || !tiles || !n_tiles || !col_src || !col_dst || K <= 0 ||
+        nrows <= 0 || dst_row_stride < nrows || max_tiles < 1 || (uintptr_t)tiles % 16 != 0 || !glu_op_valid(glu_op))
+        return (int)hipErrorInvalidValue;
+    if (K % BK != 0 || K > (1 << 30) || (bn != 32 && bn != 64)) return (int)hipErrorInvalidValue;
+    if (int e = check_weights(type, w, K, row_stride)) return e;
+    if (int e = check_weights(type, w_gate, K, row_stride)) return e;
+    const MmqGlu glu{(const uint8_t *)w_gate, glu_op, glu_alpha, glu_limit};
+    return launch_type(type, bn, w, K, nrows, row_stride, expert_stride, y_qs, y_ds, 0, dst, dst_row_stride, max_tiles,
+                       tiles, n_tiles, col_src, col_dst, 1, nullptr, glu, (hipStream_t)stream);
 }

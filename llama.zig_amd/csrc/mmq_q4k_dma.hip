@@ -78,7 +78,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     const int8_t *__restrict__ yqs, const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst,
     int64_t dst_col_stride, const int32_t *__restrict__ tiles, const int32_t *__restrict__ n_tiles,
     const int32_t *__restrict__ col_src, const int32_t *__restrict__ col_dst, float *__restrict__ partial, int gx,
-    int gy, int gz) {
+    int gy, int gz, MmqGlu glu) {
     constexpr int TJ = BN / 32;
     constexpr int NQB = BN / 4;    // 1 KiB transfers of B int8 per step
     constexpr int NQD = BN / 32;   // 1 KiB transfers of B headers per step
@@ -100,23 +100,29 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     const int nitems = gx * gy_live * gz;  // < 2^31, checked by the host
     const int nkb_all = (int)(K / QK_K);
     // one item's tile, as 32-bit values (the host bounds rows, columns and
-    // K-steps below 2^31); wexp is the expert's weights in grouped mode
+    // K-steps below 2^31); wexp is the expert's weights in grouped mode (wgexp
+    // its gate weights when fused).  row0 is the tile's first output row: a
+    // fused tile has 64 of them.
+    const bool fused = glu.gate != nullptr;  // uniform
+    const int tile_rows = fused ? BM / 2 : BM;
     struct Item {
         int row0, col0, col_end, kb0, kb1, z;
-        const uint8_t *wexp;
+        const uint8_t *wexp, *wgexp;
     };
     auto item_xyz = [&](int bx, int by, int bz) {
         Item I;
-        I.row0 = bx * BM;
+        I.row0 = bx * tile_rows;
         I.z = bz;
         I.kb0 = nkb_all * bz / gz;
         I.kb1 = nkb_all * (bz + 1) / gz;
         I.col0 = by * BN;
         I.col_end = (int)ncols;
         I.wexp = w;
+        I.wgexp = glu.gate;
         if constexpr (GROUPED) {
             const int4 t = *reinterpret_cast<const int4 *>(tiles + 4 * by);  // {expert, col_low, col_high, -}
             I.wexp = w + (int64_t)t.x * expert_stride;
+            I.wgexp = fused ? glu.gate + (int64_t)t.x * expert_stride : nullptr;
             I.col0 = t.y;
             I.col_end = t.z;
         }
@@ -140,8 +146,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             const int q = wave + 4 * i;
             const int pos = (q < 18 ? q : 0) * 1024 + lane * 16;
             const int r = pos / Q4K_BYTES, ch = (pos - r * Q4K_BYTES) / 16;
-            const int64_t grow = (int64_t)I.row0 + r < nrows ? (int64_t)I.row0 + r : nrows - 1;
-            a_src[i] = I.wexp + grow * row_stride + ch * 16;
+            const int64_t orow = (int64_t)I.row0 + (fused ? mmq_glu_tile_row(r) : r);
+            const int64_t grow = orow < nrows ? orow : nrows - 1;
+            a_src[i] = (fused && (r & 2) == 0 ? I.wgexp : I.wexp) + grow * row_stride + ch * 16;
         }
     };
     // activation rows (planar Q8_1 columns) of the lane's B and header transfers
@@ -346,7 +353,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             float *o;
             if constexpr (GROUPED) o = dst + (int64_t)col_dst[c] * dst_col_stride;
             else o = partial ? partial + ((int64_t)C.z * ncols + c) * nrows : dst + c * dst_col_stride;
-            store_tile_column(o, (int64_t)C.row0 + wr + 4 * lh, nrows, acc[j]);
+            if (fused) store_glu_column(o, (int64_t)C.row0 + wr / 2 + 2 * lh, nrows, acc[j], glu);
+            else store_tile_column(o, (int64_t)C.row0 + wr + 4 * lh, nrows, acc[j]);
         }
     } else {
         // Persistent workgroups walk items blockIdx.x, +G, +2G, ... (G =
@@ -365,11 +373,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
         auto tile_of = [&](int it) { return *reinterpret_cast<const int4 *>(tiles + 4 * ((it / gx) % gy_live)); };
         auto item_of = [&](int it, const int4 &t) {
             Item I;
-            I.row0 = (it % gx) * BM;
+            I.row0 = (it % gx) * tile_rows;
             I.z = 0;
             I.kb0 = 0;
             I.kb1 = nkb_all;
             I.wexp = w + (int64_t)t.x * expert_stride;
+            I.wgexp = fused ? glu.gate + (int64_t)t.x * expert_stride : nullptr;
             I.col0 = t.y;
             I.col_end = t.z;
             return I;
@@ -414,8 +423,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             for (int j = 0; j < TJ; ++j) {
                 const int64_t c = (int64_t)C.col0 + 32 * j + li;
                 if (c >= C.col_end) continue;
-                store_tile_column(dst + (int64_t)drow[j] * dst_col_stride, (int64_t)C.row0 + wr + 4 * lh, nrows,
-                                  acc[j]);
+                float *o = dst + (int64_t)drow[j] * dst_col_stride;
+                if (fused) store_glu_column(o, (int64_t)C.row0 + wr / 2 + 2 * lh, nrows, acc[j], glu);
+                else store_tile_column(o, (int64_t)C.row0 + wr + 4 * lh, nrows, acc[j]);
             }
         };
         // after a step's contraction: at an item's last step store it and move on
@@ -470,7 +480,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
 int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t expert_stride,
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
-                       const int32_t *col_dst, float *partial, hipStream_t s) {
+                       const int32_t *col_dst, float *partial, const MmqGlu &glu, hipStream_t s) {
     // workgroups resident at once: 2 per CU of the current device (queried per
     // call: a process may drive GPUs of different sizes; the query is a host
     // attribute read)
@@ -492,7 +502,7 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        nrows,                                                                                          \
                        row_stride,                                                                                     \
                        expert_stride, yqs, ds, ncols, dst, dst_col_stride, tiles, n_tiles, col_src, col_dst,         \
-                       partial, gx, gy, gz)
+                       partial, gx, gy, gz, glu)
     if (tiles) {
         if (bn == 32) MMQ_DMA_LAUNCH(32, true);
         else MMQ_DMA_LAUNCH(64, true);

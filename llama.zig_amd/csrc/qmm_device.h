@@ -249,6 +249,10 @@ enum : int {
     GLU_SWIGLU_CLAMP = 6,
 };
 
+__host__ __device__ constexpr bool glu_op_valid(int op) {
+    return op == GLU_REGLU || op == GLU_GEGLU || op == GLU_SWIGLU || op == GLU_SWIGLU_OAI || op == GLU_SWIGLU_CLAMP;
+}
+
 // out = glu(gate g, value u) for one element, as the CPU ops define it:
 //   REGLU         g > 0 ? g*u : 0                      (vecinline.zig:507-511)
 //   GEGLU         gelu from the f16 table: g rounded to f16, gelu of that,
@@ -278,6 +282,39 @@ __device__ __forceinline__ float glu_apply(int op, float g, float u, float alpha
     const float y = u < -limit ? -limit : (limit < u ? limit : u);
     if (op == GLU_SWIGLU_OAI) return x / (1.0f + expf(alpha * (-x))) * (y + 1.0f);
     return x / (1.0f + expf(-x)) * y;  // GLU_SWIGLU_CLAMP
+}
+
+// Gate/up/GLU fusion of the MMQ kernels (the reference's mul_mat_q with a
+// gate, src/ggml/cuda/mmq.zig:568-640).  With gate != nullptr a 128-row tile
+// holds 64 output rows: tile row t reads output row 2 * (t / 4) + t % 2 of the
+// tile from the gate weights (t % 4 < 2) or the up weights (t % 4 >= 2).  A
+// 32x32 MFMA result gives lane half h rows 8q + 4h + i (i = 0..3), so each
+// lane holds gate (i = 0, 1) and up (i = 2, 3) of the same two output rows,
+// and the epilogue writes glu(gate, up) without any exchange.
+struct MmqGlu {
+    const uint8_t *gate;
+    int op;
+    float alpha, limit;
+};
+
+__device__ __forceinline__ int mmq_glu_tile_row(int t) { return 2 * (t >> 2) + (t & 1); }
+
+// One lane's 8 fused outputs of a 32x32 tile column: rows r0 + 4q + {0, 1}
+// (q = 0..3) of the column at o, from accumulators a[4q + i].
+template <typename V>
+__device__ __forceinline__ void store_glu_column(float *o, int64_t r0, int64_t nrows, const V &a, const MmqGlu &g) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float v0 = glu_apply(g.op, a[4 * q], a[4 * q + 2], g.alpha, g.limit);
+        const float v1 = glu_apply(g.op, a[4 * q + 1], a[4 * q + 3], g.alpha, g.limit);
+        const int64_t r = r0 + 4 * q;
+        if (((uintptr_t)(o + r) & 7) == 0 && r + 1 < nrows) {
+            *reinterpret_cast<float2 *>(o + r) = make_float2(v0, v1);
+        } else {
+            if (r < nrows) o[r] = v0;
+            if (r + 1 < nrows) o[r + 1] = v1;
+        }
+    }
 }
 
 }  // namespace qmm

@@ -86,6 +86,22 @@ def lib():
         L.hip_qmm_mul_mat_id.restype = i32
         L.hip_qmm_mul_mat_id.argtypes = [i32, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, i64,
                                          vp, ctypes.c_size_t, vp]
+        L.hip_qmm_mmq_glu.restype = i32
+        L.hip_qmm_mmq_glu.argtypes = [i32, vp, vp, i64, i64, i64, vp, vp, i64, i32, ctypes.c_float, ctypes.c_float,
+                                      vp, i64, vp]
+        L.hip_qmm_mmq_grouped_glu.restype = i32
+        L.hip_qmm_mmq_grouped_glu.argtypes = [i32, vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, i32, i64, vp, vp,
+                                              vp, vp, i32, ctypes.c_float, ctypes.c_float, vp]
+        L.hip_qmm_mul_mat_glu_workspace_size.restype = ctypes.c_size_t
+        L.hip_qmm_mul_mat_glu_workspace_size.argtypes = [i32, i64, i64, i64]
+        L.hip_qmm_mul_mat_glu_fused.restype = i32
+        L.hip_qmm_mul_mat_glu_fused.argtypes = [i32, i64, i64, i64]
+        L.hip_qmm_mul_mat_glu.restype = i32
+        L.hip_qmm_mul_mat_glu.argtypes = [i32, vp, vp, i64, i64, i64, vp, i64, i64, i32, ctypes.c_float,
+                                          ctypes.c_float, vp, i64, vp, ctypes.c_size_t, vp]
+        L.hip_qmm_mul_mat_id_glu.restype = i32
+        L.hip_qmm_mul_mat_id_glu.argtypes = [i32, vp, vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64,
+                                             i32, ctypes.c_float, ctypes.c_float, vp, i64, vp, ctypes.c_size_t, vp]
         L.hip_qmm_mul_mat_vec_q.restype = i32
         L.hip_qmm_mul_mat_vec_q.argtypes = [i32, vp, vp, vp, vp] + [i64] * 18 + [vp]
         L.hip_qmm_block_dots.restype = i32
@@ -355,6 +371,47 @@ def mmq(qtype, w: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor, out=
     return out
 
 
+def _glu_weights(qtype, w, w_gate, K):
+    t, nrows, rs = _weight_args(qtype, w, K)
+    tg, ng, rg = _weight_args(qtype, w_gate, K)
+    if (ng, rg) != (nrows, rs):
+        raise HipQmmError("w_gate must match w")
+    return t, nrows, rs
+
+
+def mmq_glu(qtype, w: torch.Tensor, w_gate: torch.Tensor, K: int, qs: torch.Tensor, ds: torch.Tensor,
+            glu="SWIGLU", alpha=1.702, limit=7.0, out=None):
+    """Gate/up/GLU fused MMQ: out[c] = glu(Wg y_c, W y_c) over planar Q8_1 columns."""
+    t, nrows, rs = _glu_weights(qtype, w, w_gate, K)
+    n = qs.shape[0]
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    out = torch.empty((n, nrows), dtype=torch.float32, device=w.device) if out is None else out
+    _check(lib().hip_qmm_mmq_glu(t, _ptr(w), _ptr(w_gate), K, nrows, rs, _ptr(qs), _ptr(ds), n, op, alpha, limit,
+                                 _ptr(out), out.stride(0), _stream()), "hip_qmm_mmq_glu")
+    return out
+
+
+def mul_mat_glu(qtype, w: torch.Tensor, w_gate: torch.Tensor, x: torch.Tensor, glu="SWIGLU", alpha=1.702,
+                limit=7.0, out=None, workspace=None):
+    """{MUL_MAT gate, MUL_MAT up, GLU}: x f32 [N, K] -> glu(Wg x, W x) f32 [N, nrows]."""
+    _require_cuda(x)
+    if x.dtype != torch.float32 or x.dim() != 2:
+        raise HipQmmError("x must be a 2-D float32 tensor [ncols, K]")
+    n, K = x.shape
+    t, nrows, rs = _glu_weights(qtype, w, w_gate, K)
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    need = int(lib().hip_qmm_mul_mat_glu_workspace_size(t, K, nrows, n))
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=x.device)
+    elif workspace.numel() < need:
+        raise HipQmmError(f"workspace too small: {workspace.numel()} < {need}")
+    out = torch.empty((n, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_glu(t, _ptr(w), _ptr(w_gate), K, nrows, rs, _ptr(x), n, x.stride(0), op, alpha,
+                                     limit, _ptr(out), out.stride(0), _ptr(workspace), workspace.numel(), _stream()),
+           "hip_qmm_mul_mat_glu")
+    return out
+
+
 def mul_mat_vec_q(qtype, w: torch.Tensor, y_q8_1: torch.Tensor, K: int, ncols_dst: int, dst: torch.Tensor, *,
                   nchannels_x=1, nchannels_y=1, nchannels_dst=1, nsamples_x=1, nsamples_dst=1,
                   stride_col_y, stride_col_dst, stride_channel_x=0, stride_channel_y=0, stride_channel_dst=0,
@@ -456,4 +513,32 @@ def mul_mat_id(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, out=N
     _check(lib().hip_qmm_mul_mat_id(t, _ptr(w), K, nrows, w.stride(1), w.stride(0), n_as, _ptr(x), ne11, n_tokens,
                                     K, _ptr(ids), n_ids, n_ids, _ptr(out), nrows, _ptr(workspace),
                                     workspace.numel(), _stream()), "hip_qmm_mul_mat_id")
+    return out
+
+
+def mul_mat_id_glu(qtype, w: torch.Tensor, w_gate: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, glu="SWIGLU",
+                   alpha=1.702, limit=7.0, out=None, workspace=None):
+    """Gate/up/GLU over ggml_mul_mat_id's routed pairs: f32 [n_tokens, n_ids, nrows] =
+    glu(Wg_e x, W_e x) with e = ids[t, s] (zero rows for ids outside [0, n_as))."""
+    _require_cuda(w, w_gate, x, ids)
+    if w.shape != w_gate.shape or w.stride() != w_gate.stride() or w.dtype != torch.uint8 or w.dim() != 3:
+        raise HipQmmError("w and w_gate must be matching 3-D uint8 tensors [n_as, nrows, row_bytes]")
+    if x.dtype != torch.float32 or x.dim() != 3 or ids.dtype != torch.int32 or ids.dim() != 2:
+        raise HipQmmError("x must be f32 [n_tokens, ne11, K] and ids int32 [n_tokens, n_ids]")
+    t = TYPE_IDS[qtype] if isinstance(qtype, str) else int(qtype)
+    n_as, nrows, rb = w.shape
+    n_tokens, ne11, K = x.shape
+    n_ids = ids.shape[1]
+    if ids.shape[0] != n_tokens or rb < row_size(t, K):
+        raise HipQmmError("ids, x and w disagree on the shape")
+    op = GLU_OPS[glu] if isinstance(glu, str) else int(glu)
+    need = int(lib().hip_qmm_mul_mat_id_workspace_size(t, K, n_as, ne11, n_tokens, n_ids))
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    elif workspace.numel() < need:
+        raise HipQmmError(f"workspace too small: {workspace.numel()} < {need}")
+    out = torch.empty((n_tokens, n_ids, nrows), dtype=torch.float32, device=x.device) if out is None else out
+    _check(lib().hip_qmm_mul_mat_id_glu(t, _ptr(w), _ptr(w_gate), K, nrows, w.stride(1), w.stride(0), n_as, _ptr(x),
+                                        ne11, n_tokens, K, _ptr(ids), n_ids, n_ids, op, alpha, limit, _ptr(out), nrows,
+                                        _ptr(workspace), workspace.numel(), _stream()), "hip_qmm_mul_mat_id_glu")
     return out
