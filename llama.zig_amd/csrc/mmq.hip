@@ -378,14 +378,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_kernel(
     constexpr bool LEGACY = TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0;  // one scale per 32-block, no super-block
     __shared__ Smem<TYPE, BN> sm;
     const int64_t Kp = pad_k(K);
-    const bool fused = glu.gate != nullptr;                        // uniform
-    const int64_t row0 = (int64_t)blockIdx.x * (fused ? BM / 2 : BM);  // first output row
+    const bool fused = glu.gate != nullptr;  // uniform
+    // dense tiles in the XCD-aware banded order (one K part); grouped tiles as launched
+    int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+    if (!tiles && gridDim.z == 1) mmq_tile_order(bx + (int)gridDim.x * by, (int)gridDim.x, (int)gridDim.y, bx, by);
+    const int64_t row0 = (int64_t)bx * (fused ? BM / 2 : BM);  // first output row
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
 
     // column tile: dense (col0 .. col0+BN of ncols) or one expert's routed columns
-    int64_t col0 = (int64_t)blockIdx.y * BN, col_end = ncols;
+    int64_t col0 = (int64_t)by * BN, col_end = ncols;
     const uint8_t *wexp = w, *wgexp = glu.gate;
     if (tiles) {
         if ((int)blockIdx.y >= *n_tiles) return;  // uniform per workgroup

@@ -329,7 +329,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     if constexpr (!PERSIST) {
         // one tile per workgroup: grid (row tiles, column tiles, K parts)
         if ((int)blockIdx.y >= gy_live) return;  // grouped: past the live tiles (uniform)
-        const Item C = item_xyz((int)blockIdx.x, (int)blockIdx.y, (int)blockIdx.z);
+        int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+        if (!GROUPED && gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
+        const Item C = item_xyz(bx, by, (int)blockIdx.z);
         set_sources(C);
         dma(C.kb0, sA0, sB0, sD0);
         wait_vmem();

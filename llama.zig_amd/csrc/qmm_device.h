@@ -284,6 +284,25 @@ __device__ __forceinline__ float glu_apply(int op, float g, float u, float alpha
     return x / (1.0f + expf(-x)) * y;  // GLU_SWIGLU_CLAMP
 }
 
+// Tile order of a dense MMQ grid (gx row tiles x gy column tiles, one K part),
+// from the workgroup's linear id L = blockIdx.x + gx * blockIdx.y.  The
+// dispatcher deals consecutive workgroups to the 8 XCDs in turn, and each XCD
+// has its own L2, so the workgroups of one XCD (ids L = xcd mod 8) get one
+// contiguous run v of the tile sequence.  The sequence walks bands of
+// MMQ_BAND row tiles: within a band every column tile in turn, and for each
+// the band's row tiles, so the tiles an XCD holds at once share a few weight
+// row tiles and a few activation column tiles in its L2.  A bijection of
+// [0, gx*gy).
+constexpr int MMQ_BAND = 8;
+__device__ __forceinline__ void mmq_tile_order(int L, int gx, int gy, int &bx, int &by) {
+    const int n = gx * gy, q = n >> 3, r = n & 7, xcd = L & 7, slot = L >> 3;
+    const int v = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + slot;
+    const int band = v / (MMQ_BAND * gy), idx = v - band * (MMQ_BAND * gy);
+    const int rows = gx - band * MMQ_BAND < MMQ_BAND ? gx - band * MMQ_BAND : MMQ_BAND;
+    bx = band * MMQ_BAND + idx % rows;
+    by = idx / rows;
+}
+
 // Gate/up/GLU fusion of the MMQ kernels (the reference's mul_mat_q with a
 // gate, src/ggml/cuda/mmq.zig:568-640).  With gate != nullptr a 128-row tile
 // holds 64 output rows: tile row t reads output row 2 * (t / 4) + t % 2 of the
