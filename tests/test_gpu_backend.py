@@ -186,3 +186,77 @@ def test_graph_mul_mat_batched_dims_2_and_3(hb, tname, N, bw, bx):
             xi = i3 * bx[0] + i2
             cpu = O.mul_mat(t, w[wi], M, K, x[xi], nth=8)
             assert nmse(got[xi], cpu) < NMSE_GATE, (i2, i3)
+
+
+def test_chunked_async_upload_as_the_loader_does(hb):
+    """The loader's upload of a tensor from a GGUF file (src/llama/loader.zig:
+    1601-1640): the file read at an aligned offset into a ring of pinned host
+    buffers from the host buffer type, each chunk sent with the backend's
+    set_tensor_async at its running offset, an event recorded per buffer and
+    synchronized before the buffer is reused.  The uploaded weight equals a
+    one-call set_tensor byte for byte, and a MUL_MAT on it equals the same
+    MUL_MAT on the one-call copy."""
+    import ggml_hip.backend as B
+    from ggml_hip import abi
+    L = B.lib()
+    K, M = 4096, 2048
+    wq = np.array(weights_q(O.TYPE_Q4_K, M, K, 3))
+    rng = np.random.default_rng(8)
+    head = 123_457  # the tensor's offset in the file: not a multiple of the read alignment
+    blob = np.concatenate([rng.integers(0, 256, head, dtype=np.uint8), wq.reshape(-1),
+                           rng.integers(0, 256, 999, dtype=np.uint8)])
+    n_size = wq.nbytes
+    a = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M], name=b"chunked")
+    ref = abi.make_tensor(abi.GGML_TYPE_Q4_K, [K, M], name=b"one_call")
+    hb.alloc([a, ref], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.set(ref, wq)
+    # the ring: n_buffers pinned host buffers of buffer_size (+ alignment slack) and an event each
+    hbt_ptr = L.ggml_backend_hip_host_buffer_type()
+    hbt = abi.deref(hbt_ptr, abi.buffer_type)
+    rp = L.ggml_backend_hip_reg()
+    dp = B.registry().iface.get_device(rp, 0)
+    dev = abi.deref(dp, abi.device)
+    n_buffers, buffer_size, alignment = 4, 1 << 20, 4096
+    bufs = [hbt.iface.alloc_buffer(hbt_ptr, buffer_size + alignment) for _ in range(n_buffers)]
+    assert all(bufs)
+    host = [abi.deref(b, abi.buffer).iface.get_base(b) for b in bufs]
+    events = [dev.iface.event_new(dp) for _ in range(n_buffers)]
+    try:
+        aligned_offset = head & ~(alignment - 1)
+        offset_from_alignment = head - aligned_offset
+        read_end = (head + n_size + alignment - 1) & ~(alignment - 1)
+        bytes_read = data_read = 0
+        idx = 0
+        while bytes_read < read_end - aligned_offset:
+            read_size = min(buffer_size, read_end - aligned_offset - bytes_read)
+            dst = (host[idx] + alignment - 1) & ~(alignment - 1)
+            dev.iface.event_synchronize(dp, events[idx])
+            src = blob[aligned_offset + bytes_read:aligned_offset + bytes_read + read_size]
+            C.memmove(dst, src.ctypes.data, src.nbytes)  # the file read (short at the file's end)
+            ptr, to_copy = dst, read_size
+            if bytes_read == 0:
+                ptr += offset_from_alignment
+                to_copy -= offset_from_alignment
+            if aligned_offset + bytes_read + read_size > head + n_size:
+                to_copy -= read_end - (head + n_size)
+            hb.be.iface.set_tensor_async(hb.be_ptr, C.pointer(a), ptr, data_read, to_copy)
+            hb.be.iface.event_record(hb.be_ptr, events[idx])
+            data_read += to_copy
+            bytes_read += read_size
+            idx = (idx + 1) % n_buffers
+        assert data_read == n_size
+        hb.be.iface.synchronize(hb.be_ptr)
+    finally:
+        for e in events:
+            dev.iface.event_free(dp, e)
+        for b in bufs:
+            abi.deref(b, abi.buffer).iface.free_buffer(b)
+    got = hb.get(a, np.uint8, (n_size,))
+    np.testing.assert_array_equal(got, wq.reshape(-1))
+    x = abi.make_tensor(abi.GGML_TYPE_F32, [K, 3], name=b"x")
+    d1 = abi.make_tensor(abi.GGML_TYPE_F32, [M, 3], op=abi.GGML_OP_MUL_MAT, srcs=(a, x), name=b"d1")
+    d2 = abi.make_tensor(abi.GGML_TYPE_F32, [M, 3], op=abi.GGML_OP_MUL_MAT, srcs=(ref, x), name=b"d2")
+    hb.alloc([x, d1, d2], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    hb.set(x, acts(3, K))
+    assert hb.compute([d1, d2]) == abi.GGML_STATUS_SUCCESS
+    np.testing.assert_array_equal(hb.get(d1, np.float32, (3, M)), hb.get(d2, np.float32, (3, M)))

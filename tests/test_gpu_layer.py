@@ -144,3 +144,102 @@ def test_llama3_8b_decode_layer_in_splits(hb, layer_weights, T):
     dc = O.mul_mat_x86(W["down"][0], W["down"][1], D, FF, a_cpu, nth=8)
     assert nmse(outv, hv + dc) < NMSE_GATE
     assert np.all(np.isfinite(outv))
+
+
+# ---------------------------------------------------------------- Qwen3-30B-A3B MoE FFN in splits
+
+QN_EMBD, QN_FF, QN_EXPERTS, QN_TOP_K = 2048, 768, 128, 8
+GGML_OP_MUL, GGML_OP_SOFT_MAX, GGML_OP_GET_ROWS, GGML_OP_TOP_K = 6, 43, 39, 67  # src/ggml/types.zig:24-48
+
+
+@pytest.fixture(scope="module")
+def moe_weights():
+    """Qwen3-30B-A3B's routed experts (128 of them, gate/up 768x2048 and down
+    2048x768 each, Q4_K), synthetic N(0, 0.02) quantized by the oracle."""
+    q4 = O.TYPE_Q4_K
+    from cases import weights_f32
+
+    def experts(nrows, K, idx):
+        return O.quantize_rows(q4, weights_f32(QN_EXPERTS * nrows, K, idx)).reshape(QN_EXPERTS, nrows, -1)
+    return {"gate": experts(QN_FF, QN_EMBD, 20), "up": experts(QN_FF, QN_EMBD, 21),
+            "down": experts(QN_EMBD, QN_FF, 22)}
+
+
+@pytest.mark.parametrize("T", [1, 64])
+def test_qwen3_moe_ffn_in_splits(hb, moe_weights, T):
+    """The MoE FFN of llama's graph (build_moe_ffn, src/llama/graph.zig:3265-3400)
+    as the scheduler splits it: the router (an f32 MUL_MAT), its softmax, top-k
+    and weights stay on the CPU (supports_op false), then one split for the
+    HIP backend:
+
+      [norm, router, softmax, top-k, weights] | up gate glu down | [weighted sum]
+
+    up / gate / GLU fuse into one launch (the ids GEMV at one token, the
+    grouped fused MMQ at 64), so up and gate stay NaN; down runs the grouped
+    MMQ or the ids GEMV.  The expert outputs are checked against the CPU path
+    (mul_mat_id and the GLU op of the oracle) with NMSE < 5e-4, and so is the
+    layer's weighted sum over the 8 slots."""
+    from ggml_hip import abi
+    from cases import nmse as _nmse
+    W = moe_weights
+    f32, i32, q4 = abi.GGML_TYPE_F32, abi.GGML_TYPE_I32, abi.GGML_TYPE_Q4_K
+    x = abi.make_tensor(f32, [QN_EMBD, 1, T], name=b"x")
+    norm = abi.make_tensor(f32, [QN_EMBD, 1, T], op=GGML_OP_RMS_NORM, srcs=(x,), name=b"ffn_norm")
+    w_inp = abi.make_tensor(f32, [QN_EMBD, QN_EXPERTS], name=b"ffn_gate_inp")
+    logits = abi.make_tensor(f32, [QN_EXPERTS, T], op=abi.GGML_OP_MUL_MAT, srcs=(w_inp, norm), name=b"logits")
+    probs = abi.make_tensor(f32, [QN_EXPERTS, T], op=GGML_OP_SOFT_MAX, srcs=(logits,), name=b"probs")
+    sel = abi.make_tensor(i32, [QN_TOP_K, T], op=GGML_OP_TOP_K, srcs=(probs,), name=b"selected")
+    wts = abi.make_tensor(f32, [1, QN_TOP_K, T], op=GGML_OP_GET_ROWS, srcs=(probs, sel), name=b"weights")
+    wg = abi.make_tensor(q4, [QN_EMBD, QN_FF, QN_EXPERTS], name=b"ffn_gate_exps")
+    wu = abi.make_tensor(q4, [QN_EMBD, QN_FF, QN_EXPERTS], name=b"ffn_up_exps")
+    wd = abi.make_tensor(q4, [QN_FF, QN_EMBD, QN_EXPERTS], name=b"ffn_down_exps")
+    up = abi.make_tensor(f32, [QN_FF, QN_TOP_K, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(wu, norm, sel), name=b"up")
+    gate = abi.make_tensor(f32, [QN_FF, QN_TOP_K, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(wg, norm, sel), name=b"gate")
+    par = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, gate, up, [QN_FF, QN_TOP_K, T], name=b"ffn_par")
+    down = abi.make_tensor(f32, [QN_EMBD, QN_TOP_K, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(wd, par, sel), name=b"down")
+    weighted = abi.make_tensor(f32, [QN_EMBD, QN_TOP_K, T], op=GGML_OP_MUL, srcs=(down, wts), name=b"weighted")
+    weighted.flags |= abi.GGML_TENSOR_FLAG_OUTPUT
+    nodes = [norm, logits, probs, sel, wts, up, gate, par, down, weighted]
+    from ggml_hip.backend import lib as backend_lib
+    ok = lambda t: bool(backend_lib().ggml_backend_hip_op_supported(C.pointer(t)))  # noqa: E731
+    assert [ok(n) for n in nodes] == [False] * 5 + [True] * 4 + [False]
+
+    hb.alloc([wg, wu, wd], usage=abi.GGML_BACKEND_BUFFER_USAGE_WEIGHTS)
+    hb.alloc([norm, sel, up, gate, par, down], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    for t_, name in ((wg, "gate"), (wu, "up"), (wd, "down")):
+        hb.set(t_, W[name])
+    for n in (up, gate, par, down):
+        hb.set(n, np.full(abi.nbytes(n) // 4, np.nan, dtype=np.float32))
+
+    # CPU: norm, router, softmax, top-8, their weights (renormalised, Qwen3's norm_w)
+    xv = acts(T, QN_EMBD, 9)
+    nv = _rms_norm(xv)
+    rng = np.random.default_rng(31)
+    router = (rng.standard_normal((QN_EXPERTS, QN_EMBD)) * 0.02).astype(np.float32)
+    lg = nv @ router.T
+    p = np.exp(lg - lg.max(axis=1, keepdims=True))
+    p /= p.sum(axis=1, keepdims=True)
+    ids = np.argsort(-p, axis=1, kind="stable")[:, :QN_TOP_K].astype(np.int32)
+    wv = np.take_along_axis(p, ids, axis=1)
+    wv /= wv.sum(axis=1, keepdims=True)
+    hb.set(norm, nv)
+    hb.set(sel, ids)
+    # the HIP split: up gate glu down
+    assert hb.compute_view(nodes, 5, 9) == abi.GGML_STATUS_SUCCESS
+    shape_ff = (T, QN_TOP_K, QN_FF)
+    assert np.isnan(hb.get(up, np.float32, shape_ff)).all() and np.isnan(hb.get(gate, np.float32, shape_ff)).all()
+    par_gpu = hb.get(par, np.float32, shape_ff)
+    dn_gpu = hb.get(down, np.float32, (T, QN_TOP_K, QN_EMBD))
+    # the CPU path on the same inputs
+    xr = nv.reshape(T, 1, QN_EMBD)
+    cg = O.mul_mat_id(O.TYPE_Q4_K, W["gate"], QN_EXPERTS, QN_FF, QN_EMBD, xr, ids, nth=8)
+    cu = O.mul_mat_id(O.TYPE_Q4_K, W["up"], QN_EXPERTS, QN_FF, QN_EMBD, xr, ids, nth=8)
+    par_cpu = O.glu(O.GLU_SWIGLU, cg, cu)
+    assert _nmse(par_gpu, par_cpu) < NMSE_GATE
+    dn_cpu = O.mul_mat_id(O.TYPE_Q4_K, W["down"], QN_EXPERTS, QN_EMBD, QN_FF, par_cpu, ids, nth=8)
+    assert _nmse(dn_gpu, dn_cpu) < NMSE_GATE
+    # CPU: the weighted sum over the slots
+    out_gpu = (dn_gpu * wv[:, :, None]).sum(axis=1)
+    out_cpu = (dn_cpu * wv[:, :, None]).sum(axis=1)
+    assert _nmse(out_gpu, out_cpu) < NMSE_GATE
+    assert np.all(np.isfinite(out_gpu))
