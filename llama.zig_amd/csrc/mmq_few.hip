@@ -1,5 +1,5 @@
-// mmq_few.hip -- Q4_K / Q6_K / Q8_0 GEMM for few activation columns (up to 32),
-// on 16x16 int8 MFMA.
+// mmq_few.hip -- Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 GEMM for few activation
+// columns (up to 32), on 16x16 int8 MFMA.
 //
 // The reference sends 2-24 src1 columns to a separate "few-row" MMQ kernel
 // (src/ggml/cuda/mmq_few.zig:1-20, mulMatQFew :204-255, shouldUseMmqFew
@@ -29,8 +29,14 @@
 // (vmcnt = its transfer count of one step) before the step's barrier.  The
 // weight decode (nibbles, scales) is shared by the column tiles.
 //
+// Q5_K (176-byte blocks, 16-byte aligned like Q4_K) takes the Q4_K path with
+// the fifth bit of each element merged from qh (bit g of qh[l] for element l
+// of sub-block g).
+//
 // The 2-byte-aligned types (the reference routes them here too,
 // mmq_few.zig:246-266): a K-step is still 256 weights of a row.
+//   - Q4_0: 8 blocks of 18 bytes, 144 bytes, 16-byte aligned when the rows
+//     are; the Q8_0 path with the lane's 8 nibbles taken as q - 8 (bytewise).
 //   - Q8_0: 8 blocks of 34 bytes, 272 bytes, 16-byte aligned when the rows
 //     are; per block S_b from one int8 MFMA and the scale d_w * d8 from the
 //     f16 scale MFMA; no super-block terms.
@@ -68,6 +74,16 @@ template <>
 struct FewFmt<TYPE_Q4_K> {
     static constexpr int WROW = Q4K_BYTES;
     __device__ static int64_t aoff(int kb) { return (int64_t)kb * Q4K_BYTES; }
+};
+template <>
+struct FewFmt<TYPE_Q5_K> {
+    static constexpr int WROW = Q5K_BYTES;  // 176, 16-byte aligned
+    __device__ static int64_t aoff(int kb) { return (int64_t)kb * Q5K_BYTES; }
+};
+template <>
+struct FewFmt<TYPE_Q4_0> {
+    static constexpr int WROW = 8 * Q40_BYTES;  // 144
+    __device__ static int64_t aoff(int kb) { return (int64_t)kb * (8 * Q40_BYTES); }
 };
 template <>
 struct FewFmt<TYPE_Q8_0> {
@@ -123,6 +139,13 @@ __device__ __forceinline__ uint2 lds8_a2(const uint8_t *p) {
 __device__ __forceinline__ uint32_t q6_signed(uint32_t q) {
     const uint32_t x = q ^ 0x20202020u, t = x & 0x20202020u;
     return x | (t << 1) | (t << 2);
+}
+
+// Q4_0 nibbles q (0..15 per byte) to q - 8 as signed bytes: q ^ 8 is
+// (q - 8) mod 16; its bit 3 copied into bits 4-7 sign-extends it.
+__device__ __forceinline__ uint32_t q4_0_signed(uint32_t q) {
+    const uint32_t x = q ^ 0x08080808u, t = x & 0x08080808u;
+    return x | (t << 1) | (t << 2) | (t << 3) | (t << 4);
 }
 
 // 16 bytes per lane from global memory to LDS at base + 16 * lane (base is
@@ -274,8 +297,17 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         for (int j = 0; j < NCT; ++j) col_headers(st, j, bcol[j], dh0[j], dh1[j]);
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
-            const uint8_t *blk = arow + g * Q80_BYTES;
-            const uint2 a = lds8_a2(blk + 2 + 8 * kq);
+            // Q8_0: the lane's 8 codes of block g; Q4_0: byte j of the 16 holds
+            // element j (low nibble) and j + 16 (high), taken as q - 8
+            const uint8_t *blk = arow + g * (TYPE == TYPE_Q4_0 ? Q40_BYTES : Q80_BYTES);
+            uint2 a;
+            if constexpr (TYPE == TYPE_Q4_0) {
+                const uint2 q = lds8_a2(blk + 2 + 8 * (kq & 1));
+                const int sh = 4 * (kq >> 1);
+                a = make_uint2(q4_0_signed((q.x >> sh) & 0x0F0F0F0Fu), q4_0_signed((q.y >> sh) & 0x0F0F0F0Fu));
+            } else {
+                a = lds8_a2(blk + 2 + 8 * kq);
+            }
             const uint32_t dw = (uint32_t)*reinterpret_cast<const uint16_t *>(blk) & m_sc;
             const v4h sa = scale_a(g, dw);
             const int c = 2 * g + (kq >> 1);
@@ -344,9 +376,15 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         }
     };
 
+    // Q4_K, and Q5_K (block {d, dmin, scales[12], qh[32], qs[128]}: the same
+    // header, the fifth bit of element l of sub-block g is bit g of qh[l])
     auto compute = [&](const uint8_t *st) {
-        const uint8_t *arow = st + (wave * 16 + li) * Q4K_BYTES;
+        constexpr bool Q5 = TYPE == TYPE_Q5_K;
+        constexpr int QS = Q5 ? 48 : 16;  // the nibbles' offset in the block
+        const uint8_t *arow = st + (wave * 16 + li) * WROW;
         const uint4 hdr = *reinterpret_cast<const uint4 *>(arow);
+        uint2 qh = make_uint2(0u, 0u);  // fifth bits of the lane's 8 elements of every sub-block
+        if constexpr (Q5) qh = *reinterpret_cast<const uint2 *>(arow + 16 + 8 * kq);
         // getScaleMinK4 for all 8 sub-blocks, four per dword (bytes)
         const uint32_t sc_lo = hdr.y & 0x3F3F3F3Fu & m_sc;
         const uint32_t sc_hi = ((hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u)) & m_sc;
@@ -368,9 +406,13 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         v4f accb[NCT];
 #pragma unroll
         for (int g = 0; g < 8; ++g) {
-            const uint2 q = *reinterpret_cast<const uint2 *>(arow + 16 + 32 * (g >> 1) + 8 * kq);
+            const uint2 q = *reinterpret_cast<const uint2 *>(arow + QS + 32 * (g >> 1) + 8 * kq);
             const int sh = 4 * (g & 1);
-            const uint2 a = make_uint2((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
+            uint2 a = make_uint2((q.x >> sh) & 0x0F0F0F0Fu, (q.y >> sh) & 0x0F0F0F0Fu);
+            if constexpr (Q5) {
+                a.x |= ((qh.x >> g) & 0x01010101u) << 4;
+                a.y |= ((qh.y >> g) & 0x01010101u) << 4;
+            }
             // d8 of block g sits in K slot 0 (g even) or 2 (g odd) of the
             // headers of blocks 2h, 2h+1 (h = g/2) as stored; A puts sc there
             const uint32_t scf = byte_f16(g < 4 ? sc_lo : sc_hi, g & 3);
@@ -397,7 +439,7 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         float dr[4], dn[4];
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
-            const uint32_t dd = *reinterpret_cast<const uint32_t *>(st + (wave * 16 + 4 * kq + v) * Q4K_BYTES);
+            const uint32_t dd = *reinterpret_cast<const uint32_t *>(st + (wave * 16 + 4 * kq + v) * WROW);
             dr[v] = h2f(dd);
             dn[v] = -h2f(dd >> 16);
         }
@@ -425,8 +467,8 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
             wait_step<NST - 2, G::transfers_of(0), G::transfers_of(NW - 1)>(big, left < NST - 2 ? left : NST - 2);
             lds_barrier();
             if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
-            if constexpr (TYPE == TYPE_Q4_K) compute(st[i]);
-            else if constexpr (TYPE == TYPE_Q8_0) compute_q8_0(st[i]);
+            if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) compute(st[i]);
+            else if constexpr (TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) compute_q8_0(st[i]);
             else compute_q6_k(st[i], kb);
             if (++kb >= kb1) break;
         }
@@ -473,14 +515,14 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
     return (int)split;
 }
 
-// Whether the few-column kernel takes this weight layout: Q4_K; Q8_0 and
-// Q6_K with 16-byte-aligned rows (and, Q6_K, K % 2048 == 0, so that its
-// aligned windows stay inside the row).
+// Whether the few-column kernel takes this weight layout: Q4_K and Q5_K;
+// Q8_0, Q4_0 and Q6_K with 16-byte-aligned rows (and, Q6_K, K % 2048 == 0,
+// so that its aligned windows stay inside the row).
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride) {
-    if (type == TYPE_Q4_K) return true;
-    if (type != TYPE_Q8_0 && type != TYPE_Q6_K) return false;
+    if (type == TYPE_Q4_K || type == TYPE_Q5_K) return true;
+    if (type != TYPE_Q8_0 && type != TYPE_Q4_0 && type != TYPE_Q6_K) return false;
     if ((uintptr_t)w % 16 || row_stride % 16 || K % QK_K) return false;
-    return type == TYPE_Q8_0 || K % 2048 == 0;
+    return type != TYPE_Q6_K || K % 2048 == 0;
 }
 
 // Launch for mmq.hip's dispatch: the rows as mmq_few_takes says, the
@@ -509,6 +551,14 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
     case TYPE_Q6_K:  // one column tile: two measured slower than the 128-row MMQ tile
         if (ncols > 16) return (int)hipErrorInvalidValue;
         FEW_LAUNCH(TYPE_Q6_K, 1);
+        break;
+    case TYPE_Q5_K:
+        if (ncols > 16) FEW_LAUNCH(TYPE_Q5_K, 2);
+        else FEW_LAUNCH(TYPE_Q5_K, 1);
+        break;
+    case TYPE_Q4_0:
+        if (ncols > 16) FEW_LAUNCH(TYPE_Q4_0, 2);
+        else FEW_LAUNCH(TYPE_Q4_0, 1);
         break;
     default:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q4_K, 2);
