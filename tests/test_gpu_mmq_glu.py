@@ -52,7 +52,7 @@ def _mmq_unsplit(G, tname, w_d, K, qs, ds, n):
 
 def _few_takes(G, tname, K, n):
     """Whether hip_qmm_mmq would send n columns to the few-column kernel."""
-    return (n <= 32 and tname in ("Q4_K", "Q8_0")) or (n <= 16 and tname == "Q6_K" and K % 2048 == 0)
+    return (n <= 32 and tname in ("Q4_K", "Q5_K", "Q8_0", "Q4_0")) or (n <= 16 and tname == "Q6_K" and K % 2048 == 0)
 
 
 @pytest.mark.parametrize("tname", list(TYPES))
