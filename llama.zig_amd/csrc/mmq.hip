@@ -779,18 +779,21 @@ int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return (int)split;
 }
 
-// The few-column kernel (mmq_few.hip) takes Q4_K, Q5_K, Q8_0 and Q4_0 up to
-// 32 columns and Q6_K up to 16 (K % 2048 == 0; Q8_0 / Q4_0 / Q6_K on
-// 16-byte-aligned rows), when the activation planes are 16-byte aligned.
+// The few-column kernel (mmq_few.hip) takes Q4_K, Q5_K, Q8_0, Q4_0 and IQ4_XS
+// up to 32 columns and Q6_K up to 16 (K % 2048 == 0; Q8_0 / Q4_0 / Q6_K /
+// IQ4_XS on 16-byte-aligned rows), when the activation planes are 16-byte
+// aligned.
 // Measured against the 128-row tile (us, 4096x14336, same weights): Q8_0 9 /
 // 32 columns 18.6 / 23.2 against 33.2 / 39.1; Q5_K 16.0 / 21.0 against 23.2 /
-// 26.4; Q4_0 16.1 / 20.8 against 24.5 / 28.6; Q6_K 9 / 16 columns 22.6 / 23.2
+// 26.4; Q4_0 16.1 / 20.8 against 24.5 / 28.6; IQ4_XS (K % 512 == 0) 17.5 /
+// 21.4 against 24.0 / 24.6; Q6_K 9 / 16 columns 22.6 / 23.2
 // against 28.3 / 29.3, but 48.3 / 48.8 against 31.3 / 33.4 at 24 / 32 (two
 // column tiles), so those keep the tile.  few_cols_type is the part that depends on the shape alone
 // (the split and workspace queries); the dispatch also checks the rows
 // (mmq_few_takes).
 bool few_cols_type(int type, int64_t K, int64_t ncols) {
     return (ncols <= 32 && (type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K || type == TYPE_Q4_0)) ||
+           (ncols <= 32 && type == TYPE_IQ4_XS && K % 512 == 0) ||
            (ncols <= 16 && type == TYPE_Q6_K && K % 2048 == 0);
 }
 

@@ -1,5 +1,5 @@
-// mmq_few.hip -- Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 GEMM for few activation
-// columns (up to 32), on 16x16 int8 MFMA.
+// mmq_few.hip -- Q4_K / Q5_K / Q6_K / Q8_0 / Q4_0 / IQ4_XS GEMM for few
+// activation columns (up to 32), on 16x16 int8 MFMA.
 //
 // The reference sends 2-24 src1 columns to a separate "few-row" MMQ kernel
 // (src/ggml/cuda/mmq_few.zig:1-20, mulMatQFew :204-255, shouldUseMmqFew
@@ -37,6 +37,9 @@
 // mmq_few.zig:246-266): a K-step is still 256 weights of a row.
 //   - Q4_0: 8 blocks of 18 bytes, 144 bytes, 16-byte aligned when the rows
 //     are; the Q8_0 path with the lane's 8 nibbles taken as q - 8 (bytewise).
+//   - IQ4_XS: one 136-byte block at 8-byte alignment; the step moves the 144
+//     aligned bytes around it (from (136 * k) & ~15, the block 0 or 8 bytes
+//     in), which stay inside the row when K % 512 == 0.
 //   - Q8_0: 8 blocks of 34 bytes, 272 bytes, 16-byte aligned when the rows
 //     are; per block S_b from one int8 MFMA and the scale d_w * d8 from the
 //     f16 scale MFMA; no super-block terms.
@@ -84,6 +87,11 @@ template <>
 struct FewFmt<TYPE_Q4_0> {
     static constexpr int WROW = 8 * Q40_BYTES;  // 144
     __device__ static int64_t aoff(int kb) { return (int64_t)kb * (8 * Q40_BYTES); }
+};
+template <>
+struct FewFmt<TYPE_IQ4_XS> {
+    static constexpr int WROW = 144;  // the aligned window around one 136-byte block
+    __device__ static int64_t aoff(int kb) { return ((int64_t)kb * IQ4XS_BYTES) & ~(int64_t)15; }
 };
 template <>
 struct FewFmt<TYPE_Q8_0> {
@@ -378,6 +386,50 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
 
     // Q4_K, and Q5_K (block {d, dmin, scales[12], qh[32], qs[128]}: the same
     // header, the fifth bit of element l of sub-block g is bit g of qh[l])
+    // IQ4_XS (block {d, scales_h, scales_l[4], qs[128]}, 136 bytes): byte j of
+    // sub-block g's 16 holds elements j (low nibble) and j + 16 (high), which
+    // index the 16 int8 levels; sub-block g's scale is scales_l nibble g |
+    // scales_h bits 2g..2g+1 << 4, minus 32 (exact in f16, the scale MFMA's
+    // A); d once per step.  The window is 8-byte aligned around the block.
+    auto compute_iq4_xs = [&](const uint8_t *st, int kb) {
+        const int delta = (int)(((int64_t)kb * IQ4XS_BYTES) & 15);  // 0 or 8
+        const uint8_t *blk = st + (wave * 16 + li) * WROW + delta;
+        const uint2 hdr = *reinterpret_cast<const uint2 *>(blk);  // d | scales_h << 16, scales_l[4]
+        const uint8_t *bcol[NCT];
+        uint4 dh0[NCT], dh1[NCT];
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) col_headers(st, j, bcol[j], dh0[j], dh1[j]);
+        v4f accb[NCT];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const uint2 q = *reinterpret_cast<const uint2 *>(blk + 8 + 16 * g + 8 * (kq & 1));
+            const int sh = 4 * (kq >> 1);
+            const uint2 a = make_uint2(iq4nl_levels((q.x >> sh) & 0x0F0F0F0Fu), iq4nl_levels((q.y >> sh) & 0x0F0F0F0Fu));
+            const int ls = (int)(((hdr.y >> (4 * g)) & 0xFu) | (((hdr.x >> (16 + 2 * g)) & 3u) << 4)) - 32;
+            const v4h sa = scale_a(g, f16_bits((float)ls) & m_sc);
+            const int c = 2 * g + (kq >> 1);
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) {
+                const uint2 b = *reinterpret_cast<const uint2 *>(bcol[j] + 16 * (c ^ li) + 8 * (kq & 1));
+                const v4i zi = {0, 0, 0, 0};
+                const v4i S = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a), as_long(b), zi, 0, 0, 0);
+                const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+                const v4f SC = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, scale_b(g, dh0[j], dh1[j]), zf, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    accb[j][v] = g == 0 ? (float)S[v] * SC[v] : fmaf((float)S[v], SC[v], accb[j][v]);
+            }
+        }
+        // d of the output rows (4*kq + v of this wave's 16)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint8_t *ob = st + (wave * 16 + 4 * kq + v) * WROW + delta;
+            const float d = h2f((uint32_t)*reinterpret_cast<const uint16_t *>(ob));
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) acc[j][v] = fmaf(d, accb[j][v], acc[j][v]);
+        }
+    };
+
     auto compute = [&](const uint8_t *st) {
         constexpr bool Q5 = TYPE == TYPE_Q5_K;
         constexpr int QS = Q5 ? 48 : 16;  // the nibbles' offset in the block
@@ -469,6 +521,7 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
             if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
             if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) compute(st[i]);
             else if constexpr (TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) compute_q8_0(st[i]);
+            else if constexpr (TYPE == TYPE_IQ4_XS) compute_iq4_xs(st[i], kb);
             else compute_q6_k(st[i], kb);
             if (++kb >= kb1) break;
         }
@@ -516,12 +569,14 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
 }
 
 // Whether the few-column kernel takes this weight layout: Q4_K and Q5_K;
-// Q8_0, Q4_0 and Q6_K with 16-byte-aligned rows (and, Q6_K, K % 2048 == 0,
-// so that its aligned windows stay inside the row).
+// Q8_0, Q4_0, Q6_K and IQ4_XS with 16-byte-aligned rows (and, Q6_K,
+// K % 2048 == 0, IQ4_XS K % 512 == 0, so that their aligned windows stay
+// inside the row).
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride) {
     if (type == TYPE_Q4_K || type == TYPE_Q5_K) return true;
-    if (type != TYPE_Q8_0 && type != TYPE_Q4_0 && type != TYPE_Q6_K) return false;
+    if (type != TYPE_Q8_0 && type != TYPE_Q4_0 && type != TYPE_Q6_K && type != TYPE_IQ4_XS) return false;
     if ((uintptr_t)w % 16 || row_stride % 16 || K % QK_K) return false;
+    if (type == TYPE_IQ4_XS) return K % 512 == 0;
     return type != TYPE_Q6_K || K % 2048 == 0;
 }
 
@@ -559,6 +614,10 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
     case TYPE_Q4_0:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q4_0, 2);
         else FEW_LAUNCH(TYPE_Q4_0, 1);
+        break;
+    case TYPE_IQ4_XS:
+        if (ncols > 16) FEW_LAUNCH(TYPE_IQ4_XS, 2);
+        else FEW_LAUNCH(TYPE_IQ4_XS, 1);
         break;
     default:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q4_K, 2);

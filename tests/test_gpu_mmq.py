@@ -141,24 +141,27 @@ def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
 
 
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 3), (4096, 2048, 9), (700, 14336, 17), (4100, 4096, 32),
-                                           (64, 2048, 16), (256, 256, 24)])
-def test_few_columns_q5_k(nrows, K, ncols):
-    """Q5_K up to 32 columns takes the few-column kernel (the Q4_K data path
-    with the fifth bits merged from qh): within the f64 and CPU gates; the op
-    above 8 columns runs the same kernel."""
+                                           (64, 2048, 16), (256, 512, 24)])
+@pytest.mark.parametrize("tname", ["Q5_K", "IQ4_XS"])
+def test_few_columns_q5_k_iq4_xs(tname, nrows, K, ncols):
+    """Q5_K and IQ4_XS (K % 512 == 0) up to 32 columns take the few-column
+    kernel (Q5_K: the Q4_K data path with the fifth bits merged from qh;
+    IQ4_XS: an 8-byte-aligned window around each block, levels looked up by
+    byte permutes): within the f64 and CPU gates; the op above 8 columns runs
+    the same kernel."""
     import ggml_hip as G
-    t = O.TYPE_Q5_K
+    t = TYPES[tname]
     assert G.lib().hip_qmm_mmq_split_k(t, K, nrows, ncols) >= 1
     wq = weights_q(t, nrows, K)
     x = acts(ncols, K)
     w_d = torch.from_numpy(np.array(wq)).cuda()
     x_d = torch.from_numpy(np.array(x)).cuda()
     qs, ds = G.quantize_q8_1_planar(x_d)
-    got = G.mmq("Q5_K", w_d, K, qs, ds).cpu().numpy()
+    got = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
     y = G.quantize_q8_1(x_d, K).cpu().numpy()
     ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
     assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
     cpu = O.mul_mat_x86(t, wq, nrows, K, x, nth=8)
     assert nmse(got, cpu) < NMSE_GATE
     if ncols > 8:
-        np.testing.assert_array_equal(G.mul_mat("Q5_K", w_d, x_d).cpu().numpy(), got)
+        np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
