@@ -346,12 +346,15 @@ def run_suite(name, torch, G, dev, reps):
         elif name == "few":
             # batched decode: the few-column GEMM against the GEMV (<= 8
             # columns) and the 128-row MMQ tile it replaced (9-32 columns;
-            # for Q6_K / Q8_0 the tile is timed on the same weights at a
-            # 2-byte-aligned base, which the few-column kernel does not take)
+            # for Q6_K / Q8_0 / Q4_0 / IQ4_XS the tile is timed on the same
+            # weights at a base 2 (IQ4_XS: 8) bytes past 16-byte alignment,
+            # which the few-column kernel does not take; Q5_K rows must be
+            # 16-byte aligned for both, so it has no tile line)
             shapes = [("Q4_K", 14336, 4096, "ffn_gate/up"), ("Q4_K", 4096, 14336, "Q4_K 4096x14336"),
                       ("Q4_K", 4096, 4096, "attn_q/o"), ("Q6_K", 4096, 14336, "ffn_down"),
                       ("Q6_K", 4096, 4096, "Q6_K 4096x4096"), ("Q8_0", 4096, 4096, "Q8_0 4096x4096"),
-                      ("Q8_0", 4096, 14336, "Q8_0 4096x14336")]
+                      ("Q8_0", 4096, 14336, "Q8_0 4096x14336"), ("Q5_K", 4096, 14336, "Q5_K 4096x14336"),
+                      ("Q4_0", 4096, 14336, "Q4_0 4096x14336"), ("IQ4_XS", 4096, 14336, "IQ4_XS 4096x14336")]
             batches = (4, 6, 8, 9, 16, 24, 32)
         else:
             shapes = [(t, 4096, k, f"{t} 4096x{k}") for t in ("Q8_0", "Q6_K", "Q4_K", "Q5_K", "Q4_0", "IQ4_XS")
@@ -380,12 +383,13 @@ def run_suite(name, torch, G, dev, reps):
                     few_fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
                     extra["few_us"] = round(event_time_batch(torch, few_fn, n) * 1e3, 3)
                     extra["few_split"] = int(G.lib().hip_qmm_mmq_split_k(G.TYPE_IDS[qtype], Kx, M, T))
-                    if qtype != "Q4_K" and T > 8:
+                    if qtype not in ("Q4_K", "Q5_K") and T > 8:
                         if T == 9:
                             off = []
-                            for wt in ws:  # the same rows at a base 2 bytes past 16-byte alignment
+                            sh = 8 if qtype == "IQ4_XS" else 2
+                            for wt in ws:  # the same rows at a base sh bytes past 16-byte alignment
                                 buf = torch.zeros(wt.numel() + 16, dtype=torch.uint8, device=dev)
-                                off.append(buf[2:2 + wt.numel()].view(wt.shape))
+                                off.append(buf[sh:sh + wt.numel()].view(wt.shape))
                                 off[-1].copy_(wt)
                         tile_fn = lambda i: G.mmq(qtype, off[i % len(off)], Kx, qs, ds, out=out,  # noqa: E731
                                                   workspace=mmq_ws)
@@ -403,7 +407,7 @@ def run_suite(name, torch, G, dev, reps):
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2),
                       "int8_frac": round(ops / ms / 1e9 / INT8_PEAK_TOPS, 4), **extra})
             del ws
-            if name == "few" and qtype != "Q4_K":
+            if name == "few" and qtype not in ("Q4_K", "Q5_K"):
                 del off
             torch.cuda.empty_cache()
     elif name == "moe":

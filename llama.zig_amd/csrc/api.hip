@@ -18,6 +18,8 @@ extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows,
 
 // mmq.hip: whether the few-column kernel takes this shape (given aligned operands)
 bool few_cols_type(int type, int64_t K, int64_t ncols);
+// mmq_few.hip: whether it takes these weight rows
+bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
 
 // gemv.hip: 2-4 f32 columns through the quantize-in-GEMV kernel, or
 // hipErrorNotSupported for shapes it does not take.
@@ -31,26 +33,63 @@ size_t q8_1_bytes(int64_t K, int64_t ncols) {
 }
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
-// Whether 2-8 columns go to the MMQ dispatch (the few-column Q4_K kernel,
+// Whether 2-8 columns go to the MMQ dispatch (the few-column kernel,
 // mmq_few.hip) rather than the GEMV.  The GEMV's time grows with the columns
 // (each wave re-reads every column's activation slice), the few-column
-// kernel's hardly does; crossovers measured with device timing on Q4_K: from
-// 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.1 against 15.9 us)
-// and on >= 16384 rows (28672x4096: 22.1 against 21.1 us), from 6 at K >= 8192
-// on >= 2048 rows, from 8 on >= 6144 rows (14336x4096: 18.9 against 16.3 us;
-// 6 columns tie); the GEMV stays ahead on smaller matrices (4096x4096 at 8
-// columns: 9.2 against 10.3 us).
+// kernel's hardly does.  Crossovers measured on the op (hip_qmm_mul_mat, us,
+// GEMV against few-column) over 1024x14336, 2048x14336, 4096x4096,
+// 4096x14336, 8192x8192 and 14336x4096 at 3-8 columns:
+//   - Q4_K: from 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.1
+//     against 15.9) and on >= 16384 rows, from 6 at K >= 8192 on >= 2048
+//     rows, from 7 on >= 6144 rows (14336x4096: 17.4 against 16.3); the GEMV
+//     stays ahead on smaller matrices (4096x4096 at 8 columns: 9.7 against 11.2);
+//   - Q5_K / Q8_0: from 4 columns on matrices of >= 24M weights (Q5_K
+//     14336x4096 at 6: 26.4 against 17.5; Q8_0 at 4: 21.2 against 19.6), 8
+//     columns from 12M (Q5_K 4096x4096 12.0 against 11.4; Q8_0 only on rows
+//     of K >= 8192, 4096x4096 keeps the GEMV: 11.7 against 12.3);
+//   - Q4_0 / IQ4_XS: from 6 columns on >= 24M weights (Q4_0 14336x4096 at 6:
+//     21.3 against 19.8), from 5 on rows of K >= 8192 at <= 2048 or >= 8192
+//     rows (Q4_0 8192x8192 at 5: 21.5 against 18.9), 8 columns from 12M on
+//     rows of K >= 8192;
+//   - Q6_K: 7 columns from 12M weights (14336x4096: 45.1 against 34.6), 6 on
+//     >= 24M weights with K >= 8192 (4096x14336: 36.3 against 26.2); at 8
+//     columns its MFMA GEMV (more than 2048 rows) is as fast, so only rows of
+//     K >= 8192 on <= 2048 rows take the few-column kernel there (2048x14336:
+//     30.4 against 21.5).
 bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    if (type != TYPE_Q4_K || K % 256 != 0 || ncols > 8) return false;
-    if (K >= 8192 && nrows >= 4096) return ncols >= 5;
-    if (nrows >= 16384) return ncols >= 5;
-    if (K >= 8192 && nrows >= 2048) return ncols >= 6;
-    if (nrows >= 6144) return ncols >= 8;
-    return false;
+    if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, ncols)) return false;
+    const int64_t elems = nrows * K;
+    const bool large = elems >= ((int64_t)24 << 20), mid = elems >= ((int64_t)12 << 20), long_rows = K >= 8192;
+    switch (type) {
+    case TYPE_Q4_K:
+        if (long_rows && nrows >= 4096) return ncols >= 5;
+        if (nrows >= 16384) return ncols >= 5;
+        if (long_rows && nrows >= 2048) return ncols >= 6;
+        if (nrows >= 6144) return ncols >= 7;
+        return false;
+    case TYPE_Q5_K: return (large && ncols >= 4) || (mid && ncols == 8);
+    case TYPE_Q8_0: return (large && ncols >= 4) || (mid && long_rows && ncols == 8);
+    case TYPE_Q4_0:
+    case TYPE_IQ4_XS:
+        return (large && (ncols >= 6 || (long_rows && (nrows <= 2048 || nrows >= 8192) && ncols >= 5))) ||
+               (mid && long_rows && ncols == 8);
+    case TYPE_Q6_K:
+        return (mid && ncols == 7) || (large && long_rows && ncols == 6) ||
+               (mid && long_rows && nrows <= 2048 && ncols == 8);
+    default: return false;
+    }
 }
 
+// Shape-only (the workspace sizing): the MMQ dispatch takes these columns.
 bool use_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return K % 256 == 0 && (ncols > 8 || few_cols_wins(type, K, nrows, ncols));
+}
+
+// At the call: up to 8 columns go to the few-column kernel only where it takes
+// the rows (16-byte-aligned rows for the 2- and 8-byte-aligned types); the
+// MMQ tile would be slower than the GEMV there.
+bool use_mmq_rows(int type, int64_t K, int64_t nrows, int64_t ncols, const void *w, int64_t row_stride) {
+    return use_mmq(type, K, nrows, ncols) && (ncols > 8 || mmq_few_takes(type, K, w, row_stride));
 }
 
 // Whether gate/up/GLU over ncols columns runs the fused MMQ: where each
@@ -94,7 +133,7 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     // K shares 14.9 vs 15.6 us).
     if (ncols == 1 && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
         return hip_qmm_mul_mat_vec_f32(type, w, K, nrows, row_stride, x, dst, stream);
-    if (ncols >= 2 && ncols <= 4 && !use_mmq(type, K, nrows, ncols)) {
+    if (ncols >= 2 && ncols <= 4 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride)) {
         const int e = qmm_mul_mat_fx_cols(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride,
                                           stream);
         if (e != (int)hipErrorNotSupported) return e;
@@ -103,7 +142,7 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     int8_t *qs = (int8_t *)workspace;
     void *ds = (uint8_t *)workspace + ncols * Kp;
     if (int e = hip_qmm_quantize_q8_1_planar(x, K, ncols, x_col_stride, qs, ds, stream)) return e;
-    if (ncols <= 8 && !use_mmq(type, K, nrows, ncols))
+    if (ncols <= 8 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride))
         return hip_qmm_mul_mat_vec(type, w, K, nrows, row_stride, qs, ds, ncols, dst, dst_col_stride, stream);
     if (K % 256 == 0) {
         const size_t off = align256(q8_1_bytes(K, ncols));

@@ -159,7 +159,7 @@ def _one_column_op_splits_k(tname, nrows, K):
                                                  ("Q6_K", 1024, 4096, 2), ("IQ4_XS", 777, 2048, 3),
                                                  ("Q8_0", 4100, 4096, 4), ("Q4_0", 333, 96, 3),
                                                  ("Q8_0", 5000, 1024, 3), ("Q4_0", 4097, 4096, 2),
-                                                 ("IQ4_XS", 6000, 4096, 2), ("Q8_0", 9000, 4096, 4),
+                                                 ("IQ4_XS", 6000, 4096, 2), ("Q8_0", 9000, 4096, 3),
                                                  ("Q4_K", 8200, 2048, 2), ("Q4_0", 8195, 1024, 4),
                                                  ("Q8_0", 1024, 4096, 2), ("Q4_0", 500, 4096, 3),
                                                  ("Q8_0", 2048, 4096, 4)])

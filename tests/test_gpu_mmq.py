@@ -79,27 +79,49 @@ def test_mmq_split_k(tname, nrows, K, ncols):
     assert max_err_scaled(u, ideal) < F64_TOL, max_err_scaled(u, ideal)
 
 
-@pytest.mark.parametrize("nrows,K,ncols", [(4096, 8192, 5), (2048, 8192, 6), (6144, 4096, 8), (6150, 4096, 8)])
-def test_op_few_columns(nrows, K, ncols):
-    """The op sends 5-8 columns of large Q4_K matrices to the few-column GEMM
-    instead of the GEMV: same bits as the kernel-level MMQ on the quantized
-    columns, within the f64 and CPU gates, and within rounding of the GEMV."""
+@pytest.mark.parametrize("tname,nrows,K,ncols", [("Q4_K", 4096, 8192, 5), ("Q4_K", 2048, 8192, 6),
+                                                 ("Q4_K", 6144, 4096, 8), ("Q4_K", 6150, 4096, 7),
+                                                 ("Q5_K", 2048, 14336, 4), ("Q5_K", 4096, 4096, 8),
+                                                 ("Q8_0", 4096, 8192, 4), ("Q8_0", 1024, 14336, 8),
+                                                 ("Q4_0", 2048, 14336, 5), ("Q4_0", 6144, 4096, 6),
+                                                 ("IQ4_XS", 2048, 14336, 5), ("IQ4_XS", 1024, 14336, 8),
+                                                 ("Q6_K", 1024, 14336, 7), ("Q6_K", 2048, 14336, 8),
+                                                 ("Q6_K", 2048, 14336, 6)])
+def test_op_few_columns(tname, nrows, K, ncols):
+    """The op sends 4-8 columns of large matrices to the few-column GEMM
+    instead of the GEMV (per type, where it measured faster): same bits as
+    the kernel-level MMQ on the quantized columns, within the f64 and CPU
+    gates, and within rounding of the GEMV."""
     import ggml_hip as G
-    t = O.TYPE_Q4_K
+    t = TYPES[tname]
     wq = weights_q(t, nrows, K)
     x = acts(ncols, K)
     w_d = torch.from_numpy(np.array(wq)).cuda()
     x_d = torch.from_numpy(np.array(x)).cuda()
-    got = G.mul_mat("Q4_K", w_d, x_d).cpu().numpy()
+    got = G.mul_mat(tname, w_d, x_d).cpu().numpy()
     qs, ds = G.quantize_q8_1_planar(x_d)
-    np.testing.assert_array_equal(got, G.mmq("Q4_K", w_d, K, qs, ds).cpu().numpy())
-    gemv = G.mul_mat_vec("Q4_K", w_d, K, qs, ds).cpu().numpy()
+    np.testing.assert_array_equal(got, G.mmq(tname, w_d, K, qs, ds).cpu().numpy())
+    gemv = G.mul_mat_vec(tname, w_d, K, qs, ds).cpu().numpy()
     assert max_err_scaled(got, gemv) < 1e-6
     y = G.quantize_q8_1(x_d, K).cpu().numpy()
     ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
     assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
     cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
     assert nmse(got, cpu) < NMSE_GATE
+
+
+def test_op_few_columns_unaligned_rows_keep_the_gemv():
+    """Rows the few-column kernel does not take (2-byte-aligned Q8_0 rows)
+    keep the GEMV at 4-8 columns, where the 128-row tile would be slower:
+    the op equals hip_qmm_mul_mat_vec on the same columns bit for bit."""
+    import ggml_hip as G
+    nrows, K, ncols = 4096, 8192, 6
+    wq = weights_q(O.TYPE_Q8_0, nrows, K)
+    w_d = _offset_copy(torch.from_numpy(np.array(wq)).cuda())
+    x_d = torch.from_numpy(np.array(acts(ncols, K))).cuda()
+    got = G.mul_mat("Q8_0", w_d, x_d).cpu().numpy()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    np.testing.assert_array_equal(got, G.mul_mat_vec("Q8_0", w_d, K, qs, ds).cpu().numpy())
 
 
 def _offset_copy(w_d, off=2):
