@@ -178,6 +178,18 @@ def reference_inputs(T):
     return wq, x, xt
 
 
+CPU_ROTATE_BYTES = 1 << 30      # weight copies the CPU legs cycle through: beyond any host L3
+
+
+def cpu_copies(wq):
+    """Copies of a host weight array totalling about CPU_ROTATE_BYTES (at least
+    one, at most 64), so that each timed CPU run streams its weights from DRAM
+    as a model larger than the host's caches does."""
+    import numpy as np
+    n = max(1, min(64, CPU_ROTATE_BYTES // max(1, wq.nbytes)))
+    return [wq] + [np.array(wq, copy=True) for _ in range(n - 1)]
+
+
 def time_cpu(fn, budget_s, min_runs=5):
     fn()  # warm-up
     times, t0 = [], time.perf_counter()
@@ -209,12 +221,18 @@ def cpu_gemv_leg(wq, x, gpu_out):
     nth = O.gen_threads()
     impl = O.IMPL_AVX2 if O.has_avx2() else O.IMPL_GENERIC
     out = {}
-    med, runs = time_cpu(lambda: out.__setitem__("y", O.mul_mat(O.TYPE_Q4_K, wq, M, K, x, nth=nth, impl=impl)),
-                         CPU_SAMPLE_S, 20)
+    wqs, it = cpu_copies(wq), [0]
+
+    def run():
+        out["y"] = O.mul_mat(O.TYPE_Q4_K, wqs[it[0] % len(wqs)], M, K, x, nth=nth, impl=impl)
+        it[0] += 1
+
+    med, runs = time_cpu(run, CPU_SAMPLE_S, 20)
     bytes_alg = M * q4k_row_bytes(K) + K * 4 + M * 4
     base = {"value": round(bytes_alg / med / 1e9, 3), "unit": "GB/s", "cores": nth, "kind": "port",
-            "sample": f"Q4_K {M}x{K} b=1 mul_mat (seed-42 weights), {'AVX2' if impl == O.IMPL_AVX2 else 'generic'} "
-                      f"vec_dot path, median of {runs} runs ({med * 1e3:.3f} ms each)",
+            "sample": f"Q4_K {M}x{K} b=1 mul_mat (seed-42 weights, {len(wqs)} host copies cycled), "
+                      f"{'AVX2' if impl == O.IMPL_AVX2 else 'generic'} vec_dot path, persistent threads, "
+                      f"median of {runs} runs ({med * 1e3:.3f} ms each)",
             **host_info(nth)}
     return base, parity(gpu_out, out["y"])
 
@@ -227,15 +245,19 @@ def cpu_mmq_leg(wq, xt, gpu_out):
     nth = O.gen_threads()
     out = {}
 
+    wqs, it = cpu_copies(wq), [0]
+
     def run():
-        y = O.mul_mat_tiled(O.TYPE_Q4_K, wq, M, K, xt, nth=nth)
-        out["y"] = y if y is not None else O.mul_mat(O.TYPE_Q4_K, wq, M, K, xt, nth=nth)
+        w_i = wqs[it[0] % len(wqs)]
+        it[0] += 1
+        y = O.mul_mat_tiled(O.TYPE_Q4_K, w_i, M, K, xt, nth=nth)
+        out["y"] = y if y is not None else O.mul_mat(O.TYPE_Q4_K, w_i, M, K, xt, nth=nth)
 
     med, runs = time_cpu(run, CPU_SAMPLE_S, 3)
     tiled = O.has_avx2()
     ops = 2.0 * M * K * T_MMQ
     base = {"value": round(ops / med / 1e12, 4), "unit": "TOP/s", "cores": nth, "kind": "port",
-            "sample": f"Q4_K {M}x{K} x T={T_MMQ} mul_mat (seed-42 weights), "
+            "sample": f"Q4_K {M}x{K} x T={T_MMQ} mul_mat (seed-42 weights, {len(wqs)} host copies cycled), "
                       f"{'x86 tiled GEMM (AVX2 arm)' if tiled else 'generic vec_dot path'}, "
                       f"median of {runs} runs ({med * 1e3:.1f} ms each)",
             **host_info(nth)}
@@ -320,12 +342,51 @@ def measure_traffic():
                  "calibration": "64 MiB device copy, same counters, same pass"}
 
 
-def run_suite(name, torch, G, dev, reps):
+CPU_SUITE_S = 0.3              # CPU work per suite case
+CPU_SUITE_MACS = 2e10          # cases above this many MACs time a row sample on the CPU
+
+
+def cpu_suite_case(qtype, w_dev, M, Kx, x_dev):
+    """The reference CPU path for one suite case, through the route ggml's CPU
+    mul_mat takes on an x86 AVX2 host (the tiled GEMM for the tiled K-quants
+    from 8 columns, tinyBLAS for Q8_0 / Q4_0 from 2, else the AVX2 vec_dot;
+    oracle_lib.mul_mat_x86), on this host's threads (at most 16).  The whole
+    case where it has at most CPU_SUITE_MACS multiply-adds; above that a sample
+    of the first rows (a multiple of 256, at least 4096) against all the
+    case's columns, its time scaled by M / rows (each output row is
+    independent work)."""
+    O = _oracle()
+    tid = {"Q4_K": O.TYPE_Q4_K, "Q6_K": O.TYPE_Q6_K, "Q8_0": O.TYPE_Q8_0, "Q5_K": O.TYPE_Q5_K,
+           "Q4_0": O.TYPE_Q4_0, "IQ4_XS": O.TYPE_IQ4_XS}[qtype]
+    T = x_dev.shape[0]
+    macs = float(M) * Kx * T
+    rows = M if macs <= CPU_SUITE_MACS else min(M, max(4096, int(M * CPU_SUITE_MACS / macs) // 256 * 256))
+    wq = w_dev[:rows].cpu().numpy()
+    x = x_dev.cpu().numpy().reshape(-1, Kx)
+    nth = O.gen_threads()
+    route = ("tiled GEMM" if T >= 8 and qtype in ("Q4_K", "Q5_K", "Q6_K", "IQ4_XS") and O.has_avx2() else
+             "tinyBLAS" if T >= 2 and qtype in ("Q8_0", "Q4_0") and O.has_avx2() else
+             "AVX2 vec_dot" if O.has_avx2() else "generic vec_dot")
+    wqs, it = cpu_copies(wq), [0]
+
+    def run():
+        O.mul_mat_x86(tid, wqs[it[0] % len(wqs)], rows, Kx, x, nth=nth)
+        it[0] += 1
+
+    med, runs = time_cpu(run, CPU_SUITE_S, 2)
+    return {"cpu_us": round(med * 1e6 * M / rows, 1), "cpu_rows_timed": rows, "cpu_runs": runs,
+            "cpu_route": route, "cpu_threads": nth, "cpu_weight_copies": len(wqs)}
+
+
+def run_suite(name, torch, G, dev, reps, cpu=True):
     """Kernel-level measurements over the configs of BASELINE.json, one JSON
     line per case (device time from a HIP graph of launches between events,
-    weights rotated over > 2 x the Infinity Cache)."""
+    weights rotated over > 2 x the Infinity Cache), with the reference CPU
+    path's time for the same case beside it (cpu_us, see cpu_suite_case)."""
     gen = torch.Generator().manual_seed(42)
     xg = torch.Generator().manual_seed(43)
+    if cpu and name not in ("floor",):
+        print(json.dumps({"suite": name, "cpu_host": host_info(_oracle().gen_threads())}), flush=True)
 
     def copies(qtype, nrows, k):
         wb = nrows * row_bytes(qtype, k)
@@ -402,6 +463,9 @@ def run_suite(name, torch, G, dev, reps):
                 ms_op = event_time_batch(torch, op_fn, n)
                 alg = wb + Kx * 4 * T + M * 4 * T
                 ops = 2.0 * M * Kx * T
+                if cpu:
+                    extra.update(cpu_suite_case(qtype, ws[0], M, Kx, x))
+                    extra["op_speedup_vs_cpu"] = round(extra["cpu_us"] / (ms_op * 1e3), 1)
                 emit({"suite": name, "kernel": kern, "type": qtype, "shape": f"{M}x{Kx}", "label": label, "T": T,
                       "us": round(ms * 1e3, 3), "op_us": round(ms_op * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
                       "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2),
@@ -426,10 +490,29 @@ def run_suite(name, torch, G, dev, reps):
             ms = event_time_batch(torch, fn, n * reps)
             alg = wb + n_tokens * ne11 * Kx * 4 + n_tokens * k * M * 4
             ops = 2.0 * M * Kx * n_tokens * k
+            extra = {}
+            if cpu:
+                # the reference CPU mul_mat_id (per-slot vec_dot rows over the
+                # routed experts, AVX2 where the host has it) on the whole case
+                O = _oracle()
+                nth = O.gen_threads()
+                wqs = cpu_copies(ws[0].cpu().numpy().reshape(n_as * M, -1))
+                xh, idh = x.cpu().numpy(), ids.cpu().numpy()
+                impl = O.IMPL_AVX2 if O.has_avx2() else O.IMPL_GENERIC
+                it = [0]
+
+                def run_id():
+                    O.mul_mat_id(O.TYPE_Q4_K, wqs[it[0] % len(wqs)], n_as, M, Kx, xh, idh, nth=nth, impl=impl)
+                    it[0] += 1
+
+                med, runs = time_cpu(run_id, CPU_SUITE_S, 2)
+                extra = {"cpu_us": round(med * 1e6, 1), "cpu_runs": runs, "cpu_threads": nth,
+                         "cpu_route": "mul_mat_id, " + ("AVX2" if impl == O.IMPL_AVX2 else "generic") + " vec_dot",
+                         "speedup_vs_cpu": round(med * 1e6 / (ms * 1e3), 1)}
             emit({"suite": name, "kernel": "mul_mat_id (quantize + group + grouped MMQ)", "type": "Q4_K",
                   "shape": f"{n_as}x{M}x{Kx}", "label": label, "tokens": n_tokens, "top_k": k,
                   "us": round(ms * 1e3, 3), "GB/s": round(alg / ms / 1e6, 1),
-                  "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2)})
+                  "hbm_frac": round(alg / ms / 1e6 / HBM_PEAK_GBS, 4), "TOPS": round(ops / ms / 1e9, 2), **extra})
             # decode: one token's 8 experts through the one-launch GEMV over
             # (token, slot) pairs; bytes = the 8 selected experts' weights
             x1 = torch.randn((1, ne11, Kx), generator=xg, dtype=torch.float32).to(dev)
@@ -629,7 +712,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg (random weights, no parity)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs (headline: random weights, no parity; suites: no cpu_us)")
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
@@ -653,7 +736,7 @@ def main():
     torch.cuda.set_device(dev)
     G.lib()
     if args.suite:
-        run_suite(args.suite, torch, G, dev, args.reps)
+        run_suite(args.suite, torch, G, dev, args.reps, cpu=not args.no_cpu)
         return
 
     w_bytes = M * q4k_row_bytes(K)

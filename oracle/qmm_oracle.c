@@ -29,6 +29,7 @@
 #include <math.h>
 #include <pthread.h>
 #include <stdatomic.h>
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -1709,12 +1710,89 @@ static void *mm_compute_worker(void *arg) {
     return NULL;
 }
 
+/* Thread k of a parallel region runs fn(ts + k * stride); the caller is
+ * thread 0.  The other threads come from a persistent pool, as ggml's CPU
+ * backend keeps its threadpool alive across ops, so a call costs a wake-up, not
+ * thread creation: this matters only for timing (the CPU baseline), not for
+ * the results, which depend on the work split alone.  Workers spin briefly on
+ * the job counter before sleeping on a condition variable; callers are
+ * serialized. */
+typedef struct {
+    pthread_mutex_t mu;
+    pthread_cond_t start, done;
+    atomic_long gen;   /* job number, bumped (under mu) when a job is posted */
+    atomic_int pending; /* pool threads still running the current job */
+    int nworkers;      /* pool threads created so far (thread indices 1..nworkers) */
+    int active;        /* threads of the current job (indices < active run it) */
+    void *(*fn)(void *);
+    char *ts;
+    size_t stride;
+} orc_pool;
+static orc_pool pool = {.mu = PTHREAD_MUTEX_INITIALIZER, .start = PTHREAD_COND_INITIALIZER,
+                        .done = PTHREAD_COND_INITIALIZER};
+static pthread_mutex_t pool_call = PTHREAD_MUTEX_INITIALIZER;
+#define ORC_POOL_MAX 256
+/* the job number current when pool thread k was created (under pool.mu):
+ * the thread waits for the next one, whenever it gets to run */
+static long pool_born[ORC_POOL_MAX + 1];
+
+static void *pool_worker(void *arg) {
+    const int idx = (int)(intptr_t)arg;
+    long seen = pool_born[idx];
+    for (;;) {
+        for (long spin = 0; spin < (1L << 16) && atomic_load_explicit(&pool.gen, memory_order_acquire) == seen; ++spin) {
+#if defined(__x86_64__)
+            _mm_pause();
+#endif
+        }
+        pthread_mutex_lock(&pool.mu);
+        while (atomic_load_explicit(&pool.gen, memory_order_relaxed) == seen) pthread_cond_wait(&pool.start, &pool.mu);
+        seen = atomic_load_explicit(&pool.gen, memory_order_relaxed);
+        const int run = idx < pool.active;
+        void *(*fn)(void *) = pool.fn;
+        char *arg_k = pool.ts + (size_t)idx * pool.stride;
+        pthread_mutex_unlock(&pool.mu);
+        if (!run) continue;
+        fn(arg_k);
+        if (atomic_fetch_sub_explicit(&pool.pending, 1, memory_order_acq_rel) == 1) {
+            pthread_mutex_lock(&pool.mu);
+            pthread_cond_signal(&pool.done);
+            pthread_mutex_unlock(&pool.mu);
+        }
+    }
+    return NULL;
+}
+
 static void run_threads(int nth, void *ts, size_t stride, void *(*fn)(void *)) {
-    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)nth);
-    for (int i = 1; i < nth; ++i) pthread_create(&th[i], NULL, fn, (char *)ts + (size_t)i * stride);
+    if (nth <= 1) {
+        fn(ts);
+        return;
+    }
+    pthread_mutex_lock(&pool_call);
+    pthread_mutex_lock(&pool.mu);
+    while (pool.nworkers < nth - 1 && pool.nworkers < ORC_POOL_MAX) {
+        pthread_t th;
+        pool_born[pool.nworkers + 1] = atomic_load_explicit(&pool.gen, memory_order_relaxed);
+        if (pthread_create(&th, NULL, pool_worker, (void *)(intptr_t)(pool.nworkers + 1)) != 0) break;
+        pthread_detach(th);
+        ++pool.nworkers;
+    }
+    const int helpers = pool.nworkers < nth - 1 ? pool.nworkers : nth - 1;
+    pool.fn = fn;
+    pool.ts = (char *)ts;
+    pool.stride = stride;
+    pool.active = helpers + 1;
+    atomic_store_explicit(&pool.pending, helpers, memory_order_relaxed);
+    atomic_fetch_add_explicit(&pool.gen, 1, memory_order_release);
+    pthread_cond_broadcast(&pool.start);
+    pthread_mutex_unlock(&pool.mu);
     fn(ts);
-    for (int i = 1; i < nth; ++i) pthread_join(th[i], NULL);
-    free(th);
+    /* threads the pool could not provide: the caller runs their shares */
+    for (int k = helpers + 1; k < nth; ++k) fn((char *)ts + (size_t)k * stride);
+    pthread_mutex_lock(&pool.mu);
+    while (atomic_load_explicit(&pool.pending, memory_order_acquire) > 0) pthread_cond_wait(&pool.done, &pool.mu);
+    pthread_mutex_unlock(&pool.mu);
+    pthread_mutex_unlock(&pool_call);
 }
 
 void orc_mul_mat(int type, int impl, const void *w, int64_t nrows, int64_t K, const float *x,
