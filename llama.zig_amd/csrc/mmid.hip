@@ -54,6 +54,42 @@ __device__ __forceinline__ int block_excl_scan(int a, int &total, int *buf) {
     return pre + ia - a;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP (row_shr 1, 2, 4, 8
+// inside rows of 16, then row_bcast:15 and row_bcast:31 carry the row totals
+// forward).  Every lane of the wave must be active.
+__device__ __forceinline__ int wave_incl_scan(int x) {
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);
+    return x;
+}
+
+// Exclusive prefix sum of one value per thread over the workgroup, with the
+// total, on DPP wave scans and one barrier.  `buf` is PREP_THREADS / 64 ints of
+// LDS that no other thread reads or writes until the caller's next barrier
+// (consecutive calls alternate two buffers).
+__device__ __forceinline__ int block_excl_scan_dpp(int a, int &total, int *buf) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int incl = wave_incl_scan(a);
+    if (lane == 63) buf[wave] = incl;
+    __syncthreads();
+    int pre = 0;
+    total = 0;
+#pragma unroll
+    for (int w = 0; w < PREP_THREADS / 64; ++w) {
+        const int v = buf[w];
+        if (w < wave) pre += v;
+        total += v;
+    }
+    return pre + incl - a;
+}
+
+// Most chunks of CHUNK pairs the register path of the grouping keeps.
+constexpr int FAST_CHUNKS = 4;
+
 // One launch that prepares a MUL_MAT_ID: workgroups [0, n_group) build the
 // expert grouping, the rest quantize the activation rows to planar Q8_1 (the
 // 8-values-per-lane form of quantize_q8_1.hip); the two parts are independent.
@@ -74,15 +110,25 @@ __global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
     int bn, int n_group, int32_t *__restrict__ col_src, int32_t *__restrict__ col_dst,
     int32_t *__restrict__ tiles, int32_t *__restrict__ n_tiles,
     float *__restrict__ dst, int64_t dst_row_stride, int64_t nrows, const float *__restrict__ x, int64_t K,
-    int64_t x_row_stride, int64_t Kp, int nq_per_row, int8_t *__restrict__ qs, uint32_t *__restrict__ ds) {
+    int64_t x_row_stride, int64_t Kp, int nq_per_row, int rows_per_wg, int64_t nrows_x, int8_t *__restrict__ qs,
+    uint32_t *__restrict__ ds) {
     const int tid = threadIdx.x;
     if ((int)blockIdx.x >= n_group) {
-        // quantize: workgroup (row, K slice of QUANT_VALS values); Kp is a
-        // multiple of 512, so a quad (one 32-block) is wholly inside or past Kp
+        // quantize: workgroup (row, K slice of QUANT_VALS values), or for rows
+        // shorter than QUANT_VALS, rows_per_wg whole rows; Kp is a multiple of
+        // 512, so a quad (one 32-block) is wholly inside one row and inside or
+        // past Kp
         const int b = (int)blockIdx.x - n_group;
-        const int64_t c = b / nq_per_row;
-        const int64_t k = (int64_t)(b - c * nq_per_row) * QUANT_VALS + tid * 8;
-        if (k >= Kp) return;
+        int64_t c, k;
+        if (rows_per_wg > 1) {
+            c = (int64_t)b * rows_per_wg + (tid * 8) / Kp;
+            k = (tid * 8) % Kp;
+            if (c >= nrows_x || (tid * 8) / Kp >= rows_per_wg) return;
+        } else {
+            c = b / nq_per_row;
+            k = (int64_t)(b - c * nq_per_row) * QUANT_VALS + tid * 8;
+            if (k >= Kp) return;
+        }
         float v[8];
         if (k < K) {  // K % 32 == 0
             const float4 a0 = *reinterpret_cast<const float4 *>(x + c * x_row_stride + k);
@@ -101,7 +147,7 @@ __global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
 
     __shared__ int count[MAX_EXPERTS];
     __shared__ int coff[MAX_EXPERTS], toff[MAX_EXPERTS];
-    __shared__ int sbuf[PREP_THREADS / 64];
+    __shared__ int sbuf[2][PREP_THREADS / 64];
     const int g = (int)blockIdx.x;
     // pair indices fit in 32 bits (checked by the host): 32-bit division
     const uint32_t npairs = (uint32_t)(n_tokens * n_ids), nid = (uint32_t)n_ids;
@@ -116,6 +162,97 @@ __global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
         }
         return e >= 0 && e < n_as ? e : -1;
     };
+
+    // Register path (up to FAST_CHUNKS chunks of pairs, at most PREP_THREADS
+    // experts; uniform): the ids are read once, IDS_PER_THREAD consecutive pairs
+    // per thread and chunk, and counting, placement and the zero rows all work
+    // from registers; the column and tile offsets come from one scan of both
+    // counts packed in 16-bit fields (both totals stay below 2^16 here).  Same
+    // results as the general path below: positions depend on the ids alone.
+    if (npairs <= (uint32_t)(FAST_CHUNKS * CHUNK) && n_as <= PREP_THREADS) {
+        const int nch = (int)((npairs + CHUNK - 1) / CHUNK);
+        int ev[FAST_CHUNKS][IDS_PER_THREAD];
+#pragma unroll
+        for (int c = 0; c < FAST_CHUNKS; ++c) {
+            const uint32_t p0 = (uint32_t)c * CHUNK + (uint32_t)tid * IDS_PER_THREAD;
+            if (c < nch) {
+                if (dense_ids && p0 + IDS_PER_THREAD <= npairs && ((uintptr_t)(ids + p0) & 15) == 0) {
+#pragma unroll
+                    for (int q = 0; q < IDS_PER_THREAD / 4; ++q) {
+                        const int4 v = *reinterpret_cast<const int4 *>(ids + p0 + 4 * q);
+                        ev[c][4 * q] = v.x; ev[c][4 * q + 1] = v.y; ev[c][4 * q + 2] = v.z; ev[c][4 * q + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int k = 0; k < IDS_PER_THREAD; ++k) ev[c][k] = ev[c][k] >= 0 && ev[c][k] < n_as ? ev[c][k] : -1;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < IDS_PER_THREAD; ++k) {
+                        const uint32_t p = p0 + (uint32_t)k;
+                        ev[c][k] = p < npairs ? id_of(p) : -2;  // -2: past the end
+                    }
+                }
+            }
+        }
+        if (tid < n_as) count[tid] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < FAST_CHUNKS; ++c)
+            if (c < nch)
+#pragma unroll
+                for (int k = 0; k < IDS_PER_THREAD; ++k)
+                    if (ev[c][k] >= 0) atomicAdd(&count[ev[c][k]], 1);
+        __syncthreads();
+        const int ce_t = tid < n_as ? count[tid] : 0;
+        const int packed = ce_t | (((ce_t + bn - 1) / bn) << 16);
+        int tot;
+        const int pre = block_excl_scan_dpp(packed, tot, sbuf[0]);
+        if (tid < n_as) {
+            coff[tid] = pre & 0xFFFF;
+            toff[tid] = pre >> 16;
+        }
+        __syncthreads();
+        if (g == 0 && tid == 0) *n_tiles = tot >> 16;
+        for (int e = g; e < n_as; e += n_group) {
+            const int ce = count[e], c0 = coff[e], t0 = toff[e];
+            for (int i = tid; i * bn < ce; i += PREP_THREADS) {
+                const int lo = c0 + i * bn, hi = lo + bn < c0 + ce ? lo + bn : c0 + ce;
+                *reinterpret_cast<int4 *>(tiles + 4 * (t0 + i)) = make_int4(e, lo, hi, 0);
+            }
+            int pos = c0;
+#pragma unroll
+            for (int c = 0; c < FAST_CHUNKS; ++c) {
+                if (c >= nch) break;  // uniform
+                uint32_t mask = 0;
+#pragma unroll
+                for (int k = 0; k < IDS_PER_THREAD; ++k) mask |= (ev[c][k] == e ? 1u : 0u) << k;
+                int ctot;
+                int at = pos + block_excl_scan_dpp(__builtin_popcount(mask), ctot, sbuf[(c + 1) & 1]);
+                const uint32_t p0 = (uint32_t)c * CHUNK + (uint32_t)tid * IDS_PER_THREAD, n11 = (uint32_t)ne11;
+                while (mask) {
+                    const int k = __builtin_ctz(mask);
+                    mask &= mask - 1;
+                    const uint32_t p = p0 + k, t = p / nid, sl = p - t * nid;
+                    col_src[at] = (int32_t)(t * n11 + (n11 == 1 ? 0u : sl));
+                    col_dst[at] = (int32_t)p;
+                    ++at;
+                }
+                pos += ctot;
+            }
+        }
+        // zero rows for invalid ids: thread slot (c, tid) belongs to grouping
+        // workgroup (c * PREP_THREADS + tid) % n_group
+#pragma unroll
+        for (int c = 0; c < FAST_CHUNKS; ++c) {
+            if (c >= nch || (c * PREP_THREADS + tid) % n_group != g) continue;
+#pragma unroll
+            for (int k = 0; k < IDS_PER_THREAD; ++k) {
+                if (ev[c][k] != -1) continue;
+                float *row = dst + (int64_t)((uint32_t)c * CHUNK + (uint32_t)tid * IDS_PER_THREAD + k) * dst_row_stride;
+                for (int64_t r = 0; r < nrows; ++r) row[r] = 0.0f;
+            }
+        }
+        return;
+    }
     for (int e = tid; e < n_as; e += PREP_THREADS) count[e] = 0;
     __syncthreads();
     // ids of pair p, or -1 past the end; the loads are unconditional (index
@@ -146,8 +283,8 @@ __global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
         }
     }
     int c_tot, t_tot;
-    int c_pre = block_excl_scan(c_run, c_tot, sbuf);
-    int t_pre = block_excl_scan(t_run, t_tot, sbuf);
+    int c_pre = block_excl_scan(c_run, c_tot, sbuf[0]);
+    int t_pre = block_excl_scan(t_run, t_tot, sbuf[0]);
 #pragma unroll
     for (int i = 0; i < EPT; ++i) {
         const int e = tid * EPT + i;
@@ -178,7 +315,7 @@ __global__ __launch_bounds__(PREP_THREADS) void mmid_prepare(
 #pragma unroll
             for (int k = 0; k < IDS_PER_THREAD; ++k) mask |= (ev[k] == e ? 1u : 0u) << k;
             int tot;
-            int at = pos + block_excl_scan(__builtin_popcount(mask), tot, sbuf);
+            int at = pos + block_excl_scan(__builtin_popcount(mask), tot, sbuf[0]);
             const uint32_t n11 = (uint32_t)ne11;  // 1 or n_ids
             while (mask) {
                 const int k = __builtin_ctz(mask);
@@ -279,16 +416,20 @@ int mul_mat_id(int type, const void *w, const void *w_gate, int64_t K, int64_t n
     if ((uintptr_t)x % 16 == 0 && x_row_stride % 4 == 0 && K % QK8 == 0) {
         // one launch: grouping and quantization
         const int nq_per_row = (int)((L.Kp + QUANT_VALS - 1) / QUANT_VALS);
-        const int64_t nwg = n_group + L.nrows_x * nq_per_row;
+        // short rows (Kp < QUANT_VALS): whole rows per workgroup
+        const int rows_per_wg = L.Kp < QUANT_VALS ? (int)(QUANT_VALS / L.Kp) : 1;
+        const int64_t nq = rows_per_wg > 1 ? (L.nrows_x + rows_per_wg - 1) / rows_per_wg : L.nrows_x * nq_per_row;
+        const int64_t nwg = n_group + nq;
         if (nwg > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
         hipLaunchKernelGGL(mmid_prepare, dim3((unsigned)nwg), dim3(PREP_THREADS), 0, s, ids, ids_stride, n_tokens,
                            n_ids, (int)n_as, ne11, bn, n_group, col_src, col_dst, tiles, ntiles, dst,
-                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, nq_per_row, qs, (uint32_t *)ds);
+                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, nq_per_row, rows_per_wg, L.nrows_x, qs,
+                           (uint32_t *)ds);
     } else {
         if (int e = hip_qmm_quantize_q8_1_planar(x, K, L.nrows_x, x_row_stride, qs, ds, stream)) return e;
         hipLaunchKernelGGL(mmid_prepare, dim3((unsigned)n_group), dim3(PREP_THREADS), 0, s, ids, ids_stride, n_tokens,
                            n_ids, (int)n_as, ne11, bn, n_group, col_src, col_dst, tiles, ntiles, dst,
-                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, 1, qs, (uint32_t *)ds);
+                           dst_row_stride, nrows, x, K, x_row_stride, L.Kp, 1, 1, L.nrows_x, qs, (uint32_t *)ds);
     }
     if (int e = (int)hipGetLastError()) return e;
     if (w_gate)
