@@ -202,3 +202,52 @@ def test_mul_mat_id_grouping_chunks_expert_loops_and_unaligned_activations():
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert rc == 0
     np.testing.assert_array_equal(out.cpu().numpy(), got)
+
+
+# The grouping kernel has two paths: up to 4 chunks of 4096 (token, slot) pairs
+# and 256 experts it reads the ids once into registers (16 consecutive pairs
+# per thread, 16-byte loads when the ids are dense and aligned, single loads
+# otherwise); beyond either limit it re-reads them chunk by chunk.  Both must
+# give every row its expert's product and -1 ids zero rows.
+@pytest.mark.parametrize("n_as,n_tokens,n_ids,ids_layout", [
+    (32, 1500, 4, "dense"),        # registers, 2 chunks
+    (64, 2000, 8, "strided"),      # registers, 4 chunks, ids rows padded and misaligned
+    (16, 2100, 8, "dense"),        # general path: 16800 pairs
+    (300, 40, 4, "dense"),         # general path: more than 256 experts
+])
+def test_mul_mat_id_grouping_paths(n_as, n_tokens, n_ids, ids_layout):
+    import ctypes
+    import ggml_hip as G
+    nrows, K = 64, 256
+    t = O.TYPE_Q4_K
+    rng = np.random.default_rng(n_as * 1000 + n_tokens)
+    ids = rng.integers(-1, n_as, size=(n_tokens, n_ids)).astype(np.int32)
+    x = np.array(acts(n_tokens, K)).reshape(n_tokens, 1, K)
+    wq = _experts(t, n_as, nrows, K)
+    w_d, x_d = torch.from_numpy(wq).cuda(), torch.from_numpy(x).cuda()
+    if ids_layout == "strided":
+        stride = n_ids + 3
+        buf = torch.full((n_tokens * stride + 1,), n_as - 1, dtype=torch.int32, device="cuda")
+        view = buf[1:1 + n_tokens * stride].view(n_tokens, stride)  # 4 bytes past 16-byte alignment
+        view[:, :n_ids] = torch.from_numpy(ids).cuda()
+        ids_ptr, ids_stride = view.data_ptr(), stride
+    else:
+        ids_d = torch.from_numpy(ids).cuda()
+        ids_ptr, ids_stride = ids_d.data_ptr(), n_ids
+    L = G.lib()
+    need = int(L.hip_qmm_mul_mat_id_workspace_size(t, K, n_as, 1, n_tokens, n_ids))
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda")
+    out = torch.full((n_tokens, n_ids, nrows), float("nan"), device="cuda")
+    vp = ctypes.c_void_p
+    rc = L.hip_qmm_mul_mat_id(t, vp(w_d.data_ptr()), K, nrows, w_d.stride(1), w_d.stride(0), n_as,
+                              vp(x_d.data_ptr()), 1, n_tokens, K, vp(ids_ptr), n_ids, ids_stride,
+                              vp(out.data_ptr()), nrows, vp(ws.data_ptr()), ws.numel(),
+                              vp(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0, rc
+    got = out.cpu().numpy()
+    assert np.all(got[ids < 0] == 0.0)
+    cpu = O.mul_mat_id(t, wq, n_as, nrows, K, x, ids, nth=8)
+    assert nmse(got, cpu) < NMSE_GATE, nmse(got, cpu)
+    y = G.quantize_q8_1(torch.from_numpy(x.reshape(-1, K)).cuda(), K).cpu().numpy()
+    ideal = mul_mat_id_f64(t, wq, nrows, K, y, 1, ids)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
