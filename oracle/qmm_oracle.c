@@ -1763,11 +1763,25 @@ static void *pool_worker(void *arg) {
     return NULL;
 }
 
+/* A child forked from a process that has pool threads inherits none of them:
+ * it starts an empty pool (fresh locks, no threads). */
+static void pool_after_fork_child(void) {
+    pthread_mutex_init(&pool.mu, NULL);
+    pthread_cond_init(&pool.start, NULL);
+    pthread_cond_init(&pool.done, NULL);
+    pthread_mutex_init(&pool_call, NULL);
+    pool.nworkers = 0;
+    atomic_store_explicit(&pool.pending, 0, memory_order_relaxed);
+}
+static pthread_once_t pool_once = PTHREAD_ONCE_INIT;
+static void pool_register_fork_handler(void) { pthread_atfork(NULL, NULL, pool_after_fork_child); }
+
 static void run_threads(int nth, void *ts, size_t stride, void *(*fn)(void *)) {
     if (nth <= 1) {
         fn(ts);
         return;
     }
+    pthread_once(&pool_once, pool_register_fork_handler);
     pthread_mutex_lock(&pool_call);
     pthread_mutex_lock(&pool.mu);
     while (pool.nworkers < nth - 1 && pool.nworkers < ORC_POOL_MAX) {
