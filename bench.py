@@ -385,7 +385,7 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
     path's time for the same case beside it (cpu_us, see cpu_suite_case)."""
     gen = torch.Generator().manual_seed(42)
     xg = torch.Generator().manual_seed(43)
-    if cpu and name not in ("floor",):
+    if cpu and name not in ("floor", "overlap"):
         print(json.dumps({"suite": name, "cpu_host": host_info(_oracle().gen_threads())}), flush=True)
 
     def copies(qtype, nrows, k):
@@ -703,6 +703,20 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
                   "hbm_frac": round(wb / ms / 1e6 / HBM_PEAK_GBS, 4)})
         del ws
         torch.cuda.empty_cache()
+    elif name == "overlap":
+        # Whether MFMA and VALU work overlap on a SIMD (the MMQ ceiling rests on
+        # it), from hip_qmm_probe_mfma_valu: SIMD cycles per substep, in which
+        # each of the SIMD's two waves issues one v_mfma_f32_32x32x16_f16 and/or
+        # 16 fp32 FMAs (MFMAs alone, FMAs alone, both in every wave, both split
+        # across the waves), from HIP events around one launch of 512
+        # workgroups (2 waves per SIMD) at the 2.4 GHz shader clock.
+        iters, nblocks = 4000, 512
+        sink = torch.empty(2 * nblocks * 256, dtype=torch.float32, device=dev)
+        names = {1: "MFMAs only", 2: "FMAs only", 3: "both, in every wave", 4: "both, MFMA waves and FMA waves"}
+        for mode in (1, 2, 3, 4):
+            ms = event_time_batch(torch, lambda i: G.probe_mfma_valu(mode, iters, nblocks, sink=sink), 3)
+            emit({"suite": name, "mode": mode, "work": names[mode], "us": round(ms * 1e3, 3),
+                  "simd_cycles_per_substep": round(ms * 1e-3 * 2.4e9 / (iters * 4), 1)})
     else:
         raise SystemExit(f"unknown suite {name}")
 
@@ -716,7 +730,8 @@ def main():
     ap.add_argument("--no-mmq", action="store_true", help="skip the MMQ leg")
     ap.add_argument("--no-traffic", action="store_true", help="skip the rocprofv3 traffic passes")
     ap.add_argument("--traffic-probe", action="store_true", help=argparse.SUPPRESS)
-    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "prefill_ffn", "few", "floor"],
+    ap.add_argument("--suite", choices=["decode", "mmq", "crossquant", "moe", "ffn", "prefill_ffn", "few", "floor",
+                                        "overlap"],
                     help="instead of the headline line, measure every case of one BASELINE config")
     ap.add_argument("--reps", type=int, default=4, help="passes over the weight copies per suite case")
     args = ap.parse_args()

@@ -426,6 +426,14 @@ int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nrows, int64_
 size_t hip_qmm_probe_sink_words(size_t bytes);
 int hip_qmm_probe_stream_read(const void *src, size_t bytes, uint32_t *sink, void *stream);
 
+/* Measurement aid, no counterpart in the reference: whether MFMA and VALU
+ * work overlap on a SIMD.  mode 1: MFMAs only (4 independent chains of
+ * v_mfma_f32_32x32x16_f16 per wave and step); 2: 16 fp32 FMAs per chain step
+ * only; 3: both in every wave; 4: MFMAs in even waves, FMAs in odd waves.
+ * nblocks workgroups of 256 threads (two per CU); sink holds 2 * nblocks * 256
+ * floats: each thread's MFMA sums, then its FMA sums. */
+int hip_qmm_probe_mfma_valu(int mode, int iters, int nblocks, float *sink, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,3 +45,78 @@ extern "C" int hip_qmm_probe_stream_read(const void *src, size_t bytes, uint32_t
                        (const uint4 *)src, (int64_t)(bytes / 16), sink);
     return (int)hipGetLastError();
 }
+
+// Whether MFMA and VALU work overlap on a SIMD, the fact the MMQ's ceiling
+// rests on.  Each wave runs `iters` steps; per step it issues (mode 1) one
+// v_mfma_f32_32x32x16_f16 on each of 4 independent accumulator chains, (mode
+// 2) 16 fp32 FMAs on each of 4 steps' register sets, (mode 3) both, or (mode
+// 4) the MFMAs in even waves and the FMAs in odd waves.  256 threads, two
+// workgroups per CU.  sink[t] gets the thread's MFMA sums and sink[n + t] its
+// FMA sums (n = threads of the grid), so the work cannot be removed and each
+// mode's parts can be checked against the single-kind modes.
+namespace {
+
+typedef _Float16 pv8h __attribute__((ext_vector_type(8)));
+typedef float pv16f __attribute__((ext_vector_type(16)));
+
+template <int MODE>
+__global__ __launch_bounds__(256, 2) void mfma_valu_probe(float *__restrict__ sink, int iters, float m0) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    pv8h a, b;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        a[k] = (_Float16)(lane * 0.001f + k);
+        b[k] = (_Float16)(k * 0.01f);
+    }
+    pv16f c[4], acc[2];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) c[j][v] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = (float)(v + lane);
+    float m = m0 + lane * 1e-6f;
+    asm volatile("" : "+v"(m));
+    const bool do_mfma = MODE == 1 || MODE == 3 || (MODE == 4 && (wave & 1) == 0);
+    const bool do_fma = MODE == 2 || MODE == 3 || (MODE == 4 && (wave & 1) == 1);
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (do_mfma) c[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c[j], 0, 0, 0);
+            if (do_fma) {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) acc[j & 1][v] = __builtin_fmaf(acc[j & 1][v], m, 1.0f);
+                asm volatile("" : "+v"(acc[j & 1]));
+            }
+        }
+    }
+    float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s0 += c[j][v];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s1 += acc[j][v];
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    sink[t] = s0;
+    sink[(int64_t)gridDim.x * 256 + t] = s1;
+}
+
+}  // namespace
+
+extern "C" int hip_qmm_probe_mfma_valu(int mode, int iters, int nblocks, float *sink, void *stream) {
+    if (!sink || mode < 1 || mode > 4 || iters < 0 || nblocks < 1 || nblocks > 65536) return (int)hipErrorInvalidValue;
+    const dim3 g((unsigned)nblocks), t(256);
+    hipStream_t s = (hipStream_t)stream;
+    switch (mode) {
+    case 1: hipLaunchKernelGGL(mfma_valu_probe<1>, g, t, 0, s, sink, iters, 0.999f); break;
+    case 2: hipLaunchKernelGGL(mfma_valu_probe<2>, g, t, 0, s, sink, iters, 0.999f); break;
+    case 3: hipLaunchKernelGGL(mfma_valu_probe<3>, g, t, 0, s, sink, iters, 0.999f); break;
+    default: hipLaunchKernelGGL(mfma_valu_probe<4>, g, t, 0, s, sink, iters, 0.999f); break;
+    }
+    return (int)hipGetLastError();
+}

@@ -110,6 +110,8 @@ def lib():
         L.hip_qmm_probe_sink_words.argtypes = [ctypes.c_size_t]
         L.hip_qmm_probe_stream_read.restype = i32
         L.hip_qmm_probe_stream_read.argtypes = [vp, ctypes.c_size_t, vp, vp]
+        L.hip_qmm_probe_mfma_valu.restype = i32
+        L.hip_qmm_probe_mfma_valu.argtypes = [i32, i32, i32, vp, vp]
         _lib = L
     return _lib
 
@@ -478,6 +480,15 @@ def probe_stream_read(buf: torch.Tensor, sink=None):
     if sink is None:
         sink = torch.empty(max(words, 1), dtype=torch.int32, device=buf.device)
     _check(lib().hip_qmm_probe_stream_read(_ptr(buf), nbytes, _ptr(sink), _stream()), "hip_qmm_probe_stream_read")
+    return sink
+
+
+def probe_mfma_valu(mode: int, iters: int, nblocks: int = 512, sink=None):
+    """MFMA / VALU overlap probe (mode 1 MFMAs, 2 FMAs, 3 both per wave, 4 split by wave);
+    returns the sink: [MFMA sums of every thread, FMA sums of every thread]."""
+    if sink is None:
+        sink = torch.empty(2 * nblocks * 256, dtype=torch.float32, device="cuda")
+    _check(lib().hip_qmm_probe_mfma_valu(mode, iters, nblocks, _ptr(sink), _stream()), "hip_qmm_probe_mfma_valu")
     return sink
 
 
