@@ -1,0 +1,251 @@
+// mmq_q80_dma.hip -- the Q8_0 MMQ with direct global->LDS loads.
+//
+// Arithmetic as in mmq.hip: the 32-deep block dot on v_mfma_i32_32x32x32_i8
+// (exact), the per-(row, column, block) scale d_b * d8_b as an exact f16 outer
+// product (v_mfma_f32_32x32x8_f16, one live K slot), one convert + FMA per
+// output and block:
+//   out = sum_b (d_b * d8_b) * dot_b(qs, q8)
+// Q8_0 has no super-block, so there is no per-super-block term.
+//
+// Data path.  A K-step is 128 values: four 34-byte blocks, 136 bytes of each
+// row.  Q8_0 rows of K % 256 == 0 have a length of a multiple of 272 bytes,
+// so step s's bytes start at 136 s, 16-byte aligned for even s and 8 bytes
+// past a 16-byte boundary for odd s; the 144-byte 16-aligned window around
+// them (never past the row: the last step is odd and its window ends at the
+// row's end) goes straight from global memory into LDS with
+// global_load_lds_dwordx4, rows back to back at a 144-byte stride.  Operand
+// reads start 2 bytes into a block, so a lane reads the dwords around its 16
+// code bytes and funnel-shifts them (v_alignbyte_b32).  The columns' Q8_1
+// bytes (128 per column) and their four block headers come the same way;
+// chunk c of column n sits at slot c ^ ((n >> 1) & 7), so 16 consecutive
+// columns' reads of one chunk cover all banks.  Two buffers: the next step's
+// transfers run while the current step is contracted, one barrier per step.
+#include "../../include/ggml_hip_qmm.h"
+#include "qmm_device.h"
+
+using namespace qmm;
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void *lds_ptr;
+
+constexpr int BM = 128;
+constexpr int NTHREADS = 256;
+constexpr int KSTEP = 128;              // 4 blocks
+constexpr int WIN = 144;                // bytes of a row's step window in LDS
+constexpr int ABYTES = BM * WIN;        // 18432: 18 transfers of 1 KiB
+constexpr int STEP_BYTES = 4 * Q80_BYTES;  // 136
+
+__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_base, 16, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmem() {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
+}
+
+__device__ __forceinline__ void store_tile_column(float *o, int64_t r0, int64_t nrows, const v16f &a) {
+    if (((uintptr_t)(o + r0) & 15) == 0 && r0 + 27 < nrows) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<float4 *>(o + r0 + 8 * q) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
+    } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
+            if (r < nrows) o[r] = a[v];
+        }
+    }
+}
+
+// 16 bytes at LDS byte offset o (o % 2 == 0): the dwords around them,
+// funnel-shifted when o is not dword-aligned.
+__device__ __forceinline__ v4i lds16_a2(const uint8_t *base, int o) {
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(base + (o & ~3));
+    const uint32_t a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
+    if ((o & 3) == 0) return v4i{(int)a0, (int)a1, (int)a2, (int)a3};
+    const uint32_t a4 = p[4];
+    return v4i{(int)__builtin_amdgcn_alignbyte(a1, a0, 2), (int)__builtin_amdgcn_alignbyte(a2, a1, 2),
+               (int)__builtin_amdgcn_alignbyte(a3, a2, 2), (int)__builtin_amdgcn_alignbyte(a4, a3, 2)};
+}
+
+template <int BN>
+__global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
+    const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
+    const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
+    float *__restrict__ partial, int gx, int gy, int gz) {
+    constexpr int TJ = BN / 32;
+    constexpr int NQB = BN / 8;  // 1 KiB transfers of the B codes per step (8 columns each)
+    __shared__ alignas(16) uint8_t sA0[ABYTES], sA1[ABYTES];
+    __shared__ alignas(16) uint8_t sB0[BN * 128], sB1[BN * 128];
+    __shared__ alignas(16) uint32_t sD0[256], sD1[256];  // 64 columns x 4 block headers
+
+    const int64_t Kp = pad_k(K);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int li = lane & 31, lh = lane >> 5;
+    const int wr = wave * 32;
+
+    int bx = (int)blockIdx.x, by = (int)blockIdx.y;
+    if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
+    const int64_t row0 = (int64_t)bx * BM, col0 = (int64_t)by * BN;
+    const int nst_all = (int)(K / KSTEP);  // even
+    // a K part takes whole 256-element super-steps (two steps), as the split
+    // factor counts them
+    const int nss = nst_all / 2;
+    const int s_begin = 2 * (nss * (int)blockIdx.z / gz), s_end = 2 * (nss * ((int)blockIdx.z + 1) / gz);
+
+    // per-lane transfer sources (fixed over the K loop)
+    const uint8_t *a_src[(18 + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (18 + 3) / 4; ++i) {
+        const int t = wave + 4 * i < 18 ? wave + 4 * i : 0;
+        const int pos = t * 1024 + lane * 16, r = pos / WIN;
+        const int64_t rr = row0 + r < nrows ? row0 + r : nrows - 1;
+        a_src[i] = w + rr * row_stride + (pos - r * WIN);
+    }
+    const int8_t *b_src[(NQB + 3) / 4];
+#pragma unroll
+    for (int i = 0; i < (NQB + 3) / 4; ++i) {
+        const int t = wave + 4 * i < NQB ? wave + 4 * i : 0;
+        const int n = 8 * t + (lane >> 3);
+        const int64_t c = col0 + n < ncols ? col0 + n : col0;
+        b_src[i] = yqs + c * Kp + 16 * ((lane & 7) ^ ((n >> 1) & 7));
+    }
+    // column headers (wave 3): lane n moves the four headers of column n
+    const uint32_t *d_src;
+    {
+        const int n = lane < BN ? lane : 0;
+        const int64_t c = col0 + n < ncols ? col0 + n : col0;
+        d_src = yds + c * (Kp / QK8);
+    }
+
+    auto dma = [&](int s, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
+        const int64_t woff = ((int64_t)s * STEP_BYTES) & ~(int64_t)15;
+#pragma unroll
+        for (int i = 0; i < (18 + 3) / 4; ++i)
+            if (wave + 4 * i < 18) dma16(a_src[i] + woff, sA + (wave + 4 * i) * 1024);
+#pragma unroll
+        for (int i = 0; i < (NQB + 3) / 4; ++i)
+            if (wave + 4 * i < NQB) dma16(b_src[i] + (int64_t)s * KSTEP, sB + (wave + 4 * i) * 1024);
+        if (wave == 3) dma16(d_src + 4 * s, sD);
+    };
+
+    v16f acc[TJ];
+#pragma unroll
+    for (int j = 0; j < TJ; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
+
+    // Scale outer product on the f16 MFMA with one live K slot (slot 0 of
+    // lane half 0): lanes of half 0 hand d_b of their row and d8_b of their
+    // column, lanes of half 1 zeros.
+    const uint32_t keep = lh ? 0u : 0xFFFFu;
+
+    auto compute = [&](int s, const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
+        const int shift = (s * STEP_BYTES) & 15;  // 0 or 8, uniform
+        const uint8_t *arow = sA + (wr + li) * WIN + shift;
+        struct Ops {
+            v4i b;
+            v4h sb;
+        };
+        v4i aop[2];
+        v4h asc[2];
+        auto load_a = [&](int i, int slot) {
+            aop[slot] = lds16_a2(arow, 34 * i + 2 + 16 * lh);
+            const uint32_t dw = *reinterpret_cast<const uint32_t *>(arow + ((34 * i) & ~3));
+            const uint32_t d = ((34 * i) & 3) ? dw >> 16 : dw;
+            asc[slot] = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
+        };
+        auto load_b = [&](int p, Ops &o) {
+            const int i = p / TJ, j = p % TJ;
+            const int n = 32 * j + li;
+            o.b = *reinterpret_cast<const v4i *>(sB + n * 128 + 16 * ((2 * i + lh) ^ ((n >> 1) & 7)));
+            o.sb = __builtin_bit_cast(v4h, make_uint2(sD[4 * n + i] & keep, 0u));
+        };
+        auto issue = [&](int p, const Ops &o, v16i &S, v16f &SC) {
+            const int i = p / TJ;
+            const v16i z = {0};
+            const v16f zf = {0};
+            S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[i & 1], o.b, z, 0, 0, 0);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(asc[i & 1], o.sb, zf, 0, 0, 0);
+        };
+        auto consume = [&](int p, const v16i &S, const v16f &SC) {
+            const int j = p % TJ;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) acc[j][v] = fmaf((float)S[v], SC[v], acc[j][v]);
+            // keep the FMAs at their pair: nothing reads acc before the
+            // stores, and sinking them there would hold every S and SC
+            asm volatile("" : "+v"(acc[j]));
+        };
+        // pair p = (block p / TJ, column tile p % TJ); pair p+1's MFMAs and
+        // pair p+2's LDS reads go out before pair p's epilogue
+        constexpr int NP = 4 * TJ;
+        Ops ops[2];
+        v16i Sb[2];
+        v16f SCb[2];
+        load_a(0, 0);
+        load_b(0, ops[0]);
+        if (1 / TJ != 0) load_a(1, 1);
+        load_b(1, ops[1]);
+        issue(0, ops[0], Sb[0], SCb[0]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (p + 1 < NP) issue(p + 1, ops[(p + 1) & 1], Sb[(p + 1) & 1], SCb[(p + 1) & 1]);
+            if (p + 2 < NP) {
+                if ((p + 2) % TJ == 0) load_a((p + 2) / TJ, ((p + 2) / TJ) & 1);
+                load_b(p + 2, ops[p & 1]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            consume(p, Sb[p & 1], SCb[p & 1]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+
+    dma(s_begin, sA0, sB0, sD0);
+    wait_vmem();
+    __syncthreads();
+    for (int s = s_begin; s < s_end; s += 2) {
+        dma(s + 1, sA1, sB1, sD1);  // the part holds an even number of steps
+        compute(s, sA0, sB0, sD0);
+        wait_vmem();
+        __syncthreads();
+        if (s + 2 < s_end) dma(s + 2, sA0, sB0, sD0);
+        compute(s + 1, sA1, sB1, sD1);
+        wait_vmem();
+        __syncthreads();
+    }
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        const int64_t c = col0 + 32 * j + li;
+        if (c >= ncols) continue;
+        float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + c * dst_col_stride;
+        store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
+    }
+}
+
+}  // namespace
+
+// Launch for mmq.hip's dispatch: dense Q8_0, rows of K % 256 == 0 at 16-byte
+// aligned addresses and strides, 16-byte aligned activation planes (the
+// caller checks).  `grid` is (row tiles, column tiles, K parts).
+int mmq_q80_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
+                       hipStream_t s) {
+    if (K % 256 || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
+        return (int)hipErrorInvalidValue;
+    const uint8_t *wb = (const uint8_t *)w;
+    const uint32_t *ds = (const uint32_t *)yds;
+    if (bn == 32)
+        hipLaunchKernelGGL((mmq_q80_dma_kernel<32>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
+                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
+    else
+        hipLaunchKernelGGL((mmq_q80_dma_kernel<64>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
+                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
+    return (int)hipGetLastError();
+}
