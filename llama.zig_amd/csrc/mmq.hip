@@ -43,10 +43,10 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
                        const int32_t *col_dst, float *partial, const MmqGlu &glu, hipStream_t s);
-// mmq_q80_dma.hip: the dense Q8_0 kernel fed by direct global->LDS loads
-int mmq_q80_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
-                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                       hipStream_t s);
+// mmq_legacy_dma.hip: the dense Q8_0 / Q4_0 kernel fed by direct global->LDS loads
+int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                          const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
+                          dim3 grid, float *partial, hipStream_t s);
 // mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
@@ -693,11 +693,12 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
                                        dst_col_stride, grid, tiles, n_tiles, col_src, col_dst,
                                        split > 1 ? partial : nullptr, glu, s))
             return e;
-    } else if (TYPE == TYPE_Q8_0 && !tiles && !glu.gate && (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 &&
-               (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
-        // dense Q8_0 on 16-byte aligned rows: direct global->LDS windows
-        if (int e = mmq_q80_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
-                                       split > 1 ? partial : nullptr, s))
+    } else if ((TYPE == TYPE_Q8_0 || (TYPE == TYPE_Q4_0 && (K / BK) % (2 * split) == 0)) && !tiles && !glu.gate &&
+               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 &&
+               (uintptr_t)yds % 16 == 0) {
+        // dense Q8_0 / Q4_0 on 16-byte aligned rows: direct global->LDS steps
+        if (int e = mmq_legacy_dma_launch(TYPE, BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride,
+                                          grid, split > 1 ? partial : nullptr, s))
             return e;
     } else {
         hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,

@@ -1,25 +1,31 @@
-// mmq_q80_dma.hip -- the Q8_0 MMQ with direct global->LDS loads.
+// mmq_legacy_dma.hip -- the Q8_0 and Q4_0 MMQ with direct global->LDS loads.
 //
 // Arithmetic as in mmq.hip: the 32-deep block dot on v_mfma_i32_32x32x32_i8
 // (exact), the per-(row, column, block) scale d_b * d8_b as an exact f16 outer
 // product (v_mfma_f32_32x32x8_f16, one live K slot), one convert + FMA per
 // output and block:
-//   out = sum_b (d_b * d8_b) * dot_b(qs, q8)
-// Q8_0 has no super-block, so there is no per-super-block term.
+//   out = sum_b (d_b * d8_b) * dot_b(q, q8)
+// with q the Q8_0 codes or the Q4_0 nibbles minus 8.  These "legacy" types
+// (ggml's name) have no super-block, so there is no per-super-block term.
 //
-// Data path.  A K-step is 128 values: four 34-byte blocks, 136 bytes of each
-// row.  Q8_0 rows of K % 256 == 0 have a length of a multiple of 272 bytes,
-// so step s's bytes start at 136 s, 16-byte aligned for even s and 8 bytes
-// past a 16-byte boundary for odd s; the 144-byte 16-aligned window around
-// them (never past the row: the last step is odd and its window ends at the
-// row's end) goes straight from global memory into LDS with
-// global_load_lds_dwordx4, rows back to back at a 144-byte stride.  Operand
-// reads start 2 bytes into a block, so a lane reads the dwords around its 16
-// code bytes and funnel-shifts them (v_alignbyte_b32).  The columns' Q8_1
-// bytes (128 per column) and their four block headers come the same way;
-// chunk c of column n sits at slot c ^ ((n >> 1) & 7), so 16 consecutive
-// columns' reads of one chunk cover all banks.  Two buffers: the next step's
-// transfers run while the current step is contracted, one barrier per step.
+// Data path.  Rows of K % 256 == 0 at 16-byte aligned addresses and strides:
+//   - Q8_0: a K-step is 128 values, four 34-byte blocks, 136 bytes of a row.
+//     A Q8_0 row is a multiple of 272 bytes, so step s starts at 136 s,
+//     16-byte aligned for even s and 8 bytes past a boundary for odd s; the
+//     144-byte aligned window around it (never past the row: the last step
+//     is odd and its window ends at the row's end) is moved.
+//   - Q4_0: a K-step is 256 values, eight 18-byte blocks, 144 bytes of a row,
+//     always 16-byte aligned; the step's bytes are moved as they are.
+// Either way 144 bytes per row go straight from global memory into LDS with
+// global_load_lds_dwordx4, rows back to back.  A block's codes start 2 bytes
+// in, so a lane reads the dwords around its 16 code bytes and funnel-shifts
+// them (v_alignbyte_b32) when they are not dword-aligned.  Q4_0's lane half h
+// takes the low (h = 0) or high (h = 1) nibbles of the block's 16 bytes and
+// subtracts 8 bytewise ((n + 0x78) ^ 0x80, no carries between bytes).  The
+// columns' Q8_1 bytes (one step's worth per column) and their block headers
+// come the same way; 16 consecutive columns' reads of one 16-byte chunk cover
+// all banks.  Two buffers: the next step's transfers run while the current
+// step is contracted, one barrier per step.
 #include "../../include/ggml_hip_qmm.h"
 #include "qmm_device.h"
 
@@ -35,10 +41,25 @@ typedef __attribute__((address_space(3))) void *lds_ptr;
 
 constexpr int BM = 128;
 constexpr int NTHREADS = 256;
-constexpr int KSTEP = 128;              // 4 blocks
-constexpr int WIN = 144;                // bytes of a row's step window in LDS
-constexpr int ABYTES = BM * WIN;        // 18432: 18 transfers of 1 KiB
-constexpr int STEP_BYTES = 4 * Q80_BYTES;  // 136
+constexpr int WIN = 144;          // bytes of a row's step in LDS
+constexpr int ABYTES = BM * WIN;  // 18432: 18 transfers of 1 KiB
+
+template <int TYPE>
+struct Legacy;
+template <>
+struct Legacy<TYPE_Q8_0> {
+    static constexpr int KSTEP = 128;                // values per step
+    static constexpr int NB = 4;                     // blocks per step
+    static constexpr int BBYTES = Q80_BYTES;         // 34
+    static constexpr int STEP_BYTES = NB * BBYTES;   // 136: the window is the aligned 144 around it
+};
+template <>
+struct Legacy<TYPE_Q4_0> {
+    static constexpr int KSTEP = 256;
+    static constexpr int NB = 8;
+    static constexpr int BBYTES = Q40_BYTES;         // 18
+    static constexpr int STEP_BYTES = NB * BBYTES;   // 144: always aligned
+};
 
 __device__ __forceinline__ void dma16(const void *g, void *lds_base) {
     __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_base, 16, 0, 0);
@@ -73,16 +94,25 @@ __device__ __forceinline__ v4i lds16_a2(const uint8_t *base, int o) {
                (int)__builtin_amdgcn_alignbyte(a3, a2, 2), (int)__builtin_amdgcn_alignbyte(a4, a3, 2)};
 }
 
-template <int BN>
-__global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
+template <int TYPE, int BN>
+__global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
     float *__restrict__ partial, int gx, int gy, int gz) {
+    using L = Legacy<TYPE>;
+    constexpr int KSTEP = L::KSTEP, NB = L::NB, STEP_BYTES = L::STEP_BYTES;
     constexpr int TJ = BN / 32;
-    constexpr int NQB = BN / 8;  // 1 KiB transfers of the B codes per step (8 columns each)
+    constexpr int NCH = KSTEP / 16;                 // 16-byte chunks of a column's step codes
+    constexpr int NQB = BN * KSTEP / 1024;          // 1 KiB transfers of the B codes per step
+    constexpr int NQD = (BN * NB * 4 + 1023) / 1024;  // 1 KiB transfers of the headers per step
+    static_assert(NQB % 4 == 0 && NQD <= 2, "code transfers over 4 waves, headers on waves 2-3");
+    // slot of a column's 16-byte chunk c: c ^ bswz(n), so 16 consecutive
+    // columns' reads of one chunk spread over all banks (a column's step is
+    // 128 bytes for Q8_0, 256 for Q4_0)
+    auto bswz = [](int n) { return NCH == 16 ? (n & 15) : ((n >> 1) & 7); };
     __shared__ alignas(16) uint8_t sA0[ABYTES], sA1[ABYTES];
-    __shared__ alignas(16) uint8_t sB0[BN * 128], sB1[BN * 128];
-    __shared__ alignas(16) uint32_t sD0[256], sD1[256];  // 64 columns x 4 block headers
+    __shared__ alignas(16) uint8_t sB0[BN * KSTEP], sB1[BN * KSTEP];
+    __shared__ alignas(16) uint32_t sD0[NQD * 256], sD1[NQD * 256];  // the columns' block headers
 
     const int64_t Kp = pad_k(K);
     const int lane = threadIdx.x & 63;
@@ -93,11 +123,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
     if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
     const int64_t row0 = (int64_t)bx * BM, col0 = (int64_t)by * BN;
-    const int nst_all = (int)(K / KSTEP);  // even
-    // a K part takes whole 256-element super-steps (two steps), as the split
-    // factor counts them
-    const int nss = nst_all / 2;
-    const int s_begin = 2 * (nss * (int)blockIdx.z / gz), s_end = 2 * (nss * ((int)blockIdx.z + 1) / gz);
+    // a K part takes whole 256-value super-steps (SPS steps each), as the
+    // split factor counts them; the loop below takes steps in pairs, so a
+    // Q4_0 part needs an even number of super-steps (the caller checks)
+    constexpr int SPS = 256 / KSTEP;
+    const int nss = (int)(K / 256);
+    const int s_begin = SPS * (nss * (int)blockIdx.z / gz), s_end = SPS * (nss * ((int)blockIdx.z + 1) / gz);
 
     // per-lane transfer sources (fixed over the K loop)
     const uint8_t *a_src[(18 + 3) / 4];
@@ -112,16 +143,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
 #pragma unroll
     for (int i = 0; i < (NQB + 3) / 4; ++i) {
         const int t = wave + 4 * i < NQB ? wave + 4 * i : 0;
-        const int n = 8 * t + (lane >> 3);
+        // transfer t covers 1024 / (16 NCH) columns; lane -> (column, slot)
+        const int n = t * (64 / NCH) + lane / NCH, slot = lane % NCH;
         const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        b_src[i] = yqs + c * Kp + 16 * ((lane & 7) ^ ((n >> 1) & 7));
+        b_src[i] = yqs + c * Kp + 16 * (slot ^ bswz(n));
     }
-    // column headers (wave 3): lane n moves the four headers of column n
+    // column headers (waves 2 .. 1 + NQD): 16-byte runs of NB headers per
+    // column; transfer t, lane l -> column (64 t + l) / (NB / 4), part
     const uint32_t *d_src;
     {
-        const int n = lane < BN ? lane : 0;
+        const int per = NB / 4;  // 16-byte runs per column
+        const int q = (wave >= 2 && wave - 2 < NQD ? wave - 2 : 0) * 64 + lane;
+        const int n0 = q / per, part = q % per;
+        const int n = n0 < BN ? n0 : 0;
         const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        d_src = yds + c * (Kp / QK8);
+        d_src = yds + c * (Kp / QK8) + 4 * part;
     }
 
     auto dma = [&](int s, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
@@ -132,7 +168,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
 #pragma unroll
         for (int i = 0; i < (NQB + 3) / 4; ++i)
             if (wave + 4 * i < NQB) dma16(b_src[i] + (int64_t)s * KSTEP, sB + (wave + 4 * i) * 1024);
-        if (wave == 3) dma16(d_src + 4 * s, sD);
+        if (wave >= 2 && wave - 2 < NQD)
+            dma16(d_src + NB * s, reinterpret_cast<uint8_t *>(sD) + (wave - 2) * 1024);
     };
 
     v16f acc[TJ];
@@ -156,16 +193,28 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
         v4i aop[2];
         v4h asc[2];
         auto load_a = [&](int i, int slot) {
-            aop[slot] = lds16_a2(arow, 34 * i + 2 + 16 * lh);
-            const uint32_t dw = *reinterpret_cast<const uint32_t *>(arow + ((34 * i) & ~3));
-            const uint32_t d = ((34 * i) & 3) ? dw >> 16 : dw;
+            constexpr int BB = L::BBYTES;
+            if constexpr (TYPE == TYPE_Q8_0) {
+                aop[slot] = lds16_a2(arow, BB * i + 2 + 16 * lh);
+            } else {
+                // Q4_0: the block's 16 bytes, low or high nibbles, minus 8
+                const v4i raw = lds16_a2(arow, BB * i + 2);
+                const int sh = 4 * lh;
+                v4i q;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    q[e] = (int)((((uint32_t)raw[e] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ (int)0x80808080u;
+                aop[slot] = q;
+            }
+            const uint32_t dw = *reinterpret_cast<const uint32_t *>(arow + ((BB * i) & ~3));
+            const uint32_t d = ((BB * i) & 3) ? dw >> 16 : dw;
             asc[slot] = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
         };
         auto load_b = [&](int p, Ops &o) {
             const int i = p / TJ, j = p % TJ;
             const int n = 32 * j + li;
-            o.b = *reinterpret_cast<const v4i *>(sB + n * 128 + 16 * ((2 * i + lh) ^ ((n >> 1) & 7)));
-            o.sb = __builtin_bit_cast(v4h, make_uint2(sD[4 * n + i] & keep, 0u));
+            o.b = *reinterpret_cast<const v4i *>(sB + n * KSTEP + 16 * ((2 * i + lh) ^ bswz(n)));
+            o.sb = __builtin_bit_cast(v4h, make_uint2(sD[NB * n + i] & keep, 0u));
         };
         auto issue = [&](int p, const Ops &o, v16i &S, v16f &SC) {
             const int i = p / TJ;
@@ -184,7 +233,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
         };
         // pair p = (block p / TJ, column tile p % TJ); pair p+1's MFMAs and
         // pair p+2's LDS reads go out before pair p's epilogue
-        constexpr int NP = 4 * TJ;
+        constexpr int NP = NB * TJ;
         Ops ops[2];
         v16i Sb[2];
         v16f SCb[2];
@@ -231,21 +280,30 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q80_dma_kernel(
 
 }  // namespace
 
-// Launch for mmq.hip's dispatch: dense Q8_0, rows of K % 256 == 0 at 16-byte
-// aligned addresses and strides, 16-byte aligned activation planes (the
-// caller checks).  `grid` is (row tiles, column tiles, K parts).
-int mmq_q80_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
-                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                       hipStream_t s) {
+// Launch for mmq.hip's dispatch: dense Q8_0 or Q4_0, rows of K % 256 == 0
+// at 16-byte aligned addresses and strides, 16-byte aligned activation
+// planes (the caller checks).  `grid` is (row tiles, column tiles, K parts);
+// Q4_0 parts must hold an even number of 256-value super-steps.
+int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
+                          const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
+                          dim3 grid, float *partial, hipStream_t s) {
     if (K % 256 || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
         return (int)hipErrorInvalidValue;
+    if (type == TYPE_Q4_0 && (K / 256) % (2 * (int64_t)grid.z)) return (int)hipErrorInvalidValue;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
-    if (bn == 32)
-        hipLaunchKernelGGL((mmq_q80_dma_kernel<32>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
-                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
-    else
-        hipLaunchKernelGGL((mmq_q80_dma_kernel<64>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
-                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
+#define LEGACY_LAUNCH(T, BNV)                                                                                          \
+    hipLaunchKernelGGL((mmq_legacy_dma_kernel<T, BNV>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds, \
+                       ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z)
+    if (type == TYPE_Q8_0) {
+        if (bn == 32) LEGACY_LAUNCH(TYPE_Q8_0, 32);
+        else LEGACY_LAUNCH(TYPE_Q8_0, 64);
+    } else if (type == TYPE_Q4_0) {
+        if (bn == 32) LEGACY_LAUNCH(TYPE_Q4_0, 32);
+        else LEGACY_LAUNCH(TYPE_Q4_0, 64);
+    } else {
+        return (int)hipErrorInvalidValue;
+    }
+#undef LEGACY_LAUNCH
     return (int)hipGetLastError();
 }
