@@ -51,6 +51,10 @@ int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nr
 int mmq_iq4xs_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                          const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
                          hipStream_t s);
+// mmq_q5k_dma.hip: the dense Q5_K kernel fed by direct global->LDS loads
+int mmq_q5k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
+                       const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
+                       hipStream_t s);
 // mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
@@ -703,6 +707,12 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
         // dense Q8_0 / Q4_0 on 16-byte aligned rows: direct global->LDS steps
         if (int e = mmq_legacy_dma_launch(TYPE, BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride,
                                           grid, split > 1 ? partial : nullptr, s))
+            return e;
+    } else if (TYPE == TYPE_Q5_K && !tiles && !glu.gate && (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 &&
+               (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+        // dense Q5_K (176-byte blocks, 16-byte aligned in aligned rows): direct global->LDS steps
+        if (int e = mmq_q5k_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
+                                       split > 1 ? partial : nullptr, s))
             return e;
     } else if (TYPE == TYPE_IQ4_XS && K % 512 == 0 && (K / QK_K) % (2 * split) == 0 && !tiles && !glu.gate &&
                (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 &&
