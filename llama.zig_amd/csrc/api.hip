@@ -17,7 +17,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
 // mmq.hip: whether the few-column kernel takes this shape (given aligned operands)
-bool few_cols_type(int type, int64_t K, int64_t ncols);
+bool few_cols_type(int type, int64_t K, int64_t nrows, int64_t ncols);
 // mmq_few.hip: whether it takes these weight rows
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
 
@@ -57,7 +57,7 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 //     K >= 8192 on <= 2048 rows take the few-column kernel there (2048x14336:
 //     30.4 against 21.5).
 bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, ncols)) return false;
+    if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, nrows, ncols)) return false;
     const int64_t elems = nrows * K;
     const bool large = elems >= ((int64_t)24 << 20), mid = elems >= ((int64_t)12 << 20), long_rows = K >= 8192;
     switch (type) {
@@ -97,7 +97,7 @@ bool use_mmq_rows(int type, int64_t K, int64_t nrows, int64_t ncols, const void 
 // few-column kernel; the reference's shouldFuseMulMatQ likewise leaves the
 // matmuls its few-row MMQ and MMVQ take, src/ggml/cuda/mulmat.zig:560-567).
 bool glu_fuses_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    return ncols >= 2 && use_mmq(type, K, nrows, ncols) && !few_cols_type(type, K, ncols);
+    return ncols >= 2 && use_mmq(type, K, nrows, ncols) && !few_cols_type(type, K, nrows, ncols);
 }
 
 // The unfused gate/up/GLU's workspace: the gate and up products, then

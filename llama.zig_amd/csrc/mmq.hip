@@ -815,30 +815,48 @@ int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
 // The few-column kernel (mmq_few.hip) takes Q4_K, Q5_K, Q8_0, Q4_0 and IQ4_XS
 // up to 32 columns and Q6_K up to 16 (K % 2048 == 0; Q8_0 / Q4_0 / Q6_K /
 // IQ4_XS on 16-byte-aligned rows), when the activation planes are 16-byte
-// aligned.
-// Measured against the 128-row tile (us, 4096x14336, same weights): Q8_0 9 /
-// 32 columns 18.6 / 23.2 against 33.2 / 39.1; Q5_K 16.0 / 21.0 against 23.2 /
-// 26.4; Q4_0 16.1 / 20.8 against 24.5 / 28.6; IQ4_XS (K % 512 == 0) 17.5 /
-// 21.4 against 24.0 / 24.6; Q6_K 9 / 16 columns 22.6 / 23.2
-// against 28.3 / 29.3, but 48.3 / 48.8 against 31.3 / 33.4 at 24 / 32 (two
-// column tiles), so those keep the tile.  few_cols_type is the part that depends on the shape alone
-// (the split and workspace queries); the dispatch also checks the rows
-// (mmq_few_takes).
-bool few_cols_type(int type, int64_t K, int64_t ncols) {
-    return (ncols <= 32 && (type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K || type == TYPE_Q4_0)) ||
-           (ncols <= 32 && type == TYPE_IQ4_XS && K % 512 == 0) ||
-           (ncols <= 16 && type == TYPE_Q6_K && K % 2048 == 0);
+// aligned.  Up to 8 columns the op's GEMV / few-column choice decides
+// (api.hip).  From 9 columns the 128-row tile, fed by direct global->LDS
+// transfers for every type but Q6_K, is as fast or faster except on large
+// weights at up to 16 columns.  Measured, the whole call with its split
+// reduce, few-column against tile (us):
+//   - 17-32 columns: equal within 1 us or the tile ahead (Q8_0 14336x4096 at
+//     24 / 32: 24.7 / 25.3 against 21.4 / 22.4);
+//   - 9-16 columns on weights below 16 MiB: the tile ahead (Q4_K 4096x4096 at
+//     9 / 16: 16.3 / 13.7 against 10.3 / 11.6; 1024x4096: 13.8 / 12.2 against
+//     8.9 / 8.8);
+//   - 9-16 columns on larger weights: the few-column kernel ahead (Q4_K
+//     14336x4096: 14.3 / 16.2 against 18.7 / 19.6; 4096x14336: 16.2 / 15.9
+//     against 18.7 / 19.0; Q8_0 4096x14336: 18.5 / 19.8 against 20.8 / 21.7);
+//   - Q6_K (tile: the staged kernel) at 9-16 columns: the few-column kernel
+//     ahead or equal from 4 MiB of weights (2048x8192: 13.9 / 13.7 against
+//     15.6 / 19.8), the tile ahead on 1024x4096 (12.7 against 16.6 at 9).
+// few_cols_type is the part that depends on the shape alone (the split and
+// workspace queries); the dispatch also checks the rows (mmq_few_takes).
+bool few_cols_type(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    const bool takes = (ncols <= 32 && (type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K ||
+                                        type == TYPE_Q4_0)) ||
+                       (ncols <= 32 && type == TYPE_IQ4_XS && K % 512 == 0) ||
+                       (ncols <= 16 && type == TYPE_Q6_K && K % 2048 == 0);
+    if (!takes) return false;
+    if (ncols <= 8) return true;
+    const int64_t bytes_per_256 = type == TYPE_Q4_K ? Q4K_BYTES : type == TYPE_Q5_K ? Q5K_BYTES
+                                : type == TYPE_Q6_K ? Q6K_BYTES : type == TYPE_IQ4_XS ? IQ4XS_BYTES
+                                : type == TYPE_Q8_0 ? 8 * Q80_BYTES : 8 * Q40_BYTES;
+    const int64_t wbytes = nrows * (K / QK_K) * bytes_per_256;
+    if (type == TYPE_Q6_K) return wbytes >= ((int64_t)4 << 20);
+    return ncols <= 16 && wbytes >= ((int64_t)16 << 20);
 }
 
 extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 1;
-    return few_cols_type(type, K, ncols) ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
+    return few_cols_type(type, K, nrows, ncols) ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);
 }
 
 extern "C" size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K <= 0 || nrows <= 0 || ncols <= 0) return 0;
     int split = split_std(type, K, nrows, ncols);
-    if (few_cols_type(type, K, ncols) && mmq_few_split_k(K, nrows) > split) split = mmq_few_split_k(K, nrows);
+    if (few_cols_type(type, K, nrows, ncols) && mmq_few_split_k(K, nrows) > split) split = mmq_few_split_k(K, nrows);
     return split > 1 ? (size_t)split * (size_t)nrows * (size_t)ncols * sizeof(float) : 0;
 }
 
@@ -851,7 +869,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
     if (int e = check_weights(type, w, K, row_stride)) return e;
     const int bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
-    const bool few = few_cols_type(type, K, ncols) && mmq_few_takes(type, K, w, row_stride) &&
+    const bool few = few_cols_type(type, K, nrows, ncols) && mmq_few_takes(type, K, w, row_stride) &&
                      (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;
     // split K only when the caller's workspace holds the partials
     int split = few ? mmq_few_split_k(K, nrows) : split_std(type, K, nrows, ncols);

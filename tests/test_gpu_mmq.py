@@ -137,11 +137,12 @@ def _offset_copy(w_d, off=2):
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 3), (4096, 2048, 9), (700, 14336, 17), (4100, 4096, 32),
                                            (64, 2048, 16)])
 def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
-    """Q8_0 and Q4_0 with at most 32 columns and Q6_K with at most 16 take the
-    few-column kernel on 16-byte-aligned rows (Q6_K from K % 2048 == 0):
-    within the f64 and CPU gates, and within rounding of the 128-row MMQ tile
-    that the same rows take at a 2-byte-aligned base (and Q6_K at 17-32
-    columns)."""
+    """Q8_0, Q4_0 and Q6_K at 3-32 columns on small weights: up to 8 columns
+    the few-column kernel (16-byte-aligned rows, Q6_K from K % 2048 == 0),
+    above that the 128-row tile (these weights are below the few-column
+    kernel's size threshold): within the f64 and CPU gates, and within
+    rounding of the staged 128-row tile that the same rows take at a
+    2-byte-aligned base."""
     import ggml_hip as G
     t = TYPES[tname]
     wq = weights_q(t, nrows, K)
@@ -166,11 +167,11 @@ def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
                                            (64, 2048, 16), (256, 512, 24)])
 @pytest.mark.parametrize("tname", ["Q5_K", "IQ4_XS"])
 def test_few_columns_q5_k_iq4_xs(tname, nrows, K, ncols):
-    """Q5_K and IQ4_XS (K % 512 == 0) up to 32 columns take the few-column
-    kernel (Q5_K: the Q4_K data path with the fifth bits merged from qh;
-    IQ4_XS: an 8-byte-aligned window around each block, levels looked up by
-    byte permutes): within the f64 and CPU gates; the op above 8 columns runs
-    the same kernel."""
+    """Q5_K and IQ4_XS (K % 512 == 0) at 3-32 columns on small weights: the
+    few-column kernel up to 8 columns (Q5_K: the Q4_K data path with the fifth
+    bits merged from qh; IQ4_XS: an 8-byte-aligned window around each block,
+    levels looked up by byte permutes), the 128-row tile above: within the
+    f64 and CPU gates; the op above 8 columns runs the same kernel."""
     import ggml_hip as G
     t = TYPES[tname]
     assert G.lib().hip_qmm_mmq_split_k(t, K, nrows, ncols) >= 1
@@ -187,3 +188,27 @@ def test_few_columns_q5_k_iq4_xs(tname, nrows, K, ncols):
     assert nmse(got, cpu) < NMSE_GATE
     if ncols > 8:
         np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q8_0", "Q4_0", "IQ4_XS", "Q6_K"])
+@pytest.mark.parametrize("ncols", [9, 16])
+def test_few_columns_large_weights(tname, ncols):
+    """9-16 columns of a large weight (config 3's 4096x14336, at least 16 MiB
+    for every type) take the few-column kernel: checked on a row subset
+    against the f64 formula and the CPU path, and equal to the op."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    nrows, K = 4096, 14336
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    got = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    rows = np.r_[0:64, 2000:2064, nrows - 64:nrows]
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq[rows], len(rows), K, y, ncols)
+    assert max_err_scaled(got[:, rows], ideal) < F64_TOL, max_err_scaled(got[:, rows], ideal)
+    cpu = O.mul_mat_x86(t, wq[rows], len(rows), K, x, nth=8)
+    assert nmse(got[:, rows], cpu) < NMSE_GATE
+    np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
