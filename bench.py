@@ -406,12 +406,11 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
             batches = (128, 512, 2048)
         elif name == "few":
             # batched decode: the few-column GEMM against the GEMV (<= 8
-            # columns); from 9 columns the dispatched MMQ (the few-column
-            # kernel on large weights at <= 16 columns, else the 128-row
-            # tile) next to the staged tile (for Q6_K / Q8_0 / Q4_0 / IQ4_XS
-            # timed on the same weights at a base 2 (IQ4_XS: 8) bytes past
-            # 16-byte alignment, which neither direct-transfer kernel takes;
-            # Q5_K rows must be 16-byte aligned, so it has no staged line)
+            # columns) and the 128-row MMQ tile it replaced (9-32 columns;
+            # for Q6_K / Q8_0 / Q4_0 / IQ4_XS the tile is timed on the same
+            # weights at a base 2 (IQ4_XS: 8) bytes past 16-byte alignment,
+            # which the few-column kernel does not take; Q5_K rows must be
+            # 16-byte aligned for both, so it has no tile line)
             shapes = [("Q4_K", 14336, 4096, "ffn_gate/up"), ("Q4_K", 4096, 14336, "Q4_K 4096x14336"),
                       ("Q4_K", 4096, 4096, "attn_q/o"), ("Q6_K", 4096, 14336, "ffn_down"),
                       ("Q6_K", 4096, 4096, "Q6_K 4096x4096"), ("Q8_0", 4096, 4096, "Q8_0 4096x4096"),
@@ -440,8 +439,8 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
                 ms = event_time_batch(torch, fn, n)
                 extra = {}
                 if name == "few":
-                    # the MMQ dispatch at every width (next to the GEMV up to
-                    # 8 columns)
+                    # the few-column GEMM at every width (next to the GEMV up
+                    # to 8 columns)
                     few_fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
                     extra["few_us"] = round(event_time_batch(torch, few_fn, n) * 1e3, 3)
                     extra["few_split"] = int(G.lib().hip_qmm_mmq_split_k(G.TYPE_IDS[qtype], Kx, M, T))

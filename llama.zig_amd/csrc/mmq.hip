@@ -815,37 +815,33 @@ int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
 // The few-column kernel (mmq_few.hip) takes Q4_K, Q5_K, Q8_0, Q4_0 and IQ4_XS
 // up to 32 columns and Q6_K up to 16 (K % 2048 == 0; Q8_0 / Q4_0 / Q6_K /
 // IQ4_XS on 16-byte-aligned rows), when the activation planes are 16-byte
-// aligned.  Up to 8 columns the op's GEMV / few-column choice decides
-// (api.hip).  From 9 columns the 128-row tile, fed by direct global->LDS
-// transfers for every type but Q6_K, is as fast or faster except on large
-// weights at up to 16 columns.  Measured, the whole call with its split
-// reduce, few-column against tile (us):
-//   - 17-32 columns: equal within 1 us or the tile ahead (Q8_0 14336x4096 at
-//     24 / 32: 24.7 / 25.3 against 21.4 / 22.4);
-//   - 9-16 columns on weights below 16 MiB: the tile ahead (Q4_K 4096x4096 at
-//     9 / 16: 16.3 / 13.7 against 10.3 / 11.6; 1024x4096: 13.8 / 12.2 against
-//     8.9 / 8.8);
-//   - 9-16 columns on larger weights: the few-column kernel ahead (Q4_K
-//     14336x4096: 14.3 / 16.2 against 18.7 / 19.6; 4096x14336: 16.2 / 15.9
-//     against 18.7 / 19.0; Q8_0 4096x14336: 18.5 / 19.8 against 20.8 / 21.7);
-//   - Q6_K (tile: the staged kernel) at 9-16 columns: the few-column kernel
-//     ahead or equal from 4 MiB of weights (2048x8192: 13.9 / 13.7 against
-//     15.6 / 19.8), the tile ahead on 1024x4096 (12.7 against 16.6 at 9).
-// few_cols_type is the part that depends on the shape alone (the split and
-// workspace queries); the dispatch also checks the rows (mmq_few_takes).
+// aligned, except Q8_0 and Q4_0 at 17-32 columns of 8 MiB of weights and
+// more: their 128-row tile moves the weights by direct global->LDS transfers
+// and is faster there.  Measured, the whole call in HIP graphs, few-column
+// against the tile (us): Q4_0 14336x4096 at 24 / 32 columns 23.3 / 23.7
+// against 19.0 / 19.5, Q8_0 14336x4096 23.1 / 23.4 against 21.5 / 22.4, Q8_0
+// 6144x4096 15.9 / 16.8 against 15.1 / 15.8, Q4_0 4096x4096 12.1 / 13.0
+// against 11.6 / 12.1; on 1024x4096 (4.5 MB of Q8_0) the few-column kernel
+// stays ahead (9.4 / 9.7 against 10.6 / 10.7).  Up to 16 columns, and for the
+// K-quants and IQ4_XS up to 32, the few-column kernel is as fast or faster on
+// every shape measured (Q4_K 1024x4096 at 9: 7.3 against 9.5; 4096x14336 at
+// 32: 20.3 against 21.4).  Earlier, against the staged tile: Q8_0 4096x14336
+// at 9 / 32 columns 18.6 / 23.2 against 33.2 / 39.1; Q6_K 9 / 16 columns 22.6
+// / 23.2 against 28.3 / 29.3, but 48.3 / 48.8 against 31.3 / 33.4 at 24 / 32
+// (two column tiles), so those keep the tile.  few_cols_type is the part that
+// depends on the shape alone (the split and workspace queries); the dispatch
+// also checks the rows (mmq_few_takes).
 bool few_cols_type(int type, int64_t K, int64_t nrows, int64_t ncols) {
     const bool takes = (ncols <= 32 && (type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K ||
                                         type == TYPE_Q4_0)) ||
                        (ncols <= 32 && type == TYPE_IQ4_XS && K % 512 == 0) ||
                        (ncols <= 16 && type == TYPE_Q6_K && K % 2048 == 0);
     if (!takes) return false;
-    if (ncols <= 8) return true;
-    const int64_t bytes_per_256 = type == TYPE_Q4_K ? Q4K_BYTES : type == TYPE_Q5_K ? Q5K_BYTES
-                                : type == TYPE_Q6_K ? Q6K_BYTES : type == TYPE_IQ4_XS ? IQ4XS_BYTES
-                                : type == TYPE_Q8_0 ? 8 * Q80_BYTES : 8 * Q40_BYTES;
-    const int64_t wbytes = nrows * (K / QK_K) * bytes_per_256;
-    if (type == TYPE_Q6_K) return wbytes >= ((int64_t)4 << 20);
-    return ncols <= 16 && wbytes >= ((int64_t)16 << 20);
+    if ((type == TYPE_Q8_0 || type == TYPE_Q4_0) && ncols > 16) {
+        const int64_t wbytes = nrows * (K / QK8) * (type == TYPE_Q8_0 ? Q80_BYTES : Q40_BYTES);
+        return wbytes < ((int64_t)8 << 20);
+    }
+    return true;
 }
 
 extern "C" int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols) {

@@ -137,12 +137,12 @@ def _offset_copy(w_d, off=2):
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 3), (4096, 2048, 9), (700, 14336, 17), (4100, 4096, 32),
                                            (64, 2048, 16)])
 def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
-    """Q8_0, Q4_0 and Q6_K at 3-32 columns on small weights: up to 8 columns
-    the few-column kernel (16-byte-aligned rows, Q6_K from K % 2048 == 0),
-    above that the 128-row tile (these weights are below the few-column
-    kernel's size threshold): within the f64 and CPU gates, and within
-    rounding of the staged 128-row tile that the same rows take at a
-    2-byte-aligned base."""
+    """Q8_0 and Q4_0 with at most 32 columns and Q6_K with at most 16 take the
+    few-column kernel on 16-byte-aligned rows (Q6_K from K % 2048 == 0; Q8_0
+    and Q4_0 at 17-32 columns only below 8 MiB of weights, else their
+    direct-transfer tile): within the f64 and CPU gates, and within rounding
+    of the staged 128-row tile that the same rows take at a 2-byte-aligned
+    base."""
     import ggml_hip as G
     t = TYPES[tname]
     wq = weights_q(t, nrows, K)
@@ -167,11 +167,11 @@ def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
                                            (64, 2048, 16), (256, 512, 24)])
 @pytest.mark.parametrize("tname", ["Q5_K", "IQ4_XS"])
 def test_few_columns_q5_k_iq4_xs(tname, nrows, K, ncols):
-    """Q5_K and IQ4_XS (K % 512 == 0) at 3-32 columns on small weights: the
-    few-column kernel up to 8 columns (Q5_K: the Q4_K data path with the fifth
-    bits merged from qh; IQ4_XS: an 8-byte-aligned window around each block,
-    levels looked up by byte permutes), the 128-row tile above: within the
-    f64 and CPU gates; the op above 8 columns runs the same kernel."""
+    """Q5_K and IQ4_XS (K % 512 == 0) up to 32 columns take the few-column
+    kernel (Q5_K: the Q4_K data path with the fifth bits merged from qh;
+    IQ4_XS: an 8-byte-aligned window around each block, levels looked up by
+    byte permutes): within the f64 and CPU gates; the op above 8 columns runs
+    the same kernel."""
     import ggml_hip as G
     t = TYPES[tname]
     assert G.lib().hip_qmm_mmq_split_k(t, K, nrows, ncols) >= 1
@@ -191,11 +191,13 @@ def test_few_columns_q5_k_iq4_xs(tname, nrows, K, ncols):
 
 
 @pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q8_0", "Q4_0", "IQ4_XS", "Q6_K"])
-@pytest.mark.parametrize("ncols", [9, 16])
+@pytest.mark.parametrize("ncols", [9, 16, 24])
 def test_few_columns_large_weights(tname, ncols):
-    """9-16 columns of a large weight (config 3's 4096x14336, at least 16 MiB
-    for every type) take the few-column kernel: checked on a row subset
-    against the f64 formula and the CPU path, and equal to the op."""
+    """9-24 columns of a large weight (config 3's 4096x14336): the few-column
+    kernel for every type up to 16 columns and for the K-quants and IQ4_XS at
+    24, the direct-transfer tile for Q8_0 and Q4_0 at 24 (Q6_K's tile from 17
+    columns): checked on a row subset against the f64 formula and the CPU
+    path, and equal to the op."""
     import ggml_hip as G
     t = TYPES[tname]
     nrows, K = 4096, 14336
