@@ -798,13 +798,18 @@ extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64;
 // 16.9 us for two per CU), two per CU at K = 14336 (Q4_K 4096 rows at 512
 // columns: 108 us against 135 us unsplit), and unequal shares lost to the
 // next smaller equal split (14336 rows at 24 columns: 3 shares 21.9 us, 2
-// shares 19.3 us).
+// shares 19.3 us).  A split never takes the grid past two workgroups per CU
+// (512): the second round of workgroups costs more than the split hides
+// (14336x4096 at 256 columns, 448 tiles, graph-timed unsplit against 2
+// shares: Q8_0 65.2 against 80.3 us, Q4_0 59.6 / 74.3, Q5_K 62.9 / 77.6,
+// IQ4_XS 66.2 / 80.4, Q6_K 113.9 / 131.7).
 int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     const int64_t bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
     const int64_t target = (type == TYPE_Q4_K && nkb <= 16) ? 256 : 512;
     int64_t split = (target + wgs - 1) / wgs;
+    while (split > 1 && wgs * split > 512) --split;
     const int64_t cap = nkb / 2 < 16 ? nkb / 2 : 16;
     if (split > cap) split = cap;
     if (split < 1) split = 1;
