@@ -27,20 +27,14 @@
 // all banks.  Two buffers: the next step's transfers run while the current
 // step is contracted, one barrier per step.
 #include "../../include/ggml_hip_qmm.h"
+#include "mmq_dma.h"
 #include "qmm_device.h"
 
 using namespace qmm;
+using namespace qmm_dma;
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void *lds_ptr;
-
-constexpr int BM = 128;
-constexpr int NTHREADS = 256;
 constexpr int WIN = 144;          // bytes of a row's step in LDS
 constexpr int ABYTES = BM * WIN;  // 18432: 18 transfers of 1 KiB
 
@@ -60,28 +54,6 @@ struct Legacy<TYPE_Q4_0> {
     static constexpr int BBYTES = Q40_BYTES;         // 18
     static constexpr int STEP_BYTES = NB * BBYTES;   // 144: always aligned
 };
-
-__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_base, 16, 0, 0);
-}
-
-__device__ __forceinline__ void wait_vmem() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
-}
-
-__device__ __forceinline__ void store_tile_column(float *o, int64_t r0, int64_t nrows, const v16f &a) {
-    if (((uintptr_t)(o + r0) & 15) == 0 && r0 + 27 < nrows) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<float4 *>(o + r0 + 8 * q) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
-    } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
-            if (r < nrows) o[r] = a[v];
-        }
-    }
-}
 
 // 16 bytes at LDS byte offset o (o % 2 == 0): the dwords around them,
 // funnel-shifted when o is not dword-aligned.

@@ -21,48 +21,16 @@
 // the output rows are read from the block headers in LDS, so the kernel needs
 // no table beside the two buffers (80 KB at 64 columns: two workgroups per CU).
 #include "../../include/ggml_hip_qmm.h"
+#include "mmq_dma.h"
 #include "qmm_device.h"
 
 using namespace qmm;
+using namespace qmm_dma;
 
 namespace {
 
-typedef int v4i __attribute__((ext_vector_type(4)));
-typedef int v16i __attribute__((ext_vector_type(16)));
-typedef float v16f __attribute__((ext_vector_type(16)));
-typedef _Float16 v4h __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void *lds_ptr;
-
-constexpr int BM = 128;
-constexpr int NTHREADS = 256;
 constexpr int ABYTES = BM * Q5K_BYTES;  // 22528: 22 transfers of 1 KiB
 constexpr int NA = ABYTES / 1024;
-
-__device__ __forceinline__ void dma16(const void *g, void *lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_ptr)lds_base, 16, 0, 0);
-}
-
-__device__ __forceinline__ void wait_vmem() {
-    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
-}
-
-__device__ __forceinline__ uint32_t f16_bits(float x) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x);
-}
-
-__device__ __forceinline__ void store_tile_column(float *o, int64_t r0, int64_t nrows, const v16f &a) {
-    if (((uintptr_t)(o + r0) & 15) == 0 && r0 + 27 < nrows) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q)
-            *reinterpret_cast<float4 *>(o + r0 + 8 * q) = make_float4(a[4 * q], a[4 * q + 1], a[4 * q + 2], a[4 * q + 3]);
-    } else {
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int64_t r = r0 + 8 * (v >> 2) + (v & 3);
-            if (r < nrows) o[r] = a[v];
-        }
-    }
-}
 
 template <int BN>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_q5k_dma_kernel(
