@@ -802,12 +802,15 @@ extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64;
 // (512): the second round of workgroups costs more than the split hides
 // (14336x4096 at 256 columns, 448 tiles, graph-timed unsplit against 2
 // shares: Q8_0 65.2 against 80.3 us, Q4_0 59.6 / 74.3, Q5_K 62.9 / 77.6,
-// IQ4_XS 66.2 / 80.4, Q6_K 113.9 / 131.7).
+// IQ4_XS 66.2 / 80.4, Q6_K 113.9 / 131.7).  Q8_0's direct-transfer kernel
+// takes the one-per-CU target too (graph-timed against two per CU: 4096x2048
+// at 256 / 512 columns 21.0 / 23.3 us against 24.0 / 30.9, 2048x4096 at 256
+// 20.7 against 23.2; 2048x4096 at 512 29.1 against 27.0).
 int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
     const int64_t bn = hip_qmm_mmq_tile_n(ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
-    const int64_t target = (type == TYPE_Q4_K && nkb <= 16) ? 256 : 512;
+    const int64_t target = ((type == TYPE_Q4_K || type == TYPE_Q8_0) && nkb <= 16) ? 256 : 512;
     int64_t split = (target + wgs - 1) / wgs;
     while (split > 1 && wgs * split > 512) --split;
     const int64_t cap = nkb / 2 < 16 ? nkb / 2 : 16;
