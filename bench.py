@@ -691,9 +691,10 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
         x = torch.randn((1, hk), generator=xg, dtype=torch.float32).to(dev)
         qs, ds = G.quantize_q8_1_planar(x)
         out = torch.empty((1, hm), dtype=torch.float32, device=dev)
-        sink = torch.empty(int(G.lib().hip_qmm_probe_sink_words(wb)), dtype=torch.int32, device=dev)
+        from ggml_hip import probes as P
+        sink = torch.empty(P.sink_words(wb), dtype=torch.int32, device=dev)
         n = len(ws) * reps
-        cases = (("stream read probe", lambda i: G.probe_stream_read(ws[i % len(ws)], sink=sink)),
+        cases = (("stream read probe", lambda i: P.stream_read(ws[i % len(ws)], sink=sink)),
                  ("gemv on a quantized column", lambda i: G.mul_mat_vec("Q4_K", ws[i % len(ws)], hk, qs, ds, out=out)),
                  ("op: gemv with fused quantization", lambda i: G.mul_mat("Q4_K", ws[i % len(ws)], x, out=out)))
         for kern, fn in cases:
@@ -705,18 +706,26 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
         torch.cuda.empty_cache()
     elif name == "overlap":
         # Whether MFMA and VALU work overlap on a SIMD (the MMQ ceiling rests on
-        # it), from hip_qmm_probe_mfma_valu: SIMD cycles per substep, in which
-        # each of the SIMD's two waves issues one v_mfma_f32_32x32x16_f16 and/or
-        # 16 fp32 FMAs (MFMAs alone, FMAs alone, both in every wave, both split
-        # across the waves), from HIP events around one launch of 512
-        # workgroups (2 waves per SIMD) at the 2.4 GHz shader clock.
-        iters, nblocks = 4000, 512
-        sink = torch.empty(2 * nblocks * 256, dtype=torch.float32, device=dev)
-        names = {1: "MFMAs only", 2: "FMAs only", 3: "both, in every wave", 4: "both, MFMA waves and FMA waves"}
-        for mode in (1, 2, 3, 4):
-            ms = event_time_batch(torch, lambda i: G.probe_mfma_valu(mode, iters, nblocks, sink=sink), 3)
-            emit({"suite": name, "mode": mode, "work": names[mode], "us": round(ms * 1e3, 3),
-                  "simd_cycles_per_substep": round(ms * 1e-3 * 2.4e9 / (iters * 4), 1)})
+        # it), from the overlap probe (probes/probe.hip): one 512-thread
+        # workgroup per CU, so two waves per SIMD; SIMD cycles per substep from
+        # HIP events around one launch, at the 2.4 GHz shader clock.  Modes 3-6
+        # give every SIMD the same work per substep (two
+        # v_mfma_f32_32x32x16_f16 and 32 wave64 FMAs); modes 4 and 6 split it
+        # into MFMA waves (0-3) and FMA waves (4-7).  "mixed_simds" is the
+        # share of SIMDs that held one wave of each half, from the waves' HW_ID.
+        import numpy as np
+        from ggml_hip import probes as P
+        iters, nblocks = 4000, 256
+        sink = torch.empty(2 * nblocks * P.OV_THREADS, dtype=torch.float32, device=dev)
+        hwid = torch.empty(nblocks * P.OV_THREADS // 64, dtype=torch.int32, device=dev)
+        for mode in sorted(P.OV_MODES):
+            ms = event_time_batch(torch, lambda i: P.mfma_valu(mode, iters, nblocks, sink=sink, hwid=hwid), 3)
+            ids = hwid.cpu().numpy().astype(np.int64).reshape(nblocks, P.OV_THREADS // 64)
+            simd = (ids >> 4) & 3
+            mixed = np.mean([len(set(simd[b, :4]) & set(simd[b, 4:])) / 4.0 for b in range(nblocks)])
+            emit({"suite": name, "mode": mode, "work": P.OV_MODES[mode], "us": round(ms * 1e3, 3),
+                  "simd_cycles_per_substep": round(ms * 1e-3 * 2.4e9 / (iters * 4), 1),
+                  "mixed_simds": round(float(mixed), 3)})
     else:
         raise SystemExit(f"unknown suite {name}")
 

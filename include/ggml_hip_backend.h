@@ -10,8 +10,15 @@
  * vtables of ggml_hip_ggml_abi.h.
  *
  * Scope: the device runs MUL_MAT and MUL_MAT_ID with Q4_K / Q6_K / Q8_0
- * weights, f32 activations and f32 results; supports_op answers false for
- * every other op, so ggml_backend_sched keeps those on the CPU.
+ * weights (and Q5_K / Q4_0 / IQ4_XS), f32 activations and f32 results.  By
+ * default supports_op answers false for every other op, so
+ * ggml_backend_sched keeps those on the CPU.  With GGML_HIP_FUSION=1 in the
+ * environment (read once) it also takes f32 GLU (REGLU, GEGLU, SWIGLU,
+ * SWIGLU_OAI, SWIGLU_CLAMP), same-shape f32 ADD and ADD_ID, so that the
+ * FFN's gate / up / GLU (and bias) run stays in one split and
+ * graph_compute fuses it as the reference's CUDA backend does
+ * (cuda/fusion.zig, cuda/mulmat.zig:355-410); GGML_HIP_DISABLE_FUSION=1
+ * turns that off again.
  */
 #ifndef GGML_HIP_BACKEND_H
 #define GGML_HIP_BACKEND_H

@@ -251,12 +251,23 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
                       const void *y_ds, int64_t ncols, float *dst, int64_t dst_col_stride, void *stream);
 
 /*
- * Op-level MUL_MAT: quantizes x to Q8_1 into `workspace` and runs the GEMV
- * (ncols <= 8) or the int8-MFMA MMQ (ncols > 8).  One column, and 2-4 columns
- * of rows with K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
- * columns), skip the separate quantizer: the GEMV quantizes the columns in
- * its prologue.  Mirrors the dispatch in
- * ggml_cuda_mul_mat (src/ggml/cuda/mulmat.zig:576-639).
+ * Op-level MUL_MAT: quantizes x to Q8_1 into `workspace` and runs one of
+ * three kernels, as the dispatch in ggml_cuda_mul_mat picks between MMVQ, its
+ * few-row MMQ and MMQ (src/ggml/cuda/mulmat.zig:576-639):
+ *  - the GEMV for up to 8 columns.  One column, and 2-4 columns of rows with
+ *    K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
+ *    columns), skip the separate quantizer: the GEMV quantizes the columns in
+ *    its prologue;
+ *  - the few-column GEMM (16x16 int8 MFMA tiles) for 9-32 columns (9-16 for
+ *    Q6_K; Q8_0 / Q4_0 at 17-32 columns of 8 MiB of weights and more take the
+ *    tile), and also for 4-8 columns of large matrices, where it measured
+ *    faster than the GEMV (the shape rules are hip_qmm_mul_mat_workspace_size's:
+ *    e.g. Q4_K from 5 columns at K >= 8192 on >= 4096 rows, from 7 columns on
+ *    >= 6144 rows).  On those 4-8 column shapes the workspace grows by the
+ *    few-column kernel's split-K partials, and the results differ from
+ *    hip_qmm_mul_mat_vec's in fp32 rounding (another summation order; both
+ *    pass the f64 and CPU gates);
+ *  - the int8-MFMA MMQ tile for the rest.
  * x[c*x_col_stride + k] f32, dst[c*dst_col_stride + r] f32.
  */
 int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
@@ -415,24 +426,6 @@ int hip_qmm_mul_mat_id_glu(int type, const void *w, const void *w_gate, int64_t 
  */
 int hip_qmm_block_dots(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                        const int8_t *y_qs, int64_t ncols, int32_t *out, void *stream);
-
-/*
- * Measurement aid, no counterpart in the reference: a plain streaming read of
- * `bytes` (a multiple of 16, src 16-byte aligned) with the access shape that
- * reads HBM fastest here, the floor the decode GEMV's weight stream is
- * compared against.  The loaded words are XOR-folded into
- * hip_qmm_probe_sink_words(bytes) words of `sink` so the loads stay.
- */
-size_t hip_qmm_probe_sink_words(size_t bytes);
-int hip_qmm_probe_stream_read(const void *src, size_t bytes, uint32_t *sink, void *stream);
-
-/* Measurement aid, no counterpart in the reference: whether MFMA and VALU
- * work overlap on a SIMD.  mode 1: MFMAs only (4 independent chains of
- * v_mfma_f32_32x32x16_f16 per wave and step); 2: 16 fp32 FMAs per chain step
- * only; 3: both in every wave; 4: MFMAs in even waves, FMAs in odd waves.
- * nblocks workgroups of 256 threads (two per CU); sink holds 2 * nblocks * 256
- * floats: each thread's MFMA sums, then its FMA sums. */
-int hip_qmm_probe_mfma_valu(int mode, int iters, int nblocks, float *sink, void *stream);
 
 #ifdef __cplusplus
 }

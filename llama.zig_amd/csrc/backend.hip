@@ -639,13 +639,22 @@ bool run_add_id(BackendCtx *ctx, const ggml_tensor *node) {
 // A run fuses only when every node in it but the last is read only inside
 // the run and is not a graph output (ggml_can_fuse_subgraph_ext,
 // src/ggml/graph.zig:1207-1250), with use counts from the graph's hash set.
-// Graphs without use counts, and GGML_HIP_DISABLE_FUSION=1, run unfused.
+// Graphs without use counts run unfused.
+//
+// The fusion is opt-in: by default the device takes MUL_MAT / MUL_MAT_ID
+// and the no-op views only, and every other op (GLU, ADD, ADD_ID included)
+// stays on the CPU backend.  GGML_HIP_FUSION=1 lets the device take the GLU
+// and bias-add nodes as well, so the FFN's gate / up / GLU run stays in one
+// split and fuses; GGML_HIP_DISABLE_FUSION=1 (the reference's
+// GGML_CUDA_DISABLE_FUSION) turns it off again.  Both are read once.
+
+bool env_flag(const char *name) {
+    const char *e = std::getenv(name);
+    return e && *e && std::strcmp(e, "0") != 0;
+}
 
 bool fusion_disabled() {
-    static const bool off = [] {
-        const char *e = std::getenv("GGML_HIP_DISABLE_FUSION");
-        return e && *e && std::strcmp(e, "0") != 0;
-    }();
+    static const bool off = !env_flag("GGML_HIP_FUSION") || env_flag("GGML_HIP_DISABLE_FUSION");
     return off;
 }
 
@@ -682,6 +691,20 @@ bool run_is_closed(const ggml_cgraph *g, int i0, int n, const ggml_tensor *out) 
 bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
     const uintptr_t pa = (uintptr_t)a, pb = (uintptr_t)b;
     return pa < pb + nb && pb < pa + na;
+}
+
+// A fused launch writes its result while other workgroups still read the
+// weights, so the result must not land on the weights of either lane.  Under
+// op offload the weights are compute-buffer copies that the allocator may
+// hand to a later node once their own MUL_MAT is past; unfused, that reuse is
+// harmless, fused it is not, so the run then goes unfused.
+bool lands_on_weights(const void *out, size_t ob, const ggml_tensor *mm_a, const ggml_tensor *mm_b) {
+    for (const ggml_tensor *mm : {mm_a, mm_b}) {
+        if (!mm) continue;
+        const ggml_tensor *w = mm->src[0];
+        if (overlaps(out, ob, w->data, nbytes(w))) return true;
+    }
+    return false;
 }
 
 // A supported MUL_MAT the fused one-column entry point takes
@@ -745,6 +768,7 @@ bool launch_fused(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *gat
     if (overlaps(out->data, ob, x->data, (size_t)K * 4)) return false;
     if (ubias && overlaps(out->data, ob, ubias->data, ob)) return false;
     if (gbias && overlaps(out->data, ob, gbias->data, ob)) return false;
+    if (lands_on_weights(out->data, ob, up, gate)) return false;
     const int op = gate ? out->op_params[0] : 0;
     const float alpha = gate ? op_param_f32(out, 2) : 0.0f, limit = gate ? op_param_f32(out, 3) : 0.0f;
     const int rc = hip_qmm_mul_mat_vec_fused(w->type, w->data, gate ? gate->src[0]->data : nullptr, K, M,
@@ -785,7 +809,9 @@ bool launch_fused_id(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor *
     const ggml_tensor *w = up->src[0], *x = up->src[1], *ids = up->src[2];
     const int64_t K = w->ne[0], M = w->ne[1];
     const size_t ob = nbytes(out);
-    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids))) return false;
+    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids)) ||
+        lands_on_weights(out->data, ob, up, gate))
+        return false;
     const int rc = hip_qmm_mul_mat_id_vec_fused(
         w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
         static_cast<const float *>(x->data), x->ne[1], x->ne[2], (int64_t)(x->nb[1] / 4),
@@ -831,7 +857,8 @@ bool launch_fused_mmq(BackendCtx *ctx, const ggml_tensor *up, const ggml_tensor 
                       bool *ok) {
     const ggml_tensor *w = up->src[0], *x = up->src[1];
     const int64_t K = w->ne[0], M = w->ne[1], N = x->ne[1];
-    if (overlaps(out->data, nbytes(out), x->data, nbytes(x))) return false;
+    if (overlaps(out->data, nbytes(out), x->data, nbytes(x)) || lands_on_weights(out->data, nbytes(out), up, gate))
+        return false;
     void *ws = workspace(ctx, hip_qmm_mul_mat_glu_workspace_size(w->type, K, M, N));
     const int rc = hip_qmm_mul_mat_glu(w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1],
                                        static_cast<const float *>(x->data), N, (int64_t)(x->nb[1] / 4),
@@ -858,7 +885,9 @@ bool launch_fused_id_mmq(BackendCtx *ctx, const ggml_tensor *up, const ggml_tens
     const int64_t K = w->ne[0], M = w->ne[1], n_as = w->ne[2];
     const int64_t ne11 = x->ne[1], n_tokens = x->ne[2], n_ids = ids->ne[0];
     const size_t ob = nbytes(out);
-    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids))) return false;
+    if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids)) ||
+        lands_on_weights(out->data, ob, up, gate))
+        return false;
     void *ws = workspace(ctx, hip_qmm_mul_mat_id_workspace_size(w->type, K, n_as, ne11, n_tokens, n_ids));
     const int rc = hip_qmm_mul_mat_id_glu(
         w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], n_as,
@@ -960,7 +989,9 @@ bool launch_shared_expert(BackendCtx *ctx, const ggml_cgraph *g, int i, bool *ok
     const size_t ob = nbytes(routed), sb = nbytes(shared);
     if (overlaps(routed->data, ob, x->data, nbytes(x)) || overlaps(routed->data, ob, ids->data, nbytes(ids)) ||
         overlaps(shared->data, sb, x->data, nbytes(x)) || overlaps(shared->data, sb, ids->data, nbytes(ids)) ||
-        overlaps(routed->data, ob, shared->data, sb))
+        overlaps(routed->data, ob, shared->data, sb) || lands_on_weights(routed->data, ob, up, gate) ||
+        lands_on_weights(routed->data, ob, sup, sgate) || lands_on_weights(shared->data, sb, up, gate) ||
+        lands_on_weights(shared->data, sb, sup, sgate))
         return false;
     const int rc = hip_qmm_mul_mat_id_vec_fused_shared(
         w->type, w->data, gate->src[0]->data, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
@@ -1005,7 +1036,8 @@ bool launch_fused_id_bias(BackendCtx *ctx, const ggml_tensor *up, const ggml_ten
     if (gb && gb->nb[1] != ub->nb[1]) return false;  // one expert stride for both biases
     const size_t ob = nbytes(out);
     if (overlaps(out->data, ob, x->data, nbytes(x)) || overlaps(out->data, ob, ids->data, nbytes(ids)) ||
-        overlaps(out->data, ob, ub->data, nbytes(ub)) || (gb && overlaps(out->data, ob, gb->data, nbytes(gb))))
+        overlaps(out->data, ob, ub->data, nbytes(ub)) || (gb && overlaps(out->data, ob, gb->data, nbytes(gb))) ||
+        lands_on_weights(out->data, ob, up, gate))
         return false;
     const int rc = hip_qmm_mul_mat_id_vec_fused_bias(
         w->type, w->data, gate ? gate->src[0]->data : nullptr, K, M, (int64_t)w->nb[1], (int64_t)w->nb[2], w->ne[2],
@@ -1134,7 +1166,20 @@ ggml_status be_graph_compute(ggml_backend_t be, ggml_cgraph *g) {
 // up to follow it (it reads only the layer input and its weights, so the
 // order stays topological), and the routed input and ids are kept allocated
 // until the shared GLU has run, so the fused launch's operands cannot alias
-// its second output.  Nothing moves with fusion disabled.
+// its second output.  Then, as graph.zig:849-862 does, every gate / up / GLU
+// run the fused MMQ takes keeps its nodes and their sources (weights,
+// activations, ids) allocated until the GLU (addAllocDeps, graph.zig:753-770),
+// so the GLU's result cannot be placed on memory the fused kernel still
+// reads.  Nothing moves with fusion disabled.
+void add_alloc_deps(ggml_cgraph *g, ggml_backend_graph_optimize_params *params, int start, int last) {
+    for (int i = start; i < last; ++i) {
+        ggml_tensor *n = g->nodes[i];
+        params->add_alloc_dep(params->user_data, n, g->nodes[last]);
+        for (ggml_tensor *s : n->src)
+            if (s) params->add_alloc_dep(params->user_data, s, g->nodes[last]);
+    }
+}
+
 void be_graph_optimize(ggml_backend_t, ggml_cgraph *g, ggml_backend_graph_optimize_params *params) {
     if (fusion_disabled() || !g) return;
     for (int r = 0; r + 5 < g->n_nodes; ++r) {
@@ -1151,6 +1196,19 @@ void be_graph_optimize(ggml_backend_t, ggml_cgraph *g, ggml_backend_graph_optimi
             r += 5;
             break;
         }
+    }
+    if (!params || !params->add_alloc_dep) return;
+    for (int i = 0; i + 2 < g->n_nodes; ++i) {
+        const ggml_tensor *glu = g->nodes[i + 2], *n0 = g->nodes[i], *n1 = g->nodes[i + 1];
+        if (glu->op != GGML_OP_GLU || n0->op != n1->op) continue;
+        const ggml_tensor *gate = glu->src[0], *up = glu->src[1];
+        if (!((gate == n0 && up == n1) || (gate == n1 && up == n0))) continue;
+        const bool mmq = n0->op == GGML_OP_MUL_MAT     ? gate_up_mmq_fusable(up, gate, glu)
+                         : n0->op == GGML_OP_MUL_MAT_ID ? gate_up_id_mmq_fusable(up, gate, glu)
+                                                        : false;
+        if (!mmq) continue;
+        add_alloc_deps(g, params, i, i + 2);
+        i += 2;
     }
 }
 
@@ -1306,9 +1364,9 @@ extern "C" {
 bool ggml_backend_hip_op_supported(const ggml_tensor *op) {
     if (!op) return false;
     if (is_noop(op->op)) return true;
-    // With fusion off (GGML_HIP_DISABLE_FUSION) the GLU and bias-add nodes
-    // have no reason to stay on the device: the answer narrows to MUL_MAT /
-    // MUL_MAT_ID and the no-op views, and everything else stays on the CPU.
+    // Unless the fusion is on (GGML_HIP_FUSION=1) the GLU and bias-add nodes
+    // have no reason to be on the device: the answer is MUL_MAT / MUL_MAT_ID
+    // and the no-op views, and everything else stays on the CPU.
     if ((op->op == GGML_OP_GLU || op->op == GGML_OP_ADD || op->op == GGML_OP_ADD_ID) && fusion_disabled())
         return false;
     if (op->op == GGML_OP_GLU) {

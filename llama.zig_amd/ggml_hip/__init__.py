@@ -106,12 +106,6 @@ def lib():
         L.hip_qmm_mul_mat_vec_q.argtypes = [i32, vp, vp, vp, vp] + [i64] * 18 + [vp]
         L.hip_qmm_block_dots.restype = i32
         L.hip_qmm_block_dots.argtypes = [i32, vp, i64, i64, i64, vp, i64, vp, vp]
-        L.hip_qmm_probe_sink_words.restype = ctypes.c_size_t
-        L.hip_qmm_probe_sink_words.argtypes = [ctypes.c_size_t]
-        L.hip_qmm_probe_stream_read.restype = i32
-        L.hip_qmm_probe_stream_read.argtypes = [vp, ctypes.c_size_t, vp, vp]
-        L.hip_qmm_probe_mfma_valu.restype = i32
-        L.hip_qmm_probe_mfma_valu.argtypes = [i32, i32, i32, vp, vp]
         _lib = L
     return _lib
 
@@ -469,27 +463,6 @@ def mul_mat(qtype, w: torch.Tensor, x: torch.Tensor, out=None, workspace=None):
     _check(lib().hip_qmm_mul_mat(t, _ptr(w), K, nrows, rs, _ptr(x), n, x.stride(0), _ptr(out), out.stride(0),
                                  _ptr(workspace), workspace.numel(), _stream()), "hip_qmm_mul_mat")
     return out
-
-
-def probe_stream_read(buf: torch.Tensor, sink=None):
-    """Streaming read of a device buffer (the GEMV's memory floor probe);
-    returns the XOR-folded sink words."""
-    _require_cuda(buf)
-    nbytes = buf.numel() * buf.element_size()
-    words = int(lib().hip_qmm_probe_sink_words(nbytes))
-    if sink is None:
-        sink = torch.empty(max(words, 1), dtype=torch.int32, device=buf.device)
-    _check(lib().hip_qmm_probe_stream_read(_ptr(buf), nbytes, _ptr(sink), _stream()), "hip_qmm_probe_stream_read")
-    return sink
-
-
-def probe_mfma_valu(mode: int, iters: int, nblocks: int = 512, sink=None):
-    """MFMA / VALU overlap probe (mode 1 MFMAs, 2 FMAs, 3 both per wave, 4 split by wave);
-    returns the sink: [MFMA sums of every thread, FMA sums of every thread]."""
-    if sink is None:
-        sink = torch.empty(2 * nblocks * 256, dtype=torch.float32, device="cuda")
-    _check(lib().hip_qmm_probe_mfma_valu(mode, iters, nblocks, _ptr(sink), _stream()), "hip_qmm_probe_mfma_valu")
-    return sink
 
 
 def mul_mat_id(qtype, w: torch.Tensor, x: torch.Tensor, ids: torch.Tensor, out=None, workspace=None):

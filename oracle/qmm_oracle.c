@@ -16,9 +16,14 @@
  *   quantize_row_q4_K/q6_K/q8_0/q8_1/q8_K_ref, dequantize_* . pinned
  *   quantize_q4_K / q6_K (imatrix impls) ......... pinned (chunk_imatrix goldens)
  *   vec_dot q4_K/q6_K/q8_0 generic ............... pinned (cpu/quants/golden.zig)
- *   vec_dot AVX2 + quantize_row_q8_0 AVX2 ........ NOT golden-pinned (the tree
- *       holds no x86 goldens); checked against the pinned generic kernels
- *       (integers exact, floats within a few ulp) -- "parity unpinned" for bits.
+ *   vec_dot AVX2 + quantize_row_q8_0 AVX2 ........ the tree holds no x86
+ *       goldens: pinned by constructed cases on which the specification and
+ *       a plausible mistake differ (tie rule, 127/amax multiplier, lane
+ *       accumulation, hsum_float_8 order, min-lane fold, fused block scale;
+ *       tests/test_oracle_x86_pins.py), and held to the generic kernels.
+ *   v_expf / v_silu (SWIGLU's vector arm) ........ pinned to the routine's
+ *       published error bound, exact points, range limits and the row split
+ *       (tests/test_oracle_glu.py).
  *   mul_mat / mul_mat_id drivers .................. pinned by construction
  *       (each output is one vec_dot call) + thread-count invariance tests.
  *   block_dots_q8_1 / mul_mat_q8_1_f64 ........... GPU-semantics restatement;
@@ -1999,6 +2004,61 @@ static float glu_one(int op, float x, float g, float alpha, float limit) {
 
 void orc_glu_f32(int op, int64_t n, const float *gate, const float *up, float alpha, float limit, float *out) {
     for (int64_t i = 0; i < n; ++i) out[i] = glu_one(op, gate[i], up[i], alpha, limit);
+}
+
+/* ggml_v_expf, the AVX2 / NEON arm (src/ggml/cpu/vec.zig:537-588): ARM's
+ * optimised expf, maximum error 1.45358 + 0.5 ulp.  fma_f32(a, b, c) there is
+ * a + b * c fused and fms_f32(a, b, c) is a - b * c fused; every fusion is
+ * written as fmaf here in the same place.  The vector code takes a fast path
+ * when no lane has |n| > 126, giving k + j * k, which is also what its slow
+ * path gives a lane with |n| <= 126, so evaluating one lane at a time gives
+ * the vector's bits. */
+float orc_v_expf(float x) {
+    const float r = 0x1.8p23f;
+    const float z = fmaf(x, 0x1.715476p+0f, r);
+    const float n = z - r;
+    const float b = fmaf(-n, 0x1.7f7d1cp-20f, fmaf(-n, 0x1.62e4p-1f, x));
+    uint32_t zb, kb;
+    memcpy(&zb, &z, 4);
+    const uint32_t e = zb << 23;
+    kb = e + 0x3f800000u; /* bits of 1.0f */
+    float k;
+    memcpy(&k, &kb, 4);
+    const float u = b * b;
+    const float j = fmaf(fmaf(fmaf(0x1.0e4020p-7f, b, 0x1.573e2ep-5f), u, fmaf(0x1.555e66p-3f, b, 0x1.fffdb6p-2f)), u,
+                         0x1.ffffecp-1f * b);
+    if (!(fabsf(n) > 126.0f)) return fmaf(j, k, k);
+    const uint32_t d = n <= 0.0f ? 0x82000000u : 0u;
+    const uint32_t s1b = d + 0x7f000000u, s2b = e - d;
+    float s1, s2;
+    memcpy(&s1, &s1b, 4);
+    memcpy(&s2, &s2b, 4);
+    if (fabsf(n) > 192.0f) return s1 * s1;
+    return fmaf(s2, j, s2) * s1;
+}
+
+void orc_v_expf_n(int64_t n, const float *x, float *out) {
+    for (int64_t i = 0; i < n; ++i) out[i] = orc_v_expf(x[i]);
+}
+
+/* ggml_v_silu (vec.zig:592-599): x / (1 + v_expf(0 - x)). */
+float orc_v_silu(float x) { return x / (1.0f + orc_v_expf(0.0f - x)); }
+
+/* The CPU GLU op over nrows contiguous rows of nc (gluRows,
+ * cpu/ops/activation.zig:379-447).  SWIGLU calls ggml_vec_swiglu_f32
+ * (vec.zig:653-665) per row: on an AVX2 host 8-lane steps of
+ * v_silu(x) * g, then the scalar (x / (1 + expf(-x))) * g for the last
+ * nc % 8.  The other ops are elementwise (glu_one). */
+void orc_glu_f32_rows(int op, int64_t nrows, int64_t nc, const float *gate, const float *up, float alpha, float limit,
+                      float *out) {
+    for (int64_t r = 0; r < nrows; ++r) {
+        const float *x = gate + r * nc, *g = up + r * nc;
+        float *y = out + r * nc;
+        int64_t i = 0;
+        if (op == ORC_GLU_SWIGLU)
+            for (const int64_t nv = nc - nc % 8; i < nv; ++i) y[i] = orc_v_silu(x[i]) * g[i];
+        for (; i < nc; ++i) y[i] = glu_one(op, x[i], g[i], alpha, limit);
+    }
 }
 
 static uint64_t splitmix64(uint64_t *s) {

@@ -131,6 +131,14 @@ float orc_gelu_f32(float x);
 /* ggml_compute_forward_glu, split form, one row of n:
  * out[i] = glu(gate[i], up[i]); alpha / limit are op params 2 / 3. */
 void orc_glu_f32(int op, int64_t n, const float *gate, const float *up, float alpha, float limit, float *out);
+/* The op over nrows contiguous rows of nc, with SWIGLU's 8-lane vector arm
+ * (ggml_vec_swiglu_f32 on an AVX2 host) and its scalar tail. */
+void orc_glu_f32_rows(int op, int64_t nrows, int64_t nc, const float *gate, const float *up, float alpha, float limit,
+                      float *out);
+/* ggml_v_expf and ggml_v_silu, one lane. */
+float orc_v_expf(float x);
+void orc_v_expf_n(int64_t n, const float *x, float *out);
+float orc_v_silu(float x);
 
 /* synthetic inputs: SplitMix64 -> Box-Muller (double) -> f32 */
 void orc_fill_normal(uint64_t seed, int64_t n, float mean, float stddev, float *out);

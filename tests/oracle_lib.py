@@ -85,6 +85,14 @@ def lib():
         L.orc_gelu_f32.argtypes = [ctypes.c_float]
         L.orc_glu_f32.restype = None
         L.orc_glu_f32.argtypes = [ctypes.c_int, i64, f32p, f32p, ctypes.c_float, ctypes.c_float, f32p]
+        L.orc_glu_f32_rows.restype = None
+        L.orc_glu_f32_rows.argtypes = [ctypes.c_int, i64, i64, f32p, f32p, ctypes.c_float, ctypes.c_float, f32p]
+        L.orc_v_expf.restype = ctypes.c_float
+        L.orc_v_expf.argtypes = [ctypes.c_float]
+        L.orc_v_silu.restype = ctypes.c_float
+        L.orc_v_silu.argtypes = [ctypes.c_float]
+        L.orc_v_expf_n.restype = None
+        L.orc_v_expf_n.argtypes = [i64, f32p, f32p]
         _lib = L
     return _lib
 
@@ -243,12 +251,32 @@ def gelu_f32(x):
 
 
 def glu(op, gate, up, alpha=0.0, limit=0.0):
-    """The CPU GLU op, split form: out = glu(gate, up), elementwise."""
+    """The CPU GLU op, split form: out = glu(gate, up) over rows of the last
+    dimension, as an AVX2 host runs it (SWIGLU's 8-lane vector arm and
+    scalar tail per row)."""
     gate = np.ascontiguousarray(gate, dtype=np.float32)
     up = np.ascontiguousarray(up, dtype=np.float32)
     assert gate.shape == up.shape
     out = np.empty_like(gate)
+    nc = gate.shape[-1] if gate.ndim else 1
+    lib().orc_glu_f32_rows(op, gate.size // max(nc, 1), nc, _p(gate), _p(up), alpha, limit, _p(out))
+    return out
+
+
+def glu_elementwise(op, gate, up, alpha=0.0, limit=0.0):
+    """Every element by the scalar formula (the row tail's)."""
+    gate = np.ascontiguousarray(gate, dtype=np.float32)
+    up = np.ascontiguousarray(up, dtype=np.float32)
+    out = np.empty_like(gate)
     lib().orc_glu_f32(op, gate.size, _p(gate), _p(up), alpha, limit, _p(out))
+    return out
+
+
+def v_expf(x):
+    """ggml_v_expf (the vector arm's exp) elementwise."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().orc_v_expf_n(x.size, _p(x), _p(out))
     return out
 
 

@@ -220,11 +220,14 @@ def test_fused_and_elementwise_entry_points_reject_bad_arguments(L):
     assert L.hip_qmm_add_f32(8, 0, x, 8, x, 8, d, 8, None) == 0
 
 
-def test_fusion_off_narrows_supports_op_to_mul_mat():
-    """With GGML_HIP_DISABLE_FUSION=1 the device keeps only MUL_MAT /
-    MUL_MAT_ID and the no-op views: GLU, ADD and ADD_ID go back to the CPU, which is
-    the strict boundary of the quantized-matmul path.  Runs in a fresh
-    process, since the library reads the variable once."""
+@pytest.mark.parametrize("env_extra", [{}, {"GGML_HIP_FUSION": "0"},
+                                 {"GGML_HIP_FUSION": "1", "GGML_HIP_DISABLE_FUSION": "1"}],
+                         ids=["default", "fusion_0", "fusion_disabled"])
+def test_default_supports_op_is_mul_mat_only(env_extra):
+    """By default (and with the fusion turned off) the device keeps only
+    MUL_MAT / MUL_MAT_ID and the no-op views: GLU, ADD and ADD_ID stay on the
+    CPU, the strict boundary of the quantized-matmul path.  Runs in a fresh
+    process, since the library reads the variables once."""
     import os
     import subprocess
     import sys
@@ -247,7 +250,8 @@ assert ok(T.mmid(abi.GGML_TYPE_Q6_K, 2048, 768, 128, 8, 512)[3])
 assert ok(abi.make_tensor(abi.GGML_TYPE_F32, [8, 8], op=abi.GGML_OP_VIEW))
 print("strict ok")
 '''
-    env = dict(os.environ, GGML_HIP_DISABLE_FUSION="1")
+    env = {k: v for k, v in os.environ.items() if k not in ("GGML_HIP_FUSION", "GGML_HIP_DISABLE_FUSION")}
+    env.update(env_extra)
     r = subprocess.run([sys.executable, "-c", code, str(ROOT / "llama.zig_amd"), str(ROOT / "tests")], env=env,
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 0 and "strict ok" in r.stdout, r.stderr[-2000:]

@@ -294,3 +294,105 @@ def test_plugin_fuses_prefill_moe_gate_up_glu(hb):
     assert hb.compute([g, u, glu], use_counts=False) == abi.GGML_STATUS_SUCCESS
     assert not np.isnan(hb.get(g, np.float32, (T * k, M))).any()
     np.testing.assert_array_equal(hb.get(glu, np.float32, (T, k, M)), got)
+
+
+def _deps_want(C, nodes, last):
+    """addAllocDeps (src/ggml/cuda/graph.zig:753-770): each node before `last`
+    and each of its sources, kept allocated until `last`."""
+    want = set()
+    for n in nodes:
+        want.add((C.addressof(n), C.addressof(last)))
+        for s in n.src:
+            if s:
+                want.add((C.cast(s, C.c_void_p).value, C.addressof(last)))
+    return want
+
+
+def test_plugin_graph_optimize_keeps_fused_mmq_inputs_alive(hb):
+    """graph_optimize keeps the nodes and sources (weights, activations, ids)
+    of every gate / up / GLU run the fused MMQ takes allocated until the GLU
+    (src/ggml/cuda/graph.zig:849-862), dense at 64 columns and grouped at 64
+    tokens; a one-column run (the fused GEMV) gets none, as in the reference."""
+    from ggml_hip import abi
+    M, K, T, n_as, k = 512, 2048, 64, 8, 2
+    q4 = abi.GGML_TYPE_Q4_K
+    wu, wgt = abi.make_tensor(q4, [K, M], name=b"up_w"), abi.make_tensor(q4, [K, M], name=b"gate_w")
+    x = abi.make_tensor(abi.GGML_TYPE_F32, [K, T], name=b"x")
+    g = abi.make_tensor(abi.GGML_TYPE_F32, [M, T], op=abi.GGML_OP_MUL_MAT, srcs=(wgt, x), name=b"g")
+    u = abi.make_tensor(abi.GGML_TYPE_F32, [M, T], op=abi.GGML_OP_MUL_MAT, srcs=(wu, x), name=b"u")
+    glu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g, u, [M, T])
+    order, deps = hb.optimized([g, u, glu])
+    assert [C.addressof(n) for n in order] == [C.addressof(n) for n in (g, u, glu)]
+    assert set(deps) == _deps_want(C, (g, u), glu)
+
+    ewu, ewg = abi.make_tensor(q4, [K, M, n_as], name=b"up_exps"), abi.make_tensor(q4, [K, M, n_as], name=b"gate_exps")
+    ex = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1, T], name=b"x")
+    idt = abi.make_tensor(abi.GGML_TYPE_I32, [k, T], name=b"ids")
+    eg = abi.make_tensor(abi.GGML_TYPE_F32, [M, k, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(ewg, ex, idt), name=b"g")
+    eu = abi.make_tensor(abi.GGML_TYPE_F32, [M, k, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(ewu, ex, idt), name=b"u")
+    eglu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, eg, eu, [M, k, T])
+    _, edeps = hb.optimized([eu, eg, eglu])  # up first: either order pairs
+    assert set(edeps) == _deps_want(C, (eu, eg), eglu)
+
+    x1 = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1], name=b"x1")
+    g1 = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(wgt, x1), name=b"g1")
+    u1 = abi.make_tensor(abi.GGML_TYPE_F32, [M, 1], op=abi.GGML_OP_MUL_MAT, srcs=(wu, x1), name=b"u1")
+    glu1 = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g1, u1, [M, 1])
+    assert hb.optimized([g1, u1, glu1])[1] == []
+
+
+def test_plugin_fused_mmq_result_on_gate_weights_runs_unfused(hb):
+    """Under op offload the weights are compute-buffer copies, and without
+    the allocation dependencies the GLU's result could be placed on the gate
+    weights once their MUL_MAT is past.  The fused kernel would then write
+    tiles while other tiles still read those weights; the backend instead runs
+    the three nodes unfused (g and u are written), and the result is the
+    fused op's up to the split sums' rounding.  Dense at 64 columns and the
+    grouped form at 64 tokens."""
+    import ggml_hip as G
+    from ggml_hip import abi
+    M, K, T = 512, 2048, 64
+    q4 = abi.GGML_TYPE_Q4_K
+    wq, wgq = weights_q(O.TYPE_Q4_K, M, K, 0), weights_q(O.TYPE_Q4_K, M, K, 1)
+    wu, wgt = abi.make_tensor(q4, [K, M], name=b"up_w"), abi.make_tensor(q4, [K, M], name=b"gate_w")
+    x = abi.make_tensor(abi.GGML_TYPE_F32, [K, T], name=b"x")
+    g = abi.make_tensor(abi.GGML_TYPE_F32, [M, T], op=abi.GGML_OP_MUL_MAT, srcs=(wgt, x), name=b"g")
+    u = abi.make_tensor(abi.GGML_TYPE_F32, [M, T], op=abi.GGML_OP_MUL_MAT, srcs=(wu, x), name=b"u")
+    glu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, g, u, [M, T])
+    hb.alloc([wu, wgt, x, g, u], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    glu.data, glu.buffer = wgt.data, wgt.buffer  # the result placed on the gate weights' copy
+    hb.set(wu, wq)
+    hb.set(wgt, wgq)
+    xv = acts(T, K)
+    hb.set(x, xv)
+    for n in (g, u):
+        hb.set(n, np.full(M * T, np.nan, dtype=np.float32))
+    assert hb.compute([g, u, glu]) == abi.GGML_STATUS_SUCCESS
+    assert not np.isnan(hb.get(g, np.float32, (T, M))).any() and not np.isnan(hb.get(u, np.float32, (T, M))).any()
+    got = hb.get(glu, np.float32, (T, M))
+    want = G.mul_mat_glu("Q4_K", _dev(wq), _dev(wgq), _dev(xv)).cpu().numpy()
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+    n_as, k = 8, 2
+    ewq, ewgq = _experts(O.TYPE_Q4_K, n_as, M, K, 0), _experts(O.TYPE_Q4_K, n_as, M, K, 1)
+    ids, _ = route_top_k(T, n_as, k)
+    ewu, ewg = abi.make_tensor(q4, [K, M, n_as], name=b"up_exps"), abi.make_tensor(q4, [K, M, n_as], name=b"gate_exps")
+    ex = abi.make_tensor(abi.GGML_TYPE_F32, [K, 1, T], name=b"x")
+    idt = abi.make_tensor(abi.GGML_TYPE_I32, [k, T], name=b"ids")
+    eg = abi.make_tensor(abi.GGML_TYPE_F32, [M, k, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(ewg, ex, idt), name=b"g")
+    eu = abi.make_tensor(abi.GGML_TYPE_F32, [M, k, T], op=abi.GGML_OP_MUL_MAT_ID, srcs=(ewu, ex, idt), name=b"u")
+    eglu = abi.make_glu(abi.GGML_GLU_OP_SWIGLU, eg, eu, [M, k, T])
+    hb.alloc([ewu, ewg, ex, idt, eg, eu], usage=abi.GGML_BACKEND_BUFFER_USAGE_COMPUTE)
+    eglu.data, eglu.buffer = ewg.data, ewg.buffer
+    hb.set(ewu, ewq)
+    hb.set(ewg, ewgq)
+    exv = np.array(acts(T, K))
+    hb.set(ex, exv)
+    hb.set(idt, ids)
+    for n in (eg, eu):
+        hb.set(n, np.full(M * k * T, np.nan, dtype=np.float32))
+    assert hb.compute([eg, eu, eglu]) == abi.GGML_STATUS_SUCCESS
+    assert not np.isnan(hb.get(eg, np.float32, (T * k, M))).any()
+    got = hb.get(eglu, np.float32, (T, k, M))
+    want = G.mul_mat_id_glu("Q4_K", _dev(ewq), _dev(ewgq), _dev(exv.reshape(T, 1, K)), _dev(ids)).cpu().numpy()
+    np.testing.assert_array_equal(got, want)

@@ -124,3 +124,79 @@ def test_nan_passes_through_min_and_clamp():
     for op in (O.GLU_SWIGLU_OAI, O.GLU_SWIGLU_CLAMP):
         assert np.isnan(O.glu(op, np.float32([nan]), np.float32([1.0]), 1.702, 7.0)[0])
         assert np.isnan(O.glu(op, np.float32([1.0]), np.float32([nan]), 1.702, 7.0)[0])
+
+
+# ---------------------------------------------------------------- SWIGLU's vector arm
+#
+# On an x86 AVX2 host ggml_vec_swiglu_f32 runs 8-lane steps of
+# ggml_v_silu(x) * g, whose exp is ARM's optimised expf routine
+# (src/ggml/cpu/vec.zig:537-599; upstream records its maximum error as
+# 1.45358 + 0.5 ulp), and the scalar x / (1 + expf(-x)) * g for the last
+# nc % 8 of each row.  The reference holds no golden for either.  The
+# restatement (orc_v_expf) is pinned to the routine's published error bound
+# over its whole range, to its exact points and to its range limits, so a
+# dropped or misplaced polynomial term, a wrong constant or a broken range
+# reduction fails; and the row split is pinned by inputs on which the two
+# arms differ.
+
+def _ulp_err(got, x):
+    exact = np.exp(x.astype(np.float64))
+    spacing = np.spacing(np.abs(exact).astype(np.float32)).astype(np.float64)
+    return np.abs(got.astype(np.float64) - exact) / spacing
+
+
+def test_v_expf_within_the_routines_error_bound():
+    rng = np.random.default_rng(5)
+    x = np.concatenate([rng.uniform(-87.3, 88.7, 400_000), rng.uniform(-1, 1, 200_000),
+                        np.arange(-2000, 2000) * np.float32(np.log(2) / 16)]).astype(np.float32)
+    got = O.v_expf(x)
+    assert np.max(_ulp_err(got, x)) <= 1.45358 + 0.5
+    # and it is not libm's expf (the scalar arm): the two differ on some inputs
+    ref = np.array([math.exp(v) for v in x[:2000].astype(np.float64)], np.float32)
+    assert np.any(got[:2000] != ref)
+
+
+def test_v_expf_exact_points_and_range_limits():
+    assert O.v_expf(np.array([0.0, -0.0], np.float32)).tolist() == [1.0, 1.0]
+    for n in range(-20, 21):  # exp(n ln2) = 2^n within the bound
+        x = np.float32(n * math.log(2))
+        assert _ulp_err(O.v_expf(np.array([x])), np.array([x]))[0] <= 2.0
+    # past the overflow threshold: +inf; far below the subnormals: 0
+    big = O.v_expf(np.array([88.73, 89.0, 100.0, 200.0, 1e30], np.float32))
+    assert np.all(np.isinf(big)) and np.all(big > 0)
+    assert np.all(O.v_expf(np.array([-104.0, -150.0, -1e30], np.float32)) == 0.0)
+    # the slow path (|n| > 126) into the subnormals: within a subnormal step
+    # plus the relative bound
+    x = np.linspace(-103.9, -87.4, 20001).astype(np.float32)
+    got = O.v_expf(x).astype(np.float64)
+    exact = np.exp(x.astype(np.float64))
+    assert np.all(np.abs(got - exact) <= 2.0 ** -149 + 2.5e-7 * exact)
+    # near the top of the range (|n| up to 128): finite and within the bound
+    x = np.linspace(87.0, 88.72, 20001).astype(np.float32)
+    got = O.v_expf(x)
+    assert np.all(np.isfinite(got)) and np.max(_ulp_err(got, x)) <= 1.45358 + 0.5
+
+
+def test_swiglu_rows_take_the_vector_arm_then_the_scalar_tail():
+    """Per row of nc: the first nc - nc % 8 elements are v_silu(x) * g, the
+    rest the scalar formula.  The inputs are chosen where v_expf and libm's
+    expf round differently, so the split is visible."""
+    rng = np.random.default_rng(9)
+    cand = (rng.standard_normal(20000) * 4).astype(np.float32)
+    differ = cand[O.v_expf(-cand) != np.array([np.float32(math.exp(-float(v))) for v in cand], np.float32)]
+    vs = np.array([O.lib().orc_v_silu(float(v)) for v in differ], np.float32)
+    sc = np.array([np.float32(v) / (np.float32(1.0) + np.float32(math.exp(-float(v)))) for v in differ], np.float32)
+    differ = differ[vs != sc]
+    assert differ.size >= 64
+    for nc in (8, 13, 21, 3):
+        rows = 3
+        x = differ[:rows * nc].reshape(rows, nc)
+        g = np.ones_like(x)
+        got = O.glu(O.GLU_SWIGLU, x, g)
+        scalar = O.glu_elementwise(O.GLU_SWIGLU, x, g)
+        vec = nc - nc % 8
+        np.testing.assert_array_equal(got[:, vec:], scalar[:, vec:])
+        want_vec = np.array([[O.lib().orc_v_silu(float(v)) for v in row[:vec]] for row in x], np.float32)
+        np.testing.assert_array_equal(got[:, :vec], want_vec.reshape(rows, vec))
+        if vec:
+            assert np.all(got[:, :vec] != scalar[:, :vec])

@@ -66,3 +66,47 @@ def test_noalloc_rejects_a_workspace_beyond_the_array():
     assert e == 1
     torch.cuda.synchronize()
     assert float(out.abs().sum()) == 0.0
+
+
+def test_noalloc_under_graph_capture():
+    """The callers the entry point is for capture it: after one eager call
+    (which looks up the scratch array's address), two calls of different
+    shapes (the few-column GEMM with split-K partials in the scratch, then
+    the quantizer + GEMV) are captured into one HIP graph.  Every replay,
+    with eager work and synchronizations between replays, equals
+    hip_qmm_mul_mat bit for bit."""
+    G, L = _lib()
+    cases = [("Q4_K", 4096, 4096, 24), ("Q8_0", 1024, 4096, 3)]
+    ins, wants, outs = [], [], []
+    for tname, nrows, K, T in cases:
+        t = O.TYPE_IDS[tname]
+        w_d = torch.from_numpy(np.array(weights_q(t, nrows, K))).cuda()
+        x_d = torch.from_numpy(np.array(acts(T, K))).cuda()
+        ins.append((t, w_d, x_d, nrows, K, T))
+        wants.append(G.mul_mat(tname, w_d, x_d).cpu().numpy())
+        outs.append(torch.full((T, nrows), float("nan"), device="cuda"))
+
+    def call(i):
+        t, w_d, x_d, nrows, K, T = ins[i]
+        return L.hip_qmm_mul_mat_noalloc(t, G._ptr(w_d), K, nrows, w_d.stride(0), G._ptr(x_d), T, K,
+                                         G._ptr(outs[i]), nrows, G._stream())
+
+    assert call(0) == 0  # eager first call on the device
+    torch.cuda.synchronize()
+    cs = torch.cuda.Stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(cs):
+        with torch.cuda.graph(g, stream=cs):
+            assert call(0) == 0 and call(1) == 0
+    torch.cuda.current_stream().wait_stream(cs)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        G.mul_mat("Q4_K", ins[0][1], ins[0][2])  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, want in zip(outs, wants):
+            np.testing.assert_array_equal(o.cpu().numpy(), want, err_msg=f"replay {rep}")
