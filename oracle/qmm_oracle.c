@@ -1407,6 +1407,140 @@ AVX2_FN static float vec_dot_q8_0_q8_0_avx2(int n, const void *vx, const void *v
     return hsum_float_8(acc);
 }
 
+/* mul_sum_i8_pairs_float (x86/common.zig:120-150, non-VNNI arm): lane i is
+ * the exact sum of the products 4i..4i+3, as a float. */
+AVX2_FN static inline __m256 mul_sum_i8_pairs_float(__m256i x, __m256i y) {
+    const __m256i ax = _mm256_sign_epi8(x, x);
+    const __m256i sy = _mm256_sign_epi8(y, x);
+    return _mm256_cvtepi32_ps(_mm256_madd_epi16(_mm256_set1_epi16(1), _mm256_maddubs_epi16(ax, sy)));
+}
+
+/* bytes_from_nibbles_32 (x86/common.zig:111-116): 16 bytes to 32 nibbles, low first. */
+AVX2_FN static inline __m256i bytes_from_nibbles_32(const uint8_t *rsi) {
+    const __m128i tmp = _mm_loadu_si128((const __m128i *)rsi);
+    return _mm256_and_si256(_mm256_set1_epi8(0xF), _mm256_set_m128i(_mm_srli_epi16(tmp, 4), tmp));
+}
+
+/* ggml_vec_dot_q4_0_q8_0 AVX2 arm, x86/legacy.zig:189-226: nibbles - 8,
+ * the q8_0 arm's lane sums, one fused multiply-add per block, hsum_float_8. */
+AVX2_FN static float vec_dot_q4_0_q8_0_avx2(int n, const void *vx, const void *vy) {
+    const blk_q4_0 *x = (const blk_q4_0 *)vx;
+    const blk_q8_0 *y = (const blk_q8_0 *)vy;
+    const int nb = n / QK8_0;
+    __m256 acc = _mm256_setzero_ps();
+    for (int ib = 0; ib < nb; ++ib) {
+        const __m256 d = _mm256_set1_ps(F32(x[ib].d) * F32(y[ib].d));
+        const __m256i qx = _mm256_sub_epi8(bytes_from_nibbles_32(x[ib].qs), _mm256_set1_epi8(8));
+        const __m256i qy = _mm256_loadu_si256((const __m256i *)y[ib].qs);
+        acc = _mm256_fmadd_ps(d, mul_sum_i8_pairs_float(qx, qy), acc);
+    }
+    return hsum_float_8(acc);
+}
+
+/* ggml_vec_dot_q5_K_q8_K AVX2 arm, x86/k.zig:355-451: q4_K's lanes with the
+ * fifth bit added from qh one bit plane per 32 weights; the mins fold to a
+ * scalar per super-block (hadd twice) and accumulate as summs = fma(dmin,
+ * hsum, summs), added after hsum_float_8 of the lanes. */
+AVX2_FN static float vec_dot_q5_K_q8_K_avx2(int n, const void *vx, const void *vy) {
+    const blk_q5_K *x = (const blk_q5_K *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m256i m4 = _mm256_set1_epi8(0xF);
+    const __m128i mzero = _mm_setzero_si128();
+    const __m256i mone = _mm256_set1_epi8(1);
+    __m256 acc = _mm256_setzero_ps();
+    float summs = 0.0f;
+    for (int i = 0; i < nb; ++i) {
+        const uint8_t *q5 = x[i].qs;
+        const int8_t *q8 = y[i].qs;
+        const float d = y[i].d * F32(x[i].d);
+        const float dmin = -y[i].d * F32(x[i].dmin);
+        uint32_t utmp[4];
+        unpack_scales_k4(x[i].scales, utmp);
+        const __m256i mins_and_scales = _mm256_cvtepu8_epi16(
+            _mm_set_epi32((int)utmp[3], (int)utmp[2], (int)utmp[1], (int)utmp[0]));
+        const __m256i q8sums = _mm256_loadu_si256((const __m256i *)y[i].bsums);
+        const __m128i q8s = _mm_hadd_epi16(_mm256_extracti128_si256(q8sums, 0), _mm256_extracti128_si256(q8sums, 1));
+        const __m128i prod = _mm_madd_epi16(_mm256_extracti128_si256(mins_and_scales, 1), q8s);
+        const __m128i hsum = _mm_hadd_epi32(_mm_hadd_epi32(prod, mzero), mzero);
+        summs = fmaf(dmin, (float)_mm_extract_epi32(hsum, 0), summs);
+        const __m128i sc128 = _mm256_extracti128_si256(mins_and_scales, 0);
+        const __m256i scales = _mm256_set_m128i(sc128, sc128);
+        const __m256i hbits = _mm256_loadu_si256((const __m256i *)x[i].qh);
+        __m256i hmask = mone;
+        __m256i sumi = _mm256_setzero_si256();
+        int bit = 0;
+        for (int j = 0; j < QK_K / 64; ++j) {
+            const __m256i scale_0 = _mm256_shuffle_epi8(scales, scale_shuffle_k4(2 * j + 0));
+            const __m256i scale_1 = _mm256_shuffle_epi8(scales, scale_shuffle_k4(2 * j + 1));
+            const __m256i q5bits = _mm256_loadu_si256((const __m256i *)q5); q5 += 32;
+            const __m256i q5l_0 = _mm256_and_si256(q5bits, m4);
+            const __m256i q5h_0 = _mm256_slli_epi16(
+                _mm256_srl_epi16(_mm256_and_si256(hbits, hmask), _mm_cvtsi32_si128(bit)), 4);
+            ++bit;
+            const __m256i q5_0 = _mm256_add_epi8(q5l_0, q5h_0);
+            hmask = _mm256_slli_epi16(hmask, 1);
+            const __m256i q5l_1 = _mm256_and_si256(_mm256_srli_epi16(q5bits, 4), m4);
+            const __m256i q5h_1 = _mm256_slli_epi16(
+                _mm256_srl_epi16(_mm256_and_si256(hbits, hmask), _mm_cvtsi32_si128(bit)), 4);
+            ++bit;
+            const __m256i q5_1 = _mm256_add_epi8(q5l_1, q5h_1);
+            hmask = _mm256_slli_epi16(hmask, 1);
+            const __m256i q8_0 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q8_1 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            __m256i p16_0 = _mm256_maddubs_epi16(q5_0, q8_0);
+            __m256i p16_1 = _mm256_maddubs_epi16(q5_1, q8_1);
+            p16_0 = _mm256_madd_epi16(scale_0, p16_0);
+            p16_1 = _mm256_madd_epi16(scale_1, p16_1);
+            sumi = _mm256_add_epi32(sumi, _mm256_add_epi32(p16_0, p16_1));
+        }
+        acc = _mm256_fmadd_ps(_mm256_set1_ps(d), _mm256_cvtepi32_ps(sumi), acc);
+    }
+    return hsum_float_8(acc) + summs;
+}
+
+/* ggml_vec_dot_iq4_xs_q8_K AVX2 arm, x86/iq.zig:731-790: the codebook by
+ * pshufb, 32 weights per madd with the group scale ls - 32; two lane
+ * accumulators per super-block (even and odd groups) added before the one
+ * fused multiply-add with f32(d) * y.d. */
+AVX2_FN static float vec_dot_iq4_xs_q8_K_avx2(int n, const void *vx, const void *vy) {
+    const blk_iq4_xs *x = (const blk_iq4_xs *)vx;
+    const blk_q8_K *y = (const blk_q8_K *)vy;
+    const int nb = n / QK_K;
+    const __m128i values128 = _mm_loadu_si128((const __m128i *)KV_IQ4NL);
+    const __m128i m4b = _mm_set1_epi8(0x0f);
+    __m256 accum = _mm256_setzero_ps();
+    for (int ibl = 0; ibl < nb; ++ibl) {
+        const uint8_t *qs = x[ibl].qs;
+        const int8_t *q8 = y[ibl].qs;
+        uint16_t sh = x[ibl].scales_h;
+        __m256i sumi1 = _mm256_setzero_si256(), sumi2 = _mm256_setzero_si256();
+        for (int ib = 0; ib < QK_K / 32; ib += 2) {
+            const __m128i q4bits_1 = _mm_loadu_si128((const __m128i *)qs); qs += 16;
+            const __m128i q4bits_2 = _mm_loadu_si128((const __m128i *)qs); qs += 16;
+            const __m256i q8b_1 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q8b_2 = _mm256_loadu_si256((const __m256i *)q8); q8 += 32;
+            const __m256i q4b_1 = _mm256_set_m128i(
+                _mm_shuffle_epi8(values128, _mm_and_si128(_mm_srli_epi16(q4bits_1, 4), m4b)),
+                _mm_shuffle_epi8(values128, _mm_and_si128(q4bits_1, m4b)));
+            const __m256i q4b_2 = _mm256_set_m128i(
+                _mm_shuffle_epi8(values128, _mm_and_si128(_mm_srli_epi16(q4bits_2, 4), m4b)),
+                _mm_shuffle_epi8(values128, _mm_and_si128(q4bits_2, m4b)));
+            const __m256i p16_1 = _mm256_maddubs_epi16(_mm256_sign_epi8(q4b_1, q4b_1), _mm256_sign_epi8(q8b_1, q4b_1));
+            const __m256i p16_2 = _mm256_maddubs_epi16(_mm256_sign_epi8(q4b_2, q4b_2), _mm256_sign_epi8(q8b_2, q4b_2));
+            const int sl = x[ibl].scales_l[ib / 2];
+            const int16_t ls1 = (int16_t)(((sl & 0xf) | (((int)sh << 4) & 0x30)) - 32);
+            const int16_t ls2 = (int16_t)(((sl >> 4) | (((int)sh << 2) & 0x30)) - 32);
+            sh >>= 4;
+            sumi1 = _mm256_add_epi32(_mm256_madd_epi16(p16_1, _mm256_set1_epi16(ls1)), sumi1);
+            sumi2 = _mm256_add_epi32(_mm256_madd_epi16(p16_2, _mm256_set1_epi16(ls2)), sumi2);
+        }
+        accum = _mm256_fmadd_ps(_mm256_set1_ps(F32(x[ibl].d) * y[ibl].d),
+                                _mm256_cvtepi32_ps(_mm256_add_epi32(sumi1, sumi2)), accum);
+    }
+    return hsum_float_8(accum);
+}
+
 /* quantize_row_q8_0 AVX2 arm, x86/rows.zig:27-105: id = 127/max and
  * round-half-even, saturating packs. */
 AVX2_FN static void quantize_row_q8_0_avx2_impl(const float *x, void *vy, int64_t k) {
@@ -1470,20 +1604,23 @@ static dot_fn pick_dot(int type, int impl) {
 #if ORC_X86
     if (impl == ORC_IMPL_AVX2 && orc_has_avx2()) {
         switch (type) {
+        case ORC_TYPE_Q4_0: return vec_dot_q4_0_q8_0_avx2;
         case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_avx2;
+        case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_avx2;
         case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_avx2;
         case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_avx2;
+        case ORC_TYPE_IQ4_XS: return vec_dot_iq4_xs_q8_K_avx2;
         }
     }
 #endif
     (void)impl;
     switch (type) {
-    case ORC_TYPE_Q4_0: return vec_dot_q4_0_q8_0_generic;  /* no AVX2 restatement: generic on every impl */
+    case ORC_TYPE_Q4_0: return vec_dot_q4_0_q8_0_generic;
     case ORC_TYPE_Q4_K: return vec_dot_q4_K_q8_K_generic;
-    case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
+    case ORC_TYPE_Q5_K: return vec_dot_q5_K_q8_K_generic;
     case ORC_TYPE_Q6_K: return vec_dot_q6_K_q8_K_generic;
     case ORC_TYPE_Q8_0: return vec_dot_q8_0_q8_0_generic;
-    case ORC_TYPE_IQ4_XS: return vec_dot_iq4_xs_q8_K_generic;  /* no AVX2 restatement: generic on every impl */
+    case ORC_TYPE_IQ4_XS: return vec_dot_iq4_xs_q8_K_generic;
     }
     return NULL;
 }
@@ -2591,11 +2728,12 @@ typedef struct {
 
 typedef struct { tb_ctx *c; int ith; } tb_thread;
 
-static void *tb_worker(void *arg) {
+/* The per-output restatement above, one output at a time: the values every
+ * tile kernel must give (kept as the check of the tile loops below). */
+static void *tb_worker_scalar(void *arg) {
     tb_thread *t = (tb_thread *)arg;
     const tb_ctx *c = t->c;
     const size_t ab = c->type == ORC_TYPE_Q8_0 ? sizeof(blk_q8_0) : sizeof(blk_q4_0);
-    /* rows split statically (the tile kernels' duty split does not change values) */
     const int64_t r0 = c->nrows * t->ith / c->nth, r1 = c->nrows * (t->ith + 1) / c->nth;
     for (int64_t col = 0; col < c->ncols; ++col)
         for (int64_t r = r0; r < r1; ++r) {
@@ -2615,6 +2753,192 @@ static void *tb_worker(void *arg) {
     return NULL;
 }
 
+#if ORC_X86
+/* tinyBLAS_Q0_AVX's tile loops (sgemm.zig:578-880), the x86-64-v3 arm
+ * (VECTOR_REGISTERS 16): mnpack (:667-760) covers the m x n outputs with
+ * gemm4xN (4 rows of A, their deltas converted together, against RN
+ * columns), gemmMx4 (RM rows against 4 columns) and gemm (RM x RN), each
+ * splitting its tiles statically over the threads (duty, :763-769, columns
+ * fastest).  Every kernel gives an output the same value: per block l,
+ * fma(f32(d_a) * f32(d_b), updot(|a|, b * sign a), acc), then hsumAvx. */
+typedef struct {
+    int q4;                 /* A is Q4_0 (else Q8_0) */
+    const uint8_t *A;
+    size_t ab;              /* bytes per A block */
+    int64_t lda;            /* A row stride, blocks */
+    const blk_q8_0 *B;
+    int64_t ldb;            /* B column stride, blocks */
+    float *C;
+    int64_t ldc, k, ith, nth;
+} tbq;
+
+AVX2_FN static inline const uint8_t *tbq_a(const tbq *t, int64_t row, int64_t l) {
+    return t->A + (size_t)(t->lda * row + l) * t->ab;
+}
+AVX2_FN static inline uint16_t tbq_ad(const tbq *t, int64_t row, int64_t l) {
+    uint16_t d;
+    memcpy(&d, tbq_a(t, row, l), 2);
+    return d;
+}
+/* load (sgemm.zig:620-631): a block's 32 weights as signed bytes */
+AVX2_FN static inline __m256i tbq_load_a(const tbq *t, int64_t row, int64_t l) {
+    const uint8_t *p = tbq_a(t, row, l) + 2;
+    if (!t->q4) return _mm256_loadu_si256((const __m256i *)p);
+    const __m128i x = _mm_loadu_si128((const __m128i *)p);
+    const __m256i nib = _mm256_and_si256(_mm256_set1_epi8(15), _mm256_set_m128i(_mm_srli_epi16(x, 4), x));
+    return _mm256_sub_epi8(nib, _mm256_set1_epi8(8));
+}
+AVX2_FN static inline __m256i tbq_load_b(const tbq *t, int64_t col, int64_t l) {
+    return _mm256_loadu_si256((const __m256i *)t->B[t->ldb * col + l].qs);
+}
+/* dot (sgemm.zig:645-648): updot(sign(a, a), sign(b, a)) */
+AVX2_FN static inline __m256 tbq_dot(__m256i a, __m256i b) {
+    const __m256i u = _mm256_maddubs_epi16(_mm256_sign_epi8(a, a), _mm256_sign_epi8(b, a));
+    return _mm256_cvtepi32_ps(_mm256_madd_epi16(_mm256_set1_epi16(1), u));
+}
+/* hsumAvx (sgemm.zig:119-124) */
+AVX2_FN static inline float tbq_hsum(__m256 x) {
+    const __m128 h = _mm_add_ps(_mm256_extractf128_ps(x, 1), _mm256_castps256_ps128(x));
+    float v[4];
+    _mm_storeu_ps(v, h);
+    return (v[0] + v[2]) + (v[1] + v[3]);
+}
+static inline void tbq_duty(const tbq *t, int64_t tiles, int64_t *start, int64_t *end) {
+    const int64_t d = (tiles + t->nth - 1) / t->nth;
+    *start = d * t->ith;
+    *end = *start + d < tiles ? *start + d : tiles;
+}
+
+#define TBQ_INLINE __attribute__((always_inline, target("avx2,fma,f16c"))) static inline
+
+TBQ_INLINE void tbq_gemm4xN(const tbq *t, const int RN, int64_t m0, int64_t m, int64_t n0, int64_t n) {
+    const int64_t ytiles = (m - m0) / 4, xtiles = (n - n0) / RN;
+    int64_t job, end;
+    tbq_duty(t, xtiles * ytiles, &job, &end);
+    for (; job < end; ++job) {
+        const int64_t ii = m0 + job / xtiles * 4, jj = n0 + job % xtiles * RN;
+        __m256 Cv[4][4];
+        for (int j = 0; j < RN; ++j)
+            for (int i = 0; i < 4; ++i) Cv[j][i] = _mm256_setzero_ps();
+        for (int64_t l = 0; l < t->k; ++l) {
+            const __m128 da = _mm_cvtph_ps(_mm_set_epi16(0, 0, 0, 0, (short)tbq_ad(t, ii + 3, l),
+                                                        (short)tbq_ad(t, ii + 2, l), (short)tbq_ad(t, ii + 1, l),
+                                                        (short)tbq_ad(t, ii + 0, l)));
+            __m256i avec[4];
+            for (int i = 0; i < 4; ++i) avec[i] = tbq_load_a(t, ii + i, l);
+            for (int j = 0; j < RN; ++j) {
+                const blk_q8_0 *b = &t->B[t->ldb * (jj + j) + l];
+                float dv[4];
+                _mm_storeu_ps(dv, _mm_mul_ps(da, _mm_set1_ps(_cvtsh_ss(b->d))));
+                const __m256i bv = _mm256_loadu_si256((const __m256i *)b->qs);
+                for (int i = 0; i < 4; ++i) Cv[j][i] = _mm256_fmadd_ps(_mm256_set1_ps(dv[i]), tbq_dot(avec[i], bv), Cv[j][i]);
+            }
+        }
+        for (int j = 0; j < RN; ++j)
+            for (int i = 0; i < 4; ++i) t->C[t->ldc * (jj + j) + ii + i] = tbq_hsum(Cv[j][i]);
+    }
+}
+
+TBQ_INLINE void tbq_gemmMx4(const tbq *t, const int RM, int64_t m0, int64_t m, int64_t n0, int64_t n) {
+    const int64_t ytiles = (m - m0) / RM, xtiles = (n - n0) / 4;
+    int64_t job, end;
+    tbq_duty(t, xtiles * ytiles, &job, &end);
+    for (; job < end; ++job) {
+        const int64_t ii = m0 + job / xtiles * RM, jj = n0 + job % xtiles * 4;
+        __m256 Cv[4][4];
+        for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < RM; ++i) Cv[j][i] = _mm256_setzero_ps();
+        for (int64_t l = 0; l < t->k; ++l) {
+            const __m128 db = _mm_cvtph_ps(_mm_set_epi16(0, 0, 0, 0, (short)t->B[t->ldb * (jj + 3) + l].d,
+                                                        (short)t->B[t->ldb * (jj + 2) + l].d,
+                                                        (short)t->B[t->ldb * (jj + 1) + l].d,
+                                                        (short)t->B[t->ldb * (jj + 0) + l].d));
+            __m256i bvec[4];
+            for (int j = 0; j < 4; ++j) bvec[j] = tbq_load_b(t, jj + j, l);
+            for (int i = 0; i < RM; ++i) {
+                float dv[4];
+                _mm_storeu_ps(dv, _mm_mul_ps(_mm_set1_ps(_cvtsh_ss(tbq_ad(t, ii + i, l))), db));
+                const __m256i av = tbq_load_a(t, ii + i, l);
+                for (int j = 0; j < 4; ++j) Cv[j][i] = _mm256_fmadd_ps(_mm256_set1_ps(dv[j]), tbq_dot(av, bvec[j]), Cv[j][i]);
+            }
+        }
+        for (int j = 0; j < 4; ++j)
+            for (int i = 0; i < RM; ++i) t->C[t->ldc * (jj + j) + ii + i] = tbq_hsum(Cv[j][i]);
+    }
+}
+
+TBQ_INLINE void tbq_gemm(const tbq *t, const int RM, const int RN, int64_t m0, int64_t m, int64_t n0, int64_t n) {
+    const int64_t ytiles = (m - m0) / RM, xtiles = (n - n0) / RN;
+    int64_t job, end;
+    tbq_duty(t, xtiles * ytiles, &job, &end);
+    for (; job < end; ++job) {
+        const int64_t ii = m0 + job / xtiles * RM, jj = n0 + job % xtiles * RN;
+        __m256 Cv[3][3];
+        for (int j = 0; j < RN; ++j)
+            for (int i = 0; i < RM; ++i) Cv[j][i] = _mm256_setzero_ps();
+        for (int64_t l = 0; l < t->k; ++l)
+            for (int j = 0; j < RN; ++j)
+                for (int i = 0; i < RM; ++i) {
+                    const blk_q8_0 *b = &t->B[t->ldb * (jj + j) + l];
+                    const __m256 ud = tbq_dot(tbq_load_a(t, ii + i, l), _mm256_loadu_si256((const __m256i *)b->qs));
+                    const float d = _cvtsh_ss(tbq_ad(t, ii + i, l)) * _cvtsh_ss(b->d);
+                    Cv[j][i] = _mm256_fmadd_ps(_mm256_set1_ps(d), ud, Cv[j][i]);
+                }
+        for (int j = 0; j < RN; ++j)
+            for (int i = 0; i < RM; ++i) t->C[t->ldc * (jj + j) + ii + i] = tbq_hsum(Cv[j][i]);
+    }
+}
+
+/* mnpack (sgemm.zig:667-760), VECTOR_REGISTERS 16 */
+AVX2_FN static void tbq_mnpack(const tbq *t, int64_t m0, int64_t m, int64_t n0, int64_t n) {
+    const int64_t dm = m - m0 < 4 ? m - m0 : 4, dn = n - n0 < 4 ? n - n0 : 4;
+    int64_t mc, nc;
+    switch ((dm << 4) | dn) {
+    case 0x44: case 0x43: case 0x42: tbq_gemm4xN(t, 2, m0, m, n0, n); mc = 4; nc = 2; break;
+    case 0x34: case 0x24: tbq_gemmMx4(t, 2, m0, m, n0, n); mc = 2; nc = 4; break;
+    case 0x33: case 0x32: tbq_gemm(t, 3, 2, m0, m, n0, n); mc = 3; nc = 2; break;
+    case 0x23: tbq_gemm(t, 2, 3, m0, m, n0, n); mc = 2; nc = 3; break;
+    case 0x41: tbq_gemm4xN(t, 1, m0, m, n0, n); mc = 4; nc = 1; break;
+    case 0x22: tbq_gemm(t, 2, 2, m0, m, n0, n); mc = 2; nc = 2; break;
+    case 0x14: tbq_gemmMx4(t, 1, m0, m, n0, n); mc = 1; nc = 4; break;
+    case 0x31: tbq_gemm(t, 3, 1, m0, m, n0, n); mc = 3; nc = 1; break;
+    case 0x13: tbq_gemm(t, 1, 3, m0, m, n0, n); mc = 1; nc = 3; break;
+    case 0x21: tbq_gemm(t, 2, 1, m0, m, n0, n); mc = 2; nc = 1; break;
+    case 0x12: tbq_gemm(t, 1, 2, m0, m, n0, n); mc = 1; nc = 2; break;
+    case 0x11: tbq_gemm(t, 1, 1, m0, m, n0, n); mc = 1; nc = 1; break;
+    default: return;
+    }
+    const int64_t mp = m0 + (m - m0) / mc * mc, np = n0 + (n - n0) / nc * nc;
+    tbq_mnpack(t, mp, m, n0, np);
+    tbq_mnpack(t, m0, m, np, n);
+}
+#endif /* ORC_X86 */
+
+/* One thread's llamafile_sgemm call (mulmat.zig:336-367 calls it from every
+ * thread with its ith / nth; tinyBLAS_Q0_AVX's matmul = mnpack(0, m, 0, n)). */
+static void *tb_worker(void *arg) {
+    tb_thread *t = (tb_thread *)arg;
+    const tb_ctx *c = t->c;
+#if ORC_X86
+    tbq q;
+    q.q4 = c->type == ORC_TYPE_Q4_0;
+    q.A = c->w;
+    q.ab = q.q4 ? sizeof(blk_q4_0) : sizeof(blk_q8_0);
+    q.lda = (int64_t)(c->wrow / q.ab);
+    q.B = c->y;
+    q.ldb = c->nb;
+    q.C = c->dst;
+    q.ldc = c->nrows;
+    q.k = c->nb;
+    q.ith = t->ith;
+    q.nth = c->nth;
+    tbq_mnpack(&q, 0, c->nrows, 0, c->ncols);
+    return NULL;
+#else
+    return tb_worker_scalar(arg);
+#endif
+}
+
 int orc_tinyblas_q0(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
                     float *dst, int nth) {
     if ((type != ORC_TYPE_Q8_0 && type != ORC_TYPE_Q4_0) || K % QK8_0 != 0 || nrows <= 0 || ncols <= 0) return 0;
@@ -2632,6 +2956,29 @@ int orc_tinyblas_q0(int type, const void *w, int64_t nrows, int64_t K, const voi
     tb_thread *ts = (tb_thread *)malloc(sizeof(tb_thread) * (size_t)nth);
     for (int i = 0; i < nth; ++i) { ts[i].c = &c; ts[i].ith = i; }
     run_threads(nth, ts, sizeof *ts, tb_worker);
+    free(ts);
+    return 1;
+}
+
+/* The same outputs, one at a time (the per-output restatement: the check of
+ * the tile loops). */
+int orc_tinyblas_q0_per_output(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
+                               float *dst, int nth) {
+    if ((type != ORC_TYPE_Q8_0 && type != ORC_TYPE_Q4_0) || K % QK8_0 != 0 || nrows <= 0 || ncols <= 0) return 0;
+    if (nth < 1) nth = 1;
+    tb_ctx c;
+    c.type = type;
+    c.w = (const uint8_t *)w;
+    c.y = (const blk_q8_0 *)y_q8_0;
+    c.nrows = nrows;
+    c.nb = K / QK8_0;
+    c.ncols = ncols;
+    c.nth = nth;
+    c.wrow = orc_row_size(type, K);
+    c.dst = dst;
+    tb_thread *ts = (tb_thread *)malloc(sizeof(tb_thread) * (size_t)nth);
+    for (int i = 0; i < nth; ++i) { ts[i].c = &c; ts[i].ith = i; }
+    run_threads(nth, ts, sizeof *ts, tb_worker_scalar);
     free(ts);
     return 1;
 }

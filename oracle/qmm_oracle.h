@@ -114,6 +114,8 @@ int orc_mul_mat_tiled(int type, const void *w, int64_t nrows, int64_t K, const f
  * orc_mul_mat_tinyblas also below 2 columns or without AVX2. */
 int orc_tinyblas_q0(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
                     float *dst, int nth);
+int orc_tinyblas_q0_per_output(int type, const void *w, int64_t nrows, int64_t K, const void *y_q8_0, int64_t ncols,
+                               float *dst, int nth);
 int orc_mul_mat_tinyblas(int type, const void *w, int64_t nrows, int64_t K, const float *x, int64_t ncols,
                          float *dst, int nth);
 

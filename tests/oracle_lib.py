@@ -67,6 +67,8 @@ def lib():
         L.orc_mul_mat_tiled.argtypes = [ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
         L.orc_tinyblas_q0.restype = ctypes.c_int
         L.orc_tinyblas_q0.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, f32p, ctypes.c_int]
+        L.orc_tinyblas_q0_per_output.restype = ctypes.c_int
+        L.orc_tinyblas_q0_per_output.argtypes = [ctypes.c_int, vp, i64, i64, vp, i64, f32p, ctypes.c_int]
         L.orc_mul_mat_tinyblas.restype = ctypes.c_int
         L.orc_mul_mat_tinyblas.argtypes = [ctypes.c_int, vp, i64, i64, f32p, i64, f32p, ctypes.c_int]
         L.orc_mul_mat_id.restype = None
@@ -201,6 +203,15 @@ def tinyblas_q0(t, wq, nrows, K, y_q8_0, ncols, nth=4):
     out = np.full((ncols, nrows), np.nan, dtype=np.float32)
     ok = lib().orc_tinyblas_q0(t, _p(np.ascontiguousarray(wq)), nrows, K, _p(np.ascontiguousarray(y_q8_0)), ncols,
                                _p(out), nth)
+    return out if ok else None
+
+
+def tinyblas_q0_per_output(t, wq, nrows, K, y_q8_0, ncols, nth=4):
+    """The same outputs one at a time (the per-output restatement the tile
+    loops are checked against)."""
+    out = np.full((ncols, nrows), np.nan, dtype=np.float32)
+    ok = lib().orc_tinyblas_q0_per_output(t, _p(np.ascontiguousarray(wq)), nrows, K,
+                                          _p(np.ascontiguousarray(y_q8_0)), ncols, _p(out), nth)
     return out if ok else None
 
 

@@ -411,3 +411,25 @@ def test_tinyblas_agrees_with_vec_dot_route(t):
     assert O.mul_mat_tinyblas(t, wq, nrows, K, x[:1]) is None  # llamafile_sgemm declines one column
     assert O.mul_mat_tinyblas(O.TYPE_Q4_K, O.quantize_rows(O.TYPE_Q4_K, O.fill_normal(1, 256 * 8).reshape(8, 256)),
                               8, 256, x[:, :256]) is None
+
+
+@pytest.mark.skipif(not O.has_avx2(), reason="host has no AVX2")
+@pytest.mark.parametrize("t", [O.TYPE_Q8_0, O.TYPE_Q4_0])
+def test_tinyblas_tile_loops_equal_the_per_output_restatement(t):
+    """The timing-faithful tile loops (mnpack over gemm4xN / gemmMx4 / gemm,
+    each splitting its tiles over the threads, sgemm.zig:667-880) give every
+    output the per-output restatement's value bit for bit, on shapes whose
+    remainders reach every tile kernel (1-13 rows and columns past the 4 x 2
+    tiles), at 1-7 threads, with every output written exactly once (NaN
+    prefill)."""
+    rng = np.random.default_rng(17)
+    K = 96
+    for nrows in (1, 2, 3, 4, 5, 6, 7, 9, 13, 33):
+        for ncols in (1, 2, 3, 4, 5, 7, 13):
+            w = O.quantize_rows(t, (rng.standard_normal((nrows, K)) * 0.02).astype(np.float32))
+            y = O.quantize_rows(O.TYPE_Q8_0, rng.standard_normal((ncols, K)).astype(np.float32))
+            want = O.tinyblas_q0_per_output(t, w, nrows, K, y, ncols, nth=1)
+            for nth in (1, 3, 7):
+                got = O.tinyblas_q0(t, w, nrows, K, y, ncols, nth=nth)
+                assert np.all(np.isfinite(got)), (nrows, ncols, nth)
+                np.testing.assert_array_equal(got, want, err_msg=f"{nrows}x{ncols} nth={nth}")

@@ -254,8 +254,94 @@ def _dot_q8_0(blocks):
     return O.vec_dot(O.TYPE_Q8_0, O.IMPL_AVX2, 32 * len(blocks), np.concatenate(xs), np.concatenate(ys))
 
 
+def _q4_0(d, elems):
+    """One Q4_0 block {d f16, qs[16]}: code 8 (weight 0) but at the given
+    elements; element j < 16 is the low nibble of qs[j], j >= 16 the high
+    nibble of qs[j - 16]."""
+    codes = np.full(32, 8, np.int64)
+    for e, q in elems.items():
+        codes[e] = q
+    b = np.zeros(18, np.uint8)
+    b[0:2] = np.array([_f16(d)], np.uint16).view(np.uint8)
+    b[2:] = (codes[:16] | (codes[16:] << 4)).astype(np.uint8)
+    return b
+
+
+def _q5_K(elems, d=1.0, dmin=0.0, sc=None, mins=None):
+    """One Q5_K block {d, dmin f16, scales[12], qh[32], qs[128]}: 5-bit codes
+    at the given elements (others 0); element 64c + r takes the low (r < 32)
+    or high nibble of qs[32c + r % 32] and bit 2c (+1 for the high half) of
+    qh[r % 32]."""
+    b = np.zeros(176, np.uint8)
+    b[0:2] = np.array([_f16(d)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([_f16(dmin)], np.uint16).view(np.uint8)
+    for j, v in enumerate(sc or []):
+        b[4 + j] = v
+    for j, v in enumerate(mins or []):
+        b[8 + j] = v
+    for e, q in elems.items():
+        c, r = divmod(e, 64)
+        hi = r >= 32
+        b[48 + 32 * c + r % 32] |= (q & 15) << (4 if hi else 0)
+        b[16 + r % 32] |= ((q >> 4) & 1) << (2 * c + (1 if hi else 0))
+    return b
+
+
+def _iq4_xs(elems, d=1.0):
+    """One IQ4_XS block {d f16, scales_h u16, scales_l[4], qs[128]}: group 0's
+    scale ls = 33 (ls - 32 = 1), the given codes at group-0 elements (element
+    j < 16 the low nibble of qs[j], 16..31 the high nibble of qs[j - 16]),
+    code 8 (level 1) elsewhere."""
+    b = np.zeros(136, np.uint8)
+    b[0:2] = np.array([_f16(d)], np.uint16).view(np.uint8)
+    b[2:4] = np.array([2], np.uint16).view(np.uint8)   # scales_h: group 0 high bits = 2
+    b[4] = 1                                            # scales_l: group 0 low nibble = 1
+    codes = np.full(256, 8, np.int64)
+    for e, q in elems.items():
+        codes[e] = q
+    for g in range(8):
+        c = codes[32 * g:32 * g + 32]
+        b[8 + 16 * g:8 + 16 * g + 16] = (c[:16] | (c[16:] << 4)).astype(np.uint8)
+    return b
+
+
+# q4_0: lane l is the products 4l .. 4l + 3 of a block (code 9 is weight +1).
+# q5_K: q4_K's lanes (element 4l of sub-block 0, scale 1).
+# iq4_xs: lane l takes elements 4l .. 4l + 3 of every group (code 9 is level
+# 13, the q8 value 1 gives 13 * (ls - 32) = 13; the expected 1 becomes 13).
+
+def _dot_q4_0(blocks):
+    xs, ys = [], []
+    for s, ls in blocks:
+        dx, dy = (4096.0, 8192.0) if s == BIG else (1.0, 1.0)
+        xs.append(_q4_0(dx, {4 * l: 9 for l in ls}))
+        ys.append(_q8_0(dy, {4 * l: v for l, v in ls.items()}))
+    return O.vec_dot(O.TYPE_Q4_0, O.IMPL_AVX2, 32 * len(blocks), np.concatenate(xs), np.concatenate(ys))
+
+
+def _dot_q5_K(blocks):
+    xs, ys = [], []
+    for s, ls in blocks:
+        xs.append(_q5_K({4 * l: 1 for l in ls}, sc=[1]))
+        ys.append(_q8_K(s, {4 * l: v for l, v in ls.items()}))
+    return O.vec_dot(O.TYPE_Q5_K, O.IMPL_AVX2, 256 * len(blocks), np.concatenate(xs), np.concatenate(ys))
+
+
+def _dot_iq4_xs(blocks):
+    """Code 8 is level 1: the lane value is level * q8 = 1 * +-1."""
+    xs, ys = [], []
+    for s, ls in blocks:
+        xs.append(_iq4_xs({}))
+        ys.append(_q8_K(s, {4 * l: v for l, v in ls.items()}))
+    return O.vec_dot(O.TYPE_IQ4_XS, O.IMPL_AVX2, 256 * len(blocks), np.concatenate(xs), np.concatenate(ys))
+
+
+DOTS = [_dot_q4_K, _dot_q6_K, _dot_q8_0, _dot_q4_0, _dot_q5_K, _dot_iq4_xs]
+DOT_IDS = ["q4_K", "q6_K", "q8_0", "q4_0", "q5_K", "iq4_xs"]
+
+
 @pytest.mark.parametrize("case", list(CASES))
-@pytest.mark.parametrize("dot", [_dot_q4_K, _dot_q6_K, _dot_q8_0], ids=["q4_K", "q6_K", "q8_0"])
+@pytest.mark.parametrize("dot", DOTS, ids=DOT_IDS)
 def test_avx2_dot_accumulation_order(dot, case):
     blocks, _ = CASES[case]
     assert dot(blocks) == 1.0
@@ -278,6 +364,17 @@ def test_avx2_dot_constructed_blocks_are_what_they_say():
             assert O.vec_dot(t, O.IMPL_GENERIC, 256, x, y) == float(sum(ls.values()))
         y4 = _q8_K(1.0, {4 * l: v for l, v in ls.items()})
         assert O.vec_dot(O.TYPE_Q4_K, O.IMPL_GENERIC, 256, x4, y4) == float(sum(ls.values()))
+        x5 = _q5_K({4 * l: 1 for l in ls}, sc=[1])
+        w5 = O.dequantize(O.TYPE_Q5_K, x5, 256)
+        assert sorted(np.nonzero(w5)[0].tolist()) == sorted(4 * l for l in ls) and np.all(w5[w5 != 0] == 1.0)
+        assert O.vec_dot(O.TYPE_Q5_K, O.IMPL_GENERIC, 256, x5, y4) == float(sum(ls.values()))
+        x0 = _q4_0(1.0, {4 * l: 9 for l in ls})
+        w0 = O.dequantize(O.TYPE_Q4_0, x0, 32)
+        assert sorted(np.nonzero(w0)[0].tolist()) == sorted(4 * l for l in ls) and np.all(w0[w0 != 0] == 1.0)
+        xi = _iq4_xs({})
+        wi = O.dequantize(O.TYPE_IQ4_XS, xi, 256)
+        assert np.all(wi[:32] == 1.0)  # level 1 times (ls - 32) = 1 in group 0
+        assert O.vec_dot(O.TYPE_IQ4_XS, O.IMPL_GENERIC, 256, xi, y4) == float(sum(ls.values()))
 
 
 def test_q4_K_avx2_min_lanes_fold_once_at_the_end():
@@ -360,3 +457,31 @@ def test_avx2_q8_0_dot_fuses_the_block_scale():
     n = 32 * len(xs)
     got = np.float32(O.vec_dot(O.TYPE_Q8_0, O.IMPL_AVX2, n, np.concatenate(xs), np.concatenate(ys)))
     assert got == want and want != 0
+
+
+def test_q5_K_avx2_mins_fold_to_a_scalar_after_the_lanes():
+    """q5_K folds each super-block's mins to a scalar, summs = fma(dmin,
+    hsum, summs), added after hsum_float_8: block 0 puts 2^25 in lane 0 and
+    -2^25 in summs, block 1 puts 1 in lane 1.  hsum = 2^25 + 1 -> 2^25, total
+    0; mins folded into the lanes would give 1."""
+    x0 = _q5_K({0: 1}, dmin=1.0, sc=[1], mins=[1])
+    y0 = _q8_K(float(BIG), {0: 1})
+    x1 = _q5_K({4: 1}, sc=[1])
+    y1 = _q8_K(1.0, {4: 1})
+    got = O.vec_dot(O.TYPE_Q5_K, O.IMPL_AVX2, 512, np.concatenate([x0, x1]), np.concatenate([y0, y1]))
+    assert got == 0.0
+
+
+@pytest.mark.parametrize("t", [O.TYPE_Q4_0, O.TYPE_Q5_K, O.TYPE_IQ4_XS, O.TYPE_Q4_K, O.TYPE_Q6_K, O.TYPE_Q8_0])
+def test_avx2_dot_agrees_with_generic_on_normal_data(t):
+    """Beside the order pins, the AVX2 arms give the golden-pinned generic
+    dots' values up to float summation order, and their integer parts
+    exactly (checked through unit scales by the pins above)."""
+    rng = np.random.default_rng(int(t))
+    nrows, K, ncols = 16, 1024, 3
+    w = O.quantize_rows(t, (rng.standard_normal((nrows, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((ncols, K)).astype(np.float32)
+    g = O.mul_mat(t, w, nrows, K, x, nth=2, impl=O.IMPL_GENERIC).astype(np.float64)
+    a = O.mul_mat(t, w, nrows, K, x, nth=2, impl=O.IMPL_AVX2).astype(np.float64)
+    tol = 1e-5 if t not in (O.TYPE_Q8_0, O.TYPE_Q4_0) else 1e-2  # q8_0 activations: AVX2 ties-to-even row quantizer
+    assert np.max(np.abs(a - g)) <= tol * np.max(np.abs(g))
