@@ -694,7 +694,10 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
         from ggml_hip import probes as P
         sink = torch.empty(P.sink_words(wb), dtype=torch.int32, device=dev)
         n = len(ws) * reps
-        cases = (("stream read probe", lambda i: P.stream_read(ws[i % len(ws)], sink=sink)),
+        gsink = torch.empty(max(P.sink_words(wb), -(-hm // 28) * 14), dtype=torch.int32, device=dev)
+        cases = (("empty launch (512 workgroups of 896 threads)", lambda i: P.empty_launch(512, gsink)),
+                 ("stream read probe", lambda i: P.stream_read(ws[i % len(ws)], sink=sink)),
+                 ("the GEMV's own Q4_K loads, no arithmetic", lambda i: P.q4k_gemv_pattern(ws[i % len(ws)], gsink)),
                  ("gemv on a quantized column", lambda i: G.mul_mat_vec("Q4_K", ws[i % len(ws)], hk, qs, ds, out=out)),
                  ("op: gemv with fused quantization", lambda i: G.mul_mat("Q4_K", ws[i % len(ws)], x, out=out)))
         for kern, fn in cases:

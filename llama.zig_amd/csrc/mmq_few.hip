@@ -211,11 +211,12 @@ __device__ __forceinline__ void wait_step(bool big, int ahead) {
 template <int TYPE, int NW, int NCT>
 constexpr int few_occupancy(int nst) { return 163840 / (nst * FewGeo<TYPE, NW, NCT>::STAGE); }
 
-template <int TYPE, int NST, int NW, int NCT>
+template <int TYPE, int NST, int NW, int NCT, bool PACK>
 __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, NW, NCT>(NST))) void mmq_few_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int ncols, float *__restrict__ dst, int64_t dst_col_stride,
     float *__restrict__ partial) {
+    static_assert(!PACK || (NCT == 1 && (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K)), "packed: one tile, K-quant nibbles");
     using G = FewGeo<TYPE, NW, NCT>;
     using FF = FewFmt<TYPE>;
     constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER, WROW = G::WROW;
@@ -223,6 +224,8 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
     static_assert(NST >= 2 && few_occupancy<TYPE, NW, NCT>(NST) >= 1, "ring depth");
     static_assert((NST - 2) * G::transfers_of(0) <= 63, "vmcnt field");
     __shared__ alignas(16) uint8_t st[NST][G::STAGE];
+    __shared__ alignas(16) uint4 zero16;  // the packed path's B operand for the lanes of the other sub-block
+    if (PACK && threadIdx.x == 0) zero16 = make_uint4(0u, 0u, 0u, 0u);  // published by the ring's first barrier
 
     const int64_t Kp = pad_k(K);
     const int lane = threadIdx.x & 63;
@@ -506,6 +509,86 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         }
     };
 
+    // Up to 8 columns (PACK): one v_mfma_i32_16x16x64_i8 takes sub-blocks 2c
+    // and 2c + 1 of the step.  Lane group kq >> 1 supplies the sub-block (low
+    // nibbles of the 32 bytes qs[32c..], then high), kq & 1 its elements
+    // 16 (kq & 1) .. +16.  Output column li holds activation column li & 7
+    // against sub-block 2c + (li >> 3): B is that column's Q8_1 codes in the
+    // lane groups of its sub-block and zero in the other two, so every output
+    // is a live (column, sub-block) dot, and the scale MFMA puts sc_{2c} * d8
+    // in K slot 0 for columns 0-7 and sc_{2c+1} * d8 in slot 1 for columns
+    // 8-15.  The min term goes to columns 0-7 only, and the two halves of an
+    // output column are added at the end.  Against one 16x16x32 MFMA per
+    // sub-block with columns 8-15 idle, it halves the MFMAs and the
+    // per-output convert + FMA of a step.
+    const int phi = li >> 3, pj = li & 7;  // output column half, activation column
+    const bool plive = (kq >> 1) == phi;   // this lane group's codes belong to its column's sub-block
+    auto compute_pack = [&](const uint8_t *st) {
+        constexpr bool Q5 = TYPE == TYPE_Q5_K;
+        constexpr int QS = Q5 ? 48 : 16;  // the nibbles' offset in the block
+        const uint8_t *arow = st + (wave * 16 + li) * WROW;
+        const uint4 hdr = *reinterpret_cast<const uint4 *>(arow);
+        uint4 qh5 = make_uint4(0u, 0u, 0u, 0u);  // fifth bits of the lane's 16 elements of every sub-block
+        if constexpr (Q5) qh5 = *reinterpret_cast<const uint4 *>(arow + 16 + 16 * (kq & 1));
+        // getScaleMinK4 for all 8 sub-blocks, four per dword (bytes)
+        const uint32_t sc_lo = hdr.y & 0x3F3F3F3Fu;
+        const uint32_t sc_hi = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+        const uint32_t mn_lo = hdr.z & 0x3F3F3F3Fu;
+        const uint32_t mn_hi = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+        const uint8_t *bcol = st + FA + pj * QK_K;
+        const uint32_t *dcol = reinterpret_cast<const uint32_t *>(st + FA + FB) + pj * 8;
+        const uint4 dh0 = *reinterpret_cast<const uint4 *>(dcol), dh1 = *reinterpret_cast<const uint4 *>(dcol + 4);
+        const uint4 dm = *reinterpret_cast<const uint4 *>(dcol + 4 * (kq & 1));
+        v4f accb;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint4 q = *reinterpret_cast<const uint4 *>(arow + QS + 32 * c + 16 * (kq & 1));
+            const int sh = 4 * (kq >> 1);
+            const uint32_t m4 = 0x0F0F0F0Fu;
+            uint4 a4 = make_uint4((q.x >> sh) & m4, (q.y >> sh) & m4, (q.z >> sh) & m4, (q.w >> sh) & m4);
+            if constexpr (Q5) {
+                const int bit = 2 * c + (kq >> 1);
+                a4.x |= ((qh5.x >> bit) & 0x01010101u) << 4;
+                a4.y |= ((qh5.y >> bit) & 0x01010101u) << 4;
+                a4.z |= ((qh5.z >> bit) & 0x01010101u) << 4;
+                a4.w |= ((qh5.w >> bit) & 0x01010101u) << 4;
+            }
+            const v4i a = __builtin_bit_cast(v4i, a4);
+            // column pj's codes of block 2c + phi, elements 16 (kq & 1) .. +16: chunk 4c + 2 phi + (kq & 1)
+            const uint4 *bp = plive ? reinterpret_cast<const uint4 *>(bcol + 16 * ((4 * c + 2 * phi + (kq & 1)) ^ pj))
+                                    : &zero16;
+            const v4i b = __builtin_bit_cast(v4i, *bp);
+            const v4i zi = {0, 0, 0, 0};
+            const v4i S = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, zi, 0, 0, 0);
+            // A: (sc_{2c}, sc_{2c+1}) in K slots 0, 1 of lane group 0; B: d8 of block 2c + phi in slot phi
+            const uint32_t scb = c < 2 ? sc_lo : sc_hi;
+            const int sb = 16 * (c & 1);
+            const uint32_t sa2 = (byte_f16(scb >> sb, 0) | (byte_f16(scb >> sb, 1) << 16)) & m_sc;
+            const uint4 &dh = c < 2 ? dh0 : dh1;
+            const uint32_t d8 = ((c & 1) ? (phi ? dh.w : dh.z) : (phi ? dh.y : dh.x)) & 0xFFFFu;
+            const v4h sa = __builtin_bit_cast(v4h, make_uint2(sa2, 0u));
+            const v4h sbv = __builtin_bit_cast(v4h, make_uint2(d8 << (16 * phi), 0u));
+            const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f SC = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, sbv, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) accb[v] = c == 0 ? (float)S[v] * SC[v] : fmaf((float)S[v], SC[v], accb[v]);
+        }
+        // min term, columns 0-7 only: K slot 4*kq + t holds sub-block 4*kq + t for kq < 2
+        const uint32_t mb = ((kq & 1) ? mn_hi : mn_lo) & m_mn;
+        const v4h am = __builtin_bit_cast(
+            v4h, make_uint2(byte_f16(mb, 0) | (byte_f16(mb, 1) << 16), byte_f16(mb, 2) | (byte_f16(mb, 3) << 16)));
+        const uint32_t m_lo = phi ? 0u : 0xFFFFFFFFu;
+        const v4h bm = __builtin_bit_cast(v4h, make_uint2(__builtin_amdgcn_perm(dm.y, dm.x, 0x07060302u) & m_lo,
+                                                          __builtin_amdgcn_perm(dm.w, dm.z, 0x07060302u) & m_lo));
+        const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+        const v4f P = __builtin_amdgcn_mfma_f32_16x16x16f16(am, bm, zf, 0, 0, 0);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint32_t dd = *reinterpret_cast<const uint32_t *>(st + (wave * 16 + 4 * kq + v) * WROW);
+            acc[0][v] = fmaf(h2f(dd), accb[v], fmaf(-h2f(dd >> 16), P[v], acc[0][v]));
+        }
+    };
+
     // NST-stage ring: step kb0 + i lives in stage i % NST; while a step is
     // contracted, the next NST - 2 are in flight and one more is issued
     const bool big = wave < FNQ % NW || FNQ % NW == 0;
@@ -519,7 +602,8 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
             wait_step<NST - 2, G::transfers_of(0), G::transfers_of(NW - 1)>(big, left < NST - 2 ? left : NST - 2);
             lds_barrier();
             if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
-            if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) compute(st[i]);
+            if constexpr (PACK) compute_pack(st[i]);
+            else if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) compute(st[i]);
             else if constexpr (TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) compute_q8_0(st[i]);
             else if constexpr (TYPE == TYPE_IQ4_XS) compute_iq4_xs(st[i], kb);
             else compute_q6_k(st[i], kb);
@@ -527,6 +611,19 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
         }
     }
 
+    if constexpr (PACK) {
+        // the odd sub-blocks' half of each output column (lanes li + 8) onto the even half
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[0][v] += __shfl_xor(acc[0][v], 8, 64);
+        if (li >= 8 || li >= ncols) return;
+        float *o = partial ? partial + ((int64_t)z * ncols + li) * nrows : dst + (int64_t)li * dst_col_stride;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int64_t r = row0 + wave * 16 + 4 * kq + v;
+            if (r < nrows) o[r] = acc[0][v];
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NCT; ++j) {
         const int c = 16 * j + li;
@@ -549,6 +646,7 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
 // 33 MB, and the rest is contraction that a deeper ring or more workgroups
 // per CU did not hide.
 constexpr int FEW_NST = 3, FEW_NW = 4;
+constexpr int FEW_PACK_COLS = 8;  // most columns of the packed (two sub-blocks per MFMA) path
 
 // K-split for the few-column kernel.  From 192 row tiles (3/4 of the CUs)
 // the kernel runs unsplit: the partials' reduction is a second launch of
@@ -595,9 +693,12 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     float *pp = split > 1 ? partial : nullptr;
-#define FEW_LAUNCH(TYPE, NCT)                                                                                          \
-    hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT>), grid, dim3(64 * FEW_NW), 0, s, wb, K, nrows,      \
+#define FEW_LAUNCH_P(TYPE, NCT, PK)                                                                                    \
+    hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT, PK>), grid, dim3(64 * FEW_NW), 0, s, wb, K, nrows,  \
                        row_stride, yqs, ds, (int)ncols, dst, dst_col_stride, pp)
+#define FEW_LAUNCH(TYPE, NCT) FEW_LAUNCH_P(TYPE, NCT, false)
+    // up to 8 columns of the K-quant nibble types: two sub-blocks per MFMA
+    const bool pack = ncols <= FEW_PACK_COLS;
     switch (type) {
     case TYPE_Q8_0:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q8_0, 2);
@@ -609,6 +710,7 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
         break;
     case TYPE_Q5_K:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q5_K, 2);
+        else if (pack) FEW_LAUNCH_P(TYPE_Q5_K, 1, true);
         else FEW_LAUNCH(TYPE_Q5_K, 1);
         break;
     case TYPE_Q4_0:
@@ -621,9 +723,11 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
         break;
     default:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q4_K, 2);
+        else if (pack) FEW_LAUNCH_P(TYPE_Q4_K, 1, true);
         else FEW_LAUNCH(TYPE_Q4_K, 1);
         break;
     }
 #undef FEW_LAUNCH
+#undef FEW_LAUNCH_P
     return (int)hipGetLastError();
 }

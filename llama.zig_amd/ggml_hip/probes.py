@@ -35,6 +35,10 @@ def plib():
         L.qmm_probe_sink_words.argtypes = [ctypes.c_size_t]
         L.qmm_probe_stream_read.restype = i32
         L.qmm_probe_stream_read.argtypes = [vp, ctypes.c_size_t, vp, vp]
+        L.qmm_probe_empty_launch.restype = i32
+        L.qmm_probe_empty_launch.argtypes = [i32, vp, vp]
+        L.qmm_probe_q4k_gemv_pattern.restype = i32
+        L.qmm_probe_q4k_gemv_pattern.argtypes = [vp, ctypes.c_int64, ctypes.c_int64, vp, vp]
         L.qmm_probe_mfma_valu.restype = i32
         L.qmm_probe_mfma_valu.argtypes = [i32, i32, i32, vp, vp, vp]
         _plib = L
@@ -54,6 +58,21 @@ def stream_read(buf: torch.Tensor, sink=None):
         sink = torch.empty(max(sink_words(nbytes), 1), dtype=torch.int32, device=buf.device)
     _check(plib().qmm_probe_stream_read(_ptr(buf), nbytes, _ptr(sink), _stream()), "qmm_probe_stream_read")
     return sink
+
+
+def empty_launch(nblocks: int, sink: torch.Tensor):
+    """A launch of nblocks empty workgroups of the headline GEMV's shape: the
+    fixed cost a launch's duration carries."""
+    _require_cuda(sink)
+    _check(plib().qmm_probe_empty_launch(nblocks, _ptr(sink), _stream()), "qmm_probe_empty_launch")
+
+
+def q4k_gemv_pattern(w: torch.Tensor, sink: torch.Tensor):
+    """The headline GEMV's loads over a Q4_K [nrows, 2304-byte] matrix, no
+    arithmetic; sink holds one word per wave (ceil(nrows / 28) * 14)."""
+    _require_cuda(w)
+    _check(plib().qmm_probe_q4k_gemv_pattern(_ptr(w), w.shape[0], w.stride(0), _ptr(sink), _stream()),
+           "qmm_probe_q4k_gemv_pattern")
 
 
 def mfma_valu(mode: int, iters: int, nblocks: int = 256, sink=None, hwid=None):

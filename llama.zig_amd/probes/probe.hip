@@ -9,6 +9,11 @@
 //    not removed, one word written per wave.
 // 2. mfma_valu_probe: whether MFMA and VALU work overlap on a SIMD, the fact
 //    the MMQ's ceiling rests on.
+// 3. empty_launch: a launch that does nothing, in the headline GEMV's grid
+//    shape (the fixed cost a launch's duration carries), and q4k_gemv_pattern:
+//    the headline GEMV's own loads of a Q4_K matrix (14 waves per workgroup,
+//    two rows per wave, each lane the 16-byte header and 32 bytes of nibbles
+//    of its 64-weight slice) with no arithmetic, XOR-folded.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -31,6 +36,37 @@ __global__ __launch_bounds__(PROBE_THREADS) void stream_read(const uint4 *__rest
     for (int u = 0; u < PROBE_LOADS; ++u) v ^= a[u].x ^ a[u].y ^ a[u].z ^ a[u].w;
     for (int o = 32; o > 0; o >>= 1) v ^= __shfl_xor(v, o);
     if ((threadIdx.x & 63) == 0) sink[(int64_t)blockIdx.x * (PROBE_THREADS / 64) + (threadIdx.x >> 6)] = v;
+}
+
+// ---------------------------------------------------------------- launch cost and the GEMV's access pattern
+
+constexpr int GP_WAVES = 14, GP_ROWS = 2;  // the headline GEMV's workgroup shape
+
+__global__ __launch_bounds__(64 * GP_WAVES) void empty_launch(uint32_t *sink) {
+    if (threadIdx.x == 0 && blockIdx.x == 0xFFFFFFFFu) sink[0] = 1;  // never taken
+}
+
+__global__ __launch_bounds__(64 * GP_WAVES) void q4k_gemv_pattern(const uint8_t *__restrict__ w, int64_t nrows,
+                                                                  int64_t row_stride, uint32_t *__restrict__ sink) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row0 = ((int64_t)blockIdx.x * GP_WAVES + wave) * GP_ROWS;
+    uint4 a[GP_ROWS][3];
+#pragma unroll
+    for (int r = 0; r < GP_ROWS; ++r) {
+        const int64_t row = row0 + r < nrows ? row0 + r : nrows - 1;
+        const uint8_t *blk = w + row * row_stride + (lane >> 2) * 144;  // lane's super-block (K = 4096: 16 per row)
+        const int c = lane & 3;                                      // its 64-weight slice of the block
+        a[r][0] = *reinterpret_cast<const uint4 *>(blk);
+        a[r][1] = *reinterpret_cast<const uint4 *>(blk + 16 + 32 * c);
+        a[r][2] = *reinterpret_cast<const uint4 *>(blk + 32 + 32 * c);
+    }
+    uint32_t v = 0;
+#pragma unroll
+    for (int r = 0; r < GP_ROWS; ++r)
+#pragma unroll
+        for (int u = 0; u < 3; ++u) v ^= a[r][u].x ^ a[r][u].y ^ a[r][u].z ^ a[r][u].w;
+    for (int o = 32; o > 0; o >>= 1) v ^= __shfl_xor(v, o);
+    if (lane == 0) sink[(int64_t)blockIdx.x * GP_WAVES + wave] = v;
 }
 
 // ---------------------------------------------------------------- MFMA / VALU overlap
@@ -198,6 +234,26 @@ extern "C" int qmm_probe_stream_read(const void *src, size_t bytes, uint32_t *si
     if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
     hipLaunchKernelGGL(stream_read, dim3((unsigned)nblocks), dim3(PROBE_THREADS), 0, (hipStream_t)stream,
                        (const uint4 *)src, (int64_t)(bytes / 16), sink);
+    return (int)hipGetLastError();
+}
+
+// A launch of nblocks empty workgroups of the headline GEMV's shape (896 threads).
+extern "C" int qmm_probe_empty_launch(int nblocks, uint32_t *sink, void *stream) {
+    if (!sink || nblocks < 1) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(empty_launch, dim3((unsigned)nblocks), dim3(64 * GP_WAVES), 0, (hipStream_t)stream, sink);
+    return (int)hipGetLastError();
+}
+
+// The headline GEMV's loads over a Q4_K matrix of K = 4096 (2304-byte rows);
+// sink: one word per wave, ceil(nrows / 28) * 14 words.
+extern "C" int qmm_probe_q4k_gemv_pattern(const void *w, int64_t nrows, int64_t row_stride, uint32_t *sink,
+                                          void *stream) {
+    if (!w || !sink || nrows < 1 || row_stride < 2304 || (uintptr_t)w % 16 || row_stride % 16)
+        return (int)hipErrorInvalidValue;
+    const int64_t nblocks = (nrows + GP_WAVES * GP_ROWS - 1) / (GP_WAVES * GP_ROWS);
+    if (nblocks > 0x7FFFFFFF) return (int)hipErrorInvalidValue;
+    hipLaunchKernelGGL(q4k_gemv_pattern, dim3((unsigned)nblocks), dim3(64 * GP_WAVES), 0, (hipStream_t)stream,
+                       (const uint8_t *)w, nrows, row_stride, sink);
     return (int)hipGetLastError();
 }
 

@@ -214,3 +214,33 @@ def test_few_columns_large_weights(tname, ncols):
     cpu = O.mul_mat_x86(t, wq[rows], len(rows), K, x, nth=8)
     assert nmse(got[:, rows], cpu) < NMSE_GATE
     np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
+
+
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K"])
+@pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 1), (1000, 4096, 2), (4100, 4096, 3), (6144, 2048, 5),
+                                           (300, 14336, 8), (64, 512, 7), (14336, 4096, 8)])
+def test_few_columns_packed(tname, nrows, K, ncols):
+    """Up to 8 columns the few-column kernel packs two sub-blocks into each
+    16x16x64 MFMA (output columns 0-7 against the even sub-block, 8-15 the
+    odd one, halves added at the end): within the f64 and CPU gates, split
+    and unsplit (small row counts split K), and within rounding of the GEMV
+    on the same quantized columns."""
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    x_d = torch.from_numpy(np.array(x)).cuda()
+    qs, ds = G.quantize_q8_1_planar(x_d)
+    got = G.mmq(tname, w_d, K, qs, ds).cpu().numpy()
+    tiny = torch.empty(16, dtype=torch.uint8, device="cuda")
+    unsplit = G.mmq(tname, w_d, K, qs, ds, workspace=tiny).cpu().numpy()
+    gemv = G.mul_mat_vec(tname, w_d, K, qs, ds).cpu().numpy()
+    assert max_err_scaled(got, gemv) < 1e-6, max_err_scaled(got, gemv)
+    assert max_err_scaled(unsplit, gemv) < 1e-6, max_err_scaled(unsplit, gemv)
+    rows = np.arange(nrows) if nrows <= 1024 else np.r_[0:96, nrows // 2:nrows // 2 + 96, nrows - 96:nrows]
+    y = G.quantize_q8_1(x_d, K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq[rows], len(rows), K, y, ncols)
+    assert max_err_scaled(got[:, rows], ideal) < F64_TOL, max_err_scaled(got[:, rows], ideal)
+    cpu = O.mul_mat(t, wq[rows], len(rows), K, x, nth=8)
+    assert nmse(got[:, rows], cpu) < NMSE_GATE

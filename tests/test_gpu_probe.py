@@ -4,6 +4,9 @@ llama.zig_amd/probes/probe.hip, apart from the backend library):
 - the streaming-read probe the GEMV's floor is measured with reads every byte
   (the sink holds the XOR of each wave's loads, checked against numpy),
   including a ragged last workgroup;
+- the headline GEMV's access-pattern probe loads exactly the GEMV's bytes
+  (per wave: each lane's 16-byte block header and its two 16-byte nibble
+  chunks of two rows, XOR-folded), rows past the end clamped to the last;
 - each mode of the MFMA / VALU overlap probe does the work it is timed for."""
 import numpy as np
 import pytest
@@ -26,6 +29,28 @@ def test_probe_reads_every_byte(nbytes):
     want = np.bitwise_xor.reduce(pad.reshape(nb, 8, 4, 64, 4), axis=(1, 3, 4)).reshape(-1)
     assert sink.size == want.size
     np.testing.assert_array_equal(sink, want)
+
+
+@pytest.mark.parametrize("nrows", [28, 100, 14336])
+def test_gemv_pattern_probe_loads_the_gemv_bytes(nrows):
+    from ggml_hip import probes as P
+    rng = np.random.default_rng(nrows)
+    w = rng.integers(0, 256, size=(nrows, 2304), dtype=np.uint8)
+    nwaves = -(-nrows // 28) * 14
+    sink = torch.zeros(nwaves, dtype=torch.int32, device="cuda")
+    P.q4k_gemv_pattern(torch.from_numpy(w).cuda(), sink)
+    got = sink.cpu().numpy().view(np.uint32)
+    words = w.view(np.uint32).reshape(nrows, 16, 36)  # [row, super-block, word of the 144 bytes]
+    want = np.zeros(nwaves, dtype=np.uint32)
+    for wv in range(nwaves):
+        v = np.uint32(0)
+        for r in range(2):
+            row = min(2 * wv + r, nrows - 1)
+            for c in range(4):  # the four lanes of each super-block: header + nibble chunks 32c .. 32c + 32
+                sel = np.r_[0:4, 4 + 8 * c:12 + 8 * c]
+                v ^= np.bitwise_xor.reduce(words[row][:, sel].reshape(-1))
+        want[wv] = v
+    np.testing.assert_array_equal(got, want)
 
 
 def test_mfma_valu_probe_does_its_work():
