@@ -18,8 +18,8 @@
 //     always 16-byte aligned; the step's bytes are moved as they are.
 // Either way 144 bytes per row go straight from global memory into LDS with
 // global_load_lds_dwordx4, rows back to back.  A block's codes start 2 bytes
-// in, so a lane reads the dwords around its 16 code bytes and funnel-shifts
-// them (v_alignbyte_b32) when they are not dword-aligned.  Q4_0's lane half h
+// in, so a lane reads the aligned 16-byte chunks around its 16 code bytes and
+// funnel-shifts them (v_alignbyte_b32) into place.  Q4_0's lane half h
 // takes the low (h = 0) or high (h = 1) nibbles of the block's 16 bytes and
 // subtracts 8 bytewise ((n + 0x78) ^ 0x80, no carries between bytes).  The
 // columns' Q8_1 bytes (one step's worth per column) and their block headers
@@ -29,6 +29,8 @@
 #include "../../include/ggml_hip_qmm.h"
 #include "mmq_dma.h"
 #include "qmm_device.h"
+
+#include <type_traits>
 
 using namespace qmm;
 using namespace qmm_dma;
@@ -55,15 +57,68 @@ struct Legacy<TYPE_Q4_0> {
     static constexpr int STEP_BYTES = NB * BBYTES;   // 144: always aligned
 };
 
-// 16 bytes at LDS byte offset o (o % 2 == 0): the dwords around them,
-// funnel-shifted when o is not dword-aligned.
-__device__ __forceinline__ v4i lds16_a2(const uint8_t *base, int o) {
-    const uint32_t *p = reinterpret_cast<const uint32_t *>(base + (o & ~3));
-    const uint32_t a0 = p[0], a1 = p[1], a2 = p[2], a3 = p[3];
-    if ((o & 3) == 0) return v4i{(int)a0, (int)a1, (int)a2, (int)a3};
-    const uint32_t a4 = p[4];
-    return v4i{(int)__builtin_amdgcn_alignbyte(a1, a0, 2), (int)__builtin_amdgcn_alignbyte(a2, a1, 2),
-               (int)__builtin_amdgcn_alignbyte(a3, a2, 2), (int)__builtin_amdgcn_alignbyte(a4, a3, 2)};
+// A block's codes start 2 bytes past its header, so they are rarely 16-byte
+// aligned in the window.  The rows sit 144 bytes (36 dwords) apart, so 4-byte
+// reads of one offset by the 32 rows of a wave hit each bank 4 times; 16-byte
+// reads (8 lanes per LDS cycle) cover the banks once.  The window is
+// therefore read as the aligned 16-byte chunks around the 16 bytes and
+// funnel-shifted in registers.
+//
+// A block's 16 bytes at byte offset R (even, compile-time) of the chunk pair
+// [c, c + 1] of a 16-byte aligned row (chunk c + 1 only when R != 0), and the
+// f16 two bytes before them (the block's d) when they lie in the pair.
+template <int R>
+struct Win16 {
+    uint32_t w[8];
+    __device__ __forceinline__ void load(const uint8_t *row, int c) {
+        const uint4 a = *reinterpret_cast<const uint4 *>(row + 16 * c);
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        if constexpr (R != 0) {
+            const uint4 b = *reinterpret_cast<const uint4 *>(row + 16 * c + 16);
+            w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        }
+    }
+    __device__ __forceinline__ v4i codes() const {
+        constexpr int D = R >> 2, B = R & 3;
+        v4i q;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) q[k] = B ? (int)__builtin_amdgcn_alignbyte(w[D + k + 1], w[D + k], B) : (int)w[D + k];
+        return q;
+    }
+    // the f16 bits before the codes (R >= 2)
+    __device__ __forceinline__ uint32_t before() const {
+        static_assert(R >= 2, "the two bytes before the codes are in the previous chunk");
+        return (w[(R - 2) >> 2] >> (8 * ((R - 2) & 3))) & 0xFFFFu;
+    }
+};
+
+// Block I's A operand and scale slot for a step whose window starts SH bytes
+// into its 16-byte aligned row (SH = 0, or 8 for odd Q8_0 steps): Q8_0 lane
+// half h reads the block's codes 16h .. 16h + 15; Q4_0 lanes read all 16
+// bytes and keep the low (h = 0) or high (h = 1) nibbles, minus 8 bytewise
+// ((n + 0x78) ^ 0x80, no carries between bytes).  The block's d goes to lanes
+// of half 0 only (keep).
+template <int TYPE, int SH, int I>
+__device__ __forceinline__ void legacy_a(const uint8_t *row, int lh, uint32_t keep, v4i &aop, v4h &asc) {
+    constexpr int BB = Legacy<TYPE>::BBYTES;
+    constexpr int O = SH + BB * I + 2, R = O & 15;
+    Win16<R> win;
+    win.load(row, (O >> 4) + (TYPE == TYPE_Q8_0 ? lh : 0));
+    v4i q = win.codes();
+    if constexpr (TYPE == TYPE_Q4_0) {
+        const int sh = 4 * lh;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) q[e] = (int)((((uint32_t)q[e] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ (int)0x80808080u;
+    }
+    aop = q;
+    uint32_t d;
+    if constexpr (R >= 2) {
+        d = win.before();
+    } else {
+        const uint32_t dw = *reinterpret_cast<const uint32_t *>(row + ((O - 2) & ~3));
+        d = ((O - 2) & 3) ? dw >> 16 : dw;
+    }
+    asc = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
 }
 
 template <int TYPE, int BN>
@@ -155,32 +210,27 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     // column, lanes of half 1 zeros.
     const uint32_t keep = lh ? 0u : 0xFFFFu;
 
-    auto compute = [&](int s, const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
-        const int shift = (s * STEP_BYTES) & 15;  // 0 or 8, uniform
-        const uint8_t *arow = sA + (wr + li) * WIN + shift;
+    // the step's window starts SH bytes into its row: 0, or 8 for odd Q8_0
+    // steps (a part starts at an even step)
+    auto compute = [&](auto shc, const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) __attribute__((always_inline)) {
+        constexpr int SH = decltype(shc)::value;
+        const uint8_t *arow = sA + (wr + li) * WIN;
         struct Ops {
             v4i b;
             v4h sb;
         };
         v4i aop[2];
         v4h asc[2];
-        auto load_a = [&](int i, int slot) {
-            constexpr int BB = L::BBYTES;
-            if constexpr (TYPE == TYPE_Q8_0) {
-                aop[slot] = lds16_a2(arow, BB * i + 2 + 16 * lh);
-            } else {
-                // Q4_0: the block's 16 bytes, low or high nibbles, minus 8
-                const v4i raw = lds16_a2(arow, BB * i + 2);
-                const int sh = 4 * lh;
-                v4i q;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    q[e] = (int)((((uint32_t)raw[e] >> sh) & 0x0F0F0F0Fu) + 0x78787878u) ^ (int)0x80808080u;
-                aop[slot] = q;
+        auto load_a = [&](int i, int slot) __attribute__((always_inline)) {
+            switch (i) {
+#define LEGACY_A_CASE(I)                                                                   \
+    case I:                                                                                \
+        if constexpr (I < NB) legacy_a<TYPE, SH, I>(arow, lh, keep, aop[slot], asc[slot]); \
+        break;
+                LEGACY_A_CASE(0) LEGACY_A_CASE(1) LEGACY_A_CASE(2) LEGACY_A_CASE(3)
+                LEGACY_A_CASE(4) LEGACY_A_CASE(5) LEGACY_A_CASE(6) LEGACY_A_CASE(7)
+#undef LEGACY_A_CASE
             }
-            const uint32_t dw = *reinterpret_cast<const uint32_t *>(arow + ((BB * i) & ~3));
-            const uint32_t d = ((BB * i) & 3) ? dw >> 16 : dw;
-            asc[slot] = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
         };
         auto load_b = [&](int p, Ops &o) {
             const int i = p / TJ, j = p % TJ;
@@ -233,11 +283,11 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     __syncthreads();
     for (int s = s_begin; s < s_end; s += 2) {
         dma(s + 1, sA1, sB1, sD1);  // the part holds an even number of steps
-        compute(s, sA0, sB0, sD0);
+        compute(std::integral_constant<int, 0>{}, sA0, sB0, sD0);
         wait_vmem();
         __syncthreads();
         if (s + 2 < s_end) dma(s + 2, sA0, sB0, sD0);
-        compute(s + 1, sA1, sB1, sD1);
+        compute(std::integral_constant<int, STEP_BYTES & 15>{}, sA1, sB1, sD1);
         wait_vmem();
         __syncthreads();
     }
