@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "../../include/ggml_hip_qmm.h"
+#include "mmq_dma.h"
 #include "qmm_device.h"
 
 using namespace qmm;
@@ -43,18 +44,18 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
                        const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
                        dim3 grid, const int32_t *tiles, const int32_t *n_tiles, const int32_t *col_src,
                        const int32_t *col_dst, float *partial, const MmqGlu &glu, hipStream_t s);
-// mmq_legacy_dma.hip: the dense Q8_0 / Q4_0 kernel fed by direct global->LDS loads
+// mmq_legacy_dma.hip: the Q8_0 / Q4_0 kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                           const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                          dim3 grid, float *partial, hipStream_t s);
-// mmq_iq4xs_dma.hip: the dense IQ4_XS kernel fed by direct global->LDS loads
+                          dim3 grid, float *partial, const qmm_dma::MmqGroups *grp, hipStream_t s);
+// mmq_iq4xs_dma.hip: the IQ4_XS kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_iq4xs_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                          const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                         hipStream_t s);
-// mmq_q5k_dma.hip: the dense Q5_K kernel fed by direct global->LDS loads
+                         const qmm_dma::MmqGroups *grp, hipStream_t s);
+// mmq_q5k_dma.hip: the Q5_K kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_q5k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                        const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                       hipStream_t s);
+                       const qmm_dma::MmqGroups *grp, hipStream_t s);
 // mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
@@ -694,6 +695,7 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
     if (gx > 0x7FFFFFFF || gy > 65535 || gy < 1 || split < 1 || split > 64 || (glu.gate && split != 1))
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)split);
+    const qmm_dma::MmqGroups grp{tiles, n_tiles, col_src, col_dst, expert_stride};
     // Q4_K with 16-byte aligned operands (the transfer unit of the direct
     // global->LDS loads; the weight rows are checked by check_weights)
     if (TYPE == TYPE_Q4_K && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
@@ -701,26 +703,27 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
                                        dst_col_stride, grid, tiles, n_tiles, col_src, col_dst,
                                        split > 1 ? partial : nullptr, glu, s))
             return e;
-    } else if ((TYPE == TYPE_Q8_0 || (TYPE == TYPE_Q4_0 && (K / BK) % (2 * split) == 0)) && !tiles && !glu.gate &&
-               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 &&
-               (uintptr_t)yds % 16 == 0) {
-        // dense Q8_0 / Q4_0 on 16-byte aligned rows: direct global->LDS steps
-        if (int e = mmq_legacy_dma_launch(TYPE, BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride,
-                                          grid, split > 1 ? partial : nullptr, s))
-            return e;
-    } else if (TYPE == TYPE_Q5_K && !tiles && !glu.gate && (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 &&
+    } else if ((TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) && !glu.gate &&
+               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && expert_stride % 16 == 0 &&
                (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
-        // dense Q5_K (176-byte blocks, 16-byte aligned in aligned rows): direct global->LDS steps
-        if (int e = mmq_q5k_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
-                                       split > 1 ? partial : nullptr, s))
+        // Q8_0 / Q4_0 on 16-byte aligned rows, dense or expert-grouped: direct global->LDS steps
+        if (int e = mmq_legacy_dma_launch(TYPE, BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride,
+                                          grid, split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
             return e;
-    } else if (TYPE == TYPE_IQ4_XS && K % 512 == 0 && (K / QK_K) % (2 * split) == 0 && !tiles && !glu.gate &&
-               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 &&
-               (uintptr_t)yds % 16 == 0) {
-        // dense IQ4_XS on 16-byte aligned rows of K % 512 == 0 (super-blocks
-        // in 16-byte aligned pairs): direct global->LDS steps
+    } else if (TYPE == TYPE_Q5_K && !glu.gate && (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 &&
+               expert_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+        // Q5_K (176-byte blocks, 16-byte aligned in aligned rows), dense or
+        // expert-grouped: direct global->LDS steps
+        if (int e = mmq_q5k_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
+                                       split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
+            return e;
+    } else if (TYPE == TYPE_IQ4_XS && K % 512 == 0 && (K / QK_K) % (2 * split) == 0 && !glu.gate &&
+               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && expert_stride % 16 == 0 &&
+               (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+        // IQ4_XS on 16-byte aligned rows of K % 512 == 0 (super-blocks in
+        // 16-byte aligned pairs), dense or expert-grouped: direct global->LDS steps
         if (int e = mmq_iq4xs_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
-                                         split > 1 ? partial : nullptr, s))
+                                         split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
             return e;
     } else {
         hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,

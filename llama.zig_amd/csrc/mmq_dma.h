@@ -32,6 +32,17 @@ __device__ __forceinline__ void wait_vmem() {
     __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0), expcnt / lgkmcnt not waited
 }
 
+// Expert-grouped (MUL_MAT_ID) mode of the dense direct-transfer kernels:
+// workgroup (x, y) takes row tile x of column tile y of the device tile table
+// {expert, col_low, col_high, -} (mmid.hip's grouping; workgroups past
+// *n_tiles exit at once).  Its activation columns are gathered through
+// col_src and its output columns scattered through col_dst (dst's column
+// stride is then the output row stride).  No K split.
+struct MmqGroups {
+    const int32_t *tiles, *n_tiles, *col_src, *col_dst;
+    int64_t expert_stride;
+};
+
 // One lane's 16 outputs of a 32x32 MFMA tile (column fixed, rows r0 + 8q +
 // 0..3 for q = 0..3, r0 a multiple of 4) into the column at o: four 16-byte
 // stores when the column is 16-byte aligned and all rows are below nrows,

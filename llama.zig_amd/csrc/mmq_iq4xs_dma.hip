@@ -32,11 +32,11 @@ namespace {
 constexpr int WIN = 144;          // bytes of a row's window in LDS
 constexpr int ABYTES = BM * WIN;  // 18432: 18 transfers of 1 KiB
 
-template <int BN>
+template <int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
-    float *__restrict__ partial, int gx, int gy, int gz) {
+    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp) {
     constexpr int TJ = BN / 32;
     constexpr int NQB = BN / 4;   // 1 KiB transfers of the B codes per step (4 columns each)
     constexpr int NQD = BN / 32;  // 1 KiB transfers of the B headers per step (32 columns each)
@@ -52,8 +52,24 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     const int wr = wave * 32;
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
-    if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
-    const int64_t row0 = (int64_t)bx * BM, col0 = (int64_t)by * BN;
+    int64_t col0, col_end = ncols;
+    const uint8_t *wexp = w;
+    if constexpr (GROUPED) {
+        if ((int)blockIdx.y >= *grp.n_tiles) return;  // uniform per workgroup
+        const int4 t = *reinterpret_cast<const int4 *>(grp.tiles + 4 * blockIdx.y);
+        wexp = w + (int64_t)t.x * grp.expert_stride;
+        col0 = t.y;
+        col_end = t.z;
+    } else {
+        if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
+        col0 = (int64_t)by * BN;
+    }
+    // activation row of tile column c (clamped into the tile)
+    auto src_col = [&](int64_t c) -> int64_t {
+        const int64_t cc = c < col_end ? c : col0;
+        return GROUPED ? (int64_t)grp.col_src[cc] : cc;
+    };
+    const int64_t row0 = (int64_t)bx * BM;
     const int nkb = (int)(K / QK_K);  // even
     const int kb0 = nkb * (int)blockIdx.z / gz, kb1 = nkb * ((int)blockIdx.z + 1) / gz;
 
@@ -64,23 +80,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
         const int t = wave + 4 * i < 18 ? wave + 4 * i : 0;
         const int pos = t * 1024 + lane * 16, r = pos / WIN;
         const int64_t rr = row0 + r < nrows ? row0 + r : nrows - 1;
-        a_src[i] = w + rr * row_stride + (pos - r * WIN);
+        a_src[i] = wexp + rr * row_stride + (pos - r * WIN);
     }
     const int8_t *b_src[(NQB + 3) / 4];
 #pragma unroll
     for (int i = 0; i < (NQB + 3) / 4; ++i) {
         const int t = wave + 4 * i < NQB ? wave + 4 * i : 0;
         const int n = 4 * t + (lane >> 4);
-        const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        b_src[i] = yqs + c * Kp + 16 * ((lane & 15) ^ (n & 15));
+        b_src[i] = yqs + src_col(col0 + n) * Kp + 16 * ((lane & 15) ^ (n & 15));
     }
     // column headers (waves 2 .. 1 + NQD, which take one A transfer fewer):
     // transfer t, lane l -> column 32 t + l / 2, blocks 4 (l & 1) .. +3
     const uint32_t *d_src;
     {
         const int n = 32 * (wave >= 2 && wave - 2 < NQD ? wave - 2 : 0) + (lane >> 1);
-        const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        d_src = yds + c * (Kp / QK8) + 4 * (lane & 1);
+        d_src = yds + src_col(col0 + n) * (Kp / QK8) + 4 * (lane & 1);
     }
 
     auto dma = [&](int kb, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
@@ -223,31 +237,40 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int64_t c = col0 + 32 * j + li;
-        if (c >= ncols) continue;
-        float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + c * dst_col_stride;
+        if (c >= col_end) continue;
+        float *o = GROUPED   ? dst + (int64_t)grp.col_dst[c] * dst_col_stride
+                   : partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows
+                             : dst + c * dst_col_stride;
         store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
     }
 }
 
 }  // namespace
 
-// Launch for mmq.hip's dispatch: dense IQ4_XS on rows of K % 512 == 0 at
-// 16-byte aligned addresses and strides, 16-byte aligned activation planes,
-// K parts of an even number of super-blocks (the caller checks).  `grid` is
-// (row tiles, column tiles, K parts).
+// Launch for mmq.hip's dispatch: IQ4_XS on rows of K % 512 == 0 at 16-byte
+// aligned addresses and strides, 16-byte aligned activation planes, K parts
+// of an even number of super-blocks (the caller checks).  `grid` is (row
+// tiles, column tiles, K parts); with `grp`, (row tiles, the tile table's
+// bound, 1).
 int mmq_iq4xs_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                          const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                         hipStream_t s) {
+                         const MmqGroups *grp, hipStream_t s) {
     if (K % 512 || (K / QK_K) % (2 * (int64_t)grid.z) || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF ||
-        nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
+        nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF || (grp && (grid.z != 1 || partial)))
         return (int)hipErrorInvalidValue;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
-    if (bn == 32)
-        hipLaunchKernelGGL((mmq_iq4xs_dma_kernel<32>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
-                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
-    else
-        hipLaunchKernelGGL((mmq_iq4xs_dma_kernel<64>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,
-                           ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z);
+    const MmqGroups g = grp ? *grp : MmqGroups{};
+#define IQ4XS_LAUNCH(BNV, GR)                                                                                          \
+    hipLaunchKernelGGL((mmq_iq4xs_dma_kernel<BNV, GR>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,\
+                       ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g)
+    if (grp) {
+        if (bn == 32) IQ4XS_LAUNCH(32, true);
+        else IQ4XS_LAUNCH(64, true);
+    } else {
+        if (bn == 32) IQ4XS_LAUNCH(32, false);
+        else IQ4XS_LAUNCH(64, false);
+    }
+#undef IQ4XS_LAUNCH
     return (int)hipGetLastError();
 }

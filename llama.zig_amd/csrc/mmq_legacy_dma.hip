@@ -121,11 +121,11 @@ __device__ __forceinline__ void legacy_a(const uint8_t *row, int lh, uint32_t ke
     asc = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
 }
 
-template <int TYPE, int BN>
+template <int TYPE, int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
-    float *__restrict__ partial, int gx, int gy, int gz) {
+    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp) {
     using L = Legacy<TYPE>;
     constexpr int KSTEP = L::KSTEP, NB = L::NB, STEP_BYTES = L::STEP_BYTES;
     constexpr int TJ = BN / 32;
@@ -148,11 +148,27 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     const int wr = wave * 32;
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
-    if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
-    const int64_t row0 = (int64_t)bx * BM, col0 = (int64_t)by * BN;
+    int64_t col0, col_end = ncols;
+    const uint8_t *wexp = w;
+    if constexpr (GROUPED) {
+        if ((int)blockIdx.y >= *grp.n_tiles) return;  // uniform per workgroup
+        const int4 t = *reinterpret_cast<const int4 *>(grp.tiles + 4 * blockIdx.y);
+        wexp = w + (int64_t)t.x * grp.expert_stride;
+        col0 = t.y;
+        col_end = t.z;
+    } else {
+        if (gz == 1) mmq_tile_order(bx + gx * by, gx, gy, bx, by);
+        col0 = (int64_t)by * BN;
+    }
+    // activation row of tile column c (clamped into the tile)
+    auto src_col = [&](int64_t c) -> int64_t {
+        const int64_t cc = c < col_end ? c : col0;
+        return GROUPED ? (int64_t)grp.col_src[cc] : cc;
+    };
+    const int64_t row0 = (int64_t)bx * BM;
     // a K part takes whole 256-value super-steps (SPS steps each), as the
-    // split factor counts them; the loop below takes steps in pairs, so a
-    // Q4_0 part needs an even number of super-steps (the caller checks)
+    // split factor counts them; for Q8_0 (SPS = 2) every part starts on an
+    // even step
     constexpr int SPS = 256 / KSTEP;
     const int nss = (int)(K / 256);
     const int s_begin = SPS * (nss * (int)blockIdx.z / gz), s_end = SPS * (nss * ((int)blockIdx.z + 1) / gz);
@@ -164,7 +180,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
         const int t = wave + 4 * i < 18 ? wave + 4 * i : 0;
         const int pos = t * 1024 + lane * 16, r = pos / WIN;
         const int64_t rr = row0 + r < nrows ? row0 + r : nrows - 1;
-        a_src[i] = w + rr * row_stride + (pos - r * WIN);
+        a_src[i] = wexp + rr * row_stride + (pos - r * WIN);
     }
     const int8_t *b_src[(NQB + 3) / 4];
 #pragma unroll
@@ -172,8 +188,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
         const int t = wave + 4 * i < NQB ? wave + 4 * i : 0;
         // transfer t covers 1024 / (16 NCH) columns; lane -> (column, slot)
         const int n = t * (64 / NCH) + lane / NCH, slot = lane % NCH;
-        const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        b_src[i] = yqs + c * Kp + 16 * (slot ^ bswz(n));
+        b_src[i] = yqs + src_col(col0 + n) * Kp + 16 * (slot ^ bswz(n));
     }
     // column headers (waves 2 .. 1 + NQD): 16-byte runs of NB headers per
     // column; transfer t, lane l -> column (64 t + l) / (NB / 4), part
@@ -183,8 +198,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
         const int q = (wave >= 2 && wave - 2 < NQD ? wave - 2 : 0) * 64 + lane;
         const int n0 = q / per, part = q % per;
         const int n = n0 < BN ? n0 : 0;
-        const int64_t c = col0 + n < ncols ? col0 + n : col0;
-        d_src = yds + c * (Kp / QK8) + 4 * part;
+        d_src = yds + src_col(col0 + n) * (Kp / QK8) + 4 * part;
     }
 
     auto dma = [&](int s, uint8_t *sA, uint8_t *sB, uint32_t *sD) {
@@ -281,51 +295,65 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     dma(s_begin, sA0, sB0, sD0);
     wait_vmem();
     __syncthreads();
+    // steps in pairs from an even s_begin (Q8_0: window shift 0, then 8);
+    // a Q4_0 part may end on an odd step
     for (int s = s_begin; s < s_end; s += 2) {
-        dma(s + 1, sA1, sB1, sD1);  // the part holds an even number of steps
+        if (s + 1 < s_end) dma(s + 1, sA1, sB1, sD1);
         compute(std::integral_constant<int, 0>{}, sA0, sB0, sD0);
         wait_vmem();
         __syncthreads();
-        if (s + 2 < s_end) dma(s + 2, sA0, sB0, sD0);
-        compute(std::integral_constant<int, STEP_BYTES & 15>{}, sA1, sB1, sD1);
-        wait_vmem();
-        __syncthreads();
+        if (s + 1 < s_end) {
+            if (s + 2 < s_end) dma(s + 2, sA0, sB0, sD0);
+            compute(std::integral_constant<int, STEP_BYTES & 15>{}, sA1, sB1, sD1);
+            wait_vmem();
+            __syncthreads();
+        }
     }
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const int64_t c = col0 + 32 * j + li;
-        if (c >= ncols) continue;
-        float *o = partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows : dst + c * dst_col_stride;
+        if (c >= col_end) continue;
+        float *o = GROUPED   ? dst + (int64_t)grp.col_dst[c] * dst_col_stride
+                   : partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows
+                             : dst + c * dst_col_stride;
         store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
     }
 }
 
 }  // namespace
 
-// Launch for mmq.hip's dispatch: dense Q8_0 or Q4_0, rows of K % 256 == 0
-// at 16-byte aligned addresses and strides, 16-byte aligned activation
-// planes (the caller checks).  `grid` is (row tiles, column tiles, K parts);
-// Q4_0 parts must hold an even number of 256-value super-steps.
+// Launch for mmq.hip's dispatch: Q8_0 or Q4_0, rows of K % 256 == 0 at
+// 16-byte aligned addresses and strides, 16-byte aligned activation planes
+// (the caller checks).  `grid` is (row tiles, column tiles, K parts), with
+// `grp` (row tiles, the tile table's bound, 1).
 int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                           const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                          dim3 grid, float *partial, hipStream_t s) {
-    if (K % 256 || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF)
+                          dim3 grid, float *partial, const MmqGroups *grp, hipStream_t s) {
+    if (K % 256 || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF ||
+        (grp && (grid.z != 1 || partial)))
         return (int)hipErrorInvalidValue;
-    if (type == TYPE_Q4_0 && (K / 256) % (2 * (int64_t)grid.z)) return (int)hipErrorInvalidValue;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
-#define LEGACY_LAUNCH(T, BNV)                                                                                          \
-    hipLaunchKernelGGL((mmq_legacy_dma_kernel<T, BNV>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds, \
-                       ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z)
+    const MmqGroups g = grp ? *grp : MmqGroups{};
+#define LEGACY_LAUNCH(T, BNV, GR)                                                                                      \
+    hipLaunchKernelGGL((mmq_legacy_dma_kernel<T, BNV, GR>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, \
+                       ds, ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g)
+#define LEGACY_TYPE(T)                                                                                                 \
+    if (grp) {                                                                                                         \
+        if (bn == 32) LEGACY_LAUNCH(T, 32, true);                                                                      \
+        else LEGACY_LAUNCH(T, 64, true);                                                                               \
+    } else {                                                                                                           \
+        if (bn == 32) LEGACY_LAUNCH(T, 32, false);                                                                     \
+        else LEGACY_LAUNCH(T, 64, false);                                                                              \
+    }
     if (type == TYPE_Q8_0) {
-        if (bn == 32) LEGACY_LAUNCH(TYPE_Q8_0, 32);
-        else LEGACY_LAUNCH(TYPE_Q8_0, 64);
+        LEGACY_TYPE(TYPE_Q8_0)
     } else if (type == TYPE_Q4_0) {
-        if (bn == 32) LEGACY_LAUNCH(TYPE_Q4_0, 32);
-        else LEGACY_LAUNCH(TYPE_Q4_0, 64);
+        LEGACY_TYPE(TYPE_Q4_0)
     } else {
         return (int)hipErrorInvalidValue;
     }
+#undef LEGACY_TYPE
 #undef LEGACY_LAUNCH
     return (int)hipGetLastError();
 }
