@@ -47,15 +47,16 @@ int mmq_q4k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t 
 // mmq_legacy_dma.hip: the Q8_0 / Q4_0 kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                           const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                          dim3 grid, float *partial, const qmm_dma::MmqGroups *grp, hipStream_t s);
+                          dim3 grid, float *partial, const qmm_dma::MmqGroups *grp, const MmqGlu &glu,
+                          hipStream_t s);
 // mmq_iq4xs_dma.hip: the IQ4_XS kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_iq4xs_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                          const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                         const qmm_dma::MmqGroups *grp, hipStream_t s);
+                         const qmm_dma::MmqGroups *grp, const MmqGlu &glu, hipStream_t s);
 // mmq_q5k_dma.hip: the Q5_K kernel fed by direct global->LDS loads (dense or expert-grouped)
 int mmq_q5k_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                        const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                       const qmm_dma::MmqGroups *grp, hipStream_t s);
+                       const qmm_dma::MmqGroups *grp, const MmqGlu &glu, hipStream_t s);
 // mmq_few.hip: the Q4_K / Q8_0 / Q6_K kernel for at most 32 columns
 int mmq_few_split_k(int64_t K, int64_t nrows);
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
@@ -696,6 +697,11 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, (unsigned)gy, (unsigned)split);
     const qmm_dma::MmqGroups grp{tiles, n_tiles, col_src, col_dst, expert_stride};
+    // the direct-transfer kernels move 16-byte chunks of the weight rows
+    // (both weights' when fused) and of the activation planes
+    const bool dma_rows = (uintptr_t)w % 16 == 0 && (!glu.gate || (uintptr_t)glu.gate % 16 == 0) &&
+                          row_stride % 16 == 0 && expert_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 &&
+                          (uintptr_t)yds % 16 == 0;
     // Q4_K with 16-byte aligned operands (the transfer unit of the direct
     // global->LDS loads; the weight rows are checked by check_weights)
     if (TYPE == TYPE_Q4_K && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
@@ -703,27 +709,24 @@ int launch(const void *w, int64_t K, int64_t nrows, int64_t row_stride, int64_t 
                                        dst_col_stride, grid, tiles, n_tiles, col_src, col_dst,
                                        split > 1 ? partial : nullptr, glu, s))
             return e;
-    } else if ((TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) && !glu.gate &&
-               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && expert_stride % 16 == 0 &&
-               (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
-        // Q8_0 / Q4_0 on 16-byte aligned rows, dense or expert-grouped: direct global->LDS steps
+    } else if ((TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) && dma_rows) {
+        // Q8_0 / Q4_0 on 16-byte aligned rows, dense or expert-grouped, plain
+        // or gate/up-fused: direct global->LDS steps
         if (int e = mmq_legacy_dma_launch(TYPE, BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride,
-                                          grid, split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
+                                          grid, split > 1 ? partial : nullptr, tiles ? &grp : nullptr, glu, s))
             return e;
-    } else if (TYPE == TYPE_Q5_K && !glu.gate && (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 &&
-               expert_stride % 16 == 0 && (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+    } else if (TYPE == TYPE_Q5_K && dma_rows) {
         // Q5_K (176-byte blocks, 16-byte aligned in aligned rows), dense or
-        // expert-grouped: direct global->LDS steps
+        // expert-grouped, plain or gate/up-fused: direct global->LDS steps
         if (int e = mmq_q5k_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
-                                       split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
+                                       split > 1 ? partial : nullptr, tiles ? &grp : nullptr, glu, s))
             return e;
-    } else if (TYPE == TYPE_IQ4_XS && K % 512 == 0 && (K / QK_K) % (2 * split) == 0 && !glu.gate &&
-               (uintptr_t)w % 16 == 0 && row_stride % 16 == 0 && expert_stride % 16 == 0 &&
-               (uintptr_t)yqs % 16 == 0 && (uintptr_t)yds % 16 == 0) {
+    } else if (TYPE == TYPE_IQ4_XS && K % 512 == 0 && (K / QK_K) % (2 * split) == 0 && dma_rows) {
         // IQ4_XS on 16-byte aligned rows of K % 512 == 0 (super-blocks in
-        // 16-byte aligned pairs), dense or expert-grouped: direct global->LDS steps
+        // 16-byte aligned pairs), dense or expert-grouped, plain or
+        // gate/up-fused: direct global->LDS steps
         if (int e = mmq_iq4xs_dma_launch(BN, w, K, nrows, row_stride, yqs, yds, ncols, dst, dst_col_stride, grid,
-                                         split > 1 ? partial : nullptr, tiles ? &grp : nullptr, s))
+                                         split > 1 ? partial : nullptr, tiles ? &grp : nullptr, glu, s))
             return e;
     } else {
         hipLaunchKernelGGL((mmq_kernel<TYPE, BN>), grid, dim3(NTHREADS), 0, s, (const uint8_t *)w, K, nrows,

@@ -36,7 +36,7 @@ template <int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
-    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp) {
+    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp, MmqGlu glu) {
     constexpr int TJ = BN / 32;
     constexpr int NQB = BN / 4;   // 1 KiB transfers of the B codes per step (4 columns each)
     constexpr int NQD = BN / 32;  // 1 KiB transfers of the B headers per step (32 columns each)
@@ -53,11 +53,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
     int64_t col0, col_end = ncols;
-    const uint8_t *wexp = w;
+    // gate/up/GLU fusion (glu.gate != nullptr): 64 output rows per tile, tile
+    // row t from the gate (t % 4 < 2) or up weights of output row
+    // mmq_glu_tile_row(t); no K split
+    const bool fused = glu.gate != nullptr;  // uniform
+    const uint8_t *wexp = w, *wgexp = glu.gate;
     if constexpr (GROUPED) {
         if ((int)blockIdx.y >= *grp.n_tiles) return;  // uniform per workgroup
         const int4 t = *reinterpret_cast<const int4 *>(grp.tiles + 4 * blockIdx.y);
         wexp = w + (int64_t)t.x * grp.expert_stride;
+        if (fused) wgexp = glu.gate + (int64_t)t.x * grp.expert_stride;
         col0 = t.y;
         col_end = t.z;
     } else {
@@ -69,7 +74,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
         const int64_t cc = c < col_end ? c : col0;
         return GROUPED ? (int64_t)grp.col_src[cc] : cc;
     };
-    const int64_t row0 = (int64_t)bx * BM;
+    const int64_t row0 = (int64_t)bx * (fused ? BM / 2 : BM);  // first output row
     const int nkb = (int)(K / QK_K);  // even
     const int kb0 = nkb * (int)blockIdx.z / gz, kb1 = nkb * ((int)blockIdx.z + 1) / gz;
 
@@ -79,8 +84,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     for (int i = 0; i < (18 + 3) / 4; ++i) {
         const int t = wave + 4 * i < 18 ? wave + 4 * i : 0;
         const int pos = t * 1024 + lane * 16, r = pos / WIN;
-        const int64_t rr = row0 + r < nrows ? row0 + r : nrows - 1;
-        a_src[i] = wexp + rr * row_stride + (pos - r * WIN);
+        const int64_t orow = row0 + (fused ? mmq_glu_tile_row(r) : r);
+        const int64_t rr = orow < nrows ? orow : nrows - 1;
+        a_src[i] = (fused && (r & 2) == 0 ? wgexp : wexp) + rr * row_stride + (pos - r * WIN);
     }
     const int8_t *b_src[(NQB + 3) / 4];
 #pragma unroll
@@ -241,7 +247,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
         float *o = GROUPED   ? dst + (int64_t)grp.col_dst[c] * dst_col_stride
                    : partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows
                              : dst + c * dst_col_stride;
-        store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
+        if (fused) store_glu_column(o, row0 + wr / 2 + 2 * lh, nrows, acc[j], glu);
+        else store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
     }
 }
 
@@ -254,16 +261,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
 // bound, 1).
 int mmq_iq4xs_dma_launch(int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *yqs,
                          const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride, dim3 grid, float *partial,
-                         const MmqGroups *grp, hipStream_t s) {
+                         const MmqGroups *grp, const MmqGlu &glu, hipStream_t s) {
     if (K % 512 || (K / QK_K) % (2 * (int64_t)grid.z) || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF ||
-        nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF || (grp && (grid.z != 1 || partial)))
+        nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF || ((grp || glu.gate) && (grid.z != 1 || partial)))
         return (int)hipErrorInvalidValue;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     const MmqGroups g = grp ? *grp : MmqGroups{};
 #define IQ4XS_LAUNCH(BNV, GR)                                                                                          \
     hipLaunchKernelGGL((mmq_iq4xs_dma_kernel<BNV, GR>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, ds,\
-                       ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g)
+                       ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g, glu)
     if (grp) {
         if (bn == 32) IQ4XS_LAUNCH(32, true);
         else IQ4XS_LAUNCH(64, true);

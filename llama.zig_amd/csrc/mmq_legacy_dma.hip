@@ -125,7 +125,7 @@ template <int TYPE, int BN, bool GROUPED>
 __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int64_t ncols, float *__restrict__ dst, int64_t dst_col_stride,
-    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp) {
+    float *__restrict__ partial, int gx, int gy, int gz, MmqGroups grp, MmqGlu glu) {
     using L = Legacy<TYPE>;
     constexpr int KSTEP = L::KSTEP, NB = L::NB, STEP_BYTES = L::STEP_BYTES;
     constexpr int TJ = BN / 32;
@@ -149,11 +149,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
     int64_t col0, col_end = ncols;
-    const uint8_t *wexp = w;
+    // gate/up/GLU fusion (glu.gate != nullptr): 64 output rows per tile, tile
+    // row t from the gate (t % 4 < 2) or up weights of output row
+    // mmq_glu_tile_row(t); no K split
+    const bool fused = glu.gate != nullptr;  // uniform
+    const uint8_t *wexp = w, *wgexp = glu.gate;
     if constexpr (GROUPED) {
         if ((int)blockIdx.y >= *grp.n_tiles) return;  // uniform per workgroup
         const int4 t = *reinterpret_cast<const int4 *>(grp.tiles + 4 * blockIdx.y);
         wexp = w + (int64_t)t.x * grp.expert_stride;
+        if (fused) wgexp = glu.gate + (int64_t)t.x * grp.expert_stride;
         col0 = t.y;
         col_end = t.z;
     } else {
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
         const int64_t cc = c < col_end ? c : col0;
         return GROUPED ? (int64_t)grp.col_src[cc] : cc;
     };
-    const int64_t row0 = (int64_t)bx * BM;
+    const int64_t row0 = (int64_t)bx * (fused ? BM / 2 : BM);  // first output row
     // a K part takes whole 256-value super-steps (SPS steps each), as the
     // split factor counts them; for Q8_0 (SPS = 2) every part starts on an
     // even step
@@ -179,8 +184,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
     for (int i = 0; i < (18 + 3) / 4; ++i) {
         const int t = wave + 4 * i < 18 ? wave + 4 * i : 0;
         const int pos = t * 1024 + lane * 16, r = pos / WIN;
-        const int64_t rr = row0 + r < nrows ? row0 + r : nrows - 1;
-        a_src[i] = wexp + rr * row_stride + (pos - r * WIN);
+        const int64_t orow = row0 + (fused ? mmq_glu_tile_row(r) : r);
+        const int64_t rr = orow < nrows ? orow : nrows - 1;
+        a_src[i] = (fused && (r & 2) == 0 ? wgexp : wexp) + rr * row_stride + (pos - r * WIN);
     }
     const int8_t *b_src[(NQB + 3) / 4];
 #pragma unroll
@@ -316,7 +322,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
         float *o = GROUPED   ? dst + (int64_t)grp.col_dst[c] * dst_col_stride
                    : partial ? partial + ((int64_t)blockIdx.z * ncols + c) * nrows
                              : dst + c * dst_col_stride;
-        store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
+        if (fused) store_glu_column(o, row0 + wr / 2 + 2 * lh, nrows, acc[j], glu);
+        else store_tile_column(o, row0 + wr + 4 * lh, nrows, acc[j]);
     }
 }
 
@@ -328,16 +335,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
 // `grp` (row tiles, the tile table's bound, 1).
 int mmq_legacy_dma_launch(int type, int bn, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                           const int8_t *yqs, const void *yds, int64_t ncols, float *dst, int64_t dst_col_stride,
-                          dim3 grid, float *partial, const MmqGroups *grp, hipStream_t s) {
+                          dim3 grid, float *partial, const MmqGroups *grp, const MmqGlu &glu, hipStream_t s) {
     if (K % 256 || (int64_t)grid.x * grid.y * grid.z > 0x7FFFFFFF || nrows > 0x7FFFFFFF || ncols > 0x7FFFFFFF ||
-        (grp && (grid.z != 1 || partial)))
+        ((grp || glu.gate) && (grid.z != 1 || partial)))
         return (int)hipErrorInvalidValue;
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     const MmqGroups g = grp ? *grp : MmqGroups{};
 #define LEGACY_LAUNCH(T, BNV, GR)                                                                                      \
     hipLaunchKernelGGL((mmq_legacy_dma_kernel<T, BNV, GR>), grid, dim3(NTHREADS), 0, s, wb, K, nrows, row_stride, yqs, \
-                       ds, ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g)
+                       ds, ncols, dst, dst_col_stride, partial, (int)grid.x, (int)grid.y, (int)grid.z, g, glu)
 #define LEGACY_TYPE(T)                                                                                                 \
     if (grp) {                                                                                                         \
         if (bn == 32) LEGACY_LAUNCH(T, 32, true);                                                                      \
