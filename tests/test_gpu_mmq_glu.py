@@ -174,11 +174,20 @@ def _experts(t, n_as, nrows, K, idx):
 @pytest.mark.parametrize("tname,n_as,nrows,K,n_tokens,n_ids", [("Q4_K", 16, 192, 1024, 64, 4),
                                                                ("Q4_K", 4, 130, 512, 60, 4),
                                                                ("Q6_K", 8, 128, 512, 40, 2),
-                                                               ("Q8_0", 8, 100, 1024, 33, 2)])
+                                                               ("Q8_0", 8, 100, 1024, 33, 2),
+                                                               ("Q8_0", 4, 200, 768, 70, 2),
+                                                               ("Q4_0", 8, 100, 1024, 33, 2),
+                                                               ("Q4_0", 4, 200, 768, 70, 2),
+                                                               ("Q5_K", 8, 100, 1024, 33, 2),
+                                                               ("Q5_K", 4, 200, 768, 70, 2),
+                                                               ("IQ4_XS", 8, 100, 1024, 33, 2),
+                                                               ("IQ4_XS", 4, 200, 1024, 70, 2)])
 def test_mul_mat_id_glu_equals_unfused(tname, n_as, nrows, K, n_tokens, n_ids):
     """Grouped fused MMQ == the GLU of two grouped MMQs, bit for bit; 16
     experts x 16 routed columns run 32-column tiles (the persistent loop for
-    Q4_K), 4 experts x 60 run 64-column tiles."""
+    Q4_K), 4 experts x 60 run 64-column tiles.  Every direct-transfer type
+    takes both widths, partial row tiles and (Q4_0 at K = 768) an odd number
+    of K-steps; both the fused and the unfused results pass the CPU gate."""
     import ggml_hip as G
     t = TYPES[tname]
     wq, wgq = _experts(t, n_as, nrows, K, 0), _experts(t, n_as, nrows, K, 1)
