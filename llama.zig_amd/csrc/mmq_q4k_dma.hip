@@ -46,7 +46,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     constexpr int NQD = BN / 32;   // 1 KiB transfers of B headers per step
     __shared__ alignas(16) uint8_t sA0[ABYTES], sA1[ABYTES];
     __shared__ alignas(16) uint8_t sB0[BN * 256], sB1[BN * 256];
-    __shared__ alignas(16) uint32_t sD0[BN * 8], sD1[BN * 8];
+    // each stage's header table and, after it, a zero block of 4 words that
+    // the transfers never write (read by the scale MFMA's dead lane half)
+    __shared__ alignas(16) uint32_t sD0[BN * 8 + 4], sD1[BN * 8 + 4];
     __shared__ alignas(16) float rowd[4][2][32];
 
     const int64_t Kp = pad_k(K);
@@ -54,6 +56,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int wr = wave * 32;
+    // the zero blocks (published by the first barrier, before any contraction)
+    if (threadIdx.x < 8) (threadIdx.x < 4 ? sD0 : sD1)[BN * 8 + (threadIdx.x & 3)] = 0u;
 
     // Work items (row tile, column tile, K part), row tiles fastest; the
     // workgroups take items blockIdx.x, +gridDim.x, ...  Grouped mode has
@@ -162,13 +166,21 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
-    // Scale outer product per group g on the f16 MFMA with one live K slot:
-    // groups 0-3 live in slot 0 of lane half 0, groups 4-7 in slot 4 (slot 0
-    // of lane half 1).  A lane of half h decodes only sub-blocks 4h..4h+3
-    // (their scales and mins); its A operand for group g is sc_{4h + g%4},
-    // live when h == g/4 and otherwise paired with a zero B slot.
-    const uint32_t mask_hi = (0u - (uint32_t)lh) & 0xFFFFu, mask_lo = mask_hi ^ 0xFFFFu;
+    // Scale outer product per group g on the f16 MFMA with one live K slot.
+    // A lane of half h decodes only sub-blocks 4h..4h+3 (their scales and
+    // mins); its A operand for group g is sc_{4h + g%4} in slot 0 (g even)
+    // or slot 2 (g odd), zero elsewhere.  Its B operand is the raw pair of
+    // (d8 | s8 << 16) headers of groups 2(g/2), 2(g/2)+1, so slot 0 / 2 hold
+    // d8 of the even / odd group.  A lane reads its own half's headers (groups
+    // 4h..4h+3) and, for the other half's groups, the zero block that follows
+    // each stage's header table: a group is live in one lane half only.
     const uint32_t sel_s8 = 0x07060302u;  // s8 halves of two headers -> one dword
+    int hoff[TJ][2];  // word offsets of the lane's header reads from the stage's table
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        hoff[j][0] = lh ? BN * 8 : (32 * j + li) * 8;
+        hoff[j][1] = lh ? (32 * j + li) * 8 + 4 : BN * 8;
+    }
 
     auto compute = [&](const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
         const uint8_t *arow = sA + (wr + li) * Q4K_BYTES;
@@ -179,12 +191,17 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
                              (~hsel & hdr.y & 0x3F3F3F3Fu);
         const uint32_t mnb = (hsel & (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u))) |
                              (~hsel & hdr.z & 0x3F3F3F3Fu);
-        uint32_t sa[4], mh[4];
+        uint32_t sa[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sa[t] = f16_bits((float)((scb >> (8 * t)) & 0xFFu));
-            mh[t] = f16_bits((float)((mnb >> (8 * t)) & 0xFFu));
-        }
+        for (int t = 0; t < 4; ++t) sa[t] = f16_bits((float)((scb >> (8 * t)) & 0xFFu));
+        // the mins as packed f16 pairs: 0x64nn is 1024 + nn in f16 (nn < 64),
+        // so a byte permute against 0x64 bytes and one packed subtract of 1024
+        // give the exact values
+        const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const uint32_t mh01 = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, mnb, 0x07010700u)) - k1024);
+        const uint32_t mh23 = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, mnb, 0x07030702u)) - k1024);
         // row d / dmin into this wave's table (the two lanes of a row store the same values)
         rowd[wave][0][li] = h2f(hdr.x);
         rowd[wave][1][li] = h2f(hdr.x >> 16);
@@ -192,14 +209,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
         uint4 hd[TJ][2];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const uint32_t *h = sD + (32 * j + li) * 8;
-            hd[j][0] = *reinterpret_cast<const uint4 *>(h);
-            hd[j][1] = *reinterpret_cast<const uint4 *>(h + 4);
+            hd[j][0] = *reinterpret_cast<const uint4 *>(sD + hoff[j][0]);
+            hd[j][1] = *reinterpret_cast<const uint4 *>(sD + hoff[j][1]);
         }
-        auto hword = [&](int j, int g) -> uint32_t {
+        auto hpair = [&](int j, int g) -> uint2 {
             const uint4 &v = hd[j][g >> 2];
-            const int t = g & 3;
-            return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;
+            return (g & 2) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
         };
 
         struct BOps {
@@ -215,7 +230,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             if (j == 0 && (g & 1) == 0) qa = *reinterpret_cast<const uint4 *>(arow + 16 + 32 * (g >> 1) + 16 * lh);
             const int n = 32 * j + li;
             o.b = *reinterpret_cast<const v4i *>(sB + n * 256 + 16 * ((2 * g + lh) ^ (n & 15)));
-            o.sb = __builtin_bit_cast(v4h, make_uint2(hword(j, g) & (g < 4 ? mask_lo : mask_hi), 0u));
+            o.sb = __builtin_bit_cast(v4h, hpair(j, g));
         };
         auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
             const int g = p / TJ, j = p % TJ;
@@ -229,8 +244,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             const v16i z = {0};
             const v16f zf = {0};
             S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[g & 1], o.b, z, 0, 0, 0);
-            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, make_uint2(sa[g & 3], 0u)), o.sb, zf, 0,
-                                                      0, 0);
+            const uint2 as = (g & 1) ? make_uint2(0u, sa[g & 3]) : make_uint2(sa[g & 3], 0u);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, as), o.sb, zf, 0, 0, 0);
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / TJ, j = p % TJ;
@@ -271,7 +286,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q4k_dma_kernel(
             dr[4 * v4 + 0] = t.x; dr[4 * v4 + 1] = t.y; dr[4 * v4 + 2] = t.z; dr[4 * v4 + 3] = t.w;
             dm[4 * v4 + 0] = u.x; dm[4 * v4 + 1] = u.y; dm[4 * v4 + 2] = u.z; dm[4 * v4 + 3] = u.w;
         }
-        const v4h am = __builtin_bit_cast(v4h, make_uint2(mh[0] | (mh[1] << 16), mh[2] | (mh[3] << 16)));
+        const v4h am = __builtin_bit_cast(v4h, make_uint2(mh01, mh23));
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const uint4 s = *reinterpret_cast<const uint4 *>(sD + (32 * j + li) * 8 + 4 * lh);
