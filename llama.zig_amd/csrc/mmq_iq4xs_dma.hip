@@ -42,7 +42,9 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     constexpr int NQD = BN / 32;  // 1 KiB transfers of the B headers per step (32 columns each)
     __shared__ alignas(16) uint8_t sA0[ABYTES], sA1[ABYTES];
     __shared__ alignas(16) uint8_t sB0[BN * 256], sB1[BN * 256];
-    __shared__ alignas(16) uint32_t sD0[BN * 8], sD1[BN * 8];
+    // each stage's header table and, after it, a zero block of 4 words that
+    // the transfers never write (read by the scale MFMA's dead lane half)
+    __shared__ alignas(16) uint32_t sD0[BN * 8 + 4], sD1[BN * 8 + 4];
     __shared__ alignas(16) float rowd[4][32];
 
     const int64_t Kp = pad_k(K);
@@ -50,6 +52,8 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int li = lane & 31, lh = lane >> 5;
     const int wr = wave * 32;
+    // the zero blocks (published by the first barrier, before any contraction)
+    if (threadIdx.x < 8) (threadIdx.x < 4 ? sD0 : sD1)[BN * 8 + (threadIdx.x & 3)] = 0u;
 
     int bx = (int)blockIdx.x, by = (int)blockIdx.y;
     int64_t col0, col_end = ncols;
@@ -121,11 +125,19 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
     // Scale outer product per sub-block g on the f16 MFMA with one live K
-    // slot: groups 0-3 live in slot 0 of lane half 0, groups 4-7 in slot 4
-    // (slot 0 of lane half 1).  A lane of half h decodes only the scales of
-    // sub-blocks 4h..4h+3; its A operand for group g is (ls - 32) of sub-block
-    // 4h + g % 4, live when h == g / 4 and otherwise paired with a zero B slot.
-    const uint32_t mask_hi = (0u - (uint32_t)lh) & 0xFFFFu, mask_lo = mask_hi ^ 0xFFFFu;
+    // slot.  A lane of half h decodes only the scales of sub-blocks 4h..4h+3;
+    // its A operand for sub-block g is (ls - 32) of sub-block 4h + g % 4, live
+    // when h == g / 4 (the other half reads zero headers below).
+    // The A operand sits in slot 0 (g even) or slot 2 (g odd); the B operand is
+    // the raw pair of (d8 | s8 << 16) headers of groups 2(g/2), 2(g/2)+1.  A
+    // lane reads its own half's four headers and, for the other half's
+    // groups, the zero block after the stage's header table.
+    int hoff[TJ][2];  // word offsets of the lane's header reads from the stage's table
+#pragma unroll
+    for (int j = 0; j < TJ; ++j) {
+        hoff[j][0] = lh ? BN * 8 : (32 * j + li) * 8;
+        hoff[j][1] = lh ? (32 * j + li) * 8 + 4 : BN * 8;
+    }
 
     auto compute = [&](int kb, const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
         const int shift = (kb * IQ4XS_BYTES) & 15;  // 0 or 8, uniform
@@ -142,14 +154,12 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
         uint4 hd[TJ][2];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const uint32_t *h = sD + (32 * j + li) * 8;
-            hd[j][0] = *reinterpret_cast<const uint4 *>(h);
-            hd[j][1] = *reinterpret_cast<const uint4 *>(h + 4);
+            hd[j][0] = *reinterpret_cast<const uint4 *>(sD + hoff[j][0]);
+            hd[j][1] = *reinterpret_cast<const uint4 *>(sD + hoff[j][1]);
         }
-        auto hword = [&](int j, int g) -> uint32_t {
+        auto hpair = [&](int j, int g) -> uint2 {
             const uint4 &v = hd[j][g >> 2];
-            const int t = g & 3;
-            return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;
+            return (g & 2) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
         };
         struct BOps {
             v4i b;
@@ -169,15 +179,15 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_iq4xs_dma_kernel(
             const int g = p / TJ, j = p % TJ;
             const int n = 32 * j + li;
             o.b = *reinterpret_cast<const v4i *>(sB + n * 256 + 16 * ((2 * g + lh) ^ (n & 15)));
-            o.sb = __builtin_bit_cast(v4h, make_uint2(hword(j, g) & (g < 4 ? mask_lo : mask_hi), 0u));
+            o.sb = __builtin_bit_cast(v4h, hpair(j, g));
         };
         auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
             const int g = p / TJ;
             const v16i z = {0};
             const v16f zf = {0};
             S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[g & 1], o.b, z, 0, 0, 0);
-            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, make_uint2(sa[g & 3], 0u)), o.sb, zf, 0,
-                                                      0, 0);
+            const uint2 as = (g & 1) ? make_uint2(0u, sa[g & 3]) : make_uint2(sa[g & 3], 0u);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, as), o.sb, zf, 0, 0, 0);
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / TJ, j = p % TJ;

@@ -121,12 +121,14 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q5k_dma_kernel(
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
     // Scale outer product per sub-block g on the f16 MFMA with one live K
-    // slot: sub-blocks 0-3 live in slot 0 of lane half 0, 4-7 in slot 4
-    // (slot 0 of lane half 1).  A lane of half h decodes only the scales and
-    // mins of sub-blocks 4h..4h+3; its A operand for sub-block g is sc of
-    // sub-block 4h + g % 4, live when h == g / 4 and otherwise paired with a
-    // zero B slot.
-    const uint32_t mask_hi = (0u - (uint32_t)lh) & 0xFFFFu, mask_lo = mask_hi ^ 0xFFFFu;
+    // slot.  A lane of half h decodes only the scales and mins of sub-blocks
+    // 4h..4h+3; its A operand for sub-block g is sc of sub-block 4h + g % 4,
+    // live when h == g / 4 and zero in the other half.  The A operand sits in
+    // slot 0 (g even) or slot 2 (g odd); the B operand is the raw pair of
+    // (d8 | s8 << 16) headers of groups 2(g/2), 2(g/2)+1, unmasked (a zero
+    // block after each header table, as the Q4_K kernel reads for the dead
+    // half, would take this kernel's LDS past 80 KiB and one workgroup per CU).
+    const uint32_t live_lo = lh ? 0u : 0xFFFFFFFFu;  // groups 0-3 are live in lane half 0
     const uint32_t sel_s8 = 0x07060302u;  // s8 halves of two headers -> one dword
 
     auto compute = [&](const uint8_t *sA, const uint8_t *sB, const uint32_t *sD) {
@@ -138,25 +140,28 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q5k_dma_kernel(
                              (~hsel & hdr.y & 0x3F3F3F3Fu);
         const uint32_t mnb = (hsel & (((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u))) |
                              (~hsel & hdr.z & 0x3F3F3F3Fu);
-        uint32_t sa[4], mh[4];
+        uint32_t sa[4];
 #pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            sa[t] = f16_bits((float)((scb >> (8 * t)) & 0xFFu));
-            mh[t] = f16_bits((float)((mnb >> (8 * t)) & 0xFFu));
-        }
+        for (int t = 0; t < 4; ++t) sa[t] = f16_bits((float)((scb >> (8 * t)) & 0xFFu));
+        // the mins as packed f16 pairs: 0x64nn is 1024 + nn in f16 (nn < 64),
+        // so a byte permute against 0x64 bytes and one packed subtract of 1024
+        // give the exact values
+        const v2h k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
+        const uint32_t mh01 = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, mnb, 0x07010700u)) - k1024);
+        const uint32_t mh23 = __builtin_bit_cast(
+            uint32_t, __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, mnb, 0x07030702u)) - k1024);
         // fifth bits of elements 16 lh .. 16 lh + 15 (bit j: sub-block j)
         const uint4 qh = *reinterpret_cast<const uint4 *>(arow + 16 + 16 * lh);
         uint4 hd[TJ][2];
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const uint32_t *h = sD + (32 * j + li) * 8;
-            hd[j][0] = *reinterpret_cast<const uint4 *>(h);
-            hd[j][1] = *reinterpret_cast<const uint4 *>(h + 4);
+            hd[j][0] = *reinterpret_cast<const uint4 *>(sD + (32 * j + li) * 8);
+            hd[j][1] = *reinterpret_cast<const uint4 *>(sD + (32 * j + li) * 8 + 4);
         }
-        auto hword = [&](int j, int g) -> uint32_t {
+        auto hpair = [&](int j, int g) -> uint2 {
             const uint4 &v = hd[j][g >> 2];
-            const int t = g & 3;
-            return t == 0 ? v.x : t == 1 ? v.y : t == 2 ? v.z : v.w;
+            return (g & 2) ? make_uint2(v.z, v.w) : make_uint2(v.x, v.y);
         };
         struct BOps {
             v4i b;
@@ -178,15 +183,16 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q5k_dma_kernel(
             const int g = p / TJ, j = p % TJ;
             const int n = 32 * j + li;
             o.b = *reinterpret_cast<const v4i *>(sB + n * 256 + 16 * ((2 * g + lh) ^ (n & 15)));
-            o.sb = __builtin_bit_cast(v4h, make_uint2(hword(j, g) & (g < 4 ? mask_lo : mask_hi), 0u));
+            o.sb = __builtin_bit_cast(v4h, hpair(j, g));
         };
         auto issue = [&](int p, const BOps &o, v16i &S, v16f &SC) {
             const int g = p / TJ;
             const v16i z = {0};
             const v16f zf = {0};
             S = __builtin_amdgcn_mfma_i32_32x32x32_i8(aop[g & 1], o.b, z, 0, 0, 0);
-            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, make_uint2(sa[g & 3], 0u)), o.sb, zf, 0,
-                                                      0, 0);
+            const uint32_t a = sa[g & 3] & (g < 4 ? live_lo : ~live_lo);
+            const uint2 as = (g & 1) ? make_uint2(0u, a) : make_uint2(a, 0u);
+            SC = __builtin_amdgcn_mfma_f32_32x32x8f16(__builtin_bit_cast(v4h, as), o.sb, zf, 0, 0, 0);
         };
         auto consume = [&](int p, const v16i &S, const v16f &SC) {
             const int g = p / TJ, j = p % TJ;
@@ -235,7 +241,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_q5k_dma_kernel(
             dr[v] = h2f(dd);
             dm[v] = h2f(dd >> 16);
         }
-        const v4h am = __builtin_bit_cast(v4h, make_uint2(mh[0] | (mh[1] << 16), mh[2] | (mh[3] << 16)));
+        const v4h am = __builtin_bit_cast(v4h, make_uint2(mh01, mh23));
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const uint4 s = *reinterpret_cast<const uint4 *>(sD + (32 * j + li) * 8 + 4 * lh);
