@@ -97,7 +97,7 @@ struct Win16 {
 // half h reads the block's codes 16h .. 16h + 15; Q4_0 lanes read all 16
 // bytes and keep the low (h = 0) or high (h = 1) nibbles, minus 8 bytewise
 // ((n + 0x78) ^ 0x80, no carries between bytes).  The block's d goes to lanes
-// of half 0 only (keep).
+// of half 0 only (keep), in K slot 0 (I even) or 2 (I odd).
 template <int TYPE, int SH, int I>
 __device__ __forceinline__ void legacy_a(const uint8_t *row, int lh, uint32_t keep, v4i &aop, v4h &asc) {
     constexpr int BB = Legacy<TYPE>::BBYTES;
@@ -118,7 +118,7 @@ __device__ __forceinline__ void legacy_a(const uint8_t *row, int lh, uint32_t ke
         const uint32_t dw = *reinterpret_cast<const uint32_t *>(row + ((O - 2) & ~3));
         d = ((O - 2) & 3) ? dw >> 16 : dw;
     }
-    asc = __builtin_bit_cast(v4h, make_uint2(d & keep, 0u));
+    asc = __builtin_bit_cast(v4h, (I & 1) ? make_uint2(0u, d & keep) : make_uint2(d & keep, 0u));
 }
 
 template <int TYPE, int BN, bool GROUPED>
@@ -225,9 +225,10 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[j][v] = 0.0f;
 
-    // Scale outer product on the f16 MFMA with one live K slot (slot 0 of
-    // lane half 0): lanes of half 0 hand d_b of their row and d8_b of their
-    // column, lanes of half 1 zeros.
+    // Scale outer product on the f16 MFMA with one live K slot (slot 0 or 2
+    // of lane half 0 for even or odd blocks b): lanes of half 0 hand d_b of
+    // their row, lanes of half 1 zeros; the B operand is the column's raw
+    // (d8 | s8 << 16) headers of blocks b & ~1 and b | 1 as read.
     const uint32_t keep = lh ? 0u : 0xFFFFu;
 
     // the step's window starts SH bytes into its row: 0, or 8 for odd Q8_0
@@ -256,7 +257,7 @@ __global__ __launch_bounds__(NTHREADS, 2) void mmq_legacy_dma_kernel(
             const int i = p / TJ, j = p % TJ;
             const int n = 32 * j + li;
             o.b = *reinterpret_cast<const v4i *>(sB + n * KSTEP + 16 * ((2 * i + lh) ^ bswz(n)));
-            o.sb = __builtin_bit_cast(v4h, make_uint2(sD[NB * n + i] & keep, 0u));
+            o.sb = __builtin_bit_cast(v4h, *reinterpret_cast<const uint2 *>(sD + NB * n + (i & ~1)));
         };
         auto issue = [&](int p, const Ops &o, v16i &S, v16f &SC) {
             const int i = p / TJ;
