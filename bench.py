@@ -140,6 +140,27 @@ def event_time_batch(torch, launch, n):
     return a.elapsed_time(b) / n
 
 
+def event_time_replays(torch, launch, n, warm=3, reps=5):
+    """As event_time_batch, over `reps` timed replays of the graph after `warm`
+    untimed ones (the first replays after a switch of kernel run slower while
+    the clocks and caches settle): the mean per-launch time over the timed
+    replays, and each replay's per-launch time."""
+    g = capture(torch, launch, n)
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    s = torch.cuda.current_stream()
+    per = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(s)
+        g.replay()
+        b.record(s)
+        torch.cuda.synchronize()
+        per.append(a.elapsed_time(b) / n)
+    return sum(per) / len(per), per
+
+
 # ---------------------------------------------------------------- the CPU-baseline leg
 
 def _oracle():
@@ -889,11 +910,11 @@ def main():
         outt = torch.empty((T_MMQ, M), dtype=torch.float32, device=dev)
         n_m = 2 * ncopy
         mmq = lambda i: G.mmq("Q4_K", weights[i % ncopy], K, qst, dst_, out=outt)  # noqa: E731
-        mmq_avg_ms = event_time_batch(torch, mmq, n_m)
+        mmq_avg_ms, mmq_reps = event_time_replays(torch, mmq, n_m)
         _, mmq_med_ms = event_time_kernel(torch, mmq, n_m)
         wst = torch.empty(G.workspace_size("Q4_K", K, T_MMQ, M), dtype=torch.uint8, device=dev)
         op = lambda i: G.mul_mat("Q4_K", weights[i % ncopy], xt, out=outt, workspace=wst)  # noqa: E731
-        op_avg_ms = event_time_batch(torch, op, n_m)
+        op_avg_ms, op_reps = event_time_replays(torch, op, n_m)
         gpu_mmq_out = G.mul_mat("Q4_K", weights[0], xt).cpu().numpy()
         ops = 2.0 * M * K * T_MMQ
         tops = ops / (mmq_avg_ms * 1e-3) / 1e12
@@ -901,13 +922,16 @@ def main():
             "workload": f"Q4_K {M}x{K} x T={T_MMQ} (config 2)", "tops": round(tops, 2), "peak_tops": INT8_PEAK_TOPS,
             "frac": round(tops / INT8_PEAK_TOPS, 4), "avg_us": round(mmq_avg_ms * 1e3, 2),
             "event_pair_median_us": round(mmq_med_ms * 1e3, 2),
+            "replays_us": [round(v * 1e3, 2) for v in mmq_reps],
             "op_avg_us": round(op_avg_ms * 1e3, 2),
+            "op_replays_us": [round(v * 1e3, 2) for v in op_reps],
             "op": "mul_mat on f32 columns: Q8_1 quantizer + the MMQ",
             "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TOP/s",
                          "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
                          "algorithmic_ops": ops, "algorithmic_bytes_read": w_bytes + T_MMQ * (G.padded_k(K) * 9 // 8),
                          "kernel": "mmq_q4k_dma_kernel (int8 MFMA, direct-to-LDS staging)",
-                         "timing": f"HIP graph of {n_m} launches between HIP events, weights rotated over {ncopy} copies"},
+                         "timing": f"HIP graph of {n_m} launches, weights rotated over {ncopy} copies; 3 untimed "
+                                   "replays, then the mean of 5 replays each between HIP events"},
         }
 
     if not args.no_traffic:
