@@ -39,23 +39,26 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 // kernel's hardly does.  Crossovers measured on the op (hip_qmm_mul_mat, us,
 // GEMV against few-column) over 1024x14336, 2048x14336, 4096x4096,
 // 4096x14336, 8192x8192 and 14336x4096 at 3-8 columns:
-//   - Q4_K: from 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.1
-//     against 15.9) and on >= 16384 rows, from 6 at K >= 8192 on >= 2048
-//     rows, from 7 on >= 6144 rows (14336x4096: 17.4 against 16.3); the GEMV
-//     stays ahead on smaller matrices (4096x4096 at 8 columns: 9.7 against 11.2);
+//   - Q4_K: from 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.6
+//     against 16.4) and on >= 12288 rows (14336x4096, whose unsplit grid runs
+//     two K halves per workgroup: 14.8 against 14.0), from 6 at K >= 8192 on
+//     >= 2048 rows, from 7 on >= 6144 rows; the GEMV stays ahead on smaller
+//     matrices (4096x4096 at 8 columns: 9.7 against 11.1);
 //   - Q5_K / Q8_0: from 4 columns on matrices of >= 24M weights (Q5_K
-//     14336x4096 at 6: 26.4 against 17.5; Q8_0 at 4: 21.2 against 19.6), 8
-//     columns from 12M (Q5_K 4096x4096 12.0 against 11.4; Q8_0 only on rows
-//     of K >= 8192, 4096x4096 keeps the GEMV: 11.7 against 12.3);
-//   - Q4_0 / IQ4_XS: from 6 columns on >= 24M weights (Q4_0 14336x4096 at 6:
-//     21.3 against 19.8), from 5 on rows of K >= 8192 at <= 2048 or >= 8192
-//     rows (Q4_0 8192x8192 at 5: 21.5 against 18.9), 8 columns from 12M on
-//     rows of K >= 8192;
-//   - Q6_K: 7 columns from 12M weights (14336x4096: 45.1 against 34.6), 6 on
-//     >= 24M weights with K >= 8192 (4096x14336: 36.3 against 26.2); at 8
-//     columns its MFMA GEMV (more than 2048 rows) is as fast, so only rows of
-//     K >= 8192 on <= 2048 rows take the few-column kernel there (2048x14336:
-//     30.4 against 21.5).
+//     14336x4096 at 4: 18.0 against 16.0; Q8_0 4096x14336 at 4: 24.0 against
+//     21.1; at 3 columns the one-launch GEMV with the quantization fused in
+//     stays, 16.5 / 22.4 against 15.9 / 20.9), 8 columns from 12M (Q5_K
+//     4096x4096 11.8 against 11.5; Q8_0 only on rows of K >= 8192, 4096x4096
+//     keeps the GEMV: 11.7 against 12.3);
+//   - Q4_0: from 4 columns on >= 24M weights (14336x4096 at 4: 17.9 against
+//     16.5); IQ4_XS from 5 (14336x4096 at 5: 18.5 against 18.0); both from 5
+//     on rows of K >= 8192 at <= 2048 or >= 8192 rows (Q4_0 8192x8192 at 5:
+//     21.5 against 18.9), 8 columns from 12M on rows of K >= 8192;
+//   - Q6_K: 7 columns from 12M weights (14336x4096: 44.6 against 27.8), 6 on
+//     >= 24M weights (14336x4096: 31.6 against 27.7; 4096x14336: 38.3 against
+//     28.8); at 8 columns its MFMA GEMV (more than 2048 rows) is as fast, so
+//     only rows of K >= 8192 on <= 2048 rows take the few-column kernel there
+//     (2048x14336: 30.4 against 21.5).
 bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, nrows, ncols)) return false;
     const int64_t elems = nrows * K;
@@ -63,7 +66,7 @@ bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
     switch (type) {
     case TYPE_Q4_K:
         if (long_rows && nrows >= 4096) return ncols >= 5;
-        if (nrows >= 16384) return ncols >= 5;
+        if (nrows >= 12288) return ncols >= 5;
         if (long_rows && nrows >= 2048) return ncols >= 6;
         if (nrows >= 6144) return ncols >= 7;
         return false;
@@ -71,11 +74,11 @@ bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
     case TYPE_Q8_0: return (large && ncols >= 4) || (mid && long_rows && ncols == 8);
     case TYPE_Q4_0:
     case TYPE_IQ4_XS:
-        return (large && (ncols >= 6 || (long_rows && (nrows <= 2048 || nrows >= 8192) && ncols >= 5))) ||
+        return (large && (ncols >= (type == TYPE_Q4_0 ? 4 : 5) ||
+                          (long_rows && (nrows <= 2048 || nrows >= 8192) && ncols >= 5))) ||
                (mid && long_rows && ncols == 8);
     case TYPE_Q6_K:
-        return (mid && ncols == 7) || (large && long_rows && ncols == 6) ||
-               (mid && long_rows && nrows <= 2048 && ncols == 8);
+        return (mid && ncols == 7) || (large && ncols == 6) || (mid && long_rows && nrows <= 2048 && ncols == 8);
     default: return false;
     }
 }

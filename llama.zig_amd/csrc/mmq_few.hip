@@ -207,12 +207,17 @@ __device__ __forceinline__ void wait_step(bool big, int ahead) {
     }
 }
 
-// workgroups per CU that the LDS (160 KiB) holds with an NST-stage ring
+// workgroups per CU that the LDS (160 KiB) holds with KH NST-stage rings
 template <int TYPE, int NW, int NCT>
-constexpr int few_occupancy(int nst) { return 163840 / (nst * FewGeo<TYPE, NW, NCT>::STAGE); }
+constexpr int few_occupancy(int nst, int kh = 1) { return 163840 / (kh * nst * FewGeo<TYPE, NW, NCT>::STAGE); }
 
-template <int TYPE, int NST, int NW, int NCT, bool PACK>
-__global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, NW, NCT>(NST))) void mmq_few_kernel(
+// KH K halves: the workgroup's waves are KH groups of NW, each with its own
+// ring over an equal share of the workgroup's K-steps (the launcher makes the
+// step count a multiple of KH), so two waves with independent work share a
+// SIMD; the groups meet at every ring barrier (equal step counts) and add
+// their sums through LDS at the end, group 0 first (deterministic).
+template <int TYPE, int NST, int NW, int NCT, bool PACK, int KH>
+__global__ __launch_bounds__((KH * FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, NW, NCT>(NST, KH))) void mmq_few_kernel(
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int ncols, float *__restrict__ dst, int64_t dst_col_stride,
     float *__restrict__ partial) {
@@ -221,20 +226,25 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
     using FF = FewFmt<TYPE>;
     constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER, WROW = G::WROW;
     constexpr int NQA = FA / 1024;  // transfers 0 .. NQA-1 move weights
-    static_assert(NST >= 2 && few_occupancy<TYPE, NW, NCT>(NST) >= 1, "ring depth");
+    static_assert(NST >= 2 && few_occupancy<TYPE, NW, NCT>(NST, KH) >= 1, "ring depth");
     static_assert((NST - 2) * G::transfers_of(0) <= 63, "vmcnt field");
-    __shared__ alignas(16) uint8_t st[NST][G::STAGE];
+    static_assert(KH == 1 || NCT * NW * 1024 <= G::STAGE, "K-half sums fit one stage");
+    __shared__ alignas(16) uint8_t rings[KH][NST][G::STAGE];
     __shared__ alignas(16) uint4 zero16;  // the packed path's B operand for the lanes of the other sub-block
     if (PACK && threadIdx.x == 0) zero16 = make_uint4(0u, 0u, 0u, 0u);  // published by the ring's first barrier
 
     const int64_t Kp = pad_k(K);
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kh = wave_all / NW, wave = wave_all - kh * NW;  // K half, wave within it
+    uint8_t(*st)[G::STAGE] = rings[kh];
     const int li = lane & 15, kq = lane >> 4;
     const int64_t row0 = (int64_t)blockIdx.x * G::BM;
     const int nkb = (int)(K / QK_K);
     const int gz = (int)gridDim.z, z = (int)blockIdx.z;
-    const int kb0 = (int)((int64_t)nkb * z / gz), kb1 = (int)((int64_t)nkb * (z + 1) / gz);
+    const int kz0 = (int)((int64_t)nkb * z / gz), kz1 = (int)((int64_t)nkb * (z + 1) / gz);
+    const int nkh = (kz1 - kz0) / KH;  // steps per K half (the launcher makes them equal)
+    const int kb0 = kz0 + kh * nkh, kb1 = kb0 + nkh;
 
     // Per-lane sources of this wave's transfers (q = wave + NW*i), as a base
     // at K-step 0 and the bytes one K-step adds.
@@ -610,6 +620,20 @@ __global__ __launch_bounds__((FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TYPE, N
             if (++kb >= kb1) break;
         }
     }
+    if constexpr (KH > 1) {
+        // every wave's ring reads (and transfers: the last wait was vmcnt(0))
+        // are done; K half 1 hands its sums to half 0 through the first stage
+        lds_barrier();
+        v4f *part = reinterpret_cast<v4f *>(&rings[0][0][0]);
+        if (kh == 1) {
+#pragma unroll
+            for (int j = 0; j < NCT; ++j) part[(j * NW + wave) * 64 + lane] = acc[j];
+        }
+        lds_barrier();
+        if (kh == 1) return;
+#pragma unroll
+        for (int j = 0; j < NCT; ++j) acc[j] += part[(j * NW + wave) * 64 + lane];
+    }
 
     if constexpr (PACK) {
         // the odd sub-blocks' half of each output column (lanes li + 8) onto the even half
@@ -666,6 +690,20 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
     return (int)split;
 }
 
+// Whether a workgroup runs two K halves of its K part (KH = 2): K parts of
+// an even step count, at least 4.  Against one ring of 4 waves (graph-timed,
+// same box): Q4_K 14336x4096 at 8 columns 13.4-13.5 -> 11.9-12.0 us, at 16
+// 13.9-14.1 -> 13.0-13.1, at 32 18.9-19.0 -> 18.3; Q5_K at 8 15.6-15.8 ->
+// 13.7, Q4_0 18.0-18.1 -> 14.5, IQ4_XS 18.7-18.9 -> 15.5-15.6, Q8_0
+// 17.2 -> 16.7.  Two waves with independent work share each SIMD, where one
+// wave alone stalled on its own LDS and MFMA latencies.  Halving the K
+// shares of the split grids (4096 rows) in exchange for K halves measured
+// level (and slower on 1024 rows), so those keep one ring.
+bool few_k_halves(int64_t K, int split) {
+    const int64_t per = K / QK_K / split;
+    return per % 2 == 0 && per >= 4;
+}
+
 // Whether the few-column kernel takes this weight layout: Q4_K and Q5_K;
 // Q8_0, Q4_0, Q6_K and IQ4_XS with 16-byte-aligned rows (and, Q6_K,
 // K % 2048 == 0, IQ4_XS K % 512 == 0, so that their aligned windows stay
@@ -690,12 +728,18 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
         !mmq_few_takes(type, K, w, row_stride))
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, 1, (unsigned)split);
+    // two K halves per workgroup where the K parts split evenly
+    const bool khalves = few_k_halves(K, split);
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     float *pp = split > 1 ? partial : nullptr;
 #define FEW_LAUNCH_P(TYPE, NCT, PK)                                                                                    \
-    hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT, PK>), grid, dim3(64 * FEW_NW), 0, s, wb, K, nrows,  \
-                       row_stride, yqs, ds, (int)ncols, dst, dst_col_stride, pp)
+    if (khalves)                                                                                                       \
+        hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT, PK, 2>), grid, dim3(128 * FEW_NW), 0, s, wb, K, \
+                           nrows, row_stride, yqs, ds, (int)ncols, dst, dst_col_stride, pp);                           \
+    else                                                                                                               \
+        hipLaunchKernelGGL((mmq_few_kernel<TYPE, FEW_NST, FEW_NW, NCT, PK, 1>), grid, dim3(64 * FEW_NW), 0, s, wb, K,  \
+                           nrows, row_stride, yqs, ds, (int)ncols, dst, dst_col_stride, pp)
 #define FEW_LAUNCH(TYPE, NCT) FEW_LAUNCH_P(TYPE, NCT, false)
     // up to 8 columns of the K-quant nibble types: two sub-blocks per MFMA
     const bool pack = ncols <= FEW_PACK_COLS;
