@@ -54,11 +54,13 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 //     16.5); IQ4_XS from 5 (14336x4096 at 5: 18.5 against 18.0); both from 5
 //     on rows of K >= 8192 at <= 2048 or >= 8192 rows (Q4_0 8192x8192 at 5:
 //     21.5 against 18.9), 8 columns from 12M on rows of K >= 8192;
-//   - Q6_K: 7 columns from 12M weights (14336x4096: 44.6 against 27.8), 6 on
-//     >= 24M weights (14336x4096: 31.6 against 27.7; 4096x14336: 38.3 against
-//     28.8); at 8 columns its MFMA GEMV (more than 2048 rows) is as fast, so
-//     only rows of K >= 8192 on <= 2048 rows take the few-column kernel there
-//     (2048x14336: 30.4 against 21.5).
+//   - Q6_K (two 16-deep sub-blocks per MFMA up to 8 columns): from 4 columns
+//     on >= 24M weights (4096x14336 at 4 / 8: 24.7 / 27.9 against 22.4 /
+//     22.3; 14336x4096 at 4: 24.3 against 21.1; at 3 the one-launch GEMV
+//     stays, 23.0 / 19.1 against 22.6 / 21.3), 7 columns from 12M (4096x4096
+//     13.0 against 12.7), 8 columns on rows of K >= 8192 at <= 2048 rows; the
+//     GEMV stays ahead on 4096x4096 at 5, 6 and 8 columns (10.7 / 12.3 / 11.3
+//     against 12.7 / 12.8 / 12.9) and on 1024x4096.
 bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, nrows, ncols)) return false;
     const int64_t elems = nrows * K;
@@ -78,7 +80,7 @@ bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
                           (long_rows && (nrows <= 2048 || nrows >= 8192) && ncols >= 5))) ||
                (mid && long_rows && ncols == 8);
     case TYPE_Q6_K:
-        return (mid && ncols == 7) || (large && ncols == 6) || (mid && long_rows && nrows <= 2048 && ncols == 8);
+        return (large && ncols >= 4) || (mid && ncols == 7) || (mid && long_rows && nrows <= 2048 && ncols == 8);
     default: return false;
     }
 }

@@ -142,12 +142,10 @@ __device__ __forceinline__ uint2 lds8_a2(const uint8_t *p) {
     return make_uint2(__builtin_amdgcn_alignbyte(a1, a0, sh), __builtin_amdgcn_alignbyte(a2, a1, sh));
 }
 
-// Q6_K weights q (0..63 per byte) to q - 32 as signed bytes: q ^ 32 is
-// (q - 32) mod 64; its bit 5 copied into bits 6 and 7 sign-extends it.
-__device__ __forceinline__ uint32_t q6_signed(uint32_t q) {
-    const uint32_t x = q ^ 0x20202020u, t = x & 0x20202020u;
-    return x | (t << 1) | (t << 2);
-}
+// Q6_K weights q (0..63 per byte) to q - 32 as signed bytes: q + 96 stays
+// below 256 (no carry between bytes), and flipping its bit 7 gives q + 224,
+// which is q - 32 mod 256.
+__device__ __forceinline__ uint32_t q6_signed(uint32_t q) { return (q + 0x60606060u) ^ 0x80808080u; }
 
 // Q4_0 nibbles q (0..15 per byte) to q - 8 as signed bytes: q ^ 8 is
 // (q - 8) mod 16; its bit 3 copied into bits 4-7 sign-extends it.
@@ -221,7 +219,8 @@ __global__ __launch_bounds__((KH * FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TY
     const uint8_t *__restrict__ w, int64_t K, int64_t nrows, int64_t row_stride, const int8_t *__restrict__ yqs,
     const uint32_t *__restrict__ yds, int ncols, float *__restrict__ dst, int64_t dst_col_stride,
     float *__restrict__ partial) {
-    static_assert(!PACK || (NCT == 1 && (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K)), "packed: one tile, K-quant nibbles");
+    static_assert(!PACK || (NCT == 1 && (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K || TYPE == TYPE_Q6_K)),
+                  "packed: one tile, K-quants");
     using G = FewGeo<TYPE, NW, NCT>;
     using FF = FewFmt<TYPE>;
     constexpr int FA = G::A, FB = G::B, FD = G::D, FNQ = G::NQ, PER = G::PER, WROW = G::WROW;
@@ -599,6 +598,58 @@ __global__ __launch_bounds__((KH * FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TY
         }
     };
 
+    // Q6_K up to 8 columns (PACK): one v_mfma_i32_16x16x32_i8 per 32-weight
+    // window g takes both of its 16-weight sub-blocks.  Lane groups kq < 2 hold
+    // sub-block 2g and kq >= 2 sub-block 2g + 1 (as in compute_q6_k); output
+    // column li holds activation column li & 7 against sub-block 2g + (li >> 3):
+    // B is that column's codes in the lane groups of its sub-block and zero in
+    // the other two.  The scale MFMA puts sc_{2g} * d8 in K slot 0 for columns
+    // 0-7 and sc_{2g+1} * d8 in slot 1 for columns 8-15; d once per step; the
+    // two halves of an output column are added at the end.  Against two masked
+    // MFMAs per window it halves the MFMAs and the per-output convert + FMA.
+    auto compute_q6_k_pack = [&](const uint8_t *st, int kb) {
+        const int delta = (int)(((int64_t)kb * Q6K_BYTES) & 15);  // the block's start in the window
+        const uint8_t *blk = st + (wave * 16 + li) * WROW + delta;
+        const uint8_t *bcol = st + FA + pj * QK_K;
+        const uint32_t *dcol = reinterpret_cast<const uint32_t *>(st + FA + FB) + pj * 8;
+        const uint4 dh0 = *reinterpret_cast<const uint4 *>(dcol), dh1 = *reinterpret_cast<const uint4 *>(dcol + 4);
+        v4f accb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            const int n = g >> 2, m = g & 3;
+            const uint2 ql = lds8_a2(blk + 64 * n + 32 * (m & 1) + 8 * kq);
+            const uint2 qh = lds8_a2(blk + 128 + 32 * n + 8 * kq);
+            const int sl = 4 * (m >> 1), shh = 2 * m;
+            const uint2 a = make_uint2(q6_signed(((ql.x >> sl) & 0x0F0F0F0Fu) | (((qh.x >> shh) & 0x03030303u) << 4)),
+                                       q6_signed(((ql.y >> sl) & 0x0F0F0F0Fu) | (((qh.y >> shh) & 0x03030303u) << 4)));
+            // column pj's codes of sub-block 2g + phi, elements 8 (kq & 1) .. +8: chunk 2g + phi
+            const uint2 *bp = plive ? reinterpret_cast<const uint2 *>(bcol + 16 * ((2 * g + phi) ^ pj) + 8 * (kq & 1))
+                                    : reinterpret_cast<const uint2 *>(&zero16);
+            const uint2 b = *bp;
+            const v4i zi = {0, 0, 0, 0};
+            const v4i S = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_long(a), as_long(b), zi, 0, 0, 0);
+            // A: the row's int8 scales of sub-blocks 2g, 2g+1 in K slots 0, 1 of
+            // lane group 0; B: d8 of block g of column pj in slot phi
+            const uint32_t w2 = *reinterpret_cast<const uint16_t *>(blk + 192 + 2 * g);
+            const uint32_t sa2 = (f16_bits((float)(int8_t)w2) | (f16_bits((float)(int8_t)(w2 >> 8)) << 16)) & m_sc;
+            const uint4 &dh = g < 4 ? dh0 : dh1;
+            const uint32_t hw = (g & 2) ? ((g & 1) ? dh.w : dh.z) : ((g & 1) ? dh.y : dh.x);
+            const v4h sa = __builtin_bit_cast(v4h, make_uint2(sa2, 0u));
+            const v4h sbv = __builtin_bit_cast(v4h, make_uint2((hw & 0xFFFFu) << (16 * phi), 0u));
+            const v4f zf = {0.0f, 0.0f, 0.0f, 0.0f};
+            const v4f SC = __builtin_amdgcn_mfma_f32_16x16x16f16(sa, sbv, zf, 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) accb[v] = fmaf((float)S[v], SC[v], accb[v]);
+        }
+        // d of the output rows (4*kq + v of this wave's 16)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint8_t *ob = st + (wave * 16 + 4 * kq + v) * WROW + delta;
+            const float d = h2f((uint32_t)*reinterpret_cast<const uint16_t *>(ob + 208));
+            acc[0][v] = fmaf(d, accb[v], acc[0][v]);
+        }
+    };
+
     // NST-stage ring: step kb0 + i lives in stage i % NST; while a step is
     // contracted, the next NST - 2 are in flight and one more is issued
     const bool big = wave < FNQ % NW || FNQ % NW == 0;
@@ -612,7 +663,8 @@ __global__ __launch_bounds__((KH * FewGeo<TYPE, NW, NCT>::NT), (few_occupancy<TY
             wait_step<NST - 2, G::transfers_of(0), G::transfers_of(NW - 1)>(big, left < NST - 2 ? left : NST - 2);
             lds_barrier();
             if (kb + NST - 1 < kb1) dma(kb + NST - 1, st[(i + NST - 1) % NST]);
-            if constexpr (PACK) compute_pack(st[i]);
+            if constexpr (PACK && TYPE == TYPE_Q6_K) compute_q6_k_pack(st[i], kb);
+            else if constexpr (PACK) compute_pack(st[i]);
             else if constexpr (TYPE == TYPE_Q4_K || TYPE == TYPE_Q5_K) compute(st[i]);
             else if constexpr (TYPE == TYPE_Q8_0 || TYPE == TYPE_Q4_0) compute_q8_0(st[i]);
             else if constexpr (TYPE == TYPE_IQ4_XS) compute_iq4_xs(st[i], kb);
@@ -750,7 +802,8 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
         break;
     case TYPE_Q6_K:  // one column tile: two measured slower than the 128-row MMQ tile
         if (ncols > 16) return (int)hipErrorInvalidValue;
-        FEW_LAUNCH(TYPE_Q6_K, 1);
+        if (pack) FEW_LAUNCH_P(TYPE_Q6_K, 1, true);
+        else FEW_LAUNCH(TYPE_Q6_K, 1);
         break;
     case TYPE_Q5_K:
         if (ncols > 16) FEW_LAUNCH(TYPE_Q5_K, 2);

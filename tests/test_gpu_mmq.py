@@ -86,7 +86,7 @@ def test_mmq_split_k(tname, nrows, K, ncols):
                                                  ("Q4_0", 2048, 14336, 5), ("Q4_0", 6144, 4096, 6),
                                                  ("IQ4_XS", 2048, 14336, 5), ("IQ4_XS", 1024, 14336, 8),
                                                  ("Q6_K", 1024, 14336, 7), ("Q6_K", 2048, 14336, 8),
-                                                 ("Q6_K", 2048, 14336, 6)])
+                                                 ("Q6_K", 2048, 14336, 6), ("Q6_K", 4096, 14336, 4)])
 def test_op_few_columns(tname, nrows, K, ncols):
     """The op sends 4-8 columns of large matrices to the few-column GEMM
     instead of the GEMV (per type, where it measured faster): same bits as
@@ -216,15 +216,18 @@ def test_few_columns_large_weights(tname, ncols):
     np.testing.assert_array_equal(G.mul_mat(tname, w_d, x_d).cpu().numpy(), got)
 
 
-@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K"])
+@pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K"])
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 1), (1000, 4096, 2), (4100, 4096, 3), (6144, 2048, 5),
-                                           (300, 14336, 8), (64, 512, 7), (14336, 4096, 8)])
+                                           (300, 14336, 8), (64, 512, 7), (14336, 4096, 8), (4096, 14336, 6)])
 def test_few_columns_packed(tname, nrows, K, ncols):
     """Up to 8 columns the few-column kernel packs two sub-blocks into each
-    16x16x64 MFMA (output columns 0-7 against the even sub-block, 8-15 the
-    odd one, halves added at the end): within the f64 and CPU gates, split
-    and unsplit (small row counts split K), and within rounding of the GEMV
-    on the same quantized columns."""
+    MFMA (Q4_K / Q5_K: two 32-deep sub-blocks per 16x16x64, Q6_K: two 16-deep
+    sub-blocks per 16x16x32; output columns 0-7 against the even sub-block,
+    8-15 the odd one, halves added at the end): within the f64 and CPU gates,
+    split and unsplit (small row counts split K; 14336 rows run two K halves
+    per workgroup), and within rounding of the GEMV on the same quantized
+    columns.  Q6_K at K = 512 is not the few-column kernel's (its aligned
+    windows need K % 2048 == 0) and runs the tile."""
     import ggml_hip as G
     t = TYPES[tname]
     wq = weights_q(t, nrows, K)
