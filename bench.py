@@ -451,14 +451,18 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
                 n = len(ws) * reps
                 mmq_ws = torch.empty(max(1, int(G.lib().hip_qmm_mmq_workspace_size(G.TYPE_IDS[qtype], Kx, M, T))),
                                      dtype=torch.uint8, device=dev)
-                if T <= 8:
-                    fn = lambda i: G.mul_mat_vec(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
-                    kern = "gemv"
+                # the kernel the op takes for these columns (the GEMV up to 8
+                # columns except where the few-column GEMM measured faster)
+                gemv_fn = lambda i: G.mul_mat_vec(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
+                mmq_fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
+                if T <= 8 and not G.lib().hip_qmm_mul_mat_uses_mmq(G.TYPE_IDS[qtype], Kx, M, T):
+                    fn, kern = gemv_fn, "gemv"
                 else:
-                    fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
-                    kern = "mmq"
+                    fn, kern = mmq_fn, ("mmq few-column" if T <= 8 else "mmq")
                 ms = event_time_batch(torch, fn, n)
                 extra = {}
+                if T <= 8 and kern != "gemv":
+                    extra["gemv_us"] = round(event_time_batch(torch, gemv_fn, n) * 1e3, 3)
                 if name == "few":
                     # the few-column GEMM at every width (next to the GEMV up
                     # to 8 columns)

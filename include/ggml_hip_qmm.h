@@ -75,6 +75,13 @@ int hip_qmm_quantize_q8_1_planar(const float *x, int64_t K, int64_t ncols, int64
  * MMQ spreads K over several workgroups. */
 size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
+/* 1 if hip_qmm_mul_mat runs an MMQ kernel (the few-column GEMM or the tile)
+ * rather than the GEMV for this shape on 16-byte-aligned rows, else 0 (the
+ * shape rules that hip_qmm_mul_mat_workspace_size applies).  No counterpart
+ * in the reference: a query for measurement and tests that time or check the
+ * kernel the op takes. */
+int hip_qmm_mul_mat_uses_mmq(int type, int64_t K, int64_t nrows, int64_t ncols);
+
 /*
  * Decode GEMV against planar Q8_1 activations, 1..8 columns: dst[c*dst_col_stride + r]
  * = sum_k W[r,k] * y[c,k].  Replaces mul_mat_vec_q_switch_type
@@ -261,9 +268,10 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
  *  - the few-column GEMM (16x16 int8 MFMA tiles) for 9-32 columns (9-16 for
  *    Q6_K; Q8_0 / Q4_0 at 17-32 columns of 8 MiB of weights and more take the
  *    tile), and also for 4-8 columns of large matrices, where it measured
- *    faster than the GEMV (the shape rules are hip_qmm_mul_mat_workspace_size's:
- *    e.g. Q4_K from 5 columns at K >= 8192 on >= 4096 rows, from 7 columns on
- *    >= 6144 rows).  On those 4-8 column shapes the workspace grows by the
+ *    faster than the GEMV (the shape rules are hip_qmm_mul_mat_workspace_size's
+ *    and hip_qmm_mul_mat_uses_mmq's: e.g. Q4_K from 5 columns at K >= 8192 on
+ *    >= 4096 rows and on >= 12288 rows, from 7 columns on >= 6144 rows; Q6_K
+ *    from 4 columns on >= 24M weights).  On those 4-8 column shapes the workspace grows by the
  *    few-column kernel's split-K partials, and the results differ from
  *    hip_qmm_mul_mat_vec's in fp32 rounding (another summation order; both
  *    pass the f64 and CPU gates);

@@ -124,6 +124,10 @@ extern "C" size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nr
     return n;
 }
 
+extern "C" int hip_qmm_mul_mat_uses_mmq(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return K > 0 && nrows > 0 && ncols > 1 && use_mmq(type, K, nrows, ncols) ? 1 : 0;
+}
+
 extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride,
                                const float *x, int64_t ncols, int64_t x_col_stride, float *dst,
                                int64_t dst_col_stride, void *workspace, size_t workspace_size, void *stream) {

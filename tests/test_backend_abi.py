@@ -303,3 +303,22 @@ def test_supports_add_id(L):
     assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, b, bad_ids)))
     f16_ids = abi.make_tensor(abi.GGML_TYPE_F16, [8, 5], name=b"ids")
     assert not ok(abi.make_tensor(abi.GGML_TYPE_F32, [768, 8, 5], op=abi.GGML_OP_ADD_ID, srcs=(a, b, f16_ids)))
+
+
+def test_mul_mat_route_query(L):
+    """hip_qmm_mul_mat_uses_mmq answers the op's shape rules without a device:
+    the GEMV for one column and for small matrices, the few-column GEMM for
+    4-8 columns of large ones (per type), the MMQ from 9 columns on."""
+    L.hip_qmm_mul_mat_uses_mmq.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int64]
+    q4k, q6k, q8_0 = 12, 14, 8
+    q = lambda t, K, rows, cols: L.hip_qmm_mul_mat_uses_mmq(t, K, rows, cols)  # noqa: E731
+    assert q(q4k, 4096, 14336, 1) == 0 and q(q4k, 4096, 14336, 4) == 0
+    assert q(q4k, 4096, 14336, 5) == 1 and q(q4k, 4096, 14336, 8) == 1
+    assert q(q4k, 4096, 4096, 8) == 0 and q(q4k, 4096, 1024, 8) == 0
+    assert q(q4k, 14336, 4096, 4) == 0 and q(q4k, 14336, 4096, 5) == 1
+    assert q(q6k, 14336, 4096, 3) == 0 and q(q6k, 14336, 4096, 4) == 1 and q(q6k, 14336, 4096, 8) == 1
+    assert q(q6k, 4096, 1024, 8) == 0
+    assert q(q8_0, 4096, 14336, 3) == 0 and q(q8_0, 4096, 14336, 4) == 1
+    assert all(q(t, 4096, 4096, 9) == 1 for t in (q4k, q6k, q8_0))
+    assert q(q4k, 4000, 4096, 16) == 0  # K % 256 != 0: no MMQ
+    assert q(q4k, 4096, 0, 8) == 0 and q(q4k, 0, 4096, 8) == 0
