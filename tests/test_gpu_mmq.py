@@ -135,7 +135,7 @@ def _offset_copy(w_d, off=2):
 
 @pytest.mark.parametrize("tname", ["Q6_K", "Q8_0", "Q4_0"])
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 3), (4096, 2048, 9), (700, 14336, 17), (4100, 4096, 32),
-                                           (64, 2048, 16)])
+                                           (64, 2048, 16), (12300, 2048, 12)])
 def test_few_columns_q6_k_q8_0(tname, nrows, K, ncols):
     """Q8_0 and Q4_0 with at most 32 columns and Q6_K with at most 16 take the
     few-column kernel on 16-byte-aligned rows (Q6_K from K % 2048 == 0; Q8_0
@@ -218,7 +218,8 @@ def test_few_columns_large_weights(tname, ncols):
 
 @pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K"])
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 1), (1000, 4096, 2), (4100, 4096, 3), (6144, 2048, 5),
-                                           (300, 14336, 8), (64, 512, 7), (14336, 4096, 8), (4096, 14336, 6)])
+                                           (300, 14336, 8), (64, 512, 7), (14336, 4096, 8), (4096, 14336, 6),
+                                           (12300, 2048, 8)])
 def test_few_columns_packed(tname, nrows, K, ncols):
     """Up to 8 columns the few-column kernel packs two sub-blocks into each
     MFMA (Q4_K / Q5_K: two 32-deep sub-blocks per 16x16x64, Q6_K: two 16-deep
