@@ -795,6 +795,24 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
 // that does not leave most of a tile empty.
 extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64; }
 
+// Column-tile width of the plain MMQ: hip_qmm_mmq_tile_n's, except that the
+// Q4_K, Q5_K, Q8_0 and Q4_0 direct-transfer kernels take 32-column tiles up to
+// 128 columns on rows of at most 16 K-steps, where twice the column tiles
+// fill the grid with fewer K shares.  Graph-timed against 64 columns (A/B of
+// both libraries, same box): Q4_K 14336x4096 at 48 / 64 / 96 / 128 columns
+// 28.4-28.5 / 29.5-29.9 / 39.0 / 41.2 -> 25.9-26.2 / 27.0-27.1 / 35.0-35.1 /
+// 38.6-38.8 us, 4096x4096 at 128 20.8 -> 18.7-18.8, 1024x4096 at 128 13.5 ->
+// 11.2; 14336x4096 at 128 Q8_0 43.4-43.7 -> 42.0-42.5, Q5_K 44.4-45.4 ->
+// 42.1-42.6, Q4_0 41.7-41.8 -> 39.2-39.9.  Longer rows keep 64 (Q4_K
+// 4096x14336 at 128: 36.9-37.2 against 38.8-39.2), and so do IQ4_XS (46.4-44.8
+// against 47.6-48.0) and the staged kernel (Q6_K 14336x4096 at 128: 70.5-71.8
+// against 77.7-80.0).
+int mmq_bn(int type, int64_t K, int64_t ncols) {
+    if (ncols <= 32) return 32;
+    const bool narrow = type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K || type == TYPE_Q4_0;
+    return narrow && ncols <= 128 && K / BK <= 16 ? 32 : 64;
+}
+
 // K-split factor: spread the K-steps over more workgroups until the grid
 // holds about one workgroup per CU (256 CUs on MI355X) for the Q4_K
 // direct-to-LDS kernel on rows of at most 16 K-steps, about two otherwise;
@@ -813,7 +831,7 @@ extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64;
 // at 256 / 512 columns 21.0 / 23.3 us against 24.0 / 30.9, 2048x4096 at 256
 // 20.7 against 23.2; 2048x4096 at 512 29.1 against 27.0).
 int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    const int64_t bn = hip_qmm_mmq_tile_n(ncols);
+    const int64_t bn = mmq_bn(type, K, ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
     const int64_t target = ((type == TYPE_Q4_K || type == TYPE_Q8_0) && nkb <= 16) ? 256 : 512;
@@ -877,7 +895,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
         return (int)hipErrorInvalidValue;
     if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
-    const int bn = hip_qmm_mmq_tile_n(ncols);
+    const int bn = mmq_bn(type, K, ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
     const bool few = few_cols_type(type, K, nrows, ncols) && mmq_few_takes(type, K, w, row_stride) &&
                      (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;

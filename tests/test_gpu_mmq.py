@@ -219,7 +219,7 @@ def test_few_columns_large_weights(tname, ncols):
 @pytest.mark.parametrize("tname", ["Q4_K", "Q5_K", "Q6_K"])
 @pytest.mark.parametrize("nrows,K,ncols", [(1000, 4096, 1), (1000, 4096, 2), (4100, 4096, 3), (6144, 2048, 5),
                                            (300, 14336, 8), (64, 512, 7), (14336, 4096, 8), (4096, 14336, 6),
-                                           (12300, 2048, 8)])
+                                           (12300, 2048, 8), (12300, 1280, 4)])
 def test_few_columns_packed(tname, nrows, K, ncols):
     """Up to 8 columns the few-column kernel packs two sub-blocks into each
     MFMA (Q4_K / Q5_K: two 32-deep sub-blocks per 16x16x64, Q6_K: two 16-deep

@@ -27,10 +27,10 @@ def _lib():
 
 
 # one case per dispatch path, in decreasing workspace: MMQ with split-K
-# partials (15.3 MB), the few-column GEMM with split-K (3.3 MB), the MMQ
+# partials (18.8 MB), the few-column GEMM with split-K (3.3 MB), the MMQ
 # (2.4 MB), quantizer + GEMV, the one-launch 2-4 column GEMV (no scratch),
 # the one-column fused GEMV (no scratch)
-CASES = [("Q4_K", 14336, 4096, 128), ("Q4_K", 4096, 4096, 24), ("Q4_K", 4096, 4096, 512), ("Q6_K", 1024, 4096, 7),
+CASES = [("Q4_K", 4096, 14336, 128), ("Q4_K", 4096, 4096, 24), ("Q4_K", 4096, 4096, 512), ("Q6_K", 1024, 4096, 7),
          ("Q8_0", 1024, 4096, 3), ("Q4_K", 4096, 4096, 1)]
 
 
