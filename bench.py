@@ -128,19 +128,31 @@ def event_time_batch(torch, launch, n):
     """Average device time per launch of n back-to-back launches: the launches
     are captured into one HIP graph, and each replay is bracketed by two HIP
     events on the replaying stream, so host launch cost cannot starve the GPU.
-    The mean of 3 timed replays after 2 untimed ones (event_time_replays)."""
+    The mean of 3 timed replays after the warm-up (event_time_replays)."""
     return event_time_replays(torch, launch, n, warm=2, reps=3)[0]
 
 
-def event_time_replays(torch, launch, n, warm=3, reps=5):
-    """As event_time_batch, over `reps` timed replays of the graph after `warm`
-    untimed ones (the first replays after a switch of kernel run slower while
-    the clocks and caches settle): the mean per-launch time over the timed
-    replays, and each replay's per-launch time."""
-    g = capture(torch, launch, n)
-    for _ in range(warm):
+WARM_S = 0.02  # untimed GPU work before a timed replay: the clocks ramp up over the first tens of ms
+
+
+def warm_up(torch, g, min_replays):
+    """Untimed replays of graph g: at least min_replays, and until WARM_S of
+    wall time has passed (the first replays after an idle period or a switch
+    of kernel run slower while the clocks settle)."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < min_replays or time.perf_counter() - t0 < WARM_S:
         g.replay()
-    torch.cuda.synchronize()
+        torch.cuda.synchronize()
+        i += 1
+
+
+def event_time_replays(torch, launch, n, warm=3, reps=5):
+    """As event_time_batch, over `reps` timed replays of the graph after the
+    warm-up (warm_up with `warm` replays at least): the mean per-launch time
+    over the timed replays, and each replay's per-launch time."""
+    g = capture(torch, launch, n)
+    warm_up(torch, g, warm)
     s = torch.cuda.current_stream()
     per = []
     for _ in range(reps):
@@ -813,8 +825,7 @@ def main():
         step(i)
     torch.cuda.synchronize()
     graph = capture(torch, step, args.steps)
-    graph.replay()
-    torch.cuda.synchronize()
+    warm_up(torch, graph, 1)  # includes the graph's upload
     t0 = time.perf_counter()
     graph.replay()
     torch.cuda.synchronize()
@@ -879,14 +890,16 @@ def main():
                    "batch": 1, "weight_copies": ncopy,
                    "step": "mul_mat: GEMV with the Q8_1 quantization fused (one kernel)",
                    "timed": f"one HIP-graph replay of exactly {args.steps} steps between synchronizes; untimed "
-                            f"before it: {args.warmup} warm-up steps and one replay of the same graph (upload)"},
+                            f"before it: {args.warmup} warm-up steps, then replays of the same graph (its upload "
+                            f"first) for at least {WARM_S * 1e3:.0f} ms"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": bytes_alg,
                      "kernel": "gemv_fx_kernel<Q4_K, 14 waves (2 workgroups per CU), 2 rows per wave> (quantize-in-GEMV)",
                      "avg_us": round(fused_batch_ms * 1e3, 3),
-                     "timing": f"HIP graph of {n_ev} launches, weights rotated over {ncopy} copies; 2 untimed "
-                               "replays, then the mean of 3 replays each between HIP events",
+                     "timing": f"HIP graph of {n_ev} launches, weights rotated over {ncopy} copies; untimed "
+                               f"replays for at least {WARM_S * 1e3:.0f} ms, then the mean of 3 replays each between "
+                               "HIP events",
                      "event_pair_avg_us": round(fused_pair_ms * 1e3, 3),
                      "event_pair_median_us": round(fused_pair_med_ms * 1e3, 3),
                      "unfused_gemv_avg_us": round(gemv_batch_ms * 1e3, 3),
@@ -927,8 +940,9 @@ def main():
                          "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
                          "algorithmic_ops": ops, "algorithmic_bytes_read": w_bytes + T_MMQ * (G.padded_k(K) * 9 // 8),
                          "kernel": "mmq_q4k_dma_kernel (int8 MFMA, direct-to-LDS staging)",
-                         "timing": f"HIP graph of {n_m} launches, weights rotated over {ncopy} copies; 3 untimed "
-                                   "replays, then the mean of 5 replays each between HIP events"},
+                         "timing": f"HIP graph of {n_m} launches, weights rotated over {ncopy} copies; untimed "
+                                   f"replays for at least {WARM_S * 1e3:.0f} ms, then the mean of 5 replays each "
+                                   "between HIP events"},
         }
 
     if not args.no_traffic:
