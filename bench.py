@@ -132,7 +132,7 @@ def event_time_batch(torch, launch, n):
     return event_time_replays(torch, launch, n, warm=2, reps=3)[0]
 
 
-WARM_S = 0.02  # untimed GPU work before a timed replay: the clocks ramp up over the first tens of ms
+WARM_S = 0.1  # untimed GPU work before a timed replay: the clocks ramp up over the first tens of ms of load
 
 
 def warm_up(torch, g, min_replays):
