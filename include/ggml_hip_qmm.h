@@ -322,8 +322,9 @@ int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_s
 size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
 /* Column-tile width (32 or 64) of the gate/up-fused MMQ (hip_qmm_mmq_glu:
- * 32 up to 32 columns; hip_qmm_mmq also takes 32 up to 128 columns on rows
- * of at most 16 K-steps for Q4_K, Q5_K, Q8_0 and Q4_0) and the K-split
+ * 32 up to 32 columns; hip_qmm_mmq also takes 32 for Q4_K, Q5_K, Q8_0 and
+ * Q4_0 on rows of at most 16 K-steps where 64-column tiles would number at
+ * most 256 and 32-column ones at most 512) and the K-split
  * factor hip_qmm_mmq picks (1: no split; otherwise a divisor of K / 256). */
 int hip_qmm_mmq_tile_n(int64_t ncols);
 int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols);

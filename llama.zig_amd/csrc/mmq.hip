@@ -796,21 +796,28 @@ int check_weights(int type, const void *w, int64_t K, int64_t row_stride) {
 extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64; }
 
 // Column-tile width of the plain MMQ: hip_qmm_mmq_tile_n's, except that the
-// Q4_K, Q5_K, Q8_0 and Q4_0 direct-transfer kernels take 32-column tiles up to
-// 128 columns on rows of at most 16 K-steps, where twice the column tiles
-// fill the grid with fewer K shares.  Graph-timed against 64 columns (A/B of
-// both libraries, same box): Q4_K 14336x4096 at 48 / 64 / 96 / 128 columns
-// 28.4-28.5 / 29.5-29.9 / 39.0 / 41.2 -> 25.9-26.2 / 27.0-27.1 / 35.0-35.1 /
-// 38.6-38.8 us, 4096x4096 at 128 20.8 -> 18.7-18.8, 1024x4096 at 128 13.5 ->
-// 11.2; 14336x4096 at 128 Q8_0 43.4-43.7 -> 42.0-42.5, Q5_K 44.4-45.4 ->
-// 42.1-42.6, Q4_0 41.7-41.8 -> 39.2-39.9.  Longer rows keep 64 (Q4_K
-// 4096x14336 at 128: 36.9-37.2 against 38.8-39.2), and so do IQ4_XS (46.4-44.8
+// Q4_K, Q5_K, Q8_0 and Q4_0 direct-transfer kernels take 32-column tiles on
+// rows of at most 16 K-steps whenever 64-column tiles would leave the chip at
+// one workgroup per CU or fewer (at most 256 tiles) and 32-column tiles fit
+// one round of two per CU (at most 512): twice the tiles fill the grid with
+// fewer K shares and two workgroups per CU.  Graph-timed against 64 columns
+// (A/B of both libraries, same box): Q4_K 14336x4096 at 48 / 64 / 96 / 128
+// columns 28.4-28.5 / 29.5-29.9 / 39.0 / 41.2 -> 25.9-26.2 / 27.0-27.1 /
+// 35.0-35.1 / 38.6-38.8 us; 4096x4096 at 128 / 256 / 512 20.8 / 29.7 / 39.9
+// -> 18.7-18.8 / 23.8 / 33.8-33.9; 8192x4096 at 256 40.3-40.4 -> 34.1-34.4;
+// 2048x4096 at 512 29.7 -> 23.4; 1024x4096 at 128 13.5 -> 11.2; Q5_K / Q4_0 /
+// Q8_0 4096x4096 at 512 42.1-42.2 / 40.7-40.8 / 39.1-39.2 -> 39.2-39.3 /
+// 37.8-38.1 / 38.5.  Where 64-column tiles already fill the chip they keep it
+// (Q4_K 14336x4096 at 256: 52.8-53.2 against 60.6-61.2; 4096x4096 at 1024:
+// 53.8-54.1 against 61.6-62.2), and so do longer rows (Q4_K 4096x14336 at 512:
+// 98.5-98.7 against 105.2-105.6), IQ4_XS (14336x4096 at 128: 44.8-46.4
 // against 47.6-48.0) and the staged kernel (Q6_K 14336x4096 at 128: 70.5-71.8
 // against 77.7-80.0).
-int mmq_bn(int type, int64_t K, int64_t ncols) {
+int mmq_bn(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (ncols <= 32) return 32;
     const bool narrow = type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K || type == TYPE_Q4_0;
-    return narrow && ncols <= 128 && K / BK <= 16 ? 32 : 64;
+    const int64_t rt = (nrows + BM - 1) / BM;
+    return narrow && K / BK <= 16 && rt * ((ncols + 63) / 64) <= 256 && rt * ((ncols + 31) / 32) <= 512 ? 32 : 64;
 }
 
 // K-split factor: spread the K-steps over more workgroups until the grid
@@ -831,7 +838,7 @@ int mmq_bn(int type, int64_t K, int64_t ncols) {
 // at 256 / 512 columns 21.0 / 23.3 us against 24.0 / 30.9, 2048x4096 at 256
 // 20.7 against 23.2; 2048x4096 at 512 29.1 against 27.0).
 int split_std(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    const int64_t bn = mmq_bn(type, K, ncols);
+    const int64_t bn = mmq_bn(type, K, nrows, ncols);
     const int64_t wgs = ((nrows + BM - 1) / BM) * ((ncols + bn - 1) / bn);
     const int64_t nkb = K / BK;
     const int64_t target = ((type == TYPE_Q4_K || type == TYPE_Q8_0) && nkb <= 16) ? 256 : 512;
@@ -895,7 +902,7 @@ extern "C" int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, in
         return (int)hipErrorInvalidValue;
     if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
-    const int bn = mmq_bn(type, K, ncols);
+    const int bn = mmq_bn(type, K, nrows, ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
     const bool few = few_cols_type(type, K, nrows, ncols) && mmq_few_takes(type, K, w, row_stride) &&
                      (uintptr_t)y_qs % 16 == 0 && (uintptr_t)y_ds % 16 == 0;
