@@ -743,17 +743,22 @@ int mmq_few_split_k(int64_t K, int64_t nrows) {
 }
 
 // Whether a workgroup runs two K halves of its K part (KH = 2): K parts of
-// an even step count, at least 4.  Against one ring of 4 waves (graph-timed,
+// an even step count, at least 4, on grids of at most 256 workgroups (two
+// rings take twice the LDS, so a workgroup fills a CU's LDS by itself: a
+// larger grid would run a second round).  Against one ring of 4 waves (graph-timed,
 // same box): Q4_K 14336x4096 at 8 columns 13.4-13.5 -> 11.9-12.0 us, at 16
 // 13.9-14.1 -> 13.0-13.1, at 32 18.9-19.0 -> 18.3; Q5_K at 8 15.6-15.8 ->
 // 13.7, Q4_0 18.0-18.1 -> 14.5, IQ4_XS 18.7-18.9 -> 15.5-15.6, Q8_0
 // 17.2 -> 16.7.  Two waves with independent work share each SIMD, where one
 // wave alone stalled on its own LDS and MFMA latencies.  Halving the K
 // shares of the split grids (4096 rows) in exchange for K halves measured
-// level (and slower on 1024 rows), so those keep one ring.
-bool few_k_halves(int64_t K, int split) {
+// level (and slower on 1024 rows), so those keep one ring.  Split grids of
+// more than 256 workgroups with K halves ran a second round: 6144x4096 /
+// 8192x4096 / 10240x4096 / 8192x8192 / 2048x14336 at 8 columns 12.9 / 13.5 /
+// 17.4 / 17.6 / 14.4 us against 10.3 / 10.7 / 12.4 / 14.0 / 11.7 with one ring.
+bool few_k_halves(int64_t K, int64_t gx, int split) {
     const int64_t per = K / QK_K / split;
-    return per % 2 == 0 && per >= 4;
+    return per % 2 == 0 && per >= 4 && gx * split <= 256;
 }
 
 // Whether the few-column kernel takes this weight layout: Q4_K and Q5_K;
@@ -781,7 +786,7 @@ int mmq_few_launch(int type, const void *w, int64_t K, int64_t nrows, int64_t ro
         return (int)hipErrorInvalidValue;
     const dim3 grid((unsigned)gx, 1, (unsigned)split);
     // two K halves per workgroup where the K parts split evenly
-    const bool khalves = few_k_halves(K, split);
+    const bool khalves = few_k_halves(K, gx, split);
     const uint8_t *wb = (const uint8_t *)w;
     const uint32_t *ds = (const uint32_t *)yds;
     float *pp = split > 1 ? partial : nullptr;
