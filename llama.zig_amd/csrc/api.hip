@@ -36,35 +36,47 @@ size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 // Whether 2-8 columns go to the MMQ dispatch (the few-column kernel,
 // mmq_few.hip) rather than the GEMV.  The GEMV's time grows with the columns
 // (each wave re-reads every column's activation slice), the few-column
-// kernel's hardly does.  Crossovers measured on the op (hip_qmm_mul_mat, us,
-// GEMV against few-column) over 1024x14336, 2048x14336, 4096x4096,
-// 4096x14336, 8192x8192 and 14336x4096 at 3-8 columns:
+// kernel's hardly does; the few-column kernel is at its best on long rows (K
+// >= 8192, where the GEMV's per-wave activation slices are longest) and on
+// >= 12288 rows (an unsplit grid, two K halves per workgroup), while on
+// 6144-8192 rows of K = 4096 its split grid loses to the GEMV.  Crossovers
+// measured on the op (hip_qmm_mul_mat, us, GEMV path against few-column):
 //   - Q4_K: from 5 columns at K >= 8192 on >= 4096 rows (4096x14336: 19.6
-//     against 16.4) and on >= 12288 rows (14336x4096, whose unsplit grid runs
-//     two K halves per workgroup: 14.8 against 14.0), from 6 at K >= 8192 on
-//     >= 2048 rows, from 7 on >= 6144 rows; the GEMV stays ahead on smaller
-//     matrices (4096x4096 at 8 columns: 9.7 against 11.1);
-//   - Q5_K / Q8_0: from 4 columns on matrices of >= 24M weights (Q5_K
-//     14336x4096 at 4: 18.0 against 16.0; Q8_0 4096x14336 at 4: 24.0 against
-//     21.1; at 3 columns the one-launch GEMV with the quantization fused in
-//     stays, 16.5 / 22.4 against 15.9 / 20.9), 8 columns from 12M (Q5_K
-//     4096x4096 11.8 against 11.5; Q8_0 only on rows of K >= 8192, 4096x4096
-//     keeps the GEMV: 11.7 against 12.3);
-//   - Q4_0: from 4 columns on >= 24M weights (14336x4096 at 4: 17.9 against
-//     16.5); IQ4_XS from 5 (14336x4096 at 5: 18.5 against 18.0); both from 5
-//     on rows of K >= 8192 at <= 2048 or >= 8192 rows (Q4_0 8192x8192 at 5:
-//     21.5 against 18.9), 8 columns from 12M on rows of K >= 8192;
-//   - Q6_K (two 16-deep sub-blocks per MFMA up to 8 columns): from 4 columns
-//     on >= 24M weights (4096x14336 at 4 / 8: 24.7 / 27.9 against 22.4 /
-//     22.3; 14336x4096 at 4: 24.3 against 21.1; at 3 the one-launch GEMV
-//     stays, 23.0 / 19.1 against 22.6 / 21.3), 7 columns from 12M (4096x4096
-//     13.0 against 12.7), 8 columns on rows of K >= 8192 at <= 2048 rows; the
-//     GEMV stays ahead on 4096x4096 at 5, 6 and 8 columns (10.7 / 12.3 / 11.3
-//     against 12.7 / 12.8 / 12.9) and on 1024x4096.
+//     against 16.4) and on >= 12288 rows (14336x4096 at 5: 14.8 against 14.0;
+//     12288x4096 13.9 against 13.4), from 6 at K >= 8192 on >= 2048 rows, from
+//     7 on >= 6144 rows; the GEMV stays ahead on smaller matrices (4096x4096 at
+//     8 columns: 9.7 against 11.1);
+//   - Q5_K: from 4 columns on >= 24M weights of long rows or >= 12288 rows
+//     (14336x4096 at 4: 18.0 against 16.0), from 6 on other >= 24M weights
+//     (6144x4096 at 4 / 5 / 6: 10.5 / 12.9 / 13.9 against 13.5 / 13.5 / 13.6),
+//     8 columns from 12M (4096x4096 11.8 against 11.5);
+//   - Q8_0: from 4 columns on >= 24M weights of long rows or >= 12288 rows
+//     (4096x14336 at 4: 24.0 against 21.1), 8 columns from 12M on long rows;
+//     6144x4096 keeps the GEMV (12.4-14.4 against 14.8-15.1 at 4-8 columns);
+//   - Q4_0: on >= 24M weights, from 4 columns on >= 12288 rows (14336x4096:
+//     17.9 against 16.5) and on long rows of <= 2048 (2048x14336: 15.2 against
+//     14.9), from 5 on other long rows (4096x14336 at 4 / 5: 17.3 / 19.9
+//     against 17.9 / 17.9); 6144x4096 keeps the GEMV (9.7-13.2 against
+//     13.4-13.7); 8 columns from 12M on long rows;
+//   - IQ4_XS: from 5 columns on >= 24M weights of long rows or >= 12288 rows
+//     (14336x4096: 18.5 against 18.0; 2048x14336: 16.6 against 15.3), 8
+//     columns from 12M on long rows;
+//   - Q6_K (two 16-deep sub-blocks per MFMA up to 8 columns): on >= 24M
+//     weights from 4 columns on long rows or >= 12288 rows (4096x14336 at 4 /
+//     8: 24.7 / 27.9 against 22.4 / 22.3; 14336x4096 at 4: 24.3 against 21.1;
+//     2048x14336 at 4: 20.5 against 17.6), from 5 on >= 8192 rows (8192x4096
+//     at 4 / 5: 15.4 / 17.4 against 16.7 / 16.7), from 6 on the rest
+//     (6144x4096 at 5 / 6: 14.7 / 16.6 against 16.1 / 16.2); 7 columns from
+//     12M (4096x4096 13.0 against 12.7), 8 columns on rows of K >= 8192 at <=
+//     2048 rows; the GEMV stays ahead on 4096x4096 at 5, 6 and 8 columns (10.7
+//     / 12.3 / 11.3 against 12.7 / 12.8 / 12.9) and on 1024x4096.
+//   At 3 columns the one-launch GEMV with the quantization fused in stays
+//   (Q5_K 14336x4096 16.5 against 15.9; Q8_0 4096x14336 22.4 against 20.9).
 bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (K % 256 != 0 || ncols > 8 || !few_cols_type(type, K, nrows, ncols)) return false;
     const int64_t elems = nrows * K;
     const bool large = elems >= ((int64_t)24 << 20), mid = elems >= ((int64_t)12 << 20), long_rows = K >= 8192;
+    const bool strong = large && (long_rows || nrows >= 12288);  // the few-column kernel's best grids
     switch (type) {
     case TYPE_Q4_K:
         if (long_rows && nrows >= 4096) return ncols >= 5;
@@ -72,15 +84,15 @@ bool few_cols_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
         if (long_rows && nrows >= 2048) return ncols >= 6;
         if (nrows >= 6144) return ncols >= 7;
         return false;
-    case TYPE_Q5_K: return (large && ncols >= 4) || (mid && ncols == 8);
-    case TYPE_Q8_0: return (large && ncols >= 4) || (mid && long_rows && ncols == 8);
+    case TYPE_Q5_K: return (strong && ncols >= 4) || (large && ncols >= 6) || (mid && ncols == 8);
+    case TYPE_Q8_0: return (strong && ncols >= 4) || (mid && long_rows && ncols == 8);
     case TYPE_Q4_0:
-    case TYPE_IQ4_XS:
-        return (large && (ncols >= (type == TYPE_Q4_0 ? 4 : 5) ||
-                          (long_rows && (nrows <= 2048 || nrows >= 8192) && ncols >= 5))) ||
+        return (strong && ncols >= (long_rows && nrows > 2048 && nrows < 12288 ? 5 : 4)) ||
                (mid && long_rows && ncols == 8);
+    case TYPE_IQ4_XS: return (strong && ncols >= 5) || (mid && long_rows && ncols == 8);
     case TYPE_Q6_K:
-        return (large && ncols >= 4) || (mid && ncols == 7) || (mid && long_rows && nrows <= 2048 && ncols == 8);
+        return (strong && ncols >= 4) || (large && nrows >= 8192 && ncols >= 5) || (large && ncols >= 6) ||
+               (mid && ncols == 7) || (mid && long_rows && nrows <= 2048 && ncols == 8);
     default: return false;
     }
 }

@@ -83,7 +83,7 @@ def test_mmq_split_k(tname, nrows, K, ncols):
                                                  ("Q4_K", 6144, 4096, 8), ("Q4_K", 6150, 4096, 7),
                                                  ("Q5_K", 2048, 14336, 4), ("Q5_K", 4096, 4096, 8),
                                                  ("Q8_0", 4096, 8192, 4), ("Q8_0", 1024, 14336, 8),
-                                                 ("Q4_0", 2048, 14336, 5), ("Q4_0", 6144, 4096, 6),
+                                                 ("Q4_0", 2048, 14336, 5), ("Q4_0", 12300, 2048, 5),
                                                  ("IQ4_XS", 2048, 14336, 5), ("IQ4_XS", 1024, 14336, 8),
                                                  ("Q6_K", 1024, 14336, 7), ("Q6_K", 2048, 14336, 8),
                                                  ("Q6_K", 2048, 14336, 6), ("Q6_K", 4096, 14336, 4)])
