@@ -811,8 +811,9 @@ extern "C" int hip_qmm_mmq_tile_n(int64_t ncols) { return ncols <= 32 ? 32 : 64;
 // (Q4_K 14336x4096 at 256: 52.8-53.2 against 60.6-61.2; 4096x4096 at 1024:
 // 53.8-54.1 against 61.6-62.2), and so do longer rows (Q4_K 4096x14336 at 512:
 // 98.5-98.7 against 105.2-105.6), IQ4_XS (14336x4096 at 128: 44.8-46.4
-// against 47.6-48.0) and the staged kernel (Q6_K 14336x4096 at 128: 70.5-71.8
-// against 77.7-80.0).
+// against 47.6-48.0; 4096x4096 at 512: 44.7 against 46.0-46.1) and the staged
+// kernel (Q6_K 14336x4096 at 128: 70.5-71.8 against 77.7-80.0; 4096x4096 at
+// 512: 70.1-70.2 against 76.8-77.2).
 int mmq_bn(int type, int64_t K, int64_t nrows, int64_t ncols) {
     if (ncols <= 32) return 32;
     const bool narrow = type == TYPE_Q4_K || type == TYPE_Q8_0 || type == TYPE_Q5_K || type == TYPE_Q4_0;
