@@ -271,7 +271,8 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
  *    faster than the GEMV (the shape rules are hip_qmm_mul_mat_workspace_size's
  *    and hip_qmm_mul_mat_uses_mmq's: e.g. Q4_K from 5 columns at K >= 8192 on
  *    >= 4096 rows and on >= 12288 rows, from 7 columns on >= 6144 rows; Q6_K
- *    from 4 columns on >= 24M weights).  On those 4-8 column shapes the workspace grows by the
+ *    from 4 columns on >= 24M weights of long rows or >= 12288 rows).  On
+ *    those 4-8 column shapes the workspace grows by the
  *    few-column kernel's split-K partials, and the results differ from
  *    hip_qmm_mul_mat_vec's in fp32 rounding (another summation order; both
  *    pass the f64 and CPU gates);
