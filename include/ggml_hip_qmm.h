@@ -322,11 +322,12 @@ int hip_qmm_mmq(int type, const void *w, int64_t K, int64_t nrows, int64_t row_s
 /* Bytes of split-K workspace hip_qmm_mmq uses for this shape (0: no split). */
 size_t hip_qmm_mmq_workspace_size(int type, int64_t K, int64_t nrows, int64_t ncols);
 
-/* Column-tile width (32 or 64) of the gate/up-fused MMQ (hip_qmm_mmq_glu:
- * 32 up to 32 columns; hip_qmm_mmq also takes 32 for Q4_K, Q5_K, Q8_0 and
- * Q4_0 on rows of at most 16 K-steps where 64-column tiles would number at
- * most 256 and 32-column ones at most 512) and the K-split
- * factor hip_qmm_mmq picks (1: no split; otherwise a divisor of K / 256). */
+/* Column-tile width (32 or 64) for ncols columns: 32 up to 32 columns, 64
+ * above.  hip_qmm_mmq also takes 32 for Q4_K, Q5_K, Q8_0 and Q4_0 on rows of
+ * at most 16 K-steps where 64-column tiles would number at most 256 and
+ * 32-column ones at most 512; hip_qmm_mmq_glu does the same over its tiles of
+ * 64 output rows, except for Q8_0.  hip_qmm_mmq_split_k: the K-split factor
+ * hip_qmm_mmq picks (1: no split; otherwise a divisor of K / 256). */
 int hip_qmm_mmq_tile_n(int64_t ncols);
 int hip_qmm_mmq_split_k(int type, int64_t K, int64_t nrows, int64_t ncols);
 

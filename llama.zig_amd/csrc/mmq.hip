@@ -821,6 +821,26 @@ int mmq_bn(int type, int64_t K, int64_t nrows, int64_t ncols) {
     return narrow && K / BK <= 16 && rt * ((ncols + 63) / 64) <= 256 && rt * ((ncols + 31) / 32) <= 512 ? 32 : 64;
 }
 
+// Column-tile width of the gate/up-fused MMQ: mmq_bn's rule over its tiles of
+// 64 output rows (each tile reads 64 rows of both weights, the work of one
+// 128-row tile of the plain kernel), except for Q8_0.  The fused kernel splits
+// no K, so twice the column tiles are its only way to fill the chip.  The
+// whole call graph-timed, 64- against 32-column tiles (A/B of both libraries,
+// same box, us): Q4_K 14336x4096 at 33 / 48 / 64 columns 47.0-47.1 / 46.6-46.8
+// / 46.8-47.0 -> 37.9-38.1 / 38.2-38.5 / 38.6-38.9; 4096x4096 at 64 / 128 /
+// 256 44.4-44.5 / 44.7-44.8 / 45.8-45.9 -> 27.5 / 27.8 / 38.9-39.2; 8192x4096
+// at 128 46.0-46.1 -> 39.1-39.4; 2048x4096 at 512 47.1 -> 40.1-40.4; Q5_K /
+// Q4_0 14336x4096 at 48 52.2-52.4 / 48.3-48.4 -> 45.2-45.4 / 41.9-42.0, and
+// 4096x4096 at 256 51.7-51.8 / 47.3-47.4 -> 44.2-44.3 / 41.7-41.8.  Q8_0 loses
+// on the large weights (14336x4096 at 48 / 64: 49.4-49.5 / 49.8-49.9 against
+// 53.7-53.8 / 56.0-56.1) for 2 us won at 4096x4096 (256 columns 46.0-46.2
+// against 43.9-44.2), and keeps 64 columns.  Where 64-column tiles already
+// fill the chip nothing changes (Q4_K 14336x4096 at 96 / 128: 59.0-59.4 /
+// 59.7-60.2 either way).
+int mmq_glu_bn(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return type == TYPE_Q8_0 ? hip_qmm_mmq_tile_n(ncols) : mmq_bn(type, K, 2 * nrows, ncols);
+}
+
 // K-split factor: spread the K-steps over more workgroups until the grid
 // holds about one workgroup per CU (256 CUs on MI355X) for the Q4_K
 // direct-to-LDS kernel on rows of at most 16 K-steps, about two otherwise;
@@ -958,7 +978,7 @@ extern "C" int hip_qmm_mmq_glu(int type, const void *w, const void *w_gate, int6
     if (K % BK != 0 || K > (1 << 30)) return (int)hipErrorInvalidValue;
     if (int e = check_weights(type, w, K, row_stride)) return e;
     if (int e = check_weights(type, w_gate, K, row_stride)) return e;
-    const int bn = hip_qmm_mmq_tile_n(ncols);
+    const int bn = mmq_glu_bn(type, K, nrows, ncols);
     const int64_t gy = (ncols + bn - 1) / bn;
     const MmqGlu glu{(const uint8_t *)w_gate, glu_op, glu_alpha, glu_limit};
     return launch_type(type, bn, w, K, nrows, row_stride, 0, y_qs, y_ds, ncols, dst, dst_col_stride, gy, nullptr,

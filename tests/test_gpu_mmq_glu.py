@@ -91,10 +91,11 @@ def test_mmq_glu_every_op(opname):
 def test_mmq_glu_32_column_tiles_match_64(tname):
     """The 32-column tile (20 columns) gives the 64-column tile's bits on the
     same columns: per output the two tiles run the same sums in the same
-    order."""
+    order.  Rows of 18 K-steps keep 40 columns on 64-column tiles (the
+    grid-fill rule takes 32-column tiles on rows of at most 16)."""
     import ggml_hip as G
     t = TYPES[tname]
-    nrows, K = 300, 2048
+    nrows, K = 300, 4608
     w = _dev(weights_q(t, nrows, K, 0))
     wg = _dev(weights_q(t, nrows, K, 1))
     x_d = _dev(acts(40, K))
