@@ -459,7 +459,15 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
                 # columns except where the few-column GEMM measured faster)
                 gemv_fn = lambda i: G.mul_mat_vec(qtype, ws[i % len(ws)], Kx, qs, ds, out=out)  # noqa: E731
                 mmq_fn = lambda i: G.mmq(qtype, ws[i % len(ws)], Kx, qs, ds, out=out, workspace=mmq_ws)  # noqa: E731
-                if T <= 8 and not G.lib().hip_qmm_mul_mat_uses_mmq(G.TYPE_IDS[qtype], Kx, M, T):
+                # the op on f32 activations (hip_qmm_mul_mat: quantizer + kernel,
+                # or for one column the GEMV that quantizes in its prologue)
+                wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_workspace_size(G.TYPE_IDS[qtype], Kx, M, T)),
+                                  dtype=torch.uint8, device=dev)
+                op_fn = lambda i: G.mul_mat(qtype, ws[i % len(ws)], x, out=out, workspace=wsp)  # noqa: E731
+                if 2 <= T <= 8 and G.lib().hip_qmm_mul_mat_per_column(G.TYPE_IDS[qtype], Kx, M, T):
+                    # one launch: the one-column kernel per column, quantizing in the kernel
+                    fn, kern = op_fn, "gemv one-column kernel per column"
+                elif T <= 8 and not G.lib().hip_qmm_mul_mat_uses_mmq(G.TYPE_IDS[qtype], Kx, M, T):
                     fn, kern = gemv_fn, "gemv"
                 else:
                     fn, kern = mmq_fn, ("mmq few-column" if T <= 8 else "mmq")
@@ -484,11 +492,6 @@ def run_suite(name, torch, G, dev, reps, cpu=True):
                         tile_fn = lambda i: G.mmq(qtype, off[i % len(off)], Kx, qs, ds, out=out,  # noqa: E731
                                                   workspace=mmq_ws)
                         extra["tile128_us"] = round(event_time_batch(torch, tile_fn, n) * 1e3, 3)
-                # the op on f32 activations (hip_qmm_mul_mat: quantizer + kernel,
-                # or for one column the GEMV that quantizes in its prologue)
-                wsp = torch.empty(int(G.lib().hip_qmm_mul_mat_workspace_size(G.TYPE_IDS[qtype], Kx, M, T)),
-                                  dtype=torch.uint8, device=dev)
-                op_fn = lambda i: G.mul_mat(qtype, ws[i % len(ws)], x, out=out, workspace=wsp)  # noqa: E731
                 ms_op = event_time_batch(torch, op_fn, n)
                 alg = wb + Kx * 4 * T + M * 4 * T
                 ops = 2.0 * M * Kx * T

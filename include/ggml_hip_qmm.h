@@ -82,6 +82,13 @@ size_t hip_qmm_mul_mat_workspace_size(int type, int64_t K, int64_t nrows, int64_
  * kernel the op takes. */
 int hip_qmm_mul_mat_uses_mmq(int type, int64_t K, int64_t nrows, int64_t ncols);
 
+/* 1 if hip_qmm_mul_mat runs these 2-8 f32 columns as rows of the one-column
+ * fused kernel's grid (each column quantized in the kernel and equal bit for
+ * bit to hip_qmm_mul_mat_vec_f32 on it; 16-byte-aligned x with a column
+ * stride of a multiple of 4 floats), else 0.  No counterpart in the reference:
+ * a query for measurement and tests, like hip_qmm_mul_mat_uses_mmq. */
+int hip_qmm_mul_mat_per_column(int type, int64_t K, int64_t nrows, int64_t ncols);
+
 /*
  * Decode GEMV against planar Q8_1 activations, 1..8 columns: dst[c*dst_col_stride + r]
  * = sum_k W[r,k] * y[c,k].  Replaces mul_mat_vec_q_switch_type
@@ -264,7 +271,10 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
  *  - the GEMV for up to 8 columns.  One column, and 2-4 columns of rows with
  *    K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
  *    columns), skip the separate quantizer: the GEMV quantizes the columns in
- *    its prologue;
+ *    its prologue.  2-8 columns of small matrices (at most 2048 rows of
+ *    K <= 4096; Q8_0 at most 1024 rows and 4 columns; not Q4_0) run as rows
+ *    of the one-column kernel's grid, each column quantized in the kernel
+ *    (hip_qmm_mul_mat_per_column), with no workspace;
  *  - the few-column GEMM (16x16 int8 MFMA tiles) for 9-32 columns (9-16 for
  *    Q6_K; Q8_0 / Q4_0 at 17-32 columns of 8 MiB of weights and more take the
  *    tile), and also for 4-8 columns of large matrices, where it measured

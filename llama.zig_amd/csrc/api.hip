@@ -25,6 +25,10 @@ bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
 // hipErrorNotSupported for shapes it does not take.
 int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
                         int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream);
+// gemv.hip: 2-8 f32 columns of a small matrix through the one-column kernel
+// (grid y = column), or hipErrorNotSupported where it does not win.
+int qmm_mul_mat_fx_percol(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
+                          int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream);
 
 namespace {
 size_t q8_1_bytes(int64_t K, int64_t ncols) {
@@ -154,6 +158,11 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
     // K shares 14.9 vs 15.6 us).
     if (ncols == 1 && K <= 32768 && K % QK8 == 0 && (uintptr_t)x % 16 == 0)
         return hip_qmm_mul_mat_vec_f32(type, w, K, nrows, row_stride, x, dst, stream);
+    if (ncols >= 2 && ncols <= 8 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride)) {
+        const int e = qmm_mul_mat_fx_percol(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst,
+                                            dst_col_stride, stream);
+        if (e != (int)hipErrorNotSupported) return e;
+    }
     if (ncols >= 2 && ncols <= 4 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride)) {
         const int e = qmm_mul_mat_fx_cols(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride,
                                           stream);

@@ -722,7 +722,8 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
             const int t = p / fi.n_ids, slot = p - t * fi.n_ids;
             x += (int64_t)(t * fi.ne11 + slot % fi.ne11) * fi.x_row_stride;
             dst += (int64_t)p * fi.dst_row_stride;
-            expert = __builtin_amdgcn_readfirstlane(fi.ids[(int64_t)t * fi.ids_stride + slot]);
+            // no ids: every pair runs through the one matrix (the op's columns, qmm_mul_mat_fx_percol)
+            expert = fi.ids ? __builtin_amdgcn_readfirstlane(fi.ids[(int64_t)t * fi.ids_stride + slot]) : 0;
         } else {
             const int t = p - fi.n_pairs;
             x += (int64_t)t * fi.ne11 * fi.x_row_stride;
@@ -1482,6 +1483,46 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, cons
     return id_vec_fused(type, w, w_gate, K, nrows, row_stride, expert_stride, n_as, x, 1, n_tokens, x_row_stride, ids,
                         n_ids, ids_stride, glu_op, glu_alpha, glu_limit, dst, dst_row_stride, &sh, nullptr, nullptr, 0,
                         stream);
+}
+
+// 2-8 f32 columns of a small matrix as rows of the one-column kernel's grid
+// (the ids form with no ids: grid y is the column, x + c * x_col_stride in,
+// dst + c * dst_col_stride out), each quantizing its own column.  On a grid
+// that leaves most CUs idle the columns run side by side and read the
+// weights from the L2 / MALL after the first, and no quantizer launch comes
+// first.  Each column equals hip_qmm_mul_mat_vec_f32 on it bit for bit.
+// Returns hipErrorNotSupported outside the shapes where it measured faster
+// (fx_percol_wins), so the caller goes on to its other paths.
+//
+// Measured (op us, graph-timed, the other paths against this): Q4_K 1024x4096
+// at 2 / 4 / 8 columns 4.12 / 5.68 / 7.17 against 3.71 / 3.79 / 4.96, 2048x4096
+// 4.57 / 8.06 / 11.33 against 4.20 / 5.46 / 7.62, 1024x2048 3.66 / 5.40 / 6.80
+// against 3.01 / 3.05 / 3.75; Q6_K 1024x4096 5.08 / 7.46 / 9.83 against 4.68 /
+// 4.69 / 6.65, 2048x4096 5.64 / 10.54 / 17.33 against 5.54 / 7.40 / 11.24; Q5_K
+// and IQ4_XS alike.  Larger grids lose (Q4_K 4096x4096 at 2 / 8: 4.96 / 9.67
+// against 5.84 / 12.98; Q6_K 3072x4096 at 8: 10.79 against 15.37), and so do
+// long rows (Q4_K 1024x14336 at 4: 9.70 against 12.42), which keep the other
+// paths.  Q8_0 wins up to 1024 rows at 2-4 columns (1024x4096 5.60 / 7.29
+// against 4.35 / 5.76) and loses at 8 (6.85 against 8.93) and on 2048 rows
+// (2048x4096 at 4: 7.47 against 9.08).  Q4_0 was not measured and keeps the
+// other paths.
+static bool fx_percol_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    if (ncols < 2 || ncols > 8 || K > 4096 || type == TYPE_Q4_0) return false;
+    if (type == TYPE_Q8_0) return nrows <= 1024 && ncols <= 4;
+    return nrows <= 2048;
+}
+
+extern "C" int hip_qmm_mul_mat_per_column(int type, int64_t K, int64_t nrows, int64_t ncols) {
+    return nrows > 0 && K > 0 && K % QK8 == 0 && fx_percol_wins(type, K, nrows, ncols) ? 1 : 0;
+}
+
+int qmm_mul_mat_fx_percol(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
+                          int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream) {
+    if (!fx_percol_wins(type, K, nrows, ncols) || K % QK8 != 0 || (uintptr_t)x % 16 || x_col_stride % 4)
+        return (int)hipErrorNotSupported;
+    if (dst_col_stride < nrows || x_col_stride < K || !dst) return (int)hipErrorInvalidValue;
+    const FxIds fi{nullptr, 1, x_col_stride, 0, dst_col_stride, 1, 1, 1, (int)ncols, nullptr, nullptr, nullptr, 0, 0, 0};
+    return fused_launch(type, w, nullptr, K, nrows, row_stride, x, nullptr, nullptr, 0, 0.0f, 0.0f, dst, &fi, stream);
 }
 
 // 2-4 f32 columns through the quantize-in-GEMV kernel (hip_qmm_mul_mat's

@@ -46,6 +46,7 @@ def lib():
         L.hip_qmm_mul_mat_workspace_size.restype = ctypes.c_size_t
         L.hip_qmm_mul_mat_workspace_size.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mul_mat_uses_mmq.argtypes = [i32, i64, i64, i64]
+        L.hip_qmm_mul_mat_per_column.argtypes = [i32, i64, i64, i64]
         L.hip_qmm_mul_mat_vec.restype = i32
         L.hip_qmm_mul_mat_vec.argtypes = [i32, vp, i64, i64, i64, vp, vp, i64, vp, i64, vp]
         L.hip_qmm_gemv_mfma.restype = i32

@@ -322,3 +322,12 @@ def test_mul_mat_route_query(L):
     assert all(q(t, 4096, 4096, 9) == 1 for t in (q4k, q6k, q8_0))
     assert q(q4k, 4000, 4096, 16) == 0  # K % 256 != 0: no MMQ
     assert q(q4k, 4096, 0, 8) == 0 and q(q4k, 0, 4096, 8) == 0
+    # 2-8 columns of small matrices: the one-column kernel per column
+    L.hip_qmm_mul_mat_per_column.argtypes = [C.c_int, C.c_int64, C.c_int64, C.c_int64]
+    pc = lambda t, K, rows, cols: L.hip_qmm_mul_mat_per_column(t, K, rows, cols)  # noqa: E731
+    q5k, q4_0, iq4xs = 13, 2, 23
+    assert all(pc(t, 4096, 1024, c) == 1 for t in (q4k, q5k, q6k, iq4xs) for c in range(2, 9))
+    assert pc(q4k, 4096, 2048, 8) == 1 and pc(q4k, 4096, 2049, 2) == 0 and pc(q4k, 4352, 1024, 2) == 0
+    assert pc(q4k, 4096, 1024, 1) == 0 and pc(q4k, 4096, 1024, 9) == 0
+    assert pc(q8_0, 4096, 1024, 4) == 1 and pc(q8_0, 4096, 1024, 5) == 0 and pc(q8_0, 4096, 2048, 2) == 0
+    assert pc(q4_0, 4096, 1024, 2) == 0 and pc(q4k, 4096, 0, 2) == 0 and pc(q4k, 0, 1024, 2) == 0

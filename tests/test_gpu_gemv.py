@@ -147,7 +147,8 @@ def _one_column_op_splits_k(tname, nrows, K):
 
 
 # 2-4 f32 columns on at most 4096-long rows below 8192 rows (and above, for
-# Q8_0 at 3-4 columns and rows of K <= 2048): the op runs the
+# Q8_0 at 3-4 columns and rows of K <= 2048), where the per-column grid below
+# does not take them: the op runs the
 # quantize-in-GEMV kernel over all columns in one launch (2 columns for the
 # K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0).  Where the one-column op runs
 # one K share, each column equals it bit for bit; where the one-column op
@@ -178,6 +179,44 @@ def test_op_few_columns_one_launch(tname, nrows, K, ncols):
     assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
     cpu = O.mul_mat(t, wq, nrows, K, x, nth=8)
     assert nmse(got, cpu) < NMSE_GATE
+
+
+# 2-8 f32 columns of matrices of at most 2048 rows of at most 4096 elements
+# (Q8_0: 1024 rows, up to 4 columns; not Q4_0): the op runs every column
+# through the one-column kernel as one row of its grid
+# (qmm_mul_mat_fx_percol, gemv.hip), so each column equals the one-column op
+# on it bit for bit, K shares included.  Columns strided in and out; nothing
+# is written past a column's rows.
+@pytest.mark.parametrize("tname,nrows,K,ncols", [("Q4_K", 1024, 4096, 8), ("Q4_K", 2048, 4096, 3),
+                                                 ("Q5_K", 1000, 2048, 5), ("Q6_K", 1024, 4096, 4),
+                                                 ("Q6_K", 777, 4096, 8), ("IQ4_XS", 2048, 4096, 6),
+                                                 ("Q8_0", 1024, 4096, 4), ("Q8_0", 520, 1024, 2),
+                                                 ("Q4_K", 300, 256, 7), ("Q6_K", 64, 2048, 2)])
+def test_op_few_columns_per_column_grid(tname, nrows, K, ncols):
+    import ctypes
+
+    import ggml_hip as G
+    t = TYPES[tname]
+    wq = weights_q(t, nrows, K)
+    x = acts(ncols, K)
+    w_d = torch.from_numpy(np.array(wq)).cuda()
+    xb = torch.zeros((ncols, K + 64), dtype=torch.float32, device="cuda")
+    xb[:, :K] = torch.from_numpy(np.array(x)).cuda()
+    x_d = xb[:, :K]
+    ob = torch.full((ncols, nrows + 40), 7.0, dtype=torch.float32, device="cuda")
+    ws = torch.empty(max(16, G.workspace_size(tname, K, ncols, nrows)), dtype=torch.uint8, device="cuda")
+    e = G.lib().hip_qmm_mul_mat(t, G._ptr(w_d), K, nrows, w_d.stride(0), G._ptr(x_d), ncols, K + 64, G._ptr(ob),
+                                nrows + 40, G._ptr(ws), ctypes.c_size_t(ws.numel()), G._stream())
+    assert e == 0, e
+    got = ob.cpu().numpy()
+    assert np.all(got[:, nrows:] == 7.0)
+    got = got[:, :nrows]
+    for c in range(ncols):
+        one = G.mul_mat_vec_f32(tname, w_d, K, x_d[c]).cpu().numpy().reshape(-1)
+        np.testing.assert_array_equal(got[c], one)
+    y = G.quantize_q8_1(x_d.contiguous(), K).cpu().numpy()
+    ideal = O.mul_mat_q8_1_f64(t, wq, nrows, K, y, ncols)
+    assert max_err_scaled(got, ideal) < F64_TOL, max_err_scaled(got, ideal)
 
 
 def test_gemv_config0_op_level():
