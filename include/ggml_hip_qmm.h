@@ -271,7 +271,8 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
  *  - the GEMV for up to 8 columns.  One column, and 2-4 columns of rows with
  *    K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
  *    columns), skip the separate quantizer: the GEMV quantizes the columns in
- *    its prologue.  2-8 columns of small matrices (at most 2048 rows of
+ *    its prologue, as it does for 4 columns of the K-quants, 6 of IQ4_XS and 8
+ *    of Q8_0 on at most 4096 rows (two rows of its grid).  2-8 columns of small matrices (at most 2048 rows of
  *    K <= 4096; Q8_0 at most 1024 rows and 4 columns; not Q4_0) run as rows
  *    of the one-column kernel's grid, each column quantized in the kernel
  *    (hip_qmm_mul_mat_per_column), with no workspace;

@@ -21,8 +21,9 @@ bool few_cols_type(int type, int64_t K, int64_t nrows, int64_t ncols);
 // mmq_few.hip: whether it takes these weight rows
 bool mmq_few_takes(int type, int64_t K, const void *w, int64_t row_stride);
 
-// gemv.hip: 2-4 f32 columns through the quantize-in-GEMV kernel, or
-// hipErrorNotSupported for shapes it does not take.
+// gemv.hip: 2-4 f32 columns (or twice the kernel's columns as two grid rows)
+// through the quantize-in-GEMV kernel, or hipErrorNotSupported for shapes it
+// does not take.
 int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
                         int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream);
 // gemv.hip: 2-8 f32 columns of a small matrix through the one-column kernel
@@ -163,7 +164,7 @@ extern "C" int hip_qmm_mul_mat(int type, const void *w, int64_t K, int64_t nrows
                                             dst_col_stride, stream);
         if (e != (int)hipErrorNotSupported) return e;
     }
-    if (ncols >= 2 && ncols <= 4 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride)) {
+    if (ncols >= 2 && ncols <= 8 && !use_mmq_rows(type, K, nrows, ncols, w, row_stride)) {
         const int e = qmm_mul_mat_fx_cols(type, w, K, nrows, row_stride, x, ncols, x_col_stride, dst, dst_col_stride,
                                           stream);
         if (e != (int)hipErrorNotSupported) return e;

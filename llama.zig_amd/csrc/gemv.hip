@@ -914,7 +914,8 @@ __global__ __launch_bounds__(64 * FW) void gemv_fx_kernel(const uint8_t *__restr
 // one-column kernel's prologue once per column -- all columns' first-pass
 // loads first, then the weights -- into NC LDS copies of K + K/8 bytes, then
 // each K-step's weights contract against every column in turn.  Column c of
-// x starts at x + c * x_col_stride, of dst at dst + c * dst_col_stride.  The
+// x starts at x + c * x_col_stride, of dst at dst + c * dst_col_stride; grid
+// row y takes columns NC * y .. NC * y + NC - 1.  The
 // per-column arithmetic is the one-column kernel's with one K share, so a
 // column equals hip_qmm_mul_mat_vec_f32 on it bit for bit wherever that runs
 // one share.
@@ -928,6 +929,8 @@ __global__ __launch_bounds__(64 * FW) void gemv_fxn_kernel(const uint8_t *__rest
     constexpr int STEP = 64 * F::W;
     extern __shared__ __align__(16) uint8_t fx_lds[];
     const int cb = fx_part_offset(K32);  // bytes per column copy
+    x += (int64_t)blockIdx.y * NC * x_col_stride;
+    dst += (int64_t)blockIdx.y * NC * dst_col_stride;
     const int kq = 8 * (int)threadIdx.x;
     const int kqc = kq < K32 ? kq : 0;
     float4 xa[NC], xb[NC];
@@ -1322,18 +1325,19 @@ void launch_fx_type(const uint8_t *w, const uint8_t *wg, int64_t K, int64_t nrow
 
 template <int TYPE, int FW, int R, int NC>
 void launch_fxn(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t xs,
-                float *dst, int64_t ds, hipStream_t s) {
+                float *dst, int64_t ds, int groups, hipStream_t s) {
     const int64_t nblocks = (nrows + FW * R - 1) / (FW * R);
     const size_t lds = (size_t)NC * fx_part_offset((int)K);
-    hipLaunchKernelGGL((gemv_fxn_kernel<TYPE, FW, R, NC>), dim3((unsigned)nblocks), dim3(64 * FW), lds, s, w, (int)K,
+    hipLaunchKernelGGL((gemv_fxn_kernel<TYPE, FW, R, NC>), dim3((unsigned)nblocks, (unsigned)groups), dim3(64 * FW),
+                       lds, s, w, (int)K,
                        nrows, row_stride, x, xs, dst, ds);
 }
 
 template <int TYPE, int NC>
 void launch_fxn_shape(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t xs,
-                      float *dst, int64_t ds, hipStream_t s) {
+                      float *dst, int64_t ds, hipStream_t s, int groups = 1) {
     // the one-column kernel's workgroup shape below 8192 rows (8 waves of 2 rows)
-    launch_fxn<TYPE, 8, 2, NC>(w, K, nrows, row_stride, x, xs, dst, ds, s);
+    launch_fxn<TYPE, 8, 2, NC>(w, K, nrows, row_stride, x, xs, dst, ds, groups, s);
 }
 
 // Most columns per launch: 2 for the K-quants, 3 for IQ4_XS, 4 for Q8_0 /
@@ -1345,6 +1349,8 @@ constexpr int fxn_max_cols(int type) {
 template <int TYPE>
 void launch_fxn_type(const uint8_t *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x, int64_t ncols,
                      int64_t xs, float *dst, int64_t ds, hipStream_t s) {
+    constexpr int MC = fxn_max_cols(TYPE);
+    if (ncols == 2 * MC) return launch_fxn_shape<TYPE, MC>(w, K, nrows, row_stride, x, xs, dst, ds, s, 2);
     if constexpr (fxn_max_cols(TYPE) >= 4)
         if (ncols == 4) return launch_fxn_shape<TYPE, 4>(w, K, nrows, row_stride, x, xs, dst, ds, s);
     if constexpr (fxn_max_cols(TYPE) >= 3)
@@ -1536,11 +1542,20 @@ int qmm_mul_mat_fx_percol(int type, const void *w, int64_t K, int64_t nrows, int
 // but for Q8_0 at 3-4 columns (14336x4096, 4 columns: 24.56 vs 20.77) and
 // Q4_K / Q4_0 rows of K <= 2048 (8192x2048 Q4_K 2 columns 7.71 vs 5.86; the
 // other types were not measured there and keep quantizer + GEMV); slower on rows
-// of K > 4096 (4096x14336 Q4_K 13.08 vs 14.63: no K shares here).
+// of K > 4096 (4096x14336 Q4_K 13.08 vs 14.63: no K shares here).  Twice the
+// kernel's columns (4 for the K-quants, 6 for IQ4_XS, 8 for Q8_0) run as two
+// rows of its grid up to 4096 rows: Q4_K 4096x4096 at 4 columns 7.82 vs 7.08,
+// 3072x4096 8.32 vs 6.82, 4096x2048 7.28 vs 5.58; Q5_K 4096x4096 8.93 vs 8.42;
+// Q6_K 4096x2048 8.52 vs 7.48 (4096x4096 9.56 vs 9.40); IQ4_XS 4096x4096 at 6
+// 9.71 vs 9.19; Q8_0 4096x4096 at 8 11.63 vs 10.53.  Three groups lost (Q5_K
+// 4096x4096 at 6: 10.37 vs 11.28), and so did two from 8192 rows (Q5_K
+// 8192x4096 at 4: 12.32 vs 14.96); Q4_0 was not measured there.
 int qmm_mul_mat_fx_cols(int type, const void *w, int64_t K, int64_t nrows, int64_t row_stride, const float *x,
                         int64_t ncols, int64_t x_col_stride, float *dst, int64_t dst_col_stride, void *stream) {
     const bool big_wins = (K <= 2048 && (type == TYPE_Q4_K || type == TYPE_Q4_0)) || (type == TYPE_Q8_0 && ncols >= 3);
-    if (ncols < 2 || ncols > fxn_max_cols(type) || K % QK8 != 0 || K > 4096 || (nrows >= 8192 && !big_wins) ||
+    const bool two_groups = ncols == 2 * fxn_max_cols(type) && nrows <= 4096 && type != TYPE_Q4_0;
+    if (ncols < 2 || (ncols > fxn_max_cols(type) && !two_groups) || K % QK8 != 0 || K > 4096 ||
+        (nrows >= 8192 && !big_wins) ||
         (uintptr_t)x % 16 || x_col_stride % 4)
         return (int)hipErrorNotSupported;
     if (dst_col_stride < nrows || x_col_stride < K) return (int)hipErrorInvalidValue;

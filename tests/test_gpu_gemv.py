@@ -150,7 +150,8 @@ def _one_column_op_splits_k(tname, nrows, K):
 # Q8_0 at 3-4 columns and rows of K <= 2048), where the per-column grid below
 # does not take them: the op runs the
 # quantize-in-GEMV kernel over all columns in one launch (2 columns for the
-# K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0).  Where the one-column op runs
+# K-quants, 3 for IQ4_XS, 4 for Q8_0 / Q4_0; twice that on at most 4096 rows
+# as two rows of its grid, except Q4_0).  Where the one-column op runs
 # one K share, each column equals it bit for bit; where the one-column op
 # splits the row into K shares (Q8_0 / Q4_0 rows of two 2048-steps on at most
 # 2048 rows: attn_k / attn_v shapes) the one-launch kernel adds both steps in
@@ -163,7 +164,10 @@ def _one_column_op_splits_k(tname, nrows, K):
                                                  ("IQ4_XS", 6000, 4096, 2), ("Q8_0", 9000, 4096, 3),
                                                  ("Q4_K", 8200, 2048, 2), ("Q4_0", 8195, 1024, 4),
                                                  ("Q8_0", 1024, 4096, 2), ("Q4_0", 500, 4096, 3),
-                                                 ("Q8_0", 2048, 4096, 4)])
+                                                 ("Q8_0", 2048, 4096, 4), ("Q4_K", 4096, 4096, 4),
+                                                 ("Q6_K", 3000, 4096, 4), ("Q5_K", 2500, 3072, 4),
+                                                 ("IQ4_XS", 4096, 2048, 6), ("Q8_0", 4096, 4096, 8),
+                                                 ("Q8_0", 4000, 1024, 8)])
 def test_op_few_columns_one_launch(tname, nrows, K, ncols):
     import ggml_hip as G
     t, wq, x, w_d, x_d, qs, _ = _run(tname, nrows, K, ncols)
