@@ -272,9 +272,10 @@ int hip_qmm_gemv_mfma(int type, const void *w, int64_t K, int64_t nrows, int64_t
  *    K <= 4096 (below 8192 rows, except for K <= 2048 and Q8_0 at 3-4
  *    columns), skip the separate quantizer: the GEMV quantizes the columns in
  *    its prologue, as it does for 4 columns of the K-quants, 6 of IQ4_XS and 8
- *    of Q8_0 on at most 4096 rows (two rows of its grid).  2-8 columns of small matrices (at most 2048 rows of
- *    K <= 4096; Q8_0 at most 1024 rows and 4 columns; not Q4_0) run as rows
- *    of the one-column kernel's grid, each column quantized in the kernel
+ *    of Q8_0 on at most 4096 rows (two rows of its grid).  2-8 columns of
+ *    small matrices (at most 2048 rows of K <= 4096; Q8_0 / Q4_0 at most 1024
+ *    rows, and 4 columns unless K <= 2048) run as rows of the one-column
+ *    kernel's grid, each column quantized in the kernel
  *    (hip_qmm_mul_mat_per_column), with no workspace;
  *  - the few-column GEMM (16x16 int8 MFMA tiles) for 9-32 columns (9-16 for
  *    Q6_K; Q8_0 / Q4_0 at 17-32 columns of 8 MiB of weights and more take the

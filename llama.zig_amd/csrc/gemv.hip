@@ -1508,13 +1508,15 @@ extern "C" int hip_qmm_mul_mat_id_vec_fused_shared(int type, const void *w, cons
 // and IQ4_XS alike.  Larger grids lose (Q4_K 4096x4096 at 2 / 8: 4.96 / 9.67
 // against 5.84 / 12.98; Q6_K 3072x4096 at 8: 10.79 against 15.37), and so do
 // long rows (Q4_K 1024x14336 at 4: 9.70 against 12.42), which keep the other
-// paths.  Q8_0 wins up to 1024 rows at 2-4 columns (1024x4096 5.60 / 7.29
-// against 4.35 / 5.76) and loses at 8 (6.85 against 8.93) and on 2048 rows
-// (2048x4096 at 4: 7.47 against 9.08).  Q4_0 was not measured and keeps the
-// other paths.
+// paths.  The legacy types win up to 1024 rows at 2-4 columns (Q8_0 1024x4096
+// 5.60 / 7.29 against 4.35 / 5.76; Q4_0 4.48 / 6.63 against 3.96 / 5.59) and
+// at every column count on rows of K <= 2048 (Q4_0 1024x2048 at 8: 5.49
+// against 3.83; Q8_0 4.51 / 5.45 against 3.45 / 4.39 at 4 / 8), but lose at 6-8
+// columns of K = 4096 (Q8_0 1024x4096 at 8: 6.85 against 8.93) and on 2048
+// rows (Q8_0 2048x4096 at 4: 7.47 against 9.08; Q4_0 7.12 against 8.49).
 static bool fx_percol_wins(int type, int64_t K, int64_t nrows, int64_t ncols) {
-    if (ncols < 2 || ncols > 8 || K > 4096 || type == TYPE_Q4_0) return false;
-    if (type == TYPE_Q8_0) return nrows <= 1024 && ncols <= 4;
+    if (ncols < 2 || ncols > 8 || K > 4096) return false;
+    if (type == TYPE_Q8_0 || type == TYPE_Q4_0) return nrows <= 1024 && (ncols <= 4 || K <= 2048);
     return nrows <= 2048;
 }
 

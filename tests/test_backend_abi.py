@@ -330,4 +330,6 @@ def test_mul_mat_route_query(L):
     assert pc(q4k, 4096, 2048, 8) == 1 and pc(q4k, 4096, 2049, 2) == 0 and pc(q4k, 4352, 1024, 2) == 0
     assert pc(q4k, 4096, 1024, 1) == 0 and pc(q4k, 4096, 1024, 9) == 0
     assert pc(q8_0, 4096, 1024, 4) == 1 and pc(q8_0, 4096, 1024, 5) == 0 and pc(q8_0, 4096, 2048, 2) == 0
-    assert pc(q4_0, 4096, 1024, 2) == 0 and pc(q4k, 4096, 0, 2) == 0 and pc(q4k, 0, 1024, 2) == 0
+    assert pc(q4_0, 4096, 1024, 4) == 1 and pc(q4_0, 4096, 1024, 6) == 0 and pc(q4_0, 2048, 1024, 8) == 1
+    assert pc(q8_0, 2048, 1024, 8) == 1 and pc(q4_0, 2048, 1025, 2) == 0
+    assert pc(q4k, 4096, 0, 2) == 0 and pc(q4k, 0, 1024, 2) == 0

@@ -186,7 +186,7 @@ def test_op_few_columns_one_launch(tname, nrows, K, ncols):
 
 
 # 2-8 f32 columns of matrices of at most 2048 rows of at most 4096 elements
-# (Q8_0: 1024 rows, up to 4 columns; not Q4_0): the op runs every column
+# (Q8_0 / Q4_0: 1024 rows, up to 4 columns unless K <= 2048): the op runs every column
 # through the one-column kernel as one row of its grid
 # (qmm_mul_mat_fx_percol, gemv.hip), so each column equals the one-column op
 # on it bit for bit, K shares included.  Columns strided in and out; nothing
@@ -195,7 +195,9 @@ def test_op_few_columns_one_launch(tname, nrows, K, ncols):
                                                  ("Q5_K", 1000, 2048, 5), ("Q6_K", 1024, 4096, 4),
                                                  ("Q6_K", 777, 4096, 8), ("IQ4_XS", 2048, 4096, 6),
                                                  ("Q8_0", 1024, 4096, 4), ("Q8_0", 520, 1024, 2),
-                                                 ("Q4_K", 300, 256, 7), ("Q6_K", 64, 2048, 2)])
+                                                 ("Q4_K", 300, 256, 7), ("Q6_K", 64, 2048, 2),
+                                                 ("Q4_0", 1024, 4096, 3), ("Q4_0", 1000, 2048, 8),
+                                                 ("Q8_0", 700, 2048, 6)])
 def test_op_few_columns_per_column_grid(tname, nrows, K, ncols):
     import ctypes
 
